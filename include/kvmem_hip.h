@@ -1,0 +1,292 @@
+/*
+ * kvmem_hip.h -- C ABI of the MI355X (gfx950) KVMem reselect library.
+ *
+ * This is the device layer that replaces the reference's CUDA stage-in helper
+ * (src/adapter/llama-kvmem-stagein.h:12-62, free functions over a global
+ * singleton on cudaStreamPerThread) and the host scoring loop of the adapter
+ * (src/adapter/llama-memory-kvmem.cpp:2869-2916).  Differences by design:
+ *   - explicit context handle instead of the global `g_st` (stagein.cu:60-90);
+ *   - explicit HIP stream (default: a stream owned by the context);
+ *   - integer status codes (0 = ok) plus kvmem_hip_last_error() instead of
+ *     `bool` + stderr (stagein.cu:92-98); no exception crosses this ABI.
+ *
+ * Pointer lifetimes: every `const void *` / `void *` that names device memory
+ * is borrowed for the duration of the call and of the asynchronous work it
+ * enqueues on the context stream; the caller keeps it alive until
+ * kvmem_hip_sync() (or its own stream synchronisation) returns.  Host arrays
+ * passed in (op lists, ids, slots, pointer tables) are copied before the call
+ * returns and may be reused immediately.  Calls on one context are not
+ * re-entrant: use one context per host thread.
+ *
+ * Numeric formats use ggml's type codes and block layouts:
+ *   Q8_0 (8)  {f16 d; int8 qs[32]}             34 bytes / 32 elements
+ *   Q5_0 (6)  {f16 d; u8 qh[4]; u8 qs[16]}     22 bytes / 32 elements
+ *   Q4_0 (2)  {f16 d; u8 qs[16]}               18 bytes / 32 elements
+ *   F16  (1)  raw half rows (copy)
+ * Quantized bytes are bit-identical to ggml's quantize_row_*_ref applied to
+ * the F16 rows converted to f32.
+ */
+#ifndef KVMEM_HIP_H
+#define KVMEM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define KVMEM_HIP_API __attribute__((visibility("default")))
+#else
+#define KVMEM_HIP_API
+#endif
+
+/* ---------------------------------------------------------------- status */
+enum kvmem_hip_status {
+    KVMEM_HIP_OK = 0,
+    KVMEM_HIP_ERR_INVALID = 1,    /* bad argument (shape, alignment, range) */
+    KVMEM_HIP_ERR_RUNTIME = 2,    /* a HIP runtime call failed */
+    KVMEM_HIP_ERR_NOMEM = 3,      /* device or pinned allocation failed */
+    KVMEM_HIP_ERR_STALE = 4,      /* selection epoch/rows mismatch */
+    KVMEM_HIP_ERR_UNSUPPORTED = 5 /* type / head_dim not built */
+};
+
+/* ggml_type codes (ggml.h) for the formats on this path. */
+enum kvmem_hip_type {
+    KVMEM_TYPE_F32 = 0,
+    KVMEM_TYPE_F16 = 1,
+    KVMEM_TYPE_Q4_0 = 2,
+    KVMEM_TYPE_Q5_0 = 6,
+    KVMEM_TYPE_Q8_0 = 8,
+    KVMEM_TYPE_BF16 = 30
+};
+
+/* Layer combination of per-layer block scores. */
+enum kvmem_hip_layer_reduce {
+    KVMEM_LAYER_MEAN = 0, /* layer averaging, llama-memory-kvmem.cpp:2910-2913 */
+    KVMEM_LAYER_MAX = 1,
+    KVMEM_LAYER_SUM = 2
+};
+
+typedef struct kvmem_hip_ctx kvmem_hip_ctx;
+
+/* ------------------------------------------------------------- lifetime */
+
+/* Create a context on `device` (HIP ordinal).  Replaces the lazy singleton
+ * set-up of kvmem_stagein_gpu_ready (llama-kvmem-stagein.h:12,
+ * stagein.cu:319-393).  Scratch grows on demand inside later calls. */
+KVMEM_HIP_API int kvmem_hip_create(int device, kvmem_hip_ctx **out);
+
+/* Release every device/pinned buffer the context owns.  Replaces
+ * kvmem_stagein_gpu_free (llama-kvmem-stagein.h:13, stagein.cu:395-438). */
+KVMEM_HIP_API void kvmem_hip_destroy(kvmem_hip_ctx *ctx);
+
+/* Message of the last failing call on this context ("" if none).  Replaces
+ * the stderr line of cuda_ok (stagein.cu:92-98). */
+KVMEM_HIP_API const char *kvmem_hip_last_error(const kvmem_hip_ctx *ctx);
+
+/* Use `stream` (a hipStream_t; NULL = the context's own stream) for all
+ * later work.  The reference hard-wires cudaStreamPerThread
+ * (stagein.cu:100-102). */
+KVMEM_HIP_API int kvmem_hip_set_stream(kvmem_hip_ctx *ctx, void *stream);
+KVMEM_HIP_API void *kvmem_hip_get_stream(const kvmem_hip_ctx *ctx);
+
+/* Block the host until all work enqueued by this context has finished.
+ * Replaces kvmem_stagein_sync (llama-kvmem-stagein.h:27, stagein.cu:615-617). */
+KVMEM_HIP_API int kvmem_hip_sync(kvmem_hip_ctx *ctx);
+
+/* 1 if `type` can be produced by the stage-in kernels.  Replaces
+ * kvmem_stagein_quant_ok (llama-kvmem-stagein.h:16; the reference accepts
+ * only Q8_0 and Q4_0, stagein.cu:444-446). */
+KVMEM_HIP_API int kvmem_hip_quant_ok(int type);
+
+/* Bytes of a row of n elements of `type` (ggml_row_size), 0 if unsupported
+ * or n % 32 != 0.  Used as at llama-memory-kvmem.cpp:2738-2739. */
+KVMEM_HIP_API size_t kvmem_hip_row_size(int type, int64_t n);
+
+/* ------------------------------------------------------------- stage-in */
+
+/* One quantize-scatter operation: n_rows rows of n_embd F16 values at `src`
+ * (row stride src_stride bytes, 0 = n_embd*2) become n_rows contiguous rows
+ * of kvmem_hip_row_size(type, n_embd) bytes at `dst`.  src and dst must be
+ * 16-byte aligned, src_stride a multiple of 16, n_embd a multiple of 32. */
+typedef struct kvmem_hip_quant_op {
+    const void *src;
+    void *dst;
+    uint32_t n_rows;
+    uint32_t n_embd;
+    int32_t type;
+    uint32_t src_stride;
+} kvmem_hip_quant_op;
+
+/* Enqueue a batch of quantize-scatter operations (one kernel launch per
+ * output type present).  Replaces the enqueue_k/enqueue_v + flush slab
+ * sequence and kvmem_stagein_quantize (llama-kvmem-stagein.h:25,31-40;
+ * stagein.cu:579-605, 632-753, 776-840), fused: F16 rows are read once from
+ * HBM and written once in the pool's format. */
+KVMEM_HIP_API int kvmem_hip_stagein_quant(kvmem_hip_ctx *ctx,
+                                          const kvmem_hip_quant_op *ops,
+                                          int n_ops);
+
+/* Device-resident F16 block history: for each of K and V, the layer-major
+ * array [n_layers][n_blocks][block_tokens][n_embd] of halves (one 128-token
+ * block of one layer is contiguous, as RawKvStore keeps it per
+ * (block, layer), raw_kv_store.hpp:98-117).  v may be NULL (K only). */
+typedef struct kvmem_hip_history {
+    const void *k;
+    const void *v;
+    uint32_t n_layers;
+    uint32_t n_blocks;
+    uint32_t block_tokens;
+    uint32_t n_embd_k;
+    uint32_t n_embd_v;
+    uint32_t last_block_tokens; /* tokens in block n_blocks-1 (0 = full) */
+} kvmem_hip_history;
+
+/* Slot pool: per layer one K and one V tensor of n_slots*block_tokens rows
+ * of kvmem_hip_row_size(type, n_embd) bytes (the cache tensors of
+ * llama-memory-kvmem.cpp:2736-2742; cell = slot*block_tokens + t,
+ * llama-kvmem-batch.cpp:48).  k_layers/v_layers are host arrays of device
+ * pointers, 16-byte aligned.  v_layers may be NULL. */
+typedef struct kvmem_hip_pool {
+    uint32_t n_layers;
+    uint32_t n_slots;
+    uint32_t block_tokens;
+    uint32_t n_embd_k;
+    uint32_t n_embd_v;
+    int32_t type_k;
+    int32_t type_v;
+    void *const *k_layers;
+    void *const *v_layers;
+} kvmem_hip_pool;
+
+/* Quantize blocks block_ids[i] of a device-resident history into pool slot
+ * slots[i], every layer, K and V.  The single-launch-per-kind replacement
+ * of write_block_to_gpu's per-(block, layer) slab items
+ * (llama-memory-kvmem.cpp:2726-2791). */
+KVMEM_HIP_API int kvmem_hip_stagein_blocks(kvmem_hip_ctx *ctx,
+                                           const kvmem_hip_history *hist,
+                                           const kvmem_hip_pool *pool,
+                                           const uint32_t *block_ids,
+                                           const uint32_t *slots,
+                                           uint32_t n);
+
+/* Host-resident history in pinned memory, block-major: block b occupies
+ * one contiguous span of n_layers*(block_tokens*(n_embd_k+n_embd_v)) halves
+ * laid out [layer][K rows then V rows].  Blocks are copied with
+ * hipMemcpyAsync on a side stream into a device ring and quantized on the
+ * context stream as each copy lands (copy/kernel overlap).  Replaces the
+ * 32 MiB slab H2D of kvmem_stagein_flush (stagein.cu:632-753), which
+ * event-synchronises every H2D. */
+typedef struct kvmem_hip_host_history {
+    const void *base;           /* pinned host memory */
+    uint32_t n_layers;
+    uint32_t n_blocks;
+    uint32_t block_tokens;
+    uint32_t n_embd_k;
+    uint32_t n_embd_v;
+    uint32_t last_block_tokens;
+} kvmem_hip_host_history;
+
+KVMEM_HIP_API int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx,
+                                                const kvmem_hip_host_history *hist,
+                                                const kvmem_hip_pool *pool,
+                                                const uint32_t *block_ids,
+                                                const uint32_t *slots,
+                                                uint32_t n);
+
+/* Move whole slots inside the pool: slot src_slots[i] -> dst_slots[i] for
+ * every layer, K and V (quantized bytes copied unchanged).  Overlapping
+ * moves are hazard-free: sources are gathered to device scratch first.
+ * Replaces the gather/scatter D2D of layout_gpu_slots_by_orig_pos
+ * (llama-memory-kvmem.cpp:1003-1093). */
+KVMEM_HIP_API int kvmem_hip_move_slots(kvmem_hip_ctx *ctx,
+                                       const kvmem_hip_pool *pool,
+                                       const uint32_t *src_slots,
+                                       const uint32_t *dst_slots,
+                                       uint32_t n);
+
+/* Batched device-to-device byte copies in one launch.  Replaces
+ * kvmem_d2d_batched (llama-kvmem-stagein.h:52-53, stagein.cu:965-998);
+ * no 8192-op limit. */
+KVMEM_HIP_API int kvmem_hip_d2d_batched(kvmem_hip_ctx *ctx,
+                                        const void *const *src,
+                                        void *const *dst,
+                                        const size_t *nbytes,
+                                        int n);
+
+/* -------------------------------------------------------------- scoring */
+
+/* Per-token max block scorer on the matrix cores:
+ *   s[l][b] = max_{t<n_q_tokens, hq<n_head, j<n_tok(b)}
+ *             (q[l][t][hq] . k[l][b][j][hq / (n_head/n_head_kv)]) / sqrt(head_dim)
+ * with fp32 accumulation, and scores[b] = reduce_l s[l][b].
+ *   q       : device [n_layers][n_q_tokens][n_head][head_dim], bf16 or f16
+ *   hist->k : device history (see kvmem_hip_history), n_embd_k must equal
+ *             n_head_kv*head_dim
+ *   layer_scores (device [n_layers][n_blocks] f32, may be NULL), scores
+ *   (device [n_blocks] f32).
+ * The reference's scorer is mean-K cosine on the host
+ * (llama-memory-kvmem.cpp:2869-2916, per-block std::vector per head); its
+ * GQA head map (qh_i = h*g + gi, :2890-2892) is kept. */
+typedef struct kvmem_hip_score_args {
+    const void *q;
+    int32_t q_type;             /* KVMEM_TYPE_BF16 or KVMEM_TYPE_F16 */
+    uint32_t n_q_tokens;
+    uint32_t n_head;
+    uint32_t n_head_kv;
+    uint32_t head_dim;          /* 128 or 256 */
+    int32_t layer_reduce;       /* kvmem_hip_layer_reduce */
+    float *layer_scores;
+    float *scores;
+} kvmem_hip_score_args;
+
+KVMEM_HIP_API int kvmem_hip_score(kvmem_hip_ctx *ctx,
+                                  const kvmem_hip_history *hist,
+                                  const kvmem_hip_score_args *args);
+
+/* Top-k block selection on device.  From scores[0..n) (device, finite),
+ * keep every id in forced[] (host array, the sink / mandatory / recent
+ * blocks already charged by the host), then the `need` best remaining ids
+ * by score (equal scores: lower id first if tie_lower_index, else higher id
+ * first as kvmem_store.cpp:602-609), and write the union in ascending id
+ * order to sel_out (host array, capacity n_forced + need); *n_sel receives
+ * its length.  Replaces the nth_element fill of pick_topk_ungrouped
+ * (kvmem_store.cpp:594-622).  Synchronises the context stream.  n <= 16384. */
+KVMEM_HIP_API int kvmem_hip_topk(kvmem_hip_ctx *ctx,
+                                 const float *scores, uint32_t n,
+                                 const uint32_t *forced, uint32_t n_forced,
+                                 uint32_t need, int tie_lower_index,
+                                 uint32_t *sel_out, uint32_t *n_sel);
+
+/* ------------------------------------------------------------ profiling */
+
+/* Per-stage GPU time (hipEvent pairs on the context stream), the device
+ * analogue of the KVMEM_RETR_SUM buckets (llama-memory-kvmem.cpp:2918-2936):
+ * score = scoring kernels, topk = selection kernel, set = stage-in kernels,
+ * copy = H2D of host blocks, layout = slot moves.  Milliseconds summed over
+ * calls since the last reset; counts are numbers of timed calls. */
+typedef struct kvmem_hip_perf {
+    double score_ms;
+    double topk_ms;
+    double set_ms;
+    double copy_ms;
+    double layout_ms;
+    uint64_t n_score;
+    uint64_t n_topk;
+    uint64_t n_set;
+    uint64_t n_copy;
+    uint64_t n_layout;
+    uint64_t h2d_bytes;
+    uint64_t d2d_bytes;
+} kvmem_hip_perf;
+
+KVMEM_HIP_API int kvmem_hip_perf_enable(kvmem_hip_ctx *ctx, int on);
+KVMEM_HIP_API int kvmem_hip_perf_get(kvmem_hip_ctx *ctx, kvmem_hip_perf *out);
+KVMEM_HIP_API void kvmem_hip_perf_reset(kvmem_hip_ctx *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

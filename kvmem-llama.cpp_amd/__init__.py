@@ -1,0 +1,284 @@
+"""kvmem-llama.cpp_amd -- MI355X-native KVMem reselect path.
+
+Python view of libkvmem_hip.so (built in-tree by build.py): the device ABI of
+include/kvmem_hip.h (stage-in quantize-scatter, MFMA block scorer, top-k)
+and the host mirror of the reference's store / runtime / reselect interface
+of include/kvmem_host.h (KvMemStore, KvMemRuntime, ReselectEngine).
+
+The directory name is not a Python identifier; load it with
+`load_package()` from tests/conftest.py or __graft_entry__.py, which imports
+this file under the module name ``kvmem_amd``.
+
+Nothing here falls back to a CPU path: if the shared library is missing or
+a call fails, an exception is raised.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+from typing import Iterable, Sequence
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libkvmem_hip.so"
+
+# ggml type codes (include/kvmem_hip.h)
+TYPE_F32 = 0
+TYPE_F16 = 1
+TYPE_Q4_0 = 2
+TYPE_Q5_0 = 6
+TYPE_Q8_0 = 8
+TYPE_BF16 = 30
+TYPE_NAMES = {TYPE_F16: "f16", TYPE_Q4_0: "q4_0", TYPE_Q5_0: "q5_0", TYPE_Q8_0: "q8_0"}
+GROUP_BYTES = {TYPE_Q8_0: 34, TYPE_Q4_0: 18, TYPE_Q5_0: 22, TYPE_F16: 64}
+
+LAYER_MEAN, LAYER_MAX, LAYER_SUM = 0, 1, 2
+
+OK, ERR_INVALID, ERR_RUNTIME, ERR_NOMEM, ERR_STALE, ERR_UNSUPPORTED = range(6)
+
+
+def row_size(type_: int, n: int) -> int:
+    """ggml_row_size for the types on this path (n % 32 == 0)."""
+    return GROUP_BYTES[type_] * (n // 32)
+
+
+class KvMemError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class StaleSelection(KvMemError):
+    """The selection's epoch / row count no longer matches the memory
+    (the reference throws std::runtime_error("stale KVMem selection"),
+    llama-memory-kvmem.cpp:3144-3147)."""
+
+
+# ----------------------------------------------------------------- ABI types
+class QuantOp(C.Structure):
+    _fields_ = [("src", C.c_void_p), ("dst", C.c_void_p), ("n_rows", C.c_uint32),
+                ("n_embd", C.c_uint32), ("type", C.c_int32), ("src_stride", C.c_uint32)]
+
+
+class History(C.Structure):
+    _fields_ = [("k", C.c_void_p), ("v", C.c_void_p), ("n_layers", C.c_uint32),
+                ("n_blocks", C.c_uint32), ("block_tokens", C.c_uint32),
+                ("n_embd_k", C.c_uint32), ("n_embd_v", C.c_uint32),
+                ("last_block_tokens", C.c_uint32)]
+
+
+class HostHistory(C.Structure):
+    _fields_ = [("base", C.c_void_p), ("n_layers", C.c_uint32), ("n_blocks", C.c_uint32),
+                ("block_tokens", C.c_uint32), ("n_embd_k", C.c_uint32),
+                ("n_embd_v", C.c_uint32), ("last_block_tokens", C.c_uint32)]
+
+
+class Pool(C.Structure):
+    _fields_ = [("n_layers", C.c_uint32), ("n_slots", C.c_uint32), ("block_tokens", C.c_uint32),
+                ("n_embd_k", C.c_uint32), ("n_embd_v", C.c_uint32), ("type_k", C.c_int32),
+                ("type_v", C.c_int32), ("k_layers", C.POINTER(C.c_void_p)),
+                ("v_layers", C.POINTER(C.c_void_p))]
+
+
+class ScoreArgs(C.Structure):
+    _fields_ = [("q", C.c_void_p), ("q_type", C.c_int32), ("n_q_tokens", C.c_uint32),
+                ("n_head", C.c_uint32), ("n_head_kv", C.c_uint32), ("head_dim", C.c_uint32),
+                ("layer_reduce", C.c_int32), ("layer_scores", C.c_void_p), ("scores", C.c_void_p)]
+
+
+class Perf(C.Structure):
+    _fields_ = [("score_ms", C.c_double), ("topk_ms", C.c_double), ("set_ms", C.c_double),
+                ("copy_ms", C.c_double), ("layout_ms", C.c_double), ("n_score", C.c_uint64),
+                ("n_topk", C.c_uint64), ("n_set", C.c_uint64), ("n_copy", C.c_uint64),
+                ("n_layout", C.c_uint64), ("h2d_bytes", C.c_uint64), ("d2d_bytes", C.c_uint64)]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+_lib: C.CDLL | None = None
+
+
+def _sig(lib: C.CDLL, name: str, res, *args) -> None:
+    f = getattr(lib, name)
+    f.restype = res
+    f.argtypes = list(args)
+
+
+def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
+    """Load libkvmem_hip.so (raises if it was not built)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(f"{p} not built: run `python kvmem-llama.cpp_amd/build.py`")
+    lib = C.CDLL(str(p), mode=C.RTLD_LOCAL)
+    vp, u32, i32, sz = C.c_void_p, C.c_uint32, C.c_int, C.c_size_t
+    pu32 = C.POINTER(C.c_uint32)
+    _sig(lib, "kvmem_hip_create", i32, i32, C.POINTER(vp))
+    _sig(lib, "kvmem_hip_destroy", None, vp)
+    _sig(lib, "kvmem_hip_last_error", C.c_char_p, vp)
+    _sig(lib, "kvmem_hip_set_stream", i32, vp, vp)
+    _sig(lib, "kvmem_hip_get_stream", vp, vp)
+    _sig(lib, "kvmem_hip_sync", i32, vp)
+    _sig(lib, "kvmem_hip_quant_ok", i32, i32)
+    _sig(lib, "kvmem_hip_row_size", sz, i32, C.c_int64)
+    _sig(lib, "kvmem_hip_stagein_quant", i32, vp, C.POINTER(QuantOp), i32)
+    _sig(lib, "kvmem_hip_stagein_blocks", i32, vp, C.POINTER(History), C.POINTER(Pool), pu32, pu32, u32)
+    _sig(lib, "kvmem_hip_stagein_blocks_host", i32, vp, C.POINTER(HostHistory), C.POINTER(Pool),
+         pu32, pu32, u32)
+    _sig(lib, "kvmem_hip_move_slots", i32, vp, C.POINTER(Pool), pu32, pu32, u32)
+    _sig(lib, "kvmem_hip_d2d_batched", i32, vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(sz), i32)
+    _sig(lib, "kvmem_hip_score", i32, vp, C.POINTER(History), C.POINTER(ScoreArgs))
+    _sig(lib, "kvmem_hip_topk", i32, vp, vp, u32, pu32, u32, u32, i32, pu32, pu32)
+    _sig(lib, "kvmem_hip_perf_enable", i32, vp, i32)
+    _sig(lib, "kvmem_hip_perf_get", i32, vp, C.POINTER(Perf))
+    _sig(lib, "kvmem_hip_perf_reset", None, vp)
+    try:
+        from . import host as _host  # noqa: F401  (host mirror signatures)
+    except ImportError:
+        pass
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _u32_array(xs: Iterable[int]):
+    xs = list(xs)
+    return (C.c_uint32 * max(1, len(xs)))(*xs), len(xs)
+
+
+def _ptr_array(ptrs: Sequence[int]):
+    return (C.c_void_p * max(1, len(ptrs)))(*ptrs)
+
+
+class Context:
+    """A kvmem_hip_ctx on one GPU (explicit handle, own stream by default)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = C.c_void_p()
+        rc = self.lib.kvmem_hip_create(device, C.byref(h))
+        if rc != OK:
+            raise KvMemError(rc, f"kvmem_hip_create(device={device}) failed")
+        self.h = h
+        self._keep: list = []
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            self.lib.kvmem_hip_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # -- errors
+    def check(self, rc: int, what: str) -> None:
+        if rc == OK:
+            return
+        msg = self.lib.kvmem_hip_last_error(self.h).decode()
+        cls = StaleSelection if rc == ERR_STALE else KvMemError
+        raise cls(rc, f"{what}: {msg}")
+
+    def last_error(self) -> str:
+        return self.lib.kvmem_hip_last_error(self.h).decode()
+
+    # -- streams
+    def set_stream(self, stream_handle: int | None) -> None:
+        self.check(self.lib.kvmem_hip_set_stream(self.h, stream_handle or None), "set_stream")
+
+    def stream(self) -> int:
+        return self.lib.kvmem_hip_get_stream(self.h) or 0
+
+    def sync(self) -> None:
+        self.check(self.lib.kvmem_hip_sync(self.h), "sync")
+
+    # -- stage-in
+    def stagein_quant(self, ops: Sequence[tuple]) -> None:
+        """ops: (src_ptr, dst_ptr, n_rows, n_embd, type[, src_stride])."""
+        arr = (QuantOp * max(1, len(ops)))()
+        for i, op in enumerate(ops):
+            src, dst, n_rows, n_embd, type_ = op[:5]
+            stride = op[5] if len(op) > 5 else 0
+            arr[i] = QuantOp(src, dst, n_rows, n_embd, type_, stride)
+        self.check(self.lib.kvmem_hip_stagein_quant(self.h, arr, len(ops)), "stagein_quant")
+
+    @staticmethod
+    def make_history(k_ptr, v_ptr, n_layers, n_blocks, block_tokens, n_embd_k, n_embd_v,
+                     last_block_tokens=0) -> History:
+        return History(k_ptr or None, v_ptr or None, n_layers, n_blocks, block_tokens,
+                       n_embd_k, n_embd_v, last_block_tokens)
+
+    def make_pool(self, n_layers, n_slots, block_tokens, n_embd_k, n_embd_v, type_k, type_v,
+                  k_ptrs: Sequence[int], v_ptrs: Sequence[int] | None) -> Pool:
+        ka = _ptr_array(k_ptrs)
+        va = _ptr_array(v_ptrs) if v_ptrs is not None else None
+        self._keep.extend([ka, va])
+        return Pool(n_layers, n_slots, block_tokens, n_embd_k, n_embd_v, type_k, type_v,
+                    C.cast(ka, C.POINTER(C.c_void_p)),
+                    C.cast(va, C.POINTER(C.c_void_p)) if va is not None else None)
+
+    def stagein_blocks(self, hist: History, pool: Pool, block_ids, slots) -> None:
+        ids, n = _u32_array(block_ids)
+        sl, m = _u32_array(slots)
+        assert n == m
+        self.check(self.lib.kvmem_hip_stagein_blocks(self.h, C.byref(hist), C.byref(pool), ids, sl, n),
+                   "stagein_blocks")
+
+    def stagein_blocks_host(self, hist: HostHistory, pool: Pool, block_ids, slots) -> None:
+        ids, n = _u32_array(block_ids)
+        sl, m = _u32_array(slots)
+        assert n == m
+        self.check(self.lib.kvmem_hip_stagein_blocks_host(self.h, C.byref(hist), C.byref(pool), ids,
+                                                          sl, n), "stagein_blocks_host")
+
+    def move_slots(self, pool: Pool, src_slots, dst_slots) -> None:
+        s, n = _u32_array(src_slots)
+        d, m = _u32_array(dst_slots)
+        assert n == m
+        self.check(self.lib.kvmem_hip_move_slots(self.h, C.byref(pool), s, d, n), "move_slots")
+
+    def d2d_batched(self, srcs, dsts, nbytes) -> None:
+        n = len(srcs)
+        s = (C.c_void_p * max(1, n))(*srcs)
+        d = (C.c_void_p * max(1, n))(*dsts)
+        b = (C.c_size_t * max(1, n))(*nbytes)
+        self.check(self.lib.kvmem_hip_d2d_batched(self.h, s, d, b, n), "d2d_batched")
+
+    # -- scoring / selection
+    def score(self, hist: History, q_ptr: int, q_type: int, n_q_tokens: int, n_head: int,
+              n_head_kv: int, head_dim: int, scores_ptr: int, layer_scores_ptr: int = 0,
+              layer_reduce: int = LAYER_MEAN) -> None:
+        a = ScoreArgs(q_ptr, q_type, n_q_tokens, n_head, n_head_kv, head_dim, layer_reduce,
+                      layer_scores_ptr or None, scores_ptr)
+        self.check(self.lib.kvmem_hip_score(self.h, C.byref(hist), C.byref(a)), "score")
+
+    def topk(self, scores_ptr: int, n: int, need: int, forced=(), tie_lower_index: bool = True) -> list[int]:
+        f, nf = _u32_array(forced)
+        out = (C.c_uint32 * max(1, n))()
+        cnt = C.c_uint32(0)
+        self.check(self.lib.kvmem_hip_topk(self.h, scores_ptr, n, f, nf, need, int(tie_lower_index),
+                                           out, C.byref(cnt)), "topk")
+        return list(out[: cnt.value])
+
+    # -- profiling
+    def perf_enable(self, on: bool = True) -> None:
+        self.check(self.lib.kvmem_hip_perf_enable(self.h, int(on)), "perf_enable")
+
+    def perf(self) -> dict:
+        p = Perf()
+        self.check(self.lib.kvmem_hip_perf_get(self.h, C.byref(p)), "perf_get")
+        return p.as_dict()
+
+    def perf_reset(self) -> None:
+        self.lib.kvmem_hip_perf_reset(self.h)

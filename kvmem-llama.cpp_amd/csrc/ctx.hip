@@ -1,0 +1,352 @@
+// Context lifetime, error reporting, streams, upload ring, profiling and the
+// batched device copy of libkvmem_hip.so.
+#include "kvmem_internal.hpp"
+
+#include <cstring>
+#include <new>
+#include <vector>
+
+namespace kvmem_hip {
+
+int fail(kvmem_hip_ctx *ctx, int code, const std::string &msg) {
+    if (ctx) {
+        ctx->last_error = msg;
+    }
+    return code;
+}
+
+bool hip_ok(kvmem_hip_ctx *ctx, hipError_t e, const char *what) {
+    if (e == hipSuccess) {
+        return true;
+    }
+    if (ctx) {
+        ctx->last_error = std::string(what) + ": " + hipGetErrorString(e);
+    }
+    return false;
+}
+
+bool ensure_dev(kvmem_hip_ctx *ctx, DevBuf &b, size_t bytes, const char *what) {
+    if (b.ptr && b.bytes >= bytes) {
+        return true;
+    }
+    if (b.ptr) {
+        // the old buffer may still be read by enqueued work
+        if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), what)) {
+            return false;
+        }
+        hipFree(b.ptr);
+        b.ptr = nullptr;
+        b.bytes = 0;
+    }
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    if (!hip_ok(ctx, hipMalloc(&b.ptr, want), what)) {
+        b.ptr = nullptr;
+        return false;
+    }
+    b.bytes = want;
+    return true;
+}
+
+bool ensure_pin(kvmem_hip_ctx *ctx, PinBuf &b, size_t bytes, const char *what) {
+    if (b.ptr && b.bytes >= bytes) {
+        return true;
+    }
+    if (b.ptr) {
+        if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), what)) {
+            return false;
+        }
+        hipHostFree(b.ptr);
+        b.ptr = nullptr;
+        b.bytes = 0;
+    }
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    if (!hip_ok(ctx, hipHostMalloc(&b.ptr, want, hipHostMallocDefault), what)) {
+        b.ptr = nullptr;
+        return false;
+    }
+    b.bytes = want;
+    return true;
+}
+
+void *upload(kvmem_hip_ctx *ctx, const void *src, size_t bytes, const char *what) {
+    UploadSlot &s = ctx->upload[ctx->upload_next];
+    ctx->upload_next = (ctx->upload_next + 1) % kUploadRing;
+    if (s.pending) {
+        // the pinned staging area is still the source of an enqueued copy
+        if (!hip_ok(ctx, hipEventSynchronize(s.done), what)) {
+            return nullptr;
+        }
+        s.pending = false;
+    }
+    if (!ensure_pin(ctx, s.host, bytes, what) || !ensure_dev(ctx, s.dev, bytes, what)) {
+        return nullptr;
+    }
+    if (!s.done && !hip_ok(ctx, hipEventCreateWithFlags(&s.done, hipEventDisableTiming), what)) {
+        return nullptr;
+    }
+    std::memcpy(s.host.ptr, src, bytes);
+    if (!hip_ok(ctx, hipMemcpyAsync(s.dev.ptr, s.host.ptr, bytes, hipMemcpyHostToDevice,
+                                    ctx->stream), what) ||
+        !hip_ok(ctx, hipEventRecord(s.done, ctx->stream), what)) {
+        return nullptr;
+    }
+    s.pending = true;
+    return s.dev.ptr;
+}
+
+void perf_begin(kvmem_hip_ctx *ctx, PerfStage s) {
+    if (!ctx->perf_on) {
+        return;
+    }
+    if (ctx->perf_pending[s]) {
+        perf_collect(ctx);
+    }
+    if (!ctx->perf_ev[s][0]) {
+        hipEventCreate(&ctx->perf_ev[s][0]);
+        hipEventCreate(&ctx->perf_ev[s][1]);
+    }
+    hipEventRecord(ctx->perf_ev[s][0], ctx->stream);
+}
+
+void perf_end(kvmem_hip_ctx *ctx, PerfStage s) {
+    if (!ctx->perf_on || !ctx->perf_ev[s][1]) {
+        return;
+    }
+    hipEventRecord(ctx->perf_ev[s][1], ctx->stream);
+    ctx->perf_pending[s] = true;
+}
+
+void perf_collect(kvmem_hip_ctx *ctx) {
+    for (int s = 0; s < kPerfStages; ++s) {
+        if (!ctx->perf_pending[s]) {
+            continue;
+        }
+        float ms = 0.0f;
+        if (hipEventSynchronize(ctx->perf_ev[s][1]) == hipSuccess &&
+            hipEventElapsedTime(&ms, ctx->perf_ev[s][0], ctx->perf_ev[s][1]) == hipSuccess) {
+            ctx->perf_ms[s] += ms;
+            ctx->perf_n[s] += 1;
+        }
+        ctx->perf_pending[s] = false;
+    }
+}
+
+// ------------------------------------------------------------------------
+// Batched byte copies: one workgroup per op, 16-byte vectors when both
+// addresses and the size are 16-byte aligned.
+// ------------------------------------------------------------------------
+struct CopyOpDev {
+    const uint8_t *src;
+    uint8_t *dst;
+    uint64_t nbytes;
+};
+
+__global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops, int n) {
+    const int i = blockIdx.x;
+    if (i >= n) {
+        return;
+    }
+    const CopyOpDev op = ops[i];
+    const uintptr_t a = reinterpret_cast<uintptr_t>(op.src) | reinterpret_cast<uintptr_t>(op.dst);
+    if ((a & 15u) == 0 && (op.nbytes & 15u) == 0) {
+        const uint4 *s = reinterpret_cast<const uint4 *>(op.src);
+        uint4 *d = reinterpret_cast<uint4 *>(op.dst);
+        const uint64_t n16 = op.nbytes >> 4;
+        for (uint64_t j = threadIdx.x; j < n16; j += blockDim.x) {
+            d[j] = s[j];
+        }
+        return;
+    }
+    for (uint64_t j = threadIdx.x; j < op.nbytes; j += blockDim.x) {
+        op.dst[j] = op.src[j];
+    }
+}
+
+}  // namespace kvmem_hip
+
+using namespace kvmem_hip;
+
+extern "C" {
+
+int kvmem_hip_create(int device, kvmem_hip_ctx **out) {
+    if (!out) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    *out = nullptr;
+    int n_dev = 0;
+    if (hipGetDeviceCount(&n_dev) != hipSuccess || device < 0 || device >= n_dev) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    kvmem_hip_ctx *ctx = new (std::nothrow) kvmem_hip_ctx();
+    if (!ctx) {
+        return KVMEM_HIP_ERR_NOMEM;
+    }
+    ctx->device = device;
+    if (hipSetDevice(device) != hipSuccess ||
+        hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking) != hipSuccess) {
+        kvmem_hip_destroy(ctx);
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    ctx->stream = ctx->own_stream;
+    *out = ctx;
+    return KVMEM_HIP_OK;
+}
+
+void kvmem_hip_destroy(kvmem_hip_ctx *ctx) {
+    if (!ctx) {
+        return;
+    }
+    (void) hipSetDevice(ctx->device);
+    if (ctx->stream) {
+        hipStreamSynchronize(ctx->stream);
+    }
+    if (ctx->copy_stream) {
+        hipStreamSynchronize(ctx->copy_stream);
+    }
+    for (auto &s : ctx->upload) {
+        if (s.host.ptr) hipHostFree(s.host.ptr);
+        if (s.dev.ptr) hipFree(s.dev.ptr);
+        if (s.done) hipEventDestroy(s.done);
+    }
+    for (DevBuf *b : {&ctx->score_partial, &ctx->move_scratch, &ctx->topk_sel, &ctx->h2d_ring}) {
+        if (b->ptr) hipFree(b->ptr);
+    }
+    if (ctx->topk_sel_host.ptr) hipHostFree(ctx->topk_sel_host.ptr);
+    for (int i = 0; i < 8; ++i) {
+        if (ctx->h2d_copied[i]) hipEventDestroy(ctx->h2d_copied[i]);
+        if (ctx->h2d_consumed[i]) hipEventDestroy(ctx->h2d_consumed[i]);
+    }
+    for (auto &pair : ctx->perf_ev) {
+        for (hipEvent_t e : pair) {
+            if (e) hipEventDestroy(e);
+        }
+    }
+    if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
+    if (ctx->copy_stream) hipStreamDestroy(ctx->copy_stream);
+    delete ctx;
+}
+
+const char *kvmem_hip_last_error(const kvmem_hip_ctx *ctx) {
+    return ctx ? ctx->last_error.c_str() : "null context";
+}
+
+int kvmem_hip_set_stream(kvmem_hip_ctx *ctx, void *stream) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    hipStream_t next = stream ? static_cast<hipStream_t>(stream) : ctx->own_stream;
+    if (next != ctx->stream) {
+        // work on the old stream must not overtake later work on the new one
+        if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "set_stream sync")) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        ctx->stream = next;
+    }
+    return KVMEM_HIP_OK;
+}
+
+void *kvmem_hip_get_stream(const kvmem_hip_ctx *ctx) {
+    return ctx ? static_cast<void *>(ctx->stream) : nullptr;
+}
+
+int kvmem_hip_sync(kvmem_hip_ctx *ctx) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!hip_ok(ctx, hipStreamSynchronize(ctx->copy_stream), "sync copy stream") ||
+        !hip_ok(ctx, hipStreamSynchronize(ctx->stream), "sync")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_hip_quant_ok(int type) {
+    return type == KVMEM_TYPE_Q8_0 || type == KVMEM_TYPE_Q5_0 || type == KVMEM_TYPE_Q4_0 ||
+           type == KVMEM_TYPE_F16;
+}
+
+size_t kvmem_hip_row_size(int type, int64_t n) {
+    if (n <= 0 || n % 32 != 0) {
+        return 0;
+    }
+    return static_cast<size_t>(group_bytes(type)) * static_cast<size_t>(n / 32);
+}
+
+int kvmem_hip_d2d_batched(kvmem_hip_ctx *ctx, const void *const *src, void *const *dst,
+                          const size_t *nbytes, int n) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (n <= 0) {
+        return KVMEM_HIP_OK;
+    }
+    if (!src || !dst || !nbytes) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "d2d_batched: null array");
+    }
+    std::vector<CopyOpDev> ops(static_cast<size_t>(n));
+    uint64_t total = 0;
+    for (int i = 0; i < n; ++i) {
+        if (!src[i] || !dst[i] || nbytes[i] == 0) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "d2d_batched: null pointer or empty op");
+        }
+        ops[i] = {static_cast<const uint8_t *>(src[i]), static_cast<uint8_t *>(dst[i]), nbytes[i]};
+        total += nbytes[i];
+    }
+    (void) hipSetDevice(ctx->device);
+    void *dops = upload(ctx, ops.data(), ops.size() * sizeof(CopyOpDev), "d2d_batched ops");
+    if (!dops) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    perf_begin(ctx, kPerfLayout);
+    batched_copy_kernel<<<n, 256, 0, ctx->stream>>>(static_cast<const CopyOpDev *>(dops), n);
+    perf_end(ctx, kPerfLayout);
+    if (!hip_ok(ctx, hipGetLastError(), "d2d_batched launch")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    ctx->d2d_bytes += total;
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_hip_perf_enable(kvmem_hip_ctx *ctx, int on) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    ctx->perf_on = on != 0;
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_hip_perf_get(kvmem_hip_ctx *ctx, kvmem_hip_perf *out) {
+    if (!ctx || !out) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    perf_collect(ctx);
+    out->score_ms = ctx->perf_ms[kPerfScore];
+    out->topk_ms = ctx->perf_ms[kPerfTopk];
+    out->set_ms = ctx->perf_ms[kPerfSet];
+    out->copy_ms = ctx->perf_ms[kPerfCopy];
+    out->layout_ms = ctx->perf_ms[kPerfLayout];
+    out->n_score = ctx->perf_n[kPerfScore];
+    out->n_topk = ctx->perf_n[kPerfTopk];
+    out->n_set = ctx->perf_n[kPerfSet];
+    out->n_copy = ctx->perf_n[kPerfCopy];
+    out->n_layout = ctx->perf_n[kPerfLayout];
+    out->h2d_bytes = ctx->h2d_bytes;
+    out->d2d_bytes = ctx->d2d_bytes;
+    return KVMEM_HIP_OK;
+}
+
+void kvmem_hip_perf_reset(kvmem_hip_ctx *ctx) {
+    if (!ctx) {
+        return;
+    }
+    perf_collect(ctx);
+    for (int s = 0; s < kPerfStages; ++s) {
+        ctx->perf_ms[s] = 0.0;
+        ctx->perf_n[s] = 0;
+    }
+    ctx->h2d_bytes = 0;
+    ctx->d2d_bytes = 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,112 @@
+// Internal definitions shared by the gfx950 translation units of
+// libkvmem_hip.so: the context object, status helpers, scratch buffers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "kvmem_hip.h"
+
+namespace kvmem_hip {
+
+// Grow-only device buffer owned by a context.
+struct DevBuf {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+// Grow-only pinned host buffer owned by a context.
+struct PinBuf {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+// Ring slot for small host->device uploads (op tables, id lists): a pinned
+// staging area, a device copy and the event that marks the copy consumed.
+struct UploadSlot {
+    PinBuf host;
+    DevBuf dev;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+};
+
+constexpr int kUploadRing = 4;
+constexpr int kPerfStages = 5;  // score, topk, set, copy, layout
+enum PerfStage { kPerfScore = 0, kPerfTopk = 1, kPerfSet = 2, kPerfCopy = 3, kPerfLayout = 4 };
+
+}  // namespace kvmem_hip
+
+struct kvmem_hip_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;       // active compute stream
+    hipStream_t copy_stream = nullptr;  // side stream for H2D of host blocks
+    std::string last_error;
+
+    kvmem_hip::UploadSlot upload[kvmem_hip::kUploadRing];
+    int upload_next = 0;
+
+    kvmem_hip::DevBuf score_partial;    // [row_groups][L][Hkv][B] f32
+    kvmem_hip::DevBuf move_scratch;     // gathered slots for kvmem_hip_move_slots
+    kvmem_hip::DevBuf topk_sel;         // device selection output
+    kvmem_hip::PinBuf topk_sel_host;    // pinned copy of the selection
+
+    // pinned-host stage-in: device ring of block buffers + events
+    kvmem_hip::DevBuf h2d_ring;
+    size_t h2d_slot_bytes = 0;
+    int h2d_slots = 0;
+    hipEvent_t h2d_copied[8] = {};
+    hipEvent_t h2d_consumed[8] = {};
+
+    // profiling
+    bool perf_on = false;
+    hipEvent_t perf_ev[kvmem_hip::kPerfStages][2] = {};
+    bool perf_pending[kvmem_hip::kPerfStages] = {};
+    double perf_ms[kvmem_hip::kPerfStages] = {};
+    uint64_t perf_n[kvmem_hip::kPerfStages] = {};
+    uint64_t h2d_bytes = 0;
+    uint64_t d2d_bytes = 0;
+};
+
+namespace kvmem_hip {
+
+// Record `msg` as the context's last error and return `code`.
+int fail(kvmem_hip_ctx *ctx, int code, const std::string &msg);
+// Check a HIP call; on failure record "<what>: <hip error string>".
+bool hip_ok(kvmem_hip_ctx *ctx, hipError_t e, const char *what);
+
+bool ensure_dev(kvmem_hip_ctx *ctx, DevBuf &b, size_t bytes, const char *what);
+bool ensure_pin(kvmem_hip_ctx *ctx, PinBuf &b, size_t bytes, const char *what);
+
+// Copy `bytes` of host data to device memory through the upload ring,
+// ordered on the context stream.  Returns the device address or nullptr.
+void *upload(kvmem_hip_ctx *ctx, const void *src, size_t bytes, const char *what);
+
+// Profiling brackets around a stage's launches on the context stream.
+void perf_begin(kvmem_hip_ctx *ctx, PerfStage s);
+void perf_end(kvmem_hip_ctx *ctx, PerfStage s);
+// Harvest finished event pairs into the accumulators (blocking).
+void perf_collect(kvmem_hip_ctx *ctx);
+
+// 16-byte load that is not expected to be reused (streamed history data).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ inline uint4 load_stream16(const void *p) {
+    const u32x4_t v = __builtin_nontemporal_load(static_cast<const u32x4_t *>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Block format helpers (ggml layouts).
+inline uint32_t group_bytes(int type) {
+    switch (type) {
+        case KVMEM_TYPE_Q8_0: return 34;
+        case KVMEM_TYPE_Q4_0: return 18;
+        case KVMEM_TYPE_Q5_0: return 22;
+        case KVMEM_TYPE_F16: return 64;
+        default: return 0;
+    }
+}
+
+}  // namespace kvmem_hip

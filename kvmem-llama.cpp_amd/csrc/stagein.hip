@@ -1,0 +1,749 @@
+// Stage-in: F16 KV rows -> ggml q8_0 / q5_0 / q4_0 (or F16) rows scattered
+// into pool slots.  HBM-bound: every F16 byte is read once with 16-byte
+// coalesced loads and every output byte is written once with 16-byte stores.
+//
+// Work decomposition.  An operation (one block of one layer of K or V) is a
+// linear run of 32-element groups (rows are contiguous groups and the
+// output rows of a slot are contiguous cells).  A workgroup of 256 threads
+// handles a chunk of 256 groups; inside a wave, four consecutive lanes own
+// one group (8 halves = 16 bytes each), so a wave-wide load instruction
+// reads 1 KiB of contiguous F16.  The group scale comes from a two-step
+// quad reduction through DPP, the quantized bytes are packed in registers,
+// written to the wave's LDS region in ggml's byte layout, and copied out
+// with aligned 16-byte global stores.
+//
+// Arithmetic follows ggml's quantize_row_*_ref exactly (restated in the
+// reference's CUDA kernels, llama-kvmem-stagein.cu:180-233):
+//   q8_0: d = amax/127, id = d ? 1/d : 0, q = roundf(x*id)
+//   q4_0: d = vmax/-8,  q = min(15, trunc(x*id + 8.5))
+//   q5_0: d = vmax/-16, q = min(31, trunc(x*id + 16.5)), bit 4 -> qh
+// where vmax is the first element of largest magnitude.  The products and
+// sums are separate IEEE operations (no FMA contraction in this file),
+// divisions are correctly rounded (HIP default), d is stored as f16 RNE.
+#include "kvmem_internal.hpp"
+
+#include <algorithm>
+#include <vector>
+
+#pragma clang fp contract(off)
+
+namespace kvmem_hip {
+
+constexpr int kChunkGroups = 256;  // groups per workgroup
+constexpr int kWaveGroups = 64;    // groups per wave (4 rounds x 16)
+
+template <int TYPE> struct Fmt;
+template <> struct Fmt<KVMEM_TYPE_Q8_0> { static constexpr int GB = 34; };
+template <> struct Fmt<KVMEM_TYPE_Q4_0> { static constexpr int GB = 18; };
+template <> struct Fmt<KVMEM_TYPE_Q5_0> { static constexpr int GB = 22; };
+template <> struct Fmt<KVMEM_TYPE_F16> { static constexpr int GB = 64; };
+
+// A contiguous run of groups of one operation.
+struct Chunk {
+    const uint8_t *src;   // first byte of the operation's F16 rows
+    uint8_t *dst;         // first byte of the operation's output rows
+    uint32_t g0;          // first group of this chunk within the operation
+    uint32_t ng;          // groups in this chunk (<= kChunkGroups)
+    uint32_t gpr;         // groups per row
+    uint32_t src_stride;  // bytes between F16 rows
+};
+
+// Source 1: an explicit list of operations.  chunk0 is the index of the
+// operation's first chunk; the list is sorted by it.
+struct QuantOpDev {
+    const uint8_t *src;
+    uint8_t *dst;
+    uint32_t n_groups;
+    uint32_t gpr;
+    uint32_t src_stride;
+    uint32_t chunk0;
+};
+
+struct OpListSource {
+    const QuantOpDev *ops;
+    uint32_t n_ops;
+    __device__ bool chunk(uint32_t c, Chunk &out) const {
+        uint32_t lo = 0, hi = n_ops;  // last op with chunk0 <= c
+        while (hi - lo > 1) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (ops[mid].chunk0 <= c) {
+                lo = mid;
+            } else {
+                hi = mid;
+            }
+        }
+        const QuantOpDev op = ops[lo];
+        out.src = op.src;
+        out.dst = op.dst;
+        out.g0 = (c - op.chunk0) * kChunkGroups;
+        if (out.g0 >= op.n_groups) {
+            return false;
+        }
+        out.ng = min(static_cast<uint32_t>(kChunkGroups), op.n_groups - out.g0);
+        out.gpr = op.gpr;
+        out.src_stride = op.src_stride;
+        return true;
+    }
+};
+
+// Source 2: whole blocks of a history, for every layer.  Item i names a
+// source block (addressing index), its destination slot and its tokens.
+//   src(item, layer) = base + block*block_stride + layer*layer_stride
+//   dst(item, layer) = layer_dst[layer] + slot*block_tokens*row_bytes
+struct BlockSource {
+    const uint8_t *base;
+    const uint8_t *const *layer_dst;  // device array [n_layers]
+    const uint32_t *items;            // device [n_items][3]: block, slot, n_tokens
+    uint64_t block_stride;
+    uint64_t layer_stride;
+    uint32_t n_layers;
+    uint32_t block_tokens;
+    uint32_t gpr;
+    uint32_t row_bytes;               // output bytes per row
+    uint32_t chunks_per_op;           // ceil(block_tokens*gpr / kChunkGroups)
+    __device__ bool chunk(uint32_t c, Chunk &out) const {
+        const uint32_t op = c / chunks_per_op;
+        const uint32_t sub = c - op * chunks_per_op;
+        const uint32_t item = op / n_layers;
+        const uint32_t layer = op - item * n_layers;
+        const uint32_t block = items[3 * item + 0];
+        const uint32_t slot = items[3 * item + 1];
+        const uint32_t ntok = items[3 * item + 2];
+        const uint32_t total = ntok * gpr;
+        out.g0 = sub * kChunkGroups;
+        if (out.g0 >= total) {
+            return false;
+        }
+        out.ng = min(static_cast<uint32_t>(kChunkGroups), total - out.g0);
+        out.src = base + block * block_stride + layer * layer_stride;
+        out.dst = const_cast<uint8_t *>(layer_dst[layer]) +
+                  static_cast<uint64_t>(slot) * block_tokens * row_bytes;
+        out.gpr = gpr;
+        out.src_stride = gpr * 64u;
+        return true;
+    }
+};
+
+// ---------------------------------------------------------------- lanes
+
+// Quad exchange through DPP: lane i of each 4-lane quad reads lane i^1 / i^2.
+__device__ inline uint32_t quad_xor1(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ inline uint32_t quad_xor2(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false));
+}
+
+__device__ inline float half_bits_to_float(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+__device__ inline uint32_t float_to_half_bits(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));  // v_cvt_f16_f32, RNE
+}
+
+__device__ inline void unpack8(const uint4 &v, uint32_t h[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h[2 * i] = w[i] & 0xffffu;
+        h[2 * i + 1] = w[i] >> 16;
+    }
+}
+
+__device__ inline void store_u16(uint8_t *p, uint32_t v) {
+    *reinterpret_cast<uint16_t *>(p) = static_cast<uint16_t>(v);
+}
+
+// Eight bytes packed in two words -> four 2-byte LDS stores (the group
+// layouts only guarantee 2-byte alignment).
+__device__ inline void store_8bytes(uint8_t *p, uint32_t lo, uint32_t hi) {
+    store_u16(p + 0, lo & 0xffffu);
+    store_u16(p + 2, lo >> 16);
+    store_u16(p + 4, hi & 0xffffu);
+    store_u16(p + 6, hi >> 16);
+}
+
+// Quantize the 8 elements a lane owns (elements 8q..8q+7 of its group) and
+// write its share of the group's bytes to `g` (the group's LDS bytes).
+template <int TYPE>
+__device__ inline void quant_quarter(const uint4 &v, uint32_t q, uint8_t *g, bool valid);
+
+template <>
+__device__ inline void quant_quarter<KVMEM_TYPE_Q8_0>(const uint4 &v, uint32_t q, uint8_t *g,
+                                                       bool valid) {
+    uint32_t h[8];
+    unpack8(v, h);
+    float x[8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        x[i] = half_bits_to_float(h[i]);
+        amax = fmaxf(amax, fabsf(x[i]));
+    }
+    amax = fmaxf(amax, __uint_as_float(quad_xor1(__float_as_uint(amax))));
+    amax = fmaxf(amax, __uint_as_float(quad_xor2(__float_as_uint(amax))));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float s = x[i] * id;
+        const int c = static_cast<int>(roundf(s));
+        w[i >> 2] |= (static_cast<uint32_t>(c) & 0xffu) << (8 * (i & 3));
+    }
+    if (valid) {
+        if (q == 0) {
+            store_u16(g, float_to_half_bits(d));
+        }
+        store_8bytes(g + 2 + 8 * q, w[0], w[1]);
+    }
+}
+
+// vmax of ggml's q4_0/q5_0: the FIRST element of largest magnitude (strict
+// `amax < |v|` scan).  Reduced as a max over 21-bit keys
+// (|h| << 6) | ((31 - e) << 1) | sign(h): larger magnitude wins, then lower
+// element index.  An all-zero group keeps ggml's initial vmax = +0.
+__device__ inline float quad_vmax(const uint32_t h[8], uint32_t q) {
+    uint32_t key = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t e = 8 * q + i;
+        const uint32_t k = ((h[i] & 0x7fffu) << 6) | ((31u - e) << 1) | (h[i] >> 15);
+        key = k > key ? k : key;
+    }
+    uint32_t o = quad_xor1(key);
+    key = o > key ? o : key;
+    o = quad_xor2(key);
+    key = o > key ? o : key;
+    const uint32_t mag = key >> 6;
+    if (mag == 0) {
+        return 0.0f;
+    }
+    return half_bits_to_float(mag | ((key & 1u) << 15));
+}
+
+template <int TOP>
+__device__ inline uint32_t trunc_code(float x, float id, float bias) {
+    const float s = x * id;     // rounded product
+    const float t = s + bias;   // rounded sum (separate operation)
+    const int c = static_cast<int>(t);
+    return static_cast<uint32_t>(c < TOP ? c : TOP);
+}
+
+template <>
+__device__ inline void quant_quarter<KVMEM_TYPE_Q4_0>(const uint4 &v, uint32_t q, uint8_t *g,
+                                                       bool valid) {
+    uint32_t h[8];
+    unpack8(v, h);
+    const float vmax = quad_vmax(h, q);
+    const float d = vmax / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t nib = 0;  // 8 codes, 4 bits each, element order
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        nib |= trunc_code<15>(half_bits_to_float(h[i]), id, 8.5f) << (4 * i);
+    }
+    // qs[j] = code(j) | code(j+16) << 4: lanes 0/1 pair with lanes 2/3
+    const uint32_t hi = quad_xor2(nib);
+    if (valid) {
+        if (q == 0) {
+            store_u16(g, float_to_half_bits(d));
+        }
+        if (q < 2) {
+            uint32_t w[2] = {0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t b = ((nib >> (4 * i)) & 0xfu) | (((hi >> (4 * i)) & 0xfu) << 4);
+                w[i >> 2] |= b << (8 * (i & 3));
+            }
+            store_8bytes(g + 2 + 8 * q, w[0], w[1]);
+        }
+    }
+}
+
+template <>
+__device__ inline void quant_quarter<KVMEM_TYPE_Q5_0>(const uint4 &v, uint32_t q, uint8_t *g,
+                                                       bool valid) {
+    uint32_t h[8];
+    unpack8(v, h);
+    const float vmax = quad_vmax(h, q);
+    const float d = vmax / -16.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t nib = 0;
+    uint32_t qh = 0;  // bit e = bit 4 of the code of element e
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t c = trunc_code<31>(half_bits_to_float(h[i]), id, 16.5f);
+        nib |= (c & 0xfu) << (4 * i);
+        qh |= ((c >> 4) & 1u) << (8 * q + i);
+    }
+    qh |= quad_xor1(qh);
+    qh |= quad_xor2(qh);
+    const uint32_t hi = quad_xor2(nib);
+    if (valid) {
+        if (q == 0) {
+            store_u16(g, float_to_half_bits(d));
+            store_u16(g + 2, qh & 0xffffu);
+            store_u16(g + 4, qh >> 16);
+        }
+        if (q < 2) {
+            uint32_t w[2] = {0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t b = ((nib >> (4 * i)) & 0xfu) | (((hi >> (4 * i)) & 0xfu) << 4);
+                w[i >> 2] |= b << (8 * (i & 3));
+            }
+            store_8bytes(g + 6 + 8 * q, w[0], w[1]);
+        }
+    }
+}
+
+template <>
+__device__ inline void quant_quarter<KVMEM_TYPE_F16>(const uint4 &v, uint32_t q, uint8_t *g,
+                                                      bool valid) {
+    if (valid) {
+        *reinterpret_cast<uint4 *>(g + 16 * q) = v;
+    }
+}
+
+template <int TYPE, class Source>
+__global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
+    constexpr int GB = Fmt<TYPE>::GB;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kWaveGroups * GB];
+    Chunk c;
+    if (!source.chunk(blockIdx.x, c)) {
+        return;  // uniform across the workgroup
+    }
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid >> 6;
+    const uint32_t lane = tid & 63u;
+    const uint32_t quad = lane >> 2;
+    const uint32_t q = lane & 3u;
+    const uint32_t wg0 = wave * kWaveGroups;
+    uint8_t *wl = lds + wave * kWaveGroups * GB;
+
+    uint4 v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t gl = wg0 + 16u * r + quad;
+        v[r] = make_uint4(0u, 0u, 0u, 0u);
+        if (gl < c.ng) {
+            const uint32_t g = c.g0 + gl;
+            const uint32_t row = g / c.gpr;
+            const uint32_t col = g - row * c.gpr;
+            const uint8_t *p = c.src + static_cast<uint64_t>(row) * c.src_stride + col * 64u + q * 16u;
+            v[r] = load_stream16(p);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t gl = wg0 + 16u * r + quad;
+        quant_quarter<TYPE>(v[r], q, wl + (16u * r + quad) * GB, gl < c.ng);
+    }
+    __syncthreads();
+
+    const uint32_t ngw = c.ng > wg0 ? min(static_cast<uint32_t>(kWaveGroups), c.ng - wg0) : 0u;
+    const uint32_t nb = ngw * GB;
+    uint8_t *dst = c.dst + static_cast<uint64_t>(c.g0 + wg0) * GB;
+    const uint32_t full = nb & ~15u;
+    for (uint32_t off = lane * 16u; off < full; off += 1024u) {
+        *reinterpret_cast<uint4 *>(dst + off) = *reinterpret_cast<const uint4 *>(wl + off);
+    }
+    for (uint32_t off = full + lane * 2u; off < nb; off += 128u) {
+        *reinterpret_cast<uint16_t *>(dst + off) = *reinterpret_cast<const uint16_t *>(wl + off);
+    }
+}
+
+template <class Source>
+bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Source &s) {
+    if (n_chunks == 0) {
+        return true;
+    }
+    switch (type) {
+        case KVMEM_TYPE_Q8_0:
+            quant_scatter_kernel<KVMEM_TYPE_Q8_0, Source><<<n_chunks, 256, 0, ctx->stream>>>(s);
+            break;
+        case KVMEM_TYPE_Q4_0:
+            quant_scatter_kernel<KVMEM_TYPE_Q4_0, Source><<<n_chunks, 256, 0, ctx->stream>>>(s);
+            break;
+        case KVMEM_TYPE_Q5_0:
+            quant_scatter_kernel<KVMEM_TYPE_Q5_0, Source><<<n_chunks, 256, 0, ctx->stream>>>(s);
+            break;
+        case KVMEM_TYPE_F16:
+            quant_scatter_kernel<KVMEM_TYPE_F16, Source><<<n_chunks, 256, 0, ctx->stream>>>(s);
+            break;
+        default:
+            fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported type");
+            return false;
+    }
+    return hip_ok(ctx, hipGetLastError(), "stage-in kernel launch");
+}
+
+static bool aligned16(const void *p) {
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+static int check_pool(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, uint32_t n_layers,
+                      uint32_t block_tokens, uint32_t ek, uint32_t ev, bool want_v) {
+    if (!pool || !pool->k_layers) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "pool: null");
+    }
+    if (pool->n_layers != n_layers || pool->block_tokens != block_tokens ||
+        pool->n_embd_k != ek || (want_v && pool->n_embd_v != ev)) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "pool: geometry does not match the history");
+    }
+    if (!kvmem_hip_quant_ok(pool->type_k) || (want_v && !kvmem_hip_quant_ok(pool->type_v))) {
+        return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "pool: unsupported cache type");
+    }
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        if (!pool->k_layers[l] || !aligned16(pool->k_layers[l]) ||
+            (want_v && (!pool->v_layers[l] || !aligned16(pool->v_layers[l])))) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "pool: layer pointer null or not 16-byte aligned");
+        }
+    }
+    return KVMEM_HIP_OK;
+}
+
+// Device copy of a pool's per-layer pointer tables: K at [0, L), V at [L, 2L).
+static const void *const *upload_layer_tables(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool,
+                                              bool want_v) {
+    std::vector<const void *> t(2 * static_cast<size_t>(pool->n_layers), nullptr);
+    for (uint32_t l = 0; l < pool->n_layers; ++l) {
+        t[l] = pool->k_layers[l];
+        t[pool->n_layers + l] = want_v ? pool->v_layers[l] : nullptr;
+    }
+    return static_cast<const void *const *>(
+        upload(ctx, t.data(), t.size() * sizeof(void *), "stage-in layer tables"));
+}
+
+// Launch one kind (K or V) of a block job.  items_dev: device [n][3].
+static int launch_blocks(kvmem_hip_ctx *ctx, int type, const uint8_t *base, uint64_t block_stride,
+                         uint64_t layer_stride, const void *layer_table_dev, uint32_t n_layers,
+                         uint32_t block_tokens, uint32_t n_embd, const uint32_t *items_dev,
+                         uint32_t n_items) {
+    const uint32_t gpr = n_embd / 32;
+    BlockSource s;
+    s.base = base;
+    s.layer_dst = static_cast<const uint8_t *const *>(layer_table_dev);
+    s.items = items_dev;
+    s.block_stride = block_stride;
+    s.layer_stride = layer_stride;
+    s.n_layers = n_layers;
+    s.block_tokens = block_tokens;
+    s.gpr = gpr;
+    s.row_bytes = gpr * group_bytes(type);
+    s.chunks_per_op = (block_tokens * gpr + kChunkGroups - 1) / kChunkGroups;
+    const uint64_t n_chunks = static_cast<uint64_t>(n_items) * n_layers * s.chunks_per_op;
+    if (n_chunks > 0x7fffffffu) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "stage-in: too many chunks in one call");
+    }
+    return launch_quant(ctx, type, static_cast<uint32_t>(n_chunks), s) ? KVMEM_HIP_OK
+                                                                        : KVMEM_HIP_ERR_RUNTIME;
+}
+
+}  // namespace kvmem_hip
+
+using namespace kvmem_hip;
+
+extern "C" {
+
+int kvmem_hip_stagein_quant(kvmem_hip_ctx *ctx, const kvmem_hip_quant_op *ops, int n_ops) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (n_ops <= 0) {
+        return KVMEM_HIP_OK;
+    }
+    if (!ops) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "stagein_quant: null ops");
+    }
+    (void) hipSetDevice(ctx->device);
+    const int types[4] = {KVMEM_TYPE_Q8_0, KVMEM_TYPE_Q5_0, KVMEM_TYPE_Q4_0, KVMEM_TYPE_F16};
+    for (int i = 0; i < n_ops; ++i) {
+        const kvmem_hip_quant_op &op = ops[i];
+        if (!kvmem_hip_quant_ok(op.type)) {
+            return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stagein_quant: unsupported type");
+        }
+        const uint32_t stride = op.src_stride ? op.src_stride : op.n_embd * 2u;
+        if (op.n_rows == 0) {
+            continue;
+        }
+        if (!op.src || !op.dst || op.n_embd == 0 || op.n_embd % 32 != 0 || !aligned16(op.src) ||
+            !aligned16(op.dst) || stride % 16 != 0 || stride < op.n_embd * 2u) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID,
+                        "stagein_quant: op needs 16-byte aligned src/dst/stride and n_embd % 32 == 0");
+        }
+    }
+    perf_begin(ctx, kPerfSet);
+    for (int type : types) {
+        std::vector<QuantOpDev> dev;
+        uint64_t chunks = 0;
+        for (int i = 0; i < n_ops; ++i) {
+            const kvmem_hip_quant_op &op = ops[i];
+            if (op.type != type || op.n_rows == 0) {
+                continue;
+            }
+            QuantOpDev d;
+            d.src = static_cast<const uint8_t *>(op.src);
+            d.dst = static_cast<uint8_t *>(op.dst);
+            d.gpr = op.n_embd / 32;
+            d.n_groups = op.n_rows * d.gpr;
+            d.src_stride = op.src_stride ? op.src_stride : op.n_embd * 2u;
+            d.chunk0 = static_cast<uint32_t>(chunks);
+            chunks += (d.n_groups + kChunkGroups - 1) / kChunkGroups;
+            dev.push_back(d);
+        }
+        if (dev.empty()) {
+            continue;
+        }
+        if (chunks > 0x7fffffffu) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "stagein_quant: too many chunks");
+        }
+        void *ops_dev = upload(ctx, dev.data(), dev.size() * sizeof(QuantOpDev), "stagein_quant ops");
+        if (!ops_dev) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        OpListSource s{static_cast<const QuantOpDev *>(ops_dev), static_cast<uint32_t>(dev.size())};
+        if (!launch_quant(ctx, type, static_cast<uint32_t>(chunks), s)) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+    }
+    perf_end(ctx, kPerfSet);
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_hip_stagein_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
+                             const kvmem_hip_pool *pool, const uint32_t *block_ids,
+                             const uint32_t *slots, uint32_t n) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (n == 0) {
+        return KVMEM_HIP_OK;
+    }
+    if (!hist || !hist->k || !block_ids || !slots) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "stagein_blocks: null argument");
+    }
+    const bool want_v = hist->v != nullptr && pool && pool->v_layers != nullptr;
+    const uint32_t T = hist->block_tokens;
+    if (T == 0 || hist->n_embd_k % 32 != 0 || (want_v && hist->n_embd_v % 32 != 0) ||
+        !aligned16(hist->k) || (want_v && !aligned16(hist->v))) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "stagein_blocks: bad history geometry/alignment");
+    }
+    int st = check_pool(ctx, pool, hist->n_layers, T, hist->n_embd_k, hist->n_embd_v, want_v);
+    if (st != KVMEM_HIP_OK) {
+        return st;
+    }
+    std::vector<uint32_t> items(3 * static_cast<size_t>(n));
+    for (uint32_t i = 0; i < n; ++i) {
+        if (block_ids[i] >= hist->n_blocks || slots[i] >= pool->n_slots) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "stagein_blocks: block id or slot out of range");
+        }
+        const bool last = block_ids[i] + 1 == hist->n_blocks && hist->last_block_tokens != 0;
+        items[3 * i + 0] = block_ids[i];
+        items[3 * i + 1] = slots[i];
+        items[3 * i + 2] = last ? std::min(hist->last_block_tokens, T) : T;
+    }
+    (void) hipSetDevice(ctx->device);
+    void *items_dev = upload(ctx, items.data(), items.size() * sizeof(uint32_t), "stagein_blocks items");
+    const void *const *tables = upload_layer_tables(ctx, pool, want_v);
+    if (!items_dev || !tables) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    perf_begin(ctx, kPerfSet);
+    const uint64_t bk = static_cast<uint64_t>(T) * hist->n_embd_k * 2u;
+    st = launch_blocks(ctx, pool->type_k, static_cast<const uint8_t *>(hist->k), bk,
+                       bk * hist->n_blocks, tables, hist->n_layers, T, hist->n_embd_k,
+                       static_cast<const uint32_t *>(items_dev), n);
+    if (st == KVMEM_HIP_OK && want_v) {
+        const uint64_t bv = static_cast<uint64_t>(T) * hist->n_embd_v * 2u;
+        st = launch_blocks(ctx, pool->type_v, static_cast<const uint8_t *>(hist->v), bv,
+                           bv * hist->n_blocks, tables + hist->n_layers, hist->n_layers, T, hist->n_embd_v,
+                           static_cast<const uint32_t *>(items_dev), n);
+    }
+    perf_end(ctx, kPerfSet);
+    return st;
+}
+
+int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_history *hist,
+                                  const kvmem_hip_pool *pool, const uint32_t *block_ids,
+                                  const uint32_t *slots, uint32_t n) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (n == 0) {
+        return KVMEM_HIP_OK;
+    }
+    if (!hist || !hist->base || !block_ids || !slots || !pool) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "stagein_blocks_host: null argument");
+    }
+    const uint32_t T = hist->block_tokens;
+    const uint32_t L = hist->n_layers;
+    const bool want_v = hist->n_embd_v != 0 && pool->v_layers != nullptr;
+    if (T == 0 || hist->n_embd_k % 32 != 0 || hist->n_embd_v % 32 != 0) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "stagein_blocks_host: bad geometry");
+    }
+    int st = check_pool(ctx, pool, L, T, hist->n_embd_k, hist->n_embd_v, want_v);
+    if (st != KVMEM_HIP_OK) {
+        return st;
+    }
+    const uint64_t kbytes = static_cast<uint64_t>(T) * hist->n_embd_k * 2u;
+    const uint64_t vbytes = static_cast<uint64_t>(T) * hist->n_embd_v * 2u;
+    const uint64_t layer_bytes = kbytes + vbytes;
+    const uint64_t span = layer_bytes * L;  // one block, every layer, K then V
+    for (uint32_t i = 0; i < n; ++i) {
+        if (block_ids[i] >= hist->n_blocks || slots[i] >= pool->n_slots) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "stagein_blocks_host: block id or slot out of range");
+        }
+    }
+    (void) hipSetDevice(ctx->device);
+    // Device ring: kRing slots of up to 32 MiB (at least one block each).
+    constexpr int kRing = 4;
+    const uint64_t target = 32ull << 20;
+    const uint32_t per_slot = static_cast<uint32_t>(std::max<uint64_t>(1, target / span));
+    const uint64_t slot_bytes = per_slot * span;
+    if (ctx->h2d_slot_bytes != slot_bytes || !ctx->h2d_ring.ptr) {
+        if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "h2d ring sync")) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        if (ctx->h2d_ring.ptr) {
+            hipFree(ctx->h2d_ring.ptr);
+            ctx->h2d_ring.ptr = nullptr;
+            ctx->h2d_ring.bytes = 0;
+        }
+        if (!ensure_dev(ctx, ctx->h2d_ring, slot_bytes * kRing, "h2d ring")) {
+            return KVMEM_HIP_ERR_NOMEM;
+        }
+        ctx->h2d_slot_bytes = slot_bytes;
+        ctx->h2d_slots = kRing;
+    }
+    for (int r = 0; r < kRing; ++r) {
+        if (!ctx->h2d_copied[r]) {
+            if (!hip_ok(ctx, hipEventCreateWithFlags(&ctx->h2d_copied[r], hipEventDisableTiming), "h2d event") ||
+                !hip_ok(ctx, hipEventCreateWithFlags(&ctx->h2d_consumed[r], hipEventDisableTiming), "h2d event")) {
+                return KVMEM_HIP_ERR_RUNTIME;
+            }
+            // a fresh "consumed" marker on the compute stream
+            hipEventRecord(ctx->h2d_consumed[r], ctx->stream);
+        }
+    }
+    const void *const *tables = upload_layer_tables(ctx, pool, want_v);
+    if (!tables) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    perf_begin(ctx, kPerfSet);
+    const uint8_t *host = static_cast<const uint8_t *>(hist->base);
+    uint8_t *ring = static_cast<uint8_t *>(ctx->h2d_ring.ptr);
+    int r = 0;
+    for (uint32_t first = 0; first < n; first += per_slot) {
+        const uint32_t cnt = std::min(per_slot, n - first);
+        uint8_t *slot_base = ring + static_cast<uint64_t>(r) * slot_bytes;
+        // the previous kernel reading this ring slot must be done
+        if (!hip_ok(ctx, hipStreamWaitEvent(ctx->copy_stream, ctx->h2d_consumed[r], 0), "h2d wait consumed")) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        std::vector<uint32_t> items(3 * static_cast<size_t>(cnt));
+        for (uint32_t j = 0; j < cnt; ++j) {
+            const uint32_t b = block_ids[first + j];
+            const uint32_t ntok = (b + 1 == hist->n_blocks && hist->last_block_tokens != 0)
+                                      ? std::min(hist->last_block_tokens, T) : T;
+            if (!hip_ok(ctx, hipMemcpyAsync(slot_base + j * span, host + static_cast<uint64_t>(b) * span,
+                                            span, hipMemcpyHostToDevice, ctx->copy_stream),
+                        "h2d block copy")) {
+                return KVMEM_HIP_ERR_RUNTIME;
+            }
+            ctx->h2d_bytes += span;
+            items[3 * j + 0] = j;
+            items[3 * j + 1] = slots[first + j];
+            items[3 * j + 2] = ntok;
+        }
+        if (!hip_ok(ctx, hipEventRecord(ctx->h2d_copied[r], ctx->copy_stream), "h2d record") ||
+            !hip_ok(ctx, hipStreamWaitEvent(ctx->stream, ctx->h2d_copied[r], 0), "h2d wait copied")) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        void *items_dev = upload(ctx, items.data(), items.size() * sizeof(uint32_t), "h2d items");
+        if (!items_dev) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        st = launch_blocks(ctx, pool->type_k, slot_base, span, layer_bytes, tables, L, T,
+                           hist->n_embd_k, static_cast<const uint32_t *>(items_dev), cnt);
+        if (st == KVMEM_HIP_OK && want_v) {
+            st = launch_blocks(ctx, pool->type_v, slot_base + kbytes, span, layer_bytes, tables + L,
+                               L, T, hist->n_embd_v, static_cast<const uint32_t *>(items_dev), cnt);
+        }
+        if (st != KVMEM_HIP_OK) {
+            return st;
+        }
+        if (!hip_ok(ctx, hipEventRecord(ctx->h2d_consumed[r], ctx->stream), "h2d record consumed")) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        r = (r + 1) % kRing;
+    }
+    perf_end(ctx, kPerfSet);
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const uint32_t *src_slots,
+                         const uint32_t *dst_slots, uint32_t n) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (n == 0) {
+        return KVMEM_HIP_OK;
+    }
+    if (!pool || !pool->k_layers || !src_slots || !dst_slots) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "move_slots: null argument");
+    }
+    const bool want_v = pool->v_layers != nullptr;
+    const uint64_t krow = kvmem_hip_row_size(pool->type_k, pool->n_embd_k);
+    const uint64_t vrow = want_v ? kvmem_hip_row_size(pool->type_v, pool->n_embd_v) : 0;
+    const uint64_t kspan = krow * pool->block_tokens;
+    const uint64_t vspan = vrow * pool->block_tokens;
+    if (kspan == 0 || (want_v && vspan == 0)) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "move_slots: bad pool geometry");
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        if (src_slots[i] >= pool->n_slots || dst_slots[i] >= pool->n_slots) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "move_slots: slot out of range");
+        }
+    }
+    const uint64_t per_move = (kspan + vspan) * pool->n_layers;
+    (void) hipSetDevice(ctx->device);
+    if (!ensure_dev(ctx, ctx->move_scratch, per_move * n, "move_slots scratch")) {
+        return KVMEM_HIP_ERR_NOMEM;
+    }
+    uint8_t *scratch = static_cast<uint8_t *>(ctx->move_scratch.ptr);
+    std::vector<const void *> gs, ss;
+    std::vector<void *> gd, sd;
+    std::vector<size_t> nb;
+    for (uint32_t i = 0; i < n; ++i) {
+        uint8_t *sc = scratch + per_move * i;
+        for (uint32_t l = 0; l < pool->n_layers; ++l) {
+            uint8_t *kb = static_cast<uint8_t *>(pool->k_layers[l]);
+            gs.push_back(kb + src_slots[i] * kspan);
+            gd.push_back(sc);
+            ss.push_back(sc);
+            sd.push_back(kb + dst_slots[i] * kspan);
+            nb.push_back(kspan);
+            sc += kspan;
+            if (want_v) {
+                uint8_t *vb = static_cast<uint8_t *>(pool->v_layers[l]);
+                gs.push_back(vb + src_slots[i] * vspan);
+                gd.push_back(sc);
+                ss.push_back(sc);
+                sd.push_back(vb + dst_slots[i] * vspan);
+                nb.push_back(vspan);
+                sc += vspan;
+            }
+        }
+    }
+    const int nops = static_cast<int>(nb.size());
+    int st = kvmem_hip_d2d_batched(ctx, gs.data(), gd.data(), nb.data(), nops);
+    if (st == KVMEM_HIP_OK) {
+        st = kvmem_hip_d2d_batched(ctx, ss.data(), sd.data(), nb.data(), nops);
+    }
+    return st;
+}
+
+}  // extern "C"

@@ -1,0 +1,122 @@
+/*
+ * kvmem_oracle.h -- CPU restatement of the KVMem reselect path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product library links, loads or
+ * calls this code: only tests/, __graft_entry__.smoke() and the cpu_baseline
+ * leg of bench.py use it, and only as the checker.
+ *
+ * Every function cites the reference file:line whose behaviour it restates
+ * (paths relative to the CrKcel/kvmem-llama.cpp tree).  The ggml quantizers
+ * live in the un-vendored llama.cpp submodule (CrKcel/llama.cpp, branch
+ * kvmem/prism on PrismML prism 9a9394a, see .gitmodules:1-3 and
+ * patches/README.md:3); they are restated from ggml's published
+ * quantize_row_{q8_0,q4_0,q5_0}_ref algorithm and anchored on the
+ * reference's own CUDA restatement (src/adapter/llama-kvmem-stagein.cu:180-233).
+ *
+ * Pinning (what checks each function against something other than itself):
+ *   ko_f32_to_f16 / ko_f16_to_f32 : numpy float16 (IEEE RNE), exhaustive f16.
+ *   ko_quantize_row_*             : golden vectors from an independent numpy
+ *                                   restatement (tests/golden), closed-form
+ *                                   special groups, dequantisation bounds.
+ *   ko_score_pertoken_max         : brute force fp64 numpy on tiny shapes,
+ *                                   permutation / scaling invariants.
+ *   ko_pick_topk                  : the reference kvmem library compiled from
+ *                                   its own sources (oracle/_ref), the
+ *                                   reference's own unit-test cases, sort-based
+ *                                   brute force.
+ */
+#ifndef KVMEM_ORACLE_H
+#define KVMEM_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml_type codes for the formats on this path (ggml.h enum values). */
+enum { KO_TYPE_F32 = 0, KO_TYPE_F16 = 1, KO_TYPE_Q4_0 = 2, KO_TYPE_Q5_0 = 6, KO_TYPE_Q8_0 = 8 };
+
+/* Half precision <-> single precision, IEEE round-to-nearest-even.
+ * raw_kv_store.cpp:22-56 (f32_to_f16) and :58-83 (f16_to_f32). */
+uint16_t ko_f32_to_f16(float f);
+float    ko_f16_to_f32(uint16_t h);
+float    ko_bf16_to_f32(uint16_t h);
+
+/* Bytes of one 32-element group, and of a row of n elements. */
+size_t ko_group_bytes(int type);
+size_t ko_row_bytes(int type, int64_t n);
+
+/* ggml quantize_row_*_ref restated; k must be a multiple of 32.
+ * q8_0: llama-kvmem-stagein.cu:180-198; q4_0: :200-233; q5_0: ggml only. */
+void ko_quantize_row_q8_0(const float *x, uint8_t *y, int64_t k);
+void ko_quantize_row_q4_0(const float *x, uint8_t *y, int64_t k);
+void ko_quantize_row_q5_0(const float *x, uint8_t *y, int64_t k);
+
+/* Dequantisation (inverse maps, used for error-bound invariants).
+ * q8_0 / q4_0: llama-kvmem-stagein.cu:132-157. */
+void ko_dequantize_row(int type, const uint8_t *y, float *x, int64_t k);
+
+/* F16 rows -> packed rows of `type` (F16 rows are converted exactly to f32
+ * first, as ggml_quantize_chunk does; llama-kvmem-quant.h:96-119).
+ * type KO_TYPE_F16 copies the rows unchanged. */
+int ko_quantize_rows_f16(int type, const uint16_t *src, uint8_t *dst,
+                         int64_t n_rows, int64_t n_embd);
+
+/* Stage-in of whole blocks into a slot pool:
+ * src  : [n_blocks][block_tokens][n_embd] f16 (one layer, one of K/V)
+ * slots: slot of each block; pool row (cell) = slot*block_tokens + t
+ *        (llama-kvmem-batch.cpp:48, llama-memory-kvmem.cpp:2742)
+ * pool : n_slots*block_tokens rows of ko_row_bytes(type, n_embd).
+ * Returns 0, or -1 on a bad argument (slot out of range). */
+int ko_stagein_blocks(int type, const uint16_t *src, const uint32_t *slots,
+                      uint32_t n_blocks, uint32_t block_tokens, uint32_t n_embd,
+                      uint8_t *pool, uint32_t n_slots);
+
+/* Per-token max scorer (the retrieval scorer of the reselect step):
+ *   s[l][b] = max_{t, hq, j<n_tok(b)} (q[l][t][hq] . k[l][b][j][hq/g]) / sqrt(D)
+ * q: [L][Tq][Hq][D] f32 (exact image of the bf16 query), k: [L][B][T][Hkv][D]
+ * f16 bits.  Accumulates in double.  layer_scores: [L][B].  The reference
+ * scorer it replaces is mean-K cosine (llama-memory-kvmem.cpp:2869-2916);
+ * GQA head map hq -> hq/g follows :2890-2892.  block_ids (optional) restricts
+ * the computation to the listed blocks (others untouched). */
+void ko_score_pertoken_max(const float *q, const uint16_t *k,
+                           uint32_t L, uint32_t Tq, uint32_t Hq, uint32_t Hkv,
+                           uint32_t D, uint32_t B, uint32_t T,
+                           uint32_t last_block_tokens,
+                           const uint32_t *block_ids, uint32_t n_ids,
+                           double *layer_scores);
+
+/* Same computation with fp32 accumulation, written for speed: the CPU
+ * baseline of the scoring step (not a checker).  n_threads <= 0 = all. */
+void ko_score_pertoken_max_f32(const float *q, const uint16_t *k,
+                               uint32_t L, uint32_t Tq, uint32_t Hq, uint32_t Hkv,
+                               uint32_t D, uint32_t B, uint32_t T,
+                               uint32_t b_begin, uint32_t b_end,
+                               float *layer_scores, int n_threads);
+
+/* Layer combination of per-layer scores into one score per block:
+ * mode 0 = mean (layer averaging as llama-memory-kvmem.cpp:2910-2913),
+ * 1 = max, 2 = sum. */
+void ko_combine_layers(const double *layer_scores, uint32_t L, uint32_t B,
+                       int mode, double *scores);
+
+/* Top-k selection of KvMemStore::pick_topk_ungrouped (TopK policy),
+ * kvmem_store.cpp:482-623: keep [0,sink), then mandatory ids newest-first,
+ * then the last `recent` ids, then the best remaining scores; returns the
+ * kept ids ascending in out (capacity n), count in *n_out.
+ * tie_lower_index = 1: equal scores prefer the LOWER id (reselect contract);
+ *                   0: equal scores prefer the higher id (kvmem_store.cpp:602-609). */
+void ko_pick_topk(const double *scores, uint32_t n, uint32_t budget,
+                  uint32_t sink, uint32_t recent,
+                  const uint32_t *mandatory, uint32_t n_mandatory,
+                  int tie_lower_index, uint32_t *out, uint32_t *n_out);
+
+/* Number of OpenMP threads the oracle uses (for the baseline's core count). */
+int ko_max_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,113 @@
+"""MFMA per-token max scorer vs the fp64 oracle (1e-3 relative, fp32
+accumulation on the GPU), plus the full 16-layer x 2048-block scoring
+workload checked on sampled blocks and through its top-k."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from conftest import load_pkg  # noqa: E402
+
+kv = load_pkg()
+from kvmem_amd import workloads  # noqa: E402
+
+RTOL = 1e-3
+
+
+def announce(msg: str) -> None:
+    print(f"[score] {msg}", flush=True)
+
+
+def run_score(ctx, k, q, q_type, Hq, Hkv, D, last_T=0, reduce=kv.LAYER_MEAN):
+    L, B, T = k.shape[0], k.shape[1], k.shape[2]
+    scores = torch.empty(B, dtype=torch.float32, device="cuda")
+    layer = torch.empty((L, B), dtype=torch.float32, device="cuda")
+    hist = ctx.make_history(k.data_ptr(), None, L, B, T, Hkv * D, 0, last_T)
+    torch.cuda.synchronize()
+    ctx.score(hist, q.data_ptr(), q_type, q.shape[1], Hq, Hkv, D, scores.data_ptr(), layer.data_ptr(),
+              reduce)
+    ctx.sync()
+    return scores.cpu().numpy().astype(np.float64), layer.cpu().numpy().astype(np.float64)
+
+
+def q_f32(q) -> np.ndarray:
+    return q.float().cpu().numpy()
+
+
+def assert_close(got, want, what):
+    err = np.abs(got - want) / np.maximum(np.abs(want), 1e-6)
+    i = int(np.argmax(err))
+    assert err.max() <= RTOL, f"{what}: max rel err {err.max():.3e} at {i}: got {got.flat[i]} want {want.flat[i]}"
+
+
+@pytest.mark.parametrize("D,Tq,q_dtype,last_T", [
+    (256, 16, "bf16", 77),
+    (256, 80, "bf16", 0),      # 480 query rows: two 384-row slices
+    (128, 64, "f16", 5),
+    (256, 7, "f16", 128),
+])
+def test_score_small_vs_fp64_oracle(ctx, oracle, D, Tq, q_dtype, last_T):
+    announce(f"small scorer D={D} Tq={Tq} q={q_dtype} last_T={last_T}")
+    L, B, T, Hkv, Hq = 2, 19, 128, 4, 24
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=Tq, seed=3 + D + Tq, D=D)
+    qt = kv.TYPE_BF16
+    if q_dtype == "f16":
+        q = q.to(torch.float16)
+        qt = kv.TYPE_F16
+    s, ls = run_score(ctx, k, q, qt, Hq, Hkv, D, last_T)
+    want_ls = oracle.score_pertoken_max(q_f32(q), workloads.to_bits(torch, k), last_T)
+    assert_close(ls, want_ls, "layer scores")
+    assert_close(s, oracle.combine_layers(want_ls, 0), "mean scores")
+
+
+@pytest.mark.parametrize("mode", [kv.LAYER_MEAN, kv.LAYER_MAX, kv.LAYER_SUM])
+def test_score_layer_reduce_modes(ctx, oracle, mode):
+    announce(f"layer reduce mode {mode}")
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=3, B=9, Tq=8, seed=17)
+    s, ls = run_score(ctx, k, q, kv.TYPE_BF16, 24, 4, 256, reduce=mode)
+    want = oracle.combine_layers(oracle.score_pertoken_max(q_f32(q), workloads.to_bits(torch, k)), mode)
+    assert_close(s, want, f"mode {mode}")
+
+
+def test_score_invariants(ctx):
+    """Permuting tokens inside a block and query heads inside a GQA group
+    leaves scores unchanged; scaling Q by 2 scales them by 2."""
+    announce("scorer invariants")
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=2, B=6, Tq=8, seed=23)
+    base, _ = run_score(ctx, k, q, kv.TYPE_BF16, 24, 4, 256)
+    perm = torch.randperm(128, generator=torch.Generator().manual_seed(1)).cuda()
+    s1, _ = run_score(ctx, k[:, :, perm].contiguous(), q, kv.TYPE_BF16, 24, 4, 256)
+    assert np.array_equal(s1, base) or np.allclose(s1, base, rtol=1e-6, atol=0)
+    hp = torch.tensor([5, 4, 3, 2, 1, 0] + list(range(6, 24)), device="cuda")
+    s2, _ = run_score(ctx, k, q[:, :, hp].contiguous(), kv.TYPE_BF16, 24, 4, 256)
+    assert np.allclose(s2, base, rtol=1e-6, atol=0)
+    s3, _ = run_score(ctx, k, (q.float() * 2).to(torch.bfloat16), kv.TYPE_BF16, 24, 4, 256)
+    assert np.allclose(s3, 2 * base, rtol=1e-6, atol=0)
+
+
+def test_score_full_256k_sampled_and_topk(ctx, oracle):
+    """16 layers x 2048 blocks x 64-token query: every block scored on the
+    GPU; 6 sampled blocks checked against the fp64 oracle; the device top-256
+    (sink 0, ties to the lower id) equal to the oracle's top-k over the same
+    scores."""
+    announce("full scoring workload 16 x 2048 blocks")
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=16, B=2048, Tq=64, seed=2)
+    s, ls = run_score(ctx, k, q, kv.TYPE_BF16, 24, 4, 256)
+    assert np.isfinite(s).all()
+    rng = np.random.default_rng(0)
+    ids = np.sort(rng.choice(2048, 6, replace=False)).astype(np.uint32)
+    ksub = workloads.to_bits(torch, k[:, torch.from_numpy(ids.astype(np.int64)).cuda()])
+    want = oracle.score_pertoken_max(q_f32(q), ksub)
+    assert_close(ls[:, ids], want, "sampled layer scores")
+    assert_close(s[ids], want.mean(axis=0), "sampled mean scores")
+    scores_dev = torch.from_numpy(s.astype(np.float32)).cuda()
+    torch.cuda.synchronize()
+    sel = ctx.topk(scores_dev.data_ptr(), 2048, 255, forced=[0], tie_lower_index=True)
+    want_sel = oracle.pick_topk(s.astype(np.float32).astype(np.float64), 256, sink=1)
+    assert sel == want_sel
+    del k
+    torch.cuda.empty_cache()

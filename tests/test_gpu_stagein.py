@@ -1,0 +1,219 @@
+"""Stage-in quantize-scatter on the GPU vs the oracle: bit-exact pool bytes.
+
+Covers the single-layer q8_0 stage-in workload (64 blocks x 128 tokens x
+4 heads x 256, outlier channels, seeded slot permutation), heavy-tailed
+q4_0 / q5_0 / q8_0 / F16, partial last blocks, strided op sources, crafted
+special groups (zeros, -0, half-way codes, first-index sign ties, f16
+extremes, subnormal scales) and that untouched pool rows keep their bytes.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from conftest import load_pkg  # noqa: E402
+
+kv = load_pkg()
+from kvmem_amd import workloads  # noqa: E402
+
+SENTINEL = 0xA5
+TYPES = [kv.TYPE_Q8_0, kv.TYPE_Q5_0, kv.TYPE_Q4_0, kv.TYPE_F16]
+
+
+def dev_bits(a: np.ndarray):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()
+
+
+def new_pool(n_slots: int, T: int, row_bytes: int):
+    return torch.full((n_slots * T * row_bytes,), SENTINEL, dtype=torch.uint8, device="cuda")
+
+
+def expected_pool(oracle, type_, blocks: np.ndarray, slots, n_slots, T, ntoks=None):
+    """Sentinel pool with block i's rows quantized at slot slots[i]."""
+    E = blocks.shape[-1]
+    rb = oracle.row_bytes(type_, E)
+    out = np.full((n_slots * T, rb), SENTINEL, dtype=np.uint8)
+    for i, s in enumerate(slots):
+        nt = T if ntoks is None else ntoks[i]
+        out[s * T: s * T + nt] = oracle.quantize_rows_f16(type_, blocks[i, :nt])
+    return out
+
+
+def first_diff(a: np.ndarray, b: np.ndarray) -> str:
+    idx = np.flatnonzero(a.ravel() != b.ravel())
+    if idx.size == 0:
+        return "identical"
+    i = int(idx[0])
+    return f"{idx.size} bytes differ; first at byte {i}: got {a.ravel()[i]:#x} want {b.ravel()[i]:#x}"
+
+
+def announce(msg: str) -> None:
+    print(f"[stagein] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def test_stagein_1layer_q8_0_bit_exact(ctx, oracle):
+    announce("1-layer q8_0 stage-in, 64 blocks -> permuted slots of 256")
+    K, V, slots = workloads.stagein_1layer(seed=1)
+    nb, T, E = K.shape
+    kd, vd = dev_bits(K), dev_bits(V)
+    rb = kv.row_size(kv.TYPE_Q8_0, E)
+    pk, pv = new_pool(256, T, rb), new_pool(256, T, rb)
+    hist = ctx.make_history(kd.data_ptr(), vd.data_ptr(), 1, nb, T, E, E)
+    pool = ctx.make_pool(1, 256, T, E, E, kv.TYPE_Q8_0, kv.TYPE_Q8_0, [pk.data_ptr()], [pv.data_ptr()])
+    torch.cuda.synchronize()
+    ctx.stagein_blocks(hist, pool, list(range(nb)), slots.tolist())
+    ctx.sync()
+    for name, src, p in (("K", K, pk), ("V", V, pv)):
+        got = p.cpu().numpy().reshape(256 * T, rb)
+        want = expected_pool(oracle, kv.TYPE_Q8_0, src, slots, 256, T)
+        assert np.array_equal(got, want), f"{name}: {first_diff(got, want)}"
+
+
+@pytest.mark.parametrize("type_", TYPES)
+def test_stagein_heavy_tailed_multilayer_partial(ctx, oracle, type_):
+    announce(f"heavy-tailed 3-layer stage-in type={type_}, partial last block")
+    L, B, T, Ek, Ev = 3, 9, 128, 1024, 512
+    last = 77
+    Kh = workloads.heavy_tailed(11 + type_, (L, B, T, Ek))
+    Vh = workloads.heavy_tailed(31 + type_, (L, B, T, Ev))
+    ids = [8, 0, 5, 3]           # includes the partial last block
+    n_slots = 12
+    slots = [11, 2, 7, 0]
+    kd, vd = dev_bits(Kh), dev_bits(Vh)
+    rbk, rbv = kv.row_size(type_, Ek), kv.row_size(type_, Ev)
+    pks = [new_pool(n_slots, T, rbk) for _ in range(L)]
+    pvs = [new_pool(n_slots, T, rbv) for _ in range(L)]
+    hist = ctx.make_history(kd.data_ptr(), vd.data_ptr(), L, B, T, Ek, Ev, last)
+    pool = ctx.make_pool(L, n_slots, T, Ek, Ev, type_, type_, [p.data_ptr() for p in pks],
+                         [p.data_ptr() for p in pvs])
+    torch.cuda.synchronize()
+    ctx.stagein_blocks(hist, pool, ids, slots)
+    ctx.sync()
+    ntoks = [last if b == B - 1 else T for b in ids]
+    for l in range(L):
+        for name, src, p, rb in (("K", Kh, pks[l], rbk), ("V", Vh, pvs[l], rbv)):
+            got = p.cpu().numpy().reshape(n_slots * T, rb)
+            want = expected_pool(oracle, type_, src[l][ids], slots, n_slots, T, ntoks)
+            assert np.array_equal(got, want), f"layer {l} {name}: {first_diff(got, want)}"
+
+
+def special_rows(E: int = 1024) -> np.ndarray:
+    """128 rows of crafted groups (f16 bits), remaining groups random."""
+    rng = np.random.default_rng(7)
+    rows = workloads.f16_bits(rng.standard_normal((128, E), dtype=np.float32))
+    groups = []
+    groups.append(np.zeros(32, np.float32))                                 # all zero
+    g = np.zeros(32, np.float32); g[0] = -0.0; groups.append(g)             # -0 first
+    g = np.zeros(32, np.float32)
+    g[:8] = [127, 2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 126.5]; groups.append(g)  # q8 half-way
+    g = np.zeros(32, np.float32); g[2] = -3.0; g[5] = 3.0; groups.append(g)  # sign tie, neg first
+    g = np.zeros(32, np.float32); g[2] = 3.0; g[5] = -3.0; groups.append(g)  # sign tie, pos first
+    g = np.zeros(32, np.float32); g[31] = -8.0; g[0] = 7.5; g[1] = 0.5; g[2] = -0.5; groups.append(g)
+    g = np.zeros(32, np.float32); g[31] = -16.0; g[:6] = [15.5, 0.5, -0.5, 1.5, 7.5, -15.5]; groups.append(g)
+    g = np.zeros(32, np.float32); g[3] = 65504.0; g[4] = -65504.0; g[5] = 1.0; groups.append(g)
+    gb = np.zeros(32, np.uint16); gb[9] = 0x0001                             # 2^-24 only
+    gb_rows = [gb]
+    gb = np.zeros(32, np.uint16); gb[0] = 0x8001; gb[1] = 0x0001; gb_rows.append(gb)  # +-min subnormal
+    gb = (rng.integers(0, 0x0400, 32)).astype(np.uint16); gb_rows.append(gb)          # subnormal group
+    g = (rng.standard_normal(32) * 1e-6).astype(np.float32); groups.append(g)        # tiny scale
+    g = np.full(32, 0.75, np.float32); groups.append(g)                               # constant
+    g = np.full(32, -1.0, np.float32); g[::2] = 1.0; groups.append(g)                 # +-1 alternating
+    all_groups = [workloads.f16_bits(x) for x in groups] + gb_rows
+    for i, gbits in enumerate(all_groups):
+        r, c = divmod(i, E // 32)
+        rows[r, c * 32:(c + 1) * 32] = gbits
+        # the same group again at the last column of a later row
+        rows[64 + i, E - 32:] = gbits
+    return rows
+
+
+@pytest.mark.parametrize("type_", TYPES)
+def test_stagein_special_groups(ctx, oracle, type_):
+    announce(f"special groups type={type_}")
+    rows = special_rows()
+    T, E = rows.shape
+    src = dev_bits(rows)
+    rb = kv.row_size(type_, E)
+    out = torch.full((T * rb,), SENTINEL, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    ctx.stagein_quant([(src.data_ptr(), out.data_ptr(), T, E, type_)])
+    ctx.sync()
+    got = out.cpu().numpy().reshape(T, rb)
+    want = oracle.quantize_rows_f16(type_, rows)
+    assert np.array_equal(got, want), first_diff(got, want)
+
+
+def test_stagein_ops_strided_mixed_types(ctx, oracle):
+    announce("op list: strided sources, mixed types in one call")
+    rng = np.random.default_rng(3)
+    E = 512
+    buf = workloads.f16_bits(rng.standard_normal((40, 2 * E), dtype=np.float32) * 3)
+    src = dev_bits(buf)
+    stride = 2 * E * 2
+    outs, ops, want = [], [], []
+    for i, (type_, r0, nr) in enumerate([(kv.TYPE_Q8_0, 0, 17), (kv.TYPE_Q4_0, 5, 33),
+                                         (kv.TYPE_Q5_0, 3, 1), (kv.TYPE_F16, 9, 31),
+                                         (kv.TYPE_Q8_0, 20, 20)]):
+        rb = kv.row_size(type_, E)
+        o = torch.full((nr * rb,), SENTINEL, dtype=torch.uint8, device="cuda")
+        outs.append(o)
+        col = (i % 2) * E          # left or right half of each row
+        ops.append((src.data_ptr() + r0 * stride + col * 2, o.data_ptr(), nr, E, type_, stride))
+        want.append(oracle.quantize_rows_f16(type_, buf[r0:r0 + nr, col:col + E]))
+    torch.cuda.synchronize()
+    ctx.stagein_quant(ops)
+    ctx.sync()
+    for o, w in zip(outs, want):
+        got = o.cpu().numpy().reshape(w.shape)
+        assert np.array_equal(got, w), first_diff(got, w)
+
+
+def test_stagein_rejects_bad_arguments(ctx):
+    announce("argument validation")
+    a = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    with pytest.raises(kv.KvMemError):
+        ctx.stagein_quant([(a.data_ptr() + 2, a.data_ptr(), 1, 64, kv.TYPE_Q8_0)])  # misaligned
+    with pytest.raises(kv.KvMemError):
+        ctx.stagein_quant([(a.data_ptr(), a.data_ptr(), 1, 48, kv.TYPE_Q8_0)])      # n_embd % 32
+    with pytest.raises(kv.KvMemError):
+        ctx.stagein_quant([(a.data_ptr(), a.data_ptr(), 1, 64, 3)])                 # q4_1
+    hist = ctx.make_history(a.data_ptr(), None, 1, 1, 1, 64, 0)
+    pool = ctx.make_pool(1, 2, 1, 64, 0, kv.TYPE_Q8_0, kv.TYPE_Q8_0, [a.data_ptr()], None)
+    with pytest.raises(kv.KvMemError):
+        ctx.stagein_blocks(hist, pool, [0], [2])                                    # slot range
+    with pytest.raises(kv.KvMemError):
+        ctx.stagein_blocks(hist, pool, [1], [0])                                    # block range
+
+
+def test_move_slots_overlapping(ctx):
+    announce("move_slots with overlapping source/destination slots")
+    L, n_slots, T, E = 2, 8, 16, 256
+    rb = kv.row_size(kv.TYPE_Q8_0, E)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    pk = [torch.randint(0, 256, (n_slots * T * rb,), dtype=torch.uint8, device="cuda", generator=g)
+          for _ in range(L)]
+    pv = [torch.randint(0, 256, (n_slots * T * rb,), dtype=torch.uint8, device="cuda", generator=g)
+          for _ in range(L)]
+    before_k = [p.cpu().numpy().reshape(n_slots, -1).copy() for p in pk]
+    before_v = [p.cpu().numpy().reshape(n_slots, -1).copy() for p in pv]
+    pool = ctx.make_pool(L, n_slots, T, E, E, kv.TYPE_Q8_0, kv.TYPE_Q8_0,
+                         [p.data_ptr() for p in pk], [p.data_ptr() for p in pv])
+    src, dst = [1, 2, 3, 6], [0, 1, 2, 3]     # a left shift chain + a jump
+    torch.cuda.synchronize()
+    ctx.move_slots(pool, src, dst)
+    ctx.sync()
+    for l in range(L):
+        for before, p in ((before_k[l], pk[l]), (before_v[l], pv[l])):
+            want = before.copy()
+            for s, d in zip(src, dst):
+                want[d] = before[s]
+            got = p.cpu().numpy().reshape(n_slots, -1)
+            assert np.array_equal(got, want)

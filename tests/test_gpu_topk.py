@@ -1,0 +1,77 @@
+"""Device top-k vs the oracle's KvMemStore top-k restatement (same f32
+scores in, identical ids out), ties in both tie modes, forced ids."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from conftest import load_pkg  # noqa: E402
+
+kv = load_pkg()
+
+
+def announce(msg: str) -> None:
+    print(f"[topk] {msg}", flush=True)
+
+
+def dev(a: np.ndarray):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+
+
+@pytest.mark.parametrize("n,budget", [(1, 1), (7, 3), (100, 37), (2048, 256), (2049, 256),
+                                      (8192, 512), (16384, 4096), (300, 299)])
+def test_topk_sink_matches_oracle(ctx, oracle, n, budget):
+    announce(f"n={n} budget={budget}")
+    rng = np.random.default_rng(n + budget)
+    s = rng.standard_normal(n).astype(np.float32)
+    d = dev(s)
+    torch.cuda.synchronize()
+    need = max(0, budget - 1) if n > budget else n
+    forced = [0] if n > budget else []
+    got = ctx.topk(d.data_ptr(), n, need, forced=forced)
+    want = oracle.pick_topk(s.astype(np.float64), budget, sink=1)
+    assert got == want
+
+
+@pytest.mark.parametrize("tie_lower", [True, False])
+def test_topk_ties(ctx, oracle, tie_lower):
+    announce(f"ties tie_lower={tie_lower}")
+    rng = np.random.default_rng(9)
+    n = 3000
+    s = rng.integers(-3, 4, n).astype(np.float32) * 0.5  # 7 distinct values
+    s[rng.choice(n, 20, replace=False)] = -0.0
+    d = dev(s)
+    torch.cuda.synchronize()
+    got = ctx.topk(d.data_ptr(), n, 700, forced=[0, 1], tie_lower_index=tie_lower)
+    want = oracle.pick_topk(s.astype(np.float64), 702, sink=2, tie_lower_index=tie_lower)
+    assert got == want
+
+
+def test_topk_forced_mandatory_recent(ctx, oracle):
+    """Forced = sink + mandatory + recent as the store charges them."""
+    announce("forced sink/mandatory/recent")
+    rng = np.random.default_rng(5)
+    n, budget, sink, recent = 1000, 64, 2, 3
+    mand = [700, 701, 702, 999]
+    s = rng.standard_normal(n).astype(np.float32)
+    want = oracle.pick_topk(s.astype(np.float64), budget, sink=sink, recent=recent, mandatory=mand)
+    forced = sorted(set(list(range(sink)) + mand + [n - 1 - i for i in range(recent)]))
+    d = dev(s)
+    torch.cuda.synchronize()
+    got = ctx.topk(d.data_ptr(), n, budget - len(forced), forced=forced)
+    assert got == want
+
+
+def test_topk_need_exceeds_candidates(ctx):
+    announce("need > candidates")
+    s = np.arange(10, dtype=np.float32)
+    d = dev(s)
+    torch.cuda.synchronize()
+    assert ctx.topk(d.data_ptr(), 10, 50, forced=[3]) == list(range(10))
+    assert ctx.topk(d.data_ptr(), 10, 0, forced=[3, 7]) == [3, 7]
+    with pytest.raises(kv.KvMemError):
+        ctx.topk(d.data_ptr(), 10, 1, forced=[10])
