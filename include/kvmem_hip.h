@@ -130,9 +130,10 @@ KVMEM_HIP_API int kvmem_hip_stagein_quant(kvmem_hip_ctx *ctx,
                                           int n_ops);
 
 /* Device-resident F16 block history: for each of K and V, the layer-major
- * array [n_layers][n_blocks][block_tokens][n_embd] of halves (one 128-token
- * block of one layer is contiguous, as RawKvStore keeps it per
- * (block, layer), raw_kv_store.hpp:98-117).  v may be NULL (K only). */
+ * array [n_layers][capacity_blocks][block_tokens][n_embd] of halves (one
+ * 128-token block of one layer is contiguous, as RawKvStore keeps it per
+ * (block, layer), raw_kv_store.hpp:98-117), of which blocks
+ * [0, n_blocks) hold history.  v may be NULL (K only). */
 typedef struct kvmem_hip_history {
     const void *k;
     const void *v;
@@ -142,6 +143,7 @@ typedef struct kvmem_hip_history {
     uint32_t n_embd_k;
     uint32_t n_embd_v;
     uint32_t last_block_tokens; /* tokens in block n_blocks-1 (0 = full) */
+    uint32_t capacity_blocks;   /* blocks per layer in memory (0 = n_blocks) */
 } kvmem_hip_history;
 
 /* Slot pool: per layer one K and one V tensor of n_slots*block_tokens rows

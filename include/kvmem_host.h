@@ -1,0 +1,193 @@
+/*
+ * kvmem_host.h -- C ABI of the reselect engine: the per-agent-step
+ * score -> top-k -> diff -> stage-in path of the reference adapter,
+ * driving the gfx950 kernels of kvmem_hip.h.
+ *
+ * It replaces, for this path, llama_memory_kvmem's preview_retrieval /
+ * apply_selection / apply_retrieval (src/adapter/llama-memory-kvmem.cpp:
+ * 3047-3067, 3139-3263; C API llama_kvmem_preview_retrieval /
+ * llama_kvmem_apply_selection / llama_kvmem_apply_retrieval,
+ * src/adapter/llama-kvmem-hooks.h:100,149-160) together with the host
+ * library calls they make (KvMemStore::set_retrieval_scores,
+ * pick_topk_blocks, set_selection; KvMemRuntime::prepare_selection,
+ * spill_outgoing, admit_incoming; kvmem/src/host/kvmem_store.cpp,
+ * kvmem_runtime.cpp).  The two-phase shape is kept: preview returns a
+ * selection stamped with an epoch and the history row count, apply rejects
+ * a stale one (KVMEM_HIP_ERR_STALE; the reference throws
+ * std::runtime_error("stale KVMem selection"), llama-memory-kvmem.cpp:
+ * 3144-3147).
+ *
+ * Also exported: the host store alone (kvmem_store_*), with no device, for
+ * callers and tests that exercise selection and diff semantics.
+ *
+ * Lifetimes: history pointers (device K/V, pinned host blocks) and query
+ * pointers are borrowed; the caller keeps them valid until the call that
+ * uses them returns (preview and apply synchronise the engine's stream
+ * before returning).  Pool memory is owned by the engine.  An engine is
+ * not re-entrant: one engine per host thread.
+ */
+#ifndef KVMEM_HOST_H
+#define KVMEM_HOST_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "kvmem_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------ selection & plan */
+
+/* Counters of one applied selection (KvMemPlan, kvmem_store.hpp:108-124,
+ * plus the device work it caused). */
+typedef struct kvmem_plan_stats {
+    uint32_t n_stage_in;               /* blocks entering the working set */
+    uint32_t n_stage_out;              /* resident blocks leaving it */
+    uint32_t n_staged;                 /* blocks quantized into the pool */
+    uint32_t n_moved;                  /* resident blocks moved (canonical layout) */
+    uint32_t selection_overlap_blocks;
+    uint32_t gpu_reused_blocks;
+    uint32_t retained_position_stable;
+    uint32_t retained_position_moved;
+    uint32_t total_window_tokens;
+} kvmem_plan_stats;
+
+/* ----------------------------------------------------------- host store */
+
+typedef struct kvmem_store kvmem_store;
+
+/* Store with block_tokens per block and a budget of budget_blocks, keeping
+ * sink_blocks first and recent_blocks last blocks (KvMemStoreConfig,
+ * kvmem_store.hpp:223-232).  tie_lower_index = 1 ranks equal scores by
+ * lower block id; 0 by higher id as the reference (kvmem_store.cpp:602-609).
+ * The store has a slot pool of n_slots (LIFO, llama-memory-kvmem.cpp:
+ * 621-627, 693-707) and every registered block starts outside the pool. */
+KVMEM_HIP_API int kvmem_store_create(uint32_t block_tokens, uint32_t budget_blocks,
+                                     uint32_t sink_blocks, uint32_t recent_blocks,
+                                     int tie_lower_index, uint32_t n_slots,
+                                     kvmem_store **out);
+KVMEM_HIP_API void kvmem_store_destroy(kvmem_store *s);
+/* KvMemStore::register_append (kvmem_store.cpp:179-205). */
+KVMEM_HIP_API int kvmem_store_register_append(kvmem_store *s, uint32_t n_tokens);
+/* KvMemRuntime::truncate_to (kvmem_runtime.cpp:75-92): frees pool slots. */
+KVMEM_HIP_API int kvmem_store_truncate_to(kvmem_store *s, uint32_t token_pos);
+KVMEM_HIP_API uint32_t kvmem_store_block_count(const kvmem_store *s);
+KVMEM_HIP_API uint32_t kvmem_store_total_tokens(const kvmem_store *s);
+/* KvMemStore::set_retrieval_scores (kvmem_store.cpp:242-248). */
+KVMEM_HIP_API int kvmem_store_set_scores(kvmem_store *s, const double *scores, uint32_t n);
+/* KvMemStore::pick_topk_blocks(mandatory) (kvmem_store.cpp:482-623):
+ * ascending ids into out (capacity block count). */
+KVMEM_HIP_API int kvmem_store_pick_topk(kvmem_store *s, const uint32_t *mandatory,
+                                        uint32_t n_mandatory, uint32_t *out, uint32_t *n_out);
+/* prepare_selection + finish_reselect (kvmem_runtime.cpp:108-113,
+ * 223-236): the diff, then slots freed for stage-out and allocated for
+ * stage-in.  stage_in / stage_out (capacity block count each) receive the
+ * plan's lists. */
+KVMEM_HIP_API int kvmem_store_apply(kvmem_store *s, const uint32_t *sel, uint32_t n_sel,
+                                    uint32_t *stage_in, uint32_t *n_in, uint32_t *stage_out,
+                                    uint32_t *n_out, kvmem_plan_stats *stats);
+/* Per block: pool slot (-1 = none), tier (0 GPU, 1 CPU), in-working-set
+ * flag, baked window position.  Arrays of block count entries. */
+KVMEM_HIP_API int kvmem_store_blocks(const kvmem_store *s, int32_t *gpu_slot, uint8_t *tier,
+                                     uint8_t *in_ws, int64_t *baked_pos);
+/* KvMemStore::commit_resident_selection (kvmem_store.cpp:884-895):
+ * 1 if committed, 0 if refused. */
+KVMEM_HIP_API int kvmem_store_commit_resident(kvmem_store *s, const uint32_t *sel, uint32_t n);
+
+/* ------------------------------------------------------ reselect engine */
+
+typedef struct kvmem_engine kvmem_engine;
+
+typedef struct kvmem_engine_params {
+    int32_t device;            /* HIP ordinal */
+    uint32_t n_layers;         /* attention layers */
+    uint32_t block_tokens;     /* --kvmem-block-tokens (<= 128) */
+    uint32_t n_head;           /* query heads */
+    uint32_t n_head_kv;        /* KV heads */
+    uint32_t head_dim;         /* 128 or 256 */
+    uint32_t n_embd_v;         /* V row elements (0 = n_head_kv*head_dim) */
+    uint32_t budget_blocks;    /* --kvmem-budget / block_tokens */
+    uint32_t reserve_blocks;   /* --kvmem-gen-reserve / block_tokens */
+    uint32_t sink_blocks;      /* default 1 (llama-memory-kvmem.cpp:295-297) */
+    uint32_t recent_blocks;    /* default 0 */
+    int32_t type_k;            /* KVMEM_TYPE_Q8_0 / Q5_0 / Q4_0 / F16 (-ctk) */
+    int32_t type_v;            /* (-ctv) */
+    int32_t tie_lower_index;   /* 1: equal scores -> lower id first */
+    int32_t layer_reduce;      /* kvmem_hip_layer_reduce */
+    int32_t canonical_layout;  /* 1: selected block i (ascending) lives in
+                                  slot i after apply, as
+                                  layout_gpu_slots_by_orig_pos
+                                  (llama-memory-kvmem.cpp:931-1254) */
+} kvmem_engine_params;
+
+/* Defaults: 16 layers, 128-token blocks, 24/4 heads x 256, budget 256 +
+ * reserve 128 blocks, sink 1, recent 0, q8_0 K and V, lower-id ties, mean
+ * layer reduce, free-list (non-canonical) layout. */
+KVMEM_HIP_API kvmem_engine_params kvmem_engine_default_params(void);
+
+/* Create the engine: its kvmem_hip_ctx, the slot pool of
+ * (budget + reserve) slots per layer for K and V (kv_size = budget +
+ * gen_reserve blocks, llama-memory-kvmem.cpp:363-426) and the store. */
+KVMEM_HIP_API int kvmem_engine_create(const kvmem_engine_params *p, kvmem_engine **out);
+KVMEM_HIP_API void kvmem_engine_destroy(kvmem_engine *e);
+KVMEM_HIP_API const char *kvmem_engine_last_error(const kvmem_engine *e);
+/* The device context (stream, perf counters) the engine runs on. */
+KVMEM_HIP_API kvmem_hip_ctx *kvmem_engine_ctx(kvmem_engine *e);
+
+/* Device-resident F16 history: K and V [n_layers][capacity_blocks]
+ * [block_tokens][n_embd] (K doubles as the scorer's key mirror).  The
+ * store's block table is brought to n_tokens tokens (register_append /
+ * truncate_to); capacity_blocks bounds later appends.  Bumps the epoch. */
+KVMEM_HIP_API int kvmem_engine_set_device_history(kvmem_engine *e, const void *k, const void *v,
+                                                  uint32_t capacity_blocks, uint32_t n_tokens);
+/* Pinned host history, block-major (see kvmem_hip_host_history): when
+ * set, stage-in reads changed blocks from it over PCIe instead of from the
+ * device history.  NULL clears it. */
+KVMEM_HIP_API int kvmem_engine_set_host_history(kvmem_engine *e, const void *pinned_base,
+                                                uint32_t capacity_blocks);
+/* The history grew (caller wrote the new tokens): register_append.
+ * Bumps the epoch. */
+KVMEM_HIP_API int kvmem_engine_append_tokens(kvmem_engine *e, uint32_t n_new_tokens);
+/* Rewind to token_pos tokens (truncate_to); frees their pool slots. */
+KVMEM_HIP_API int kvmem_engine_truncate_to(kvmem_engine *e, uint32_t token_pos);
+
+KVMEM_HIP_API uint32_t kvmem_engine_block_count(const kvmem_engine *e);
+KVMEM_HIP_API uint32_t kvmem_engine_total_tokens(const kvmem_engine *e);
+KVMEM_HIP_API uint64_t kvmem_engine_epoch(const kvmem_engine *e);
+/* Pool slots and per-layer device pool tensors. */
+KVMEM_HIP_API uint32_t kvmem_engine_n_slots(const kvmem_engine *e);
+KVMEM_HIP_API int kvmem_engine_pool_layer(const kvmem_engine *e, uint32_t layer, void **k,
+                                          void **v);
+/* Slot of every block (-1 = not in the pool), block count entries. */
+KVMEM_HIP_API int kvmem_engine_block_slots(const kvmem_engine *e, int32_t *slots);
+
+/* Phase 1 (preview_retrieval): score every block with the per-token max
+ * scorer over q (device [n_layers][n_q_tokens][n_head][head_dim], bf16 or
+ * f16), then top-k with sink / mandatory (host ids, newest last) / recent
+ * charged first.  Writes the ascending selection (capacity block count),
+ * its epoch and rows (history tokens). */
+KVMEM_HIP_API int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type,
+                                       uint32_t n_q_tokens, const uint32_t *mandatory,
+                                       uint32_t n_mandatory, uint32_t *sel, uint32_t *n_sel,
+                                       uint64_t *epoch, uint32_t *rows);
+/* Phase 2 (apply_selection): reject a stale selection, diff it against the
+ * working set, free and allocate slots, quantize every incoming block into
+ * its slot (one launch for K and V, from device or pinned host history),
+ * and in canonical mode move resident blocks to their window slots.
+ * Synchronises the engine stream. */
+KVMEM_HIP_API int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows,
+                                     const uint32_t *sel, uint32_t n_sel,
+                                     kvmem_plan_stats *stats);
+/* preview + apply (apply_retrieval, llama-memory-kvmem.cpp:3139-3142). */
+KVMEM_HIP_API int kvmem_engine_apply_retrieval(kvmem_engine *e, const void *q, int32_t q_type,
+                                               uint32_t n_q_tokens, const uint32_t *mandatory,
+                                               uint32_t n_mandatory, kvmem_plan_stats *stats);
+/* Scores of the last preview (host copy, block count entries). */
+KVMEM_HIP_API int kvmem_engine_scores(kvmem_engine *e, float *out, uint32_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

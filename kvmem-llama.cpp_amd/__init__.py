@@ -64,7 +64,7 @@ class History(C.Structure):
     _fields_ = [("k", C.c_void_p), ("v", C.c_void_p), ("n_layers", C.c_uint32),
                 ("n_blocks", C.c_uint32), ("block_tokens", C.c_uint32),
                 ("n_embd_k", C.c_uint32), ("n_embd_v", C.c_uint32),
-                ("last_block_tokens", C.c_uint32)]
+                ("last_block_tokens", C.c_uint32), ("capacity_blocks", C.c_uint32)]
 
 
 class HostHistory(C.Structure):
@@ -135,10 +135,6 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_perf_enable", i32, vp, i32)
     _sig(lib, "kvmem_hip_perf_get", i32, vp, C.POINTER(Perf))
     _sig(lib, "kvmem_hip_perf_reset", None, vp)
-    try:
-        from . import host as _host  # noqa: F401  (host mirror signatures)
-    except ImportError:
-        pass
     if path is None:
         _lib = lib
     return lib
@@ -165,9 +161,21 @@ class Context:
         self.h = h
         self._keep: list = []
 
+    @classmethod
+    def borrow(cls, handle: int) -> "Context":
+        """Wrap a context owned elsewhere (e.g. a reselect engine's); close()
+        leaves it alive."""
+        c = cls.__new__(cls)
+        c.lib = load_library()
+        c.h = C.c_void_p(handle)
+        c._keep = []
+        c._borrowed = True
+        return c
+
     def close(self) -> None:
         if getattr(self, "h", None):
-            self.lib.kvmem_hip_destroy(self.h)
+            if not getattr(self, "_borrowed", False):
+                self.lib.kvmem_hip_destroy(self.h)
             self.h = None
 
     def __del__(self):
@@ -215,9 +223,9 @@ class Context:
 
     @staticmethod
     def make_history(k_ptr, v_ptr, n_layers, n_blocks, block_tokens, n_embd_k, n_embd_v,
-                     last_block_tokens=0) -> History:
+                     last_block_tokens=0, capacity_blocks=0) -> History:
         return History(k_ptr or None, v_ptr or None, n_layers, n_blocks, block_tokens,
-                       n_embd_k, n_embd_v, last_block_tokens)
+                       n_embd_k, n_embd_v, last_block_tokens, capacity_blocks)
 
     def make_pool(self, n_layers, n_slots, block_tokens, n_embd_k, n_embd_v, type_k, type_v,
                   k_ptrs: Sequence[int], v_ptrs: Sequence[int] | None) -> Pool:

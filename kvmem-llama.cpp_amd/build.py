@@ -6,7 +6,7 @@
 The library is compiled with hipcc for gfx950 only.  Every HIP translation
 unit disables packed-FP32 instruction selection, and the stage-in unit
 disables FP contraction (ggml's reference quantizers round products and sums
-separately).  Host C++ units are compiled by hipcc in C++ mode so that one
+separately).  Host C++ units (csrc/*.cpp) are compiled by hipcc in C++ mode so that one
 shared object carries both the device ABI (include/kvmem_hip.h) and the host
 mirror of the reference's store / runtime / reselect interface
 (include/kvmem_host.h).
@@ -24,7 +24,6 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
-HOST = PKG / "host"
 INCLUDE = ROOT / "include"
 OBJ = PKG / "_build"
 LIB = PKG / "libkvmem_hip.so"
@@ -34,7 +33,7 @@ REFERENCE = Path("/root/reference")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-COMMON = ["-O3", "-fPIC", "-std=c++17", f"-I{INCLUDE}", f"-I{CSRC}", f"-I{HOST}",
+COMMON = ["-O3", "-fPIC", "-std=c++17", f"-I{INCLUDE}", f"-I{CSRC}",
           "-fvisibility=hidden", "-Wall", "-Wno-unused-result"]
 HIP_FLAGS = [f"--offload-arch={ARCH}", "-x", "hip",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -46,7 +45,7 @@ EXTRA = {
 
 
 def _sources() -> list[Path]:
-    return sorted(CSRC.glob("*.hip")) + sorted(HOST.glob("*.cpp"))
+    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
 def _compile(src: Path) -> tuple[Path, str]:
@@ -54,7 +53,8 @@ def _compile(src: Path) -> tuple[Path, str]:
     if src.suffix == ".hip":
         cmd = [HIPCC, *HIP_FLAGS, *COMMON, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     else:
-        cmd = [HIPCC, "-x", "c++", *COMMON, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, "-x", "c++", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", *COMMON,
+               "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {src.name}\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

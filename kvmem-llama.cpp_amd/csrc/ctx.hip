@@ -94,40 +94,61 @@ void *upload(kvmem_hip_ctx *ctx, const void *src, size_t bytes, const char *what
     return s.dev.ptr;
 }
 
+static hipEvent_t perf_event(kvmem_hip_ctx *ctx) {
+    if (!ctx->perf_free.empty()) {
+        hipEvent_t e = ctx->perf_free.back();
+        ctx->perf_free.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) {
+        return nullptr;
+    }
+    return e;
+}
+
 void perf_begin(kvmem_hip_ctx *ctx, PerfStage s) {
-    if (!ctx->perf_on) {
-        return;
+    if (!ctx->perf_on || ctx->perf_open[s]) {
+        return;  // off, or already inside this stage
     }
-    if (ctx->perf_pending[s]) {
-        perf_collect(ctx);
+    hipEvent_t e = perf_event(ctx);
+    if (e && hipEventRecord(e, ctx->stream) == hipSuccess) {
+        ctx->perf_open[s] = e;
+    } else if (e) {
+        ctx->perf_free.push_back(e);
     }
-    if (!ctx->perf_ev[s][0]) {
-        hipEventCreate(&ctx->perf_ev[s][0]);
-        hipEventCreate(&ctx->perf_ev[s][1]);
-    }
-    hipEventRecord(ctx->perf_ev[s][0], ctx->stream);
 }
 
 void perf_end(kvmem_hip_ctx *ctx, PerfStage s) {
-    if (!ctx->perf_on || !ctx->perf_ev[s][1]) {
+    hipEvent_t start = ctx->perf_open[s];
+    if (!start) {
         return;
     }
-    hipEventRecord(ctx->perf_ev[s][1], ctx->stream);
-    ctx->perf_pending[s] = true;
+    ctx->perf_open[s] = nullptr;
+    hipEvent_t end = perf_event(ctx);
+    if (end && hipEventRecord(end, ctx->stream) == hipSuccess) {
+        ctx->perf_done[s].emplace_back(start, end);
+        return;
+    }
+    ctx->perf_free.push_back(start);
+    if (end) {
+        ctx->perf_free.push_back(end);
+    }
 }
 
 void perf_collect(kvmem_hip_ctx *ctx) {
     for (int s = 0; s < kPerfStages; ++s) {
-        if (!ctx->perf_pending[s]) {
-            continue;
+        for (auto &pr : ctx->perf_done[s]) {
+            float ms = 0.0f;
+            if (hipEventSynchronize(pr.second) == hipSuccess &&
+                hipEventElapsedTime(&ms, pr.first, pr.second) == hipSuccess) {
+                ctx->perf_ms[s] += ms;
+                ctx->perf_n[s] += 1;
+            }
+            ctx->perf_free.push_back(pr.first);
+            ctx->perf_free.push_back(pr.second);
         }
-        float ms = 0.0f;
-        if (hipEventSynchronize(ctx->perf_ev[s][1]) == hipSuccess &&
-            hipEventElapsedTime(&ms, ctx->perf_ev[s][0], ctx->perf_ev[s][1]) == hipSuccess) {
-            ctx->perf_ms[s] += ms;
-            ctx->perf_n[s] += 1;
-        }
-        ctx->perf_pending[s] = false;
+        ctx->perf_done[s].clear();
     }
 }
 
@@ -217,10 +238,15 @@ void kvmem_hip_destroy(kvmem_hip_ctx *ctx) {
         if (ctx->h2d_copied[i]) hipEventDestroy(ctx->h2d_copied[i]);
         if (ctx->h2d_consumed[i]) hipEventDestroy(ctx->h2d_consumed[i]);
     }
-    for (auto &pair : ctx->perf_ev) {
-        for (hipEvent_t e : pair) {
-            if (e) hipEventDestroy(e);
+    for (int s = 0; s < kPerfStages; ++s) {
+        if (ctx->perf_open[s]) hipEventDestroy(ctx->perf_open[s]);
+        for (auto &pr : ctx->perf_done[s]) {
+            hipEventDestroy(pr.first);
+            hipEventDestroy(pr.second);
         }
+    }
+    for (hipEvent_t e : ctx->perf_free) {
+        hipEventDestroy(e);
     }
     if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
     if (ctx->copy_stream) hipStreamDestroy(ctx->copy_stream);

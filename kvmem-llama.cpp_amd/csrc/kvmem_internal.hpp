@@ -7,6 +7,8 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "kvmem_hip.h"
 
@@ -61,10 +63,11 @@ struct kvmem_hip_ctx {
     hipEvent_t h2d_copied[8] = {};
     hipEvent_t h2d_consumed[8] = {};
 
-    // profiling
+    // profiling: start/end event pairs per stage, harvested when read
     bool perf_on = false;
-    hipEvent_t perf_ev[kvmem_hip::kPerfStages][2] = {};
-    bool perf_pending[kvmem_hip::kPerfStages] = {};
+    std::vector<hipEvent_t> perf_free;                       // reusable events
+    hipEvent_t perf_open[kvmem_hip::kPerfStages] = {};       // started, not ended
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> perf_done[kvmem_hip::kPerfStages];
     double perf_ms[kvmem_hip::kPerfStages] = {};
     uint64_t perf_n[kvmem_hip::kPerfStages] = {};
     uint64_t h2d_bytes = 0;

@@ -1,0 +1,386 @@
+// Host block table, top-k selection, selection diff and slot plan of the
+// reselect step.  Behaviour follows the reference host library file:line
+// cited on each function; the code is written for this library.
+#include "kvmem_store.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+
+namespace kvmem_amd {
+
+namespace {
+
+uint64_t abs_diff(int64_t a, int64_t b) {
+    return static_cast<uint64_t>(a > b ? a - b : b - a);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ block table
+
+void KvMemStore::register_append(uint32_t n_new_tokens) {
+    const uint32_t bt = cfg_.block_tokens;
+    uint32_t left = n_new_tokens;
+    if (left && !blocks_.empty() && blocks_.back().n_tokens < bt) {
+        Block &tail = blocks_.back();
+        const uint32_t add = std::min(bt - tail.n_tokens, left);
+        tail.n_tokens += add;
+        total_tokens_ += add;
+        left -= add;
+    }
+    while (left) {
+        Block b;
+        b.block_id = block_count();
+        b.orig_pos_start = total_tokens_;
+        b.n_tokens = std::min(bt, left);
+        b.baked_pos = b.orig_pos_start;
+        total_tokens_ += b.n_tokens;
+        left -= b.n_tokens;
+        blocks_.push_back(b);
+    }
+}
+
+std::vector<uint32_t> KvMemStore::truncate_to(uint32_t token_pos) {
+    std::vector<uint32_t> dropped;
+    if (token_pos >= total_tokens_) {
+        return dropped;
+    }
+    while (!blocks_.empty() && blocks_.back().orig_pos_start >= token_pos) {
+        dropped.push_back(blocks_.back().block_id);
+        total_tokens_ -= blocks_.back().n_tokens;
+        blocks_.pop_back();
+    }
+    if (!blocks_.empty() && blocks_.back().orig_pos_end() > token_pos) {
+        Block &tail = blocks_.back();
+        const uint32_t keep = token_pos - tail.orig_pos_start;
+        total_tokens_ -= tail.n_tokens - keep;
+        tail.n_tokens = keep;
+    }
+    return dropped;
+}
+
+void KvMemStore::set_retrieval_scores(const std::vector<double> &scores) {
+    for (Block &b : blocks_) {
+        b.retrieval_score = b.block_id < scores.size() ? scores[b.block_id] : 0.0;
+    }
+}
+
+void KvMemStore::set_block_tier(uint32_t id, Tier tier) {
+    if (id >= block_count()) {
+        return;
+    }
+    blocks_[id].tier = tier;
+    if (tier != Tier::GPU) {
+        blocks_[id].gpu_slot = -1;
+    }
+}
+
+void KvMemStore::set_block_gpu_slot(uint32_t id, int32_t slot) {
+    if (id < block_count()) {
+        blocks_[id].gpu_slot = slot;
+    }
+}
+
+// ---------------------------------------------------------------- top-k
+
+TopkCharge KvMemStore::charge_topk(const std::vector<uint32_t> &mandatory) const {
+    TopkCharge c;
+    const uint32_t n = block_count();
+    const uint32_t budget = budget_blocks();
+    if (n == 0) {
+        return c;
+    }
+    if (budget == 0 || n <= budget) {
+        c.all_fit = true;
+        return c;
+    }
+    std::vector<uint8_t> charged(n, 0);
+    auto charge = [&](uint32_t id) {
+        if (id < n && !charged[id] && c.forced.size() < budget) {
+            charged[id] = 1;
+            c.forced.push_back(id);
+        }
+    };
+    for (uint32_t i = 0; i < std::min(cfg_.sink_blocks, n); ++i) {
+        charge(i);
+    }
+    for (auto it = mandatory.rbegin(); it != mandatory.rend(); ++it) {
+        charge(*it);
+    }
+    for (uint32_t i = 0; i < std::min(cfg_.recent_blocks, n); ++i) {
+        charge(n - 1 - i);
+    }
+    c.need = budget - static_cast<uint32_t>(c.forced.size());
+    return c;
+}
+
+std::vector<uint32_t> KvMemStore::pick_topk_blocks(const std::vector<uint32_t> &mandatory,
+                                                   const Ranker &ranker) const {
+    const uint32_t n = block_count();
+    std::vector<uint32_t> out;
+    const TopkCharge c = charge_topk(mandatory);
+    if (n == 0) {
+        return out;
+    }
+    if (c.all_fit) {
+        out.resize(n);
+        for (uint32_t i = 0; i < n; ++i) {
+            out[i] = i;
+        }
+        return out;
+    }
+    std::vector<uint8_t> keep(n, 0);
+    for (uint32_t id : c.forced) {
+        keep[id] = 1;
+    }
+    const uint32_t candidates = n - static_cast<uint32_t>(c.forced.size());
+    const uint32_t need = std::min(c.need, candidates);
+    if (need > 0) {
+        std::vector<uint32_t> best;
+        if (ranker) {
+            best = ranker(keep, need);
+        } else {
+            // strict total order: higher score first, then the tie rule
+            const bool lower_first = cfg_.tie_lower_index;
+            auto before = [&](uint32_t a, uint32_t b) {
+                const double sa = blocks_[a].retrieval_score;
+                const double sb = blocks_[b].retrieval_score;
+                if (sa != sb) {
+                    return sa > sb;
+                }
+                return lower_first ? a < b : a > b;
+            };
+            best.reserve(candidates);
+            for (uint32_t i = 0; i < n; ++i) {
+                if (!keep[i]) {
+                    best.push_back(i);
+                }
+            }
+            std::partial_sort(best.begin(), best.begin() + need, best.end(), before);
+            best.resize(need);
+        }
+        for (uint32_t id : best) {
+            if (id < n) {
+                keep[id] = 1;
+            }
+        }
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        if (keep[i]) {
+            out.push_back(i);
+        }
+    }
+    return out;
+}
+
+// ------------------------------------------------------------------ diff
+
+Plan KvMemStore::set_selection(std::vector<uint32_t> ids) {
+    const uint32_t n = block_count();
+    std::sort(ids.begin(), ids.end());
+    ids.erase(std::unique(ids.begin(), ids.end()), ids.end());
+    ids.erase(std::remove_if(ids.begin(), ids.end(), [n](uint32_t id) { return id >= n; }),
+              ids.end());
+
+    Plan plan;
+    std::vector<uint8_t> selected(n, 0);
+    for (uint32_t id : ids) {
+        selected[id] = 1;
+    }
+    std::vector<uint8_t> was_ws(n, 0);
+    for (const Block &b : blocks_) {
+        was_ws[b.block_id] = b.in_working_set;
+        plan.selection_overlap_blocks += (b.in_working_set && selected[b.block_id]) ? 1u : 0u;
+    }
+    const bool reload_all = !cfg_.optimize_stage_in;
+
+    // outgoing: GPU-tier blocks the new selection drops (all of them on a
+    // forced full reload), in id order
+    for (Block &b : blocks_) {
+        if (b.tier == Tier::GPU && (reload_all || !selected[b.block_id])) {
+            plan.stage_out.push_back(b.block_id);
+            b.in_working_set = false;
+        }
+    }
+
+    // window order = ascending id, packed from position 0
+    int64_t pos = 0;
+    for (uint32_t id : ids) {
+        Block &b = blocks_[id];
+        const bool on_gpu = b.tier == Tier::GPU;
+        if (was_ws[id] && on_gpu) {
+            if (b.baked_pos == pos) {
+                ++plan.retained_position_stable;
+            } else {
+                ++plan.retained_position_moved;
+            }
+            if (!reload_all) {
+                ++plan.gpu_reused_blocks;
+            }
+        }
+        if (!b.in_working_set) {
+            plan.stage_in.push_back(id);
+        }
+        Remap r;
+        r.block_id = id;
+        r.n_tokens = b.n_tokens;
+        r.from_base = static_cast<int32_t>(b.baked_pos);
+        r.to_base = static_cast<int32_t>(pos);
+        r.working_k_resident = on_gpu && !reload_all;
+        r.skip = b.baked_pos == pos;
+        plan.remaps.push_back(r);
+        if (!r.skip) {
+            ++b.remap_count;
+            b.remap_abs_delta += abs_diff(b.baked_pos, pos);
+        }
+        b.in_working_set = true;
+        b.baked_pos = pos;
+        pos += b.n_tokens;
+    }
+    plan.total_window_tokens = static_cast<uint32_t>(pos);
+    return plan;
+}
+
+bool KvMemStore::commit_resident_selection(const std::vector<uint32_t> &ids) {
+    std::vector<uint32_t> resident;
+    for (const Block &b : blocks_) {
+        if (b.gpu_slot < 0 || b.n_tokens == 0) {
+            continue;
+        }
+        if (b.tier != Tier::GPU) {
+            return false;
+        }
+        resident.push_back(b.block_id);
+    }
+    if (resident != ids) {
+        return false;
+    }
+    for (Block &b : blocks_) {
+        b.in_working_set = b.gpu_slot >= 0 && b.n_tokens > 0;
+    }
+    return true;
+}
+
+void KvMemStore::clear_working_set() {
+    for (Block &b : blocks_) {
+        b.in_working_set = false;
+    }
+}
+
+// ------------------------------------------------------------ slot pool
+
+SlotPool::SlotPool(uint32_t n_slots) : n_slots_(n_slots) {
+    reset();
+}
+
+void SlotPool::reset() {
+    free_.clear();
+    free_.reserve(n_slots_);
+    for (uint32_t i = n_slots_; i > 0; --i) {
+        free_.push_back(static_cast<int32_t>(i - 1));
+    }
+}
+
+int32_t SlotPool::alloc_gpu_slot() {
+    if (free_.empty()) {
+        return -1;
+    }
+    const int32_t s = free_.back();
+    free_.pop_back();
+    return s;
+}
+
+void SlotPool::free_gpu_slot(int32_t slot) {
+    if (slot >= 0) {
+        free_.push_back(slot);
+    }
+}
+
+// --------------------------------------------------------------- runtime
+
+KvMemRuntime::KvMemRuntime(StoreConfig cfg, KvMemBackend *backend)
+    : store_(cfg), backend_(backend) {
+    if (!backend_) {
+        throw std::invalid_argument("KvMemRuntime needs a backend");
+    }
+}
+
+std::vector<uint32_t> KvMemRuntime::truncate_to(uint32_t token_pos) {
+    std::vector<int32_t> slots;
+    for (const Block &b : store_.blocks()) {
+        if (b.orig_pos_start >= token_pos && b.gpu_slot >= 0) {
+            slots.push_back(b.gpu_slot);
+        }
+    }
+    std::vector<uint32_t> dropped = store_.truncate_to(token_pos);
+    for (int32_t s : slots) {
+        backend_->free_gpu_slot(s);
+    }
+    return dropped;
+}
+
+std::vector<uint32_t> KvMemRuntime::preview_reselect(const std::vector<uint32_t> &mandatory,
+                                                     const Ranker &ranker) const {
+    return store_.pick_topk_blocks(mandatory, ranker);
+}
+
+Plan KvMemRuntime::prepare_selection(const std::vector<uint32_t> &selected) {
+    last_plan_ = store_.set_selection(selected);
+    pending_ = true;
+    return last_plan_;
+}
+
+bool KvMemRuntime::commit_resident_selection(const std::vector<uint32_t> &selected) {
+    if (pending_ || !store_.commit_resident_selection(selected)) {
+        return false;
+    }
+    last_plan_ = Plan{};
+    for (uint32_t id : selected) {
+        last_plan_.total_window_tokens += store_.blocks()[id].n_tokens;
+    }
+    return true;
+}
+
+void KvMemRuntime::spill_outgoing() {
+    if (!pending_) {
+        return;
+    }
+    pending_frees_.clear();
+    for (uint32_t id : last_plan_.stage_out) {
+        const int32_t slot = store_.blocks()[id].gpu_slot;
+        store_.set_block_tier(id, Tier::CPU);   // the host history keeps the block
+        if (slot >= 0) {
+            pending_frees_.push_back(slot);
+        }
+    }
+}
+
+void KvMemRuntime::admit_incoming() {
+    if (!pending_) {
+        return;
+    }
+    for (int32_t s : pending_frees_) {
+        backend_->free_gpu_slot(s);
+    }
+    pending_frees_.clear();
+    for (uint32_t id : last_plan_.stage_in) {
+        const Block &b = store_.blocks()[id];
+        if (b.tier == Tier::GPU && b.gpu_slot >= 0) {
+            continue;  // still resident (only a working-set transition)
+        }
+        const int32_t slot = backend_->alloc_gpu_slot();
+        store_.set_block_tier(id, Tier::GPU);
+        store_.set_block_gpu_slot(id, slot);
+        if (slot >= 0) {
+            backend_->block_staged_in(id, slot);
+        }
+    }
+    pending_ = false;
+}
+
+void KvMemRuntime::finish_reselect() {
+    spill_outgoing();
+    admit_incoming();
+}
+
+}  // namespace kvmem_amd

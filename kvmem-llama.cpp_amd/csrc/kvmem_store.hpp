@@ -1,0 +1,200 @@
+// Host mirror of the reference's KVMem block table, selection and diff
+// (kvmem/include/kvmem/kvmem_store.hpp, kvmem_runtime.hpp,
+// kvmem_backend.hpp), restricted to what the reselect step uses.  Pure host
+// logic: no HIP call is made here.
+//
+// Kept from the reference interface: the names register_append,
+// truncate_to, set_retrieval_scores, pick_topk_blocks(mandatory),
+// set_selection -> KvMemPlan, commit_resident_selection, clear_working_set,
+// preview_reselect, prepare_selection, spill_outgoing, admit_incoming,
+// finish_reselect, and the backend hooks alloc_gpu_slot / free_gpu_slot.
+// Their argument meaning and results follow the reference (file:line on
+// each declaration).  Left out: CPU/NVMe tiers, the quota and media
+// policies, semantic groups and the immutable-source-K refresh counters
+// (the latter's remap_count / remap_abs_delta bookkeeping is kept).
+#pragma once
+
+#include <cstdint>
+#include <functional>
+#include <stdexcept>
+#include <vector>
+
+namespace kvmem_amd {
+
+enum class Tier : uint8_t { GPU = 0, CPU = 1, SSD = 2 };
+
+// kvmem_store.hpp:36-73 (fields on this path).
+struct Block {
+    uint32_t block_id = 0;
+    uint32_t orig_pos_start = 0;
+    uint32_t n_tokens = 0;
+    Tier tier = Tier::GPU;
+    int32_t gpu_slot = -1;
+    int64_t baked_pos = -1;
+    uint32_t remap_count = 0;
+    uint64_t remap_abs_delta = 0;
+    bool in_working_set = false;
+    double retrieval_score = 0.0;
+    uint32_t orig_pos_end() const { return orig_pos_start + n_tokens; }
+};
+
+// kvmem_store.hpp:80-94.
+struct Remap {
+    uint32_t block_id = 0;
+    uint32_t n_tokens = 0;
+    int32_t from_base = 0;
+    int32_t to_base = 0;
+    bool working_k_resident = false;
+    bool skip = false;
+};
+
+// kvmem_store.hpp:108-124.
+struct Plan {
+    std::vector<uint32_t> stage_in;
+    std::vector<uint32_t> stage_out;
+    std::vector<Remap> remaps;
+    uint32_t total_window_tokens = 0;
+    uint32_t selection_overlap_blocks = 0;
+    uint32_t gpu_reused_blocks = 0;
+    uint32_t retained_position_stable = 0;
+    uint32_t retained_position_moved = 0;
+};
+
+struct StoreConfig {
+    uint32_t block_tokens = 128;      // --kvmem-block-tokens
+    uint32_t select_budget = 131072;  // tokens; budget_blocks = select_budget / block_tokens
+    uint32_t sink_blocks = 1;
+    uint32_t recent_blocks = 0;
+    // Equal scores: true ranks the lower block id first (the reselect
+    // contract); false ranks the higher id first, the reference's recency
+    // rule (kvmem_store.cpp:602-609).
+    bool tie_lower_index = true;
+    // false forces every selected block to be staged in again
+    // (optimize_stage_in, kvmem_store.hpp:229-231).
+    bool optimize_stage_in = true;
+};
+
+// Blocks charged before the score fill of pick_topk: sink, mandatory
+// (newest listed first) and recent, each while the budget has room.
+struct TopkCharge {
+    bool all_fit = false;             // n <= budget: every block is selected
+    std::vector<uint32_t> forced;     // charged ids, in charge order
+    uint32_t need = 0;                // best-scored blocks still to add
+};
+
+// Ranks the uncharged blocks: writes the `need` best ids (any order) given
+// the charged-id mask.  The default ranks the store's retrieval scores on
+// the host; the reselect engine plugs in the device top-k.
+using Ranker = std::function<std::vector<uint32_t>(const std::vector<uint8_t> &charged,
+                                                   uint32_t need)>;
+
+class KvMemStore {
+public:
+    explicit KvMemStore(StoreConfig cfg) : cfg_(cfg) {
+        if (cfg_.block_tokens == 0) {
+            throw std::invalid_argument("block_tokens must be positive");
+        }
+    }
+
+    const StoreConfig &config() const { return cfg_; }
+    uint32_t block_count() const { return static_cast<uint32_t>(blocks_.size()); }
+    uint32_t total_tokens() const { return total_tokens_; }
+    const std::vector<Block> &blocks() const { return blocks_; }
+    uint32_t budget_blocks() const { return cfg_.select_budget / cfg_.block_tokens; }
+
+    // kvmem_store.cpp:179-205: fill the trailing partial block, then open
+    // new blocks of up to block_tokens, each baked at its true position.
+    void register_append(uint32_t n_new_tokens);
+    // kvmem_store.cpp:207-227: drop blocks starting at or past token_pos,
+    // shrink a straddling last block.  Returns the dropped ids.
+    std::vector<uint32_t> truncate_to(uint32_t token_pos);
+
+    // kvmem_store.cpp:242-248: replace every block's score; blocks past
+    // scores.size() get 0.
+    void set_retrieval_scores(const std::vector<double> &scores);
+
+    // kvmem_store.cpp:482-623 (TopK policy): sink, mandatory newest-first,
+    // recent, then the best scores; ids returned ascending.
+    std::vector<uint32_t> pick_topk_blocks(const std::vector<uint32_t> &mandatory = {},
+                                           const Ranker &ranker = nullptr) const;
+    // The charge phase of pick_topk_blocks alone.
+    TopkCharge charge_topk(const std::vector<uint32_t> &mandatory) const;
+
+    // kvmem_store.cpp:250-277 with optimize_stage_out: leaving the GPU
+    // clears the slot.
+    void set_block_tier(uint32_t id, Tier tier);
+    void set_block_gpu_slot(uint32_t id, int32_t slot);
+
+    // kvmem_store.cpp:758-882: diff a selection against the working set.
+    Plan set_selection(std::vector<uint32_t> selected_ids);
+    // kvmem_store.cpp:884-895.
+    bool commit_resident_selection(const std::vector<uint32_t> &selected_ids);
+    // kvmem_store.cpp:897-901.
+    void clear_working_set();
+
+private:
+    StoreConfig cfg_;
+    std::vector<Block> blocks_;
+    uint32_t total_tokens_ = 0;
+};
+
+// kvmem_backend.hpp:11-27 (slot hooks; block bytes move in batches through
+// the reselect engine instead of one copy call per block).
+class KvMemBackend {
+public:
+    virtual ~KvMemBackend() = default;
+    virtual int32_t alloc_gpu_slot() { return -1; }
+    virtual void free_gpu_slot(int32_t /*slot*/) {}
+    // A block entered `slot` (called once per staged block, ascending ids).
+    virtual void block_staged_in(uint32_t /*block_id*/, int32_t /*slot*/) {}
+};
+
+// LIFO slot free list of the adapter (llama-memory-kvmem.cpp:621-627
+// reset_slots, :693-707 alloc_slot / free_slot): slot 0 is handed out
+// first, a freed slot is the next one handed out.
+class SlotPool final : public KvMemBackend {
+public:
+    explicit SlotPool(uint32_t n_slots);
+    int32_t alloc_gpu_slot() override;
+    void free_gpu_slot(int32_t slot) override;
+    uint32_t n_slots() const { return n_slots_; }
+    uint32_t n_free() const { return static_cast<uint32_t>(free_.size()); }
+    void reset();
+
+private:
+    uint32_t n_slots_;
+    std::vector<int32_t> free_;
+};
+
+// kvmem_runtime.hpp:28-100 / kvmem_runtime.cpp:104-113, 212-236, 294-328:
+// the stage-out-before-stage-in ordering and the slot plan, with no
+// lower tiers (a block leaving the GPU keeps its host history copy).
+class KvMemRuntime {
+public:
+    KvMemRuntime(StoreConfig cfg, KvMemBackend *backend);
+
+    KvMemStore &store() { return store_; }
+    const KvMemStore &store() const { return store_; }
+    const Plan &last_plan() const { return last_plan_; }
+    bool pending() const { return pending_; }
+
+    void register_append(uint32_t n_tokens) { store_.register_append(n_tokens); }
+    std::vector<uint32_t> truncate_to(uint32_t token_pos);
+
+    std::vector<uint32_t> preview_reselect(const std::vector<uint32_t> &mandatory = {},
+                                           const Ranker &ranker = nullptr) const;
+    Plan prepare_selection(const std::vector<uint32_t> &selected);
+    bool commit_resident_selection(const std::vector<uint32_t> &selected);
+    void spill_outgoing();
+    void admit_incoming();
+    void finish_reselect();
+
+private:
+    KvMemStore store_;
+    KvMemBackend *backend_;
+    Plan last_plan_;
+    bool pending_ = false;
+    std::vector<int32_t> pending_frees_;
+};
+
+}  // namespace kvmem_amd

@@ -1,0 +1,728 @@
+// Reselect engine and host-store C ABI (include/kvmem_host.h).
+//
+// The engine owns a kvmem_hip_ctx, the K/V slot pool and the host store;
+// one agent step is preview (device scorer + device top-k with the store's
+// sink / mandatory / recent charge) then apply (store diff and slot plan,
+// one stage-in launch for every incoming block, optional canonical slot
+// layout).  It stands where llama_memory_kvmem::preview_retrieval /
+// apply_selection stand in the reference (src/adapter/llama-memory-kvmem.cpp:
+// 3047-3067, 3139-3263); the per-block write_block_to_gpu loop
+// (:2726-2791) becomes a single batched device call.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstddef>
+#include <cstring>
+#include <exception>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "kvmem_host.h"
+#include "kvmem_store.hpp"
+
+using kvmem_amd::Block;
+using kvmem_amd::KvMemRuntime;
+using kvmem_amd::Plan;
+using kvmem_amd::SlotPool;
+using kvmem_amd::StoreConfig;
+using kvmem_amd::Tier;
+
+namespace {
+
+// Slot pool that records the blocks admitted in one apply.
+class RecordingSlots final : public kvmem_amd::KvMemBackend {
+public:
+    explicit RecordingSlots(uint32_t n) : pool_(n) {}
+    int32_t alloc_gpu_slot() override { return pool_.alloc_gpu_slot(); }
+    void free_gpu_slot(int32_t s) override { pool_.free_gpu_slot(s); }
+    void block_staged_in(uint32_t id, int32_t slot) override {
+        staged_ids.push_back(id);
+        staged_slots.push_back(static_cast<uint32_t>(slot));
+    }
+    // Free list holding every slot except [0, n_used), lowest on top.
+    void reset_after(uint32_t n_used) {
+        pool_.reset();
+        for (uint32_t i = 0; i < n_used; ++i) {
+            (void) pool_.alloc_gpu_slot();
+        }
+    }
+    uint32_t n_free() const { return pool_.n_free(); }
+    std::vector<uint32_t> staged_ids;
+    std::vector<uint32_t> staged_slots;
+
+private:
+    SlotPool pool_;
+};
+
+void fill_stats(const Plan &p, uint32_t n_staged, uint32_t n_moved, kvmem_plan_stats *st) {
+    if (!st) {
+        return;
+    }
+    st->n_stage_in = static_cast<uint32_t>(p.stage_in.size());
+    st->n_stage_out = static_cast<uint32_t>(p.stage_out.size());
+    st->n_staged = n_staged;
+    st->n_moved = n_moved;
+    st->selection_overlap_blocks = p.selection_overlap_blocks;
+    st->gpu_reused_blocks = p.gpu_reused_blocks;
+    st->retained_position_stable = p.retained_position_stable;
+    st->retained_position_moved = p.retained_position_moved;
+    st->total_window_tokens = p.total_window_tokens;
+}
+
+StoreConfig store_config(uint32_t block_tokens, uint32_t budget_blocks, uint32_t sink,
+                         uint32_t recent, bool tie_lower) {
+    StoreConfig c;
+    c.block_tokens = block_tokens;
+    c.select_budget = budget_blocks * block_tokens;
+    c.sink_blocks = sink;
+    c.recent_blocks = recent;
+    c.tie_lower_index = tie_lower;
+    return c;
+}
+
+}  // namespace
+
+// ================================================================ store
+
+struct kvmem_store {
+    RecordingSlots slots;
+    KvMemRuntime rt;
+    kvmem_store(const StoreConfig &c, uint32_t n_slots) : slots(n_slots), rt(c, &slots) {}
+};
+
+extern "C" {
+
+int kvmem_store_create(uint32_t block_tokens, uint32_t budget_blocks, uint32_t sink_blocks,
+                       uint32_t recent_blocks, int tie_lower_index, uint32_t n_slots,
+                       kvmem_store **out) {
+    if (!out || block_tokens == 0) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    *out = new (std::nothrow) kvmem_store(
+        store_config(block_tokens, budget_blocks, sink_blocks, recent_blocks, tie_lower_index != 0),
+        n_slots);
+    return *out ? KVMEM_HIP_OK : KVMEM_HIP_ERR_NOMEM;
+}
+
+void kvmem_store_destroy(kvmem_store *s) {
+    delete s;
+}
+
+int kvmem_store_register_append(kvmem_store *s, uint32_t n_tokens) {
+    if (!s) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    const uint32_t first_new = s->rt.store().block_count();
+    s->rt.register_append(n_tokens);
+    // new blocks live in the host history until a selection stages them in
+    for (uint32_t id = first_new; id < s->rt.store().block_count(); ++id) {
+        s->rt.store().set_block_tier(id, Tier::CPU);
+    }
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_store_truncate_to(kvmem_store *s, uint32_t token_pos) {
+    if (!s) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    s->rt.truncate_to(token_pos);
+    return KVMEM_HIP_OK;
+}
+
+uint32_t kvmem_store_block_count(const kvmem_store *s) {
+    return s ? s->rt.store().block_count() : 0;
+}
+
+uint32_t kvmem_store_total_tokens(const kvmem_store *s) {
+    return s ? s->rt.store().total_tokens() : 0;
+}
+
+int kvmem_store_set_scores(kvmem_store *s, const double *scores, uint32_t n) {
+    if (!s || (n && !scores)) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    s->rt.store().set_retrieval_scores(std::vector<double>(scores, scores + n));
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_store_pick_topk(kvmem_store *s, const uint32_t *mandatory, uint32_t n_mandatory,
+                          uint32_t *out, uint32_t *n_out) {
+    if (!s || !out || !n_out || (n_mandatory && !mandatory)) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    const std::vector<uint32_t> sel =
+        s->rt.preview_reselect(std::vector<uint32_t>(mandatory, mandatory + n_mandatory));
+    std::copy(sel.begin(), sel.end(), out);
+    *n_out = static_cast<uint32_t>(sel.size());
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_store_apply(kvmem_store *s, const uint32_t *sel, uint32_t n_sel, uint32_t *stage_in,
+                      uint32_t *n_in, uint32_t *stage_out, uint32_t *n_out,
+                      kvmem_plan_stats *stats) {
+    if (!s || (n_sel && !sel)) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    s->slots.staged_ids.clear();
+    s->slots.staged_slots.clear();
+    const Plan p = s->rt.prepare_selection(std::vector<uint32_t>(sel, sel + n_sel));
+    s->rt.finish_reselect();
+    if (stage_in) {
+        std::copy(p.stage_in.begin(), p.stage_in.end(), stage_in);
+    }
+    if (stage_out) {
+        std::copy(p.stage_out.begin(), p.stage_out.end(), stage_out);
+    }
+    if (n_in) {
+        *n_in = static_cast<uint32_t>(p.stage_in.size());
+    }
+    if (n_out) {
+        *n_out = static_cast<uint32_t>(p.stage_out.size());
+    }
+    fill_stats(p, static_cast<uint32_t>(s->slots.staged_ids.size()), 0, stats);
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_store_blocks(const kvmem_store *s, int32_t *gpu_slot, uint8_t *tier, uint8_t *in_ws,
+                       int64_t *baked_pos) {
+    if (!s) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    const auto &bl = s->rt.store().blocks();
+    for (size_t i = 0; i < bl.size(); ++i) {
+        if (gpu_slot) gpu_slot[i] = bl[i].gpu_slot;
+        if (tier) tier[i] = static_cast<uint8_t>(bl[i].tier);
+        if (in_ws) in_ws[i] = bl[i].in_working_set ? 1 : 0;
+        if (baked_pos) baked_pos[i] = bl[i].baked_pos;
+    }
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_store_commit_resident(kvmem_store *s, const uint32_t *sel, uint32_t n) {
+    if (!s || (n && !sel)) {
+        return 0;
+    }
+    return s->rt.commit_resident_selection(std::vector<uint32_t>(sel, sel + n)) ? 1 : 0;
+}
+
+}  // extern "C"
+
+// =============================================================== engine
+
+struct kvmem_engine {
+    kvmem_engine_params p{};
+    uint32_t n_embd_k = 0;
+    uint32_t n_embd_v = 0;
+    uint32_t n_slots = 0;
+    kvmem_hip_ctx *ctx = nullptr;
+    RecordingSlots slots;
+    KvMemRuntime rt;
+    std::vector<void *> pool_k, pool_v;
+    const void *hist_k = nullptr;
+    const void *hist_v = nullptr;
+    uint32_t hist_capacity = 0;
+    const void *host_base = nullptr;
+    uint32_t host_capacity = 0;
+    float *d_scores = nullptr;
+    uint32_t d_scores_n = 0;
+    int64_t dirty_tail = -1;   // resident partial block that grew since staged
+    uint64_t epoch = 1;
+    std::string err;
+
+    kvmem_engine(const kvmem_engine_params &pp, uint32_t n)
+        : p(pp),
+          n_slots(n),
+          slots(n),
+          rt(store_config(pp.block_tokens, pp.budget_blocks, pp.sink_blocks, pp.recent_blocks,
+                          pp.tie_lower_index != 0),
+             &slots) {}
+
+    int fail(int code, const std::string &msg) {
+        err = msg;
+        return code;
+    }
+    int fail_ctx(int code, const char *what) {
+        err = std::string(what) + ": " + kvmem_hip_last_error(ctx);
+        return code;
+    }
+
+    kvmem_hip_pool pool_desc() const {
+        kvmem_hip_pool d{};
+        d.n_layers = p.n_layers;
+        d.n_slots = n_slots;
+        d.block_tokens = p.block_tokens;
+        d.n_embd_k = n_embd_k;
+        d.n_embd_v = n_embd_v;
+        d.type_k = p.type_k;
+        d.type_v = p.type_v;
+        d.k_layers = pool_k.data();
+        d.v_layers = pool_v.data();
+        return d;
+    }
+
+    uint32_t last_block_tokens() const {
+        const auto &bl = rt.store().blocks();
+        if (bl.empty() || bl.back().n_tokens == p.block_tokens) {
+            return 0;
+        }
+        return bl.back().n_tokens;
+    }
+
+    kvmem_hip_history device_history() const {
+        kvmem_hip_history h{};
+        h.k = hist_k;
+        h.v = hist_v;
+        h.n_layers = p.n_layers;
+        h.n_blocks = rt.store().block_count();
+        h.block_tokens = p.block_tokens;
+        h.n_embd_k = n_embd_k;
+        h.n_embd_v = n_embd_v;
+        h.last_block_tokens = last_block_tokens();
+        h.capacity_blocks = hist_capacity;
+        return h;
+    }
+};
+
+namespace {
+
+int engine_stage(kvmem_engine *e, const std::vector<uint32_t> &ids,
+                 const std::vector<uint32_t> &slots) {
+    if (ids.empty()) {
+        return KVMEM_HIP_OK;
+    }
+    const kvmem_hip_pool pool = e->pool_desc();
+    const uint32_t n_blocks = e->rt.store().block_count();
+    const uint32_t last = e->last_block_tokens();
+    int rc;
+    if (e->host_base) {
+        kvmem_hip_host_history h{};
+        h.base = e->host_base;
+        h.n_layers = e->p.n_layers;
+        h.n_blocks = n_blocks;
+        h.block_tokens = e->p.block_tokens;
+        h.n_embd_k = e->n_embd_k;
+        h.n_embd_v = e->n_embd_v;
+        h.last_block_tokens = last;
+        rc = kvmem_hip_stagein_blocks_host(e->ctx, &h, &pool, ids.data(), slots.data(),
+                                           static_cast<uint32_t>(ids.size()));
+    } else {
+        const kvmem_hip_history h = e->device_history();
+        rc = kvmem_hip_stagein_blocks(e->ctx, &h, &pool, ids.data(), slots.data(),
+                                      static_cast<uint32_t>(ids.size()));
+    }
+    return rc == KVMEM_HIP_OK ? rc : e->fail_ctx(rc, "stage-in");
+}
+
+}  // namespace
+
+extern "C" {
+
+kvmem_engine_params kvmem_engine_default_params(void) {
+    kvmem_engine_params p{};
+    p.device = 0;
+    p.n_layers = 16;
+    p.block_tokens = 128;
+    p.n_head = 24;
+    p.n_head_kv = 4;
+    p.head_dim = 256;
+    p.n_embd_v = 0;
+    p.budget_blocks = 256;
+    p.reserve_blocks = 128;
+    p.sink_blocks = 1;
+    p.recent_blocks = 0;
+    p.type_k = KVMEM_TYPE_Q8_0;
+    p.type_v = KVMEM_TYPE_Q8_0;
+    p.tie_lower_index = 1;
+    p.layer_reduce = KVMEM_LAYER_MEAN;
+    p.canonical_layout = 0;
+    return p;
+}
+
+int kvmem_engine_create(const kvmem_engine_params *pp, kvmem_engine **out) {
+    if (!pp || !out) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    *out = nullptr;
+    const kvmem_engine_params &p = *pp;
+    if (p.n_layers == 0 || p.block_tokens == 0 || p.block_tokens > 128 || p.n_head_kv == 0 ||
+        p.n_head % p.n_head_kv != 0 || (p.head_dim != 128 && p.head_dim != 256) ||
+        p.budget_blocks == 0 || !kvmem_hip_quant_ok(p.type_k) || !kvmem_hip_quant_ok(p.type_v)) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    const uint32_t n_slots = p.budget_blocks + p.reserve_blocks;
+    kvmem_engine *e = new (std::nothrow) kvmem_engine(p, n_slots);
+    if (!e) {
+        return KVMEM_HIP_ERR_NOMEM;
+    }
+    e->n_embd_k = p.n_head_kv * p.head_dim;
+    e->n_embd_v = p.n_embd_v ? p.n_embd_v : e->n_embd_k;
+    if (e->n_embd_v % 32 != 0) {
+        delete e;
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    int rc = kvmem_hip_create(p.device, &e->ctx);
+    if (rc != KVMEM_HIP_OK) {
+        delete e;
+        return rc;
+    }
+    const size_t kbytes = static_cast<size_t>(n_slots) * p.block_tokens *
+                          kvmem_hip_row_size(p.type_k, e->n_embd_k);
+    const size_t vbytes = static_cast<size_t>(n_slots) * p.block_tokens *
+                          kvmem_hip_row_size(p.type_v, e->n_embd_v);
+    e->pool_k.assign(p.n_layers, nullptr);
+    e->pool_v.assign(p.n_layers, nullptr);
+    for (uint32_t l = 0; l < p.n_layers; ++l) {
+        if (hipMalloc(&e->pool_k[l], kbytes) != hipSuccess ||
+            hipMalloc(&e->pool_v[l], vbytes) != hipSuccess) {
+            kvmem_engine_destroy(e);
+            return KVMEM_HIP_ERR_NOMEM;
+        }
+    }
+    *out = e;
+    return KVMEM_HIP_OK;
+}
+
+void kvmem_engine_destroy(kvmem_engine *e) {
+    if (!e) {
+        return;
+    }
+    if (e->ctx) {
+        kvmem_hip_sync(e->ctx);
+    }
+    for (void *ptr : e->pool_k) {
+        if (ptr) (void) hipFree(ptr);
+    }
+    for (void *ptr : e->pool_v) {
+        if (ptr) (void) hipFree(ptr);
+    }
+    if (e->d_scores) {
+        (void) hipFree(e->d_scores);
+    }
+    kvmem_hip_destroy(e->ctx);
+    delete e;
+}
+
+const char *kvmem_engine_last_error(const kvmem_engine *e) {
+    return e ? e->err.c_str() : "null engine";
+}
+
+kvmem_hip_ctx *kvmem_engine_ctx(kvmem_engine *e) {
+    return e ? e->ctx : nullptr;
+}
+
+int kvmem_engine_set_device_history(kvmem_engine *e, const void *k, const void *v,
+                                    uint32_t capacity_blocks, uint32_t n_tokens) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!k || !v) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "set_device_history: null K or V");
+    }
+    const uint64_t cap_tokens = static_cast<uint64_t>(capacity_blocks) * e->p.block_tokens;
+    if (n_tokens > cap_tokens) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "set_device_history: n_tokens exceeds the capacity");
+    }
+    e->hist_k = k;
+    e->hist_v = v;
+    e->hist_capacity = capacity_blocks;
+    const uint32_t have = e->rt.store().total_tokens();
+    if (n_tokens < have) {
+        e->rt.truncate_to(n_tokens);
+    } else if (n_tokens > have) {
+        const uint32_t first_new = e->rt.store().block_count();
+        e->rt.register_append(n_tokens - have);
+        for (uint32_t id = first_new; id < e->rt.store().block_count(); ++id) {
+            e->rt.store().set_block_tier(id, Tier::CPU);
+        }
+    }
+    ++e->epoch;
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_set_host_history(kvmem_engine *e, const void *pinned_base,
+                                  uint32_t capacity_blocks) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (pinned_base && capacity_blocks < e->rt.store().block_count()) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "set_host_history: capacity below the block count");
+    }
+    e->host_base = pinned_base;
+    e->host_capacity = pinned_base ? capacity_blocks : 0;
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_append_tokens(kvmem_engine *e, uint32_t n_new_tokens) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    const uint64_t want = static_cast<uint64_t>(e->rt.store().total_tokens()) + n_new_tokens;
+    if (want > static_cast<uint64_t>(e->hist_capacity) * e->p.block_tokens ||
+        (e->host_base && want > static_cast<uint64_t>(e->host_capacity) * e->p.block_tokens)) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "append_tokens: history capacity exceeded");
+    }
+    const uint32_t first_new = e->rt.store().block_count();
+    if (first_new > 0 && n_new_tokens > 0) {
+        // a partial tail that is in the pool must be staged again
+        const Block &tail = e->rt.store().blocks().back();
+        if (tail.n_tokens < e->p.block_tokens && tail.tier == Tier::GPU && tail.gpu_slot >= 0) {
+            e->dirty_tail = tail.block_id;
+        }
+    }
+    e->rt.register_append(n_new_tokens);
+    for (uint32_t id = first_new; id < e->rt.store().block_count(); ++id) {
+        e->rt.store().set_block_tier(id, Tier::CPU);
+    }
+    ++e->epoch;
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_truncate_to(kvmem_engine *e, uint32_t token_pos) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    e->rt.truncate_to(token_pos);
+    ++e->epoch;
+    return KVMEM_HIP_OK;
+}
+
+uint32_t kvmem_engine_block_count(const kvmem_engine *e) {
+    return e ? e->rt.store().block_count() : 0;
+}
+
+uint32_t kvmem_engine_total_tokens(const kvmem_engine *e) {
+    return e ? e->rt.store().total_tokens() : 0;
+}
+
+uint64_t kvmem_engine_epoch(const kvmem_engine *e) {
+    return e ? e->epoch : 0;
+}
+
+uint32_t kvmem_engine_n_slots(const kvmem_engine *e) {
+    return e ? e->n_slots : 0;
+}
+
+int kvmem_engine_pool_layer(const kvmem_engine *e, uint32_t layer, void **k, void **v) {
+    if (!e || layer >= e->p.n_layers) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (k) *k = e->pool_k[layer];
+    if (v) *v = e->pool_v[layer];
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_block_slots(const kvmem_engine *e, int32_t *slots) {
+    if (!e || !slots) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    const auto &bl = e->rt.store().blocks();
+    for (size_t i = 0; i < bl.size(); ++i) {
+        slots[i] = bl[i].tier == Tier::GPU ? bl[i].gpu_slot : -1;
+    }
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_t n_q_tokens,
+                         const uint32_t *mandatory, uint32_t n_mandatory, uint32_t *sel,
+                         uint32_t *n_sel, uint64_t *epoch, uint32_t *rows) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!q || !sel || !n_sel || (n_mandatory && !mandatory)) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "preview: null argument");
+    }
+    if (!e->hist_k) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "preview: no device history (the scorer reads keys in HBM)");
+    }
+    const uint32_t n = e->rt.store().block_count();
+    *n_sel = 0;
+    if (epoch) *epoch = e->epoch;
+    if (rows) *rows = e->rt.store().total_tokens();
+    if (n == 0) {
+        return KVMEM_HIP_OK;
+    }
+    if (e->d_scores_n < n) {
+        if (e->d_scores) {
+            if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
+                return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "preview");
+            }
+            (void) hipFree(e->d_scores);
+            e->d_scores = nullptr;
+        }
+        if (hipMalloc(&e->d_scores, sizeof(float) * n) != hipSuccess) {
+            e->d_scores_n = 0;
+            return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: score buffer");
+        }
+        e->d_scores_n = n;
+    }
+    std::vector<uint32_t> mand(mandatory, mandatory + n_mandatory);
+    const kvmem_amd::TopkCharge charge = e->rt.store().charge_topk(mand);
+    std::vector<uint32_t> out;
+    if (charge.all_fit) {
+        out.resize(n);
+        for (uint32_t i = 0; i < n; ++i) out[i] = i;
+    } else {
+        const kvmem_hip_history h = e->device_history();
+        kvmem_hip_score_args a{};
+        a.q = q;
+        a.q_type = q_type;
+        a.n_q_tokens = n_q_tokens;
+        a.n_head = e->p.n_head;
+        a.n_head_kv = e->p.n_head_kv;
+        a.head_dim = e->p.head_dim;
+        a.layer_reduce = e->p.layer_reduce;
+        a.layer_scores = nullptr;
+        a.scores = e->d_scores;
+        int rc = kvmem_hip_score(e->ctx, &h, &a);
+        if (rc != KVMEM_HIP_OK) {
+            return e->fail_ctx(rc, "preview score");
+        }
+        // top-k over the registered blocks only; the charged ids are forced
+        std::vector<uint32_t> got(n);
+        uint32_t cnt = 0;
+        rc = kvmem_hip_topk(e->ctx, e->d_scores, n, charge.forced.data(),
+                            static_cast<uint32_t>(charge.forced.size()), charge.need,
+                            e->p.tie_lower_index, got.data(), &cnt);
+        if (rc != KVMEM_HIP_OK) {
+            return e->fail_ctx(rc, "preview top-k");
+        }
+        got.resize(cnt);
+        out.swap(got);
+    }
+    std::copy(out.begin(), out.end(), sel);
+    *n_sel = static_cast<uint32_t>(out.size());
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uint32_t *sel,
+                       uint32_t n_sel, kvmem_plan_stats *stats) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (n_sel && !sel) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "apply: null selection");
+    }
+    if (epoch != e->epoch || rows != e->rt.store().total_tokens()) {
+        return e->fail(KVMEM_HIP_ERR_STALE, "stale KVMem selection");
+    }
+    if (!e->hist_k && !e->host_base) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "apply: no history");
+    }
+    std::vector<uint32_t> ids(sel, sel + n_sel);
+    const uint32_t n = e->rt.store().block_count();
+    std::sort(ids.begin(), ids.end());
+    ids.erase(std::unique(ids.begin(), ids.end()), ids.end());
+    ids.erase(std::remove_if(ids.begin(), ids.end(), [n](uint32_t id) { return id >= n; }), ids.end());
+    if (ids.size() > e->n_slots) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "apply: selection larger than the slot pool");
+    }
+    // slots the selection keeps before the plan changes them
+    std::vector<int32_t> old_slot(n, -1);
+    for (const Block &b : e->rt.store().blocks()) {
+        old_slot[b.block_id] = b.tier == Tier::GPU ? b.gpu_slot : -1;
+    }
+    e->slots.staged_ids.clear();
+    e->slots.staged_slots.clear();
+    const Plan plan = e->rt.prepare_selection(ids);
+    e->rt.finish_reselect();
+    std::vector<uint32_t> stage_ids = e->slots.staged_ids;
+    std::vector<uint32_t> stage_slots = e->slots.staged_slots;
+    if (e->dirty_tail >= 0) {
+        // the grown tail keeps its slot and is quantized again
+        const uint32_t id = static_cast<uint32_t>(e->dirty_tail);
+        if (id < n) {
+            const Block &b = e->rt.store().blocks()[id];
+            if (b.tier == Tier::GPU && b.gpu_slot >= 0 &&
+                std::find(stage_ids.begin(), stage_ids.end(), id) == stage_ids.end()) {
+                auto at = std::lower_bound(stage_ids.begin(), stage_ids.end(), id);
+                const size_t k = static_cast<size_t>(at - stage_ids.begin());
+                stage_ids.insert(at, id);
+                stage_slots.insert(stage_slots.begin() + static_cast<std::ptrdiff_t>(k),
+                                   static_cast<uint32_t>(b.gpu_slot));
+            }
+        }
+        e->dirty_tail = -1;
+    }
+    for (uint32_t s : stage_slots) {
+        if (s >= e->n_slots) {
+            return e->fail(KVMEM_HIP_ERR_RUNTIME, "apply: slot pool exhausted");
+        }
+    }
+    uint32_t n_moved = 0;
+    int rc = KVMEM_HIP_OK;
+    if (e->p.canonical_layout) {
+        // window slot i holds the i-th selected block
+        std::vector<uint32_t> src, dst;
+        std::vector<uint8_t> staged(n, 0);
+        for (uint32_t id : stage_ids) staged[id] = 1;
+        stage_slots.clear();
+        for (uint32_t i = 0; i < ids.size(); ++i) {
+            const uint32_t id = ids[i];
+            if (staged[id]) {
+                stage_slots.push_back(i);
+            } else if (old_slot[id] >= 0 && static_cast<uint32_t>(old_slot[id]) != i) {
+                src.push_back(static_cast<uint32_t>(old_slot[id]));
+                dst.push_back(i);
+            }
+            e->rt.store().set_block_gpu_slot(id, static_cast<int32_t>(i));
+        }
+        // staged ids come in ascending order, so stage_slots pairs with stage_ids
+        e->slots.reset_after(static_cast<uint32_t>(ids.size()));
+        if (!src.empty()) {
+            const kvmem_hip_pool pool = e->pool_desc();
+            rc = kvmem_hip_move_slots(e->ctx, &pool, src.data(), dst.data(),
+                                      static_cast<uint32_t>(src.size()));
+            if (rc != KVMEM_HIP_OK) {
+                return e->fail_ctx(rc, "apply: canonical layout");
+            }
+            n_moved = static_cast<uint32_t>(src.size());
+        }
+    }
+    rc = engine_stage(e, stage_ids, stage_slots);
+    if (rc != KVMEM_HIP_OK) {
+        return rc;
+    }
+    if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
+        return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "apply sync");
+    }
+    fill_stats(plan, static_cast<uint32_t>(stage_ids.size()), n_moved, stats);
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_apply_retrieval(kvmem_engine *e, const void *q, int32_t q_type,
+                                 uint32_t n_q_tokens, const uint32_t *mandatory,
+                                 uint32_t n_mandatory, kvmem_plan_stats *stats) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    std::vector<uint32_t> sel(std::max<uint32_t>(1, e->rt.store().block_count()));
+    uint32_t n_sel = 0, rows = 0;
+    uint64_t epoch = 0;
+    int rc = kvmem_engine_preview(e, q, q_type, n_q_tokens, mandatory, n_mandatory, sel.data(),
+                                  &n_sel, &epoch, &rows);
+    if (rc != KVMEM_HIP_OK) {
+        return rc;
+    }
+    return kvmem_engine_apply(e, epoch, rows, sel.data(), n_sel, stats);
+}
+
+int kvmem_engine_scores(kvmem_engine *e, float *out, uint32_t n) {
+    if (!e || (n && !out)) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (n > e->d_scores_n) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "scores: more than the last preview produced");
+    }
+    if (n == 0) {
+        return KVMEM_HIP_OK;
+    }
+    hipStream_t s = static_cast<hipStream_t>(kvmem_hip_get_stream(e->ctx));
+    if (hipMemcpyAsync(out, e->d_scores, sizeof(float) * n, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+        return e->fail(KVMEM_HIP_ERR_RUNTIME, "scores: copy");
+    }
+    return KVMEM_HIP_OK;
+}
+
+}  // extern "C"

@@ -44,6 +44,7 @@ struct ScoreParams {
     const uint8_t *k;        // [L][B][T][Hkv][D] f16
     float *partial;          // [RG][L][Hkv][B]
     uint32_t L, Tq, Hq, Hkv, B, T, last_T, g, R, RG;
+    uint32_t cap;            // blocks per layer in memory (>= B)
     uint32_t n_chunks;       // block chunks per (l, h, row slice)
     uint32_t blocks_per_chunk;
     uint32_t q_bf16;
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(kScoreThreads, 1) void score_kernel(ScoreParams p) 
     // tokens read the block's last valid key.
     const uint64_t key_stride = static_cast<uint64_t>(p.Hkv) * ROW_BYTES;  // bytes between keys
     auto block_base = [&](uint32_t b) -> const uint8_t * {
-        return p.k + ((static_cast<uint64_t>(l) * p.B + b) * p.T) * key_stride +
+        return p.k + ((static_cast<uint64_t>(l) * p.cap + b) * p.T) * key_stride +
                static_cast<uint64_t>(h) * ROW_BYTES;
     };
     auto n_tokens = [&](uint32_t b) -> uint32_t {
@@ -299,6 +300,10 @@ extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist
     p.Hq = args->n_head;
     p.Hkv = args->n_head_kv;
     p.B = B;
+    p.cap = hist->capacity_blocks ? hist->capacity_blocks : B;
+    if (p.cap < B) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "score: capacity_blocks below n_blocks");
+    }
     p.T = hist->block_tokens;
     p.last_T = hist->last_block_tokens;
     p.g = args->n_head / args->n_head_kv;
@@ -332,12 +337,15 @@ extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist
     } else {
         score_kernel<128><<<static_cast<uint32_t>(grid), kScoreThreads, 0, ctx->stream>>>(p);
     }
+    perf_end(ctx, kPerfScore);
     if (!hip_ok(ctx, hipGetLastError(), "score kernel launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
+    // the layer combination is timed with the selection stage
+    perf_begin(ctx, kPerfTopk);
     score_finalize_kernel<<<(B + 255) / 256, 256, 0, ctx->stream>>>(
         p.partial, p.RG, L, p.Hkv, B, args->layer_reduce, args->layer_scores, args->scores);
-    perf_end(ctx, kPerfScore);
+    perf_end(ctx, kPerfTopk);
     if (!hip_ok(ctx, hipGetLastError(), "score finalize launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }

@@ -23,6 +23,7 @@
 #include "kvmem_internal.hpp"
 
 #include <algorithm>
+#include <cstring>
 #include <vector>
 
 #pragma clang fp contract(off)
@@ -307,12 +308,13 @@ __device__ inline void quant_quarter<KVMEM_TYPE_F16>(const uint4 &v, uint32_t q,
     }
 }
 
+// Quantize chunk `c` of `source` into its destination.  `lds` holds
+// 4 * kWaveGroups groups of the type's layout.
 template <int TYPE, class Source>
-__global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
+__device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8_t *lds) {
     constexpr int GB = Fmt<TYPE>::GB;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kWaveGroups * GB];
     Chunk c;
-    if (!source.chunk(blockIdx.x, c)) {
+    if (!source.chunk(c_index, c)) {
         return;  // uniform across the workgroup
     }
     const uint32_t tid = threadIdx.x;
@@ -341,7 +343,10 @@ __global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
         const uint32_t gl = wg0 + 16u * r + quad;
         quant_quarter<TYPE>(v[r], q, wl + (16u * r + quad) * GB, gl < c.ng);
     }
-    __syncthreads();
+    // each wave reads back only the bytes it wrote itself
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     const uint32_t ngw = c.ng > wg0 ? min(static_cast<uint32_t>(kWaveGroups), c.ng - wg0) : 0u;
     const uint32_t nb = ngw * GB;
@@ -352,6 +357,26 @@ __global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
     }
     for (uint32_t off = full + lane * 2u; off < nb; off += 128u) {
         *reinterpret_cast<uint16_t *>(dst + off) = *reinterpret_cast<const uint16_t *>(wl + off);
+    }
+}
+
+template <int TYPE, class Source>
+__global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kWaveGroups * Fmt<TYPE>::GB];
+    quant_chunk<TYPE>(source, blockIdx.x, lds);
+}
+
+// K and V of a block job in one launch: workgroups [0, n_k) take K chunks,
+// the rest V chunks (the branch is uniform per workgroup).
+template <int TK, int TV>
+__global__ __launch_bounds__(256) void quant_scatter_kv_kernel(BlockSource sk, BlockSource sv,
+                                                               uint32_t n_k) {
+    constexpr int GB = Fmt<TK>::GB > Fmt<TV>::GB ? Fmt<TK>::GB : Fmt<TV>::GB;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kWaveGroups * GB];
+    if (blockIdx.x < n_k) {
+        quant_chunk<TK>(sk, blockIdx.x, lds);
+    } else {
+        quant_chunk<TV>(sv, blockIdx.x - n_k, lds);
     }
 }
 
@@ -380,6 +405,46 @@ bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Source 
     return hip_ok(ctx, hipGetLastError(), "stage-in kernel launch");
 }
 
+template <int TK>
+bool launch_kv_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, const BlockSource &sk,
+                 const BlockSource &sv, uint32_t n_k) {
+    switch (tv) {
+        case KVMEM_TYPE_Q8_0:
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q8_0><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
+            break;
+        case KVMEM_TYPE_Q4_0:
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q4_0><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
+            break;
+        case KVMEM_TYPE_Q5_0:
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q5_0><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
+            break;
+        case KVMEM_TYPE_F16:
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_F16><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
+            break;
+        default:
+            fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported V type");
+            return false;
+    }
+    return hip_ok(ctx, hipGetLastError(), "stage-in K/V kernel launch");
+}
+
+bool launch_quant_kv(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_t n_v,
+                     const BlockSource &sk, const BlockSource &sv) {
+    const uint32_t grid = n_k + n_v;
+    if (grid == 0) {
+        return true;
+    }
+    switch (tk) {
+        case KVMEM_TYPE_Q8_0: return launch_kv_v<KVMEM_TYPE_Q8_0>(ctx, tv, grid, sk, sv, n_k);
+        case KVMEM_TYPE_Q4_0: return launch_kv_v<KVMEM_TYPE_Q4_0>(ctx, tv, grid, sk, sv, n_k);
+        case KVMEM_TYPE_Q5_0: return launch_kv_v<KVMEM_TYPE_Q5_0>(ctx, tv, grid, sk, sv, n_k);
+        case KVMEM_TYPE_F16: return launch_kv_v<KVMEM_TYPE_F16>(ctx, tv, grid, sk, sv, n_k);
+        default:
+            fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported K type");
+            return false;
+    }
+}
+
 static bool aligned16(const void *p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
@@ -405,24 +470,38 @@ static int check_pool(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, uint32_t n
     return KVMEM_HIP_OK;
 }
 
-// Device copy of a pool's per-layer pointer tables: K at [0, L), V at [L, 2L).
-static const void *const *upload_layer_tables(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool,
-                                              bool want_v) {
-    std::vector<const void *> t(2 * static_cast<size_t>(pool->n_layers), nullptr);
-    for (uint32_t l = 0; l < pool->n_layers; ++l) {
-        t[l] = pool->k_layers[l];
-        t[pool->n_layers + l] = want_v ? pool->v_layers[l] : nullptr;
+// One upload holding a block job's device tables: the pool's per-layer
+// pointers (K at [0, L), V at [L, 2L)) followed by the items ([n][3] u32:
+// block, slot, tokens).  A single upload per call keeps both inside one
+// upload-ring slot for as long as the call's kernels need them.
+struct JobTables {
+    const void *const *layers = nullptr;
+    const uint32_t *items = nullptr;
+};
+
+static bool upload_block_job(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, bool want_v,
+                             const std::vector<uint32_t> &items, JobTables &out) {
+    const size_t L = pool->n_layers;
+    std::vector<uint64_t> buf(2 * L + (items.size() + 1) / 2, 0);
+    for (size_t l = 0; l < L; ++l) {
+        buf[l] = reinterpret_cast<uint64_t>(pool->k_layers[l]);
+        buf[L + l] = want_v ? reinterpret_cast<uint64_t>(pool->v_layers[l]) : 0;
     }
-    return static_cast<const void *const *>(
-        upload(ctx, t.data(), t.size() * sizeof(void *), "stage-in layer tables"));
+    std::memcpy(buf.data() + 2 * L, items.data(), items.size() * sizeof(uint32_t));
+    void *dev = upload(ctx, buf.data(), buf.size() * sizeof(uint64_t), "stage-in job tables");
+    if (!dev) {
+        return false;
+    }
+    out.layers = static_cast<const void *const *>(dev);
+    out.items = reinterpret_cast<const uint32_t *>(static_cast<const uint64_t *>(dev) + 2 * L);
+    return true;
 }
 
-// Launch one kind (K or V) of a block job.  items_dev: device [n][3].
-static int launch_blocks(kvmem_hip_ctx *ctx, int type, const uint8_t *base, uint64_t block_stride,
-                         uint64_t layer_stride, const void *layer_table_dev, uint32_t n_layers,
-                         uint32_t block_tokens, uint32_t n_embd, const uint32_t *items_dev,
-                         uint32_t n_items) {
-    const uint32_t gpr = n_embd / 32;
+// Source of one kind (K or V) of a block job.  items_dev: device [n][3].
+static BlockSource make_block_source(int type, const uint8_t *base, uint64_t block_stride,
+                                     uint64_t layer_stride, const void *layer_table_dev,
+                                     uint32_t n_layers, uint32_t block_tokens, uint32_t n_embd,
+                                     const uint32_t *items_dev) {
     BlockSource s;
     s.base = base;
     s.layer_dst = static_cast<const uint8_t *const *>(layer_table_dev);
@@ -431,15 +510,28 @@ static int launch_blocks(kvmem_hip_ctx *ctx, int type, const uint8_t *base, uint
     s.layer_stride = layer_stride;
     s.n_layers = n_layers;
     s.block_tokens = block_tokens;
-    s.gpr = gpr;
-    s.row_bytes = gpr * group_bytes(type);
-    s.chunks_per_op = (block_tokens * gpr + kChunkGroups - 1) / kChunkGroups;
-    const uint64_t n_chunks = static_cast<uint64_t>(n_items) * n_layers * s.chunks_per_op;
-    if (n_chunks > 0x7fffffffu) {
+    s.gpr = n_embd / 32;
+    s.row_bytes = s.gpr * group_bytes(type);
+    s.chunks_per_op = (block_tokens * s.gpr + kChunkGroups - 1) / kChunkGroups;
+    return s;
+}
+
+// One launch for K (and V when sv_on): chunks of K first, then of V.
+static int launch_block_job(kvmem_hip_ctx *ctx, int type_k, const BlockSource &sk, int type_v,
+                            const BlockSource *sv, uint32_t n_items) {
+    const uint64_t nk = static_cast<uint64_t>(n_items) * sk.n_layers * sk.chunks_per_op;
+    const uint64_t nv = sv ? static_cast<uint64_t>(n_items) * sv->n_layers * sv->chunks_per_op : 0;
+    if (nk + nv > 0x7fffffffu) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "stage-in: too many chunks in one call");
     }
-    return launch_quant(ctx, type, static_cast<uint32_t>(n_chunks), s) ? KVMEM_HIP_OK
-                                                                        : KVMEM_HIP_ERR_RUNTIME;
+    bool ok;
+    if (sv) {
+        ok = launch_quant_kv(ctx, type_k, type_v, static_cast<uint32_t>(nk),
+                             static_cast<uint32_t>(nv), sk, *sv);
+    } else {
+        ok = launch_quant(ctx, type_k, static_cast<uint32_t>(nk), sk);
+    }
+    return ok ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
 }
 
 }  // namespace kvmem_hip
@@ -531,6 +623,10 @@ int kvmem_hip_stagein_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
         !aligned16(hist->k) || (want_v && !aligned16(hist->v))) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "stagein_blocks: bad history geometry/alignment");
     }
+    const uint32_t cap = hist->capacity_blocks ? hist->capacity_blocks : hist->n_blocks;
+    if (cap < hist->n_blocks) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "stagein_blocks: capacity_blocks below n_blocks");
+    }
     int st = check_pool(ctx, pool, hist->n_layers, T, hist->n_embd_k, hist->n_embd_v, want_v);
     if (st != KVMEM_HIP_OK) {
         return st;
@@ -546,22 +642,23 @@ int kvmem_hip_stagein_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
         items[3 * i + 2] = last ? std::min(hist->last_block_tokens, T) : T;
     }
     (void) hipSetDevice(ctx->device);
-    void *items_dev = upload(ctx, items.data(), items.size() * sizeof(uint32_t), "stagein_blocks items");
-    const void *const *tables = upload_layer_tables(ctx, pool, want_v);
-    if (!items_dev || !tables) {
+    JobTables jt;
+    if (!upload_block_job(ctx, pool, want_v, items, jt)) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
-    perf_begin(ctx, kPerfSet);
     const uint64_t bk = static_cast<uint64_t>(T) * hist->n_embd_k * 2u;
-    st = launch_blocks(ctx, pool->type_k, static_cast<const uint8_t *>(hist->k), bk,
-                       bk * hist->n_blocks, tables, hist->n_layers, T, hist->n_embd_k,
-                       static_cast<const uint32_t *>(items_dev), n);
-    if (st == KVMEM_HIP_OK && want_v) {
+    const BlockSource sk = make_block_source(pool->type_k, static_cast<const uint8_t *>(hist->k), bk,
+                                             bk * cap, jt.layers, hist->n_layers, T,
+                                             hist->n_embd_k, jt.items);
+    BlockSource sv{};
+    if (want_v) {
         const uint64_t bv = static_cast<uint64_t>(T) * hist->n_embd_v * 2u;
-        st = launch_blocks(ctx, pool->type_v, static_cast<const uint8_t *>(hist->v), bv,
-                           bv * hist->n_blocks, tables + hist->n_layers, hist->n_layers, T, hist->n_embd_v,
-                           static_cast<const uint32_t *>(items_dev), n);
+        sv = make_block_source(pool->type_v, static_cast<const uint8_t *>(hist->v), bv,
+                               bv * cap, jt.layers + hist->n_layers, hist->n_layers, T,
+                               hist->n_embd_v, jt.items);
     }
+    perf_begin(ctx, kPerfSet);
+    st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n);
     perf_end(ctx, kPerfSet);
     return st;
 }
@@ -628,8 +725,17 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
             hipEventRecord(ctx->h2d_consumed[r], ctx->stream);
         }
     }
-    const void *const *tables = upload_layer_tables(ctx, pool, want_v);
-    if (!tables) {
+    // items of every batch, block index relative to its ring slot
+    std::vector<uint32_t> items(3 * static_cast<size_t>(n));
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t b = block_ids[i];
+        items[3 * i + 0] = i % per_slot;
+        items[3 * i + 1] = slots[i];
+        items[3 * i + 2] = (b + 1 == hist->n_blocks && hist->last_block_tokens != 0)
+                               ? std::min(hist->last_block_tokens, T) : T;
+    }
+    JobTables jt;
+    if (!upload_block_job(ctx, pool, want_v, items, jt)) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     perf_begin(ctx, kPerfSet);
@@ -643,35 +749,28 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
         if (!hip_ok(ctx, hipStreamWaitEvent(ctx->copy_stream, ctx->h2d_consumed[r], 0), "h2d wait consumed")) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
-        std::vector<uint32_t> items(3 * static_cast<size_t>(cnt));
         for (uint32_t j = 0; j < cnt; ++j) {
             const uint32_t b = block_ids[first + j];
-            const uint32_t ntok = (b + 1 == hist->n_blocks && hist->last_block_tokens != 0)
-                                      ? std::min(hist->last_block_tokens, T) : T;
             if (!hip_ok(ctx, hipMemcpyAsync(slot_base + j * span, host + static_cast<uint64_t>(b) * span,
                                             span, hipMemcpyHostToDevice, ctx->copy_stream),
                         "h2d block copy")) {
                 return KVMEM_HIP_ERR_RUNTIME;
             }
             ctx->h2d_bytes += span;
-            items[3 * j + 0] = j;
-            items[3 * j + 1] = slots[first + j];
-            items[3 * j + 2] = ntok;
         }
         if (!hip_ok(ctx, hipEventRecord(ctx->h2d_copied[r], ctx->copy_stream), "h2d record") ||
             !hip_ok(ctx, hipStreamWaitEvent(ctx->stream, ctx->h2d_copied[r], 0), "h2d wait copied")) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
-        void *items_dev = upload(ctx, items.data(), items.size() * sizeof(uint32_t), "h2d items");
-        if (!items_dev) {
-            return KVMEM_HIP_ERR_RUNTIME;
+        const uint32_t *batch_items = jt.items + 3 * static_cast<size_t>(first);
+        const BlockSource sk = make_block_source(pool->type_k, slot_base, span, layer_bytes, jt.layers,
+                                                 L, T, hist->n_embd_k, batch_items);
+        BlockSource sv{};
+        if (want_v) {
+            sv = make_block_source(pool->type_v, slot_base + kbytes, span, layer_bytes, jt.layers + L, L,
+                                   T, hist->n_embd_v, batch_items);
         }
-        st = launch_blocks(ctx, pool->type_k, slot_base, span, layer_bytes, tables, L, T,
-                           hist->n_embd_k, static_cast<const uint32_t *>(items_dev), cnt);
-        if (st == KVMEM_HIP_OK && want_v) {
-            st = launch_blocks(ctx, pool->type_v, slot_base + kbytes, span, layer_bytes, tables + L,
-                               L, T, hist->n_embd_v, static_cast<const uint32_t *>(items_dev), cnt);
-        }
+        st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, cnt);
         if (st != KVMEM_HIP_OK) {
             return st;
         }

@@ -1,0 +1,289 @@
+"""ctypes view of the reselect engine and host store (include/kvmem_host.h).
+
+Store  -- the host block table / top-k / diff / slot plan alone (no GPU);
+          method names follow KvMemStore / KvMemRuntime
+          (kvmem/include/kvmem/kvmem_store.hpp, kvmem_runtime.hpp).
+Engine -- one agent step on the GPU: preview (score + top-k) then apply
+          (diff, slots, stage-in), as llama_memory_kvmem::preview_retrieval /
+          apply_selection (src/adapter/llama-memory-kvmem.cpp:3047-3263).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Sequence
+
+from . import (ERR_STALE, OK, KvMemError, StaleSelection, TYPE_BF16, TYPE_Q8_0, LAYER_MEAN,
+               load_library)
+
+
+class PlanStats(C.Structure):
+    _fields_ = [("n_stage_in", C.c_uint32), ("n_stage_out", C.c_uint32), ("n_staged", C.c_uint32),
+                ("n_moved", C.c_uint32), ("selection_overlap_blocks", C.c_uint32),
+                ("gpu_reused_blocks", C.c_uint32), ("retained_position_stable", C.c_uint32),
+                ("retained_position_moved", C.c_uint32), ("total_window_tokens", C.c_uint32)]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+class EngineParams(C.Structure):
+    _fields_ = [("device", C.c_int32), ("n_layers", C.c_uint32), ("block_tokens", C.c_uint32),
+                ("n_head", C.c_uint32), ("n_head_kv", C.c_uint32), ("head_dim", C.c_uint32),
+                ("n_embd_v", C.c_uint32), ("budget_blocks", C.c_uint32),
+                ("reserve_blocks", C.c_uint32), ("sink_blocks", C.c_uint32),
+                ("recent_blocks", C.c_uint32), ("type_k", C.c_int32), ("type_v", C.c_int32),
+                ("tie_lower_index", C.c_int32), ("layer_reduce", C.c_int32),
+                ("canonical_layout", C.c_int32)]
+
+
+_bound = set()
+
+
+def bind(lib: C.CDLL) -> C.CDLL:
+    if id(lib) in _bound:
+        return lib
+    vp, u32, i32, u64 = C.c_void_p, C.c_uint32, C.c_int, C.c_uint64
+    pu32, pi32, pu8, pi64 = (C.POINTER(C.c_uint32), C.POINTER(C.c_int32), C.POINTER(C.c_uint8),
+                             C.POINTER(C.c_int64))
+    pd = C.POINTER(C.c_double)
+
+    def sig(name, res, *args):
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = list(args)
+
+    sig("kvmem_store_create", i32, u32, u32, u32, u32, i32, u32, C.POINTER(vp))
+    sig("kvmem_store_destroy", None, vp)
+    sig("kvmem_store_register_append", i32, vp, u32)
+    sig("kvmem_store_truncate_to", i32, vp, u32)
+    sig("kvmem_store_block_count", u32, vp)
+    sig("kvmem_store_total_tokens", u32, vp)
+    sig("kvmem_store_set_scores", i32, vp, pd, u32)
+    sig("kvmem_store_pick_topk", i32, vp, pu32, u32, pu32, pu32)
+    sig("kvmem_store_apply", i32, vp, pu32, u32, pu32, pu32, pu32, pu32, C.POINTER(PlanStats))
+    sig("kvmem_store_blocks", i32, vp, pi32, pu8, pu8, pi64)
+    sig("kvmem_store_commit_resident", i32, vp, pu32, u32)
+    sig("kvmem_engine_default_params", EngineParams)
+    sig("kvmem_engine_create", i32, C.POINTER(EngineParams), C.POINTER(vp))
+    sig("kvmem_engine_destroy", None, vp)
+    sig("kvmem_engine_last_error", C.c_char_p, vp)
+    sig("kvmem_engine_ctx", vp, vp)
+    sig("kvmem_engine_set_device_history", i32, vp, vp, vp, u32, u32)
+    sig("kvmem_engine_set_host_history", i32, vp, vp, u32)
+    sig("kvmem_engine_append_tokens", i32, vp, u32)
+    sig("kvmem_engine_truncate_to", i32, vp, u32)
+    sig("kvmem_engine_block_count", u32, vp)
+    sig("kvmem_engine_total_tokens", u32, vp)
+    sig("kvmem_engine_epoch", u64, vp)
+    sig("kvmem_engine_n_slots", u32, vp)
+    sig("kvmem_engine_pool_layer", i32, vp, u32, C.POINTER(vp), C.POINTER(vp))
+    sig("kvmem_engine_block_slots", i32, vp, pi32)
+    sig("kvmem_engine_preview", i32, vp, vp, i32, u32, pu32, u32, pu32, pu32, C.POINTER(u64), pu32)
+    sig("kvmem_engine_apply", i32, vp, u64, u32, pu32, u32, C.POINTER(PlanStats))
+    sig("kvmem_engine_apply_retrieval", i32, vp, vp, i32, u32, pu32, u32, C.POINTER(PlanStats))
+    sig("kvmem_engine_scores", i32, vp, C.POINTER(C.c_float), u32)
+    _bound.add(id(lib))
+    return lib
+
+
+def _u32(xs: Sequence[int]):
+    xs = list(xs)
+    return (C.c_uint32 * max(1, len(xs)))(*xs), len(xs)
+
+
+@dataclass
+class Selection:
+    """llama_kvmem_selection (src/adapter/llama-kvmem-hooks.h:140-144)."""
+    epoch: int
+    rows: int
+    blocks: list
+
+
+class Store:
+    """Host store + slot plan (no device).  Every block starts outside the
+    pool; apply() runs prepare_selection + finish_reselect."""
+
+    def __init__(self, block_tokens: int = 128, budget_blocks: int = 256, sink_blocks: int = 1,
+                 recent_blocks: int = 0, tie_lower_index: bool = True, n_slots: int = 384):
+        self.lib = bind(load_library())
+        h = C.c_void_p()
+        rc = self.lib.kvmem_store_create(block_tokens, budget_blocks, sink_blocks, recent_blocks,
+                                         int(tie_lower_index), n_slots, C.byref(h))
+        if rc != OK:
+            raise KvMemError(rc, "kvmem_store_create failed")
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.kvmem_store_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def register_append(self, n_tokens: int) -> None:
+        self.lib.kvmem_store_register_append(self.h, n_tokens)
+
+    def truncate_to(self, token_pos: int) -> None:
+        self.lib.kvmem_store_truncate_to(self.h, token_pos)
+
+    def block_count(self) -> int:
+        return self.lib.kvmem_store_block_count(self.h)
+
+    def total_tokens(self) -> int:
+        return self.lib.kvmem_store_total_tokens(self.h)
+
+    def set_retrieval_scores(self, scores: Sequence[float]) -> None:
+        arr = (C.c_double * max(1, len(scores)))(*[float(x) for x in scores])
+        self.lib.kvmem_store_set_scores(self.h, arr, len(scores))
+
+    def pick_topk_blocks(self, mandatory: Sequence[int] = ()) -> list:
+        m, nm = _u32(mandatory)
+        out = (C.c_uint32 * max(1, self.block_count()))()
+        n = C.c_uint32(0)
+        self.lib.kvmem_store_pick_topk(self.h, m, nm, out, C.byref(n))
+        return list(out[: n.value])
+
+    def apply(self, sel: Sequence[int]) -> tuple[list, list, dict]:
+        s, ns = _u32(sel)
+        cap = max(1, self.block_count())
+        si, so = (C.c_uint32 * cap)(), (C.c_uint32 * cap)()
+        ni, no = C.c_uint32(0), C.c_uint32(0)
+        st = PlanStats()
+        rc = self.lib.kvmem_store_apply(self.h, s, ns, si, C.byref(ni), so, C.byref(no), C.byref(st))
+        if rc != OK:
+            raise KvMemError(rc, "kvmem_store_apply failed")
+        return list(si[: ni.value]), list(so[: no.value]), st.as_dict()
+
+    def blocks(self) -> dict:
+        n = self.block_count()
+        slot = (C.c_int32 * max(1, n))()
+        tier = (C.c_uint8 * max(1, n))()
+        ws = (C.c_uint8 * max(1, n))()
+        baked = (C.c_int64 * max(1, n))()
+        self.lib.kvmem_store_blocks(self.h, slot, tier, ws, baked)
+        return {"gpu_slot": list(slot[:n]), "tier": list(tier[:n]), "in_ws": list(ws[:n]),
+                "baked_pos": list(baked[:n])}
+
+    def commit_resident_selection(self, sel: Sequence[int]) -> bool:
+        s, n = _u32(sel)
+        return bool(self.lib.kvmem_store_commit_resident(self.h, s, n))
+
+
+class Engine:
+    """The reselect engine on one GPU (owns its context, pool and store)."""
+
+    def __init__(self, **params):
+        self.lib = bind(load_library())
+        p = self.lib.kvmem_engine_default_params()
+        for k, v in params.items():
+            if not hasattr(p, k):
+                raise TypeError(f"unknown engine parameter {k}")
+            setattr(p, k, int(v))
+        self.params = p
+        h = C.c_void_p()
+        rc = self.lib.kvmem_engine_create(C.byref(p), C.byref(h))
+        if rc != OK:
+            raise KvMemError(rc, "kvmem_engine_create failed")
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.kvmem_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def check(self, rc: int, what: str) -> None:
+        if rc == OK:
+            return
+        msg = self.lib.kvmem_engine_last_error(self.h).decode()
+        raise (StaleSelection if rc == ERR_STALE else KvMemError)(rc, f"{what}: {msg}")
+
+    def ctx_handle(self) -> int:
+        return self.lib.kvmem_engine_ctx(self.h)
+
+    def set_device_history(self, k_ptr: int, v_ptr: int, capacity_blocks: int, n_tokens: int):
+        self.check(self.lib.kvmem_engine_set_device_history(self.h, k_ptr, v_ptr, capacity_blocks,
+                                                            n_tokens), "set_device_history")
+
+    def set_host_history(self, base_ptr: int | None, capacity_blocks: int = 0):
+        self.check(self.lib.kvmem_engine_set_host_history(self.h, base_ptr or None, capacity_blocks),
+                   "set_host_history")
+
+    def append_tokens(self, n: int):
+        self.check(self.lib.kvmem_engine_append_tokens(self.h, n), "append_tokens")
+
+    def truncate_to(self, pos: int):
+        self.check(self.lib.kvmem_engine_truncate_to(self.h, pos), "truncate_to")
+
+    def block_count(self) -> int:
+        return self.lib.kvmem_engine_block_count(self.h)
+
+    def total_tokens(self) -> int:
+        return self.lib.kvmem_engine_total_tokens(self.h)
+
+    def epoch(self) -> int:
+        return self.lib.kvmem_engine_epoch(self.h)
+
+    def n_slots(self) -> int:
+        return self.lib.kvmem_engine_n_slots(self.h)
+
+    def pool_layer(self, layer: int) -> tuple[int, int]:
+        k, v = C.c_void_p(), C.c_void_p()
+        self.check(self.lib.kvmem_engine_pool_layer(self.h, layer, C.byref(k), C.byref(v)), "pool_layer")
+        return k.value, v.value
+
+    def block_slots(self) -> list:
+        n = self.block_count()
+        out = (C.c_int32 * max(1, n))()
+        self.check(self.lib.kvmem_engine_block_slots(self.h, out), "block_slots")
+        return list(out[:n])
+
+    def preview(self, q_ptr: int, n_q_tokens: int, q_type: int = TYPE_BF16,
+                mandatory: Sequence[int] = ()) -> Selection:
+        m, nm = _u32(mandatory)
+        out = (C.c_uint32 * max(1, self.block_count()))()
+        n, rows = C.c_uint32(0), C.c_uint32(0)
+        ep = C.c_uint64(0)
+        self.check(self.lib.kvmem_engine_preview(self.h, q_ptr, q_type, n_q_tokens, m, nm, out,
+                                                 C.byref(n), C.byref(ep), C.byref(rows)), "preview")
+        return Selection(ep.value, rows.value, list(out[: n.value]))
+
+    def apply(self, sel: Selection) -> dict:
+        s, n = _u32(sel.blocks)
+        st = PlanStats()
+        self.check(self.lib.kvmem_engine_apply(self.h, sel.epoch, sel.rows, s, n, C.byref(st)), "apply")
+        return st.as_dict()
+
+    def apply_retrieval(self, q_ptr: int, n_q_tokens: int, q_type: int = TYPE_BF16,
+                        mandatory: Sequence[int] = ()) -> dict:
+        m, nm = _u32(mandatory)
+        st = PlanStats()
+        self.check(self.lib.kvmem_engine_apply_retrieval(self.h, q_ptr, q_type, n_q_tokens, m, nm,
+                                                         C.byref(st)), "apply_retrieval")
+        return st.as_dict()
+
+    def scores(self) -> list:
+        n = self.block_count()
+        out = (C.c_float * max(1, n))()
+        self.check(self.lib.kvmem_engine_scores(self.h, out, n), "scores")
+        return list(out[:n])
+
+
+__all__ = ["Store", "Engine", "Selection", "PlanStats", "EngineParams", "bind",
+           "TYPE_Q8_0", "LAYER_MEAN"]

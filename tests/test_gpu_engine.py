@@ -1,0 +1,212 @@
+"""The reselect engine (include/kvmem_host.h) on the GPU against the oracle.
+
+One agent step = preview (device scorer + device top-k with the store's
+sink / mandatory / recent charge) then apply (store diff, slot plan, one
+stage-in launch).  Checked: scores within 1e-3 relative of the fp64
+oracle, the selection equal to the oracle's top-k over the engine's own
+scores, every selected block's pool rows bit-exact against the oracle's
+quantizer, the stale-selection rule, canonical slot layout, a growing
+partial tail block, stage-in from pinned host history, and a pinned-host
+stage-in long enough to cycle the device upload ring many times.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from conftest import load_pkg  # noqa: E402
+
+kv = load_pkg()
+from kvmem_amd import host, workloads  # noqa: E402
+
+RTOL = 1e-3
+L, T, HKV, HQ, D = 2, 128, 4, 24, 256
+E = HKV * D
+
+
+def announce(msg: str) -> None:
+    print(f"[engine] {msg}", flush=True)
+
+
+def history(cap: int, seed: int, Tq: int = 8):
+    k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=cap, Tq=Tq, seed=seed, with_v=True)
+    torch.cuda.synchronize()
+    return k, v, q
+
+
+def make_engine(budget: int, reserve: int, type_k=kv.TYPE_Q8_0, type_v=kv.TYPE_Q8_0, **kw):
+    return host.Engine(n_layers=L, block_tokens=T, n_head=HQ, n_head_kv=HKV, head_dim=D,
+                       budget_blocks=budget, reserve_blocks=reserve, type_k=type_k, type_v=type_v,
+                       **kw)
+
+
+def check_pool(eng, oracle, k, v, sel, type_k, type_v, ntok_of=None):
+    kb = workloads.to_bits(torch, k)
+    vb = workloads.to_bits(torch, v)
+    slots = eng.block_slots()
+    for layer in range(L):
+        for which, src, ty in ((0, kb, type_k), (1, vb, type_v)):
+            rb = kv.row_size(ty, E)
+            ptr = eng.pool_layer(layer)[which]
+            n = eng.n_slots() * T * rb
+            buf = torch.empty(n, dtype=torch.uint8, device="cuda")
+            c = kv.Context(0)
+            c.d2d_batched([ptr], [buf.data_ptr()], [n])
+            c.sync()
+            c.close()
+            pool = buf.cpu().numpy().reshape(eng.n_slots() * T, rb)
+            for b in sel:
+                s = slots[b]
+                assert s >= 0, f"block {b} has no slot"
+                nt = T if ntok_of is None else ntok_of(b)
+                rows = src[layer, b].reshape(T, E)[:nt]
+                want = oracle.quantize_rows_f16(ty, rows)
+                got = pool[s * T: s * T + nt]
+                assert np.array_equal(got, want), f"layer {layer} {'KV'[which]} block {b} slot {s}"
+
+
+def oracle_scores(oracle, q, k, n_blocks, last_T=0):
+    ls = oracle.score_pertoken_max(q.float().cpu().numpy(), workloads.to_bits(torch, k[:, :n_blocks]),
+                                   last_T)
+    return oracle.combine_layers(ls, 0)
+
+
+def test_engine_two_steps_vs_oracle(oracle):
+    announce("two agent steps, 40 blocks, budget 8 + 4 reserve, K q8_0 / V q4_0")
+    cap, nb = 48, 40
+    k, v, q1 = history(cap, seed=31)
+    q2 = (q1.float() * -1.0).to(torch.bfloat16)     # a different query direction
+    with make_engine(8, 4, kv.TYPE_Q8_0, kv.TYPE_Q4_0) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        assert eng.block_count() == nb
+        sel1 = eng.preview(q1.data_ptr(), q1.shape[1])
+        got_scores = np.array(eng.scores(), dtype=np.float64)
+        want_scores = oracle_scores(oracle, q1, k, nb)
+        rel = np.abs(got_scores - want_scores) / np.maximum(np.abs(want_scores), 1e-6)
+        assert rel.max() <= RTOL, f"scores: max rel err {rel.max():.3e}"
+        assert sel1.blocks == oracle.pick_topk(got_scores.astype(np.float32).astype(np.float64), 8, sink=1)
+        st1 = eng.apply(sel1)
+        assert st1["n_staged"] == 8 and st1["n_stage_in"] == 8
+        check_pool(eng, oracle, k, v, sel1.blocks, kv.TYPE_Q8_0, kv.TYPE_Q4_0)
+
+        sel2 = eng.preview(q2.data_ptr(), q2.shape[1])
+        s2 = np.array(eng.scores(), dtype=np.float64)
+        assert sel2.blocks == oracle.pick_topk(s2.astype(np.float32).astype(np.float64), 8, sink=1)
+        st2 = eng.apply(sel2)
+        new = set(sel2.blocks) - set(sel1.blocks)
+        assert st2["n_staged"] == len(new)
+        assert st2["selection_overlap_blocks"] == len(set(sel1.blocks) & set(sel2.blocks))
+        check_pool(eng, oracle, k, v, sel2.blocks, kv.TYPE_Q8_0, kv.TYPE_Q4_0)
+        # the stage-in slots came from the LIFO free list of the store mirror
+        st = host.Store(T, 8, 1, 0, True, eng.n_slots())
+        st.register_append(nb * T)
+        st.apply(sel1.blocks)
+        st.apply(sel2.blocks)
+        assert st.blocks()["gpu_slot"] == eng.block_slots()
+
+
+def test_engine_stale_selection():
+    announce("stale selection after the history grows")
+    cap = 12
+    k, v, q = history(cap, seed=5)
+    with make_engine(4, 2) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, 10 * T)
+        sel = eng.preview(q.data_ptr(), q.shape[1])
+        eng.append_tokens(T)
+        with pytest.raises(kv.StaleSelection):
+            eng.apply(sel)
+        fresh = eng.preview(q.data_ptr(), q.shape[1])
+        eng.apply(fresh)
+
+
+def test_engine_canonical_layout(oracle):
+    announce("canonical layout: selected block i in slot i")
+    cap, nb = 32, 30
+    k, v, q1 = history(cap, seed=9)
+    q2 = (q1.float() * -1.0).to(torch.bfloat16)
+    with make_engine(10, 4, canonical_layout=1) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        for q in (q1, q2, q1):
+            sel = eng.preview(q.data_ptr(), q.shape[1])
+            eng.apply(sel)
+            slots = eng.block_slots()
+            assert [slots[b] for b in sel.blocks] == list(range(len(sel.blocks)))
+            check_pool(eng, oracle, k, v, sel.blocks, kv.TYPE_Q8_0, kv.TYPE_Q8_0)
+
+
+def test_engine_partial_tail_grows(oracle):
+    announce("partial tail block kept by recent=1, then grown and re-staged")
+    cap = 16
+    k, v, q = history(cap, seed=13)
+    n_tok = 9 * T + 37
+    with make_engine(4, 2, recent_blocks=1) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, n_tok)
+        assert eng.block_count() == 10
+        sel = eng.preview(q.data_ptr(), q.shape[1])
+        assert 9 in sel.blocks and 0 in sel.blocks
+        eng.apply(sel)
+        check_pool(eng, oracle, k, v, sel.blocks, kv.TYPE_Q8_0, kv.TYPE_Q8_0,
+                   ntok_of=lambda b: 37 if b == 9 else T)
+        eng.append_tokens(50)      # the tail now has 87 tokens
+        sel = eng.preview(q.data_ptr(), q.shape[1])
+        st = eng.apply(sel)
+        assert st["n_staged"] >= 1
+        check_pool(eng, oracle, k, v, sel.blocks, kv.TYPE_Q8_0, kv.TYPE_Q8_0,
+                   ntok_of=lambda b: 87 if b == 9 else T)
+
+
+def block_major_pinned(k, v, n_blocks):
+    """[block][layer][K rows, V rows] halves in pinned host memory."""
+    kk = k[:, :n_blocks].permute(1, 0, 2, 3, 4).reshape(n_blocks, L, T * E)
+    vv = v[:, :n_blocks].permute(1, 0, 2, 3, 4).reshape(n_blocks, L, T * E)
+    host_buf = torch.empty((n_blocks, L * 2 * T * E), dtype=torch.float16, pin_memory=True)
+    host_buf.copy_(torch.cat([kk, vv], dim=2).reshape(n_blocks, -1).cpu())
+    return host_buf
+
+
+def test_engine_pinned_host_history(oracle):
+    announce("stage-in from pinned host history")
+    cap, nb = 24, 24
+    k, v, q = history(cap, seed=17)
+    hb = block_major_pinned(k, v, nb)
+    with make_engine(12, 4, kv.TYPE_Q5_0, kv.TYPE_Q8_0) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        eng.set_host_history(hb.data_ptr(), nb)
+        sel = eng.preview(q.data_ptr(), q.shape[1])
+        eng.apply(sel)
+        check_pool(eng, oracle, k, v, sel.blocks, kv.TYPE_Q5_0, kv.TYPE_Q8_0)
+
+
+def test_stagein_host_many_ring_batches(ctx, oracle):
+    """Regression: a pinned-host stage-in spanning many device-ring batches
+    (per-call tables must stay valid through every batch)."""
+    announce("pinned-host stage-in, 4 layers, 47 blocks in 5 ring batches, K q8_0 / V q4_0")
+    Lh, Ek, Ev, nb, n_slots = 4, 2048, 1024, 60, 64
+    rng = np.random.default_rng(21)
+    kh = workloads.heavy_tailed(22, (nb, Lh, T, Ek))
+    vh = workloads.heavy_tailed(23, (nb, Lh, T, Ev))
+    span = Lh * T * (Ek + Ev)
+    hb = torch.empty((nb, span), dtype=torch.int16, pin_memory=True)
+    hb.copy_(torch.from_numpy(np.concatenate([kh.reshape(nb, Lh, -1), vh.reshape(nb, Lh, -1)],
+                                             axis=2).reshape(nb, span).view(np.int16)))
+    ids = sorted(rng.choice(nb, 47, replace=False).tolist())
+    slots = rng.permutation(n_slots)[:47].tolist()
+    rbk, rbv = kv.row_size(kv.TYPE_Q8_0, Ek), kv.row_size(kv.TYPE_Q4_0, Ev)
+    pk = [torch.zeros(n_slots * T * rbk, dtype=torch.uint8, device="cuda") for _ in range(Lh)]
+    pv = [torch.zeros(n_slots * T * rbv, dtype=torch.uint8, device="cuda") for _ in range(Lh)]
+    pool = ctx.make_pool(Lh, n_slots, T, Ek, Ev, kv.TYPE_Q8_0, kv.TYPE_Q4_0,
+                         [p.data_ptr() for p in pk], [p.data_ptr() for p in pv])
+    hh = kv.HostHistory(hb.data_ptr(), Lh, nb, T, Ek, Ev, 0)
+    torch.cuda.synchronize()
+    ctx.stagein_blocks_host(hh, pool, ids, slots)
+    ctx.sync()
+    for layer in range(Lh):
+        gk = pk[layer].cpu().numpy().reshape(n_slots * T, rbk)
+        gv = pv[layer].cpu().numpy().reshape(n_slots * T, rbv)
+        for b, s in zip(ids, slots):
+            assert np.array_equal(gk[s * T:(s + 1) * T], oracle.quantize_rows_f16(kv.TYPE_Q8_0, kh[b, layer]))
+            assert np.array_equal(gv[s * T:(s + 1) * T], oracle.quantize_rows_f16(kv.TYPE_Q4_0, vh[b, layer]))
