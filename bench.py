@@ -43,6 +43,10 @@ N_SLOTS = BUDGET + RESERVE
 N_CHANGED = round(0.3 * BUDGET)   # 77
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE on this
+# workload, scaled by the copy-kernel calibration (profiles/traffic_reselect_256k.md)
+SCORE_TRAFFIC_BYTES = 8.597e9 + 2.945e7
+STAGEIN_TRAFFIC_BYTES = 6.458e8 + 3.431e8
 MFMA_F16_PEAK_TFLOPS = 2500.0
 PCIE_PEAK_GBS = 64.0
 
@@ -60,16 +64,61 @@ def load_pkg():
     return mod
 
 
-def make_engine(kv, torch, k, v):
+def make_engine(kv, torch, k, v, n_blocks: int = B, budget: int = BUDGET, reserve: int = RESERVE,
+                type_k: int | None = None, type_v: int | None = None):
     """The reselect engine over the device-resident history (C++ host store
     + slot plan, gfx950 kernels)."""
     from kvmem_amd import host
     eng = host.Engine(n_layers=L, block_tokens=T, n_head=HQ, n_head_kv=HKV, head_dim=D,
-                      budget_blocks=BUDGET, reserve_blocks=RESERVE, sink_blocks=1, recent_blocks=0,
-                      type_k=kv.TYPE_Q8_0, type_v=kv.TYPE_Q8_0, tie_lower_index=1,
+                      budget_blocks=budget, reserve_blocks=reserve, sink_blocks=1, recent_blocks=0,
+                      type_k=kv.TYPE_Q8_0 if type_k is None else type_k,
+                      type_v=kv.TYPE_Q8_0 if type_v is None else type_v, tie_lower_index=1,
                       layer_reduce=kv.LAYER_MEAN)
-    eng.set_device_history(k.data_ptr(), v.data_ptr(), B, B * T)
+    eng.set_device_history(k.data_ptr(), v.data_ptr(), n_blocks, n_blocks * T)
     return eng
+
+
+def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, warmup: int) -> dict:
+    """`warmup` untimed then `steps` timed agent steps, each from the
+    previous selection `prev` (restored, untimed, between steps).  Returns
+    mean wall ms per step and the per-stage device ms of the engine stream."""
+    from kvmem_amd import host
+
+    def restore():
+        eng.apply(host.Selection(eng.epoch(), eng.total_tokens(), prev))
+
+    def step() -> dict:
+        return eng.apply_retrieval(q.data_ptr(), n_q_tokens)
+
+    restore()
+    for _ in range(warmup):
+        step()
+        restore()
+    ctx.perf_enable(True)
+    times, staged, score_ms, set_ms, sel_ms = [], [], 0.0, 0.0, 0.0
+    for _ in range(steps):
+        ctx.perf_reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        st = step()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        pf = ctx.perf()
+        score_ms += pf["score_ms"]
+        set_ms += pf["set_ms"]
+        sel_ms += pf["topk_ms"]
+        staged.append(st["n_staged"])
+        restore()
+    ctx.perf_enable(False)
+    assert all(x == staged[0] for x in staged), staged
+    return {"ms_step": 1e3 * sum(times) / steps, "score_ms": score_ms / steps,
+            "set_ms": set_ms / steps, "sel_ms": sel_ms / steps, "n_staged": staged[0]}
+
+
+def stage_bytes(kv, n_blocks: int, type_k: int, type_v: int) -> int:
+    """Algorithmic HBM bytes of a stage-in: F16 K and V read once, packed
+    rows written once."""
+    return n_blocks * L * T * (2 * E * 2 + kv.row_size(type_k, E) + kv.row_size(type_v, E))
 
 
 def make_previous(sel: list[int], seed: int = 7) -> list[int]:
@@ -173,86 +222,33 @@ def pinned_host_mode(kv, ctx, torch, k, v, eng, incoming: list[int], reps: int =
             "link_peak_GBs": PCIE_PEAK_GBS, "frac": round(h2d / best / 1e9 / PCIE_PEAK_GBS, 3)}
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-pinned", action="store_true")
-    a = ap.parse_args()
-    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: the reselect path runs on a single MI355X "
-              "(multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
-        return 2
-
-    import torch
-    kv = load_pkg()
-    from kvmem_amd import host, workloads
-
+def run_reselect_256k(a, torch, kv, workloads) -> dict:
     log("generating history K/V [16][2048][128][4][256] f16 and query [16][64][24][256] bf16")
     k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=TQ, seed=2, with_v=True)
     torch.cuda.synchronize()
     eng = make_engine(kv, torch, k, v)
     ctx = kv.Context.borrow(eng.ctx_handle())
-
     sel = eng.preview(q.data_ptr(), TQ).blocks
     prev = make_previous(sel)
-
-    def restore():
-        """Apply the previous step's selection (untimed between steps)."""
-        eng.apply(host.Selection(eng.epoch(), eng.total_tokens(), prev))
-
-    restore()
-    changed = len(set(sel) - set(prev))
-    log(f"selection {len(sel)} blocks, {changed} changed vs previous step")
-
-    def step() -> dict:
-        return eng.apply_retrieval(q.data_ptr(), TQ)
-
-    for _ in range(a.warmup):
-        step()
-        restore()
-    ctx.perf_enable(True)
-    times, staged, score_ms, set_ms, sel_ms = [], [], 0.0, 0.0, 0.0
-    for _ in range(a.steps):
-        ctx.perf_reset()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        st = step()
-        torch.cuda.synchronize()
-        times.append(time.perf_counter() - t0)
-        pf = ctx.perf()
-        score_ms += pf["score_ms"]
-        set_ms += pf["set_ms"]
-        sel_ms += pf["topk_ms"]
-        staged.append(st["n_staged"])
-        restore()
-    ctx.perf_enable(False)
-    K = a.steps
-    ms_step = 1e3 * sum(times) / K
-    score_ms /= K
-    set_ms /= K
-    sel_ms /= K
-    n_staged = staged[0]
-    assert all(x == n_staged for x in staged), staged
-    log(f"step {ms_step:.3f} ms: score kernel {score_ms:.3f} ms, combine+top-k {sel_ms:.3f} ms, "
-        f"stage-in kernel {set_ms:.3f} ms ({n_staged} blocks)")
+    log(f"selection {len(sel)} blocks, {len(set(sel) - set(prev))} changed vs previous step")
+    m = timed_steps(eng, ctx, torch, q, TQ, prev, a.steps, a.warmup)
+    n_staged = m["n_staged"]
+    log(f"step {m['ms_step']:.3f} ms: score kernel {m['score_ms']:.3f} ms, combine+top-k "
+        f"{m['sel_ms']:.3f} ms, stage-in kernel {m['set_ms']:.3f} ms ({n_staged} blocks)")
 
     flops = 2.0 * TQ * HQ * D * (B * T) * L
     k_bytes = L * B * T * E * 2
-    score_tflops = flops / (score_ms * 1e-3) / 1e12
-    stage_bytes = n_staged * L * 2 * (T * E * 2 + T * kv.row_size(kv.TYPE_Q8_0, E))
-    stage_gbs = stage_bytes / (set_ms * 1e-3) / 1e9
-
+    score_tflops = flops / (m["score_ms"] * 1e-3) / 1e12
+    sbytes = stage_bytes(kv, n_staged, kv.TYPE_Q8_0, kv.TYPE_Q8_0)
+    stage_gbs = sbytes / (m["set_ms"] * 1e-3) / 1e9
     result = {
         "metric": "reselect latency ms/agent-step @256K ctx; stage-in GB/s vs HBM peak",
-        "value": round(ms_step, 4),
+        "value": round(m["ms_step"], 4),
         "unit": "ms/step",
         "n_gpus": 1,
-        "steps": K,
+        "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": round(ms_step, 4),
+        "ms_per_step": round(m["ms_step"], 4),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -265,15 +261,16 @@ def main() -> int:
         "roofline": {"bound": "mfma", "kernel": "score_kernel<256>",
                      "achieved": round(score_tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(score_tflops / MFMA_F16_PEAK_TFLOPS, 4),
-                     "traffic": None, "algorithmic_bytes": k_bytes, "flops": flops,
-                     "hbm_GBs_algorithmic": round(k_bytes / (score_ms * 1e-3) / 1e9, 1)},
+                     "traffic": SCORE_TRAFFIC_BYTES, "algorithmic_bytes": k_bytes, "flops": flops,
+                     "hbm_GBs_algorithmic": round(k_bytes / (m["score_ms"] * 1e-3) / 1e9, 1)},
         "stagein_roofline": {"bound": "hbm", "kernel": "quant_scatter_kv_kernel<q8_0,q8_0>",
                              "achieved": round(stage_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                             "frac": round(stage_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                             "algorithmic_bytes": stage_bytes, "kernel_ms": round(set_ms, 4)},
-        "parts_ms": {"score_kernel": round(score_ms, 4), "combine_topk": round(sel_ms, 4),
-                     "stagein_kernel": round(set_ms, 4)},
+                             "frac": round(stage_gbs / HBM_PEAK_GBS, 4), "traffic": STAGEIN_TRAFFIC_BYTES,
+                             "algorithmic_bytes": sbytes, "kernel_ms": round(m["set_ms"], 4)},
+        "parts_ms": {"score_kernel": round(m["score_ms"], 4), "combine_topk": round(m["sel_ms"], 4),
+                     "stagein_kernel": round(m["set_ms"], 4)},
     }
+    ctx = kv.Context.borrow(eng.ctx_handle())
     if not a.no_pinned:
         incoming = sorted(set(sel) - set(prev))
         result["pinned_host"] = pinned_host_mode(kv, ctx, torch, k, v, eng, incoming)
@@ -281,6 +278,127 @@ def main() -> int:
         log("cpu baseline (oracle restatement on host cores)")
         result["cpu_baseline"] = cpu_baseline(torch, k, v, q, sorted(set(sel) - set(prev)))
     eng.close()
+    return result
+
+
+def run_mixed_precision(a, torch, kv, workloads) -> dict:
+    """Student-t (nu = 4) history; run A K q8_0 + V q4_0 (reserve 128
+    blocks), run B K and V q5_0 (reserve 96 blocks)."""
+    log("generating Student-t history K/V [16][2048][128][4][256] f16")
+    k, v, q = workloads.student_t_tensors(torch, "cuda", L=L, B=B, Tq=TQ, seed=4)
+    torch.cuda.synchronize()
+    runs = {}
+    for name, tk, tv, reserve in (("A_q8_0_q4_0", kv.TYPE_Q8_0, kv.TYPE_Q4_0, 128),
+                                  ("B_q5_0_q5_0", kv.TYPE_Q5_0, kv.TYPE_Q5_0, 96)):
+        eng = make_engine(kv, torch, k, v, reserve=reserve, type_k=tk, type_v=tv)
+        ctx = kv.Context.borrow(eng.ctx_handle())
+        sel = eng.preview(q.data_ptr(), TQ).blocks
+        prev = make_previous(sel)
+        m = timed_steps(eng, ctx, torch, q, TQ, prev, a.steps, a.warmup)
+        sb = stage_bytes(kv, m["n_staged"], tk, tv)
+        runs[name] = {"ms_per_step": round(m["ms_step"], 4), "score_kernel_ms": round(m["score_ms"], 4),
+                      "stagein_kernel_ms": round(m["set_ms"], 4), "n_staged": m["n_staged"],
+                      "stagein_algorithmic_bytes": sb,
+                      "stagein_GBs": round(sb / (m["set_ms"] * 1e-3) / 1e9, 1),
+                      "stagein_frac_hbm": round(sb / (m["set_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                      "pool_slots": BUDGET + reserve}
+        log(f"{name}: {runs[name]}")
+        eng.close()
+    return {"metric": "mixed-precision reselect @256K (Student-t nu=4 history)", "unit": "ms/step",
+            "higher_is_better": False, "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+            "data": "synthetic (seeded Student-t nu=4 K/V, bf16 query)", "runs": runs}
+
+
+def run_recall_1m(a, torch, kv, workloads) -> dict:
+    """1M-token workspace: 8192 blocks x 16 layers, 512-token query, 32
+    planted blocks (Zipf relevance), budget 512.  A cold step (empty pool)
+    then warm steps with the same query; reports recall of the planted
+    blocks."""
+    nb, tq, budget = 8192, 512, 512
+    log("generating history K/V [16][8192][128][4][256] f16 (64 GiB) and query [16][512][24][256]")
+    k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=nb, Tq=tq, seed=6, with_v=True)
+    planted = workloads.plant_blocks(torch, k, q, n_planted=32, seed=5)
+    torch.cuda.synchronize()
+    eng = make_engine(kv, torch, k, v, n_blocks=nb, budget=budget, reserve=128)
+    ctx = kv.Context.borrow(eng.ctx_handle())
+    ctx.perf_enable(True)
+    ctx.perf_reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    st = eng.apply_retrieval(q.data_ptr(), tq)
+    torch.cuda.synchronize()
+    cold_ms = 1e3 * (time.perf_counter() - t0)
+    pf_cold = ctx.perf()
+    sel = set(eng.preview(q.data_ptr(), tq).blocks)
+    recall = sum(int(b) in sel for b in planted) / len(planted)
+    warm = []
+    for _ in range(max(1, a.steps // 2)):
+        ctx.perf_reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.apply_retrieval(q.data_ptr(), tq)
+        torch.cuda.synchronize()
+        warm.append(1e3 * (time.perf_counter() - t0))
+    pf = ctx.perf()
+    flops = 2.0 * tq * HQ * D * (nb * T) * L
+    eng.close()
+    return {"metric": "1M-workspace reselect step + planted-block recall", "unit": "ms/step",
+            "higher_is_better": False, "n_gpus": 1,
+            "config": {"workload": "16 layers x 8192 blocks x 128 tokens, 512-token query, budget 512, "
+                                   "32 planted blocks"},
+            "cold_step_ms": round(cold_ms, 3), "cold_staged": st["n_staged"],
+            "cold_stagein_kernel_ms": round(pf_cold["set_ms"], 4),
+            "warm_step_ms": round(sum(warm) / len(warm), 3),
+            "score_kernel_ms": round(pf["score_ms"], 3),
+            "score_TFLOPs": round(flops / (pf["score_ms"] * 1e-3) / 1e12, 1),
+            "recall_planted": recall, "n_planted": len(planted)}
+
+
+def run_copy_calibration(a, torch, kv, workloads) -> dict:
+    """A plain device copy of known size (1 GiB in 4096 ops of 256 KiB,
+    batched_copy_kernel): the reference point for HBM byte counters."""
+    n_ops, op = 4096, 256 << 10
+    src = torch.randint(0, 255, (n_ops * op,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    ctx = kv.Context(0)
+    srcs = [src.data_ptr() + i * op for i in range(n_ops)]
+    dsts = [dst.data_ptr() + i * op for i in range(n_ops)]
+    ctx.d2d_batched(srcs, dsts, [op] * n_ops)
+    ctx.sync()
+    ctx.perf_enable(True)
+    ctx.perf_reset()
+    for _ in range(a.steps):
+        ctx.d2d_batched(srcs, dsts, [op] * n_ops)
+    ctx.sync()
+    ms = ctx.perf()["layout_ms"] / a.steps
+    ok = bool(torch.equal(src, dst))
+    ctx.close()
+    return {"metric": "device copy calibration", "bytes_read": n_ops * op, "bytes_written": n_ops * op,
+            "kernel_ms": round(ms, 4), "GBs_read_plus_write": round(2 * n_ops * op / (ms * 1e-3) / 1e9, 1),
+            "copy_ok": ok}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="reselect_256k",
+                    choices=["reselect_256k", "mixed_precision", "recall_1m", "copy_calibration"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-pinned", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the reselect path runs on a single MI355X "
+              "(multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
+        return 2
+
+    import torch
+    kv = load_pkg()
+    from kvmem_amd import workloads
+    run = {"reselect_256k": run_reselect_256k, "mixed_precision": run_mixed_precision,
+           "recall_1m": run_recall_1m, "copy_calibration": run_copy_calibration}[a.workload]
+    result = run(a, torch, kv, workloads)
     print(json.dumps(result), flush=True)
     return 0
 

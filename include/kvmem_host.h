@@ -23,7 +23,8 @@
  * Lifetimes: history pointers (device K/V, pinned host blocks) and query
  * pointers are borrowed; the caller keeps them valid until the call that
  * uses them returns (preview and apply synchronise the engine's stream
- * before returning).  Pool memory is owned by the engine.  An engine is
+ * before returning).  Pool memory is owned by the engine unless borrowed
+ * with kvmem_engine_set_pool.  An engine is
  * not re-entrant: one engine per host thread.
  */
 #ifndef KVMEM_HOST_H
@@ -156,6 +157,17 @@ KVMEM_HIP_API int kvmem_engine_truncate_to(kvmem_engine *e, uint32_t token_pos);
 KVMEM_HIP_API uint32_t kvmem_engine_block_count(const kvmem_engine *e);
 KVMEM_HIP_API uint32_t kvmem_engine_total_tokens(const kvmem_engine *e);
 KVMEM_HIP_API uint64_t kvmem_engine_epoch(const kvmem_engine *e);
+/* Borrow caller-owned pool tensors instead of the engine's own (the
+ * llama.cpp K/V cache tensors, whose data pointers the reference adapter
+ * takes with kvmem_cuda_tensor_ptr, llama-memory-kvmem.cpp:196-205):
+ * k_layers / v_layers are host arrays of n_layers device pointers, each to
+ * at least n_slots * block_tokens rows of the pool type, 16-byte aligned.
+ * The engine's own pool is released.  The caller keeps the tensors alive
+ * while the engine uses them; the working set is cleared (every block is
+ * staged again by the next apply).  NULL k_layers returns to an engine-owned
+ * pool. */
+KVMEM_HIP_API int kvmem_engine_set_pool(kvmem_engine *e, void *const *k_layers,
+                                        void *const *v_layers);
 /* Pool slots and per-layer device pool tensors. */
 KVMEM_HIP_API uint32_t kvmem_engine_n_slots(const kvmem_engine *e);
 KVMEM_HIP_API int kvmem_engine_pool_layer(const kvmem_engine *e, uint32_t layer, void **k,

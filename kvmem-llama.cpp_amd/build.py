@@ -41,6 +41,7 @@ HIP_FLAGS = [f"--offload-arch={ARCH}", "-x", "hip",
 # per-file extras
 EXTRA = {
     "stagein.hip": ["-ffp-contract=off"],
+    "score.hip": ["-ffinite-math-only"],
 }
 
 

@@ -219,6 +219,7 @@ struct kvmem_engine {
     RecordingSlots slots;
     KvMemRuntime rt;
     std::vector<void *> pool_k, pool_v;
+    bool own_pool = true;
     const void *hist_k = nullptr;
     const void *hist_v = nullptr;
     uint32_t hist_capacity = 0;
@@ -316,6 +317,8 @@ int engine_stage(kvmem_engine *e, const std::vector<uint32_t> &ids,
 
 }  // namespace
 
+static bool alloc_own_pool(kvmem_engine *e);
+
 extern "C" {
 
 kvmem_engine_params kvmem_engine_default_params(void) {
@@ -366,18 +369,9 @@ int kvmem_engine_create(const kvmem_engine_params *pp, kvmem_engine **out) {
         delete e;
         return rc;
     }
-    const size_t kbytes = static_cast<size_t>(n_slots) * p.block_tokens *
-                          kvmem_hip_row_size(p.type_k, e->n_embd_k);
-    const size_t vbytes = static_cast<size_t>(n_slots) * p.block_tokens *
-                          kvmem_hip_row_size(p.type_v, e->n_embd_v);
-    e->pool_k.assign(p.n_layers, nullptr);
-    e->pool_v.assign(p.n_layers, nullptr);
-    for (uint32_t l = 0; l < p.n_layers; ++l) {
-        if (hipMalloc(&e->pool_k[l], kbytes) != hipSuccess ||
-            hipMalloc(&e->pool_v[l], vbytes) != hipSuccess) {
-            kvmem_engine_destroy(e);
-            return KVMEM_HIP_ERR_NOMEM;
-        }
+    if (!alloc_own_pool(e)) {
+        kvmem_engine_destroy(e);
+        return KVMEM_HIP_ERR_NOMEM;
     }
     *out = e;
     return KVMEM_HIP_OK;
@@ -390,11 +384,13 @@ void kvmem_engine_destroy(kvmem_engine *e) {
     if (e->ctx) {
         kvmem_hip_sync(e->ctx);
     }
-    for (void *ptr : e->pool_k) {
-        if (ptr) (void) hipFree(ptr);
-    }
-    for (void *ptr : e->pool_v) {
-        if (ptr) (void) hipFree(ptr);
+    if (e->own_pool) {
+        for (void *ptr : e->pool_k) {
+            if (ptr) (void) hipFree(ptr);
+        }
+        for (void *ptr : e->pool_v) {
+            if (ptr) (void) hipFree(ptr);
+        }
     }
     if (e->d_scores) {
         (void) hipFree(e->d_scores);
@@ -501,6 +497,68 @@ uint64_t kvmem_engine_epoch(const kvmem_engine *e) {
 
 uint32_t kvmem_engine_n_slots(const kvmem_engine *e) {
     return e ? e->n_slots : 0;
+}
+
+static bool alloc_own_pool(kvmem_engine *e) {
+    const size_t kbytes = static_cast<size_t>(e->n_slots) * e->p.block_tokens *
+                          kvmem_hip_row_size(e->p.type_k, e->n_embd_k);
+    const size_t vbytes = static_cast<size_t>(e->n_slots) * e->p.block_tokens *
+                          kvmem_hip_row_size(e->p.type_v, e->n_embd_v);
+    e->pool_k.assign(e->p.n_layers, nullptr);
+    e->pool_v.assign(e->p.n_layers, nullptr);
+    e->own_pool = true;
+    for (uint32_t l = 0; l < e->p.n_layers; ++l) {
+        if (hipMalloc(&e->pool_k[l], kbytes) != hipSuccess ||
+            hipMalloc(&e->pool_v[l], vbytes) != hipSuccess) {
+            return false;
+        }
+    }
+    return true;
+}
+
+int kvmem_engine_set_pool(kvmem_engine *e, void *const *k_layers, void *const *v_layers) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (k_layers && !v_layers) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "set_pool: V tensors missing");
+    }
+    if (k_layers) {
+        for (uint32_t l = 0; l < e->p.n_layers; ++l) {
+            if (!k_layers[l] || !v_layers[l] || (reinterpret_cast<uintptr_t>(k_layers[l]) & 15u) ||
+                (reinterpret_cast<uintptr_t>(v_layers[l]) & 15u)) {
+                return e->fail(KVMEM_HIP_ERR_INVALID, "set_pool: null or misaligned layer tensor");
+            }
+        }
+    }
+    if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
+        return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "set_pool");
+    }
+    if (e->own_pool) {
+        for (void *ptr : e->pool_k) {
+            if (ptr) (void) hipFree(ptr);
+        }
+        for (void *ptr : e->pool_v) {
+            if (ptr) (void) hipFree(ptr);
+        }
+    }
+    if (k_layers) {
+        e->pool_k.assign(k_layers, k_layers + e->p.n_layers);
+        e->pool_v.assign(v_layers, v_layers + e->p.n_layers);
+        e->own_pool = false;
+    } else if (!alloc_own_pool(e)) {
+        return e->fail(KVMEM_HIP_ERR_NOMEM, "set_pool: pool allocation");
+    }
+    // the new tensors hold none of the working set
+    for (const Block &b : e->rt.store().blocks()) {
+        if (b.tier == Tier::GPU) {
+            e->rt.store().set_block_tier(b.block_id, Tier::CPU);
+        }
+    }
+    e->rt.store().clear_working_set();
+    e->slots.reset_after(0);
+    e->dirty_tail = -1;
+    return KVMEM_HIP_OK;
 }
 
 int kvmem_engine_pool_layer(const kvmem_engine *e, uint32_t layer, void **k, void **v) {

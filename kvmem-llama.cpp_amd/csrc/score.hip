@@ -4,45 +4,58 @@
 //     max_{query rows r of group h, keys j of block b} q_r . k_j
 // where the query rows of group h are the (token, head) pairs with head in
 // [h*g, (h+1)*g) (GQA, llama-memory-kvmem.cpp:2890-2892).  That is a small
-// GEMM (rows x 128 keys x head_dim) whose output is reduced by max at once.
+// GEMM (rows x 128 keys x head_dim) whose output is reduced by max at once,
+// so no score ever goes to memory.
 //
-// Mapping.  A workgroup of 8 waves owns one (layer, KV head, 384-row slice)
-// and a contiguous range of blocks.  Each wave keeps 48 query rows resident
-// in VGPRs as f16 A-fragments of v_mfma_f32_16x16x32_f16 (loaded once;
-// bf16 queries are converted to f16 on the way, exact for normal-range
-// values).  Every block's K tile (128 keys x head_dim halves) is copied
-// from HBM to LDS once per workgroup (row stride padded by 16 bytes so the
-// 16 keys of a B-fragment read hit distinct banks) and consumed by all 8
-// waves; the next block's tile is prefetched into registers while the
-// current one is multiplied.  Out-of-range query rows and keys (partial
-// last block, row count not a multiple of 384) are replaced by duplicates
-// of valid ones, which leaves the max unchanged and needs no masking.
+// Mapping.  A workgroup of 4 waves (one per SIMD) owns one (layer, KV head,
+// 384-row slice) and a contiguous range of blocks.  Each wave keeps 96
+// query rows resident in VGPRs as f16 A-fragments of
+// v_mfma_f32_16x16x32_f16 (loaded once; bf16 queries are converted to f16
+// on the way, exact for normal-range values), so every 16-byte B-fragment
+// read from LDS feeds six MFMAs.  A block's K tile (128 keys x head_dim
+// halves of one KV head) moves HBM -> LDS with global_load_lds_dwordx4
+// (no register staging) into one of two LDS buffers while the other
+// buffer's block is multiplied: one barrier per block.  Inside a tile the
+// 16-byte chunk c of key j sits at chunk position c ^ (j mod chunks-per-
+// key), so the 16 keys of a B-fragment read hit 16 different bank groups;
+// the swizzle is applied on the global side (each lane of a direct LDS load
+// fetches the chunk that belongs to its fixed LDS slot).  Out-of-range
+// query rows and keys (partial last block, row count not a multiple of
+// 384) are replaced by duplicates of valid ones, which leaves the max
+// unchanged and needs no masking.  Each wave writes its own per-block max
+// to a partial array; a small kernel folds waves, row slices, KV heads and
+// layers.
+//
+// The file is built with finite-math semantics (max needs no NaN
+// canonicalisation); every identity is -FLT_MAX and inputs are finite F16.
 //
 // Dispatch order is XCD-aware: consecutive workgroup ids go to different
 // XCDs, so the id is decoded such that each XCD works through its own set
 // of (layer, head) pairs, keeping their query rows resident in that XCD's
-// L2, and row slices of the same block range run next to each other.
+// L2.
 #include "kvmem_internal.hpp"
 
 #include <algorithm>
+#include <cfloat>
 #include <cmath>
 
 namespace kvmem_hip {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
 
-constexpr int kScoreWaves = 8;
+constexpr int kScoreWaves = 4;
 constexpr int kScoreThreads = kScoreWaves * 64;
-constexpr int kRowTiles = 3;                            // 16-row tiles per wave
-constexpr int kRowsPerWave = kRowTiles * 16;            // 48
+constexpr int kRowTiles = 6;                               // 16-row tiles per wave
+constexpr int kRowsPerWave = kRowTiles * 16;               // 96
 constexpr int kRowsPerGroup = kScoreWaves * kRowsPerWave;  // 384
-constexpr int kMaxTokens = 128;                         // keys per LDS tile
+constexpr int kMaxTokens = 128;                            // keys per LDS tile
 
 struct ScoreParams {
     const uint16_t *q;       // [L][Tq][Hq][D] bf16 or f16 bits
-    const uint8_t *k;        // [L][B][T][Hkv][D] f16
-    float *partial;          // [RG][L][Hkv][B]
+    const uint8_t *k;        // [L][cap][T][Hkv][D] f16
+    float *partial;          // [RG * kScoreWaves][L][Hkv][B]
     uint32_t L, Tq, Hq, Hkv, B, T, last_T, g, R, RG;
     uint32_t cap;            // blocks per layer in memory (>= B)
     uint32_t n_chunks;       // block chunks per (l, h, row slice)
@@ -63,15 +76,14 @@ __device__ inline _Float16 q_elem_to_half(uint16_t bits, bool bf16) {
 template <int D>
 __global__ __launch_bounds__(kScoreThreads, 1) void score_kernel(ScoreParams p) {
     constexpr int KS = D / 32;                       // k-steps of 32
-    constexpr int ROW_BYTES = D * 2;
-    constexpr int LDS_STRIDE = ROW_BYTES + 16;       // padded key row
-    constexpr int PIECES = kMaxTokens * D / 8;       // 16-byte pieces per tile
-    constexpr int PER_THREAD = PIECES / kScoreThreads;
-    static_assert(PIECES % kScoreThreads == 0, "tile must split evenly");
-    constexpr int PIECES_PER_ROW = D / 8;
+    constexpr int ROW_BYTES = D * 2;                 // one key of one head
+    constexpr int CH = D / 8;                        // 16-byte chunks per key
+    constexpr int TILE = kMaxTokens * ROW_BYTES;     // 64 KiB (D = 256)
+    constexpr int LOADS = TILE / 1024;               // wave-wide 1 KiB loads per tile
+    constexpr int LOADS_PER_WAVE = LOADS / kScoreWaves;
+    static_assert(LOADS % kScoreWaves == 0, "tile must split over the waves");
 
-    __shared__ __attribute__((aligned(16))) uint8_t tile[kMaxTokens * LDS_STRIDE];
-    __shared__ float red[kScoreWaves];
+    __shared__ __attribute__((aligned(1024))) uint8_t tiles[2][TILE];
 
     // ---- decode (layer, head, row slice, chunk) from the workgroup id
     const uint32_t pairs = p.L * p.Hkv;
@@ -104,10 +116,31 @@ __global__ __launch_bounds__(kScoreThreads, 1) void score_kernel(ScoreParams p) 
     }
 
     const uint32_t tid = threadIdx.x;
-    const uint32_t wave = tid >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t lane = tid & 63u;
     const uint32_t lrow = lane & 15u;   // row (A) / key (B) within a 16-tile
     const uint32_t kgrp = lane >> 4;    // which 8 of the 32 k-values
+
+    // ---- K tiles: direct HBM -> LDS, swizzled chunk order
+    const uint64_t key_stride = static_cast<uint64_t>(p.Hkv) * ROW_BYTES;
+    auto issue_tile = [&](uint32_t b, int buf) {
+        const uint8_t *base = p.k + ((static_cast<uint64_t>(l) * p.cap + b) * p.T) * key_stride +
+                              static_cast<uint64_t>(h) * ROW_BYTES;
+        const uint32_t nt = (b + 1 == p.B && p.last_T != 0) ? p.last_T : p.T;
+#pragma unroll
+        for (int i = 0; i < LOADS_PER_WAVE; ++i) {
+            const uint32_t inst = wave * LOADS_PER_WAVE + i;
+            const uint32_t slot = inst * 64u + lane;            // 16-byte LDS slot
+            const uint32_t j = slot / CH;                       // key
+            const uint32_t c = (slot % CH) ^ (j % CH);          // global chunk held there
+            const uint32_t jj = min(j, nt - 1u);                // duplicate the last key
+            const uint8_t *src = base + jj * key_stride + c * 16u;
+            __builtin_amdgcn_global_load_lds(
+                src, (lds_void_t *) (&tiles[buf][inst * 1024u]), 16, 0, 0);
+        }
+    };
+
+    issue_tile(b_begin, 0);
 
     // ---- query rows -> A fragments (resident for the whole workgroup)
     half8_t a[kRowTiles][KS];
@@ -132,61 +165,23 @@ __global__ __launch_bounds__(kScoreThreads, 1) void score_kernel(ScoreParams p) 
         }
     }
 
-    // ---- K tile prefetch: piece -> (key, part); keys beyond the block's
-    // tokens read the block's last valid key.
-    const uint64_t key_stride = static_cast<uint64_t>(p.Hkv) * ROW_BYTES;  // bytes between keys
-    auto block_base = [&](uint32_t b) -> const uint8_t * {
-        return p.k + ((static_cast<uint64_t>(l) * p.cap + b) * p.T) * key_stride +
-               static_cast<uint64_t>(h) * ROW_BYTES;
-    };
-    auto n_tokens = [&](uint32_t b) -> uint32_t {
-        return (b + 1 == p.B && p.last_T != 0) ? p.last_T : p.T;
-    };
-    uint4 pre[PER_THREAD];
-    auto prefetch = [&](uint32_t b) {
-        const uint8_t *base = block_base(b);
-        const uint32_t nt = n_tokens(b);
-#pragma unroll
-        for (int s = 0; s < PER_THREAD; ++s) {
-            const uint32_t piece = tid + s * kScoreThreads;
-            const uint32_t key = min(piece / PIECES_PER_ROW, nt - 1u);
-            const uint32_t part = piece % PIECES_PER_ROW;
-            pre[s] = load_stream16(base + key * key_stride + part * 16u);
-        }
-    };
-
-    prefetch(b_begin);
+    float *out = p.partial +
+                 ((static_cast<uint64_t>(rg * kScoreWaves + wave) * p.L + l) * p.Hkv + h) * p.B;
     for (uint32_t b = b_begin; b < b_end; ++b) {
-        __syncthreads();  // previous block's tile fully consumed, red[] written
-        if (tid == 0 && b > b_begin) {
-            float m = red[0];
-#pragma unroll
-            for (int w = 1; w < kScoreWaves; ++w) {
-                m = fmaxf(m, red[w]);
-            }
-            p.partial[((static_cast<uint64_t>(rg) * p.L + l) * p.Hkv + h) * p.B + (b - 1)] = m * p.scale;
-        }
-#pragma unroll
-        for (int s = 0; s < PER_THREAD; ++s) {
-            const uint32_t piece = tid + s * kScoreThreads;
-            const uint32_t key = piece / PIECES_PER_ROW;
-            const uint32_t part = piece % PIECES_PER_ROW;
-            *reinterpret_cast<uint4 *>(tile + key * LDS_STRIDE + part * 16u) = pre[s];
-        }
+        const int buf = static_cast<int>((b - b_begin) & 1u);
+        // this thread's loads of tile b have landed; after the barrier every
+        // thread's have, and every wave is done reading the other buffer
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (b + 1 < b_end) {
-            prefetch(b + 1);
+            issue_tile(b + 1, buf ^ 1);
         }
-
-        float m = -INFINITY;
-#pragma unroll 1
-        for (int kt = 0; kt < kMaxTokens / 16; ++kt) {
-            const uint8_t *krow = tile + (kt * 16 + lrow) * LDS_STRIDE + kgrp * 16;
-            half8_t bf[KS];
+        const uint8_t *tile = tiles[buf];
+        float m = -FLT_MAX;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                bf[ks] = *reinterpret_cast<const half8_t *>(krow + ks * 64);
-            }
+        for (int kt = 0; kt < kMaxTokens / 16; ++kt) {
+            const uint32_t key = kt * 16 + lrow;
+            const uint8_t *krow = tile + key * ROW_BYTES;
             float4_t acc[kRowTiles];
 #pragma unroll
             for (int rt = 0; rt < kRowTiles; ++rt) {
@@ -194,57 +189,74 @@ __global__ __launch_bounds__(kScoreThreads, 1) void score_kernel(ScoreParams p) 
             }
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
+                const uint32_t cpos = (static_cast<uint32_t>(ks * 4) + kgrp) ^ (key % CH);
+                const half8_t bf = *reinterpret_cast<const half8_t *>(krow + cpos * 16u);
 #pragma unroll
                 for (int rt = 0; rt < kRowTiles; ++rt) {
-                    acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rt][ks], bf[ks], acc[rt], 0, 0, 0);
+                    acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rt][ks], bf, acc[rt], 0, 0, 0);
                 }
             }
 #pragma unroll
             for (int rt = 0; rt < kRowTiles; ++rt) {
-                m = fmaxf(m, fmaxf(fmaxf(acc[rt][0], acc[rt][1]), fmaxf(acc[rt][2], acc[rt][3])));
+                m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(acc[rt][0], acc[rt][1]),
+                                                       __builtin_fmaxf(acc[rt][2], acc[rt][3])));
             }
         }
-        // wave max -> red[wave]
+        // Issue order of the tile's 64 B-fragment reads and 384 MFMAs: the
+        // read of fragment f+1 goes out right after the first MFMA of
+        // fragment f, so the other five MFMAs of f cover its latency.  (An
+        // LDS DMA in flight makes the compiler wait for every outstanding
+        // LDS read before a consumer, so reads further ahead would not help.)
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int f = 0; f < (kMaxTokens / 16) * KS - 1; ++f) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, kRowTiles - 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, kRowTiles, 0);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) {
-            m = fmaxf(m, __shfl_xor(m, off, 64));
+            m = __builtin_fmaxf(m, __shfl_xor(m, off, 64));
         }
         if (lane == 0) {
-            red[wave] = m;
+            out[b] = m * p.scale;
         }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float m = red[0];
-#pragma unroll
-        for (int w = 1; w < kScoreWaves; ++w) {
-            m = fmaxf(m, red[w]);
-        }
-        p.partial[((static_cast<uint64_t>(rg) * p.L + l) * p.Hkv + h) * p.B + (b_end - 1)] = m * p.scale;
     }
 }
 
-// scores[b] = reduce_l max_{rg, h} partial[rg][l][h][b]
-__global__ __launch_bounds__(256) void score_finalize_kernel(const float *partial, uint32_t RG,
-                                                             uint32_t L, uint32_t Hkv, uint32_t B,
-                                                             int mode, float *layer_scores,
-                                                             float *scores) {
+// layer_scores[l][b] = max_{slice, h} partial[slice][l][h][b]; one thread
+// per (layer, block).
+__global__ __launch_bounds__(256) void score_layer_kernel(const float *partial, uint32_t S,
+                                                          uint32_t L, uint32_t Hkv, uint32_t B,
+                                                          float *layer_scores) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= L * B) {
+        return;
+    }
+    const uint32_t l = i / B;
+    const uint32_t b = i - l * B;
+    float best = -FLT_MAX;
+    for (uint32_t s = 0; s < S; ++s) {
+        for (uint32_t h = 0; h < Hkv; ++h) {
+            best = fmaxf(best, partial[((static_cast<uint64_t>(s) * L + l) * Hkv + h) * B + b]);
+        }
+    }
+    layer_scores[i] = best;
+}
+
+// scores[b] = reduce over layers (in layer order) of layer_scores[l][b].
+__global__ __launch_bounds__(256) void score_combine_kernel(const float *layer_scores, uint32_t L,
+                                                            uint32_t B, int mode, float *scores) {
     const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= B) {
         return;
     }
-    float acc = mode == KVMEM_LAYER_MAX ? -INFINITY : 0.0f;
+    float acc = mode == KVMEM_LAYER_MAX ? -FLT_MAX : 0.0f;
     for (uint32_t l = 0; l < L; ++l) {
-        float best = -INFINITY;
-        for (uint32_t rg = 0; rg < RG; ++rg) {
-            for (uint32_t h = 0; h < Hkv; ++h) {
-                best = fmaxf(best, partial[((static_cast<uint64_t>(rg) * L + l) * Hkv + h) * B + b]);
-            }
-        }
-        if (layer_scores) {
-            layer_scores[static_cast<uint64_t>(l) * B + b] = best;
-        }
-        acc = mode == KVMEM_LAYER_MAX ? fmaxf(acc, best) : acc + best;
+        const float v = layer_scores[static_cast<uint64_t>(l) * B + b];
+        acc = mode == KVMEM_LAYER_MAX ? fmaxf(acc, v) : acc + v;
     }
     if (mode == KVMEM_LAYER_MEAN && L > 0) {
         acc = acc / static_cast<float>(L);
@@ -312,7 +324,8 @@ extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist
     p.q_bf16 = args->q_type == KVMEM_TYPE_BF16;
     p.scale = 1.0f / std::sqrt(static_cast<float>(D));
     const uint32_t pairs = L * p.Hkv;
-    // about four workgroups per CU over the whole launch
+    // one workgroup per CU holds the LDS double buffer; a few workgroups
+    // per CU over the launch keep every XCD busy to the end
     const uint32_t target = 1024;
     const uint32_t per_chunk_target = std::max<uint32_t>(1, target / std::max<uint32_t>(1, pairs * p.RG));
     p.n_chunks = std::min(B, per_chunk_target);
@@ -321,13 +334,13 @@ extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist
     p.xcd_major = (pairs % 8u) == 0;
 
     (void) hipSetDevice(ctx->device);
-    const size_t partial_bytes = sizeof(float) * static_cast<size_t>(p.RG) * L * p.Hkv * B;
+    const uint32_t slices = p.RG * kScoreWaves;
+    const size_t partial_bytes = sizeof(float) * static_cast<size_t>(slices) * L * p.Hkv * B;
     if (!ensure_dev(ctx, ctx->score_partial, partial_bytes, "score partial")) {
         return KVMEM_HIP_ERR_NOMEM;
     }
     p.partial = static_cast<float *>(ctx->score_partial.ptr);
-    const uint64_t n_wg = static_cast<uint64_t>(pairs) * p.RG * p.n_chunks;
-    const uint64_t grid = p.xcd_major ? n_wg : n_wg;
+    const uint64_t grid = static_cast<uint64_t>(pairs) * p.RG * p.n_chunks;
     if (grid > 0x7fffffffu) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "score: problem too large for one launch");
     }
@@ -341,10 +354,21 @@ extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist
     if (!hip_ok(ctx, hipGetLastError(), "score kernel launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
+    float *layers = args->layer_scores;
+    if (!layers) {
+        if (!ensure_dev(ctx, ctx->score_layers, sizeof(float) * static_cast<size_t>(L) * B,
+                        "score layer buffer")) {
+            return KVMEM_HIP_ERR_NOMEM;
+        }
+        layers = static_cast<float *>(ctx->score_layers.ptr);
+    }
     // the layer combination is timed with the selection stage
     perf_begin(ctx, kPerfTopk);
-    score_finalize_kernel<<<(B + 255) / 256, 256, 0, ctx->stream>>>(
-        p.partial, p.RG, L, p.Hkv, B, args->layer_reduce, args->layer_scores, args->scores);
+    const uint64_t lb = static_cast<uint64_t>(L) * B;
+    score_layer_kernel<<<static_cast<uint32_t>((lb + 255) / 256), 256, 0, ctx->stream>>>(
+        p.partial, slices, L, p.Hkv, B, layers);
+    score_combine_kernel<<<(B + 255) / 256, 256, 0, ctx->stream>>>(layers, L, B, args->layer_reduce,
+                                                                   args->scores);
     perf_end(ctx, kPerfTopk);
     if (!hip_ok(ctx, hipGetLastError(), "score finalize launch")) {
         return KVMEM_HIP_ERR_RUNTIME;

@@ -78,6 +78,7 @@ def bind(lib: C.CDLL) -> C.CDLL:
     sig("kvmem_engine_epoch", u64, vp)
     sig("kvmem_engine_n_slots", u32, vp)
     sig("kvmem_engine_pool_layer", i32, vp, u32, C.POINTER(vp), C.POINTER(vp))
+    sig("kvmem_engine_set_pool", i32, vp, C.POINTER(vp), C.POINTER(vp))
     sig("kvmem_engine_block_slots", i32, vp, pi32)
     sig("kvmem_engine_preview", i32, vp, vp, i32, u32, pu32, u32, pu32, pu32, C.POINTER(u64), pu32)
     sig("kvmem_engine_apply", i32, vp, u64, u32, pu32, u32, C.POINTER(PlanStats))
@@ -247,6 +248,16 @@ class Engine:
         k, v = C.c_void_p(), C.c_void_p()
         self.check(self.lib.kvmem_engine_pool_layer(self.h, layer, C.byref(k), C.byref(v)), "pool_layer")
         return k.value, v.value
+
+    def set_pool(self, k_ptrs: Sequence[int] | None, v_ptrs: Sequence[int] | None = None):
+        """Borrow caller-owned per-layer pool tensors (None: engine-owned)."""
+        if k_ptrs is None:
+            self.check(self.lib.kvmem_engine_set_pool(self.h, None, None), "set_pool")
+            return
+        ka = (C.c_void_p * len(k_ptrs))(*k_ptrs)
+        va = (C.c_void_p * len(v_ptrs))(*v_ptrs)
+        self._pool_keep = (ka, va)
+        self.check(self.lib.kvmem_engine_set_pool(self.h, ka, va), "set_pool")
 
     def block_slots(self) -> list:
         n = self.block_count()

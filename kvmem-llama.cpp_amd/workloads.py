@@ -77,10 +77,38 @@ def scoring_tensors(torch, device: str, L: int = 16, B: int = 2048, Tq: int = 64
     return k, v, q
 
 
-def plant_blocks(torch, k, q, n_planted: int = 32, seed: int = 5, alpha: float = 6.0):
+def student_t_tensors(torch, device: str, L: int = 16, B: int = 2048, Tq: int = 64, seed: int = 4,
+                      T: int = T_BLOCK, Hkv: int = HKV, Hq: int = HQ, D: int = HEAD_DIM,
+                      nu: int = 4):
+    """K, V history [L][B][T][Hkv][D] f16 with Student-t (nu = 4) values,
+    t = z / sqrt(chi2_nu / nu) with chi2_nu a sum of nu squared normals,
+    generated on `device` one layer at a time; Q [L][Tq][Hq][D] bf16 N(0,1)."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    k = torch.empty((L, B, T, Hkv, D), dtype=torch.float16, device=device)
+    v = torch.empty_like(k)
+    for dst in (k, v):
+        for l in range(L):
+            chi2 = torch.zeros((B, T, Hkv, D), device=device, dtype=torch.float32)
+            for _ in range(nu):
+                chi2.addcmul_(z := torch.randn((B, T, Hkv, D), generator=g, device=device), z)
+            z = torch.randn((B, T, Hkv, D), generator=g, device=device)
+            dst[l] = (z / torch.sqrt(chi2 / nu)).clamp_(-60000.0, 60000.0).half()
+            del chi2, z
+    q = torch.randn((L, Tq, Hq, D), generator=g, device=device, dtype=torch.float32).to(torch.bfloat16)
+    return k, v, q
+
+
+def plant_blocks(torch, k, q, n_planted: int = 32, seed: int = 5, alpha: float = 48.0):
     """Add alpha * rank-scaled unit query directions to the keys of
     n_planted seeded blocks (Zipf relevance: the r-th planted block gets
-    weight 1/r^0.5 of alpha).  Returns the planted block ids."""
+    weight 1/r^0.5 of alpha).  Returns the planted block ids.
+
+    Scale: a unit direction raises a block's per-token max by about
+    w * 4.3 / sqrt(head_dim) (the largest projection of 3072 N(0,1) query
+    rows on their mean direction), while the max over ~4e5 random dot
+    products already spreads unplanted blocks by ~0.3; alpha = 48 lifts
+    the weakest rank (r = 32) by ~2.3, clear of that spread."""
     L, B, T, Hkv, D = k.shape
     rng = np.random.default_rng(seed)
     ids = np.sort(rng.choice(np.arange(1, B), n_planted, replace=False))
