@@ -373,9 +373,19 @@ def run_copy_calibration(a, torch, kv, workloads) -> dict:
     ms = ctx.perf()["layout_ms"] / a.steps
     ok = bool(torch.equal(src, dst))
     ctx.close()
+    # the runtime's own device copy of the same bytes, for comparison
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    dst.copy_(src)
+    e0.record()
+    for _ in range(a.steps):
+        dst.copy_(src)
+    e1.record()
+    e1.synchronize()
+    rt_ms = e0.elapsed_time(e1) / a.steps
     return {"metric": "device copy calibration", "bytes_read": n_ops * op, "bytes_written": n_ops * op,
             "kernel_ms": round(ms, 4), "GBs_read_plus_write": round(2 * n_ops * op / (ms * 1e-3) / 1e9, 1),
-            "copy_ok": ok}
+            "runtime_copy_ms": round(rt_ms, 4),
+            "runtime_copy_GBs": round(2 * n_ops * op / (rt_ms * 1e-3) / 1e9, 1), "copy_ok": ok}
 
 
 def main() -> int:

@@ -262,6 +262,44 @@ KVMEM_HIP_API int kvmem_hip_topk(kvmem_hip_ctx *ctx,
                                  uint32_t need, int tie_lower_index,
                                  uint32_t *sel_out, uint32_t *n_sel);
 
+/* ---------------------------------------------- mean-K cosine (reference) */
+
+/* Mean-K producer: for every listed block and every layer of a device
+ * history, k_sum[l][b][e] = fp32 sum of the block's F16 keys in token order
+ * and mean_tokens[l][b] = the tokens summed (RawKvStore::capture_mean_f16,
+ * kvmem/src/host/raw_kv_store.cpp:184-202; bit-identical sums).  k_sum is
+ * device [n_layers][capacity][n_embd_k] f32 (16-byte aligned), mean_tokens
+ * device [n_layers][capacity] u32; n_embd_k a multiple of 8, <= 2048. */
+KVMEM_HIP_API int kvmem_hip_meank_sums(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
+                                       const uint32_t *block_ids, uint32_t n,
+                                       float *k_sum, uint32_t *mean_tokens);
+
+/* The reference's retrieval scorer (llama_memory_kvmem::score_retrieval,
+ * src/adapter/llama-memory-kvmem.cpp:2869-2916): per block the mean over
+ * layers with query rows of the mean over KV heads of
+ *   cos(sum_{gi<g} q_sum[h*g+gi] / (q_count*g), k_sum_h / mean_tokens)
+ * (denominator sqrt|q|^2 * sqrt|k|^2 + 1e-6), layer and block sums in
+ * double; blocks without keys in any layer score 0.
+ *   q_sum       device [n_layers][n_head*head_dim] f32 (sums of query rows)
+ *   q_count     host   [n_layers] rows summed (0 = layer not scored)
+ *   k_sum, mean_tokens as produced by kvmem_hip_meank_sums
+ *   scores      device [n_blocks] f32 */
+typedef struct kvmem_hip_meank_args {
+    const float *q_sum;
+    const uint32_t *q_count;
+    const float *k_sum;
+    const uint32_t *mean_tokens;
+    uint32_t n_layers;
+    uint32_t n_blocks;
+    uint32_t capacity_blocks;   /* 0 = n_blocks */
+    uint32_t n_head;
+    uint32_t n_head_kv;
+    uint32_t head_dim;          /* 128 or 256 */
+    float *scores;
+} kvmem_hip_meank_args;
+
+KVMEM_HIP_API int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *args);
+
 /* ------------------------------------------------------------ profiling */
 
 /* Per-stage GPU time (hipEvent pairs on the context stream), the device

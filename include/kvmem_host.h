@@ -192,6 +192,16 @@ KVMEM_HIP_API int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q
 KVMEM_HIP_API int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows,
                                      const uint32_t *sel, uint32_t n_sel,
                                      kvmem_plan_stats *stats);
+/* Phase 1 with the reference's own scorer, mean-K cosine
+ * (score_retrieval, llama-memory-kvmem.cpp:2869-2916): q_sum is device
+ * [n_layers][n_head*head_dim] f32 (the per-layer sum of query rows the
+ * reference keeps in q_sum_), q_count host [n_layers] (q_count_).  The
+ * per-block key sums are produced on the device from the history and kept
+ * current across appends.  Same outputs as kvmem_engine_preview. */
+KVMEM_HIP_API int kvmem_engine_preview_meank(kvmem_engine *e, const float *q_sum,
+                                             const uint32_t *q_count, const uint32_t *mandatory,
+                                             uint32_t n_mandatory, uint32_t *sel, uint32_t *n_sel,
+                                             uint64_t *epoch, uint32_t *rows);
 /* preview + apply (apply_retrieval, llama-memory-kvmem.cpp:3139-3142). */
 KVMEM_HIP_API int kvmem_engine_apply_retrieval(kvmem_engine *e, const void *q, int32_t q_type,
                                                uint32_t n_q_tokens, const uint32_t *mandatory,

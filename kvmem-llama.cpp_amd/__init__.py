@@ -86,6 +86,13 @@ class ScoreArgs(C.Structure):
                 ("layer_reduce", C.c_int32), ("layer_scores", C.c_void_p), ("scores", C.c_void_p)]
 
 
+class MeanKArgs(C.Structure):
+    _fields_ = [("q_sum", C.c_void_p), ("q_count", C.POINTER(C.c_uint32)), ("k_sum", C.c_void_p),
+                ("mean_tokens", C.c_void_p), ("n_layers", C.c_uint32), ("n_blocks", C.c_uint32),
+                ("capacity_blocks", C.c_uint32), ("n_head", C.c_uint32), ("n_head_kv", C.c_uint32),
+                ("head_dim", C.c_uint32), ("scores", C.c_void_p)]
+
+
 class Perf(C.Structure):
     _fields_ = [("score_ms", C.c_double), ("topk_ms", C.c_double), ("set_ms", C.c_double),
                 ("copy_ms", C.c_double), ("layout_ms", C.c_double), ("n_score", C.c_uint64),
@@ -132,6 +139,8 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_d2d_batched", i32, vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(sz), i32)
     _sig(lib, "kvmem_hip_score", i32, vp, C.POINTER(History), C.POINTER(ScoreArgs))
     _sig(lib, "kvmem_hip_topk", i32, vp, vp, u32, pu32, u32, u32, i32, pu32, pu32)
+    _sig(lib, "kvmem_hip_meank_sums", i32, vp, C.POINTER(History), pu32, u32, vp, vp)
+    _sig(lib, "kvmem_hip_score_meank", i32, vp, C.POINTER(MeanKArgs))
     _sig(lib, "kvmem_hip_perf_enable", i32, vp, i32)
     _sig(lib, "kvmem_hip_perf_get", i32, vp, C.POINTER(Perf))
     _sig(lib, "kvmem_hip_perf_reset", None, vp)
@@ -278,6 +287,20 @@ class Context:
         self.check(self.lib.kvmem_hip_topk(self.h, scores_ptr, n, f, nf, need, int(tie_lower_index),
                                            out, C.byref(cnt)), "topk")
         return list(out[: cnt.value])
+
+    # -- mean-K cosine scorer (reference semantics)
+    def meank_sums(self, hist: History, block_ids, k_sum_ptr: int, mean_tokens_ptr: int) -> None:
+        ids, n = _u32_array(block_ids)
+        self.check(self.lib.kvmem_hip_meank_sums(self.h, C.byref(hist), ids, n, k_sum_ptr,
+                                                 mean_tokens_ptr), "meank_sums")
+
+    def score_meank(self, q_sum_ptr: int, q_count, k_sum_ptr: int, mean_tokens_ptr: int,
+                    n_layers: int, n_blocks: int, n_head: int, n_head_kv: int, head_dim: int,
+                    scores_ptr: int, capacity_blocks: int = 0) -> None:
+        qc, _ = _u32_array(q_count)
+        a = MeanKArgs(q_sum_ptr, C.cast(qc, C.POINTER(C.c_uint32)), k_sum_ptr, mean_tokens_ptr,
+                      n_layers, n_blocks, capacity_blocks, n_head, n_head_kv, head_dim, scores_ptr)
+        self.check(self.lib.kvmem_hip_score_meank(self.h, C.byref(a)), "score_meank")
 
     # -- profiling
     def perf_enable(self, on: bool = True) -> None:

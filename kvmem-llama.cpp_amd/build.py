@@ -42,6 +42,7 @@ HIP_FLAGS = [f"--offload-arch={ARCH}", "-x", "hip",
 EXTRA = {
     "stagein.hip": ["-ffp-contract=off"],
     "score.hip": ["-ffinite-math-only"],
+    "meank.hip": ["-ffp-contract=off"],
 }
 
 

@@ -230,8 +230,8 @@ void kvmem_hip_destroy(kvmem_hip_ctx *ctx) {
         if (s.dev.ptr) hipFree(s.dev.ptr);
         if (s.done) hipEventDestroy(s.done);
     }
-    for (DevBuf *b : {&ctx->score_partial, &ctx->score_layers, &ctx->move_scratch, &ctx->topk_sel,
-                      &ctx->h2d_ring}) {
+    for (DevBuf *b : {&ctx->score_partial, &ctx->score_layers, &ctx->meank_scratch,
+                      &ctx->move_scratch, &ctx->topk_sel, &ctx->h2d_ring}) {
         if (b->ptr) hipFree(b->ptr);
     }
     if (ctx->topk_sel_host.ptr) hipHostFree(ctx->topk_sel_host.ptr);

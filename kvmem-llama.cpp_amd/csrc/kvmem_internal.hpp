@@ -53,6 +53,7 @@ struct kvmem_hip_ctx {
 
     kvmem_hip::DevBuf score_partial;    // [slices][L][Hkv][B] f32
     kvmem_hip::DevBuf score_layers;     // [L][B] f32 when the caller passes none
+    kvmem_hip::DevBuf meank_scratch;    // mean-K scorer: layer cosines, query vectors
     kvmem_hip::DevBuf move_scratch;     // gathered slots for kvmem_hip_move_slots
     kvmem_hip::DevBuf topk_sel;         // device selection output
     kvmem_hip::PinBuf topk_sel_host;    // pinned copy of the selection

@@ -1,0 +1,261 @@
+// Mean-K cosine block scorer (the reference's retrieval scorer) and its
+// mean-K producer.
+//
+// Producer: k_sum[l][b][e] = fp32 sum of the block's F16 keys in token
+// order, mean_tokens[l][b] = tokens summed (RawKvStore::capture_mean_f16,
+// kvmem/src/host/raw_kv_store.cpp:184-202).  A thread owns 8 consecutive
+// channels and adds token after token, so every channel's sum is the same
+// sequence of IEEE additions as the reference's: bit-identical.
+//
+// Scorer (llama_memory_kvmem::score_retrieval, src/adapter/
+// llama-memory-kvmem.cpp:2869-2916):
+//   qv[l][h]   = (sum_{gi<g} q_sum[l][h*g+gi]) * (1 / (q_count[l]*g))
+//   mk         = k_sum[l][b] * (1 / mean_tokens[l][b])
+//   cos[l][b][h] = (qv . mk_h) / (sqrt(|qv|^2) * sqrt(|mk_h|^2) + 1e-6)
+//   score[b]   = mean over layers with q_count > 0 of (sum_h cos) / Hkv,
+// layer and block sums in double as the reference; blocks with no keys in
+// any layer score 0.  One wave per (block, layer) computes the four heads'
+// dot products with a lane-then-tree reduction (the reference sums in
+// channel order: results agree to ~1e-7 of the norms).  HBM-bound: the
+// 16 x 2048-block scorer reads 128 MiB of fp32 sums.
+#include "kvmem_internal.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+namespace kvmem_hip {
+
+// grid: (items * L) workgroups of E/8 threads; item i = block_ids[i].
+__global__ __launch_bounds__(256) void meank_sum_kernel(const uint8_t *k, const uint32_t *items,
+                                                        uint32_t L, uint32_t cap, uint32_t T,
+                                                        uint32_t E, uint32_t last_block,
+                                                        uint32_t last_tokens, float *k_sum,
+                                                        uint32_t *mean_tokens) {
+    const uint32_t job = blockIdx.x;
+    const uint32_t item = job / L;
+    const uint32_t l = job - item * L;
+    const uint32_t b = items[item];
+    const uint32_t e0 = threadIdx.x * 8u;
+    if (e0 >= E) {
+        return;
+    }
+    const uint32_t nt = (b == last_block && last_tokens != 0) ? last_tokens : T;
+    const uint8_t *base = k + ((static_cast<uint64_t>(l) * cap + b) * T) * E * 2u + e0 * 2u;
+    float s[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t t = 0; t < nt; ++t) {
+        const uint4 raw = *reinterpret_cast<const uint4 *>(base + static_cast<uint64_t>(t) * E * 2u);
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s[2 * i] += static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] & 0xffffu)));
+            s[2 * i + 1] += static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[i] >> 16)));
+        }
+    }
+    float *out = k_sum + (static_cast<uint64_t>(l) * cap + b) * E + e0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        out[i] = s[i];
+    }
+    if (threadIdx.x == 0) {
+        mean_tokens[static_cast<uint64_t>(l) * cap + b] = nt;
+    }
+}
+
+// One thread per (layer, KV head): the group's query sum scaled by invq,
+// and its squared norm summed in channel order.
+__global__ __launch_bounds__(64) void meank_query_kernel(const float *q_sum, const float *invq,
+                                                         uint32_t L, uint32_t Hq, uint32_t Hkv,
+                                                         uint32_t D, float *qv, float *nq) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= L * Hkv) {
+        return;
+    }
+    const uint32_t l = i / Hkv;
+    const uint32_t h = i - l * Hkv;
+    const uint32_t g = Hq / Hkv;
+    const float inv = invq[l];
+    float n = 0.0f;
+    for (uint32_t d = 0; d < D; ++d) {
+        float acc = 0.0f;
+        for (uint32_t gi = 0; gi < g; ++gi) {
+            acc += q_sum[(static_cast<uint64_t>(l) * Hq + h * g + gi) * D + d];
+        }
+        const float v = acc * inv;
+        qv[static_cast<uint64_t>(i) * D + d] = v;
+        n += v * v;
+    }
+    nq[i] = n;
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void meank_cos_kernel(const float *k_sum, const uint32_t *mean_tokens,
+                                                        const float *qv, const float *nq,
+                                                        const float *invq, uint32_t L, uint32_t B,
+                                                        uint32_t cap, uint32_t Hkv, double *layer_cos) {
+    constexpr int PER = D / 64;  // channels per lane per head
+    const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    if (wave >= L * B) {
+        return;
+    }
+    const uint32_t l = wave / B;
+    const uint32_t b = wave - l * B;
+    if (invq[l] == 0.0f) {
+        return;  // layer without query rows
+    }
+    const uint32_t mt = mean_tokens[static_cast<uint64_t>(l) * cap + b];
+    const float inv = mt ? 1.0f / static_cast<float>(mt) : 0.0f;
+    const float *ks = k_sum + (static_cast<uint64_t>(l) * cap + b) * Hkv * D;
+    double layer = 0.0;
+    for (uint32_t h = 0; h < Hkv; ++h) {
+        const float *q = qv + (static_cast<uint64_t>(l) * Hkv + h) * D;
+        float dot = 0.0f, nk = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const uint32_t d = lane * PER + j;
+            const float m = mt ? ks[h * D + d] * inv : 0.0f;
+            dot += q[d] * m;
+            nk += m * m;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            dot += __shfl_xor(dot, off, 64);
+            nk += __shfl_xor(nk, off, 64);
+        }
+        const float c = dot / (sqrtf(nq[l * Hkv + h]) * sqrtf(nk) + 1e-6f);
+        layer += static_cast<double>(c);
+    }
+    if (lane == 0) {
+        layer_cos[static_cast<uint64_t>(l) * B + b] = layer;
+    }
+}
+
+__global__ __launch_bounds__(256) void meank_combine_kernel(const double *layer_cos,
+                                                            const uint32_t *mean_tokens,
+                                                            const float *invq, uint32_t L, uint32_t B,
+                                                            uint32_t cap, uint32_t Hkv, float *scores) {
+    const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) {
+        return;
+    }
+    bool has = false;
+    for (uint32_t l = 0; l < L; ++l) {
+        has |= mean_tokens[static_cast<uint64_t>(l) * cap + b] != 0;
+    }
+    double acc = 0.0;
+    uint32_t nlay = 0;
+    if (has) {
+        for (uint32_t l = 0; l < L; ++l) {
+            if (invq[l] == 0.0f) {
+                continue;
+            }
+            acc += layer_cos[static_cast<uint64_t>(l) * B + b] / static_cast<double>(Hkv ? Hkv : 1);
+            ++nlay;
+        }
+    }
+    scores[b] = static_cast<float>(nlay ? acc / nlay : 0.0);
+}
+
+}  // namespace kvmem_hip
+
+using namespace kvmem_hip;
+
+extern "C" {
+
+int kvmem_hip_meank_sums(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
+                         const uint32_t *block_ids, uint32_t n, float *k_sum,
+                         uint32_t *mean_tokens) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (n == 0) {
+        return KVMEM_HIP_OK;
+    }
+    if (!hist || !hist->k || !block_ids || !k_sum || !mean_tokens) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "meank_sums: null argument");
+    }
+    const uint32_t E = hist->n_embd_k;
+    const uint32_t cap = hist->capacity_blocks ? hist->capacity_blocks : hist->n_blocks;
+    if (E == 0 || E % 8 != 0 || E / 8 > 256 || hist->block_tokens == 0 || cap < hist->n_blocks ||
+        (reinterpret_cast<uintptr_t>(hist->k) & 15u) || (reinterpret_cast<uintptr_t>(k_sum) & 15u)) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID,
+                    "meank_sums: n_embd_k must be a multiple of 8 and at most 2048, 16-byte aligned");
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        if (block_ids[i] >= hist->n_blocks) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "meank_sums: block id out of range");
+        }
+    }
+    const uint64_t jobs = static_cast<uint64_t>(n) * hist->n_layers;
+    if (jobs > 0x7fffffffu) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "meank_sums: too many blocks in one call");
+    }
+    (void) hipSetDevice(ctx->device);
+    const void *items = upload(ctx, block_ids, sizeof(uint32_t) * n, "meank_sums ids");
+    if (!items) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    meank_sum_kernel<<<static_cast<uint32_t>(jobs), E / 8, 0, ctx->stream>>>(
+        static_cast<const uint8_t *>(hist->k), static_cast<const uint32_t *>(items), hist->n_layers,
+        cap, hist->block_tokens, E, hist->n_blocks - 1, hist->last_block_tokens, k_sum, mean_tokens);
+    return hip_ok(ctx, hipGetLastError(), "meank_sums launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
+}
+
+int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!a || !a->q_sum || !a->q_count || !a->k_sum || !a->mean_tokens || !a->scores) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "score_meank: null argument");
+    }
+    const uint32_t L = a->n_layers, B = a->n_blocks, D = a->head_dim;
+    const uint32_t cap = a->capacity_blocks ? a->capacity_blocks : B;
+    if (a->n_head_kv == 0 || a->n_head % a->n_head_kv != 0 || (D != 128 && D != 256) || cap < B) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "score_meank: bad head geometry");
+    }
+    if (L == 0 || B == 0) {
+        return KVMEM_HIP_OK;
+    }
+    const uint32_t g = a->n_head / a->n_head_kv;
+    // per-layer 1 / (q_count * g) as the reference computes it in fp32; 0
+    // marks a layer without query rows
+    std::vector<float> invq(L);
+    for (uint32_t l = 0; l < L; ++l) {
+        invq[l] = a->q_count[l] ? 1.0f / static_cast<float>(a->q_count[l] * g) : 0.0f;
+    }
+    (void) hipSetDevice(ctx->device);
+    const size_t qv_bytes = sizeof(float) * static_cast<size_t>(L) * a->n_head_kv * (D + 1);
+    const size_t cos_bytes = sizeof(double) * static_cast<size_t>(L) * B;
+    if (!ensure_dev(ctx, ctx->meank_scratch, qv_bytes + cos_bytes + 256, "score_meank scratch")) {
+        return KVMEM_HIP_ERR_NOMEM;
+    }
+    uint8_t *scratch = static_cast<uint8_t *>(ctx->meank_scratch.ptr);
+    double *layer_cos = reinterpret_cast<double *>(scratch);
+    float *qv = reinterpret_cast<float *>(scratch + cos_bytes);
+    float *nq = qv + static_cast<size_t>(L) * a->n_head_kv * D;
+    const float *invq_dev = static_cast<const float *>(upload(ctx, invq.data(), sizeof(float) * L,
+                                                              "score_meank invq"));
+    if (!invq_dev) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    perf_begin(ctx, kPerfScore);
+    const uint32_t lh = L * a->n_head_kv;
+    meank_query_kernel<<<(lh + 63) / 64, 64, 0, ctx->stream>>>(a->q_sum, invq_dev, L, a->n_head,
+                                                              a->n_head_kv, D, qv, nq);
+    const uint64_t waves = static_cast<uint64_t>(L) * B;
+    const uint32_t grid = static_cast<uint32_t>((waves * 64 + 255) / 256);
+    if (D == 256) {
+        meank_cos_kernel<256><<<grid, 256, 0, ctx->stream>>>(a->k_sum, a->mean_tokens, qv, nq, invq_dev,
+                                                             L, B, cap, a->n_head_kv, layer_cos);
+    } else {
+        meank_cos_kernel<128><<<grid, 256, 0, ctx->stream>>>(a->k_sum, a->mean_tokens, qv, nq, invq_dev,
+                                                             L, B, cap, a->n_head_kv, layer_cos);
+    }
+    meank_combine_kernel<<<(B + 255) / 256, 256, 0, ctx->stream>>>(layer_cos, a->mean_tokens, invq_dev,
+                                                                   L, B, cap, a->n_head_kv, a->scores);
+    perf_end(ctx, kPerfScore);
+    return hip_ok(ctx, hipGetLastError(), "score_meank launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
+}
+
+}  // extern "C"

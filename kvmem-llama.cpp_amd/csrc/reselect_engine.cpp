@@ -228,6 +228,10 @@ struct kvmem_engine {
     float *d_scores = nullptr;
     uint32_t d_scores_n = 0;
     int64_t dirty_tail = -1;   // resident partial block that grew since staged
+    float *d_ksum = nullptr;   // mean-K sums [L][capacity][n_embd_k]
+    uint32_t *d_mt = nullptr;  // mean-K token counts [L][capacity]
+    uint32_t meank_cap = 0;    // capacity the sums are allocated for
+    uint32_t meank_valid = 0;  // leading blocks whose sums are current
     uint64_t epoch = 1;
     std::string err;
 
@@ -395,6 +399,12 @@ void kvmem_engine_destroy(kvmem_engine *e) {
     if (e->d_scores) {
         (void) hipFree(e->d_scores);
     }
+    if (e->d_ksum) {
+        (void) hipFree(e->d_ksum);
+    }
+    if (e->d_mt) {
+        (void) hipFree(e->d_mt);
+    }
     kvmem_hip_destroy(e->ctx);
     delete e;
 }
@@ -422,6 +432,7 @@ int kvmem_engine_set_device_history(kvmem_engine *e, const void *k, const void *
     e->hist_k = k;
     e->hist_v = v;
     e->hist_capacity = capacity_blocks;
+    e->meank_valid = 0;
     const uint32_t have = e->rt.store().total_tokens();
     if (n_tokens < have) {
         e->rt.truncate_to(n_tokens);
@@ -459,6 +470,10 @@ int kvmem_engine_append_tokens(kvmem_engine *e, uint32_t n_new_tokens) {
         return e->fail(KVMEM_HIP_ERR_INVALID, "append_tokens: history capacity exceeded");
     }
     const uint32_t first_new = e->rt.store().block_count();
+    if (first_new > 0 && n_new_tokens > 0 &&
+        e->rt.store().blocks().back().n_tokens < e->p.block_tokens) {
+        e->meank_valid = std::min(e->meank_valid, first_new - 1);  // the tail grows
+    }
     if (first_new > 0 && n_new_tokens > 0) {
         // a partial tail that is in the pool must be staged again
         const Block &tail = e->rt.store().blocks().back();
@@ -479,6 +494,9 @@ int kvmem_engine_truncate_to(kvmem_engine *e, uint32_t token_pos) {
         return KVMEM_HIP_ERR_INVALID;
     }
     e->rt.truncate_to(token_pos);
+    const uint32_t nb = e->rt.store().block_count();
+    // a block cut short has stale sums
+    e->meank_valid = std::min(e->meank_valid, nb > 0 ? nb - 1 : 0u);
     ++e->epoch;
     return KVMEM_HIP_OK;
 }
@@ -581,6 +599,59 @@ int kvmem_engine_block_slots(const kvmem_engine *e, int32_t *slots) {
     return KVMEM_HIP_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+bool ensure_scores(kvmem_engine *e, uint32_t n) {
+    if (e->d_scores_n >= n) {
+        return true;
+    }
+    if (e->d_scores) {
+        if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
+            return false;
+        }
+        (void) hipFree(e->d_scores);
+        e->d_scores = nullptr;
+    }
+    if (hipMalloc(&e->d_scores, sizeof(float) * n) != hipSuccess) {
+        e->d_scores_n = 0;
+        return false;
+    }
+    e->d_scores_n = n;
+    return true;
+}
+
+// The store's charge (sink, mandatory, recent) then the device top-k over
+// d_scores for the remaining budget; ascending selection into sel.
+int select_topk(kvmem_engine *e, const std::vector<uint32_t> &mand, uint32_t *sel, uint32_t *n_sel) {
+    const uint32_t n = e->rt.store().block_count();
+    const kvmem_amd::TopkCharge charge = e->rt.store().charge_topk(mand);
+    std::vector<uint32_t> out;
+    if (charge.all_fit) {
+        out.resize(n);
+        for (uint32_t i = 0; i < n; ++i) out[i] = i;
+    } else {
+        std::vector<uint32_t> got(n);
+        uint32_t cnt = 0;
+        const int rc = kvmem_hip_topk(e->ctx, e->d_scores, n, charge.forced.data(),
+                                      static_cast<uint32_t>(charge.forced.size()), charge.need,
+                                      e->p.tie_lower_index, got.data(), &cnt);
+        if (rc != KVMEM_HIP_OK) {
+            return e->fail_ctx(rc, "preview top-k");
+        }
+        got.resize(cnt);
+        out.swap(got);
+    }
+    std::copy(out.begin(), out.end(), sel);
+    *n_sel = static_cast<uint32_t>(out.size());
+    return KVMEM_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_t n_q_tokens,
                          const uint32_t *mandatory, uint32_t n_mandatory, uint32_t *sel,
                          uint32_t *n_sel, uint64_t *epoch, uint32_t *rows) {
@@ -600,27 +671,11 @@ int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_
     if (n == 0) {
         return KVMEM_HIP_OK;
     }
-    if (e->d_scores_n < n) {
-        if (e->d_scores) {
-            if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
-                return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "preview");
-            }
-            (void) hipFree(e->d_scores);
-            e->d_scores = nullptr;
-        }
-        if (hipMalloc(&e->d_scores, sizeof(float) * n) != hipSuccess) {
-            e->d_scores_n = 0;
-            return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: score buffer");
-        }
-        e->d_scores_n = n;
+    if (!ensure_scores(e, n)) {
+        return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: score buffer");
     }
     std::vector<uint32_t> mand(mandatory, mandatory + n_mandatory);
-    const kvmem_amd::TopkCharge charge = e->rt.store().charge_topk(mand);
-    std::vector<uint32_t> out;
-    if (charge.all_fit) {
-        out.resize(n);
-        for (uint32_t i = 0; i < n; ++i) out[i] = i;
-    } else {
+    if (!e->rt.store().charge_topk(mand).all_fit) {
         const kvmem_hip_history h = e->device_history();
         kvmem_hip_score_args a{};
         a.q = q;
@@ -632,25 +687,87 @@ int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_
         a.layer_reduce = e->p.layer_reduce;
         a.layer_scores = nullptr;
         a.scores = e->d_scores;
-        int rc = kvmem_hip_score(e->ctx, &h, &a);
+        const int rc = kvmem_hip_score(e->ctx, &h, &a);
         if (rc != KVMEM_HIP_OK) {
             return e->fail_ctx(rc, "preview score");
         }
-        // top-k over the registered blocks only; the charged ids are forced
-        std::vector<uint32_t> got(n);
-        uint32_t cnt = 0;
-        rc = kvmem_hip_topk(e->ctx, e->d_scores, n, charge.forced.data(),
-                            static_cast<uint32_t>(charge.forced.size()), charge.need,
-                            e->p.tie_lower_index, got.data(), &cnt);
-        if (rc != KVMEM_HIP_OK) {
-            return e->fail_ctx(rc, "preview top-k");
-        }
-        got.resize(cnt);
-        out.swap(got);
     }
-    std::copy(out.begin(), out.end(), sel);
-    *n_sel = static_cast<uint32_t>(out.size());
-    return KVMEM_HIP_OK;
+    return select_topk(e, mand, sel, n_sel);
+}
+
+int kvmem_engine_preview_meank(kvmem_engine *e, const float *q_sum, const uint32_t *q_count,
+                               const uint32_t *mandatory, uint32_t n_mandatory, uint32_t *sel,
+                               uint32_t *n_sel, uint64_t *epoch, uint32_t *rows) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!q_sum || !q_count || !sel || !n_sel || (n_mandatory && !mandatory)) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "preview_meank: null argument");
+    }
+    if (!e->hist_k) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "preview_meank: no device history");
+    }
+    const uint32_t n = e->rt.store().block_count();
+    *n_sel = 0;
+    if (epoch) *epoch = e->epoch;
+    if (rows) *rows = e->rt.store().total_tokens();
+    if (n == 0) {
+        return KVMEM_HIP_OK;
+    }
+    if (!ensure_scores(e, n)) {
+        return e->fail(KVMEM_HIP_ERR_NOMEM, "preview_meank: score buffer");
+    }
+    std::vector<uint32_t> mand(mandatory, mandatory + n_mandatory);
+    if (!e->rt.store().charge_topk(mand).all_fit) {
+        // key sums for the blocks written since the last preview
+        if (e->meank_cap != e->hist_capacity) {
+            if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
+                return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "preview_meank");
+            }
+            if (e->d_ksum) (void) hipFree(e->d_ksum);
+            if (e->d_mt) (void) hipFree(e->d_mt);
+            e->d_ksum = nullptr;
+            e->d_mt = nullptr;
+            const size_t lc = static_cast<size_t>(e->p.n_layers) * e->hist_capacity;
+            if (hipMalloc(&e->d_ksum, sizeof(float) * lc * e->n_embd_k) != hipSuccess ||
+                hipMalloc(&e->d_mt, sizeof(uint32_t) * lc) != hipSuccess) {
+                e->meank_cap = 0;
+                return e->fail(KVMEM_HIP_ERR_NOMEM, "preview_meank: key sums");
+            }
+            e->meank_cap = e->hist_capacity;
+            e->meank_valid = 0;
+        }
+        const kvmem_hip_history h = e->device_history();
+        if (e->meank_valid < n) {
+            std::vector<uint32_t> ids;
+            for (uint32_t b = e->meank_valid; b < n; ++b) ids.push_back(b);
+            const int rc = kvmem_hip_meank_sums(e->ctx, &h, ids.data(), static_cast<uint32_t>(ids.size()),
+                                                e->d_ksum, e->d_mt);
+            if (rc != KVMEM_HIP_OK) {
+                return e->fail_ctx(rc, "preview_meank sums");
+            }
+            // a partial tail is summed again once it grows
+            const bool tail_partial = e->rt.store().blocks().back().n_tokens < e->p.block_tokens;
+            e->meank_valid = tail_partial ? n - 1 : n;
+        }
+        kvmem_hip_meank_args a{};
+        a.q_sum = q_sum;
+        a.q_count = q_count;
+        a.k_sum = e->d_ksum;
+        a.mean_tokens = e->d_mt;
+        a.n_layers = e->p.n_layers;
+        a.n_blocks = n;
+        a.capacity_blocks = e->hist_capacity;
+        a.n_head = e->p.n_head;
+        a.n_head_kv = e->p.n_head_kv;
+        a.head_dim = e->p.head_dim;
+        a.scores = e->d_scores;
+        const int rc = kvmem_hip_score_meank(e->ctx, &a);
+        if (rc != KVMEM_HIP_OK) {
+            return e->fail_ctx(rc, "preview_meank score");
+        }
+    }
+    return select_topk(e, mand, sel, n_sel);
 }
 
 int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uint32_t *sel,

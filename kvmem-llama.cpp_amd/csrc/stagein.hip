@@ -5,9 +5,11 @@
 // Work decomposition.  An operation (one block of one layer of K or V) is a
 // linear run of 32-element groups (rows are contiguous groups and the
 // output rows of a slot are contiguous cells).  A workgroup of 256 threads
-// handles a chunk of 256 groups; inside a wave, four consecutive lanes own
-// one group (8 halves = 16 bytes each), so a wave-wide load instruction
-// reads 1 KiB of contiguous F16.  The group scale comes from a two-step
+// handles a chunk of 512 groups, eight 16-group rounds per wave with all
+// eight 16-byte loads of a lane in flight together; inside a wave, four
+// consecutive lanes own one group (8 halves = 16 bytes each), so a
+// wave-wide load instruction reads 1 KiB of contiguous F16.  Output goes
+// out with nontemporal 16-byte stores.  The group scale comes from a two-step
 // quad reduction through DPP, the quantized bytes are packed in registers,
 // written to the wave's LDS region in ggml's byte layout, and copied out
 // with aligned 16-byte global stores.
@@ -17,6 +19,8 @@
 //   q8_0: d = amax/127, id = d ? 1/d : 0, q = roundf(x*id)
 //   q4_0: d = vmax/-8,  q = min(15, trunc(x*id + 8.5))
 //   q5_0: d = vmax/-16, q = min(31, trunc(x*id + 16.5)), bit 4 -> qh
+// (division by -8 / -16 is done as the exactly equal multiplication by
+// -0.125 / -0.0625: both round the same exact quotient once)
 // where vmax is the first element of largest magnitude.  The products and
 // sums are separate IEEE operations (no FMA contraction in this file),
 // divisions are correctly rounded (HIP default), d is stored as f16 RNE.
@@ -30,8 +34,9 @@
 
 namespace kvmem_hip {
 
-constexpr int kChunkGroups = 256;  // groups per workgroup
-constexpr int kWaveGroups = 64;    // groups per wave (4 rounds x 16)
+constexpr int kRounds = 8;                     // 16-group rounds per wave
+constexpr int kWaveGroups = 16 * kRounds;      // groups per wave (128)
+constexpr int kChunkGroups = 4 * kWaveGroups;  // groups per workgroup (512)
 
 template <int TYPE> struct Fmt;
 template <> struct Fmt<KVMEM_TYPE_Q8_0> { static constexpr int GB = 34; };
@@ -232,35 +237,48 @@ __device__ inline uint32_t trunc_code(float x, float id, float bias) {
     return static_cast<uint32_t>(c < TOP ? c : TOP);
 }
 
+// Codes of the 8 elements a lane owns, one per byte: element i of the lane
+// in byte i % 4 of word i / 4 (codes fit in 5 bits).
+template <int TOP>
+__device__ inline void trunc_codes(const uint32_t h[8], float id, float bias, uint32_t &w0,
+                                   uint32_t &w1) {
+    w0 = 0u;
+    w1 = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        w0 |= trunc_code<TOP>(half_bits_to_float(h[i]), id, bias) << (8 * i);
+        w1 |= trunc_code<TOP>(half_bits_to_float(h[i + 4]), id, bias) << (8 * i);
+    }
+}
+
 template <>
 __device__ inline void quant_quarter<KVMEM_TYPE_Q4_0>(const uint4 &v, uint32_t q, uint8_t *g,
                                                        bool valid) {
     uint32_t h[8];
     unpack8(v, h);
     const float vmax = quad_vmax(h, q);
-    const float d = vmax / -8.0f;
+    const float d = vmax * -0.125f;        // == vmax / -8 (exact scaling)
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t nib = 0;  // 8 codes, 4 bits each, element order
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        nib |= trunc_code<15>(half_bits_to_float(h[i]), id, 8.5f) << (4 * i);
-    }
-    // qs[j] = code(j) | code(j+16) << 4: lanes 0/1 pair with lanes 2/3
-    const uint32_t hi = quad_xor2(nib);
+    uint32_t w0, w1;
+    trunc_codes<15>(h, id, 8.5f, w0, w1);
+    // qs[j] = code(j) | code(j + 16) << 4: lanes 0 and 1 write the bytes,
+    // the partner code j + 16 sits in the same byte of lane q + 2
+    const uint32_t p0 = quad_xor2(w0);
+    const uint32_t p1 = quad_xor2(w1);
     if (valid) {
         if (q == 0) {
             store_u16(g, float_to_half_bits(d));
         }
         if (q < 2) {
-            uint32_t w[2] = {0u, 0u};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t b = ((nib >> (4 * i)) & 0xfu) | (((hi >> (4 * i)) & 0xfu) << 4);
-                w[i >> 2] |= b << (8 * (i & 3));
-            }
-            store_8bytes(g + 2 + 8 * q, w[0], w[1]);
+            store_8bytes(g + 2 + 8 * q, w0 | (p0 << 4), w1 | (p1 << 4));
         }
     }
+}
+
+// Bit 4 of each of the 4 bytes of w, as a 4-bit value (byte i -> bit i).
+__device__ inline uint32_t bit4_of_bytes(uint32_t w) {
+    const uint32_t x = (w >> 4) & 0x01010101u;
+    return (x * 0x01020408u) >> 24;  // bits 0, 8, 16, 24 -> 24..27, no carries
 }
 
 template <>
@@ -269,19 +287,18 @@ __device__ inline void quant_quarter<KVMEM_TYPE_Q5_0>(const uint4 &v, uint32_t q
     uint32_t h[8];
     unpack8(v, h);
     const float vmax = quad_vmax(h, q);
-    const float d = vmax / -16.0f;
+    const float d = vmax * -0.0625f;       // == vmax / -16 (exact scaling)
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t nib = 0;
-    uint32_t qh = 0;  // bit e = bit 4 of the code of element e
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t c = trunc_code<31>(half_bits_to_float(h[i]), id, 16.5f);
-        nib |= (c & 0xfu) << (4 * i);
-        qh |= ((c >> 4) & 1u) << (8 * q + i);
-    }
+    uint32_t w0, w1;
+    trunc_codes<31>(h, id, 16.5f, w0, w1);
+    // qh bit e = bit 4 of the code of element e (e = 8q + i)
+    uint32_t qh = (bit4_of_bytes(w0) | (bit4_of_bytes(w1) << 4)) << (8 * q);
     qh |= quad_xor1(qh);
     qh |= quad_xor2(qh);
-    const uint32_t hi = quad_xor2(nib);
+    w0 &= 0x0f0f0f0fu;
+    w1 &= 0x0f0f0f0fu;
+    const uint32_t p0 = quad_xor2(w0);
+    const uint32_t p1 = quad_xor2(w1);
     if (valid) {
         if (q == 0) {
             store_u16(g, float_to_half_bits(d));
@@ -289,13 +306,7 @@ __device__ inline void quant_quarter<KVMEM_TYPE_Q5_0>(const uint4 &v, uint32_t q
             store_u16(g + 4, qh >> 16);
         }
         if (q < 2) {
-            uint32_t w[2] = {0u, 0u};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t b = ((nib >> (4 * i)) & 0xfu) | (((hi >> (4 * i)) & 0xfu) << 4);
-                w[i >> 2] |= b << (8 * (i & 3));
-            }
-            store_8bytes(g + 6 + 8 * q, w[0], w[1]);
+            store_8bytes(g + 6 + 8 * q, w0 | (p0 << 4), w1 | (p1 << 4));
         }
     }
 }
@@ -325,9 +336,9 @@ __device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8
     const uint32_t wg0 = wave * kWaveGroups;
     uint8_t *wl = lds + wave * kWaveGroups * GB;
 
-    uint4 v[4];
+    uint4 v[kRounds];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < kRounds; ++r) {
         const uint32_t gl = wg0 + 16u * r + quad;
         v[r] = make_uint4(0u, 0u, 0u, 0u);
         if (gl < c.ng) {
@@ -339,7 +350,7 @@ __device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8
         }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < kRounds; ++r) {
         const uint32_t gl = wg0 + 16u * r + quad;
         quant_quarter<TYPE>(v[r], q, wl + (16u * r + quad) * GB, gl < c.ng);
     }
@@ -353,7 +364,9 @@ __device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8
     uint8_t *dst = c.dst + static_cast<uint64_t>(c.g0 + wg0) * GB;
     const uint32_t full = nb & ~15u;
     for (uint32_t off = lane * 16u; off < full; off += 1024u) {
-        *reinterpret_cast<uint4 *>(dst + off) = *reinterpret_cast<const uint4 *>(wl + off);
+        // packed rows are read by attention later, not by this launch
+        const u32x4_t w = *reinterpret_cast<const u32x4_t *>(wl + off);
+        __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t *>(dst + off));
     }
     for (uint32_t off = full + lane * 2u; off < nb; off += 128u) {
         *reinterpret_cast<uint16_t *>(dst + off) = *reinterpret_cast<const uint16_t *>(wl + off);

@@ -81,6 +81,7 @@ def bind(lib: C.CDLL) -> C.CDLL:
     sig("kvmem_engine_set_pool", i32, vp, C.POINTER(vp), C.POINTER(vp))
     sig("kvmem_engine_block_slots", i32, vp, pi32)
     sig("kvmem_engine_preview", i32, vp, vp, i32, u32, pu32, u32, pu32, pu32, C.POINTER(u64), pu32)
+    sig("kvmem_engine_preview_meank", i32, vp, vp, pu32, pu32, u32, pu32, pu32, C.POINTER(u64), pu32)
     sig("kvmem_engine_apply", i32, vp, u64, u32, pu32, u32, C.POINTER(PlanStats))
     sig("kvmem_engine_apply_retrieval", i32, vp, vp, i32, u32, pu32, u32, C.POINTER(PlanStats))
     sig("kvmem_engine_scores", i32, vp, C.POINTER(C.c_float), u32)
@@ -273,6 +274,19 @@ class Engine:
         ep = C.c_uint64(0)
         self.check(self.lib.kvmem_engine_preview(self.h, q_ptr, q_type, n_q_tokens, m, nm, out,
                                                  C.byref(n), C.byref(ep), C.byref(rows)), "preview")
+        return Selection(ep.value, rows.value, list(out[: n.value]))
+
+    def preview_meank(self, q_sum_ptr: int, q_count: Sequence[int],
+                      mandatory: Sequence[int] = ()) -> Selection:
+        """Preview with the reference's mean-K cosine scorer (q_sum: device
+        [n_layers][n_head*head_dim] f32 sums of query rows, q_count per layer)."""
+        qc, _ = _u32(q_count)
+        m, nm = _u32(mandatory)
+        out = (C.c_uint32 * max(1, self.block_count()))()
+        n, rows = C.c_uint32(0), C.c_uint32(0)
+        ep = C.c_uint64(0)
+        self.check(self.lib.kvmem_engine_preview_meank(self.h, q_sum_ptr, qc, m, nm, out, C.byref(n),
+                                                       C.byref(ep), C.byref(rows)), "preview_meank")
         return Selection(ep.value, rows.value, list(out[: n.value]))
 
     def apply(self, sel: Selection) -> dict:

@@ -24,6 +24,12 @@
  *                                   its own sources (oracle/_ref), the
  *                                   reference's own unit-test cases, sort-based
  *                                   brute force.
+ *   ko_meank_sum_f16 / ko_mean_k  : the reference RawKvStore (oracle/_ref),
+ *                                   bit-exact; the reference's own
+ *                                   cancellation pattern (raw_kv_store_test).
+ *   ko_score_meank                : an independent float64 numpy restatement,
+ *                                   closed forms (parallel / orthogonal /
+ *                                   scaled directions, GQA head sums).
  */
 #ifndef KVMEM_ORACLE_H
 #define KVMEM_ORACLE_H
@@ -112,6 +118,19 @@ void ko_pick_topk(const double *scores, uint32_t n, uint32_t budget,
                   uint32_t sink, uint32_t recent,
                   const uint32_t *mandatory, uint32_t n_mandatory,
                   int tie_lower_index, uint32_t *out, uint32_t *n_out);
+
+/* Mean-K producer of the reference (RawKvStore::capture_mean_f16,
+ * raw_kv_store.cpp:184-202): fp32 sum of n_tokens F16 rows in token order. */
+void ko_meank_sum_f16(const uint16_t *rows, uint32_t n_tokens, uint32_t n_embd,
+                      uint64_t row_stride, float *k_sum);
+/* RawKvStore::mean_k normalisation (raw_kv_store.cpp:984-995). */
+void ko_mean_k(const float *k_sum, uint32_t mean_tokens, uint32_t n_embd, float *out);
+/* The reference's retrieval scorer, mean-K cosine
+ * (llama-memory-kvmem.cpp:2869-2916): q_sum [L][Hq*D], q_count [L],
+ * k_sum [L][B][Hkv*D], mean_tokens [L][B] -> scores [B] (double). */
+void ko_score_meank(const float *q_sum, const uint32_t *q_count, const float *k_sum,
+                    const uint32_t *mean_tokens, uint32_t L, uint32_t B, uint32_t Hq,
+                    uint32_t Hkv, uint32_t D, double *scores);
 
 /* Number of OpenMP threads the oracle uses (for the baseline's core count). */
 int ko_max_threads(void);

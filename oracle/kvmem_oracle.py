@@ -64,6 +64,12 @@ def lib() -> C.CDLL:
     L.ko_pick_topk.restype = None
     L.ko_pick_topk.argtypes = [f64p, u32, u32, u32, u32, C.c_void_p, u32, C.c_int, u32p,
                                C.POINTER(C.c_uint32)]
+    L.ko_meank_sum_f16.restype = None
+    L.ko_meank_sum_f16.argtypes = [u16p, u32, u32, C.c_uint64, f32p]
+    L.ko_mean_k.restype = None
+    L.ko_mean_k.argtypes = [f32p, u32, u32, f32p]
+    L.ko_score_meank.restype = None
+    L.ko_score_meank.argtypes = [f32p, u32p, f32p, u32p, u32, u32, u32, u32, u32, f64p]
     L.ko_max_threads.restype = C.c_int
     L.ko_max_threads.argtypes = []
     _lib = L
@@ -172,6 +178,36 @@ def pick_topk(scores, budget: int, sink: int = 1, recent: int = 0, mandatory=(),
     lib().ko_pick_topk(s, n, budget, sink, recent, mand.ctypes.data if mand.size else None,
                        mand.size, int(tie_lower_index), out, C.byref(cnt))
     return out[: cnt.value].tolist()
+
+
+def meank_sum_f16(rows: np.ndarray) -> np.ndarray:
+    """[n_tokens, n_embd] f16 bits -> fp32 token-order sum (capture_mean_f16)."""
+    rows = np.ascontiguousarray(rows, dtype=np.uint16)
+    n, e = rows.shape
+    out = np.zeros(e, dtype=np.float32)
+    lib().ko_meank_sum_f16(rows, n, e, e, out)
+    return out
+
+
+def mean_k(k_sum: np.ndarray, mean_tokens: int) -> np.ndarray:
+    k_sum = np.ascontiguousarray(k_sum, dtype=np.float32)
+    out = np.zeros_like(k_sum)
+    lib().ko_mean_k(k_sum, mean_tokens, k_sum.size, out)
+    return out
+
+
+def score_meank(q_sum: np.ndarray, q_count, k_sum: np.ndarray, mean_tokens: np.ndarray,
+                Hq: int, Hkv: int, D: int) -> np.ndarray:
+    """q_sum [L, Hq*D] f32, q_count [L], k_sum [L, B, Hkv*D] f32,
+    mean_tokens [L, B] -> scores [B] f64 (score_retrieval)."""
+    q_sum = np.ascontiguousarray(q_sum, dtype=np.float32)
+    k_sum = np.ascontiguousarray(k_sum, dtype=np.float32)
+    mt = np.ascontiguousarray(mean_tokens, dtype=np.uint32)
+    qc = np.ascontiguousarray(q_count, dtype=np.uint32)
+    L, B = mt.shape
+    out = np.zeros(B, dtype=np.float64)
+    lib().ko_score_meank(q_sum, qc, k_sum, mt, L, B, Hq, Hkv, D, out)
+    return out
 
 
 def max_threads() -> int:

@@ -1,6 +1,6 @@
 // C entry points over the reference's own host kvmem library (KvMemStore /
-// KvMemRuntime compiled from kvmem/src/host/*.cpp where the reference tree
-// lies), so that ctypes can drive it as a second checker.
+// KvMemRuntime / RawKvStore compiled from kvmem/src/host/*.cpp where the
+// reference tree lies), so that ctypes can drive it as a second checker.
 //
 // TEST INFRASTRUCTURE ONLY: built into oracle/_ref/ by `make ref`; used by
 // tests/golden/make_golden.py to write fixtures and by CPU tests when the
@@ -12,6 +12,7 @@
 // slots are pushed back (LIFO).
 #include "kvmem/kvmem_runtime.hpp"
 #include "kvmem/kvmem_store.hpp"
+#include "kvmem/raw_kv_store.hpp"
 
 #include <cstdint>
 #include <cstring>
@@ -161,4 +162,47 @@ KREF_API uint32_t kref_runtime_blocks(void *h, int32_t *gpu_slot, uint8_t *tier,
         baked_pos[i] = bl[i].baked_pos;
     }
     return static_cast<uint32_t>(bl.size());
+}
+
+// RawKvStore mean-K of block `block` after writing n_tokens F16 K rows
+// (token-major [n_tokens][n_embd]) from position 0 with
+// write_layer_tokens_f16 (capture_mean_f16 path), one layer.
+KREF_API int kref_mean_k_f16(uint32_t n_embd, uint32_t block_tokens, const uint16_t *k_rows,
+                             uint32_t n_tokens, uint32_t block, float *out) {
+    try {
+        kvmem::RawKvStoreConfig cfg;
+        cfg.n_layer = 1;
+        cfg.n_embd_k = n_embd;
+        cfg.n_embd_v = n_embd;
+        cfg.block_tokens = block_tokens;
+        kvmem::RawKvStore raw(cfg);
+        raw.write_layer_tokens_f16(0, n_tokens, 0, k_rows, nullptr);
+        raw.mean_k(block, 0, out);
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+// RawKvStore mean-K after write_layer_mean_k of f32 rows in batches of
+// `batch` tokens (the add_mean_f32 path), one layer.
+KREF_API int kref_mean_k_f32(uint32_t n_embd, uint32_t block_tokens, const float *rows,
+                             uint32_t n_tokens, uint32_t batch, uint32_t block, float *out) {
+    try {
+        kvmem::RawKvStoreConfig cfg;
+        cfg.n_layer = 1;
+        cfg.n_embd_k = n_embd;
+        cfg.n_embd_v = n_embd;
+        cfg.block_tokens = block_tokens;
+        cfg.k_row_bytes = 1088;
+        kvmem::RawKvStore raw(cfg);
+        for (uint32_t pos = 0; pos < n_tokens; pos += batch) {
+            const uint32_t n = n_tokens - pos < batch ? n_tokens - pos : batch;
+            raw.write_layer_mean_k(pos, n, 0, rows + static_cast<size_t>(pos) * n_embd);
+        }
+        raw.mean_k(block, 0, out);
+        return 0;
+    } catch (...) {
+        return -1;
+    }
 }

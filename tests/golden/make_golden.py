@@ -10,6 +10,11 @@ quant_vectors.npz
     from zero, f16 scale by round-to-nearest-even).  Independent of
     oracle/kvmem_oracle_quant.c, which the tests check against it.
 
+meank_vectors.npz
+    F16 key rows of 2.6 blocks and the mean-K of each block as the
+    reference's own RawKvStore computes it (kvmem/src/host/raw_kv_store.cpp,
+    compiled into oracle/_ref).
+
 select_sequences.json
     Multi-step reselect scenarios produced by the reference's own host
     library (kvmem/src/host/kvmem_store.cpp + kvmem_runtime.cpp, compiled
@@ -221,9 +226,29 @@ def write_select(n_scenarios: int = 40, steps: int = 3) -> None:
         "scenarios": scenarios}, separators=(",", ":")))
 
 
+def write_meank() -> None:
+    """F16 key rows and the reference RawKvStore's mean-K of each block
+    (write_layer_tokens_f16 then mean_k, the capture_mean_f16 path)."""
+    lib = C.CDLL(str(REF_LIB))
+    lib.kref_mean_k_f16.argtypes = [C.c_uint32, C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32,
+                                    C.c_void_p]
+    rng = np.random.default_rng(33)
+    E, bt, n = 256, 32, 75                       # two full blocks and a partial one
+    x = rng.standard_normal((n, E)).astype(np.float32)
+    x[:, 5] *= 3e3                                # large channel: rounding in the sums
+    x[::3, 9] = -x[::3, 9] * 1e4
+    rows = x.astype(np.float16).view(np.uint16)
+    means = np.zeros((3, E), np.float32)
+    for b in range(3):
+        lib.kref_mean_k_f16(E, bt, rows.ctypes.data, n, b, means[b].ctypes.data)
+    np.savez_compressed(HERE / "meank_vectors.npz", rows=rows, block_tokens=np.array(bt),
+                        means=means)
+
+
 if __name__ == "__main__":
     write_quant()
     if REF_LIB.exists():
         write_select()
+        write_meank()
     else:
         print(f"{REF_LIB} not built: `make -C oracle ref` (needs the reference tree)")

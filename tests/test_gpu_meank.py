@@ -1,0 +1,132 @@
+"""Mean-K producer and mean-K cosine scorer on the GPU vs the oracle.
+
+Sums are compared bit-exact (the producer adds the F16 keys in token order,
+as the reference); scores within 1e-5 absolute of the oracle (cosines in
+[-1, 1]; the GPU reduces channels in a lane-then-tree order).  Covers a
+partial last block, a capacity larger than the history, layers without
+query rows and blocks without keys, and the full 16-layer x 2048-block
+history shape on sampled blocks.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from conftest import load_pkg  # noqa: E402
+
+kv = load_pkg()
+from kvmem_amd import host, workloads  # noqa: E402
+
+T, HKV, HQ, D = 128, 4, 24, 256
+E = HKV * D
+
+
+def announce(msg: str) -> None:
+    print(f"[meank] {msg}", flush=True)
+
+
+def device_sums(ctx, k, n_blocks, cap, last_T=0, ids=None):
+    L = k.shape[0]
+    ks = torch.full((L, cap, E), float("nan"), dtype=torch.float32, device="cuda")
+    mt = torch.zeros((L, cap), dtype=torch.int32, device="cuda")
+    hist = ctx.make_history(k.data_ptr(), None, L, n_blocks, T, E, 0, last_T, cap)
+    torch.cuda.synchronize()
+    ctx.meank_sums(hist, list(range(n_blocks)) if ids is None else ids, ks.data_ptr(), mt.data_ptr())
+    ctx.sync()
+    return ks, mt
+
+
+def test_meank_sums_bit_exact(ctx, oracle):
+    announce("sums: 3 layers, 11 of 14 capacity blocks, partial last block of 53 tokens")
+    L, nb, cap, last = 3, 11, 14, 53
+    k, _, _ = workloads.scoring_tensors(torch, "cuda", L=L, B=cap, Tq=1, seed=21)
+    k[0, 7] *= 900.0                       # large values: rounding inside the sums
+    ks, mt = device_sums(ctx, k, nb, cap, last)
+    kb = workloads.to_bits(torch, k)
+    got, mtn = ks.cpu().numpy(), mt.cpu().numpy()
+    for l in range(L):
+        for b in range(nb):
+            nt = last if b == nb - 1 else T
+            assert mtn[l, b] == nt
+            want = oracle.meank_sum_f16(kb[l, b].reshape(T, E)[:nt])
+            assert np.array_equal(got[l, b].view(np.uint32), want.view(np.uint32)), (l, b)
+    assert np.isnan(got[:, nb:]).all()     # blocks past the history are untouched
+
+
+def test_meank_scores_vs_oracle(ctx, oracle):
+    announce("scores: 4 layers x 40 blocks, layer 2 without query rows, block 9 without keys")
+    L, nb = 4, 40
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=L, B=nb, Tq=16, seed=22)
+    ks, mt = device_sums(ctx, k, nb, nb)
+    mt[:, 9] = 0
+    q_sum = q.float().sum(dim=1).contiguous()          # [L][Hq*D] sums of 16 query rows
+    q_count = [16, 16, 0, 16]
+    scores = torch.empty(nb, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.score_meank(q_sum.data_ptr(), q_count, ks.data_ptr(), mt.data_ptr(), L, nb, HQ, HKV, D,
+                    scores.data_ptr())
+    ctx.sync()
+    got = scores.cpu().numpy().astype(np.float64)
+    want = oracle.score_meank(q_sum.cpu().numpy().reshape(L, HQ * D), q_count, ks.cpu().numpy(),
+                              mt.cpu().numpy().astype(np.uint32), HQ, HKV, D)
+    assert got[9] == 0.0
+    assert np.max(np.abs(got - want)) <= 1e-5, np.max(np.abs(got - want))
+
+
+def test_meank_full_history_sampled(ctx, oracle):
+    announce("full history 16 layers x 2048 blocks, sampled blocks")
+    L, nb = 16, 2048
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=L, B=nb, Tq=64, seed=2)
+    ks, mt = device_sums(ctx, k, nb, nb)
+    q_sum = q.float().sum(dim=1).contiguous()
+    scores = torch.empty(nb, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.score_meank(q_sum.data_ptr(), [64] * L, ks.data_ptr(), mt.data_ptr(), L, nb, HQ, HKV, D,
+                    scores.data_ptr())
+    ctx.sync()
+    ids = np.array([0, 1, 777, 1500, 2047])
+    idx = torch.from_numpy(ids).cuda()
+    kb = workloads.to_bits(torch, k[:, idx])
+    sums = np.stack([[oracle.meank_sum_f16(kb[l, i].reshape(T, E)) for i in range(len(ids))]
+                     for l in range(L)])
+    assert np.array_equal(ks[:, idx].cpu().numpy().view(np.uint32), sums.view(np.uint32))
+    want = oracle.score_meank(q_sum.cpu().numpy().reshape(L, HQ * D), [64] * L, sums,
+                              np.full((L, len(ids)), T, np.uint32), HQ, HKV, D)
+    got = scores.cpu().numpy()[ids].astype(np.float64)
+    assert np.max(np.abs(got - want)) <= 1e-5
+    del k, ks
+    torch.cuda.empty_cache()
+
+
+def test_engine_meank_preview_apply(oracle):
+    """The engine with the reference scorer: scores within 1e-5 of the
+    oracle over sums it produced itself, selection = the oracle's top-k over
+    the engine's scores, sums refreshed after the history grows."""
+    announce("engine mean-K preview: 2 layers x 30 blocks, grown tail")
+    L, cap = 2, 32
+    k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=cap, Tq=8, seed=23, with_v=True)
+    q_sum = q.float().sum(dim=1).contiguous()
+    n_tok = 29 * T + 40
+    with host.Engine(n_layers=L, block_tokens=T, n_head=HQ, n_head_kv=HKV, head_dim=D,
+                     budget_blocks=6, reserve_blocks=2, recent_blocks=1) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, n_tok)
+        for step in range(2):
+            sel = eng.preview_meank(q_sum.data_ptr(), [8] * L)
+            nb = eng.block_count()
+            kb = workloads.to_bits(torch, k)
+            last = eng.total_tokens() - (nb - 1) * T
+            sums = np.stack([[oracle.meank_sum_f16(kb[l, b].reshape(T, E)[:(T if b < nb - 1 else last)])
+                              for b in range(nb)] for l in range(L)])
+            mt = np.full((L, nb), T, np.uint32)
+            mt[:, nb - 1] = last
+            want = oracle.score_meank(q_sum.cpu().numpy().reshape(L, HQ * D), [8] * L, sums, mt, HQ, HKV, D)
+            got = np.array(eng.scores(), dtype=np.float64)
+            assert np.max(np.abs(got - want)) <= 1e-5, step
+            assert sel.blocks == oracle.pick_topk(got.astype(np.float32).astype(np.float64), 6, sink=1,
+                                                  recent=1)
+            eng.apply(sel)
+            eng.append_tokens(50)           # the partial tail grows: its sums are redone
