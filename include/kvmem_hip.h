@@ -274,6 +274,21 @@ KVMEM_HIP_API int kvmem_hip_meank_sums(kvmem_hip_ctx *ctx, const kvmem_hip_histo
                                        const uint32_t *block_ids, uint32_t n,
                                        float *k_sum, uint32_t *mean_tokens);
 
+/* Query-sum producer (the reference's Q harvest into q_sum_,
+ * src/adapter/llama-memory-kvmem.cpp:2164-2172 and :2206-2219): for every
+ * layer and channel, q_sum[l][e] += q[l][t][e] over the listed tokens in
+ * list order, fp32 additions as the reference (bit-identical).
+ *   q       device [n_layers][n_tokens][n_embd_q], F32, F16 or BF16
+ *   tokens  host list of token indices (the query span; NULL = every token
+ *           in order), n_list entries
+ *   reset   nonzero: start from 0 (q_sum_ cleared), else add onto q_sum
+ *   q_sum   device [n_layers][n_embd_q] f32
+ * The caller counts the rows (q_count_) itself. */
+KVMEM_HIP_API int kvmem_hip_q_accumulate(kvmem_hip_ctx *ctx, const void *q, int32_t q_type,
+                                         uint32_t n_layers, uint32_t n_tokens, uint32_t n_embd_q,
+                                         const uint32_t *tokens, uint32_t n_list, int reset,
+                                         float *q_sum);
+
 /* The reference's retrieval scorer (llama_memory_kvmem::score_retrieval,
  * src/adapter/llama-memory-kvmem.cpp:2869-2916): per block the mean over
  * layers with query rows of the mean over KV heads of

@@ -121,11 +121,20 @@ typedef struct kvmem_engine_params {
                                   slot i after apply, as
                                   layout_gpu_slots_by_orig_pos
                                   (llama-memory-kvmem.cpp:931-1254) */
+    int32_t scorer;            /* kvmem_engine_scorer used by preview */
 } kvmem_engine_params;
+
+/* Block scorer of kvmem_engine_preview / apply_retrieval. */
+enum kvmem_engine_scorer {
+    KVMEM_SCORER_TOKEN_MAX = 0, /* per-token max of q.k / sqrt(head_dim) on MFMA */
+    KVMEM_SCORER_MEAN_K = 1     /* the reference's mean-K cosine (score_retrieval,
+                                   llama-memory-kvmem.cpp:2869-2916) over the
+                                   sum of the query rows */
+};
 
 /* Defaults: 16 layers, 128-token blocks, 24/4 heads x 256, budget 256 +
  * reserve 128 blocks, sink 1, recent 0, q8_0 K and V, lower-id ties, mean
- * layer reduce, free-list (non-canonical) layout. */
+ * layer reduce, free-list (non-canonical) layout, per-token max scorer. */
 KVMEM_HIP_API kvmem_engine_params kvmem_engine_default_params(void);
 
 /* Create the engine: its kvmem_hip_ctx, the slot pool of
@@ -175,11 +184,13 @@ KVMEM_HIP_API int kvmem_engine_pool_layer(const kvmem_engine *e, uint32_t layer,
 /* Slot of every block (-1 = not in the pool), block count entries. */
 KVMEM_HIP_API int kvmem_engine_block_slots(const kvmem_engine *e, int32_t *slots);
 
-/* Phase 1 (preview_retrieval): score every block with the per-token max
- * scorer over q (device [n_layers][n_q_tokens][n_head][head_dim], bf16 or
- * f16), then top-k with sink / mandatory (host ids, newest last) / recent
- * charged first.  Writes the ascending selection (capacity block count),
- * its epoch and rows (history tokens). */
+/* Phase 1 (preview_retrieval): score every block over q (device
+ * [n_layers][n_q_tokens][n_head][head_dim], bf16 or f16) with the engine's
+ * scorer -- the per-token max, or mean-K cosine over the sum of the
+ * n_q_tokens rows (q_count_ = n_q_tokens in every layer) -- then top-k
+ * with sink / mandatory (host ids, newest last) / recent charged first.
+ * Writes the ascending selection (capacity block count), its epoch and rows
+ * (history tokens). */
 KVMEM_HIP_API int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type,
                                        uint32_t n_q_tokens, const uint32_t *mandatory,
                                        uint32_t n_mandatory, uint32_t *sel, uint32_t *n_sel,

@@ -141,6 +141,7 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_topk", i32, vp, vp, u32, pu32, u32, u32, i32, pu32, pu32)
     _sig(lib, "kvmem_hip_meank_sums", i32, vp, C.POINTER(History), pu32, u32, vp, vp)
     _sig(lib, "kvmem_hip_score_meank", i32, vp, C.POINTER(MeanKArgs))
+    _sig(lib, "kvmem_hip_q_accumulate", i32, vp, vp, i32, u32, u32, u32, pu32, u32, i32, vp)
     _sig(lib, "kvmem_hip_perf_enable", i32, vp, i32)
     _sig(lib, "kvmem_hip_perf_get", i32, vp, C.POINTER(Perf))
     _sig(lib, "kvmem_hip_perf_reset", None, vp)
@@ -293,6 +294,16 @@ class Context:
         ids, n = _u32_array(block_ids)
         self.check(self.lib.kvmem_hip_meank_sums(self.h, C.byref(hist), ids, n, k_sum_ptr,
                                                  mean_tokens_ptr), "meank_sums")
+
+    def q_accumulate(self, q_ptr: int, q_type: int, n_layers: int, n_tokens: int, n_embd_q: int,
+                     q_sum_ptr: int, tokens=None, reset: bool = True) -> None:
+        """q_sum[l] (+)= the listed query rows of layer l, in list order."""
+        if tokens is None:
+            ids, n = None, 0
+        else:
+            ids, n = _u32_array(tokens)
+        self.check(self.lib.kvmem_hip_q_accumulate(self.h, q_ptr, q_type, n_layers, n_tokens, n_embd_q,
+                                                   ids, n, int(reset), q_sum_ptr), "q_accumulate")
 
     def score_meank(self, q_sum_ptr: int, q_count, k_sum_ptr: int, mean_tokens_ptr: int,
                     n_layers: int, n_blocks: int, n_head: int, n_head_kv: int, head_dim: int,

@@ -1,5 +1,5 @@
 // Mean-K cosine block scorer (the reference's retrieval scorer) and its
-// mean-K producer.
+// two producers, the per-block key sums and the per-layer query sums.
 //
 // Producer: k_sum[l][b][e] = fp32 sum of the block's F16 keys in token
 // order, mean_tokens[l][b] = tokens summed (RawKvStore::capture_mean_f16,
@@ -60,6 +60,29 @@ __global__ __launch_bounds__(256) void meank_sum_kernel(const uint8_t *k, const 
     if (threadIdx.x == 0) {
         mean_tokens[static_cast<uint64_t>(l) * cap + b] = nt;
     }
+}
+
+// Query-sum producer: one thread per (layer, channel) adds the listed
+// tokens' values in list order onto (or from zero into) q_sum, as the
+// reference's harvest loop does per layer (llama-memory-kvmem.cpp:2164-2172).
+template <typename QT>
+__global__ __launch_bounds__(256) void q_accumulate_kernel(const QT *q, const uint32_t *tokens,
+                                                           uint32_t n_list, uint32_t n_tokens,
+                                                           uint32_t E, uint32_t L, int reset,
+                                                           float *q_sum) {
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t l = blockIdx.y;
+    if (e >= E || l >= L) {
+        return;
+    }
+    float *dst = q_sum + static_cast<uint64_t>(l) * E + e;
+    float acc = reset ? 0.0f : *dst;
+    const QT *src = q + static_cast<uint64_t>(l) * n_tokens * E + e;
+    for (uint32_t i = 0; i < n_list; ++i) {
+        const uint32_t t = tokens ? tokens[i] : i;
+        acc += static_cast<float>(src[static_cast<uint64_t>(t) * E]);
+    }
+    *dst = acc;
 }
 
 // One thread per (layer, KV head): the group's query sum scaled by invq,
@@ -200,6 +223,55 @@ int kvmem_hip_meank_sums(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
         static_cast<const uint8_t *>(hist->k), static_cast<const uint32_t *>(items), hist->n_layers,
         cap, hist->block_tokens, E, hist->n_blocks - 1, hist->last_block_tokens, k_sum, mean_tokens);
     return hip_ok(ctx, hipGetLastError(), "meank_sums launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
+}
+
+int kvmem_hip_q_accumulate(kvmem_hip_ctx *ctx, const void *q, int32_t q_type, uint32_t n_layers,
+                           uint32_t n_tokens, uint32_t n_embd_q, const uint32_t *tokens,
+                           uint32_t n_list, int reset, float *q_sum) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!q || !q_sum) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "q_accumulate: null argument");
+    }
+    if (q_type != KVMEM_TYPE_F32 && q_type != KVMEM_TYPE_F16 && q_type != KVMEM_TYPE_BF16) {
+        return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "q_accumulate: q_type must be F32, F16 or BF16");
+    }
+    if (!tokens) {
+        n_list = n_tokens;
+    }
+    for (uint32_t i = 0; tokens && i < n_list; ++i) {
+        if (tokens[i] >= n_tokens) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "q_accumulate: token index out of range");
+        }
+    }
+    if (n_layers == 0 || n_embd_q == 0 || (n_list == 0 && !reset)) {
+        return KVMEM_HIP_OK;
+    }
+    if (n_layers > 65535) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "q_accumulate: too many layers");
+    }
+    (void) hipSetDevice(ctx->device);
+    const uint32_t *dev_tokens = nullptr;
+    if (tokens && n_list) {
+        dev_tokens = static_cast<const uint32_t *>(upload(ctx, tokens, sizeof(uint32_t) * n_list,
+                                                          "q_accumulate tokens"));
+        if (!dev_tokens) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+    }
+    const dim3 grid((n_embd_q + 255) / 256, n_layers);
+    if (q_type == KVMEM_TYPE_F32) {
+        q_accumulate_kernel<float><<<grid, 256, 0, ctx->stream>>>(
+            static_cast<const float *>(q), dev_tokens, n_list, n_tokens, n_embd_q, n_layers, reset, q_sum);
+    } else if (q_type == KVMEM_TYPE_F16) {
+        q_accumulate_kernel<_Float16><<<grid, 256, 0, ctx->stream>>>(
+            static_cast<const _Float16 *>(q), dev_tokens, n_list, n_tokens, n_embd_q, n_layers, reset, q_sum);
+    } else {
+        q_accumulate_kernel<__bf16><<<grid, 256, 0, ctx->stream>>>(
+            static_cast<const __bf16 *>(q), dev_tokens, n_list, n_tokens, n_embd_q, n_layers, reset, q_sum);
+    }
+    return hip_ok(ctx, hipGetLastError(), "q_accumulate launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
 }
 
 int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {

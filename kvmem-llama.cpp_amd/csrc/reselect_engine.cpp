@@ -232,6 +232,7 @@ struct kvmem_engine {
     uint32_t *d_mt = nullptr;  // mean-K token counts [L][capacity]
     uint32_t meank_cap = 0;    // capacity the sums are allocated for
     uint32_t meank_valid = 0;  // leading blocks whose sums are current
+    float *d_qsum = nullptr;   // query sums [L][n_head*head_dim] (mean-K scorer)
     uint64_t epoch = 1;
     std::string err;
 
@@ -343,6 +344,7 @@ kvmem_engine_params kvmem_engine_default_params(void) {
     p.tie_lower_index = 1;
     p.layer_reduce = KVMEM_LAYER_MEAN;
     p.canonical_layout = 0;
+    p.scorer = KVMEM_SCORER_TOKEN_MAX;
     return p;
 }
 
@@ -354,7 +356,8 @@ int kvmem_engine_create(const kvmem_engine_params *pp, kvmem_engine **out) {
     const kvmem_engine_params &p = *pp;
     if (p.n_layers == 0 || p.block_tokens == 0 || p.block_tokens > 128 || p.n_head_kv == 0 ||
         p.n_head % p.n_head_kv != 0 || (p.head_dim != 128 && p.head_dim != 256) ||
-        p.budget_blocks == 0 || !kvmem_hip_quant_ok(p.type_k) || !kvmem_hip_quant_ok(p.type_v)) {
+        p.budget_blocks == 0 || !kvmem_hip_quant_ok(p.type_k) || !kvmem_hip_quant_ok(p.type_v) ||
+        (p.scorer != KVMEM_SCORER_TOKEN_MAX && p.scorer != KVMEM_SCORER_MEAN_K)) {
         return KVMEM_HIP_ERR_INVALID;
     }
     const uint32_t n_slots = p.budget_blocks + p.reserve_blocks;
@@ -401,6 +404,9 @@ void kvmem_engine_destroy(kvmem_engine *e) {
     }
     if (e->d_ksum) {
         (void) hipFree(e->d_ksum);
+    }
+    if (e->d_qsum) {
+        (void) hipFree(e->d_qsum);
     }
     if (e->d_mt) {
         (void) hipFree(e->d_mt);
@@ -648,6 +654,56 @@ int select_topk(kvmem_engine *e, const std::vector<uint32_t> &mand, uint32_t *se
     return KVMEM_HIP_OK;
 }
 
+// Mean-K cosine scores of every block into d_scores.  The per-block key
+// sums are produced on the device for the blocks written since the last
+// call (a partial tail block is summed again once it grows).
+int meank_scores(kvmem_engine *e, const float *q_sum, const uint32_t *q_count) {
+    const uint32_t n = e->rt.store().block_count();
+    if (e->meank_cap != e->hist_capacity) {
+        if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
+            return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "mean-K scorer");
+        }
+        if (e->d_ksum) (void) hipFree(e->d_ksum);
+        if (e->d_mt) (void) hipFree(e->d_mt);
+        e->d_ksum = nullptr;
+        e->d_mt = nullptr;
+        const size_t lc = static_cast<size_t>(e->p.n_layers) * e->hist_capacity;
+        if (hipMalloc(&e->d_ksum, sizeof(float) * lc * e->n_embd_k) != hipSuccess ||
+            hipMalloc(&e->d_mt, sizeof(uint32_t) * lc) != hipSuccess) {
+            e->meank_cap = 0;
+            return e->fail(KVMEM_HIP_ERR_NOMEM, "mean-K scorer: key sums");
+        }
+        e->meank_cap = e->hist_capacity;
+        e->meank_valid = 0;
+    }
+    const kvmem_hip_history h = e->device_history();
+    if (e->meank_valid < n) {
+        std::vector<uint32_t> ids;
+        for (uint32_t b = e->meank_valid; b < n; ++b) ids.push_back(b);
+        const int rc = kvmem_hip_meank_sums(e->ctx, &h, ids.data(), static_cast<uint32_t>(ids.size()),
+                                            e->d_ksum, e->d_mt);
+        if (rc != KVMEM_HIP_OK) {
+            return e->fail_ctx(rc, "mean-K key sums");
+        }
+        const bool tail_partial = e->rt.store().blocks().back().n_tokens < e->p.block_tokens;
+        e->meank_valid = tail_partial ? n - 1 : n;
+    }
+    kvmem_hip_meank_args a{};
+    a.q_sum = q_sum;
+    a.q_count = q_count;
+    a.k_sum = e->d_ksum;
+    a.mean_tokens = e->d_mt;
+    a.n_layers = e->p.n_layers;
+    a.n_blocks = n;
+    a.capacity_blocks = e->hist_capacity;
+    a.n_head = e->p.n_head;
+    a.n_head_kv = e->p.n_head_kv;
+    a.head_dim = e->p.head_dim;
+    a.scores = e->d_scores;
+    const int rc = kvmem_hip_score_meank(e->ctx, &a);
+    return rc == KVMEM_HIP_OK ? rc : e->fail_ctx(rc, "mean-K score");
+}
+
 }  // namespace
 
 extern "C" {
@@ -675,7 +731,25 @@ int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_
         return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: score buffer");
     }
     std::vector<uint32_t> mand(mandatory, mandatory + n_mandatory);
-    if (!e->rt.store().charge_topk(mand).all_fit) {
+    if (!e->rt.store().charge_topk(mand).all_fit && e->p.scorer == KVMEM_SCORER_MEAN_K) {
+        // the reference's scorer over the sum of the query rows
+        const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
+        if (!e->d_qsum &&
+            hipMalloc(&e->d_qsum, sizeof(float) * e->p.n_layers * n_embd_q) != hipSuccess) {
+            e->d_qsum = nullptr;
+            return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: query sums");
+        }
+        int rc = kvmem_hip_q_accumulate(e->ctx, q, q_type, e->p.n_layers, n_q_tokens, n_embd_q,
+                                        nullptr, 0, 1, e->d_qsum);
+        if (rc != KVMEM_HIP_OK) {
+            return e->fail_ctx(rc, "preview query sums");
+        }
+        const std::vector<uint32_t> q_count(e->p.n_layers, n_q_tokens);
+        rc = meank_scores(e, e->d_qsum, q_count.data());
+        if (rc != KVMEM_HIP_OK) {
+            return rc;
+        }
+    } else if (!e->rt.store().charge_topk(mand).all_fit) {
         const kvmem_hip_history h = e->device_history();
         kvmem_hip_score_args a{};
         a.q = q;
@@ -719,52 +793,9 @@ int kvmem_engine_preview_meank(kvmem_engine *e, const float *q_sum, const uint32
     }
     std::vector<uint32_t> mand(mandatory, mandatory + n_mandatory);
     if (!e->rt.store().charge_topk(mand).all_fit) {
-        // key sums for the blocks written since the last preview
-        if (e->meank_cap != e->hist_capacity) {
-            if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
-                return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "preview_meank");
-            }
-            if (e->d_ksum) (void) hipFree(e->d_ksum);
-            if (e->d_mt) (void) hipFree(e->d_mt);
-            e->d_ksum = nullptr;
-            e->d_mt = nullptr;
-            const size_t lc = static_cast<size_t>(e->p.n_layers) * e->hist_capacity;
-            if (hipMalloc(&e->d_ksum, sizeof(float) * lc * e->n_embd_k) != hipSuccess ||
-                hipMalloc(&e->d_mt, sizeof(uint32_t) * lc) != hipSuccess) {
-                e->meank_cap = 0;
-                return e->fail(KVMEM_HIP_ERR_NOMEM, "preview_meank: key sums");
-            }
-            e->meank_cap = e->hist_capacity;
-            e->meank_valid = 0;
-        }
-        const kvmem_hip_history h = e->device_history();
-        if (e->meank_valid < n) {
-            std::vector<uint32_t> ids;
-            for (uint32_t b = e->meank_valid; b < n; ++b) ids.push_back(b);
-            const int rc = kvmem_hip_meank_sums(e->ctx, &h, ids.data(), static_cast<uint32_t>(ids.size()),
-                                                e->d_ksum, e->d_mt);
-            if (rc != KVMEM_HIP_OK) {
-                return e->fail_ctx(rc, "preview_meank sums");
-            }
-            // a partial tail is summed again once it grows
-            const bool tail_partial = e->rt.store().blocks().back().n_tokens < e->p.block_tokens;
-            e->meank_valid = tail_partial ? n - 1 : n;
-        }
-        kvmem_hip_meank_args a{};
-        a.q_sum = q_sum;
-        a.q_count = q_count;
-        a.k_sum = e->d_ksum;
-        a.mean_tokens = e->d_mt;
-        a.n_layers = e->p.n_layers;
-        a.n_blocks = n;
-        a.capacity_blocks = e->hist_capacity;
-        a.n_head = e->p.n_head;
-        a.n_head_kv = e->p.n_head_kv;
-        a.head_dim = e->p.head_dim;
-        a.scores = e->d_scores;
-        const int rc = kvmem_hip_score_meank(e->ctx, &a);
+        const int rc = meank_scores(e, q_sum, q_count);
         if (rc != KVMEM_HIP_OK) {
-            return e->fail_ctx(rc, "preview_meank score");
+            return rc;
         }
     }
     return select_topk(e, mand, sel, n_sel);

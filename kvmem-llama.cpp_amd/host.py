@@ -34,7 +34,7 @@ class EngineParams(C.Structure):
                 ("reserve_blocks", C.c_uint32), ("sink_blocks", C.c_uint32),
                 ("recent_blocks", C.c_uint32), ("type_k", C.c_int32), ("type_v", C.c_int32),
                 ("tie_lower_index", C.c_int32), ("layer_reduce", C.c_int32),
-                ("canonical_layout", C.c_int32)]
+                ("canonical_layout", C.c_int32), ("scorer", C.c_int32)]
 
 
 _bound = set()

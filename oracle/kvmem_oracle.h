@@ -30,6 +30,9 @@
  *   ko_score_meank                : an independent float64 numpy restatement,
  *                                   closed forms (parallel / orthogonal /
  *                                   scaled directions, GQA head sums).
+ *   ko_q_accumulate               : exact integer sums, an order-sensitive
+ *                                   cancellation sequence only the token-order
+ *                                   fp32 sum reproduces, float64 error bound.
  */
 #ifndef KVMEM_ORACLE_H
 #define KVMEM_ORACLE_H
@@ -131,6 +134,12 @@ void ko_mean_k(const float *k_sum, uint32_t mean_tokens, uint32_t n_embd, float 
 void ko_score_meank(const float *q_sum, const uint32_t *q_count, const float *k_sum,
                     const uint32_t *mean_tokens, uint32_t L, uint32_t B, uint32_t Hq,
                     uint32_t Hkv, uint32_t D, double *scores);
+
+/* The reference's query harvest (llama-memory-kvmem.cpp:2164-2172):
+ * q [L][T][E] f32; q_sum[l] (+)= q[l][tokens[i]] for i < n_list in order
+ * (tokens NULL = 0..n_list-1); reset != 0 starts from zeros. */
+void ko_q_accumulate(const float *q, uint32_t L, uint32_t T, uint32_t E, const uint32_t *tokens,
+                     uint32_t n_list, int reset, float *q_sum);
 
 /* Number of OpenMP threads the oracle uses (for the baseline's core count). */
 int ko_max_threads(void);

@@ -70,6 +70,8 @@ def lib() -> C.CDLL:
     L.ko_mean_k.argtypes = [f32p, u32, u32, f32p]
     L.ko_score_meank.restype = None
     L.ko_score_meank.argtypes = [f32p, u32p, f32p, u32p, u32, u32, u32, u32, u32, f64p]
+    L.ko_q_accumulate.restype = None
+    L.ko_q_accumulate.argtypes = [f32p, u32, u32, u32, C.c_void_p, u32, C.c_int, f32p]
     L.ko_max_threads.restype = C.c_int
     L.ko_max_threads.argtypes = []
     _lib = L
@@ -207,6 +209,23 @@ def score_meank(q_sum: np.ndarray, q_count, k_sum: np.ndarray, mean_tokens: np.n
     L, B = mt.shape
     out = np.zeros(B, dtype=np.float64)
     lib().ko_score_meank(q_sum, qc, k_sum, mt, L, B, Hq, Hkv, D, out)
+    return out
+
+
+def q_accumulate(q: np.ndarray, tokens=None, q_sum: np.ndarray | None = None) -> np.ndarray:
+    """q [L, T, E] (f32 values; widen bf16/f16 first) -> q_sum [L, E] f32:
+    the listed tokens added in order onto q_sum (zeros when None)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    L, T, E = q.shape
+    reset = q_sum is None
+    out = np.zeros((L, E), np.float32) if reset else np.array(q_sum, dtype=np.float32, copy=True)
+    if tokens is None:
+        tk, n = None, T
+    else:
+        tk = np.ascontiguousarray(tokens, dtype=np.uint32)
+        n = tk.size
+    lib().ko_q_accumulate(q, L, T, E, tk.ctypes.data if tk is not None and n else None, n,
+                          int(reset), out)
     return out
 
 

@@ -105,3 +105,26 @@ void ko_score_meank(const float *q_sum, const uint32_t *q_count, const float *k_
         scores[b] = nlay ? acc / nlay : 0.0;
     }
 }
+
+/* The reference's query harvest into q_sum_ (src/adapter/llama-memory-
+ * kvmem.cpp:2164-2172 and :2206-2219): per layer, every listed token's row
+ * (already widened to f32) is added element by element onto q_sum in list
+ * order.  reset != 0 starts from zeros (q_sum_ assigned 0.0f). */
+void ko_q_accumulate(const float *q, uint32_t L, uint32_t T, uint32_t E, const uint32_t *tokens,
+                     uint32_t n_list, int reset, float *q_sum) {
+    for (uint32_t l = 0; l < L; ++l) {
+        float *dst = q_sum + (size_t) l * E;
+        if (reset) {
+            for (uint32_t e = 0; e < E; ++e) {
+                dst[e] = 0.0f;
+            }
+        }
+        for (uint32_t i = 0; i < n_list; ++i) {
+            const uint32_t t = tokens ? tokens[i] : i;
+            const float *src = q + ((size_t) l * T + t) * E;
+            for (uint32_t e = 0; e < E; ++e) {
+                dst[e] += src[e];
+            }
+        }
+    }
+}

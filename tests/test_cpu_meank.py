@@ -122,3 +122,33 @@ def test_score_meank_invariances(oracle):
     assert np.allclose(oracle.score_meank(q_sum * 4, [12, 12], k_sum, mt, Hq, Hkv, D), base, atol=1e-6)
     perm = q_sum.reshape(L, Hq, D)[:, [2, 0, 1, 5, 3, 4]].reshape(L, Hq * D).copy()
     assert np.allclose(oracle.score_meank(perm, [3, 3], k_sum, mt, Hq, Hkv, D), base, atol=1e-6)
+
+
+def test_q_accumulate_exact_integers(oracle):
+    rng = np.random.default_rng(8)
+    q = rng.integers(-1000, 1000, (3, 40, 96)).astype(np.float32)
+    got = oracle.q_accumulate(q)
+    assert np.array_equal(got, q.astype(np.int64).sum(axis=1).astype(np.float32))
+    sub = [5, 0, 39, 7]
+    assert np.array_equal(oracle.q_accumulate(q, sub),
+                          q[:, sub].astype(np.int64).sum(axis=1).astype(np.float32))
+
+
+def test_q_accumulate_token_order(oracle):
+    # fp32: (1e8 + 5) rounds to 1e8 + 8, so the token-order sum is 8, while
+    # pairing 1e8 with -1e8 first gives 5: only the reference's sequential
+    # order reproduces 8, and the list order is honoured
+    q = np.array([1e8, 5.0, -1e8], np.float32).reshape(1, 3, 1)
+    assert oracle.q_accumulate(q)[0, 0] == 8.0
+    assert oracle.q_accumulate(q, [0, 2, 1])[0, 0] == 5.0
+
+
+def test_q_accumulate_continues_and_bounds(oracle):
+    rng = np.random.default_rng(9)
+    q = (rng.standard_normal((2, 64, 256)) * 3).astype(np.float32)
+    first = oracle.q_accumulate(q, list(range(20)))
+    both = oracle.q_accumulate(q, list(range(20, 64)), q_sum=first)
+    assert np.array_equal(both, oracle.q_accumulate(q))
+    exact = q.astype(np.float64).sum(axis=1)
+    bound = 64 * np.finfo(np.float32).eps * np.abs(q).astype(np.float64).sum(axis=1)
+    assert np.all(np.abs(both - exact) <= bound)

@@ -130,3 +130,49 @@ def test_engine_meank_preview_apply(oracle):
                                                   recent=1)
             eng.apply(sel)
             eng.append_tokens(50)           # the partial tail grows: its sums are redone
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_q_accumulate_bit_exact(ctx, oracle, dtype):
+    announce(f"query sums {dtype}: 3 layers x 40 tokens x 6144, token list, continue")
+    L, Tq, E = 3, 40, HQ * D
+    g = torch.Generator(device="cpu").manual_seed(31)
+    qf = torch.randn((L, Tq, E), generator=g) * 4
+    qf[0, :3, 0] = torch.tensor([1e4, 3.0, -1e4])  # order-sensitive in fp32 for narrow types too
+    tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[dtype]
+    code = {"f32": kv.TYPE_F32, "f16": kv.TYPE_F16, "bf16": kv.TYPE_BF16}[dtype]
+    q = qf.to(tdt).cuda()
+    wide = q.float().cpu().numpy()
+    qs = torch.full((L, E), float("nan"), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.q_accumulate(q.data_ptr(), code, L, Tq, E, qs.data_ptr())
+    ctx.sync()
+    want = oracle.q_accumulate(wide)
+    assert np.array_equal(qs.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    sub = [7, 0, 33, 2]
+    ctx.q_accumulate(q.data_ptr(), code, L, Tq, E, qs.data_ptr(), tokens=sub, reset=False)
+    ctx.sync()
+    want = oracle.q_accumulate(wide, sub, q_sum=want)
+    assert np.array_equal(qs.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_engine_scorer_meank_from_query_rows(oracle):
+    """scorer = mean-K: preview takes the per-token query itself; the query
+    sums, key sums and scores agree with the oracle chain."""
+    announce("engine scorer=mean-K from query rows: 3 layers x 40 blocks")
+    L, nb, Tq = 3, 40, 16
+    k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=nb, Tq=Tq, seed=24, with_v=True)
+    with host.Engine(n_layers=L, block_tokens=T, n_head=HQ, n_head_kv=HKV, head_dim=D,
+                     budget_blocks=8, reserve_blocks=2, scorer=1) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), nb, nb * T)
+        sel = eng.preview(q.data_ptr(), Tq)
+        q_sum = oracle.q_accumulate(q.float().cpu().numpy().reshape(L, Tq, HQ * D))
+        kb = workloads.to_bits(torch, k)
+        sums = np.stack([[oracle.meank_sum_f16(kb[l, b].reshape(T, E)) for b in range(nb)]
+                         for l in range(L)])
+        want = oracle.score_meank(q_sum, [Tq] * L, sums, np.full((L, nb), T, np.uint32), HQ, HKV, D)
+        got = np.array(eng.scores(), dtype=np.float64)
+        assert np.max(np.abs(got - want)) <= 1e-5
+        assert sel.blocks == oracle.pick_topk(got.astype(np.float32).astype(np.float64), 8, sink=1)
+        stats = eng.apply(sel)
+        assert stats["n_stage_in"] == len(sel.blocks)
