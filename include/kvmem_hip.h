@@ -146,11 +146,46 @@ typedef struct kvmem_hip_history {
     uint32_t capacity_blocks;   /* blocks per layer in memory (0 = n_blocks) */
 } kvmem_hip_history;
 
+/* How the cache expects its rows: the transform the stage-in applies to the
+ * F16 history rows before it quantizes them, in the order of the reference's
+ * raw-K stage-in (kvmem_stagein_flush for K items, llama-kvmem-stagein.cu:
+ * 704-740: widen -> NeoX RoPE -> Walsh-Hadamard -> quantize):
+ *   RoPE (K only; rope_neox_kernel stagein.cu:159-178, kvmem/src/host/
+ *   rope.cpp:8-45): in every head, for i < n_rot/2, with a = (float)p *
+ *   theta[i] at the token's position p,
+ *       x'[i]          = x[i]*cos(a) - x[i+n_rot/2]*sin(a)
+ *       x'[i+n_rot/2]  = x[i]*sin(a) + x[i+n_rot/2]*cos(a)
+ *   (separate IEEE products and sums; cos/sin of the fp32 angle are the
+ *   library's own, within one rounding of the exact values); elements at
+ *   n_rot and beyond are unchanged.
+ *   attn_rot (llama-kvmem-quant.h:22-94; fwht_kernel stagein.cu:104-130):
+ *   every run of `width` elements of a head becomes H x, H the orthonormal
+ *   Walsh-Hadamard matrix: the run is first scaled by 1/sqrtf(width), then
+ *   butterflies (a+b, a-b) of span 1, 2, 4, ... width/2.  The reference
+ *   uses width = the largest power of two dividing head_dim (>= 64) for K
+ *   (kvmem_hadamard_nrot_k) and 64 for V, on quantized caches.
+ * Limits: head_dim 64, 128, 256 or 512 dividing n_embd; n_rot a multiple of
+ * 16 up to head_dim; widths 64..512 dividing head_dim; a workgroup chunk of
+ * 512 groups may span at most 4096 (row, rotary pair) entries, i.e.
+ * (16384 / n_embd + 1) * n_rot / 2 <= 4096. */
+typedef struct kvmem_hip_transform {
+    uint32_t head_dim;
+    uint32_t n_rot;           /* K rotary dims (0 = no RoPE) */
+    const float *theta;       /* host [n_rot/2] pair frequencies (rope.cpp:
+                                 freq_base^(-2i/n_rot) * freq_scale) */
+    uint32_t hadamard_k;      /* K rotation width (0 = none) */
+    uint32_t hadamard_v;      /* V rotation width (0 = none) */
+    const int32_t *pos0;      /* host, one per staged block of a call: the
+                                 position of its token 0 (NULL = block_id *
+                                 block_tokens, the block's original start) */
+} kvmem_hip_transform;
+
 /* Slot pool: per layer one K and one V tensor of n_slots*block_tokens rows
  * of kvmem_hip_row_size(type, n_embd) bytes (the cache tensors of
  * llama-memory-kvmem.cpp:2736-2742; cell = slot*block_tokens + t,
  * llama-kvmem-batch.cpp:48).  k_layers/v_layers are host arrays of device
- * pointers, 16-byte aligned.  v_layers may be NULL. */
+ * pointers, 16-byte aligned.  v_layers may be NULL.  xf (may be NULL: rows
+ * stored as given) is applied by the block stage-in calls. */
 typedef struct kvmem_hip_pool {
     uint32_t n_layers;
     uint32_t n_slots;
@@ -161,6 +196,7 @@ typedef struct kvmem_hip_pool {
     int32_t type_v;
     void *const *k_layers;
     void *const *v_layers;
+    const kvmem_hip_transform *xf;
 } kvmem_hip_pool;
 
 /* Quantize blocks block_ids[i] of a device-resident history into pool slot

@@ -73,11 +73,17 @@ class HostHistory(C.Structure):
                 ("n_embd_v", C.c_uint32), ("last_block_tokens", C.c_uint32)]
 
 
+class Transform(C.Structure):
+    _fields_ = [("head_dim", C.c_uint32), ("n_rot", C.c_uint32), ("theta", C.POINTER(C.c_float)),
+                ("hadamard_k", C.c_uint32), ("hadamard_v", C.c_uint32),
+                ("pos0", C.POINTER(C.c_int32))]
+
+
 class Pool(C.Structure):
     _fields_ = [("n_layers", C.c_uint32), ("n_slots", C.c_uint32), ("block_tokens", C.c_uint32),
                 ("n_embd_k", C.c_uint32), ("n_embd_v", C.c_uint32), ("type_k", C.c_int32),
                 ("type_v", C.c_int32), ("k_layers", C.POINTER(C.c_void_p)),
-                ("v_layers", C.POINTER(C.c_void_p))]
+                ("v_layers", C.POINTER(C.c_void_p)), ("xf", C.POINTER(Transform))]
 
 
 class ScoreArgs(C.Structure):
@@ -238,13 +244,26 @@ class Context:
                        n_embd_k, n_embd_v, last_block_tokens, capacity_blocks)
 
     def make_pool(self, n_layers, n_slots, block_tokens, n_embd_k, n_embd_v, type_k, type_v,
-                  k_ptrs: Sequence[int], v_ptrs: Sequence[int] | None) -> Pool:
+                  k_ptrs: Sequence[int], v_ptrs: Sequence[int] | None,
+                  xf: "Transform | None" = None) -> Pool:
         ka = _ptr_array(k_ptrs)
         va = _ptr_array(v_ptrs) if v_ptrs is not None else None
-        self._keep.extend([ka, va])
+        self._keep.extend([ka, va, xf])
         return Pool(n_layers, n_slots, block_tokens, n_embd_k, n_embd_v, type_k, type_v,
                     C.cast(ka, C.POINTER(C.c_void_p)),
-                    C.cast(va, C.POINTER(C.c_void_p)) if va is not None else None)
+                    C.cast(va, C.POINTER(C.c_void_p)) if va is not None else None,
+                    C.pointer(xf) if xf is not None else None)
+
+    def make_transform(self, head_dim: int, n_rot: int = 0, theta=None, hadamard_k: int = 0,
+                       hadamard_v: int = 0, pos0=None) -> Transform:
+        """The cache's row transform (RoPE frequencies theta[n_rot/2], optional
+        per-block positions of token 0 for the next stage-in call)."""
+        vals = [float(t) for t in theta][: n_rot // 2] if theta is not None else []
+        th = (C.c_float * max(1, n_rot // 2))(*vals)
+        ps = (C.c_int32 * len(pos0))(*[int(p) for p in pos0]) if pos0 is not None else None
+        self._keep.extend([th, ps])
+        return Transform(head_dim, n_rot, C.cast(th, C.POINTER(C.c_float)) if theta is not None else None,
+                         hadamard_k, hadamard_v, C.cast(ps, C.POINTER(C.c_int32)) if ps is not None else None)
 
     def stagein_blocks(self, hist: History, pool: Pool, block_ids, slots) -> None:
         ids, n = _u32_array(block_ids)

@@ -24,6 +24,15 @@
 // where vmax is the first element of largest magnitude.  The products and
 // sums are separate IEEE operations (no FMA contraction in this file),
 // divisions are correctly rounded (HIP default), d is stored as f16 RNE.
+//
+// With a pool transform the rows are widened to fp32, RoPE'd (K) and
+// Hadamard-rotated before they are quantized, as the reference's raw-K
+// stage-in does (llama-kvmem-stagein.cu:704-740).  A head never straddles a
+// 16-group round (head_dim divides 512), so a rotary pair and a butterfly
+// partner are always lanes of the same wave: RoPE pairs are exchanged with
+// one lane shuffle, butterfly spans 1, 2, 4 stay inside a lane and spans
+// 8 .. width/2 exchange with lane ^ span/8.  The cos/sin of every (row,
+// rotary pair) of a chunk are computed once per workgroup into LDS.
 #include "kvmem_internal.hpp"
 
 #include <algorithm>
@@ -37,6 +46,7 @@ namespace kvmem_hip {
 constexpr int kRounds = 8;                     // 16-group rounds per wave
 constexpr int kWaveGroups = 16 * kRounds;      // groups per wave (128)
 constexpr int kChunkGroups = 4 * kWaveGroups;  // groups per workgroup (512)
+constexpr int kTabMax = 4096;                  // (row, rotary pair) entries per chunk
 
 template <int TYPE> struct Fmt;
 template <> struct Fmt<KVMEM_TYPE_Q8_0> { static constexpr int GB = 34; };
@@ -52,6 +62,7 @@ struct Chunk {
     uint32_t ng;          // groups in this chunk (<= kChunkGroups)
     uint32_t gpr;         // groups per row
     uint32_t src_stride;  // bytes between F16 rows
+    int32_t pos0;         // position of the operation's row 0 (RoPE)
 };
 
 // Source 1: an explicit list of operations.  chunk0 is the index of the
@@ -88,18 +99,25 @@ struct OpListSource {
         out.ng = min(static_cast<uint32_t>(kChunkGroups), op.n_groups - out.g0);
         out.gpr = op.gpr;
         out.src_stride = op.src_stride;
+        out.pos0 = 0;
         return true;
     }
+    // no row transform on this source
+    static constexpr uint32_t head_dim = 32, n_rot = 0, hadamard = 0;
+    static constexpr float hscale = 1.0f;
+    static constexpr const float *theta = nullptr;
 };
 
 // Source 2: whole blocks of a history, for every layer.  Item i names a
-// source block (addressing index), its destination slot and its tokens.
+// source block (addressing index), its destination slot, its tokens and
+// the position of its token 0.
 //   src(item, layer) = base + block*block_stride + layer*layer_stride
 //   dst(item, layer) = layer_dst[layer] + slot*block_tokens*row_bytes
 struct BlockSource {
     const uint8_t *base;
     const uint8_t *const *layer_dst;  // device array [n_layers]
-    const uint32_t *items;            // device [n_items][3]: block, slot, n_tokens
+    const uint32_t *items;            // device [n_items][4]: block, slot, n_tokens, pos0
+    const float *theta;               // device [n_rot/2] (RoPE)
     uint64_t block_stride;
     uint64_t layer_stride;
     uint32_t n_layers;
@@ -107,14 +125,19 @@ struct BlockSource {
     uint32_t gpr;
     uint32_t row_bytes;               // output bytes per row
     uint32_t chunks_per_op;           // ceil(block_tokens*gpr / kChunkGroups)
+    uint32_t head_dim;                // transform: head width (power of two)
+    uint32_t n_rot;                   // RoPE rotary dims (0 = none)
+    uint32_t hadamard;                // Hadamard width (0 = none)
+    float hscale;                     // 1 / sqrtf(hadamard)
     __device__ bool chunk(uint32_t c, Chunk &out) const {
         const uint32_t op = c / chunks_per_op;
         const uint32_t sub = c - op * chunks_per_op;
         const uint32_t item = op / n_layers;
         const uint32_t layer = op - item * n_layers;
-        const uint32_t block = items[3 * item + 0];
-        const uint32_t slot = items[3 * item + 1];
-        const uint32_t ntok = items[3 * item + 2];
+        const uint32_t block = items[4 * item + 0];
+        const uint32_t slot = items[4 * item + 1];
+        const uint32_t ntok = items[4 * item + 2];
+        out.pos0 = static_cast<int32_t>(items[4 * item + 3]);
         const uint32_t total = ntok * gpr;
         out.g0 = sub * kChunkGroups;
         if (out.g0 >= total) {
@@ -319,10 +342,279 @@ __device__ inline void quant_quarter<KVMEM_TYPE_F16>(const uint4 &v, uint32_t q,
     }
 }
 
-// Quantize chunk `c` of `source` into its destination.  `lds` holds
-// 4 * kWaveGroups groups of the type's layout.
+// ------------------------------------------------- transformed (fp32) rows
+
+// sin and cos of an fp32 angle.  The angle is reduced by pi/2 in double
+// (Cody-Waite: k = rint(a * 2/pi), r = a - k*pi/2 with pi/2 split into two
+// doubles, one fused multiply-add each), the Taylor series of sin (to r^17)
+// and cos (to r^16) are summed by Horner's rule on |r| <= pi/4 (truncation
+// below 1e-17), and each result is rounded once to fp32.  Every step is one
+// correctly rounded IEEE operation, so a C restatement of the same steps
+// reproduces the same bits.  Angles are finite with |a| < 2^40 (a RoPE
+// angle is an int32 position times a frequency of at most one).
+__device__ inline void rope_sincos(float a, float &sn, float &cs) {
+    const double x = static_cast<double>(a);
+    const double k = __builtin_rint(x * 0x1.45f306dc9c883p-1);
+    double r = x;  // |a| < pi/4: no reduction (keeps the sign of zero)
+    if (k != 0.0) {
+        r = __builtin_fma(-k, 0x1.921fb54442d18p+0, x);
+        r = __builtin_fma(-k, 0x1.1a62633145c07p-54, r);
+    }
+    const double r2 = r * r;
+    double ps = 0x1.952c77030ad4ap-49;
+    ps = __builtin_fma(ps, r2, -0x1.ae7f3e733b81fp-41);
+    ps = __builtin_fma(ps, r2, 0x1.6124613a86d09p-33);
+    ps = __builtin_fma(ps, r2, -0x1.ae64567f544e4p-26);
+    ps = __builtin_fma(ps, r2, 0x1.71de3a556c734p-19);
+    ps = __builtin_fma(ps, r2, -0x1.a01a01a01a01ap-13);
+    ps = __builtin_fma(ps, r2, 0x1.1111111111111p-7);
+    ps = __builtin_fma(ps, r2, -0x1.5555555555555p-3);
+    double pc = 0x1.ae7f3e733b81fp-45;
+    pc = __builtin_fma(pc, r2, -0x1.93974a8c07c9dp-37);
+    pc = __builtin_fma(pc, r2, 0x1.1eed8eff8d898p-29);
+    pc = __builtin_fma(pc, r2, -0x1.27e4fb7789f5cp-22);
+    pc = __builtin_fma(pc, r2, 0x1.a01a01a01a01ap-16);
+    pc = __builtin_fma(pc, r2, -0x1.6c16c16c16c17p-10);
+    pc = __builtin_fma(pc, r2, 0x1.5555555555555p-5);
+    pc = __builtin_fma(pc, r2, -0.5);
+    const double sr = r == 0.0 ? r : __builtin_fma(r * r2, ps, r);  // sin(+-0) = +-0
+    const double cr = __builtin_fma(r2, pc, 1.0);
+    const int quadrant = static_cast<int>(k - 4.0 * __builtin_floor(k * 0.25));  // k mod 4, exact
+    const double sv = (quadrant & 1) ? cr : sr;
+    const double cv = (quadrant & 1) ? sr : cr;
+    sn = static_cast<float>((quadrant & 2) ? -sv : sv);
+    cs = static_cast<float>(((quadrant + 1) & 2) ? -cv : cv);
+}
+
+// Walsh-Hadamard rotation of runs of `width` elements, in the order of the
+// reference's fwht_kernel: scale every element, then butterflies of span
+// 1, 2, 4 (inside the lane) and 8 .. width/2 (partner lane ^ span/8; the
+// lane with that bit set keeps partner - own, the other own + partner).
+__device__ inline void fwht_lanes(float x[8], uint32_t width, float scale, uint32_t lane) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        x[i] = x[i] * scale;
+    }
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2 * h) {
+#pragma unroll
+            for (int j = 0; j < h; ++j) {
+                const float a = x[i + j];
+                const float b = x[i + j + h];
+                x[i + j] = a + b;
+                x[i + j + h] = a - b;
+            }
+        }
+    }
+    for (uint32_t m = 1; m < width / 8u; m <<= 1) {
+        const bool upper = (lane & m) != 0u;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float p = __shfl_xor(x[i], static_cast<int>(m), 64);
+            x[i] = upper ? p - x[i] : x[i] + p;
+        }
+    }
+}
+
+// vmax of ggml's q4_0/q5_0 over fp32 values: the first element of largest
+// magnitude (NaNs never win, as in the reference's strict `amax < |v|`);
+// an all-zero group keeps the initial vmax = +0.
+__device__ inline float quad_vmax_f(const float x[8], uint32_t q) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        amax = fmaxf(amax, fabsf(x[i]));
+    }
+    amax = fmaxf(amax, __uint_as_float(quad_xor1(__float_as_uint(amax))));
+    amax = fmaxf(amax, __uint_as_float(quad_xor2(__float_as_uint(amax))));
+    uint32_t key = 0xffffffffu;  // (element << 1) | sign of the first maximum
+#pragma unroll
+    for (int i = 7; i >= 0; --i) {
+        if (fabsf(x[i]) == amax) {
+            key = ((8u * q + i) << 1) | (__float_as_uint(x[i]) >> 31);
+        }
+    }
+    uint32_t o = quad_xor1(key);
+    key = o < key ? o : key;
+    o = quad_xor2(key);
+    key = o < key ? o : key;
+    return amax == 0.0f ? 0.0f : ((key & 1u) ? -amax : amax);
+}
+
+template <int TYPE>
+__device__ inline void quant_quarter_f(const float x[8], uint32_t q, uint8_t *g, bool valid);
+
+template <>
+__device__ inline void quant_quarter_f<KVMEM_TYPE_Q8_0>(const float x[8], uint32_t q, uint8_t *g,
+                                                         bool valid) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        amax = fmaxf(amax, fabsf(x[i]));
+    }
+    amax = fmaxf(amax, __uint_as_float(quad_xor1(__float_as_uint(amax))));
+    amax = fmaxf(amax, __uint_as_float(quad_xor2(__float_as_uint(amax))));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int c = static_cast<int>(roundf(x[i] * id));
+        w[i >> 2] |= (static_cast<uint32_t>(c) & 0xffu) << (8 * (i & 3));
+    }
+    if (valid) {
+        if (q == 0) {
+            store_u16(g, float_to_half_bits(d));
+        }
+        store_8bytes(g + 2 + 8 * q, w[0], w[1]);
+    }
+}
+
+template <int TOP>
+__device__ inline void trunc_codes_f(const float x[8], float id, float bias, uint32_t &w0,
+                                     uint32_t &w1) {
+    w0 = 0u;
+    w1 = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        w0 |= trunc_code<TOP>(x[i], id, bias) << (8 * i);
+        w1 |= trunc_code<TOP>(x[i + 4], id, bias) << (8 * i);
+    }
+}
+
+template <>
+__device__ inline void quant_quarter_f<KVMEM_TYPE_Q4_0>(const float x[8], uint32_t q, uint8_t *g,
+                                                         bool valid) {
+    const float vmax = quad_vmax_f(x, q);
+    const float d = vmax * -0.125f;        // == vmax / -8 (exact scaling)
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t w0, w1;
+    trunc_codes_f<15>(x, id, 8.5f, w0, w1);
+    const uint32_t p0 = quad_xor2(w0);
+    const uint32_t p1 = quad_xor2(w1);
+    if (valid) {
+        if (q == 0) {
+            store_u16(g, float_to_half_bits(d));
+        }
+        if (q < 2) {
+            store_8bytes(g + 2 + 8 * q, w0 | (p0 << 4), w1 | (p1 << 4));
+        }
+    }
+}
+
+template <>
+__device__ inline void quant_quarter_f<KVMEM_TYPE_Q5_0>(const float x[8], uint32_t q, uint8_t *g,
+                                                         bool valid) {
+    const float vmax = quad_vmax_f(x, q);
+    const float d = vmax * -0.0625f;       // == vmax / -16 (exact scaling)
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t w0, w1;
+    trunc_codes_f<31>(x, id, 16.5f, w0, w1);
+    uint32_t qh = (bit4_of_bytes(w0) | (bit4_of_bytes(w1) << 4)) << (8 * q);
+    qh |= quad_xor1(qh);
+    qh |= quad_xor2(qh);
+    w0 &= 0x0f0f0f0fu;
+    w1 &= 0x0f0f0f0fu;
+    const uint32_t p0 = quad_xor2(w0);
+    const uint32_t p1 = quad_xor2(w1);
+    if (valid) {
+        if (q == 0) {
+            store_u16(g, float_to_half_bits(d));
+            store_u16(g + 2, qh & 0xffffu);
+            store_u16(g + 4, qh >> 16);
+        }
+        if (q < 2) {
+            store_8bytes(g + 6 + 8 * q, w0 | (p0 << 4), w1 | (p1 << 4));
+        }
+    }
+}
+
+template <>
+__device__ inline void quant_quarter_f<KVMEM_TYPE_F16>(const float x[8], uint32_t q, uint8_t *g,
+                                                        bool valid) {
+    if (valid) {
+        uint4 v;
+        v.x = float_to_half_bits(x[0]) | (float_to_half_bits(x[1]) << 16);
+        v.y = float_to_half_bits(x[2]) | (float_to_half_bits(x[3]) << 16);
+        v.z = float_to_half_bits(x[4]) | (float_to_half_bits(x[5]) << 16);
+        v.w = float_to_half_bits(x[6]) | (float_to_half_bits(x[7]) << 16);
+        *reinterpret_cast<uint4 *>(g + 16 * q) = v;
+    }
+}
+
+// The transformed rounds of a chunk: cos/sin table of the chunk's rows in
+// `tab` (built by the whole workgroup), then per round widen, RoPE,
+// rotate and quantize into the wave's LDS region.
 template <int TYPE, class Source>
-__device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8_t *lds) {
+__device__ inline void transform_rounds(const Source &s, const Chunk &c, const uint4 v[kRounds],
+                                        uint8_t *wl, float2 *tab, uint32_t wg0, uint32_t lane) {
+    constexpr int GB = Fmt<TYPE>::GB;
+    const uint32_t quad = lane >> 2;
+    const uint32_t q = lane & 3u;
+    const uint32_t half = s.n_rot / 2u;
+    const uint32_t row0 = c.g0 / c.gpr;
+    if (half != 0u) {
+        const uint32_t rows = (c.g0 + c.ng - 1u) / c.gpr - row0 + 1u;
+        for (uint32_t i = threadIdx.x; i < rows * half; i += blockDim.x) {
+            const uint32_t r = i / half;
+            const uint32_t j = i - r * half;
+            const float pos = static_cast<float>(c.pos0 + static_cast<int32_t>(row0 + r));
+            float sn, cs;
+            rope_sincos(pos * s.theta[j], sn, cs);
+            tab[i] = make_float2(cs, sn);
+        }
+        __syncthreads();
+    }
+    const uint32_t pair_lanes = half / 8u;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+        const uint32_t gl = wg0 + 16u * r + quad;
+        const bool valid = gl < c.ng;
+        const uint32_t g = c.g0 + gl;
+        const uint32_t row = g / c.gpr;
+        const uint32_t col = g - row * c.gpr;
+        const uint32_t d0 = (col * 32u + 8u * q) & (s.head_dim - 1u);  // first element in the head
+        uint32_t h[8];
+        unpack8(v[r], h);
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            x[i] = half_bits_to_float(h[i]);
+        }
+        if (half != 0u) {
+            const bool rot = d0 < s.n_rot;
+            const bool first = d0 < half;
+            const int src = static_cast<int>(rot ? (first ? lane + pair_lanes : lane - pair_lanes) : lane);
+            float p[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                p[i] = __shfl(x[i], src, 64);
+            }
+            if (rot && valid) {
+                const float2 *t = tab + (row - row0) * half + (first ? d0 : d0 - half);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float2 cs = t[i];
+                    // first half: x0 = own, x1 = partner; second half: x0 = partner, x1 = own
+                    x[i] = first ? x[i] * cs.x - p[i] * cs.y : p[i] * cs.y + x[i] * cs.x;
+                }
+            }
+        }
+        if (s.hadamard != 0u) {
+            fwht_lanes(x, s.hadamard, s.hscale, lane);
+        }
+        quant_quarter_f<TYPE>(x, q, wl + (16u * r + quad) * GB, valid);
+    }
+}
+
+// Quantize chunk `c` of `source` into its destination.  `lds` holds
+// 4 * kWaveGroups groups of the type's layout; with XF the rows go through
+// the source's transform and `tab` holds kTabMax cos/sin pairs.
+template <int TYPE, class Source, bool XF>
+__device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8_t *lds,
+                                   float2 *tab) {
     constexpr int GB = Fmt<TYPE>::GB;
     Chunk c;
     if (!source.chunk(c_index, c)) {
@@ -349,10 +641,14 @@ __device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8
             v[r] = load_stream16(p);
         }
     }
+    if constexpr (XF) {
+        transform_rounds<TYPE>(source, c, v, wl, tab, wg0, lane);
+    } else {
 #pragma unroll
-    for (int r = 0; r < kRounds; ++r) {
-        const uint32_t gl = wg0 + 16u * r + quad;
-        quant_quarter<TYPE>(v[r], q, wl + (16u * r + quad) * GB, gl < c.ng);
+        for (int r = 0; r < kRounds; ++r) {
+            const uint32_t gl = wg0 + 16u * r + quad;
+            quant_quarter<TYPE>(v[r], q, wl + (16u * r + quad) * GB, gl < c.ng);
+        }
     }
     // each wave reads back only the bytes it wrote itself
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -373,43 +669,42 @@ __device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8
     }
 }
 
-template <int TYPE, class Source>
+template <int TYPE, class Source, bool XF>
 __global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kWaveGroups * Fmt<TYPE>::GB];
-    quant_chunk<TYPE>(source, blockIdx.x, lds);
+    __shared__ float2 tab[XF ? kTabMax : 1];
+    quant_chunk<TYPE, Source, XF>(source, blockIdx.x, lds, tab);
 }
 
 // K and V of a block job in one launch: workgroups [0, n_k) take K chunks,
 // the rest V chunks (the branch is uniform per workgroup).
-template <int TK, int TV>
+template <int TK, int TV, bool XF>
 __global__ __launch_bounds__(256) void quant_scatter_kv_kernel(BlockSource sk, BlockSource sv,
                                                                uint32_t n_k) {
     constexpr int GB = Fmt<TK>::GB > Fmt<TV>::GB ? Fmt<TK>::GB : Fmt<TV>::GB;
     __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kWaveGroups * GB];
+    __shared__ float2 tab[XF ? kTabMax : 1];
     if (blockIdx.x < n_k) {
-        quant_chunk<TK>(sk, blockIdx.x, lds);
+        quant_chunk<TK, BlockSource, XF>(sk, blockIdx.x, lds, tab);
     } else {
-        quant_chunk<TV>(sv, blockIdx.x - n_k, lds);
+        quant_chunk<TV, BlockSource, XF>(sv, blockIdx.x - n_k, lds, tab);
     }
 }
 
-template <class Source>
-bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Source &s) {
-    if (n_chunks == 0) {
-        return true;
-    }
+template <class Source, bool XF>
+bool launch_quant_x(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Source &s) {
     switch (type) {
         case KVMEM_TYPE_Q8_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q8_0, Source><<<n_chunks, 256, 0, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_Q8_0, Source, XF><<<n_chunks, 256, 0, ctx->stream>>>(s);
             break;
         case KVMEM_TYPE_Q4_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q4_0, Source><<<n_chunks, 256, 0, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_Q4_0, Source, XF><<<n_chunks, 256, 0, ctx->stream>>>(s);
             break;
         case KVMEM_TYPE_Q5_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q5_0, Source><<<n_chunks, 256, 0, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_Q5_0, Source, XF><<<n_chunks, 256, 0, ctx->stream>>>(s);
             break;
         case KVMEM_TYPE_F16:
-            quant_scatter_kernel<KVMEM_TYPE_F16, Source><<<n_chunks, 256, 0, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_F16, Source, XF><<<n_chunks, 256, 0, ctx->stream>>>(s);
             break;
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported type");
@@ -418,21 +713,33 @@ bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Source 
     return hip_ok(ctx, hipGetLastError(), "stage-in kernel launch");
 }
 
-template <int TK>
+bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const OpListSource &s) {
+    return n_chunks == 0 || launch_quant_x<OpListSource, false>(ctx, type, n_chunks, s);
+}
+
+bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const BlockSource &s, bool xf) {
+    if (n_chunks == 0) {
+        return true;
+    }
+    return xf ? launch_quant_x<BlockSource, true>(ctx, type, n_chunks, s)
+              : launch_quant_x<BlockSource, false>(ctx, type, n_chunks, s);
+}
+
+template <int TK, bool XF>
 bool launch_kv_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, const BlockSource &sk,
                  const BlockSource &sv, uint32_t n_k) {
     switch (tv) {
         case KVMEM_TYPE_Q8_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q8_0><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q8_0, XF><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
             break;
         case KVMEM_TYPE_Q4_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q4_0><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q4_0, XF><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
             break;
         case KVMEM_TYPE_Q5_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q5_0><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q5_0, XF><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
             break;
         case KVMEM_TYPE_F16:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_F16><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_F16, XF><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
             break;
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported V type");
@@ -441,21 +748,28 @@ bool launch_kv_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, const BlockSource &s
     return hip_ok(ctx, hipGetLastError(), "stage-in K/V kernel launch");
 }
 
-bool launch_quant_kv(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_t n_v,
-                     const BlockSource &sk, const BlockSource &sv) {
+template <bool XF>
+bool launch_quant_kv_x(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_t n_v,
+                       const BlockSource &sk, const BlockSource &sv) {
     const uint32_t grid = n_k + n_v;
-    if (grid == 0) {
-        return true;
-    }
     switch (tk) {
-        case KVMEM_TYPE_Q8_0: return launch_kv_v<KVMEM_TYPE_Q8_0>(ctx, tv, grid, sk, sv, n_k);
-        case KVMEM_TYPE_Q4_0: return launch_kv_v<KVMEM_TYPE_Q4_0>(ctx, tv, grid, sk, sv, n_k);
-        case KVMEM_TYPE_Q5_0: return launch_kv_v<KVMEM_TYPE_Q5_0>(ctx, tv, grid, sk, sv, n_k);
-        case KVMEM_TYPE_F16: return launch_kv_v<KVMEM_TYPE_F16>(ctx, tv, grid, sk, sv, n_k);
+        case KVMEM_TYPE_Q8_0: return launch_kv_v<KVMEM_TYPE_Q8_0, XF>(ctx, tv, grid, sk, sv, n_k);
+        case KVMEM_TYPE_Q4_0: return launch_kv_v<KVMEM_TYPE_Q4_0, XF>(ctx, tv, grid, sk, sv, n_k);
+        case KVMEM_TYPE_Q5_0: return launch_kv_v<KVMEM_TYPE_Q5_0, XF>(ctx, tv, grid, sk, sv, n_k);
+        case KVMEM_TYPE_F16: return launch_kv_v<KVMEM_TYPE_F16, XF>(ctx, tv, grid, sk, sv, n_k);
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported K type");
             return false;
     }
+}
+
+bool launch_quant_kv(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_t n_v,
+                     const BlockSource &sk, const BlockSource &sv, bool xf) {
+    if (n_k + n_v == 0) {
+        return true;
+    }
+    return xf ? launch_quant_kv_x<true>(ctx, tk, tv, n_k, n_v, sk, sv)
+              : launch_quant_kv_x<false>(ctx, tk, tv, n_k, n_v, sk, sv);
 }
 
 static bool aligned16(const void *p) {
@@ -483,42 +797,120 @@ static int check_pool(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, uint32_t n
     return KVMEM_HIP_OK;
 }
 
+// A pool's transform, checked and resolved per kind.
+struct XfParams {
+    bool on = false;
+    uint32_t head_dim = 32;
+    uint32_t n_rot = 0;
+    uint32_t had_k = 0;
+    uint32_t had_v = 0;
+    float hscale_k = 1.0f;
+    float hscale_v = 1.0f;
+};
+
+// Rows of n_embd elements that one chunk of kChunkGroups groups can touch.
+static uint32_t chunk_rows(uint32_t n_embd) {
+    const uint32_t gpr = n_embd / 32;
+    return (kChunkGroups % gpr == 0) ? kChunkGroups / gpr : (kChunkGroups - 1) / gpr + 2;
+}
+
+static bool pow2_in(uint32_t x, uint32_t lo, uint32_t hi) {
+    return x >= lo && x <= hi && (x & (x - 1)) == 0;
+}
+
+static int resolve_xf(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, uint32_t ek, uint32_t ev,
+                      bool want_v, XfParams &out) {
+    out = XfParams{};
+    const kvmem_hip_transform *xf = pool->xf;
+    if (!xf || (xf->n_rot == 0 && xf->hadamard_k == 0 && (xf->hadamard_v == 0 || !want_v))) {
+        return KVMEM_HIP_OK;
+    }
+    const uint32_t D = xf->head_dim;
+    if (!pow2_in(D, 64, 512) || ek % D != 0 || (want_v && xf->hadamard_v && ev % D != 0)) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID,
+                    "transform: head_dim must be 64, 128, 256 or 512 and divide the row");
+    }
+    if (xf->n_rot && (xf->n_rot % 16 != 0 || xf->n_rot > D || !xf->theta)) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID,
+                    "transform: n_rot must be a multiple of 16 up to head_dim, with theta");
+    }
+    if (xf->n_rot && chunk_rows(ek) * (xf->n_rot / 2) > static_cast<uint32_t>(kTabMax)) {
+        return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "transform: rows too narrow for the RoPE table");
+    }
+    for (uint32_t w : {xf->hadamard_k, want_v ? xf->hadamard_v : 0u}) {
+        if (w && (!pow2_in(w, 64, 512) || D % w != 0)) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID,
+                        "transform: Hadamard width must be 64..512, a power of two dividing head_dim");
+        }
+    }
+    out.on = true;
+    out.head_dim = D;
+    out.n_rot = xf->n_rot;
+    out.had_k = xf->hadamard_k;
+    out.had_v = want_v ? xf->hadamard_v : 0u;
+    // the reference's scale, 1.0f / sqrtf((float) nrot) (stagein.cu:557)
+    out.hscale_k = out.had_k ? 1.0f / sqrtf(static_cast<float>(out.had_k)) : 1.0f;
+    out.hscale_v = out.had_v ? 1.0f / sqrtf(static_cast<float>(out.had_v)) : 1.0f;
+    return KVMEM_HIP_OK;
+}
+
 // One upload holding a block job's device tables: the pool's per-layer
-// pointers (K at [0, L), V at [L, 2L)) followed by the items ([n][3] u32:
-// block, slot, tokens).  A single upload per call keeps both inside one
-// upload-ring slot for as long as the call's kernels need them.
+// pointers (K at [0, L), V at [L, 2L)), the items ([n][4] u32: block, slot,
+// tokens, position of token 0) and the RoPE frequencies.  A single upload
+// per call keeps them inside one upload-ring slot for as long as the
+// call's kernels need them.
 struct JobTables {
     const void *const *layers = nullptr;
     const uint32_t *items = nullptr;
+    const float *theta = nullptr;
 };
 
 static bool upload_block_job(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, bool want_v,
-                             const std::vector<uint32_t> &items, JobTables &out) {
+                             const std::vector<uint32_t> &items, const XfParams &xp,
+                             JobTables &out) {
     const size_t L = pool->n_layers;
-    std::vector<uint64_t> buf(2 * L + (items.size() + 1) / 2, 0);
+    const size_t n_theta = xp.n_rot / 2;
+    const size_t words = items.size() + n_theta;  // 4-byte words after the pointers
+    std::vector<uint64_t> buf(2 * L + (words + 1) / 2, 0);
     for (size_t l = 0; l < L; ++l) {
         buf[l] = reinterpret_cast<uint64_t>(pool->k_layers[l]);
         buf[L + l] = want_v ? reinterpret_cast<uint64_t>(pool->v_layers[l]) : 0;
     }
-    std::memcpy(buf.data() + 2 * L, items.data(), items.size() * sizeof(uint32_t));
+    uint8_t *tail = reinterpret_cast<uint8_t *>(buf.data() + 2 * L);
+    std::memcpy(tail, items.data(), items.size() * sizeof(uint32_t));
+    if (n_theta) {
+        std::memcpy(tail + items.size() * sizeof(uint32_t), pool->xf->theta, n_theta * sizeof(float));
+    }
     void *dev = upload(ctx, buf.data(), buf.size() * sizeof(uint64_t), "stage-in job tables");
     if (!dev) {
         return false;
     }
     out.layers = static_cast<const void *const *>(dev);
     out.items = reinterpret_cast<const uint32_t *>(static_cast<const uint64_t *>(dev) + 2 * L);
+    out.theta = n_theta ? reinterpret_cast<const float *>(out.items + items.size()) : nullptr;
     return true;
 }
 
-// Source of one kind (K or V) of a block job.  items_dev: device [n][3].
+// Position of token 0 of staged block i (item order of the call).
+static uint32_t item_pos0(const kvmem_hip_pool *pool, const uint32_t *block_ids, uint32_t i,
+                          uint32_t block_tokens) {
+    if (pool->xf && pool->xf->pos0) {
+        return static_cast<uint32_t>(pool->xf->pos0[i]);
+    }
+    return block_ids[i] * block_tokens;
+}
+
+// Source of one kind (K or V) of a block job.  items_dev: device [n][4].
 static BlockSource make_block_source(int type, const uint8_t *base, uint64_t block_stride,
                                      uint64_t layer_stride, const void *layer_table_dev,
                                      uint32_t n_layers, uint32_t block_tokens, uint32_t n_embd,
-                                     const uint32_t *items_dev) {
+                                     const uint32_t *items_dev, const XfParams &xp, bool is_k,
+                                     const float *theta_dev) {
     BlockSource s;
     s.base = base;
     s.layer_dst = static_cast<const uint8_t *const *>(layer_table_dev);
     s.items = items_dev;
+    s.theta = theta_dev;
     s.block_stride = block_stride;
     s.layer_stride = layer_stride;
     s.n_layers = n_layers;
@@ -526,12 +918,16 @@ static BlockSource make_block_source(int type, const uint8_t *base, uint64_t blo
     s.gpr = n_embd / 32;
     s.row_bytes = s.gpr * group_bytes(type);
     s.chunks_per_op = (block_tokens * s.gpr + kChunkGroups - 1) / kChunkGroups;
+    s.head_dim = xp.head_dim;
+    s.n_rot = is_k ? xp.n_rot : 0u;
+    s.hadamard = is_k ? xp.had_k : xp.had_v;
+    s.hscale = is_k ? xp.hscale_k : xp.hscale_v;
     return s;
 }
 
-// One launch for K (and V when sv_on): chunks of K first, then of V.
+// One launch for K (and V when sv is set): chunks of K first, then of V.
 static int launch_block_job(kvmem_hip_ctx *ctx, int type_k, const BlockSource &sk, int type_v,
-                            const BlockSource *sv, uint32_t n_items) {
+                            const BlockSource *sv, uint32_t n_items, bool xf) {
     const uint64_t nk = static_cast<uint64_t>(n_items) * sk.n_layers * sk.chunks_per_op;
     const uint64_t nv = sv ? static_cast<uint64_t>(n_items) * sv->n_layers * sv->chunks_per_op : 0;
     if (nk + nv > 0x7fffffffu) {
@@ -540,9 +936,9 @@ static int launch_block_job(kvmem_hip_ctx *ctx, int type_k, const BlockSource &s
     bool ok;
     if (sv) {
         ok = launch_quant_kv(ctx, type_k, type_v, static_cast<uint32_t>(nk),
-                             static_cast<uint32_t>(nv), sk, *sv);
+                             static_cast<uint32_t>(nv), sk, *sv, xf);
     } else {
-        ok = launch_quant(ctx, type_k, static_cast<uint32_t>(nk), sk);
+        ok = launch_quant(ctx, type_k, static_cast<uint32_t>(nk), sk, xf);
     }
     return ok ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
 }
@@ -644,34 +1040,40 @@ int kvmem_hip_stagein_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
     if (st != KVMEM_HIP_OK) {
         return st;
     }
-    std::vector<uint32_t> items(3 * static_cast<size_t>(n));
+    XfParams xp;
+    st = resolve_xf(ctx, pool, hist->n_embd_k, hist->n_embd_v, want_v, xp);
+    if (st != KVMEM_HIP_OK) {
+        return st;
+    }
+    std::vector<uint32_t> items(4 * static_cast<size_t>(n));
     for (uint32_t i = 0; i < n; ++i) {
         if (block_ids[i] >= hist->n_blocks || slots[i] >= pool->n_slots) {
             return fail(ctx, KVMEM_HIP_ERR_INVALID, "stagein_blocks: block id or slot out of range");
         }
         const bool last = block_ids[i] + 1 == hist->n_blocks && hist->last_block_tokens != 0;
-        items[3 * i + 0] = block_ids[i];
-        items[3 * i + 1] = slots[i];
-        items[3 * i + 2] = last ? std::min(hist->last_block_tokens, T) : T;
+        items[4 * i + 0] = block_ids[i];
+        items[4 * i + 1] = slots[i];
+        items[4 * i + 2] = last ? std::min(hist->last_block_tokens, T) : T;
+        items[4 * i + 3] = item_pos0(pool, block_ids, i, T);
     }
     (void) hipSetDevice(ctx->device);
     JobTables jt;
-    if (!upload_block_job(ctx, pool, want_v, items, jt)) {
+    if (!upload_block_job(ctx, pool, want_v, items, xp, jt)) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     const uint64_t bk = static_cast<uint64_t>(T) * hist->n_embd_k * 2u;
     const BlockSource sk = make_block_source(pool->type_k, static_cast<const uint8_t *>(hist->k), bk,
                                              bk * cap, jt.layers, hist->n_layers, T,
-                                             hist->n_embd_k, jt.items);
+                                             hist->n_embd_k, jt.items, xp, true, jt.theta);
     BlockSource sv{};
     if (want_v) {
         const uint64_t bv = static_cast<uint64_t>(T) * hist->n_embd_v * 2u;
         sv = make_block_source(pool->type_v, static_cast<const uint8_t *>(hist->v), bv,
                                bv * cap, jt.layers + hist->n_layers, hist->n_layers, T,
-                               hist->n_embd_v, jt.items);
+                               hist->n_embd_v, jt.items, xp, false, jt.theta);
     }
     perf_begin(ctx, kPerfSet);
-    st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n);
+    st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp.on);
     perf_end(ctx, kPerfSet);
     return st;
 }
@@ -707,6 +1109,11 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
             return fail(ctx, KVMEM_HIP_ERR_INVALID, "stagein_blocks_host: block id or slot out of range");
         }
     }
+    XfParams xp;
+    st = resolve_xf(ctx, pool, hist->n_embd_k, hist->n_embd_v, want_v, xp);
+    if (st != KVMEM_HIP_OK) {
+        return st;
+    }
     (void) hipSetDevice(ctx->device);
     // Device ring: kRing slots of up to 32 MiB (at least one block each).
     constexpr int kRing = 4;
@@ -739,16 +1146,17 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
         }
     }
     // items of every batch, block index relative to its ring slot
-    std::vector<uint32_t> items(3 * static_cast<size_t>(n));
+    std::vector<uint32_t> items(4 * static_cast<size_t>(n));
     for (uint32_t i = 0; i < n; ++i) {
         const uint32_t b = block_ids[i];
-        items[3 * i + 0] = i % per_slot;
-        items[3 * i + 1] = slots[i];
-        items[3 * i + 2] = (b + 1 == hist->n_blocks && hist->last_block_tokens != 0)
+        items[4 * i + 0] = i % per_slot;
+        items[4 * i + 1] = slots[i];
+        items[4 * i + 2] = (b + 1 == hist->n_blocks && hist->last_block_tokens != 0)
                                ? std::min(hist->last_block_tokens, T) : T;
+        items[4 * i + 3] = item_pos0(pool, block_ids, i, T);
     }
     JobTables jt;
-    if (!upload_block_job(ctx, pool, want_v, items, jt)) {
+    if (!upload_block_job(ctx, pool, want_v, items, xp, jt)) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     perf_begin(ctx, kPerfSet);
@@ -775,15 +1183,15 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
             !hip_ok(ctx, hipStreamWaitEvent(ctx->stream, ctx->h2d_copied[r], 0), "h2d wait copied")) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
-        const uint32_t *batch_items = jt.items + 3 * static_cast<size_t>(first);
+        const uint32_t *batch_items = jt.items + 4 * static_cast<size_t>(first);
         const BlockSource sk = make_block_source(pool->type_k, slot_base, span, layer_bytes, jt.layers,
-                                                 L, T, hist->n_embd_k, batch_items);
+                                                 L, T, hist->n_embd_k, batch_items, xp, true, jt.theta);
         BlockSource sv{};
         if (want_v) {
             sv = make_block_source(pool->type_v, slot_base + kbytes, span, layer_bytes, jt.layers + L, L,
-                                   T, hist->n_embd_v, batch_items);
+                                   T, hist->n_embd_v, batch_items, xp, false, jt.theta);
         }
-        st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, cnt);
+        st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, cnt, xp.on);
         if (st != KVMEM_HIP_OK) {
             return st;
         }

@@ -30,6 +30,15 @@
  *   ko_score_meank                : an independent float64 numpy restatement,
  *                                   closed forms (parallel / orthogonal /
  *                                   scaled directions, GQA head sums).
+ *   ko_rope_sincos                : float64 libm sin/cos rounded to fp32 over
+ *                                   10^6 angles up to 2^20 rad, quadrant
+ *                                   identities, exact multiples of pi/2.
+ *   ko_rope_rows                  : the reference's own RoPE (rope.cpp via
+ *                                   oracle/_ref) within fp32 rounding, its unit
+ *                                   test (position 0 = identity), float64
+ *                                   rotation, pair norms preserved.
+ *   ko_hadamard_rows              : float64 Sylvester matrix products, H H = I,
+ *                                   exact images of unit vectors.
  *   ko_q_accumulate               : exact integer sums, an order-sensitive
  *                                   cancellation sequence only the token-order
  *                                   fp32 sum reproduces, float64 error bound.
@@ -134,6 +143,20 @@ void ko_mean_k(const float *k_sum, uint32_t mean_tokens, uint32_t n_embd, float 
 void ko_score_meank(const float *q_sum, const uint32_t *q_count, const float *k_sum,
                     const uint32_t *mean_tokens, uint32_t L, uint32_t B, uint32_t Hq,
                     uint32_t Hkv, uint32_t D, double *scores);
+
+/* Cache row transform of the raw-K stage-in (llama-kvmem-stagein.cu:
+ * 704-740): ko_rope_sincos is the library's own sin/cos of an fp32 angle
+ * (fp64 Cody-Waite reduction, Taylor polynomials, one rounding);
+ * ko_rope_rows the NeoX RoPE of rope_neox_kernel (:159-178, rope.cpp:8-45)
+ * at positions pos0 + t; ko_hadamard_rows fwht_kernel (:104-130) over runs
+ * of `width` with scale 1/sqrtf(width); ko_quantize_rows_f32 quantizes fp32
+ * rows (F16: RNE). */
+void ko_rope_sincos(float a, float *sn, float *cs);
+void ko_rope_sincos_n(const float *a, uint64_t n, float *sn, float *cs);
+void ko_rope_rows(float *rows, uint32_t n_rows, uint32_t n_embd, uint32_t head_dim,
+                  uint32_t n_rot, const float *theta, int32_t pos0);
+void ko_hadamard_rows(float *x, uint64_t n_elems, uint32_t width);
+int ko_quantize_rows_f32(int type, const float *src, uint8_t *dst, int64_t n_rows, int64_t n_embd);
 
 /* The reference's query harvest (llama-memory-kvmem.cpp:2164-2172):
  * q [L][T][E] f32; q_sum[l] (+)= q[l][tokens[i]] for i < n_list in order

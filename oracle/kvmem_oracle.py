@@ -70,6 +70,14 @@ def lib() -> C.CDLL:
     L.ko_mean_k.argtypes = [f32p, u32, u32, f32p]
     L.ko_score_meank.restype = None
     L.ko_score_meank.argtypes = [f32p, u32p, f32p, u32p, u32, u32, u32, u32, u32, f64p]
+    L.ko_rope_sincos_n.restype = None
+    L.ko_rope_sincos_n.argtypes = [f32p, C.c_uint64, f32p, f32p]
+    L.ko_rope_rows.restype = None
+    L.ko_rope_rows.argtypes = [f32p, u32, u32, u32, u32, f32p, C.c_int32]
+    L.ko_hadamard_rows.restype = None
+    L.ko_hadamard_rows.argtypes = [f32p, C.c_uint64, u32]
+    L.ko_quantize_rows_f32.restype = C.c_int
+    L.ko_quantize_rows_f32.argtypes = [C.c_int, f32p, u8p, C.c_int64, C.c_int64]
     L.ko_q_accumulate.restype = None
     L.ko_q_accumulate.argtypes = [f32p, u32, u32, u32, C.c_void_p, u32, C.c_int, f32p]
     L.ko_max_threads.restype = C.c_int
@@ -209,6 +217,53 @@ def score_meank(q_sum: np.ndarray, q_count, k_sum: np.ndarray, mean_tokens: np.n
     L, B = mt.shape
     out = np.zeros(B, dtype=np.float64)
     lib().ko_score_meank(q_sum, qc, k_sum, mt, L, B, Hq, Hkv, D, out)
+    return out
+
+
+def rope_sincos(a) -> tuple[np.ndarray, np.ndarray]:
+    """sin, cos (f32) of f32 angles, the library's own evaluation."""
+    a = np.ascontiguousarray(a, dtype=np.float32).ravel()
+    s = np.zeros_like(a)
+    c = np.zeros_like(a)
+    lib().ko_rope_sincos_n(a, a.size, s, c)
+    return s, c
+
+
+def rope_theta(n_rot: int, freq_base: float = 10000.0, freq_scale: float = 1.0) -> np.ndarray:
+    """Pair frequencies as rope.cpp:20-23 forms them: powf(freq_base,
+    -2.0f*i/n_rot) * freq_scale, every step in fp32 (the C library's powf,
+    which std::pow(float, float) calls)."""
+    import ctypes.util
+    libm = C.CDLL(ctypes.util.find_library("m"))
+    libm.powf.restype = C.c_float
+    libm.powf.argtypes = [C.c_float, C.c_float]
+    out = np.zeros(n_rot // 2, dtype=np.float32)
+    for i in range(n_rot // 2):
+        ex = np.float32(np.float32(-2.0) * np.float32(i)) / np.float32(n_rot)
+        out[i] = np.float32(libm.powf(float(np.float32(freq_base)), float(ex))) * np.float32(freq_scale)
+    return out
+
+
+def transform_rows(rows: np.ndarray, head_dim: int, n_rot: int = 0, theta=None, pos0: int = 0,
+                   hadamard: int = 0) -> np.ndarray:
+    """[n_rows, n_embd] f32 -> RoPE'd (n_rot > 0) then Hadamard-rotated
+    (hadamard > 0) copy, the raw-K stage-in transform."""
+    x = np.array(rows, dtype=np.float32, copy=True, order="C")
+    n, e = x.shape
+    if n_rot:
+        th = np.ascontiguousarray(theta, dtype=np.float32)
+        lib().ko_rope_rows(x, n, e, head_dim, n_rot, th, int(pos0))
+    if hadamard:
+        lib().ko_hadamard_rows(x, x.size, hadamard)
+    return x
+
+
+def quantize_rows_f32(type_: int, rows: np.ndarray) -> np.ndarray:
+    rows = np.ascontiguousarray(rows, dtype=np.float32)
+    n, e = rows.shape
+    out = np.zeros((n, row_bytes(type_, e)), dtype=np.uint8)
+    if lib().ko_quantize_rows_f32(type_, rows, out, n, e) != 0:
+        raise ValueError("ko_quantize_rows_f32 failed")
     return out
 
 

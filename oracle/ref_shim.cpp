@@ -13,6 +13,7 @@
 #include "kvmem/kvmem_runtime.hpp"
 #include "kvmem/kvmem_store.hpp"
 #include "kvmem/raw_kv_store.hpp"
+#include "kvmem/rope.hpp"
 
 #include <cstdint>
 #include <cstring>
@@ -201,6 +202,25 @@ KREF_API int kref_mean_k_f32(uint32_t n_embd, uint32_t block_tokens, const float
             raw.write_layer_mean_k(pos, n, 0, rows + static_cast<size_t>(pos) * n_embd);
         }
         raw.mean_k(block, 0, out);
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+// kvmem::rope_neox_apply (kvmem/src/host/rope.cpp): k_prerope token-major
+// [n_tokens][n_head_kv][n_embd_head] f32 rotated at positions pos0, pos0+1, ...
+KREF_API int kref_rope_neox(uint32_t n_rot, uint32_t n_embd_head, uint32_t n_head_kv, float freq_base,
+                            float freq_scale, const float *src, uint32_t n_tokens, int32_t pos0,
+                            float *out) {
+    try {
+        kvmem::RopeConfig cfg;
+        cfg.n_rot = n_rot;
+        cfg.n_embd_head = n_embd_head;
+        cfg.n_head_kv = n_head_kv;
+        cfg.freq_base = freq_base;
+        cfg.freq_scale = freq_scale;
+        kvmem::rope_neox_apply(cfg, src, n_tokens, pos0, out);
         return 0;
     } catch (...) {
         return -1;
