@@ -122,6 +122,17 @@ typedef struct kvmem_engine_params {
                                   layout_gpu_slots_by_orig_pos
                                   (llama-memory-kvmem.cpp:931-1254) */
     int32_t scorer;            /* kvmem_engine_scorer used by preview */
+    /* Cache row transform of the stage-in (kvmem_hip_transform), for a
+     * history of pre-RoPE keys and a cache that holds RoPE'd, rotated rows: */
+    uint32_t n_rot;            /* K rotary dims, RoPE at each block's original
+                                  positions (0 = keys stored as given) */
+    float rope_freq_base;      /* theta_i = powf(base, -2i/n_rot) * scale, */
+    float rope_freq_scale;     /*   as kvmem/src/host/rope.cpp:20-23 */
+    int32_t attn_rot;          /* 1: the reference's attn_rot rule
+                                  (kvmem_attn_rot_on, llama-kvmem-quant.h:
+                                  22-38): a quantized K (V) cache gets the
+                                  Walsh-Hadamard rotation of width
+                                  kvmem_hadamard_nrot_k(head_dim) (64) */
 } kvmem_engine_params;
 
 /* Block scorer of kvmem_engine_preview / apply_retrieval. */
@@ -134,7 +145,8 @@ enum kvmem_engine_scorer {
 
 /* Defaults: 16 layers, 128-token blocks, 24/4 heads x 256, budget 256 +
  * reserve 128 blocks, sink 1, recent 0, q8_0 K and V, lower-id ties, mean
- * layer reduce, free-list (non-canonical) layout, per-token max scorer. */
+ * layer reduce, free-list (non-canonical) layout, per-token max scorer, no
+ * row transform (RoPE base 10000, scale 1 when n_rot is set). */
 KVMEM_HIP_API kvmem_engine_params kvmem_engine_default_params(void);
 
 /* Create the engine: its kvmem_hip_ctx, the slot pool of

@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstddef>
 #include <cstring>
 #include <exception>
@@ -233,6 +234,9 @@ struct kvmem_engine {
     uint32_t meank_cap = 0;    // capacity the sums are allocated for
     uint32_t meank_valid = 0;  // leading blocks whose sums are current
     float *d_qsum = nullptr;   // query sums [L][n_head*head_dim] (mean-K scorer)
+    kvmem_hip_transform xf{};  // cache row transform (unused when has_xf is false)
+    std::vector<float> theta;  // RoPE pair frequencies
+    bool has_xf = false;
     uint64_t epoch = 1;
     std::string err;
 
@@ -264,6 +268,7 @@ struct kvmem_engine {
         d.type_v = p.type_v;
         d.k_layers = pool_k.data();
         d.v_layers = pool_v.data();
+        d.xf = has_xf ? &xf : nullptr;
         return d;
     }
 
@@ -324,6 +329,50 @@ int engine_stage(kvmem_engine *e, const std::vector<uint32_t> &ids,
 
 static bool alloc_own_pool(kvmem_engine *e);
 
+namespace {
+
+// The stage-in row transform from the engine parameters: RoPE frequencies
+// as rope.cpp:20-23 forms them, and the reference's attn_rot widths
+// (llama-kvmem-quant.h:22-38): on a quantized cache, K gets the largest
+// power of two dividing head_dim (at least 64), V gets 64.
+bool setup_transform(kvmem_engine *e) {
+    const kvmem_engine_params &p = e->p;
+    const auto quantized = [](int t) { return t != KVMEM_TYPE_F16 && t != KVMEM_TYPE_F32; };
+    const bool rot_ok = p.attn_rot && p.head_dim >= 64 && p.head_dim % 64 == 0;
+    uint32_t had_k = 0;
+    if (rot_ok && quantized(p.type_k)) {
+        uint32_t n = 64;
+        do {
+            n *= 2;
+        } while (p.head_dim % n == 0);
+        had_k = n / 2;
+    }
+    const uint32_t had_v = rot_ok && quantized(p.type_v) ? 64u : 0u;
+    if (p.n_rot == 0 && had_k == 0 && had_v == 0) {
+        e->has_xf = false;
+        return true;
+    }
+    if (p.n_rot % 16 != 0 || p.n_rot > p.head_dim) {
+        return false;
+    }
+    e->theta.resize(p.n_rot / 2);
+    for (uint32_t i = 0; i < p.n_rot / 2; ++i) {
+        const float ex = -2.0f * static_cast<float>(i) / static_cast<float>(p.n_rot);
+        e->theta[i] = powf(p.rope_freq_base, ex) * p.rope_freq_scale;
+    }
+    e->xf = kvmem_hip_transform{};
+    e->xf.head_dim = p.head_dim;
+    e->xf.n_rot = p.n_rot;
+    e->xf.theta = e->theta.empty() ? nullptr : e->theta.data();
+    e->xf.hadamard_k = had_k;
+    e->xf.hadamard_v = had_v;
+    e->xf.pos0 = nullptr;  // original positions: block_id * block_tokens
+    e->has_xf = true;
+    return true;
+}
+
+}  // namespace
+
 extern "C" {
 
 kvmem_engine_params kvmem_engine_default_params(void) {
@@ -345,6 +394,10 @@ kvmem_engine_params kvmem_engine_default_params(void) {
     p.layer_reduce = KVMEM_LAYER_MEAN;
     p.canonical_layout = 0;
     p.scorer = KVMEM_SCORER_TOKEN_MAX;
+    p.n_rot = 0;
+    p.rope_freq_base = 10000.0f;
+    p.rope_freq_scale = 1.0f;
+    p.attn_rot = 0;
     return p;
 }
 
@@ -368,6 +421,10 @@ int kvmem_engine_create(const kvmem_engine_params *pp, kvmem_engine **out) {
     e->n_embd_k = p.n_head_kv * p.head_dim;
     e->n_embd_v = p.n_embd_v ? p.n_embd_v : e->n_embd_k;
     if (e->n_embd_v % 32 != 0) {
+        delete e;
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!setup_transform(e)) {
         delete e;
         return KVMEM_HIP_ERR_INVALID;
     }

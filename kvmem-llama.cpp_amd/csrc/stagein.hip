@@ -16,7 +16,7 @@
 //
 // Arithmetic follows ggml's quantize_row_*_ref exactly (restated in the
 // reference's CUDA kernels, llama-kvmem-stagein.cu:180-233):
-//   q8_0: d = amax/127, id = d ? 1/d : 0, q = roundf(x*id)
+//   q8_0: d = amax/127, id = d ? 1/d : 0, q = roundf(x*id) (|x*id| <= 127)
 //   q4_0: d = vmax/-8,  q = min(15, trunc(x*id + 8.5))
 //   q5_0: d = vmax/-16, q = min(31, trunc(x*id + 16.5)), bit 4 -> qh
 // (division by -8 / -16 is done as the exactly equal multiplication by
@@ -47,6 +47,11 @@ constexpr int kRounds = 8;                     // 16-group rounds per wave
 constexpr int kWaveGroups = 16 * kRounds;      // groups per wave (128)
 constexpr int kChunkGroups = 4 * kWaveGroups;  // groups per workgroup (512)
 constexpr int kTabMax = 4096;                  // (row, rotary pair) entries per chunk
+
+// Rows of `gpr` groups that one chunk of kChunkGroups groups can touch.
+inline uint32_t chunk_rows_of(uint32_t gpr) {
+    return (kChunkGroups % gpr == 0) ? kChunkGroups / gpr : (kChunkGroups - 1) / gpr + 2;
+}
 
 template <int TYPE> struct Fmt;
 template <> struct Fmt<KVMEM_TYPE_Q8_0> { static constexpr int GB = 34; };
@@ -193,6 +198,14 @@ __device__ inline void store_8bytes(uint8_t *p, uint32_t lo, uint32_t hi) {
     store_u16(p + 6, hi >> 16);
 }
 
+// roundf (half away from zero) of |s| < 128.5, the range of q8_0's x*id:
+// truncation of s + copysign(0.49999997f, s) (the float below 0.5) equals
+// roundf for every float in that range (checked exhaustively over all of
+// them), in three instructions instead of roundf's compare-and-fix.
+__device__ inline int round_q8(float s) {
+    return static_cast<int>(s + copysignf(0x1.fffffep-2f, s));
+}
+
 // Quantize the 8 elements a lane owns (elements 8q..8q+7 of its group) and
 // write its share of the group's bytes to `g` (the group's LDS bytes).
 template <int TYPE>
@@ -217,8 +230,7 @@ __device__ inline void quant_quarter<KVMEM_TYPE_Q8_0>(const uint4 &v, uint32_t q
     uint32_t w[2] = {0u, 0u};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const float s = x[i] * id;
-        const int c = static_cast<int>(roundf(s));
+        const int c = round_q8(x[i] * id);
         w[i >> 2] |= (static_cast<uint32_t>(c) & 0xffu) << (8 * (i & 3));
     }
     if (valid) {
@@ -386,10 +398,46 @@ __device__ inline void rope_sincos(float a, float &sn, float &cs) {
     cs = static_cast<float>(((quadrant + 1) & 2) ? -cv : cv);
 }
 
+// The value of lane ^ M: DPP quad permutes for 1 and 2, a row rotation by
+// 8 (within 16 lanes, the same as ^ 8), ds_swizzle's xor mode for 4 and 16
+// (within 32 lanes; these run on the LDS pipe, off the VALU that bounds the
+// transform), a lane permute for 32.  Every lane of the wave must be active.
+template <uint32_t M>
+__device__ inline float lane_xor(float v) {
+    const int x = __float_as_int(v);
+    int r;
+    if constexpr (M == 1) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
+    } else if constexpr (M == 2) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);
+    } else if constexpr (M == 4) {
+        r = __builtin_amdgcn_ds_swizzle(x, 0x1F | (4 << 10));
+    } else if constexpr (M == 8) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);  // row_ror:8
+    } else if constexpr (M == 16) {
+        r = __builtin_amdgcn_ds_swizzle(x, 0x1F | (16 << 10));
+    } else {
+        r = __shfl_xor(x, static_cast<int>(M), 64);
+    }
+    return __int_as_float(r);
+}
+
+// One butterfly stage of span 8*M across lanes: the lane whose bit M is set
+// holds the upper element and keeps partner - own, the other own + partner
+// (p + (-x) is the IEEE subtraction p - x).
+template <uint32_t M>
+__device__ inline void butterfly_lanes(float x[8], uint32_t lane) {
+    const uint32_t flip = (lane & M) ? 0x80000000u : 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float p = lane_xor<M>(x[i]);
+        x[i] = p + __uint_as_float(__float_as_uint(x[i]) ^ flip);
+    }
+}
+
 // Walsh-Hadamard rotation of runs of `width` elements, in the order of the
 // reference's fwht_kernel: scale every element, then butterflies of span
-// 1, 2, 4 (inside the lane) and 8 .. width/2 (partner lane ^ span/8; the
-// lane with that bit set keeps partner - own, the other own + partner).
+// 1, 2, 4 (inside the lane) and 8 .. width/2 (partner lane ^ span/8).
 __device__ inline void fwht_lanes(float x[8], uint32_t width, float scale, uint32_t lane) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -408,13 +456,47 @@ __device__ inline void fwht_lanes(float x[8], uint32_t width, float scale, uint3
             }
         }
     }
-    for (uint32_t m = 1; m < width / 8u; m <<= 1) {
-        const bool upper = (lane & m) != 0u;
+    // width is uniform: whole stages are skipped together
+    butterfly_lanes<1>(x, lane);
+    butterfly_lanes<2>(x, lane);
+    butterfly_lanes<4>(x, lane);
+    if (width > 64u) {
+        butterfly_lanes<8>(x, lane);
+    }
+    if (width > 128u) {
+        butterfly_lanes<16>(x, lane);
+    }
+    if (width > 256u) {
+        butterfly_lanes<32>(x, lane);
+    }
+}
+
+// Partner values of a RoPE pair: lane ^ (n_rot/16) when that is a power of
+// two (a head's first-half lanes then differ from their partners in exactly
+// that bit), else lane +- n_rot/16 through a general lane permute.
+__device__ inline void rope_partners(const float x[8], float p[8], uint32_t n_rot, uint32_t lane,
+                                     bool rot, bool first) {
+    const uint32_t d = n_rot / 16u;
+#define KVMEM_XOR_CASE(M)                     \
+    case M:                                   \
+        for (int i = 0; i < 8; ++i) {         \
+            p[i] = lane_xor<M>(x[i]);         \
+        }                                     \
+        return;
+    switch (d) {
+        KVMEM_XOR_CASE(1)
+        KVMEM_XOR_CASE(2)
+        KVMEM_XOR_CASE(4)
+        KVMEM_XOR_CASE(8)
+        KVMEM_XOR_CASE(16)
+        KVMEM_XOR_CASE(32)
+        default: break;
+    }
+#undef KVMEM_XOR_CASE
+    const int src = static_cast<int>(rot ? (first ? lane + d : lane - d) : lane);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float p = __shfl_xor(x[i], static_cast<int>(m), 64);
-            x[i] = upper ? p - x[i] : x[i] + p;
-        }
+    for (int i = 0; i < 8; ++i) {
+        p[i] = __shfl(x[i], src, 64);
     }
 }
 
@@ -461,7 +543,7 @@ __device__ inline void quant_quarter_f<KVMEM_TYPE_Q8_0>(const float x[8], uint32
     uint32_t w[2] = {0u, 0u};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const int c = static_cast<int>(roundf(x[i] * id));
+        const int c = round_q8(x[i] * id);
         w[i >> 2] |= (static_cast<uint32_t>(c) & 0xffu) << (8 * (i & 3));
     }
     if (valid) {
@@ -555,6 +637,11 @@ __device__ inline void transform_rounds(const Source &s, const Chunk &c, const u
     const uint32_t q = lane & 3u;
     const uint32_t half = s.n_rot / 2u;
     const uint32_t row0 = c.g0 / c.gpr;
+    // Table row r holds pair j's (cos, sin) at position 2*(pl*((j%8)/2) +
+    // j/8) + j%2, pl = half/8 lanes: a lane owning pairs 8m..8m+7 reads them
+    // as four 16-byte chunks pl*u + m, u < 4, so in each read the lanes of
+    // a half-head take consecutive chunks (no bank conflicts).
+    const uint32_t pl = half / 8u;
     if (half != 0u) {
         const uint32_t rows = (c.g0 + c.ng - 1u) / c.gpr - row0 + 1u;
         for (uint32_t i = threadIdx.x; i < rows * half; i += blockDim.x) {
@@ -563,11 +650,10 @@ __device__ inline void transform_rounds(const Source &s, const Chunk &c, const u
             const float pos = static_cast<float>(c.pos0 + static_cast<int32_t>(row0 + r));
             float sn, cs;
             rope_sincos(pos * s.theta[j], sn, cs);
-            tab[i] = make_float2(cs, sn);
+            tab[r * half + 2u * (pl * ((j & 7u) >> 1) + (j >> 3)) + (j & 1u)] = make_float2(cs, sn);
         }
         __syncthreads();
     }
-    const uint32_t pair_lanes = half / 8u;
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) {
         const uint32_t gl = wg0 + 16u * r + quad;
@@ -586,19 +672,21 @@ __device__ inline void transform_rounds(const Source &s, const Chunk &c, const u
         if (half != 0u) {
             const bool rot = d0 < s.n_rot;
             const bool first = d0 < half;
-            const int src = static_cast<int>(rot ? (first ? lane + pair_lanes : lane - pair_lanes) : lane);
             float p[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                p[i] = __shfl(x[i], src, 64);
-            }
+            rope_partners(x, p, s.n_rot, lane, rot, first);
             if (rot && valid) {
-                const float2 *t = tab + (row - row0) * half + (first ? d0 : d0 - half);
+                const uint32_t m = (first ? d0 : d0 - half) / 8u;
+                const float4 *t = reinterpret_cast<const float4 *>(tab + (row - row0) * half);
+                // first half (x0 = own, x1 = partner): own*c - partner*s;
+                // second half (x0 = partner, x1 = own): own*c + partner*s
+                const uint32_t flip = first ? 0x80000000u : 0u;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float2 cs = t[i];
-                    // first half: x0 = own, x1 = partner; second half: x0 = partner, x1 = own
-                    x[i] = first ? x[i] * cs.x - p[i] * cs.y : p[i] * cs.y + x[i] * cs.x;
+                for (int u = 0; u < 4; ++u) {
+                    const float4 cs = t[pl * u + m];  // pairs 8m+2u (x, y), 8m+2u+1 (z, w)
+                    const float p0 = p[2 * u] * cs.y;
+                    const float p1 = p[2 * u + 1] * cs.w;
+                    x[2 * u] = x[2 * u] * cs.x + __uint_as_float(__float_as_uint(p0) ^ flip);
+                    x[2 * u + 1] = x[2 * u + 1] * cs.z + __uint_as_float(__float_as_uint(p1) ^ flip);
                 }
             }
         }
@@ -669,11 +757,16 @@ __device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8
     }
 }
 
+// The RoPE table lives in dynamic LDS sized by the launch (rows a chunk
+// touches x rotary pairs, at most kTabMax entries; 0 without RoPE), read
+// as 16-byte chunks.
+extern __shared__ float4 rope_tab4[];
+#define rope_tab reinterpret_cast<float2 *>(rope_tab4)
+
 template <int TYPE, class Source, bool XF>
 __global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kWaveGroups * Fmt<TYPE>::GB];
-    __shared__ float2 tab[XF ? kTabMax : 1];
-    quant_chunk<TYPE, Source, XF>(source, blockIdx.x, lds, tab);
+    quant_chunk<TYPE, Source, XF>(source, blockIdx.x, lds, rope_tab);
 }
 
 // K and V of a block job in one launch: workgroups [0, n_k) take K chunks,
@@ -683,28 +776,37 @@ __global__ __launch_bounds__(256) void quant_scatter_kv_kernel(BlockSource sk, B
                                                                uint32_t n_k) {
     constexpr int GB = Fmt<TK>::GB > Fmt<TV>::GB ? Fmt<TK>::GB : Fmt<TV>::GB;
     __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kWaveGroups * GB];
-    __shared__ float2 tab[XF ? kTabMax : 1];
     if (blockIdx.x < n_k) {
-        quant_chunk<TK, BlockSource, XF>(sk, blockIdx.x, lds, tab);
+        quant_chunk<TK, BlockSource, XF>(sk, blockIdx.x, lds, rope_tab);
     } else {
-        quant_chunk<TV, BlockSource, XF>(sv, blockIdx.x - n_k, lds, tab);
+        quant_chunk<TV, BlockSource, XF>(sv, blockIdx.x - n_k, lds, rope_tab);
     }
+}
+
+// Dynamic LDS bytes of the RoPE table for chunks of `s`.
+template <class Source>
+size_t rope_tab_bytes(const Source &s) {
+    return s.n_rot ? sizeof(float2) * chunk_rows_of(s.gpr) * (s.n_rot / 2) : 0;
 }
 
 template <class Source, bool XF>
 bool launch_quant_x(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Source &s) {
+    size_t tb = 0;
+    if constexpr (XF) {
+        tb = rope_tab_bytes(s);
+    }
     switch (type) {
         case KVMEM_TYPE_Q8_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q8_0, Source, XF><<<n_chunks, 256, 0, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_Q8_0, Source, XF><<<n_chunks, 256, tb, ctx->stream>>>(s);
             break;
         case KVMEM_TYPE_Q4_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q4_0, Source, XF><<<n_chunks, 256, 0, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_Q4_0, Source, XF><<<n_chunks, 256, tb, ctx->stream>>>(s);
             break;
         case KVMEM_TYPE_Q5_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q5_0, Source, XF><<<n_chunks, 256, 0, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_Q5_0, Source, XF><<<n_chunks, 256, tb, ctx->stream>>>(s);
             break;
         case KVMEM_TYPE_F16:
-            quant_scatter_kernel<KVMEM_TYPE_F16, Source, XF><<<n_chunks, 256, 0, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_F16, Source, XF><<<n_chunks, 256, tb, ctx->stream>>>(s);
             break;
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported type");
@@ -728,18 +830,19 @@ bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const BlockSo
 template <int TK, bool XF>
 bool launch_kv_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, const BlockSource &sk,
                  const BlockSource &sv, uint32_t n_k) {
+    const size_t tb = XF ? rope_tab_bytes(sk) : 0;  // only K is RoPE'd
     switch (tv) {
         case KVMEM_TYPE_Q8_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q8_0, XF><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q8_0, XF><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
             break;
         case KVMEM_TYPE_Q4_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q4_0, XF><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q4_0, XF><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
             break;
         case KVMEM_TYPE_Q5_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q5_0, XF><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q5_0, XF><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
             break;
         case KVMEM_TYPE_F16:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_F16, XF><<<grid, 256, 0, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_F16, XF><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
             break;
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported V type");
@@ -810,8 +913,7 @@ struct XfParams {
 
 // Rows of n_embd elements that one chunk of kChunkGroups groups can touch.
 static uint32_t chunk_rows(uint32_t n_embd) {
-    const uint32_t gpr = n_embd / 32;
-    return (kChunkGroups % gpr == 0) ? kChunkGroups / gpr : (kChunkGroups - 1) / gpr + 2;
+    return chunk_rows_of(n_embd / 32);
 }
 
 static bool pow2_in(uint32_t x, uint32_t lo, uint32_t hi) {

@@ -34,7 +34,8 @@ class EngineParams(C.Structure):
                 ("reserve_blocks", C.c_uint32), ("sink_blocks", C.c_uint32),
                 ("recent_blocks", C.c_uint32), ("type_k", C.c_int32), ("type_v", C.c_int32),
                 ("tie_lower_index", C.c_int32), ("layer_reduce", C.c_int32),
-                ("canonical_layout", C.c_int32), ("scorer", C.c_int32)]
+                ("canonical_layout", C.c_int32), ("scorer", C.c_int32), ("n_rot", C.c_uint32),
+                ("rope_freq_base", C.c_float), ("rope_freq_scale", C.c_float), ("attn_rot", C.c_int32)]
 
 
 _bound = set()
@@ -185,7 +186,7 @@ class Engine:
         for k, v in params.items():
             if not hasattr(p, k):
                 raise TypeError(f"unknown engine parameter {k}")
-            setattr(p, k, int(v))
+            setattr(p, k, float(v) if k.startswith("rope_freq") else int(v))
         self.params = p
         h = C.c_void_p()
         rc = self.lib.kvmem_engine_create(C.byref(p), C.byref(h))

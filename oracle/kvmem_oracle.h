@@ -72,6 +72,11 @@ void ko_quantize_row_q8_0(const float *x, uint8_t *y, int64_t k);
 void ko_quantize_row_q4_0(const float *x, uint8_t *y, int64_t k);
 void ko_quantize_row_q5_0(const float *x, uint8_t *y, int64_t k);
 
+/* Floats in [lo, hi) (non-negative) where roundf(s) differs from
+ * truncf(s + 0.49999997f): the stage-in's q8_0 rounding, checked over every
+ * float of the range |x*id| can take. */
+uint64_t ko_round_trick_mismatches(float lo, float hi);
+
 /* Dequantisation (inverse maps, used for error-bound invariants).
  * q8_0 / q4_0: llama-kvmem-stagein.cu:132-157. */
 void ko_dequantize_row(int type, const uint8_t *y, float *x, int64_t k);

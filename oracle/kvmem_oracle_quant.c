@@ -268,3 +268,24 @@ int ko_stagein_blocks(int type, const uint16_t *src, const uint32_t *slots,
     }
     return 0;
 }
+
+/* Number of floats in [lo, hi) (both non-negative) whose roundf differs
+ * from the truncation of s + 0.49999997f (the float below 0.5): checks the
+ * three-instruction rounding the stage-in kernel uses for q8_0 codes over
+ * every float of the range. */
+uint64_t ko_round_trick_mismatches(float lo, float hi) {
+    uint32_t b0, b1;
+    memcpy(&b0, &lo, 4);
+    memcpy(&b1, &hi, 4);
+    const float c = 0x1.fffffep-2f;
+    uint64_t bad = 0;
+    for (uint32_t b = b0; b < b1; ++b) {
+        float s;
+        memcpy(&s, &b, 4);
+        const float t = s + c;
+        if (truncf(t) != roundf(s)) {
+            ++bad;
+        }
+    }
+    return bad;
+}

@@ -266,3 +266,14 @@ def test_pick_topk_vs_sort_brute_force(oracle, tie_lower):
         key = (lambda i: (-s[i], i)) if tie_lower else (lambda i: (-s[i], -i))
         want = sorted([0] + sorted(rest, key=key)[: budget - 1])
         assert got == want
+
+
+def test_q8_rounding_shortcut_exhaustive(oracle):
+    """The kernel rounds q8_0 codes as trunc(s + copysign(0.49999997, s));
+    over every float in [0, 128.5) (|x*id| <= 127 * (1 + 2^-22)) that equals
+    roundf, and both are odd functions, so the codes are ggml's."""
+    assert oracle.lib().ko_round_trick_mismatches(0.0, 128.5) == 0
+    # the check itself sees a wrong constant: 0.5 rounds 0.49999997 up
+    assert oracle.lib().ko_round_trick_mismatches(0.0, 1.0) == 0
+    s = np.float32(0.49999997)
+    assert np.trunc(np.float32(s + np.float32(0.5))) != np.round(s)

@@ -157,3 +157,41 @@ def test_transform_rejects_bad_arguments(ctx):
     with pytest.raises(kv.KvMemError):
         ctx.stagein_blocks(h2, pool, [0], [0])
     assert (pk.cpu().numpy() == 0).all() and (p2.cpu().numpy() == 0).all()
+
+
+def test_engine_rope_attn_rot(oracle):
+    """The engine with n_rot / attn_rot: every selected block lands in its
+    slot RoPE'd at its original positions and rotated (K width 256 on q8_0,
+    V width 64 on q4_0), bit-exact."""
+    from kvmem_amd import host
+    announce("engine: RoPE 256 (base 1e6) + attn_rot, q8_0 K / q4_0 V, 2 layers x 20 blocks")
+    L, HQ, HKV, D, nb = 2, 24, 4, 256, 20
+    E = HKV * D
+    k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=nb, Tq=8, seed=81, with_v=True)
+    theta = oracle.rope_theta(256, 1e6)
+    with host.Engine(n_layers=L, block_tokens=T, n_head=HQ, n_head_kv=HKV, head_dim=D,
+                     budget_blocks=6, reserve_blocks=2, type_k=kv.TYPE_Q8_0, type_v=kv.TYPE_Q4_0,
+                     n_rot=256, rope_freq_base=1e6, attn_rot=1) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), nb, nb * T)
+        sel = eng.preview(q.data_ptr(), 8)
+        eng.apply(sel)
+        slots = eng.block_slots()
+        kb = workloads.to_bits(torch, k)
+        vb = workloads.to_bits(torch, v)
+        c = kv.Context(0)
+        for layer in range(L):
+            for which, src, ty, n_rot, width in ((0, kb, kv.TYPE_Q8_0, 256, 256),
+                                                 (1, vb, kv.TYPE_Q4_0, 0, 64)):
+                rb = kv.row_size(ty, E)
+                n = eng.n_slots() * T * rb
+                buf = torch.empty(n, dtype=torch.uint8, device="cuda")
+                c.d2d_batched([eng.pool_layer(layer)[which]], [buf.data_ptr()], [n])
+                c.sync()
+                pool = buf.cpu().numpy().reshape(eng.n_slots() * T, rb)
+                for b in sel.blocks:
+                    s = slots[b]
+                    want = expected_rows(oracle, ty, src[layer, b].reshape(T, E), D, n_rot,
+                                         theta if n_rot else None, b * T, width)
+                    got = pool[s * T:(s + 1) * T]
+                    assert np.array_equal(got, want), f"layer {layer} {'KV'[which]} block {b}: {first_diff(got, want)}"
+        c.close()
