@@ -14,7 +14,7 @@
 //   cos[l][b][h] = (qv . mk_h) / (sqrt(|qv|^2) * sqrt(|mk_h|^2) + 1e-6)
 //   score[b]   = mean over layers with q_count > 0 of (sum_h cos) / Hkv,
 // layer and block sums in double as the reference; blocks with no keys in
-// any layer score 0.  One wave per (block, layer) computes the four heads'
+// any layer score 0.  Sixteen lanes per (block, layer) compute each head's
 // dot products with a lane-then-tree reduction (the reference sums in
 // channel order: results agree to ~1e-7 of the norms).  HBM-bound: the
 // 16 x 2048-block scorer reads 128 MiB of fp32 sums.
@@ -85,71 +85,117 @@ __global__ __launch_bounds__(256) void q_accumulate_kernel(const QT *q, const ui
     *dst = acc;
 }
 
-// One thread per (layer, KV head): the group's query sum scaled by invq,
-// and its squared norm summed in channel order.
-__global__ __launch_bounds__(64) void meank_query_kernel(const float *q_sum, const float *invq,
-                                                         uint32_t L, uint32_t Hq, uint32_t Hkv,
-                                                         uint32_t D, float *qv, float *nq) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= L * Hkv) {
-        return;
-    }
+// One workgroup per (layer, KV head), one thread per channel: the group's
+// query sum (heads added in group order) scaled by invq, and its squared
+// norm reduced over the channels.
+__global__ __launch_bounds__(256) void meank_query_kernel(const float *q_sum, const float *invq,
+                                                          uint32_t L, uint32_t Hq, uint32_t Hkv,
+                                                          uint32_t D, float *qv, float *nq) {
+    __shared__ float part[4];
+    const uint32_t i = blockIdx.x;  // l * Hkv + h
+    const uint32_t d = threadIdx.x;
     const uint32_t l = i / Hkv;
     const uint32_t h = i - l * Hkv;
     const uint32_t g = Hq / Hkv;
-    const float inv = invq[l];
-    float n = 0.0f;
-    for (uint32_t d = 0; d < D; ++d) {
+    float v = 0.0f;
+    if (d < D) {
         float acc = 0.0f;
         for (uint32_t gi = 0; gi < g; ++gi) {
             acc += q_sum[(static_cast<uint64_t>(l) * Hq + h * g + gi) * D + d];
         }
-        const float v = acc * inv;
+        v = acc * invq[l];
         qv[static_cast<uint64_t>(i) * D + d] = v;
-        n += v * v;
     }
-    nq[i] = n;
+    float n = v * v;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        n += __shfl_xor(n, off, 64);
+    }
+    if ((threadIdx.x & 63u) == 0u) {
+        part[threadIdx.x >> 6] = n;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = 0.0f;
+        for (uint32_t w = 0; w < (blockDim.x + 63u) / 64u; ++w) {
+            t += part[w];
+        }
+        nq[i] = t;
+    }
 }
 
+// Sum of v over the 16 lanes of a DPP row (quad permutes, bank-masked row
+// shifts for distance 4, row rotation by 8); every lane must be active.
+__device__ inline float row16_sum(float v) {
+    int x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));  // ^1
+    x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));  // ^2
+    x = __float_as_int(v);
+    const int t = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0x5, false);        // +4 (banks 0, 2)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(t, x, 0x114, 0xF, 0xA, false));  // -4 (banks 1, 3)
+    x = __float_as_int(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));  // ^8
+    return v;
+}
+
+// 16 lanes per (layer, block) item, 16 items per 256-thread workgroup.  A
+// lane holds D/16 channels of each head as float4s; the next head's sums are
+// loaded before the current head is reduced.
 template <int D>
 __global__ __launch_bounds__(256) void meank_cos_kernel(const float *k_sum, const uint32_t *mean_tokens,
                                                         const float *qv, const float *nq,
                                                         const float *invq, uint32_t L, uint32_t B,
                                                         uint32_t cap, uint32_t Hkv, double *layer_cos) {
-    constexpr int PER = D / 64;  // channels per lane per head
-    const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const uint32_t lane = threadIdx.x & 63u;
-    if (wave >= L * B) {
-        return;
-    }
-    const uint32_t l = wave / B;
-    const uint32_t b = wave - l * B;
-    if (invq[l] == 0.0f) {
-        return;  // layer without query rows
-    }
-    const uint32_t mt = mean_tokens[static_cast<uint64_t>(l) * cap + b];
+    constexpr int P4 = D / 64;  // float4s per lane per head
+    const uint32_t item = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+    const uint32_t sub = threadIdx.x & 15u;
+    const bool live = item < L * B;
+    const uint32_t l = live ? item / B : 0u;
+    const uint32_t b = live ? item - l * B : 0u;
+    const bool scored = live && invq[l] != 0.0f;  // layers without query rows are skipped
+    const uint32_t mt = scored ? mean_tokens[static_cast<uint64_t>(l) * cap + b] : 0u;
     const float inv = mt ? 1.0f / static_cast<float>(mt) : 0.0f;
-    const float *ks = k_sum + (static_cast<uint64_t>(l) * cap + b) * Hkv * D;
+    const float4 *ks = reinterpret_cast<const float4 *>(k_sum + (static_cast<uint64_t>(l) * cap + b) * Hkv * D);
+    const float4 *qs = reinterpret_cast<const float4 *>(qv + static_cast<uint64_t>(l) * Hkv * D);
+    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 kc[P4], qc[P4];
+#pragma unroll
+    for (int j = 0; j < P4; ++j) {
+        kc[j] = mt ? ks[j * 16 + sub] : zero;
+        qc[j] = scored ? qs[j * 16 + sub] : zero;
+    }
     double layer = 0.0;
     for (uint32_t h = 0; h < Hkv; ++h) {
-        const float *q = qv + (static_cast<uint64_t>(l) * Hkv + h) * D;
+        float4 kn[P4], qn[P4];
+        const bool more = h + 1 < Hkv;
+#pragma unroll
+        for (int j = 0; j < P4; ++j) {
+            kn[j] = (more && mt) ? ks[(h + 1) * (D / 4) + j * 16 + sub] : zero;
+            qn[j] = (more && scored) ? qs[(h + 1) * (D / 4) + j * 16 + sub] : zero;
+        }
         float dot = 0.0f, nk = 0.0f;
 #pragma unroll
-        for (int j = 0; j < PER; ++j) {
-            const uint32_t d = lane * PER + j;
-            const float m = mt ? ks[h * D + d] * inv : 0.0f;
-            dot += q[d] * m;
-            nk += m * m;
-        }
+        for (int j = 0; j < P4; ++j) {
+            const float m[4] = {kc[j].x * inv, kc[j].y * inv, kc[j].z * inv, kc[j].w * inv};
+            const float q[4] = {qc[j].x, qc[j].y, qc[j].z, qc[j].w};
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            dot += __shfl_xor(dot, off, 64);
-            nk += __shfl_xor(nk, off, 64);
+            for (int e = 0; e < 4; ++e) {
+                dot += q[e] * m[e];
+                nk += m[e] * m[e];
+            }
         }
-        const float c = dot / (sqrtf(nq[l * Hkv + h]) * sqrtf(nk) + 1e-6f);
+        dot = row16_sum(dot);
+        nk = row16_sum(nk);
+        const float c = dot / (sqrtf(scored ? nq[l * Hkv + h] : 0.0f) * sqrtf(nk) + 1e-6f);
         layer += static_cast<double>(c);
+#pragma unroll
+        for (int j = 0; j < P4; ++j) {
+            kc[j] = kn[j];
+            qc[j] = qn[j];
+        }
     }
-    if (lane == 0) {
+    if (scored && sub == 0u) {
         layer_cos[static_cast<uint64_t>(l) * B + b] = layer;
     }
 }
@@ -286,6 +332,9 @@ int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {
     if (a->n_head_kv == 0 || a->n_head % a->n_head_kv != 0 || (D != 128 && D != 256) || cap < B) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "score_meank: bad head geometry");
     }
+    if (reinterpret_cast<uintptr_t>(a->k_sum) & 15u) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "score_meank: k_sum must be 16-byte aligned");
+    }
     if (L == 0 || B == 0) {
         return KVMEM_HIP_OK;
     }
@@ -298,7 +347,8 @@ int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {
     }
     (void) hipSetDevice(ctx->device);
     const size_t qv_bytes = sizeof(float) * static_cast<size_t>(L) * a->n_head_kv * (D + 1);
-    const size_t cos_bytes = sizeof(double) * static_cast<size_t>(L) * B;
+    // the fp32 query vectors start 256-byte aligned (read as float4)
+    const size_t cos_bytes = (sizeof(double) * static_cast<size_t>(L) * B + 255) & ~static_cast<size_t>(255);
     if (!ensure_dev(ctx, ctx->meank_scratch, qv_bytes + cos_bytes + 256, "score_meank scratch")) {
         return KVMEM_HIP_ERR_NOMEM;
     }
@@ -313,10 +363,10 @@ int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {
     }
     perf_begin(ctx, kPerfScore);
     const uint32_t lh = L * a->n_head_kv;
-    meank_query_kernel<<<(lh + 63) / 64, 64, 0, ctx->stream>>>(a->q_sum, invq_dev, L, a->n_head,
-                                                              a->n_head_kv, D, qv, nq);
-    const uint64_t waves = static_cast<uint64_t>(L) * B;
-    const uint32_t grid = static_cast<uint32_t>((waves * 64 + 255) / 256);
+    meank_query_kernel<<<lh, D, 0, ctx->stream>>>(a->q_sum, invq_dev, L, a->n_head, a->n_head_kv, D,
+                                                  qv, nq);
+    const uint64_t items = static_cast<uint64_t>(L) * B;  // 16 lanes each
+    const uint32_t grid = static_cast<uint32_t>((items * 16 + 255) / 256);
     if (D == 256) {
         meank_cos_kernel<256><<<grid, 256, 0, ctx->stream>>>(a->k_sum, a->mean_tokens, qv, nq, invq_dev,
                                                              L, B, cap, a->n_head_kv, layer_cos);
