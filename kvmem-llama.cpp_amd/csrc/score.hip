@@ -8,14 +8,17 @@
 // so no score ever goes to memory.
 //
 // Mapping.  A workgroup of 4 waves (one per SIMD) owns one (layer, KV head,
-// 384-row slice) and a contiguous range of blocks.  Each wave keeps 96
-// query rows resident in VGPRs as f16 A-fragments of
-// v_mfma_f32_16x16x32_f16 (loaded once; bf16 queries are converted to f16
-// on the way, exact for normal-range values), so every 16-byte B-fragment
-// read from LDS feeds six MFMAs.  A block's K tile (128 keys x head_dim
-// halves of one KV head) moves HBM -> LDS with global_load_lds_dwordx4
-// (no register staging) into one of two LDS buffers while the other
-// buffer's block is multiplied: one barrier per block.  Inside a tile the
+// 384-row slice) and a contiguous range of blocks; two workgroups share a
+// CU, so each SIMD runs two waves that cover each other's barrier and
+// load waits.  Each wave keeps 96 query rows resident in VGPRs as f16
+// A-fragments of v_mfma_f32_16x16x32_f16 (loaded once; bf16 queries are
+// converted to f16 on the way, exact for normal-range values), so every
+// 16-byte B-fragment read from LDS feeds six MFMAs.  Half a block's K tile
+// (64 keys x head_dim halves of one KV head, 32 KiB) moves HBM -> LDS with
+// global_load_lds_dwordx4 (no register staging) into one of two LDS
+// buffers while the other buffer's keys are multiplied: one barrier per
+// half block.  The per-block max over the wave's lanes uses DPP and the
+// row-swap permutes, not LDS.  Inside a tile the
 // 16-byte chunk c of key j sits at chunk position c ^ (j mod chunks-per-
 // key), so the 16 keys of a B-fragment read hit 16 different bank groups;
 // the swizzle is applied on the global side (each lane of a direct LDS load
@@ -50,7 +53,8 @@ constexpr int kScoreThreads = kScoreWaves * 64;
 constexpr int kRowTiles = 6;                               // 16-row tiles per wave
 constexpr int kRowsPerWave = kRowTiles * 16;               // 96
 constexpr int kRowsPerGroup = kScoreWaves * kRowsPerWave;  // 384
-constexpr int kMaxTokens = 128;                            // keys per LDS tile
+constexpr int kMaxTokens = 128;                            // keys per block (at most)
+constexpr int kTileKeys = 64;                              // keys per LDS tile (half a block)
 
 struct ScoreParams {
     const uint16_t *q;       // [L][Tq][Hq][D] bf16 or f16 bits
@@ -65,6 +69,28 @@ struct ScoreParams {
     float scale;             // 1/sqrt(D)
 };
 
+// Max over the 64 lanes of a wave without LDS: DPP within each 16-lane row
+// (quad permutes, then row rotations by 4 and 8; max is idempotent, so the
+// overlapping windows are harmless), then the gfx950 row swaps, which hand
+// every lane the value of the other 16-lane row and of the other 32-lane
+// half.  Every lane ends with the wave maximum.
+__device__ inline float wave_max(float m) {
+    int x = __float_as_int(m);
+    m = __builtin_fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false)));
+    x = __float_as_int(m);
+    m = __builtin_fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false)));
+    x = __float_as_int(m);
+    m = __builtin_fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x124, 0xF, 0xF, false)));
+    x = __float_as_int(m);
+    m = __builtin_fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x128, 0xF, 0xF, false)));
+    const uint32_t u = __float_as_uint(m);
+    const auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    m = __builtin_fmaxf(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+    const uint32_t v = __float_as_uint(m);
+    const auto s32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return __builtin_fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+}
+
 __device__ inline _Float16 q_elem_to_half(uint16_t bits, bool bf16) {
     if (bf16) {
         const float f = __uint_as_float(static_cast<uint32_t>(bits) << 16);
@@ -74,11 +100,11 @@ __device__ inline _Float16 q_elem_to_half(uint16_t bits, bool bf16) {
 }
 
 template <int D>
-__global__ __launch_bounds__(kScoreThreads, 1) void score_kernel(ScoreParams p) {
+__global__ __launch_bounds__(kScoreThreads, 2) void score_kernel(ScoreParams p) {
     constexpr int KS = D / 32;                       // k-steps of 32
     constexpr int ROW_BYTES = D * 2;                 // one key of one head
     constexpr int CH = D / 8;                        // 16-byte chunks per key
-    constexpr int TILE = kMaxTokens * ROW_BYTES;     // 64 KiB (D = 256)
+    constexpr int TILE = kTileKeys * ROW_BYTES;      // 32 KiB (D = 256)
     constexpr int LOADS = TILE / 1024;               // wave-wide 1 KiB loads per tile
     constexpr int LOADS_PER_WAVE = LOADS / kScoreWaves;
     static_assert(LOADS % kScoreWaves == 0, "tile must split over the waves");
@@ -123,24 +149,32 @@ __global__ __launch_bounds__(kScoreThreads, 1) void score_kernel(ScoreParams p) 
 
     // ---- K tiles: direct HBM -> LDS, swizzled chunk order
     const uint64_t key_stride = static_cast<uint64_t>(p.Hkv) * ROW_BYTES;
-    auto issue_tile = [&](uint32_t b, int buf) {
+    // tile `it` = keys [64*(it&1), 64*(it&1) + 64) of block b_begin + it/2
+    auto issue_tile = [&](uint32_t it, int buf) {
+        const uint32_t b = b_begin + (it >> 1);
+        const uint32_t k0 = (it & 1u) * kTileKeys;
         const uint8_t *base = p.k + ((static_cast<uint64_t>(l) * p.cap + b) * p.T) * key_stride +
                               static_cast<uint64_t>(h) * ROW_BYTES;
         const uint32_t nt = (b + 1 == p.B && p.last_T != 0) ? p.last_T : p.T;
+        // the lane id passes through an empty asm so the per-load offsets
+        // are recomputed here (a few VALU per tile) instead of being kept
+        // live across the loop next to the 192 registers of query rows
+        uint32_t ln = lane;
+        asm volatile("" : "+v"(ln));
 #pragma unroll
         for (int i = 0; i < LOADS_PER_WAVE; ++i) {
             const uint32_t inst = wave * LOADS_PER_WAVE + i;
-            const uint32_t slot = inst * 64u + lane;            // 16-byte LDS slot
-            const uint32_t j = slot / CH;                       // key
+            const uint32_t slot = inst * 64u + ln;              // 16-byte LDS slot
+            const uint32_t j = slot / CH;                       // key within the tile
             const uint32_t c = (slot % CH) ^ (j % CH);          // global chunk held there
-            const uint32_t jj = min(j, nt - 1u);                // duplicate the last key
+            const uint32_t jj = min(k0 + j, nt - 1u);           // duplicate the last key
             const uint8_t *src = base + jj * key_stride + c * 16u;
             __builtin_amdgcn_global_load_lds(
                 src, (lds_void_t *) (&tiles[buf][inst * 1024u]), 16, 0, 0);
         }
     };
 
-    issue_tile(b_begin, 0);
+    issue_tile(0u, 0);
 
     // ---- query rows -> A fragments (resident for the whole workgroup)
     half8_t a[kRowTiles][KS];
@@ -167,19 +201,20 @@ __global__ __launch_bounds__(kScoreThreads, 1) void score_kernel(ScoreParams p) 
 
     float *out = p.partial +
                  ((static_cast<uint64_t>(rg * kScoreWaves + wave) * p.L + l) * p.Hkv + h) * p.B;
-    for (uint32_t b = b_begin; b < b_end; ++b) {
-        const int buf = static_cast<int>((b - b_begin) & 1u);
-        // this thread's loads of tile b have landed; after the barrier every
+    const uint32_t n_tiles = 2u * (b_end - b_begin);
+    float m = -FLT_MAX;
+    for (uint32_t it = 0; it < n_tiles; ++it) {
+        const int buf = static_cast<int>(it & 1u);
+        // this thread's loads of tile it have landed; after the barrier every
         // thread's have, and every wave is done reading the other buffer
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (b + 1 < b_end) {
-            issue_tile(b + 1, buf ^ 1);
+        if (it + 1 < n_tiles) {
+            issue_tile(it + 1, buf ^ 1);
         }
         const uint8_t *tile = tiles[buf];
-        float m = -FLT_MAX;
 #pragma unroll
-        for (int kt = 0; kt < kMaxTokens / 16; ++kt) {
+        for (int kt = 0; kt < kTileKeys / 16; ++kt) {
             const uint32_t key = kt * 16 + lrow;
             const uint8_t *krow = tile + key * ROW_BYTES;
             float4_t acc[kRowTiles];
@@ -209,19 +244,19 @@ __global__ __launch_bounds__(kScoreThreads, 1) void score_kernel(ScoreParams p) 
         // LDS read before a consumer, so reads further ahead would not help.)
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
 #pragma unroll
-        for (int f = 0; f < (kMaxTokens / 16) * KS - 1; ++f) {
+        for (int f = 0; f < (kTileKeys / 16) * KS - 1; ++f) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, kRowTiles - 1, 0);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, kRowTiles, 0);
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            m = __builtin_fmaxf(m, __shfl_xor(m, off, 64));
-        }
-        if (lane == 0) {
-            out[b] = m * p.scale;
+        if (it & 1u) {  // both halves of the block are in m
+            m = wave_max(m);
+            if (lane == 0) {
+                out[b_begin + (it >> 1)] = m * p.scale;
+            }
+            m = -FLT_MAX;
         }
     }
 }
@@ -324,9 +359,9 @@ extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist
     p.q_bf16 = args->q_type == KVMEM_TYPE_BF16;
     p.scale = 1.0f / std::sqrt(static_cast<float>(D));
     const uint32_t pairs = L * p.Hkv;
-    // one workgroup per CU holds the LDS double buffer; a few workgroups
-    // per CU over the launch keep every XCD busy to the end
-    const uint32_t target = 1024;
+    // two workgroups per CU hold their LDS double buffers; eight per CU
+    // over the launch keep every XCD busy to the end
+    const uint32_t target = 2048;
     const uint32_t per_chunk_target = std::max<uint32_t>(1, target / std::max<uint32_t>(1, pairs * p.RG));
     p.n_chunks = std::min(B, per_chunk_target);
     p.blocks_per_chunk = (B + p.n_chunks - 1) / p.n_chunks;
