@@ -234,6 +234,49 @@ KVMEM_HIP_API int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx,
                                                 const uint32_t *slots,
                                                 uint32_t n);
 
+/* Packed host rows: the pool's own row formats kept in pinned host memory
+ * per block, as the reference's RawKvStore keeps packed GPU rows per (block,
+ * layer) (k_gpu / v_gpu, kvmem/include/kvmem/raw_kv_store.hpp:98-117).
+ * Block-major: block b occupies one span of
+ *     n_layers * block_tokens * (row_k + row_v) bytes
+ * laid out [layer][block_tokens rows of K][block_tokens rows of V], rows of
+ * kvmem_hip_row_size(pool type, n_embd) bytes; a block of n_tokens rows
+ * uses the first n_tokens rows of each run. */
+typedef struct kvmem_hip_packed_host {
+    void *base;                 /* pinned host memory */
+    uint32_t n_layers;
+    uint32_t n_blocks;          /* blocks the memory holds */
+    uint32_t block_tokens;
+} kvmem_hip_packed_host;
+
+/* Stage-out: copy the packed rows of pool slot slots[i] (every layer, K and
+ * V, n_tokens[i] rows) to block block_ids[i] of the packed host store.
+ * The rows are gathered into a device ring in the host layout by one copy
+ * launch per 32 MiB batch on the context stream, then copied device-to-host
+ * on the side stream, so a later call's gathers overlap earlier copies.
+ * Asynchronous: the host rows are complete after kvmem_hip_sync.  Replaces
+ * kvmem_stageout_enqueue / submit / wait (llama-kvmem-stagein.h:40-47,
+ * stagein.cu:842-963: gather kernel into a 32 MiB slab, D2H into two
+ * pinned slabs) and the per-block harvest of packed rows
+ * (llama-memory-kvmem.cpp:2317-2394). */
+KVMEM_HIP_API int kvmem_hip_stageout_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool,
+                                            const kvmem_hip_packed_host *dst,
+                                            const uint32_t *block_ids, const uint32_t *slots,
+                                            const uint32_t *n_tokens, uint32_t n);
+
+/* Stage-in of packed rows, the reference's live path (write_block_to_gpu:
+ * copy_k_gpu / copy_v_gpu into the slab, enqueue_v, flush,
+ * llama-memory-kvmem.cpp:2726-2791): block spans go host-to-device into
+ * the device ring on the side stream, and one copy launch per batch
+ * scatters them into slot slots[i] of every layer (n_tokens[i] rows), no
+ * quantization.  The pool transform (xf) does not apply: packed rows are
+ * already in the cache's form. */
+KVMEM_HIP_API int kvmem_hip_stagein_packed_host(kvmem_hip_ctx *ctx,
+                                                const kvmem_hip_packed_host *src,
+                                                const kvmem_hip_pool *pool,
+                                                const uint32_t *block_ids, const uint32_t *slots,
+                                                const uint32_t *n_tokens, uint32_t n);
+
 /* Move whole slots inside the pool: slot src_slots[i] -> dst_slots[i] for
  * every layer, K and V (quantized bytes copied unchanged).  Overlapping
  * moves are hazard-free: sources are gathered to device scratch first.

@@ -46,13 +46,16 @@ extern "C" {
 typedef struct kvmem_plan_stats {
     uint32_t n_stage_in;               /* blocks entering the working set */
     uint32_t n_stage_out;              /* resident blocks leaving it */
-    uint32_t n_staged;                 /* blocks quantized into the pool */
+    uint32_t n_staged;                 /* blocks written into the pool (quantized
+                                          or restored from packed rows) */
     uint32_t n_moved;                  /* resident blocks moved (canonical layout) */
     uint32_t selection_overlap_blocks;
     uint32_t gpu_reused_blocks;
     uint32_t retained_position_stable;
     uint32_t retained_position_moved;
     uint32_t total_window_tokens;
+    uint32_t n_saved;                  /* evicted blocks copied to the packed host store */
+    uint32_t n_restored;               /* staged blocks restored from packed rows */
 } kvmem_plan_stats;
 
 /* ----------------------------------------------------------- host store */
@@ -169,6 +172,23 @@ KVMEM_HIP_API int kvmem_engine_set_device_history(kvmem_engine *e, const void *k
  * device history.  NULL clears it. */
 KVMEM_HIP_API int kvmem_engine_set_host_history(kvmem_engine *e, const void *pinned_base,
                                                 uint32_t capacity_blocks);
+/* Packed host store (see kvmem_hip_packed_host), pinned, capacity_blocks
+ * block spans in the pool's row formats, as the reference keeps packed GPU
+ * rows per block (RawKvStore k_gpu / v_gpu).  When set:
+ *   - apply copies every evicted full block whose packed rows the store
+ *     does not hold yet to it (apply_plan_to_kv's stage-out of missing
+ *     packed rows, llama-memory-kvmem.cpp:784-830);
+ *   - with pinned host history, a selected block the store holds is
+ *     restored from its packed rows (half the PCIe bytes of F16 at q8_0)
+ *     instead of being quantized again (write_block_to_gpu,
+ *     :2726-2791).  With device history the quantizing stage-in from HBM
+ *     stays faster and is kept.
+ * A block's packed rows are dropped when its history changes (truncate,
+ * new history).  NULL clears the store. */
+KVMEM_HIP_API int kvmem_engine_set_packed_host(kvmem_engine *e, void *pinned_base,
+                                               uint32_t capacity_blocks);
+/* 1 if the packed host store holds block_id's rows. */
+KVMEM_HIP_API int kvmem_engine_packed_valid(const kvmem_engine *e, uint32_t block_id);
 /* The history grew (caller wrote the new tokens): register_append.
  * Bumps the epoch. */
 KVMEM_HIP_API int kvmem_engine_append_tokens(kvmem_engine *e, uint32_t n_new_tokens);

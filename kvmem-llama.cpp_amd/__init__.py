@@ -86,6 +86,11 @@ class Pool(C.Structure):
                 ("v_layers", C.POINTER(C.c_void_p)), ("xf", C.POINTER(Transform))]
 
 
+class PackedHost(C.Structure):
+    _fields_ = [("base", C.c_void_p), ("n_layers", C.c_uint32), ("n_blocks", C.c_uint32),
+                ("block_tokens", C.c_uint32)]
+
+
 class ScoreArgs(C.Structure):
     _fields_ = [("q", C.c_void_p), ("q_type", C.c_int32), ("n_q_tokens", C.c_uint32),
                 ("n_head", C.c_uint32), ("n_head_kv", C.c_uint32), ("head_dim", C.c_uint32),
@@ -148,6 +153,10 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_meank_sums", i32, vp, C.POINTER(History), pu32, u32, vp, vp)
     _sig(lib, "kvmem_hip_score_meank", i32, vp, C.POINTER(MeanKArgs))
     _sig(lib, "kvmem_hip_q_accumulate", i32, vp, vp, i32, u32, u32, u32, pu32, u32, i32, vp)
+    _sig(lib, "kvmem_hip_stageout_blocks", i32, vp, C.POINTER(Pool), C.POINTER(PackedHost), pu32, pu32,
+         pu32, u32)
+    _sig(lib, "kvmem_hip_stagein_packed_host", i32, vp, C.POINTER(PackedHost), C.POINTER(Pool), pu32, pu32,
+         pu32, u32)
     _sig(lib, "kvmem_hip_perf_enable", i32, vp, i32)
     _sig(lib, "kvmem_hip_perf_get", i32, vp, C.POINTER(Perf))
     _sig(lib, "kvmem_hip_perf_reset", None, vp)
@@ -271,6 +280,24 @@ class Context:
         assert n == m
         self.check(self.lib.kvmem_hip_stagein_blocks(self.h, C.byref(hist), C.byref(pool), ids, sl, n),
                    "stagein_blocks")
+
+    def stageout_blocks(self, pool: Pool, dst: PackedHost, block_ids, slots, n_tokens) -> None:
+        """Pool slots -> packed host blocks (asynchronous until sync())."""
+        ids, n = _u32_array(block_ids)
+        sl, m = _u32_array(slots)
+        nt, k = _u32_array(n_tokens)
+        assert n == m == k
+        self.check(self.lib.kvmem_hip_stageout_blocks(self.h, C.byref(pool), C.byref(dst), ids, sl, nt, n),
+                   "stageout_blocks")
+
+    def stagein_packed_host(self, src: PackedHost, pool: Pool, block_ids, slots, n_tokens) -> None:
+        """Packed host blocks -> pool slots, no quantization."""
+        ids, n = _u32_array(block_ids)
+        sl, m = _u32_array(slots)
+        nt, k = _u32_array(n_tokens)
+        assert n == m == k
+        self.check(self.lib.kvmem_hip_stagein_packed_host(self.h, C.byref(src), C.byref(pool), ids, sl, nt, n),
+                   "stagein_packed_host")
 
     def stagein_blocks_host(self, hist: HostHistory, pool: Pool, block_ids, slots) -> None:
         ids, n = _u32_array(block_ids)

@@ -2,6 +2,8 @@
 // batched device copy of libkvmem_hip.so.
 #include "kvmem_internal.hpp"
 
+#include <algorithm>
+
 #include <cstring>
 #include <new>
 #include <vector>
@@ -156,12 +158,6 @@ void perf_collect(kvmem_hip_ctx *ctx) {
 // Batched byte copies: one workgroup per op, 16-byte vectors when both
 // addresses and the size are 16-byte aligned.
 // ------------------------------------------------------------------------
-struct CopyOpDev {
-    const uint8_t *src;
-    uint8_t *dst;
-    uint64_t nbytes;
-};
-
 __global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops, int n) {
     const int i = blockIdx.x;
     if (i >= n) {
@@ -181,6 +177,59 @@ __global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops,
     for (uint64_t j = threadIdx.x; j < op.nbytes; j += blockDim.x) {
         op.dst[j] = op.src[j];
     }
+}
+
+bool launch_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, const char *what) {
+    if (ops.empty()) {
+        return true;
+    }
+    if (ops.size() > 0x7fffffffu) {
+        fail(ctx, KVMEM_HIP_ERR_INVALID, std::string(what) + ": too many copies");
+        return false;
+    }
+    void *dops = upload(ctx, ops.data(), ops.size() * sizeof(CopyOpDev), what);
+    if (!dops) {
+        return false;
+    }
+    batched_copy_kernel<<<static_cast<uint32_t>(ops.size()), 256, 0, ctx->stream>>>(
+        static_cast<const CopyOpDev *>(dops), static_cast<int>(ops.size()));
+    return hip_ok(ctx, hipGetLastError(), what);
+}
+
+bool ensure_h2d_ring(kvmem_hip_ctx *ctx, size_t min_slot_bytes) {
+    const size_t want = std::max<size_t>(size_t{32} << 20, min_slot_bytes);
+    if (ctx->h2d_ring.ptr && ctx->h2d_slot_bytes >= want) {
+        return true;
+    }
+    // earlier users of the ring must be done before it is replaced
+    if (!hip_ok(ctx, hipStreamSynchronize(ctx->copy_stream), "h2d ring sync") ||
+        !hip_ok(ctx, hipStreamSynchronize(ctx->stream), "h2d ring sync")) {
+        return false;
+    }
+    if (ctx->h2d_ring.ptr) {
+        (void) hipFree(ctx->h2d_ring.ptr);
+        ctx->h2d_ring.ptr = nullptr;
+        ctx->h2d_ring.bytes = 0;
+    }
+    if (!ensure_dev(ctx, ctx->h2d_ring, want * kH2dRing, "h2d ring")) {
+        ctx->h2d_slot_bytes = 0;
+        return false;
+    }
+    ctx->h2d_slot_bytes = want;
+    ctx->h2d_slots = kH2dRing;
+    for (int r = 0; r < kH2dRing; ++r) {
+        if (!ctx->h2d_copied[r]) {
+            if (!hip_ok(ctx, hipEventCreateWithFlags(&ctx->h2d_copied[r], hipEventDisableTiming), "h2d event") ||
+                !hip_ok(ctx, hipEventCreateWithFlags(&ctx->h2d_consumed[r], hipEventDisableTiming), "h2d event")) {
+                return false;
+            }
+        }
+        // a fresh "consumed" marker on the compute stream
+        if (!hip_ok(ctx, hipEventRecord(ctx->h2d_consumed[r], ctx->stream), "h2d event")) {
+            return false;
+        }
+    }
+    return true;
 }
 
 }  // namespace kvmem_hip
@@ -231,13 +280,17 @@ void kvmem_hip_destroy(kvmem_hip_ctx *ctx) {
         if (s.done) hipEventDestroy(s.done);
     }
     for (DevBuf *b : {&ctx->score_partial, &ctx->score_layers, &ctx->meank_scratch,
-                      &ctx->move_scratch, &ctx->topk_sel, &ctx->h2d_ring}) {
+                      &ctx->move_scratch, &ctx->topk_sel, &ctx->h2d_ring, &ctx->d2h_ring}) {
         if (b->ptr) hipFree(b->ptr);
     }
     if (ctx->topk_sel_host.ptr) hipHostFree(ctx->topk_sel_host.ptr);
     for (int i = 0; i < 8; ++i) {
         if (ctx->h2d_copied[i]) hipEventDestroy(ctx->h2d_copied[i]);
         if (ctx->h2d_consumed[i]) hipEventDestroy(ctx->h2d_consumed[i]);
+    }
+    for (int i = 0; i < 2; ++i) {
+        if (ctx->d2h_gathered[i]) hipEventDestroy(ctx->d2h_gathered[i]);
+        if (ctx->d2h_done[i]) hipEventDestroy(ctx->d2h_done[i]);
     }
     for (int s = 0; s < kPerfStages; ++s) {
         if (ctx->perf_open[s]) hipEventDestroy(ctx->perf_open[s]);

@@ -65,6 +65,13 @@ struct kvmem_hip_ctx {
     hipEvent_t h2d_copied[8] = {};
     hipEvent_t h2d_consumed[8] = {};
 
+    // stage-out: device ring the pool rows are gathered into before D2H
+    kvmem_hip::DevBuf d2h_ring;
+    size_t d2h_slot_bytes = 0;
+    int d2h_next = 0;
+    hipEvent_t d2h_gathered[2] = {};
+    hipEvent_t d2h_done[2] = {};
+
     // profiling: start/end event pairs per stage, harvested when read
     bool perf_on = false;
     std::vector<hipEvent_t> perf_free;                       // reusable events
@@ -85,6 +92,22 @@ bool hip_ok(kvmem_hip_ctx *ctx, hipError_t e, const char *what);
 
 bool ensure_dev(kvmem_hip_ctx *ctx, DevBuf &b, size_t bytes, const char *what);
 bool ensure_pin(kvmem_hip_ctx *ctx, PinBuf &b, size_t bytes, const char *what);
+
+// One device byte copy of the batched copy kernel.
+struct CopyOpDev {
+    const uint8_t *src;
+    uint8_t *dst;
+    uint64_t nbytes;
+};
+
+// Upload `ops` and copy them in one launch on the context stream (one
+// workgroup per op, 16-byte vectors where aligned).
+bool launch_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, const char *what);
+
+// The pinned-host stage-in ring: kH2dRing device slots of at least
+// `min_slot_bytes` (32 MiB or more, grown only), with their events.
+constexpr int kH2dRing = 4;
+bool ensure_h2d_ring(kvmem_hip_ctx *ctx, size_t min_slot_bytes);
 
 // Copy `bytes` of host data to device memory through the upload ring,
 // ordered on the context stream.  Returns the device address or nullptr.

@@ -56,10 +56,13 @@ private:
     SlotPool pool_;
 };
 
-void fill_stats(const Plan &p, uint32_t n_staged, uint32_t n_moved, kvmem_plan_stats *st) {
+void fill_stats(const Plan &p, uint32_t n_staged, uint32_t n_moved, uint32_t n_saved,
+                uint32_t n_restored, kvmem_plan_stats *st) {
     if (!st) {
         return;
     }
+    st->n_saved = n_saved;
+    st->n_restored = n_restored;
     st->n_stage_in = static_cast<uint32_t>(p.stage_in.size());
     st->n_stage_out = static_cast<uint32_t>(p.stage_out.size());
     st->n_staged = n_staged;
@@ -181,7 +184,7 @@ int kvmem_store_apply(kvmem_store *s, const uint32_t *sel, uint32_t n_sel, uint3
     if (n_out) {
         *n_out = static_cast<uint32_t>(p.stage_out.size());
     }
-    fill_stats(p, static_cast<uint32_t>(s->slots.staged_ids.size()), 0, stats);
+    fill_stats(p, static_cast<uint32_t>(s->slots.staged_ids.size()), 0, 0, 0, stats);
     return KVMEM_HIP_OK;
 }
 
@@ -234,6 +237,9 @@ struct kvmem_engine {
     uint32_t meank_cap = 0;    // capacity the sums are allocated for
     uint32_t meank_valid = 0;  // leading blocks whose sums are current
     float *d_qsum = nullptr;   // query sums [L][n_head*head_dim] (mean-K scorer)
+    void *packed_base = nullptr;        // pinned packed host store (may be null)
+    uint32_t packed_capacity = 0;       // blocks it holds
+    std::vector<uint8_t> packed_valid;  // block's packed rows are in the store
     kvmem_hip_transform xf{};  // cache row transform (unused when has_xf is false)
     std::vector<float> theta;  // RoPE pair frequencies
     bool has_xf = false;
@@ -297,15 +303,53 @@ struct kvmem_engine {
 
 namespace {
 
+kvmem_hip_packed_host packed_desc(const kvmem_engine *e) {
+    kvmem_hip_packed_host ph{};
+    ph.base = e->packed_base;
+    ph.n_layers = e->p.n_layers;
+    ph.n_blocks = e->packed_capacity;
+    ph.block_tokens = e->p.block_tokens;
+    return ph;
+}
+
+// Write blocks `ids` into pool slots `slots`: from the packed host store
+// when the history is on the host and the store holds the block, else by
+// quantizing the F16 history (device or pinned host).
 int engine_stage(kvmem_engine *e, const std::vector<uint32_t> &ids,
-                 const std::vector<uint32_t> &slots) {
+                 const std::vector<uint32_t> &slots, uint32_t *n_restored) {
+    *n_restored = 0;
     if (ids.empty()) {
         return KVMEM_HIP_OK;
     }
     const kvmem_hip_pool pool = e->pool_desc();
     const uint32_t n_blocks = e->rt.store().block_count();
     const uint32_t last = e->last_block_tokens();
-    int rc;
+    std::vector<uint32_t> q_ids, q_slots;
+    std::vector<uint32_t> p_ids, p_slots, p_nt;
+    for (size_t i = 0; i < ids.size(); ++i) {
+        const uint32_t id = ids[i];
+        if (e->host_base && e->packed_base && id < e->packed_capacity && e->packed_valid[id]) {
+            p_ids.push_back(id);
+            p_slots.push_back(slots[i]);
+            p_nt.push_back(e->p.block_tokens);  // only full blocks are kept
+        } else {
+            q_ids.push_back(id);
+            q_slots.push_back(slots[i]);
+        }
+    }
+    int rc = KVMEM_HIP_OK;
+    if (!p_ids.empty()) {
+        const kvmem_hip_packed_host ph = packed_desc(e);
+        rc = kvmem_hip_stagein_packed_host(e->ctx, &ph, &pool, p_ids.data(), p_slots.data(), p_nt.data(),
+                                           static_cast<uint32_t>(p_ids.size()));
+        if (rc != KVMEM_HIP_OK) {
+            return e->fail_ctx(rc, "packed stage-in");
+        }
+        *n_restored = static_cast<uint32_t>(p_ids.size());
+    }
+    if (q_ids.empty()) {
+        return KVMEM_HIP_OK;
+    }
     if (e->host_base) {
         kvmem_hip_host_history h{};
         h.base = e->host_base;
@@ -315,12 +359,12 @@ int engine_stage(kvmem_engine *e, const std::vector<uint32_t> &ids,
         h.n_embd_k = e->n_embd_k;
         h.n_embd_v = e->n_embd_v;
         h.last_block_tokens = last;
-        rc = kvmem_hip_stagein_blocks_host(e->ctx, &h, &pool, ids.data(), slots.data(),
-                                           static_cast<uint32_t>(ids.size()));
+        rc = kvmem_hip_stagein_blocks_host(e->ctx, &h, &pool, q_ids.data(), q_slots.data(),
+                                           static_cast<uint32_t>(q_ids.size()));
     } else {
         const kvmem_hip_history h = e->device_history();
-        rc = kvmem_hip_stagein_blocks(e->ctx, &h, &pool, ids.data(), slots.data(),
-                                      static_cast<uint32_t>(ids.size()));
+        rc = kvmem_hip_stagein_blocks(e->ctx, &h, &pool, q_ids.data(), q_slots.data(),
+                                      static_cast<uint32_t>(q_ids.size()));
     }
     return rc == KVMEM_HIP_OK ? rc : e->fail_ctx(rc, "stage-in");
 }
@@ -496,6 +540,7 @@ int kvmem_engine_set_device_history(kvmem_engine *e, const void *k, const void *
     e->hist_v = v;
     e->hist_capacity = capacity_blocks;
     e->meank_valid = 0;
+    std::fill(e->packed_valid.begin(), e->packed_valid.end(), 0);  // a new history
     const uint32_t have = e->rt.store().total_tokens();
     if (n_tokens < have) {
         e->rt.truncate_to(n_tokens);
@@ -520,7 +565,25 @@ int kvmem_engine_set_host_history(kvmem_engine *e, const void *pinned_base,
     }
     e->host_base = pinned_base;
     e->host_capacity = pinned_base ? capacity_blocks : 0;
+    std::fill(e->packed_valid.begin(), e->packed_valid.end(), 0);  // a new history
     return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_set_packed_host(kvmem_engine *e, void *pinned_base, uint32_t capacity_blocks) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {  // copies into the old store are done
+        return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "set_packed_host");
+    }
+    e->packed_base = pinned_base;
+    e->packed_capacity = pinned_base ? capacity_blocks : 0;
+    e->packed_valid.assign(e->packed_capacity, 0);
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_packed_valid(const kvmem_engine *e, uint32_t block_id) {
+    return e && block_id < e->packed_capacity && e->packed_valid[block_id] ? 1 : 0;
 }
 
 int kvmem_engine_append_tokens(kvmem_engine *e, uint32_t n_new_tokens) {
@@ -557,6 +620,10 @@ int kvmem_engine_truncate_to(kvmem_engine *e, uint32_t token_pos) {
         return KVMEM_HIP_ERR_INVALID;
     }
     e->rt.truncate_to(token_pos);
+    // blocks from the one holding token_pos on are cut short or gone
+    for (uint32_t id = token_pos / e->p.block_tokens; id < e->packed_capacity; ++id) {
+        e->packed_valid[id] = 0;
+    }
     const uint32_t nb = e->rt.store().block_count();
     // a block cut short has stale sums
     e->meank_valid = std::min(e->meank_valid, nb > 0 ? nb - 1 : 0u);
@@ -881,6 +948,7 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
         return e->fail(KVMEM_HIP_ERR_INVALID, "apply: selection larger than the slot pool");
     }
     // slots the selection keeps before the plan changes them
+    const int64_t dirty_at_start = e->dirty_tail;  // its pool rows are stale
     std::vector<int32_t> old_slot(n, -1);
     for (const Block &b : e->rt.store().blocks()) {
         old_slot[b.block_id] = b.tier == Tier::GPU ? b.gpu_slot : -1;
@@ -912,8 +980,35 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
             return e->fail(KVMEM_HIP_ERR_RUNTIME, "apply: slot pool exhausted");
         }
     }
-    uint32_t n_moved = 0;
     int rc = KVMEM_HIP_OK;
+    // Evicted full blocks whose packed rows the host store lacks are copied
+    // out first: the copies are ordered before the moves and stage-ins that
+    // reuse their slots on the same stream.
+    uint32_t n_saved = 0;
+    if (e->packed_base) {
+        std::vector<uint32_t> sid, sslot, snt;
+        for (uint32_t id : plan.stage_out) {
+            if (id < n && old_slot[id] >= 0 && id < e->packed_capacity && !e->packed_valid[id] &&
+                static_cast<int64_t>(id) != dirty_at_start &&
+                e->rt.store().blocks()[id].n_tokens == e->p.block_tokens) {
+                sid.push_back(id);
+                sslot.push_back(static_cast<uint32_t>(old_slot[id]));
+                snt.push_back(e->p.block_tokens);
+            }
+        }
+        if (!sid.empty()) {
+            const kvmem_hip_pool pool = e->pool_desc();
+            const kvmem_hip_packed_host ph = packed_desc(e);
+            rc = kvmem_hip_stageout_blocks(e->ctx, &pool, &ph, sid.data(), sslot.data(), snt.data(),
+                                           static_cast<uint32_t>(sid.size()));
+            if (rc != KVMEM_HIP_OK) {
+                return e->fail_ctx(rc, "apply: stage-out");
+            }
+            for (uint32_t id : sid) e->packed_valid[id] = 1;
+            n_saved = static_cast<uint32_t>(sid.size());
+        }
+    }
+    uint32_t n_moved = 0;
     if (e->p.canonical_layout) {
         // window slot i holds the i-th selected block
         std::vector<uint32_t> src, dst;
@@ -942,14 +1037,15 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
             n_moved = static_cast<uint32_t>(src.size());
         }
     }
-    rc = engine_stage(e, stage_ids, stage_slots);
+    uint32_t n_restored = 0;
+    rc = engine_stage(e, stage_ids, stage_slots, &n_restored);
     if (rc != KVMEM_HIP_OK) {
         return rc;
     }
     if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
         return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "apply sync");
     }
-    fill_stats(plan, static_cast<uint32_t>(stage_ids.size()), n_moved, stats);
+    fill_stats(plan, static_cast<uint32_t>(stage_ids.size()), n_moved, n_saved, n_restored, stats);
     return KVMEM_HIP_OK;
 }
 

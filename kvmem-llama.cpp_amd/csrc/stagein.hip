@@ -1217,36 +1217,13 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
         return st;
     }
     (void) hipSetDevice(ctx->device);
-    // Device ring: kRing slots of up to 32 MiB (at least one block each).
-    constexpr int kRing = 4;
-    const uint64_t target = 32ull << 20;
-    const uint32_t per_slot = static_cast<uint32_t>(std::max<uint64_t>(1, target / span));
-    const uint64_t slot_bytes = per_slot * span;
-    if (ctx->h2d_slot_bytes != slot_bytes || !ctx->h2d_ring.ptr) {
-        if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "h2d ring sync")) {
-            return KVMEM_HIP_ERR_RUNTIME;
-        }
-        if (ctx->h2d_ring.ptr) {
-            hipFree(ctx->h2d_ring.ptr);
-            ctx->h2d_ring.ptr = nullptr;
-            ctx->h2d_ring.bytes = 0;
-        }
-        if (!ensure_dev(ctx, ctx->h2d_ring, slot_bytes * kRing, "h2d ring")) {
-            return KVMEM_HIP_ERR_NOMEM;
-        }
-        ctx->h2d_slot_bytes = slot_bytes;
-        ctx->h2d_slots = kRing;
+    // Device ring: kH2dRing slots of 32 MiB or more (at least one block each).
+    if (!ensure_h2d_ring(ctx, span)) {
+        return KVMEM_HIP_ERR_NOMEM;  // the failing call is in kvmem_hip_last_error
     }
-    for (int r = 0; r < kRing; ++r) {
-        if (!ctx->h2d_copied[r]) {
-            if (!hip_ok(ctx, hipEventCreateWithFlags(&ctx->h2d_copied[r], hipEventDisableTiming), "h2d event") ||
-                !hip_ok(ctx, hipEventCreateWithFlags(&ctx->h2d_consumed[r], hipEventDisableTiming), "h2d event")) {
-                return KVMEM_HIP_ERR_RUNTIME;
-            }
-            // a fresh "consumed" marker on the compute stream
-            hipEventRecord(ctx->h2d_consumed[r], ctx->stream);
-        }
-    }
+    constexpr int kRing = kH2dRing;
+    const uint64_t slot_bytes = ctx->h2d_slot_bytes;
+    const uint32_t per_slot = static_cast<uint32_t>(slot_bytes / span);
     // items of every batch, block index relative to its ring slot
     std::vector<uint32_t> items(4 * static_cast<size_t>(n));
     for (uint32_t i = 0; i < n; ++i) {

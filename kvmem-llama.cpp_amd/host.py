@@ -21,7 +21,8 @@ class PlanStats(C.Structure):
     _fields_ = [("n_stage_in", C.c_uint32), ("n_stage_out", C.c_uint32), ("n_staged", C.c_uint32),
                 ("n_moved", C.c_uint32), ("selection_overlap_blocks", C.c_uint32),
                 ("gpu_reused_blocks", C.c_uint32), ("retained_position_stable", C.c_uint32),
-                ("retained_position_moved", C.c_uint32), ("total_window_tokens", C.c_uint32)]
+                ("retained_position_moved", C.c_uint32), ("total_window_tokens", C.c_uint32),
+                ("n_saved", C.c_uint32), ("n_restored", C.c_uint32)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -72,6 +73,8 @@ def bind(lib: C.CDLL) -> C.CDLL:
     sig("kvmem_engine_ctx", vp, vp)
     sig("kvmem_engine_set_device_history", i32, vp, vp, vp, u32, u32)
     sig("kvmem_engine_set_host_history", i32, vp, vp, u32)
+    sig("kvmem_engine_set_packed_host", i32, vp, vp, u32)
+    sig("kvmem_engine_packed_valid", i32, vp, u32)
     sig("kvmem_engine_append_tokens", i32, vp, u32)
     sig("kvmem_engine_truncate_to", i32, vp, u32)
     sig("kvmem_engine_block_count", u32, vp)
@@ -227,6 +230,14 @@ class Engine:
     def set_host_history(self, base_ptr: int | None, capacity_blocks: int = 0):
         self.check(self.lib.kvmem_engine_set_host_history(self.h, base_ptr or None, capacity_blocks),
                    "set_host_history")
+
+    def set_packed_host(self, base_ptr: int | None, capacity_blocks: int = 0):
+        """Pinned packed host store (block spans in the pool's formats)."""
+        self.check(self.lib.kvmem_engine_set_packed_host(self.h, base_ptr or None, capacity_blocks),
+                   "set_packed_host")
+
+    def packed_valid(self, block_id: int) -> bool:
+        return bool(self.lib.kvmem_engine_packed_valid(self.h, block_id))
 
     def append_tokens(self, n: int):
         self.check(self.lib.kvmem_engine_append_tokens(self.h, n), "append_tokens")
