@@ -16,8 +16,10 @@ steps an untimed restore re-applies it (the same stage-in path).
 Prints ONE JSON line.  `value` is ms per agent step (lower is better) with
 history and query resident in HBM.  `roofline` is the MFMA block scorer
 (the dominant kernel); `stagein_roofline` the q8_0 stage-in kernel against
-HBM; `pinned_host` the same stage-in fed over PCIe from pinned host memory;
-`cpu_baseline` the oracle's restatement of the step on the host cores.
+HBM; `pinned_host` the same stage-in fed over PCIe from pinned host memory,
+and the same blocks as packed q8_0 rows copied out to (`packed_stageout`)
+and restored from (`packed_stagein`) a pinned packed store; `cpu_baseline`
+the oracle's restatement of the step on the host cores.
 """
 from __future__ import annotations
 
@@ -218,8 +220,31 @@ def pinned_host_mode(kv, ctx, torch, k, v, eng, incoming: list[int], reps: int =
         dt = time.perf_counter() - t0
         best = dt if best is None else min(best, dt)
     h2d = n * span_el * 2
-    return {"ms": round(best * 1e3, 3), "h2d_bytes": h2d, "h2d_GBs": round(h2d / best / 1e9, 2),
-            "link_peak_GBs": PCIE_PEAK_GBS, "frac": round(h2d / best / 1e9 / PCIE_PEAK_GBS, 3)}
+    out = {"ms": round(best * 1e3, 3), "h2d_bytes": h2d, "h2d_GBs": round(h2d / best / 1e9, 2),
+           "link_peak_GBs": PCIE_PEAK_GBS, "frac": round(h2d / best / 1e9 / PCIE_PEAK_GBS, 3)}
+    # the same blocks as packed q8_0 rows: stage-out (gather + D2H) into a
+    # pinned packed store, then the packed stage-in back into the slots
+    row = kv.row_size(kv.TYPE_Q8_0, E)
+    span = L * T * 2 * row
+    store = torch.empty(n * span, dtype=torch.uint8, pin_memory=True)
+    ph = kv.PackedHost(store.data_ptr(), L, n, T)
+    ids, nts = list(range(n)), [T] * n
+    for name, fn in (("packed_stageout", lambda: ctx.stageout_blocks(pool, ph, ids, slots, nts)),
+                     ("packed_stagein", lambda: ctx.stagein_packed_host(ph, pool, ids, slots, nts))):
+        fn()
+        ctx.sync()
+        best = None
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            ctx.sync()
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+        nbytes = n * span
+        out[name] = {"ms": round(best * 1e3, 3), "bytes": nbytes, "GBs": round(nbytes / best / 1e9, 2),
+                     "frac": round(nbytes / best / 1e9 / PCIE_PEAK_GBS, 3)}
+    return out
 
 
 def run_reselect_256k(a, torch, kv, workloads) -> dict:
@@ -433,10 +458,26 @@ def run_copy_calibration(a, torch, kv, workloads) -> dict:
     e1.record()
     e1.synchronize()
     rt_ms = e0.elapsed_time(e1) / a.steps
+    # the host link: one 512 MiB pinned buffer each way, the runtime's copies
+    link = {}
+    hbuf = torch.empty(512 << 20, dtype=torch.uint8, pin_memory=True)
+    dbuf = src[: 512 << 20]
+    for name, fn in (("h2d", lambda: dbuf.copy_(hbuf, non_blocking=True)),
+                     ("d2h", lambda: hbuf.copy_(dbuf, non_blocking=True))):
+        fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(3):
+            fn()
+        e1.record()
+        e1.synchronize()
+        t = e0.elapsed_time(e1) / 3
+        link[name + "_GBs"] = round((512 << 20) / (t * 1e-3) / 1e9, 1)
     return {"metric": "device copy calibration", "bytes_read": n_ops * op, "bytes_written": n_ops * op,
             "kernel_ms": round(ms, 4), "GBs_read_plus_write": round(2 * n_ops * op / (ms * 1e-3) / 1e9, 1),
             "runtime_copy_ms": round(rt_ms, 4),
-            "runtime_copy_GBs": round(2 * n_ops * op / (rt_ms * 1e-3) / 1e9, 1), "copy_ok": ok}
+            "runtime_copy_GBs": round(2 * n_ops * op / (rt_ms * 1e-3) / 1e9, 1), "copy_ok": ok,
+            "pinned_link": link}
 
 
 def main() -> int:

@@ -252,8 +252,9 @@ typedef struct kvmem_hip_packed_host {
 /* Stage-out: copy the packed rows of pool slot slots[i] (every layer, K and
  * V, n_tokens[i] rows) to block block_ids[i] of the packed host store.
  * The rows are gathered into a device ring in the host layout by one copy
- * launch per 32 MiB batch on the context stream, then copied device-to-host
- * on the side stream, so a later call's gathers overlap earlier copies.
+ * launch per 128 MiB batch on the context stream, then copied device-to-
+ * host on the side stream, so a later call's gathers overlap earlier
+ * copies.
  * Asynchronous: the host rows are complete after kvmem_hip_sync.  Replaces
  * kvmem_stageout_enqueue / submit / wait (llama-kvmem-stagein.h:40-47,
  * stagein.cu:842-963: gather kernel into a 32 MiB slab, D2H into two

@@ -5,10 +5,11 @@
 // write_block_to_gpu upload, llama-memory-kvmem.cpp:2726-2791).
 //
 // Both are copy pipelines over two streams.  Stage-out gathers a batch of
-// blocks (every layer, K and V) into a 32 MiB device ring slot in the host
-// layout with one copy launch on the context stream, then copies each
-// block's span device-to-host on the side stream; two ring slots alternate
-// so the next gather overlaps the previous copies.  The packed stage-in
+// blocks (every layer, K and V) into a 128 MiB device ring slot in the host
+// layout with one copy launch on the context stream, then copies the spans
+// device-to-host on the side stream (runs of consecutive blocks as one
+// copy); two ring slots alternate so the next gather overlaps the previous
+// copies.  The packed stage-in
 // copies block spans host-to-device into the stage-in ring on the side
 // stream and scatters each batch into the slots with one copy launch.  HBM
 // work is a few hundred MB per step; the bound is the PCIe link.
@@ -66,7 +67,8 @@ int check_packed(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const kvmem_hip
 }
 
 bool ensure_d2h_ring(kvmem_hip_ctx *ctx, size_t min_slot_bytes) {
-    const size_t want = std::max<size_t>(size_t{32} << 20, min_slot_bytes);
+    // device-to-host copies reach the link rate only in large pieces
+    const size_t want = std::max<size_t>(size_t{128} << 20, min_slot_bytes);
     if (ctx->d2h_ring.ptr && ctx->d2h_slot_bytes >= want) {
         return true;
     }
@@ -166,11 +168,17 @@ int kvmem_hip_stageout_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool,
             uint8_t *hb = host + static_cast<uint64_t>(block_ids[i]) * g.span;
             const uint8_t *db = slot_base + j * g.span;
             if (nt == T) {
-                // a full block is one contiguous span on both sides
-                if (!hip_ok(ctx, hipMemcpyAsync(hb, db, g.span, hipMemcpyDeviceToHost, ctx->copy_stream),
+                // full blocks are contiguous spans on both sides; a run of
+                // consecutive full blocks goes out as one copy
+                uint32_t run = 1;
+                while (j + run < cnt && n_tokens[i + run] == T && block_ids[i + run] == block_ids[i] + run) {
+                    ++run;
+                }
+                if (!hip_ok(ctx, hipMemcpyAsync(hb, db, run * g.span, hipMemcpyDeviceToHost, ctx->copy_stream),
                             "d2h block copy")) {
                     return KVMEM_HIP_ERR_RUNTIME;
                 }
+                j += run - 1;
                 continue;
             }
             // a partial block: only its rows, so the rest of the host run is untouched
@@ -229,13 +237,19 @@ int kvmem_hip_stagein_packed_host(kvmem_hip_ctx *ctx, const kvmem_hip_packed_hos
             return KVMEM_HIP_ERR_RUNTIME;
         }
         for (uint32_t j = 0; j < cnt; ++j) {
+            // a run of consecutive blocks comes in as one copy
             const uint32_t b = block_ids[first + j];
+            uint32_t run = 1;
+            while (j + run < cnt && block_ids[first + j + run] == b + run) {
+                ++run;
+            }
             if (!hip_ok(ctx, hipMemcpyAsync(slot_base + j * g.span, host + static_cast<uint64_t>(b) * g.span,
-                                            g.span, hipMemcpyHostToDevice, ctx->copy_stream),
+                                            run * g.span, hipMemcpyHostToDevice, ctx->copy_stream),
                         "h2d packed block copy")) {
                 return KVMEM_HIP_ERR_RUNTIME;
             }
-            ctx->h2d_bytes += g.span;
+            ctx->h2d_bytes += run * g.span;
+            j += run - 1;
         }
         if (!hip_ok(ctx, hipEventRecord(ctx->h2d_copied[r], ctx->copy_stream), "h2d record") ||
             !hip_ok(ctx, hipStreamWaitEvent(ctx->stream, ctx->h2d_copied[r], 0), "h2d wait copied")) {

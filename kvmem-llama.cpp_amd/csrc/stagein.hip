@@ -1250,13 +1250,19 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
             return KVMEM_HIP_ERR_RUNTIME;
         }
         for (uint32_t j = 0; j < cnt; ++j) {
+            // a run of consecutive blocks comes in as one copy
             const uint32_t b = block_ids[first + j];
+            uint32_t run = 1;
+            while (j + run < cnt && block_ids[first + j + run] == b + run) {
+                ++run;
+            }
             if (!hip_ok(ctx, hipMemcpyAsync(slot_base + j * span, host + static_cast<uint64_t>(b) * span,
-                                            span, hipMemcpyHostToDevice, ctx->copy_stream),
+                                            run * span, hipMemcpyHostToDevice, ctx->copy_stream),
                         "h2d block copy")) {
                 return KVMEM_HIP_ERR_RUNTIME;
             }
-            ctx->h2d_bytes += span;
+            ctx->h2d_bytes += run * span;
+            j += run - 1;
         }
         if (!hip_ok(ctx, hipEventRecord(ctx->h2d_copied[r], ctx->copy_stream), "h2d record") ||
             !hip_ok(ctx, hipStreamWaitEvent(ctx->stream, ctx->h2d_copied[r], 0), "h2d wait copied")) {
