@@ -178,6 +178,31 @@ def cpu_baseline(torch, k, v, q, sel_ids: list[int], budget_s: float = 12.0) -> 
         list(ex.map(lambda r: oracle.quantize_rows_f16(oracle.TYPE_Q8_0, r), jobs))
     quant_s = (time.perf_counter() - t0) * N_CHANGED / n_q
     total_ms = (score_s + topk_s + quant_s) * 1e3
+    # the reference's own scorer (mean-K cosine, single thread as in the
+    # adapter) over key sums of 256 sampled blocks, scaled to every block
+    rng = np.random.default_rng(1)
+    n_mk = 256
+    k_sum = rng.standard_normal((L, n_mk, E)).astype(np.float32)
+    q_sum = qf.sum(axis=1).reshape(L, HQ * D).astype(np.float32)
+    t0 = time.perf_counter()
+    oracle.score_meank(q_sum, [TQ] * L, k_sum, np.full((L, n_mk), T, np.uint32), HQ, HKV, D)
+    meank_s = (time.perf_counter() - t0) * B / n_mk
+    # q8_0 quantize on one thread (the same jobs, serial)
+    t0 = time.perf_counter()
+    for r in jobs[: 2 * L]:
+        oracle.quantize_rows_f16(oracle.TYPE_Q8_0, r)
+    quant1_s = (time.perf_counter() - t0) * len(jobs) / (2 * L) * N_CHANGED / n_q
+    # the reference's live stage-in on the host: a memcpy of the changed
+    # blocks' packed q8_0 rows into the staging slab (write_block_to_gpu)
+    packed = np.ones(N_CHANGED * L * 2 * T * 1088, dtype=np.uint8)
+    slab = np.zeros_like(packed)
+    slab.fill(2)  # the slab's pages are resident, as the reference's pinned slab
+    memcpy_s = None
+    for _ in range(3):
+        t0 = time.perf_counter()
+        np.copyto(slab, packed)
+        dt = time.perf_counter() - t0
+        memcpy_s = dt if memcpy_s is None else min(memcpy_s, dt)
     return {
         "value": round(total_ms, 1), "unit": "ms/step", "cores": threads, "kind": "port",
         "sample": (f"fp32 per-token max scorer on {len(sample_ids)} of {B} blocks x {L} layers "
@@ -186,6 +211,13 @@ def cpu_baseline(torch, k, v, q, sel_ids: list[int], budget_s: float = 12.0) -> 
                    f"x K/V ({threads} threads) scaled x{N_CHANGED / n_q:.2f}"),
         "parts_ms": {"score": round(score_s * 1e3, 1), "topk": round(topk_s * 1e3, 3),
                      "quantize": round(quant_s * 1e3, 1)},
+        "other_legs": {
+            "meank_score_ms": round(meank_s * 1e3, 2),
+            "meank_sample": f"mean-K cosine scorer (1 thread) on {n_mk} of {B} blocks x {L} layers, scaled",
+            "quantize_1thread_ms": round(quant1_s * 1e3, 1),
+            "packed_memcpy_ms": round(memcpy_s * 1e3, 2),
+            "packed_memcpy_GBs": round(packed.nbytes / memcpy_s / 1e9, 2),
+        },
     }
 
 
