@@ -369,6 +369,21 @@ KVMEM_HIP_API int kvmem_hip_q_accumulate(kvmem_hip_ctx *ctx, const void *q, int3
                                          const uint32_t *tokens, uint32_t n_list, int reset,
                                          float *q_sum);
 
+/* Decode-time mean-K producer (the reference's running sum on the GPU,
+ * kvmem_meank_zero / kvmem_meank_add, llama-kvmem-stagein.cu:1020-1063):
+ * for e < n_embd, acc[e] (+)= K[t][e / head_dim][e % head_dim] over the
+ * tokens t = tok0 .. tok0 + n_keep - 1 in token order (fp32 additions,
+ * bit-identical to the reference's loop).  K is device memory of k_type
+ * F32, F16 or BF16 addressed with byte strides nb0 (element), nb1 (head),
+ * nb2 (token), as the ggml K view the reference reads.  acc is device
+ * [n_embd] f32, e.g. a row of the key sums kvmem_hip_meank_sums writes;
+ * count (device, may be NULL) is that row's token count, increased by
+ * n_keep.  reset != 0 starts both from zero (kvmem_meank_zero). */
+KVMEM_HIP_API int kvmem_hip_meank_add(kvmem_hip_ctx *ctx, const void *k, int32_t k_type,
+                                      uint32_t n_embd, uint32_t head_dim, size_t nb0, size_t nb1,
+                                      size_t nb2, uint32_t tok0, uint32_t n_keep, int reset,
+                                      float *acc, uint32_t *count);
+
 /* The reference's retrieval scorer (llama_memory_kvmem::score_retrieval,
  * src/adapter/llama-memory-kvmem.cpp:2869-2916): per block the mean over
  * layers with query rows of the mean over KV heads of

@@ -153,6 +153,7 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_meank_sums", i32, vp, C.POINTER(History), pu32, u32, vp, vp)
     _sig(lib, "kvmem_hip_score_meank", i32, vp, C.POINTER(MeanKArgs))
     _sig(lib, "kvmem_hip_q_accumulate", i32, vp, vp, i32, u32, u32, u32, pu32, u32, i32, vp)
+    _sig(lib, "kvmem_hip_meank_add", i32, vp, vp, i32, u32, u32, sz, sz, sz, u32, u32, i32, vp, vp)
     _sig(lib, "kvmem_hip_stageout_blocks", i32, vp, C.POINTER(Pool), C.POINTER(PackedHost), pu32, pu32,
          pu32, u32)
     _sig(lib, "kvmem_hip_stagein_packed_host", i32, vp, C.POINTER(PackedHost), C.POINTER(Pool), pu32, pu32,
@@ -340,6 +341,14 @@ class Context:
         ids, n = _u32_array(block_ids)
         self.check(self.lib.kvmem_hip_meank_sums(self.h, C.byref(hist), ids, n, k_sum_ptr,
                                                  mean_tokens_ptr), "meank_sums")
+
+    def meank_add(self, k_ptr: int, k_type: int, n_embd: int, head_dim: int, nb0: int, nb1: int,
+                  nb2: int, tok0: int, n_keep: int, acc_ptr: int, count_ptr: int = 0,
+                  reset: bool = False) -> None:
+        """acc (+)= the kept tokens' K rows (strided view), token order."""
+        self.check(self.lib.kvmem_hip_meank_add(self.h, k_ptr, k_type, n_embd, head_dim, nb0, nb1, nb2,
+                                                tok0, n_keep, int(reset), acc_ptr, count_ptr or None),
+                   "meank_add")
 
     def q_accumulate(self, q_ptr: int, q_type: int, n_layers: int, n_tokens: int, n_embd_q: int,
                      q_sum_ptr: int, tokens=None, reset: bool = True) -> None:

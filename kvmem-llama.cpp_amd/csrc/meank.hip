@@ -1,5 +1,6 @@
 // Mean-K cosine block scorer (the reference's retrieval scorer) and its
-// two producers, the per-block key sums and the per-layer query sums.
+// producers: per-block key sums from the F16 history, the decode-time
+// running key sum, and the per-layer query sums.
 //
 // Producer: k_sum[l][b][e] = fp32 sum of the block's F16 keys in token
 // order, mean_tokens[l][b] = tokens summed (RawKvStore::capture_mean_f16,
@@ -83,6 +84,30 @@ __global__ __launch_bounds__(256) void q_accumulate_kernel(const QT *q, const ui
         acc += static_cast<float>(src[static_cast<uint64_t>(t) * E]);
     }
     *dst = acc;
+}
+
+// Decode running sum: one thread per channel adds the kept tokens' values
+// in token order (strided K view of type KT).
+template <typename KT>
+__global__ __launch_bounds__(256) void meank_add_kernel(const uint8_t *k, uint32_t n_embd,
+                                                        uint32_t head_dim, uint64_t nb0, uint64_t nb1,
+                                                        uint64_t nb2, uint32_t tok0, uint32_t n_keep,
+                                                        int reset, float *acc, uint32_t *count) {
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e == 0 && count) {
+        *count = (reset ? 0u : *count) + n_keep;
+    }
+    if (e >= n_embd) {
+        return;
+    }
+    const uint32_t head = e / head_dim;
+    const uint32_t dim = e - head * head_dim;
+    const uint8_t *base = k + static_cast<uint64_t>(head) * nb1 + static_cast<uint64_t>(dim) * nb0;
+    float s = reset ? 0.0f : acc[e];
+    for (uint32_t t = 0; t < n_keep; ++t) {
+        s += static_cast<float>(*reinterpret_cast<const KT *>(base + static_cast<uint64_t>(tok0 + t) * nb2));
+    }
+    acc[e] = s;
 }
 
 // One workgroup per (layer, KV head), one thread per channel: the group's
@@ -269,6 +294,41 @@ int kvmem_hip_meank_sums(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
         static_cast<const uint8_t *>(hist->k), static_cast<const uint32_t *>(items), hist->n_layers,
         cap, hist->block_tokens, E, hist->n_blocks - 1, hist->last_block_tokens, k_sum, mean_tokens);
     return hip_ok(ctx, hipGetLastError(), "meank_sums launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
+}
+
+int kvmem_hip_meank_add(kvmem_hip_ctx *ctx, const void *k, int32_t k_type, uint32_t n_embd,
+                        uint32_t head_dim, size_t nb0, size_t nb1, size_t nb2, uint32_t tok0,
+                        uint32_t n_keep, int reset, float *acc, uint32_t *count) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!k || !acc || n_embd == 0 || head_dim == 0 || n_embd % head_dim != 0) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "meank_add: null pointer or bad geometry");
+    }
+    const size_t esz = k_type == KVMEM_TYPE_F32 ? 4 : 2;
+    if (k_type != KVMEM_TYPE_F32 && k_type != KVMEM_TYPE_F16 && k_type != KVMEM_TYPE_BF16) {
+        return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "meank_add: k_type must be F32, F16 or BF16");
+    }
+    if (nb0 % esz || nb1 % esz || nb2 % esz || (reinterpret_cast<uintptr_t>(k) % esz)) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "meank_add: strides must be multiples of the element size");
+    }
+    if (n_keep == 0 && !reset) {
+        return KVMEM_HIP_OK;
+    }
+    (void) hipSetDevice(ctx->device);
+    const uint32_t grid = (n_embd + 255) / 256;
+    const uint8_t *kb = static_cast<const uint8_t *>(k);
+    if (k_type == KVMEM_TYPE_F32) {
+        meank_add_kernel<float><<<grid, 256, 0, ctx->stream>>>(kb, n_embd, head_dim, nb0, nb1, nb2, tok0,
+                                                              n_keep, reset, acc, count);
+    } else if (k_type == KVMEM_TYPE_F16) {
+        meank_add_kernel<_Float16><<<grid, 256, 0, ctx->stream>>>(kb, n_embd, head_dim, nb0, nb1, nb2, tok0,
+                                                                 n_keep, reset, acc, count);
+    } else {
+        meank_add_kernel<__bf16><<<grid, 256, 0, ctx->stream>>>(kb, n_embd, head_dim, nb0, nb1, nb2, tok0,
+                                                               n_keep, reset, acc, count);
+    }
+    return hip_ok(ctx, hipGetLastError(), "meank_add launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
 }
 
 int kvmem_hip_q_accumulate(kvmem_hip_ctx *ctx, const void *q, int32_t q_type, uint32_t n_layers,

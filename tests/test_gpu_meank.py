@@ -176,3 +176,30 @@ def test_engine_scorer_meank_from_query_rows(oracle):
         assert sel.blocks == oracle.pick_topk(got.astype(np.float32).astype(np.float64), 8, sink=1)
         stats = eng.apply(sel)
         assert stats["n_stage_in"] == len(sel.blocks)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_meank_add_decode_running_sum(ctx, oracle, dtype):
+    """The decode producer over a strided K view (padded heads): two calls
+    (reset, then continue) equal the oracle's token-order sums, and the
+    count follows the kept tokens."""
+    announce(f"decode running key sum {dtype}: 40 tokens x 4 heads x 256, padded strides")
+    n_tok, dpad = 40, D + 8
+    tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[dtype]
+    code = {"f32": kv.TYPE_F32, "f16": kv.TYPE_F16, "bf16": kv.TYPE_BF16}[dtype]
+    g = torch.Generator(device="cpu").manual_seed(41)
+    full = (torch.randn((n_tok, HKV, dpad), generator=g) * 3).to(tdt).cuda()
+    full[0, 0, 0] = 1e4 if dtype != "f32" else 1e8   # order-sensitive large first value
+    esz = full.element_size()
+    acc = torch.full((E,), float("nan"), dtype=torch.float32, device="cuda")
+    cnt = torch.full((1,), 7, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.meank_add(full.data_ptr(), code, E, D, esz, dpad * esz, HKV * dpad * esz, 0, 25,
+                  acc.data_ptr(), cnt.data_ptr(), reset=True)
+    ctx.meank_add(full.data_ptr(), code, E, D, esz, dpad * esz, HKV * dpad * esz, 25, 15,
+                  acc.data_ptr(), cnt.data_ptr(), reset=False)
+    ctx.sync()
+    rows = full[:, :, :D].float().cpu().numpy().reshape(1, n_tok, E)
+    want = oracle.q_accumulate(rows)[0]            # every token in order from zero
+    assert np.array_equal(acc.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    assert int(cnt.item()) == n_tok
