@@ -410,6 +410,17 @@ typedef struct kvmem_hip_meank_args {
 
 KVMEM_HIP_API int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *args);
 
+/* -------------------------------------------------------- self-check */
+
+/* Check, on this device and over every float of their ranges, the two
+ * shortcuts the quantizers use for ggml's scale divisions: a / 127 for
+ * every non-negative float a (q8_0's d) and 1 / d for every normal |d| <=
+ * 2^126 (the id of all three formats); each count is the number of inputs
+ * where the shortcut differs from the IEEE quotient (0 expected).  Takes a
+ * few hundred milliseconds; no counterpart in the reference. */
+KVMEM_HIP_API int kvmem_hip_check_scale_arith(kvmem_hip_ctx *ctx, uint64_t *div127_mismatches,
+                                              uint64_t *recip_mismatches);
+
 /* ------------------------------------------------------------ profiling */
 
 /* Per-stage GPU time (hipEvent pairs on the context stream), the device

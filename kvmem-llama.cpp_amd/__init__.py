@@ -154,6 +154,7 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_score_meank", i32, vp, C.POINTER(MeanKArgs))
     _sig(lib, "kvmem_hip_q_accumulate", i32, vp, vp, i32, u32, u32, u32, pu32, u32, i32, vp)
     _sig(lib, "kvmem_hip_meank_add", i32, vp, vp, i32, u32, u32, sz, sz, sz, u32, u32, i32, vp, vp)
+    _sig(lib, "kvmem_hip_check_scale_arith", i32, vp, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64))
     _sig(lib, "kvmem_hip_stageout_blocks", i32, vp, C.POINTER(Pool), C.POINTER(PackedHost), pu32, pu32,
          pu32, u32)
     _sig(lib, "kvmem_hip_stagein_packed_host", i32, vp, C.POINTER(PackedHost), C.POINTER(Pool), pu32, pu32,
@@ -349,6 +350,12 @@ class Context:
         self.check(self.lib.kvmem_hip_meank_add(self.h, k_ptr, k_type, n_embd, head_dim, nb0, nb1, nb2,
                                                 tok0, n_keep, int(reset), acc_ptr, count_ptr or None),
                    "meank_add")
+
+    def check_scale_arith(self) -> tuple[int, int]:
+        """(div127 mismatches, reciprocal mismatches) over their full ranges."""
+        a, b = C.c_uint64(0), C.c_uint64(0)
+        self.check(self.lib.kvmem_hip_check_scale_arith(self.h, C.byref(a), C.byref(b)), "check_scale_arith")
+        return a.value, b.value
 
     def q_accumulate(self, q_ptr: int, q_type: int, n_layers: int, n_tokens: int, n_embd_q: int,
                      q_sum_ptr: int, tokens=None, reset: bool = True) -> None:

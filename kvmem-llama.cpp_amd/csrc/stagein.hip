@@ -23,7 +23,8 @@
 // -0.125 / -0.0625: both round the same exact quotient once)
 // where vmax is the first element of largest magnitude.  The products and
 // sums are separate IEEE operations (no FMA contraction in this file),
-// divisions are correctly rounded (HIP default), d is stored as f16 RNE.
+// the divisions are correctly rounded (computed by the exact shortcuts
+// scale_div127 / scale_recip below), d is stored as f16 RNE.
 //
 // With a pool transform the rows are widened to fp32, RoPE'd (K) and
 // Hadamard-rotated before they are quantized, as the reference's raw-K
@@ -107,7 +108,8 @@ struct OpListSource {
         out.pos0 = 0;
         return true;
     }
-    // no row transform on this source
+    // rows may be strided; no row transform on this source
+    static constexpr bool kContiguous = false;
     static constexpr uint32_t head_dim = 32, n_rot = 0, hadamard = 0;
     static constexpr float hscale = 1.0f;
     static constexpr const float *theta = nullptr;
@@ -119,6 +121,7 @@ struct OpListSource {
 //   src(item, layer) = base + block*block_stride + layer*layer_stride
 //   dst(item, layer) = layer_dst[layer] + slot*block_tokens*row_bytes
 struct BlockSource {
+    static constexpr bool kContiguous = true;  // group g of an operation at src + 64 g
     const uint8_t *base;
     const uint8_t *const *layer_dst;  // device array [n_layers]
     const uint32_t *items;            // device [n_items][4]: block, slot, n_tokens, pos0
@@ -198,6 +201,24 @@ __device__ inline void store_8bytes(uint8_t *p, uint32_t lo, uint32_t hi) {
     store_u16(p + 6, hi >> 16);
 }
 
+// The quantizers' scale arithmetic without the IEEE division sequence.
+// scale_div127(a) = a / 127 for every non-negative float a: the product with
+// the rounded reciprocal of 127 corrected by one exact residual (two FMAs);
+// scale_recip(d) = 1 / d for every normal |d| <= 2^126 (q8_0/q4_0/q5_0 scales
+// never exceed 2^125): the hardware reciprocal refined by one Newton step.
+// Both equal the correctly rounded quotients over their whole ranges (checked
+// exhaustively by kvmem_hip_check_scale_arith on the device).
+__device__ inline float scale_div127(float a) {
+    constexpr float r127 = 1.0f / 127.0f;
+    const float q0 = a * r127;
+    return __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, a), r127, q0);
+}
+
+__device__ inline float scale_recip(float d) {
+    const float r0 = __builtin_amdgcn_rcpf(d);
+    return __builtin_fmaf(__builtin_fmaf(-d, r0, 1.0f), r0, r0);
+}
+
 // roundf (half away from zero) of |s| < 128.5, the range of q8_0's x*id:
 // truncation of s + copysign(0.49999997f, s) (the float below 0.5) equals
 // roundf for every float in that range (checked exhaustively over all of
@@ -225,8 +246,8 @@ __device__ inline void quant_quarter<KVMEM_TYPE_Q8_0>(const uint4 &v, uint32_t q
     }
     amax = fmaxf(amax, __uint_as_float(quad_xor1(__float_as_uint(amax))));
     amax = fmaxf(amax, __uint_as_float(quad_xor2(__float_as_uint(amax))));
-    const float d = amax / 127.0f;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const float d = scale_div127(amax);
+    const float id = d != 0.0f ? scale_recip(d) : 0.0f;
     uint32_t w[2] = {0u, 0u};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -293,7 +314,7 @@ __device__ inline void quant_quarter<KVMEM_TYPE_Q4_0>(const uint4 &v, uint32_t q
     unpack8(v, h);
     const float vmax = quad_vmax(h, q);
     const float d = vmax * -0.125f;        // == vmax / -8 (exact scaling)
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const float id = d != 0.0f ? scale_recip(d) : 0.0f;
     uint32_t w0, w1;
     trunc_codes<15>(h, id, 8.5f, w0, w1);
     // qs[j] = code(j) | code(j + 16) << 4: lanes 0 and 1 write the bytes,
@@ -323,7 +344,7 @@ __device__ inline void quant_quarter<KVMEM_TYPE_Q5_0>(const uint4 &v, uint32_t q
     unpack8(v, h);
     const float vmax = quad_vmax(h, q);
     const float d = vmax * -0.0625f;       // == vmax / -16 (exact scaling)
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const float id = d != 0.0f ? scale_recip(d) : 0.0f;
     uint32_t w0, w1;
     trunc_codes<31>(h, id, 16.5f, w0, w1);
     // qh bit e = bit 4 of the code of element e (e = 8q + i)
@@ -538,8 +559,8 @@ __device__ inline void quant_quarter_f<KVMEM_TYPE_Q8_0>(const float x[8], uint32
     }
     amax = fmaxf(amax, __uint_as_float(quad_xor1(__float_as_uint(amax))));
     amax = fmaxf(amax, __uint_as_float(quad_xor2(__float_as_uint(amax))));
-    const float d = amax / 127.0f;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const float d = scale_div127(amax);
+    const float id = d != 0.0f ? scale_recip(d) : 0.0f;
     uint32_t w[2] = {0u, 0u};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -571,7 +592,7 @@ __device__ inline void quant_quarter_f<KVMEM_TYPE_Q4_0>(const float x[8], uint32
                                                          bool valid) {
     const float vmax = quad_vmax_f(x, q);
     const float d = vmax * -0.125f;        // == vmax / -8 (exact scaling)
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const float id = d != 0.0f ? scale_recip(d) : 0.0f;
     uint32_t w0, w1;
     trunc_codes_f<15>(x, id, 8.5f, w0, w1);
     const uint32_t p0 = quad_xor2(w0);
@@ -591,7 +612,7 @@ __device__ inline void quant_quarter_f<KVMEM_TYPE_Q5_0>(const float x[8], uint32
                                                          bool valid) {
     const float vmax = quad_vmax_f(x, q);
     const float d = vmax * -0.0625f;       // == vmax / -16 (exact scaling)
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const float id = d != 0.0f ? scale_recip(d) : 0.0f;
     uint32_t w0, w1;
     trunc_codes_f<31>(x, id, 16.5f, w0, w1);
     uint32_t qh = (bit4_of_bytes(w0) | (bit4_of_bytes(w1) << 4)) << (8 * q);
@@ -716,21 +737,38 @@ __device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8
     const uint32_t wg0 = wave * kWaveGroups;
     uint8_t *wl = lds + wave * kWaveGroups * GB;
 
+    // A full chunk of a contiguous source (every chunk but an operation's
+    // last) needs neither the row/column split nor per-lane bounds: one
+    // base address, 1 KiB apart per round, and no partial groups.
+    const bool full_chunk = Source::kContiguous && c.ng == static_cast<uint32_t>(kChunkGroups);
     uint4 v[kRounds];
+    if (full_chunk) {
+        const uint8_t *base = c.src + static_cast<uint64_t>(c.g0 + wg0 + quad) * 64u + q * 16u;
 #pragma unroll
-    for (int r = 0; r < kRounds; ++r) {
-        const uint32_t gl = wg0 + 16u * r + quad;
-        v[r] = make_uint4(0u, 0u, 0u, 0u);
-        if (gl < c.ng) {
-            const uint32_t g = c.g0 + gl;
-            const uint32_t row = g / c.gpr;
-            const uint32_t col = g - row * c.gpr;
-            const uint8_t *p = c.src + static_cast<uint64_t>(row) * c.src_stride + col * 64u + q * 16u;
-            v[r] = load_stream16(p);
+        for (int r = 0; r < kRounds; ++r) {
+            v[r] = load_stream16(base + r * 1024u);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < kRounds; ++r) {
+            const uint32_t gl = wg0 + 16u * r + quad;
+            v[r] = make_uint4(0u, 0u, 0u, 0u);
+            if (gl < c.ng) {
+                const uint32_t g = c.g0 + gl;
+                const uint32_t row = g / c.gpr;
+                const uint32_t col = g - row * c.gpr;
+                const uint8_t *p = c.src + static_cast<uint64_t>(row) * c.src_stride + col * 64u + q * 16u;
+                v[r] = load_stream16(p);
+            }
         }
     }
     if constexpr (XF) {
         transform_rounds<TYPE>(source, c, v, wl, tab, wg0, lane);
+    } else if (full_chunk) {
+#pragma unroll
+        for (int r = 0; r < kRounds; ++r) {
+            quant_quarter<TYPE>(v[r], q, wl + (16u * r + quad) * GB, true);
+        }
     } else {
 #pragma unroll
         for (int r = 0; r < kRounds; ++r) {
@@ -1352,3 +1390,66 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
 }
 
 }  // extern "C"
+
+namespace kvmem_hip {
+
+// Exhaustive device check of scale_div127 and scale_recip against the IEEE
+// quotients: one thread per float bit pattern of the chunk.
+__global__ __launch_bounds__(256) void check_scale_kernel(uint32_t base, uint32_t n, int which,
+                                                          unsigned long long *bad) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) {
+        return;
+    }
+    const float x = __uint_as_float(base + i);
+    const float got = which == 0 ? scale_div127(x) : scale_recip(x);
+    const float want = which == 0 ? x / 127.0f : 1.0f / x;
+    if (__float_as_uint(got) != __float_as_uint(want)) {
+        atomicAdd(bad, 1ull);
+    }
+}
+
+}  // namespace kvmem_hip
+
+extern "C" int kvmem_hip_check_scale_arith(kvmem_hip_ctx *ctx, uint64_t *div127_mismatches,
+                                           uint64_t *recip_mismatches) {
+    if (!ctx || !div127_mismatches || !recip_mismatches) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    (void) hipSetDevice(ctx->device);
+    unsigned long long *bad = nullptr;
+    if (!hip_ok(ctx, hipMalloc(&bad, 2 * sizeof(unsigned long long)), "check_scale_arith alloc")) {
+        return KVMEM_HIP_ERR_NOMEM;
+    }
+    int rc = KVMEM_HIP_OK;
+    if (!hip_ok(ctx, hipMemsetAsync(bad, 0, 2 * sizeof(unsigned long long), ctx->stream), "check_scale_arith")) {
+        rc = KVMEM_HIP_ERR_RUNTIME;
+    }
+    // division: every non-negative finite float (zero and subnormals too);
+    // reciprocal: normal floats of either sign with |x| <= 2^126
+    const struct { uint32_t lo, hi; int which; } ranges[] = {
+        {0x00000000u, 0x7f800000u, 0}, {0x00800000u, 0x7e800001u, 1}, {0x80800000u, 0xfe800001u, 1}};
+    constexpr uint32_t kChunk = 1u << 26;
+    for (const auto &r : ranges) {
+        for (uint32_t b = r.lo; rc == KVMEM_HIP_OK && b < r.hi;) {
+            const uint32_t n = (r.hi - b) < kChunk ? (r.hi - b) : kChunk;
+            check_scale_kernel<<<(n + 255) / 256, 256, 0, ctx->stream>>>(b, n, r.which, bad + r.which);
+            if (!hip_ok(ctx, hipGetLastError(), "check_scale_arith launch")) {
+                rc = KVMEM_HIP_ERR_RUNTIME;
+            }
+            b += n;
+        }
+    }
+    unsigned long long h[2] = {0, 0};
+    if (rc == KVMEM_HIP_OK &&
+        !hip_ok(ctx, hipMemcpyAsync(h, bad, sizeof(h), hipMemcpyDeviceToHost, ctx->stream), "check_scale_arith") ) {
+        rc = KVMEM_HIP_ERR_RUNTIME;
+    }
+    if (rc == KVMEM_HIP_OK && !hip_ok(ctx, hipStreamSynchronize(ctx->stream), "check_scale_arith sync")) {
+        rc = KVMEM_HIP_ERR_RUNTIME;
+    }
+    (void) hipFree(bad);
+    *div127_mismatches = h[0];
+    *recip_mismatches = h[1];
+    return rc;
+}

@@ -76,6 +76,10 @@ void ko_quantize_row_q5_0(const float *x, uint8_t *y, int64_t k);
  * truncf(s + 0.49999997f): the stage-in's q8_0 rounding, checked over every
  * float of the range |x*id| can take. */
 uint64_t ko_round_trick_mismatches(float lo, float hi);
+/* Floats with bits in [lo_bits, hi_bits) where the stage-in's division-free
+ * a / 127 (product with RN(1/127), one FMA residual, one FMA correction)
+ * differs from the IEEE quotient. */
+uint64_t ko_div127_mismatches(uint32_t lo_bits, uint32_t hi_bits);
 
 /* Dequantisation (inverse maps, used for error-bound invariants).
  * q8_0 / q4_0: llama-kvmem-stagein.cu:132-157. */

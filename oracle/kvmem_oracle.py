@@ -80,6 +80,8 @@ def lib() -> C.CDLL:
     L.ko_quantize_rows_f32.argtypes = [C.c_int, f32p, u8p, C.c_int64, C.c_int64]
     L.ko_q_accumulate.restype = None
     L.ko_q_accumulate.argtypes = [f32p, u32, u32, u32, C.c_void_p, u32, C.c_int, f32p]
+    L.ko_div127_mismatches.restype = C.c_uint64
+    L.ko_div127_mismatches.argtypes = [C.c_uint32, C.c_uint32]
     L.ko_round_trick_mismatches.restype = C.c_uint64
     L.ko_round_trick_mismatches.argtypes = [C.c_float, C.c_float]
     L.ko_max_threads.restype = C.c_int

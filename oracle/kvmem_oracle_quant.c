@@ -289,3 +289,22 @@ uint64_t ko_round_trick_mismatches(float lo, float hi) {
     }
     return bad;
 }
+
+/* Non-negative floats a in bit range [lo_bits, hi_bits) where the stage-in's
+ * q8_0 scale shortcut, q0 = a * RN(1/127), q = fma(fma(-q0, 127, a),
+ * RN(1/127), q0), differs from the IEEE quotient a / 127.0f. */
+uint64_t ko_div127_mismatches(uint32_t lo_bits, uint32_t hi_bits) {
+    const float r127 = 1.0f / 127.0f;
+    uint64_t bad = 0;
+    for (uint32_t b = lo_bits; b < hi_bits; ++b) {
+        float a;
+        memcpy(&a, &b, 4);
+        const float q0 = a * r127;
+        const float q = fmaf(fmaf(-q0, 127.0f, a), r127, q0);
+        const float want = a / 127.0f;
+        if (memcmp(&q, &want, 4) != 0) {
+            ++bad;
+        }
+    }
+    return bad;
+}

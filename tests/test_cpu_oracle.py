@@ -277,3 +277,11 @@ def test_q8_rounding_shortcut_exhaustive(oracle):
     assert oracle.lib().ko_round_trick_mismatches(0.0, 1.0) == 0
     s = np.float32(0.49999997)
     assert np.trunc(np.float32(s + np.float32(0.5))) != np.round(s)
+
+
+def test_q8_scale_division_shortcut_exhaustive(oracle):
+    """q8_0's d = amax / 127 is computed as a * RN(1/127) plus one exact FMA
+    correction; over every non-negative float (zero, subnormals, normals)
+    that equals the IEEE quotient.  The reciprocal shortcut depends on the
+    device's rcp and is checked on the GPU (test_gpu_stagein)."""
+    assert oracle.lib().ko_div127_mismatches(0x00000000, 0x7F800000) == 0

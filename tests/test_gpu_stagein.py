@@ -217,3 +217,11 @@ def test_move_slots_overlapping(ctx):
                 want[d] = before[s]
             got = p.cpu().numpy().reshape(n_slots, -1)
             assert np.array_equal(got, want)
+
+
+def test_scale_shortcuts_exhaustive(ctx):
+    """The quantizers' division-free scale arithmetic equals the IEEE
+    quotients over every float of its range, on this device."""
+    announce("scale arithmetic: a/127 over all non-negative floats, 1/d over all normal |d| <= 2^126")
+    div, rec = ctx.check_scale_arith()
+    assert (div, rec) == (0, 0)
