@@ -96,6 +96,51 @@ KVMEM_HIP_API void *kvmem_hip_get_stream(const kvmem_hip_ctx *ctx);
  * Replaces kvmem_stagein_sync (llama-kvmem-stagein.h:27, stagein.cu:615-617). */
 KVMEM_HIP_API int kvmem_hip_sync(kvmem_hip_ctx *ctx);
 
+/* Shapes a caller will use, so that later calls of at most these sizes run
+ * without allocating device or pinned memory.  Zero fields reserve nothing
+ * for their part. */
+typedef struct kvmem_hip_reserve_args {
+    uint32_t n_layers;         /* scored history layers */
+    uint32_t n_blocks;         /* history blocks scored / selected over */
+    uint32_t n_head;           /* query heads */
+    uint32_t n_head_kv;        /* KV heads */
+    uint32_t head_dim;         /* 128 or 256 */
+    uint32_t n_q_tokens;       /* query tokens per layer (per-token scorer) */
+    uint32_t max_items;        /* largest id / op list passed in one call */
+    uint32_t pad0;
+    uint64_t h2d_block_bytes;  /* one block over every layer in a host source:
+                                  F16 K+V rows (stagein_blocks_host) or packed
+                                  rows (stagein_packed_host); 0 = none */
+    uint64_t d2h_block_bytes;  /* one block's packed rows over every layer
+                                  (stageout_blocks); 0 = none */
+    uint64_t move_bytes;       /* bytes one kvmem_hip_move_slots call gathers */
+} kvmem_hip_reserve_args;
+
+/* Grow every scratch buffer, ring and upload slot to fit `args`.  Replaces
+ * the up-front sizing of kvmem_stagein_gpu_ready(n_f32, n_packed)
+ * (llama-kvmem-stagein.h:12, stagein.cu:319-393); buffers only grow, and
+ * growing waits for work still reading the old ones. */
+KVMEM_HIP_API int kvmem_hip_reserve(kvmem_hip_ctx *ctx, const kvmem_hip_reserve_args *args);
+
+/* Memory the context holds and the number of device/pinned allocations it
+ * has made since creation (a call that allocated nothing leaves the count
+ * unchanged).  No counterpart in the reference; the singleton's sizes
+ * n_f32 / n_q (stagein.cu:60-90) are the nearest. */
+typedef struct kvmem_hip_scratch {
+    uint64_t device_bytes;
+    uint64_t pinned_bytes;
+    uint64_t allocations;
+} kvmem_hip_scratch;
+KVMEM_HIP_API int kvmem_hip_scratch_info(const kvmem_hip_ctx *ctx, kvmem_hip_scratch *out);
+
+/* Enqueue a copy of `n` host bytes to device memory `dst` on the context
+ * stream.  Replaces kvmem_stagein_h2d_bytes (llama-kvmem-stagein.h:26,
+ * stagein.cu:607-613): n == 0 is a no-op that succeeds, and no fence is
+ * taken, so the host buffer stays unchanged until kvmem_hip_sync returns
+ * (pinned buffers are read asynchronously; the runtime stages pageable ones
+ * before it returns).  Counted in the profiling copy stage and h2d_bytes. */
+KVMEM_HIP_API int kvmem_hip_h2d_async(kvmem_hip_ctx *ctx, void *dst, const void *src, size_t n);
+
 /* 1 if `type` can be produced by the stage-in kernels.  Replaces
  * kvmem_stagein_quant_ok (llama-kvmem-stagein.h:16; the reference accepts
  * only Q8_0 and Q4_0, stagein.cu:444-446). */

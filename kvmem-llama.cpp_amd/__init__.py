@@ -104,6 +104,17 @@ class MeanKArgs(C.Structure):
                 ("head_dim", C.c_uint32), ("scores", C.c_void_p)]
 
 
+class ReserveArgs(C.Structure):
+    _fields_ = [("n_layers", C.c_uint32), ("n_blocks", C.c_uint32), ("n_head", C.c_uint32),
+                ("n_head_kv", C.c_uint32), ("head_dim", C.c_uint32), ("n_q_tokens", C.c_uint32),
+                ("max_items", C.c_uint32), ("pad0", C.c_uint32), ("h2d_block_bytes", C.c_uint64),
+                ("d2h_block_bytes", C.c_uint64), ("move_bytes", C.c_uint64)]
+
+
+class Scratch(C.Structure):
+    _fields_ = [("device_bytes", C.c_uint64), ("pinned_bytes", C.c_uint64), ("allocations", C.c_uint64)]
+
+
 class Perf(C.Structure):
     _fields_ = [("score_ms", C.c_double), ("topk_ms", C.c_double), ("set_ms", C.c_double),
                 ("copy_ms", C.c_double), ("layout_ms", C.c_double), ("n_score", C.c_uint64),
@@ -159,6 +170,9 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
          pu32, u32)
     _sig(lib, "kvmem_hip_stagein_packed_host", i32, vp, C.POINTER(PackedHost), C.POINTER(Pool), pu32, pu32,
          pu32, u32)
+    _sig(lib, "kvmem_hip_reserve", i32, vp, C.POINTER(ReserveArgs))
+    _sig(lib, "kvmem_hip_scratch_info", i32, vp, C.POINTER(Scratch))
+    _sig(lib, "kvmem_hip_h2d_async", i32, vp, vp, vp, sz)
     _sig(lib, "kvmem_hip_perf_enable", i32, vp, i32)
     _sig(lib, "kvmem_hip_perf_get", i32, vp, C.POINTER(Perf))
     _sig(lib, "kvmem_hip_perf_reset", None, vp)
@@ -313,6 +327,19 @@ class Context:
         d, m = _u32_array(dst_slots)
         assert n == m
         self.check(self.lib.kvmem_hip_move_slots(self.h, C.byref(pool), s, d, n), "move_slots")
+
+    def reserve(self, **sizes) -> None:
+        """Grow scratch for calls of at most these sizes (ReserveArgs fields)."""
+        self.check(self.lib.kvmem_hip_reserve(self.h, C.byref(ReserveArgs(**sizes))), "reserve")
+
+    def scratch_info(self) -> dict:
+        out = Scratch()
+        self.check(self.lib.kvmem_hip_scratch_info(self.h, C.byref(out)), "scratch_info")
+        return {name: getattr(out, name) for name, _ in out._fields_}
+
+    def h2d_async(self, dst_ptr: int, src_ptr: int, n: int) -> None:
+        """Enqueue an n-byte host-to-device copy on the context stream."""
+        self.check(self.lib.kvmem_hip_h2d_async(self.h, dst_ptr or None, src_ptr or None, n), "h2d_async")
 
     def d2d_batched(self, srcs, dsts, nbytes) -> None:
         n = len(srcs)

@@ -46,6 +46,7 @@ bool ensure_dev(kvmem_hip_ctx *ctx, DevBuf &b, size_t bytes, const char *what) {
         return false;
     }
     b.bytes = want;
+    ctx->n_allocs += 1;
     return true;
 }
 
@@ -67,6 +68,7 @@ bool ensure_pin(kvmem_hip_ctx *ctx, PinBuf &b, size_t bytes, const char *what) {
         return false;
     }
     b.bytes = want;
+    ctx->n_allocs += 1;
     return true;
 }
 
@@ -338,6 +340,110 @@ int kvmem_hip_sync(kvmem_hip_ctx *ctx) {
         !hip_ok(ctx, hipStreamSynchronize(ctx->stream), "sync")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_hip_reserve(kvmem_hip_ctx *ctx, const kvmem_hip_reserve_args *a) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!a) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "reserve: null arguments");
+    }
+    const uint32_t L = a->n_layers;
+    const uint32_t B = a->n_blocks;
+    if (a->n_head_kv && a->n_head % a->n_head_kv != 0) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "reserve: n_head must be a multiple of n_head_kv");
+    }
+    if (a->head_dim != 0 && a->head_dim != 128 && a->head_dim != 256) {
+        return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "reserve: head_dim must be 128 or 256");
+    }
+    (void) hipSetDevice(ctx->device);
+    const int nomem = KVMEM_HIP_ERR_NOMEM;  // the failing call is in last_error
+    if (L && B && a->n_head_kv && a->n_q_tokens &&
+        !ensure_dev(ctx, ctx->score_partial,
+                    score_partial_bytes(L, a->n_head_kv, B, a->n_q_tokens, a->n_head / a->n_head_kv),
+                    "reserve score partial")) {
+        return nomem;
+    }
+    if (L && B && !ensure_dev(ctx, ctx->score_layers, sizeof(float) * static_cast<size_t>(L) * B,
+                              "reserve score layers")) {
+        return nomem;
+    }
+    if (L && B && a->n_head_kv && a->head_dim &&
+        !ensure_dev(ctx, ctx->meank_scratch, meank_scratch_bytes(L, a->n_head_kv, B, a->head_dim),
+                    "reserve score_meank scratch")) {
+        return nomem;
+    }
+    if (B && (!ensure_dev(ctx, ctx->topk_sel, topk_out_bytes(B), "reserve topk output") ||
+              !ensure_pin(ctx, ctx->topk_sel_host, topk_out_bytes(B), "reserve topk pinned output"))) {
+        return nomem;
+    }
+    if (a->max_items || L) {
+        const size_t up = upload_bytes_for(std::max(a->max_items, B), L);
+        for (auto &slot : ctx->upload) {
+            if (!ensure_pin(ctx, slot.host, up, "reserve upload") ||
+                !ensure_dev(ctx, slot.dev, up, "reserve upload")) {
+                return nomem;
+            }
+            if (!slot.done && !hip_ok(ctx, hipEventCreateWithFlags(&slot.done, hipEventDisableTiming),
+                                      "reserve upload event")) {
+                return KVMEM_HIP_ERR_RUNTIME;
+            }
+        }
+    }
+    if (a->h2d_block_bytes && !ensure_h2d_ring(ctx, a->h2d_block_bytes)) {
+        return nomem;
+    }
+    if (a->d2h_block_bytes && !ensure_d2h_ring(ctx, a->d2h_block_bytes)) {
+        return nomem;
+    }
+    if (a->move_bytes && !ensure_dev(ctx, ctx->move_scratch, a->move_bytes, "reserve move_slots scratch")) {
+        return nomem;
+    }
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_hip_scratch_info(const kvmem_hip_ctx *ctx, kvmem_hip_scratch *out) {
+    if (!ctx || !out) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    uint64_t dev = 0;
+    uint64_t pin = 0;
+    for (const auto &s : ctx->upload) {
+        dev += s.dev.bytes;
+        pin += s.host.bytes;
+    }
+    for (const DevBuf *b : {&ctx->score_partial, &ctx->score_layers, &ctx->meank_scratch,
+                            &ctx->move_scratch, &ctx->topk_sel, &ctx->h2d_ring, &ctx->d2h_ring}) {
+        dev += b->bytes;
+    }
+    pin += ctx->topk_sel_host.bytes;
+    out->device_bytes = dev;
+    out->pinned_bytes = pin;
+    out->allocations = ctx->n_allocs;
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_hip_h2d_async(kvmem_hip_ctx *ctx, void *dst, const void *src, size_t n) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (n == 0) {
+        return KVMEM_HIP_OK;
+    }
+    if (!dst || !src) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "h2d_async: null pointer");
+    }
+    (void) hipSetDevice(ctx->device);
+    perf_begin(ctx, kPerfCopy);
+    const bool ok = hip_ok(ctx, hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, ctx->stream),
+                           "h2d_async");
+    perf_end(ctx, kPerfCopy);
+    if (!ok) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    ctx->h2d_bytes += n;
     return KVMEM_HIP_OK;
 }
 

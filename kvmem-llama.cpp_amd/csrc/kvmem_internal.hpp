@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstddef>
 #include <cstdint>
 #include <string>
@@ -81,6 +82,7 @@ struct kvmem_hip_ctx {
     uint64_t perf_n[kvmem_hip::kPerfStages] = {};
     uint64_t h2d_bytes = 0;
     uint64_t d2d_bytes = 0;
+    uint64_t n_allocs = 0;  // device + pinned allocations since creation
 };
 
 namespace kvmem_hip {
@@ -108,6 +110,27 @@ bool launch_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, cons
 // `min_slot_bytes` (32 MiB or more, grown only), with their events.
 constexpr int kH2dRing = 4;
 bool ensure_h2d_ring(kvmem_hip_ctx *ctx, size_t min_slot_bytes);
+
+// The stage-out ring: two device slots of at least `min_slot_bytes`
+// (128 MiB or more, grown only), with their events.
+bool ensure_d2h_ring(kvmem_hip_ctx *ctx, size_t min_slot_bytes);
+
+// Scratch sizes of the entry points, shared with kvmem_hip_reserve.
+// Per-token scorer partial maxima for `n_q_tokens` query tokens of `g` query
+// heads per KV head.
+size_t score_partial_bytes(uint32_t L, uint32_t Hkv, uint32_t B, uint32_t n_q_tokens, uint32_t g);
+// Mean-K scorer: query vectors and per-(layer, block) cosines.
+size_t meank_scratch_bytes(uint32_t L, uint32_t Hkv, uint32_t B, uint32_t D);
+// Selection output of kvmem_hip_topk over `n` blocks (device and pinned).
+inline size_t topk_out_bytes(uint32_t n) { return (static_cast<size_t>(n) + 1) * sizeof(uint32_t); }
+// Largest table one call with `items` ids / ops / blocks over `L` layers
+// uploads: 32-byte quantize ops, 24-byte copies of K and V per layer for a
+// block (packed stage-in/out, slot moves), or 16-byte block items after 2L
+// pool pointers and up to 128 RoPE frequencies.
+inline size_t upload_bytes_for(uint32_t items, uint32_t L) {
+    const size_t per_item = std::max<size_t>(32, 48 * static_cast<size_t>(L));
+    return per_item * items + 16 * static_cast<size_t>(L) + 1024;
+}
 
 // Copy `bytes` of host data to device memory through the upload ring,
 // ordered on the context stream.  Returns the device address or nullptr.

@@ -251,6 +251,17 @@ __global__ __launch_bounds__(256) void meank_combine_kernel(const double *layer_
     scores[b] = static_cast<float>(nlay ? acc / nlay : 0.0);
 }
 
+// Per-(layer, block) cosine sums in double, rounded up to 256 bytes so the
+// query vectors after them start aligned.
+static size_t meank_cos_bytes(uint32_t L, uint32_t B) {
+    return (sizeof(double) * static_cast<size_t>(L) * B + 255) & ~static_cast<size_t>(255);
+}
+
+size_t meank_scratch_bytes(uint32_t L, uint32_t Hkv, uint32_t B, uint32_t D) {
+    const size_t qv_bytes = sizeof(float) * static_cast<size_t>(L) * Hkv * (D + 1);
+    return meank_cos_bytes(L, B) + qv_bytes + 256;
+}
+
 }  // namespace kvmem_hip
 
 using namespace kvmem_hip;
@@ -406,10 +417,10 @@ int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {
         invq[l] = a->q_count[l] ? 1.0f / static_cast<float>(a->q_count[l] * g) : 0.0f;
     }
     (void) hipSetDevice(ctx->device);
-    const size_t qv_bytes = sizeof(float) * static_cast<size_t>(L) * a->n_head_kv * (D + 1);
     // the fp32 query vectors start 256-byte aligned (read as float4)
-    const size_t cos_bytes = (sizeof(double) * static_cast<size_t>(L) * B + 255) & ~static_cast<size_t>(255);
-    if (!ensure_dev(ctx, ctx->meank_scratch, qv_bytes + cos_bytes + 256, "score_meank scratch")) {
+    const size_t cos_bytes = meank_cos_bytes(L, B);
+    if (!ensure_dev(ctx, ctx->meank_scratch, meank_scratch_bytes(L, a->n_head_kv, B, D),
+                    "score_meank scratch")) {
         return KVMEM_HIP_ERR_NOMEM;
     }
     uint8_t *scratch = static_cast<uint8_t *>(ctx->meank_scratch.ptr);

@@ -66,6 +66,10 @@ int check_packed(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const kvmem_hip
     return KVMEM_HIP_OK;
 }
 
+}  // namespace
+
+namespace kvmem_hip {
+
 bool ensure_d2h_ring(kvmem_hip_ctx *ctx, size_t min_slot_bytes) {
     // device-to-host copies reach the link rate only in large pieces
     const size_t want = std::max<size_t>(size_t{128} << 20, min_slot_bytes);
@@ -101,7 +105,7 @@ bool ensure_d2h_ring(kvmem_hip_ctx *ctx, size_t min_slot_bytes) {
     return true;
 }
 
-}  // namespace
+}  // namespace kvmem_hip
 
 extern "C" {
 

@@ -299,6 +299,12 @@ __global__ __launch_bounds__(256) void score_combine_kernel(const float *layer_s
     scores[b] = acc;
 }
 
+size_t score_partial_bytes(uint32_t L, uint32_t Hkv, uint32_t B, uint32_t n_q_tokens, uint32_t g) {
+    const size_t rows = static_cast<size_t>(n_q_tokens) * g;
+    const size_t slices = (rows + kRowsPerGroup - 1) / kRowsPerGroup * kScoreWaves;
+    return sizeof(float) * slices * L * Hkv * B;
+}
+
 }  // namespace kvmem_hip
 
 using namespace kvmem_hip;
@@ -370,7 +376,7 @@ extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist
 
     (void) hipSetDevice(ctx->device);
     const uint32_t slices = p.RG * kScoreWaves;
-    const size_t partial_bytes = sizeof(float) * static_cast<size_t>(slices) * L * p.Hkv * B;
+    const size_t partial_bytes = score_partial_bytes(L, p.Hkv, B, p.Tq, p.g);
     if (!ensure_dev(ctx, ctx->score_partial, partial_bytes, "score partial")) {
         return KVMEM_HIP_ERR_NOMEM;
     }
