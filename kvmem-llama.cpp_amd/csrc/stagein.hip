@@ -801,23 +801,41 @@ __device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8
 extern __shared__ float4 rope_tab4[];
 #define rope_tab reinterpret_cast<float2 *>(rope_tab4)
 
+// Chunk of workgroup `b` out of `n`.  Workgroups go to the 8 XCDs round-robin
+// by id; in each group of 8 * kXcdTile chunks, XCD x takes kXcdTile
+// consecutive chunks (whole operations: 8 chunks are one (block, layer) run
+// at 128 tokens x 1024 elements), so the pages of an operation are
+// translated by one XCD only, while the chunks in flight on the chip stay
+// one contiguous window.  The tail of fewer than 8 * kXcdTile chunks keeps
+// the identity order.  A bijection on [0, n).
+constexpr uint32_t kXcdTile = 64;
+__device__ inline uint32_t xcd_chunk(uint32_t b, uint32_t n) {
+    constexpr uint32_t G = 8u * kXcdTile;
+    if (b >= n - n % G) {
+        return b;
+    }
+    const uint32_t r = b % G;
+    return (b - r) + (r & 7u) * kXcdTile + (r >> 3);
+}
+
 template <int TYPE, class Source, bool XF>
 __global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kWaveGroups * Fmt<TYPE>::GB];
-    quant_chunk<TYPE, Source, XF>(source, blockIdx.x, lds, rope_tab);
+    quant_chunk<TYPE, Source, XF>(source, xcd_chunk(blockIdx.x, gridDim.x), lds, rope_tab);
 }
 
-// K and V of a block job in one launch: workgroups [0, n_k) take K chunks,
-// the rest V chunks (the branch is uniform per workgroup).
+// K and V of a block job in one launch: chunks [0, n_k) are K, the rest V
+// (the branch is uniform per workgroup).
 template <int TK, int TV, bool XF>
 __global__ __launch_bounds__(256) void quant_scatter_kv_kernel(BlockSource sk, BlockSource sv,
                                                                uint32_t n_k) {
     constexpr int GB = Fmt<TK>::GB > Fmt<TV>::GB ? Fmt<TK>::GB : Fmt<TV>::GB;
     __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kWaveGroups * GB];
-    if (blockIdx.x < n_k) {
-        quant_chunk<TK, BlockSource, XF>(sk, blockIdx.x, lds, rope_tab);
+    const uint32_t c = xcd_chunk(blockIdx.x, gridDim.x);
+    if (c < n_k) {
+        quant_chunk<TK, BlockSource, XF>(sk, c, lds, rope_tab);
     } else {
-        quant_chunk<TV, BlockSource, XF>(sv, blockIdx.x - n_k, lds, rope_tab);
+        quant_chunk<TV, BlockSource, XF>(sv, c - n_k, lds, rope_tab);
     }
 }
 
