@@ -13,7 +13,8 @@
 // load waits.  Each wave keeps 96 query rows resident in VGPRs as f16
 // A-fragments of v_mfma_f32_16x16x32_f16 (loaded once; bf16 queries are
 // converted to f16 on the way, exact for normal-range values), so every
-// 16-byte B-fragment read from LDS feeds six MFMAs.  Half a block's K tile
+// 16-byte B-fragment read from LDS feeds six MFMAs (two reads kept in
+// flight ahead of their MFMAs).  Half a block's K tile
 // (64 keys x head_dim halves of one KV head, 32 KiB) moves HBM -> LDS with
 // global_load_lds_dwordx4 (no register staging) into one of two LDS
 // buffers while the other buffer's keys are multiplied: one barrier per
@@ -199,6 +200,15 @@ __global__ __launch_bounds__(kScoreThreads, 2) void score_kernel(ScoreParams p) 
         }
     }
 
+    // LDS byte address of B fragment (kt, ks) in buffer buf, i.e. of the
+    // swizzled chunk (ks*4 + kgrp) ^ (key mod CH) of key kt*16 + lrow:
+    //   (tiles + buf*TILE + kt*16*ROW_BYTES + lrow*ROW_BYTES + (kgrp ^ lrow)*16)
+    //     ^ (ks*64 ^ ((kt*16) mod CH)*16)
+    // -- everything at or above the row size is added, the swizzle bits
+    // below it XORed in, so one VALU per read and one register per lane.
+    const uint32_t lds0 = (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) uint8_t *)(&tiles[0][0]));
+    const uint32_t lane_b = lrow * ROW_BYTES + ((kgrp ^ lrow) * 16u);
+
     float *out = p.partial +
                  ((static_cast<uint64_t>(rg * kScoreWaves + wave) * p.L + l) * p.Hkv + h) * p.B;
     const uint32_t n_tiles = 2u * (b_end - b_begin);
@@ -212,45 +222,62 @@ __global__ __launch_bounds__(kScoreThreads, 2) void score_kernel(ScoreParams p) 
         if (it + 1 < n_tiles) {
             issue_tile(it + 1, buf ^ 1);
         }
-        const uint8_t *tile = tiles[buf];
+        // B fragments of the tile: f = kt * KS + ks covers keys kt*16 .. +16
+        // and k-slice ks.  The reads are inline asm with explicit
+        // lgkmcnt waits that carry the fragment register as an operand:
+        // two reads stay in flight ahead of the six MFMAs that consume a
+        // fragment, in three registers.  (Compiler-issued reads ended up
+        // with a single register, each read waiting out the MFMAs before
+        // it and its own latency after.)  Every read is waited for inside
+        // the tile, before the next barrier.
+        uint32_t tb = lds0 + static_cast<uint32_t>(buf) * TILE + lane_b;
+        asm volatile("" : "+v"(tb));  // recompute the read addresses per tile
+        auto read_b = [&](int f) {
+            const uint32_t kt = static_cast<uint32_t>(f / KS);
+            const uint32_t ks = static_cast<uint32_t>(f % KS);
+            const uint32_t addr = (tb + kt * (16u * ROW_BYTES)) ^ (ks * 64u ^ ((kt * 16u) & (CH - 1u)) * 16u);
+            half8_t r;
+            asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+            return r;
+        };
+        constexpr int NF = (kTileKeys / 16) * KS;
+        constexpr int PF = 2;  // reads in flight ahead of the consumed one
+        half8_t bq[PF + 1];
 #pragma unroll
-        for (int kt = 0; kt < kTileKeys / 16; ++kt) {
-            const uint32_t key = kt * 16 + lrow;
-            const uint8_t *krow = tile + key * ROW_BYTES;
-            float4_t acc[kRowTiles];
+        for (int f = 0; f < PF; ++f) {
+            bq[f] = read_b(f);
+        }
+        float4_t acc[kRowTiles];
 #pragma unroll
-            for (int rt = 0; rt < kRowTiles; ++rt) {
-                acc[rt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int f = 0; f < NF; ++f) {
+            const int ks = f % KS;
+            half8_t &bf = bq[f % (PF + 1)];
+            if (f + PF < NF) {
+                bq[(f + PF) % (PF + 1)] = read_b(f + PF);
+            }
+            // LDS reads return in order: wait until only the newer ones
+            // (at most PF) are outstanding
+            const int newer = (NF - 1 - f) < PF ? (NF - 1 - f) : PF;
+            if (newer == 2) {
+                asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(bf) :: "memory");
+            } else if (newer == 1) {
+                asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(bf) :: "memory");
+            } else {
+                asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(bf) :: "memory");
             }
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const uint32_t cpos = (static_cast<uint32_t>(ks * 4) + kgrp) ^ (key % CH);
-                const half8_t bf = *reinterpret_cast<const half8_t *>(krow + cpos * 16u);
+            for (int rt = 0; rt < kRowTiles; ++rt) {
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    a[rt][ks], bf, ks == 0 ? float4_t{0.0f, 0.0f, 0.0f, 0.0f} : acc[rt], 0, 0, 0);
+            }
+            if (ks == KS - 1) {
 #pragma unroll
                 for (int rt = 0; rt < kRowTiles; ++rt) {
-                    acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rt][ks], bf, acc[rt], 0, 0, 0);
+                    m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(acc[rt][0], acc[rt][1]),
+                                                           __builtin_fmaxf(acc[rt][2], acc[rt][3])));
                 }
             }
-#pragma unroll
-            for (int rt = 0; rt < kRowTiles; ++rt) {
-                m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(acc[rt][0], acc[rt][1]),
-                                                       __builtin_fmaxf(acc[rt][2], acc[rt][3])));
-            }
         }
-        // Issue order of the tile's 64 B-fragment reads and 384 MFMAs: the
-        // read of fragment f+1 goes out right after the first MFMA of
-        // fragment f, so the other five MFMAs of f cover its latency.  (An
-        // LDS DMA in flight makes the compiler wait for every outstanding
-        // LDS read before a consumer, so reads further ahead would not help.)
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-#pragma unroll
-        for (int f = 0; f < (kTileKeys / 16) * KS - 1; ++f) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, kRowTiles - 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, kRowTiles, 0);
-        __builtin_amdgcn_sched_barrier(0);
         if (it & 1u) {  // both halves of the block are in m
             m = wave_max(m);
             if (lane == 0) {
