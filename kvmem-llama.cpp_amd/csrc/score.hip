@@ -150,6 +150,18 @@ __global__ __launch_bounds__(kScoreThreads, 2) void score_kernel(ScoreParams p) 
 
     // ---- K tiles: direct HBM -> LDS, swizzled chunk order
     const uint64_t key_stride = static_cast<uint64_t>(p.Hkv) * ROW_BYTES;
+    // A full tile (64 keys inside the block) has no duplicated keys: the
+    // source offset of load `inst` (key j = KPI*inst + lane/CH, chunk
+    // (lane mod CH) ^ (j mod CH)) splits into a uniform part in SGPRs,
+    // KPI*inst*key_stride, and a per-lane part XOR a per-load constant:
+    //   lane_src ^ ((KPI*inst mod CH) * 16),
+    //   lane_src = (lane/CH)*key_stride + ((lane mod CH) ^ (lane/CH))*16
+    // (the XORed bits lie below ROW_BYTES, and key_stride is a multiple of
+    // it), one VALU per load.  The last tile of a partial block takes the
+    // general path, which clamps keys to the last valid one.
+    constexpr uint32_t KPI = 1024u / ROW_BYTES;  // keys per wave-wide 1 KiB load
+    const uint32_t lane_src = (lane / CH) * static_cast<uint32_t>(key_stride) +
+                              (((lane % CH) ^ (lane / CH)) * 16u);
     // tile `it` = keys [64*(it&1), 64*(it&1) + 64) of block b_begin + it/2
     auto issue_tile = [&](uint32_t it, int buf) {
         const uint32_t b = b_begin + (it >> 1);
@@ -157,9 +169,23 @@ __global__ __launch_bounds__(kScoreThreads, 2) void score_kernel(ScoreParams p) 
         const uint8_t *base = p.k + ((static_cast<uint64_t>(l) * p.cap + b) * p.T) * key_stride +
                               static_cast<uint64_t>(h) * ROW_BYTES;
         const uint32_t nt = (b + 1 == p.B && p.last_T != 0) ? p.last_T : p.T;
-        // the lane id passes through an empty asm so the per-load offsets
-        // are recomputed here (a few VALU per tile) instead of being kept
-        // live across the loop next to the 192 registers of query rows
+        // the lane terms pass through an empty asm so the per-load offsets
+        // are recomputed here (a VALU or a few per load) instead of being
+        // kept live across the loop next to the 192 registers of query rows
+        if (k0 + kTileKeys <= nt) {
+            uint32_t ls = lane_src;
+            asm volatile("" : "+v"(ls));
+            const uint8_t *tbase = base + static_cast<uint64_t>(k0) * key_stride;
+#pragma unroll
+            for (int i = 0; i < LOADS_PER_WAVE; ++i) {
+                const uint32_t inst = wave * LOADS_PER_WAVE + i;
+                const uint32_t voff = ls ^ (((KPI * inst) & (CH - 1u)) * 16u);
+                const uint8_t *src = tbase + static_cast<uint64_t>(KPI * inst) * key_stride + voff;
+                __builtin_amdgcn_global_load_lds(
+                    src, (lds_void_t *) (&tiles[buf][inst * 1024u]), 16, 0, 0);
+            }
+            return;
+        }
         uint32_t ln = lane;
         asm volatile("" : "+v"(ln));
 #pragma unroll
