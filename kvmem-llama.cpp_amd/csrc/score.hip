@@ -56,6 +56,9 @@ constexpr int kRowsPerWave = kRowTiles * 16;               // 96
 constexpr int kRowsPerGroup = kScoreWaves * kRowsPerWave;  // 384
 constexpr int kMaxTokens = 128;                            // keys per block (at most)
 constexpr int kTileKeys = 64;                              // keys per LDS tile (half a block)
+// Cache policy of the tile DMA: nt (streamed once; keeps L2 for the query
+// rows, and costs less energy in the power-capped regime this kernel runs in).
+constexpr int kDmaNonTemporal = 2;
 
 struct ScoreParams {
     const uint16_t *q;       // [L][Tq][Hq][D] bf16 or f16 bits
@@ -182,7 +185,7 @@ __global__ __launch_bounds__(kScoreThreads, 2) void score_kernel(ScoreParams p) 
                 const uint32_t voff = ls ^ (((KPI * inst) & (CH - 1u)) * 16u);
                 const uint8_t *src = tbase + static_cast<uint64_t>(KPI * inst) * key_stride + voff;
                 __builtin_amdgcn_global_load_lds(
-                    src, (lds_void_t *) (&tiles[buf][inst * 1024u]), 16, 0, 0);
+                    src, (lds_void_t *) (&tiles[buf][inst * 1024u]), 16, 0, kDmaNonTemporal);
             }
             return;
         }
@@ -197,7 +200,7 @@ __global__ __launch_bounds__(kScoreThreads, 2) void score_kernel(ScoreParams p) 
             const uint32_t jj = min(k0 + j, nt - 1u);           // duplicate the last key
             const uint8_t *src = base + jj * key_stride + c * 16u;
             __builtin_amdgcn_global_load_lds(
-                src, (lds_void_t *) (&tiles[buf][inst * 1024u]), 16, 0, 0);
+                src, (lds_void_t *) (&tiles[buf][inst * 1024u]), 16, 0, kDmaNonTemporal);
         }
     };
 
