@@ -47,7 +47,7 @@ N_CHANGED = round(0.3 * BUDGET)   # 77
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE on this
 # workload, scaled by the copy-kernel calibration (profiles/traffic_reselect_256k.md)
-SCORE_TRAFFIC_BYTES = 8.597e9 + 1.922e7
+SCORE_TRAFFIC_BYTES = 8.597e9 + 2.10e6
 STAGEIN_TRAFFIC_BYTES = 6.458e8 + 3.431e8
 MFMA_F16_PEAK_TFLOPS = 2500.0
 PCIE_PEAK_GBS = 64.0
