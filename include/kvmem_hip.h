@@ -323,15 +323,18 @@ KVMEM_HIP_API int kvmem_hip_stagein_packed_host(kvmem_hip_ctx *ctx,
                                                 const uint32_t *block_ids, const uint32_t *slots,
                                                 const uint32_t *n_tokens, uint32_t n);
 
-/* Move whole slots inside the pool: slot src_slots[i] -> dst_slots[i] for
- * every layer, K and V (quantized bytes copied unchanged).  Overlapping
- * moves are hazard-free: sources are gathered to device scratch first.
- * Replaces the gather/scatter D2D of layout_gpu_slots_by_orig_pos
- * (llama-memory-kvmem.cpp:1003-1093). */
+/* Move slots inside the pool: the first n_tokens[i] rows of slot
+ * src_slots[i] -> slot dst_slots[i] for every layer, K and V (quantized
+ * bytes copied unchanged; the destination's rows past n_tokens[i] keep
+ * their bytes).  n_tokens == NULL moves whole slots.  Overlapping moves are
+ * hazard-free: sources are gathered to device scratch first.  Replaces the
+ * gather/scatter D2D of layout_gpu_slots_by_orig_pos, which moves each
+ * block's n_tokens rows (llama-memory-kvmem.cpp:1003-1093). */
 KVMEM_HIP_API int kvmem_hip_move_slots(kvmem_hip_ctx *ctx,
                                        const kvmem_hip_pool *pool,
                                        const uint32_t *src_slots,
                                        const uint32_t *dst_slots,
+                                       const uint32_t *n_tokens,
                                        uint32_t n);
 
 /* Batched device-to-device byte copies in one launch.  Replaces

@@ -157,7 +157,7 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_stagein_blocks", i32, vp, C.POINTER(History), C.POINTER(Pool), pu32, pu32, u32)
     _sig(lib, "kvmem_hip_stagein_blocks_host", i32, vp, C.POINTER(HostHistory), C.POINTER(Pool),
          pu32, pu32, u32)
-    _sig(lib, "kvmem_hip_move_slots", i32, vp, C.POINTER(Pool), pu32, pu32, u32)
+    _sig(lib, "kvmem_hip_move_slots", i32, vp, C.POINTER(Pool), pu32, pu32, pu32, u32)
     _sig(lib, "kvmem_hip_d2d_batched", i32, vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(sz), i32)
     _sig(lib, "kvmem_hip_score", i32, vp, C.POINTER(History), C.POINTER(ScoreArgs))
     _sig(lib, "kvmem_hip_topk", i32, vp, vp, u32, pu32, u32, u32, i32, pu32, pu32)
@@ -322,11 +322,17 @@ class Context:
         self.check(self.lib.kvmem_hip_stagein_blocks_host(self.h, C.byref(hist), C.byref(pool), ids,
                                                           sl, n), "stagein_blocks_host")
 
-    def move_slots(self, pool: Pool, src_slots, dst_slots) -> None:
+    def move_slots(self, pool: Pool, src_slots, dst_slots, n_tokens=None) -> None:
+        """Move the first n_tokens[i] rows (default: whole slots) of slot
+        src_slots[i] to dst_slots[i]."""
         s, n = _u32_array(src_slots)
         d, m = _u32_array(dst_slots)
         assert n == m
-        self.check(self.lib.kvmem_hip_move_slots(self.h, C.byref(pool), s, d, n), "move_slots")
+        nt = None
+        if n_tokens is not None:
+            nt, k = _u32_array(n_tokens)
+            assert k == n
+        self.check(self.lib.kvmem_hip_move_slots(self.h, C.byref(pool), s, d, nt, n), "move_slots")
 
     def reserve(self, **sizes) -> None:
         """Grow scratch for calls of at most these sizes (ReserveArgs fields)."""

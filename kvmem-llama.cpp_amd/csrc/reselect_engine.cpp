@@ -1011,7 +1011,7 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
     uint32_t n_moved = 0;
     if (e->p.canonical_layout) {
         // window slot i holds the i-th selected block
-        std::vector<uint32_t> src, dst;
+        std::vector<uint32_t> src, dst, ntok;
         std::vector<uint8_t> staged(n, 0);
         for (uint32_t id : stage_ids) staged[id] = 1;
         stage_slots.clear();
@@ -1022,6 +1022,7 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
             } else if (old_slot[id] >= 0 && static_cast<uint32_t>(old_slot[id]) != i) {
                 src.push_back(static_cast<uint32_t>(old_slot[id]));
                 dst.push_back(i);
+                ntok.push_back(e->rt.store().blocks()[id].n_tokens);
             }
             e->rt.store().set_block_gpu_slot(id, static_cast<int32_t>(i));
         }
@@ -1029,7 +1030,7 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
         e->slots.reset_after(static_cast<uint32_t>(ids.size()));
         if (!src.empty()) {
             const kvmem_hip_pool pool = e->pool_desc();
-            rc = kvmem_hip_move_slots(e->ctx, &pool, src.data(), dst.data(),
+            rc = kvmem_hip_move_slots(e->ctx, &pool, src.data(), dst.data(), ntok.data(),
                                       static_cast<uint32_t>(src.size()));
             if (rc != KVMEM_HIP_OK) {
                 return e->fail_ctx(rc, "apply: canonical layout");

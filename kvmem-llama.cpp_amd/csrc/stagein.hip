@@ -1346,7 +1346,7 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
 }
 
 int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const uint32_t *src_slots,
-                         const uint32_t *dst_slots, uint32_t n) {
+                         const uint32_t *dst_slots, const uint32_t *n_tokens, uint32_t n) {
     if (!ctx) {
         return KVMEM_HIP_ERR_INVALID;
     }
@@ -1368,6 +1368,9 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
         if (src_slots[i] >= pool->n_slots || dst_slots[i] >= pool->n_slots) {
             return fail(ctx, KVMEM_HIP_ERR_INVALID, "move_slots: slot out of range");
         }
+        if (n_tokens && n_tokens[i] > pool->block_tokens) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "move_slots: n_tokens above block_tokens");
+        }
     }
     const uint64_t per_move = (kspan + vspan) * pool->n_layers;
     (void) hipSetDevice(ctx->device);
@@ -1379,6 +1382,10 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
     std::vector<void *> gd, sd;
     std::vector<size_t> nb;
     for (uint32_t i = 0; i < n; ++i) {
+        const uint64_t nt = n_tokens ? n_tokens[i] : pool->block_tokens;
+        if (nt == 0) {
+            continue;  // nothing of this block to move
+        }
         uint8_t *sc = scratch + per_move * i;
         for (uint32_t l = 0; l < pool->n_layers; ++l) {
             uint8_t *kb = static_cast<uint8_t *>(pool->k_layers[l]);
@@ -1386,7 +1393,7 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
             gd.push_back(sc);
             ss.push_back(sc);
             sd.push_back(kb + dst_slots[i] * kspan);
-            nb.push_back(kspan);
+            nb.push_back(nt * krow);
             sc += kspan;
             if (want_v) {
                 uint8_t *vb = static_cast<uint8_t *>(pool->v_layers[l]);
@@ -1394,10 +1401,13 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
                 gd.push_back(sc);
                 ss.push_back(sc);
                 sd.push_back(vb + dst_slots[i] * vspan);
-                nb.push_back(vspan);
+                nb.push_back(nt * vrow);
                 sc += vspan;
             }
         }
+    }
+    if (nb.empty()) {
+        return KVMEM_HIP_OK;
     }
     const int nops = static_cast<int>(nb.size());
     int st = kvmem_hip_d2d_batched(ctx, gs.data(), gd.data(), nb.data(), nops);
