@@ -3,11 +3,16 @@
 // Keys are 64-bit: the high word is the score mapped to an unsigned order
 // (negative floats bit-inverted, positive floats with the sign bit set,
 // -0 folded to +0), the low word encodes the id so that equal scores rank
-// by id (lower id first: ~id; higher id first: id).  Forced ids and padding
-// get key 0, below every finite score.  A bitonic sort of the keys in LDS
-// (descending) puts the `need` best candidates first; their ids plus the
-// forced ids are then flagged and compacted in ascending id order with a
-// workgroup prefix sum, which is the window order of
+// by id (lower id first: ~id; higher id first: id).  Every candidate key is
+// therefore distinct, and the selection is "the `need` largest keys".
+// Forced ids get key 0, below every finite score, and a bit in a mask.
+//
+// The need-th largest key is found by radix select, eight passes of 8 bits
+// from the top: each pass histograms the digit of the keys that match the
+// digits fixed so far, and one wave picks the digit where the running count
+// from the top reaches the remaining rank.  Winners are the keys at or above
+// that threshold; they and the forced ids are compacted in ascending id
+// order with a workgroup prefix sum, which is the window order of
 // KvMemStore::pick_topk_ungrouped (kvmem_store.cpp:618-622).
 #include "kvmem_internal.hpp"
 
@@ -17,8 +22,8 @@
 namespace kvmem_hip {
 
 constexpr int kTopkThreads = 1024;
+constexpr int kTopkWaves = kTopkThreads / 64;
 constexpr int kTopkMaxN = 16384;
-constexpr int kTopkMaxPerThread = kTopkMaxN / kTopkThreads;  // 16
 
 __device__ inline uint64_t rank_key(float s, uint32_t id, bool tie_lower) {
     if (s == 0.0f) {
@@ -30,96 +35,144 @@ __device__ inline uint64_t rank_key(float s, uint32_t id, bool tie_lower) {
     return (static_cast<uint64_t>(ord) << 32) | lo;
 }
 
-__device__ inline uint32_t key_id(uint64_t key, bool tie_lower) {
-    const uint32_t lo = static_cast<uint32_t>(key);
-    return tie_lower ? (0xffffffffu - lo) : lo;
+// Inclusive prefix sum over the workgroup (every thread passes one value).
+__device__ inline uint32_t block_inclusive_scan(uint32_t v, uint32_t *wave_tot) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t t = __shfl_up(v, off, 64);
+        if (lane >= static_cast<uint32_t>(off)) {
+            v += t;
+        }
+    }
+    if (lane == 63u) {
+        wave_tot[wave] = v;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        uint32_t w = lane < static_cast<uint32_t>(kTopkWaves) ? wave_tot[lane] : 0u;
+#pragma unroll
+        for (int off = 1; off < kTopkWaves; off <<= 1) {
+            const uint32_t t = __shfl_up(w, off, 64);
+            if (lane >= static_cast<uint32_t>(off)) {
+                w += t;
+            }
+        }
+        if (lane < static_cast<uint32_t>(kTopkWaves)) {
+            wave_tot[lane] = w;  // inclusive totals of waves 0..lane
+        }
+    }
+    __syncthreads();
+    return v + (wave > 0 ? wave_tot[wave - 1] : 0u);
 }
 
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores, uint32_t n,
-                                                            uint32_t npow2, const uint32_t *forced,
+                                                            const uint32_t *forced,
                                                             uint32_t n_forced, uint32_t need,
                                                             int tie_lower, uint32_t *sel,
                                                             uint32_t *n_sel) {
     __shared__ uint64_t keys[kTopkMaxN];
-    __shared__ uint32_t scan[kTopkThreads];
+    __shared__ uint32_t forced_bits[kTopkMaxN / 32];
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t wave_tot[kTopkWaves];
+    __shared__ uint64_t s_prefix;
+    __shared__ uint32_t s_rank;
     const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
     const bool tl = tie_lower != 0;
 
-    for (uint32_t i = tid; i < npow2; i += kTopkThreads) {
-        keys[i] = i < n ? rank_key(scores[i], i, tl) : 0ull;
+    for (uint32_t i = tid; i < n; i += kTopkThreads) {
+        keys[i] = rank_key(scores[i], i, tl);
+    }
+    for (uint32_t w = tid; w < (n + 31u) / 32u; w += kTopkThreads) {
+        forced_bits[w] = 0u;
     }
     __syncthreads();
     for (uint32_t f = tid; f < n_forced; f += kTopkThreads) {
-        keys[forced[f]] = 0ull;  // position == id before the sort
+        keys[forced[f]] = 0ull;  // out of the race
+        atomicOr(&forced_bits[forced[f] >> 5], 1u << (forced[f] & 31u));
     }
     __syncthreads();
 
-    // bitonic sort, descending
-    for (uint32_t k = 2; k <= npow2; k <<= 1) {
-        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            for (uint32_t i = tid; i < npow2; i += kTopkThreads) {
-                const uint32_t ixj = i ^ j;
-                if (ixj > i) {
-                    const uint64_t a = keys[i];
-                    const uint64_t b = keys[ixj];
-                    const bool desc = (i & k) == 0;
-                    if (desc ? (a < b) : (a > b)) {
-                        keys[i] = b;
-                        keys[ixj] = a;
-                    }
+    // ---- radix select: threshold = the need-th largest candidate key
+    uint64_t prefix = 0ull;
+    uint64_t mask = 0ull;
+    uint32_t rank = need;  // rank still to find among keys matching `prefix`
+    if (need > 0u) {
+        for (int shift = 56; shift >= 0; shift -= 8) {
+            if (tid < 256u) {
+                hist[tid] = 0u;
+            }
+            __syncthreads();
+            for (uint32_t i = tid; i < n; i += kTopkThreads) {
+                const uint64_t k = keys[i];
+                if (k != 0ull && (k & mask) == prefix) {
+                    atomicAdd(&hist[static_cast<uint32_t>(k >> shift) & 255u], 1u);
                 }
             }
             __syncthreads();
+            if (tid < 64u) {
+                // lane owns digits 4*lane .. 4*lane+3; above(d) = count of
+                // matching keys whose digit exceeds d
+                uint32_t c[4];
+                uint32_t own = 0u;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    c[j] = hist[4u * lane + j];
+                    own += c[j];
+                }
+                uint32_t suffix = own;  // sum over lanes >= this one
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1) {
+                    const uint32_t t = __shfl_down(suffix, off, 64);
+                    if (lane + off < 64u) {
+                        suffix += t;
+                    }
+                }
+                uint32_t above = suffix - own;  // digits of higher lanes
+#pragma unroll
+                for (int j = 3; j >= 0; --j) {
+                    if (above < rank && rank <= above + c[j]) {
+                        s_prefix = prefix | (static_cast<uint64_t>(4u * lane + j) << shift);
+                        s_rank = rank - above;
+                    }
+                    above += c[j];
+                }
+            }
+            __syncthreads();
+            prefix = s_prefix;
+            rank = s_rank;
+            mask |= 0xffull << shift;
+            __syncthreads();  // s_prefix / hist are rewritten by the next pass
         }
     }
+    const uint64_t threshold = prefix;  // unique key of rank `need`
 
-    // the winners' ids leave LDS before it is reused for flags
-    uint32_t mine[kTopkMaxPerThread];
-    uint32_t n_mine = 0;
-    for (uint32_t i = tid; i < need; i += kTopkThreads) {
-        const uint64_t key = keys[i];
-        if (key != 0ull) {
-            mine[n_mine++] = key_id(key, tl);
-        }
-    }
-    __syncthreads();
-    uint8_t *flags = reinterpret_cast<uint8_t *>(keys);
-    for (uint32_t i = tid; i < n; i += kTopkThreads) {
-        flags[i] = 0;
-    }
-    __syncthreads();
-    for (uint32_t j = 0; j < n_mine; ++j) {
-        flags[mine[j]] = 1;
-    }
-    for (uint32_t f = tid; f < n_forced; f += kTopkThreads) {
-        flags[forced[f]] = 1;
-    }
-    __syncthreads();
-
-    // ordered compaction: thread t owns ids [t*seg, (t+1)*seg)
+    // ---- ordered compaction: thread t owns ids [t*seg, (t+1)*seg)
     const uint32_t seg = (n + kTopkThreads - 1) / kTopkThreads;
     const uint32_t lo = min(n, tid * seg);
     const uint32_t hi = min(n, lo + seg);
+    auto chosen = [&](uint32_t i) -> bool {
+        const uint64_t k = keys[i];
+        if (k == 0ull) {
+            return (forced_bits[i >> 5] >> (i & 31u)) & 1u;
+        }
+        return need > 0u && k >= threshold;
+    };
     uint32_t cnt = 0;
     for (uint32_t i = lo; i < hi; ++i) {
-        cnt += flags[i];
+        cnt += chosen(i) ? 1u : 0u;
     }
-    scan[tid] = cnt;
-    __syncthreads();
-    for (uint32_t off = 1; off < kTopkThreads; off <<= 1) {
-        const uint32_t v = tid >= off ? scan[tid - off] : 0u;
-        __syncthreads();
-        scan[tid] += v;
-        __syncthreads();
-    }
-    uint32_t pos = scan[tid] - cnt;  // exclusive prefix
+    const uint32_t incl = block_inclusive_scan(cnt, wave_tot);
+    uint32_t pos = incl - cnt;
     for (uint32_t i = lo; i < hi; ++i) {
-        if (flags[i]) {
+        if (chosen(i)) {
             sel[pos++] = i;
         }
     }
     if (tid == kTopkThreads - 1) {
-        *n_sel = scan[tid];
+        *n_sel = incl;
     }
 }
 
@@ -157,10 +210,6 @@ extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t 
     }
     const uint32_t candidates = n - static_cast<uint32_t>(uniq.size());
     need = std::min(need, candidates);
-    uint32_t npow2 = 1;
-    while (npow2 < n) {
-        npow2 <<= 1;
-    }
     (void) hipSetDevice(ctx->device);
     const size_t out_cap = static_cast<size_t>(n) + 1;
     if (!ensure_dev(ctx, ctx->topk_sel, out_cap * sizeof(uint32_t), "topk output") ||
@@ -177,7 +226,7 @@ extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t 
     }
     uint32_t *sel_dev = static_cast<uint32_t *>(ctx->topk_sel.ptr);
     perf_begin(ctx, kPerfTopk);
-    topk_kernel<<<1, kTopkThreads, 0, ctx->stream>>>(scores, n, npow2, forced_dev,
+    topk_kernel<<<1, kTopkThreads, 0, ctx->stream>>>(scores, n, forced_dev,
                                                      static_cast<uint32_t>(uniq.size()), need,
                                                      tie_lower_index, sel_dev, sel_dev + n);
     perf_end(ctx, kPerfTopk);
