@@ -44,14 +44,24 @@
 
 namespace kvmem_hip {
 
-constexpr int kRounds = 8;                     // 16-group rounds per wave
-constexpr int kWaveGroups = 16 * kRounds;      // groups per wave (128)
-constexpr int kChunkGroups = 4 * kWaveGroups;  // groups per workgroup (512)
-constexpr int kTabMax = 4096;                  // (row, rotary pair) entries per chunk
+// A workgroup of 4 waves takes a chunk of 4 * 16 * R groups: each wave R
+// rounds of 16 groups, all R 16-byte loads of a lane in flight.  R by
+// output format, as measured on 77-block jobs at random block ids and slots
+// (fraction of HBM peak at R = 4 / 8 / 16): q8_0 0.70 / 0.66 / 0.66,
+// q5_0 0.64 / 0.67 / 0.67, q4_0 0.67 / 0.68 / 0.67, F16 0.71 / 0.70 / 0.72.
+// With the row transform (VALU-bound) every format uses 8, which bounds the
+// rows of a chunk's RoPE table.
+__host__ __device__ constexpr int rounds_of(int type, bool xf) {
+    return xf ? 8 : type == KVMEM_TYPE_Q8_0 ? 4 : type == KVMEM_TYPE_F16 ? 16 : 8;
+}
+__host__ __device__ constexpr uint32_t chunk_groups_of(int type, bool xf) {
+    return 64u * static_cast<uint32_t>(rounds_of(type, xf));
+}
+constexpr int kTabMax = 4096;  // (row, rotary pair) entries per chunk
 
-// Rows of `gpr` groups that one chunk of kChunkGroups groups can touch.
-inline uint32_t chunk_rows_of(uint32_t gpr) {
-    return (kChunkGroups % gpr == 0) ? kChunkGroups / gpr : (kChunkGroups - 1) / gpr + 2;
+// Rows of `gpr` groups that one chunk of `cg` groups can touch.
+inline uint32_t chunk_rows_of(uint32_t gpr, uint32_t cg) {
+    return (cg % gpr == 0) ? cg / gpr : (cg - 1) / gpr + 2;
 }
 
 template <int TYPE> struct Fmt;
@@ -65,7 +75,7 @@ struct Chunk {
     const uint8_t *src;   // first byte of the operation's F16 rows
     uint8_t *dst;         // first byte of the operation's output rows
     uint32_t g0;          // first group of this chunk within the operation
-    uint32_t ng;          // groups in this chunk (<= kChunkGroups)
+    uint32_t ng;          // groups in this chunk (<= the source's chunk_groups)
     uint32_t gpr;         // groups per row
     uint32_t src_stride;  // bytes between F16 rows
     int32_t pos0;         // position of the operation's row 0 (RoPE)
@@ -85,6 +95,7 @@ struct QuantOpDev {
 struct OpListSource {
     const QuantOpDev *ops;
     uint32_t n_ops;
+    uint32_t chunk_groups;  // chunk_groups_of(type, false)
     __device__ bool chunk(uint32_t c, Chunk &out) const {
         uint32_t lo = 0, hi = n_ops;  // last op with chunk0 <= c
         while (hi - lo > 1) {
@@ -98,11 +109,11 @@ struct OpListSource {
         const QuantOpDev op = ops[lo];
         out.src = op.src;
         out.dst = op.dst;
-        out.g0 = (c - op.chunk0) * kChunkGroups;
+        out.g0 = (c - op.chunk0) * chunk_groups;
         if (out.g0 >= op.n_groups) {
             return false;
         }
-        out.ng = min(static_cast<uint32_t>(kChunkGroups), op.n_groups - out.g0);
+        out.ng = min(chunk_groups, op.n_groups - out.g0);
         out.gpr = op.gpr;
         out.src_stride = op.src_stride;
         out.pos0 = 0;
@@ -132,7 +143,8 @@ struct BlockSource {
     uint32_t block_tokens;
     uint32_t gpr;
     uint32_t row_bytes;               // output bytes per row
-    uint32_t chunks_per_op;           // ceil(block_tokens*gpr / kChunkGroups)
+    uint32_t chunk_groups;            // chunk_groups_of(type, transform on)
+    uint32_t chunks_per_op;           // ceil(block_tokens*gpr / chunk_groups)
     uint32_t head_dim;                // transform: head width (power of two)
     uint32_t n_rot;                   // RoPE rotary dims (0 = none)
     uint32_t hadamard;                // Hadamard width (0 = none)
@@ -147,11 +159,11 @@ struct BlockSource {
         const uint32_t ntok = items[4 * item + 2];
         out.pos0 = static_cast<int32_t>(items[4 * item + 3]);
         const uint32_t total = ntok * gpr;
-        out.g0 = sub * kChunkGroups;
+        out.g0 = sub * chunk_groups;
         if (out.g0 >= total) {
             return false;
         }
-        out.ng = min(static_cast<uint32_t>(kChunkGroups), total - out.g0);
+        out.ng = min(chunk_groups, total - out.g0);
         out.src = base + block * block_stride + layer * layer_stride;
         out.dst = const_cast<uint8_t *>(layer_dst[layer]) +
                   static_cast<uint64_t>(slot) * block_tokens * row_bytes;
@@ -651,8 +663,10 @@ __device__ inline void quant_quarter_f<KVMEM_TYPE_F16>(const float x[8], uint32_
 // `tab` (built by the whole workgroup), then per round widen, RoPE,
 // rotate and quantize into the wave's LDS region.
 template <int TYPE, class Source>
-__device__ inline void transform_rounds(const Source &s, const Chunk &c, const uint4 v[kRounds],
-                                        uint8_t *wl, float2 *tab, uint32_t wg0, uint32_t lane) {
+__device__ inline void transform_rounds(const Source &s, const Chunk &c,
+                                        const uint4 v[rounds_of(TYPE, true)], uint8_t *wl,
+                                        float2 *tab, uint32_t wg0, uint32_t lane) {
+    constexpr int kRounds = rounds_of(TYPE, true);
     constexpr int GB = Fmt<TYPE>::GB;
     const uint32_t quad = lane >> 2;
     const uint32_t q = lane & 3u;
@@ -720,11 +734,15 @@ __device__ inline void transform_rounds(const Source &s, const Chunk &c, const u
 
 // Quantize chunk `c` of `source` into its destination.  `lds` holds
 // 4 * kWaveGroups groups of the type's layout; with XF the rows go through
-// the source's transform and `tab` holds kTabMax cos/sin pairs.
+// the source's transform and `tab` holds kTabMax cos/sin pairs.  The
+// source's chunk_groups is chunk_groups_of(TYPE, XF).
 template <int TYPE, class Source, bool XF>
 __device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8_t *lds,
                                    float2 *tab) {
     constexpr int GB = Fmt<TYPE>::GB;
+    constexpr int kRounds = rounds_of(TYPE, XF);
+    constexpr int kWaveGroups = 16 * kRounds;
+    constexpr int kChunkGroups = 4 * kWaveGroups;
     Chunk c;
     if (!source.chunk(c_index, c)) {
         return;  // uniform across the workgroup
@@ -803,8 +821,8 @@ extern __shared__ float4 rope_tab4[];
 
 // Chunk of workgroup `b` out of `n`.  Workgroups go to the 8 XCDs round-robin
 // by id; in each group of 8 * kXcdTile chunks, XCD x takes kXcdTile
-// consecutive chunks (whole operations: 8 chunks are one (block, layer) run
-// at 128 tokens x 1024 elements), so the pages of an operation are
+// consecutive chunks (whole operations: a (block, layer) run of 128 tokens
+// x 1024 elements is 4 to 16 chunks), so the pages of an operation are
 // translated by one XCD only, while the chunks in flight on the chip stay
 // one contiguous window.  The tail of fewer than 8 * kXcdTile chunks keeps
 // the identity order.  A bijection on [0, n).
@@ -818,9 +836,15 @@ __device__ inline uint32_t xcd_chunk(uint32_t b, uint32_t n) {
     return (b - r) + (r & 7u) * kXcdTile + (r >> 3);
 }
 
+// LDS staging bytes of a workgroup: 4 waves x 16 * R groups of the format.
+template <int TYPE, bool XF>
+constexpr int stage_bytes() {
+    return 4 * 16 * rounds_of(TYPE, XF) * Fmt<TYPE>::GB;
+}
+
 template <int TYPE, class Source, bool XF>
 __global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kWaveGroups * Fmt<TYPE>::GB];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[stage_bytes<TYPE, XF>()];
     quant_chunk<TYPE, Source, XF>(source, xcd_chunk(blockIdx.x, gridDim.x), lds, rope_tab);
 }
 
@@ -829,8 +853,9 @@ __global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
 template <int TK, int TV, bool XF>
 __global__ __launch_bounds__(256) void quant_scatter_kv_kernel(BlockSource sk, BlockSource sv,
                                                                uint32_t n_k) {
-    constexpr int GB = Fmt<TK>::GB > Fmt<TV>::GB ? Fmt<TK>::GB : Fmt<TV>::GB;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kWaveGroups * GB];
+    constexpr int SB = stage_bytes<TK, XF>() > stage_bytes<TV, XF>() ? stage_bytes<TK, XF>()
+                                                                     : stage_bytes<TV, XF>();
+    __shared__ __attribute__((aligned(16))) uint8_t lds[SB];
     const uint32_t c = xcd_chunk(blockIdx.x, gridDim.x);
     if (c < n_k) {
         quant_chunk<TK, BlockSource, XF>(sk, c, lds, rope_tab);
@@ -842,7 +867,7 @@ __global__ __launch_bounds__(256) void quant_scatter_kv_kernel(BlockSource sk, B
 // Dynamic LDS bytes of the RoPE table for chunks of `s`.
 template <class Source>
 size_t rope_tab_bytes(const Source &s) {
-    return s.n_rot ? sizeof(float2) * chunk_rows_of(s.gpr) * (s.n_rot / 2) : 0;
+    return s.n_rot ? sizeof(float2) * chunk_rows_of(s.gpr, s.chunk_groups) * (s.n_rot / 2) : 0;
 }
 
 template <class Source, bool XF>
@@ -967,9 +992,9 @@ struct XfParams {
     float hscale_v = 1.0f;
 };
 
-// Rows of n_embd elements that one chunk of kChunkGroups groups can touch.
-static uint32_t chunk_rows(uint32_t n_embd) {
-    return chunk_rows_of(n_embd / 32);
+// Rows of n_embd elements that one transformed chunk can touch.
+static uint32_t chunk_rows(uint32_t n_embd, int type) {
+    return chunk_rows_of(n_embd / 32, chunk_groups_of(type, true));
 }
 
 static bool pow2_in(uint32_t x, uint32_t lo, uint32_t hi) {
@@ -992,7 +1017,7 @@ static int resolve_xf(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, uint32_t e
         return fail(ctx, KVMEM_HIP_ERR_INVALID,
                     "transform: n_rot must be a multiple of 16 up to head_dim, with theta");
     }
-    if (xf->n_rot && chunk_rows(ek) * (xf->n_rot / 2) > static_cast<uint32_t>(kTabMax)) {
+    if (xf->n_rot && chunk_rows(ek, pool->type_k) * (xf->n_rot / 2) > static_cast<uint32_t>(kTabMax)) {
         return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "transform: rows too narrow for the RoPE table");
     }
     for (uint32_t w : {xf->hadamard_k, want_v ? xf->hadamard_v : 0u}) {
@@ -1075,7 +1100,8 @@ static BlockSource make_block_source(int type, const uint8_t *base, uint64_t blo
     s.block_tokens = block_tokens;
     s.gpr = n_embd / 32;
     s.row_bytes = s.gpr * group_bytes(type);
-    s.chunks_per_op = (block_tokens * s.gpr + kChunkGroups - 1) / kChunkGroups;
+    s.chunk_groups = chunk_groups_of(type, xp.on);
+    s.chunks_per_op = (block_tokens * s.gpr + s.chunk_groups - 1) / s.chunk_groups;
     s.head_dim = xp.head_dim;
     s.n_rot = is_k ? xp.n_rot : 0u;
     s.hadamard = is_k ? xp.had_k : xp.had_v;
@@ -1138,6 +1164,7 @@ int kvmem_hip_stagein_quant(kvmem_hip_ctx *ctx, const kvmem_hip_quant_op *ops, i
     for (int type : types) {
         std::vector<QuantOpDev> dev;
         uint64_t chunks = 0;
+        const uint32_t cg = chunk_groups_of(type, false);
         for (int i = 0; i < n_ops; ++i) {
             const kvmem_hip_quant_op &op = ops[i];
             if (op.type != type || op.n_rows == 0) {
@@ -1150,7 +1177,7 @@ int kvmem_hip_stagein_quant(kvmem_hip_ctx *ctx, const kvmem_hip_quant_op *ops, i
             d.n_groups = op.n_rows * d.gpr;
             d.src_stride = op.src_stride ? op.src_stride : op.n_embd * 2u;
             d.chunk0 = static_cast<uint32_t>(chunks);
-            chunks += (d.n_groups + kChunkGroups - 1) / kChunkGroups;
+            chunks += (d.n_groups + cg - 1) / cg;
             dev.push_back(d);
         }
         if (dev.empty()) {
@@ -1163,7 +1190,7 @@ int kvmem_hip_stagein_quant(kvmem_hip_ctx *ctx, const kvmem_hip_quant_op *ops, i
         if (!ops_dev) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
-        OpListSource s{static_cast<const QuantOpDev *>(ops_dev), static_cast<uint32_t>(dev.size())};
+        OpListSource s{static_cast<const QuantOpDev *>(ops_dev), static_cast<uint32_t>(dev.size()), cg};
         if (!launch_quant(ctx, type, static_cast<uint32_t>(chunks), s)) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
