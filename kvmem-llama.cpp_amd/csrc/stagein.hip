@@ -275,22 +275,32 @@ __device__ inline void quant_quarter<KVMEM_TYPE_Q8_0>(const uint4 &v, uint32_t q
 }
 
 // vmax of ggml's q4_0/q5_0: the FIRST element of largest magnitude (strict
-// `amax < |v|` scan).  Reduced as a max over 21-bit keys
-// (|h| << 6) | ((31 - e) << 1) | sign(h): larger magnitude wins, then lower
-// element index.  An all-zero group keeps ggml's initial vmax = +0.
-__device__ inline float quad_vmax(const uint32_t h[8], uint32_t q) {
+// `amax < |v|` scan).  Reduced as a max over keys
+//   |h| << 17 | (31 - e) << 1 | sign(h)
+// (larger magnitude wins, then lower element index e).  One funnel shift per
+// element rotates an f16 of the lane's packed words into place (its sign to
+// bit 0, its magnitude to bits 17..31) and one and-or drops the other half
+// and inserts the element's index within the lane; the lane's part of the
+// index is added after the lane's own max.  An all-zero group keeps
+// ggml's initial vmax = +0.
+__device__ inline float quad_vmax(const uint4 &v, uint32_t q) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     uint32_t key = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t e = 8 * q + i;
-        const uint32_t k = ((h[i] & 0x7fffu) << 6) | ((31u - e) << 1) | (h[i] >> 15);
-        key = k > key ? k : key;
+    for (int j = 0; j < 4; ++j) {
+        // element 2j sits in the low half, 2j + 1 in the high half
+        const uint32_t k0 = (__builtin_amdgcn_alignbit(w[j], w[j], 15) & 0xFFFE0001u) |
+                            static_cast<uint32_t>((7 - 2 * j) << 1);
+        const uint32_t k1 = (__builtin_amdgcn_alignbit(w[j], w[j], 31) & 0xFFFE0001u) |
+                            static_cast<uint32_t>((6 - 2 * j) << 1);
+        key = max(key, max(k0, k1));
     }
+    key |= (3u - q) << 4;
     uint32_t o = quad_xor1(key);
     key = o > key ? o : key;
     o = quad_xor2(key);
     key = o > key ? o : key;
-    const uint32_t mag = key >> 6;
+    const uint32_t mag = key >> 17;
     if (mag == 0) {
         return 0.0f;
     }
@@ -324,7 +334,7 @@ __device__ inline void quant_quarter<KVMEM_TYPE_Q4_0>(const uint4 &v, uint32_t q
                                                        bool valid) {
     uint32_t h[8];
     unpack8(v, h);
-    const float vmax = quad_vmax(h, q);
+    const float vmax = quad_vmax(v, q);
     const float d = vmax * -0.125f;        // == vmax / -8 (exact scaling)
     const float id = d != 0.0f ? scale_recip(d) : 0.0f;
     uint32_t w0, w1;
@@ -354,7 +364,7 @@ __device__ inline void quant_quarter<KVMEM_TYPE_Q5_0>(const uint4 &v, uint32_t q
                                                        bool valid) {
     uint32_t h[8];
     unpack8(v, h);
-    const float vmax = quad_vmax(h, q);
+    const float vmax = quad_vmax(v, q);
     const float d = vmax * -0.0625f;       // == vmax / -16 (exact scaling)
     const float id = d != 0.0f ? scale_recip(d) : 0.0f;
     uint32_t w0, w1;
