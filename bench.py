@@ -391,6 +391,66 @@ def run_cache_transform(a, torch, kv, workloads) -> dict:
             "parts_ms": {"score_kernel": round(m["score_ms"], 4), "stagein_kernel": round(m["set_ms"], 4)}}
 
 
+def sample_power_clocks() -> dict | None:
+    """One `amd-smi metric -c -p` reading: socket power (W) and the GFX
+    clocks (MHz) of the XCDs; None where the tool is missing or fails."""
+    import re
+    import subprocess
+    try:
+        out = subprocess.run(["amd-smi", "metric", "-c", "-p"], capture_output=True, text=True,
+                             timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    power = re.search(r"SOCKET_POWER:\s*([0-9.]+)\s*W", out)
+    clocks = [int(m) for m in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*([0-9]+)\s*MHz", out)]
+    if not power and not clocks:
+        return None
+    return {"socket_power_W": float(power.group(1)) if power else None, "gfx_clk_MHz": clocks}
+
+
+def run_scorer_sustained(a, torch, kv, workloads) -> dict:
+    """The 256K scorer (16 layers x 2048 blocks, 64-token query) back to
+    back for `--seconds`, with socket power and GFX clocks sampled in the
+    middle: the power-capped regime the kernel runs in when it is the whole
+    load, and the dense fp16 MFMA ceiling at the sampled clock."""
+    import threading
+    log("generating history K [16][2048][128][4][256] f16 and query")
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=TQ, seed=2)
+    torch.cuda.synchronize()
+    scores = torch.empty(B, dtype=torch.float32, device="cuda")
+    ctx = kv.Context(0)
+    hist = ctx.make_history(k.data_ptr(), None, L, B, T, E, 0)
+    for _ in range(3):
+        ctx.score(hist, q.data_ptr(), kv.TYPE_BF16, TQ, HQ, HKV, D, scores.data_ptr())
+    ctx.sync()
+    sample: dict = {}
+    timer = threading.Timer(a.seconds / 2, lambda: sample.update(s=sample_power_clocks()))
+    timer.start()
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < a.seconds:
+        for _ in range(20):
+            ctx.score(hist, q.data_ptr(), kv.TYPE_BF16, TQ, HQ, HKV, D, scores.data_ptr())
+        ctx.sync()
+        n += 20
+    dt = time.perf_counter() - t0
+    timer.join()
+    ctx.close()
+    ms = 1e3 * dt / n
+    flops = 2.0 * TQ * HQ * D * B * T * L
+    pc = sample.get("s")
+    out = {"metric": "scorer back to back @256K", "unit": "ms/call", "value": round(ms, 4),
+           "higher_is_better": False, "n_gpus": 1, "calls": n,
+           "data": "synthetic (seeded N(0,1) keys with per-block offsets, bf16 query)",
+           "achieved_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1), "power_clocks": pc}
+    if pc and pc["gfx_clk_MHz"]:
+        mhz = sum(pc["gfx_clk_MHz"]) / len(pc["gfx_clk_MHz"])
+        # 1024 SIMDs x 1024 dense fp16 FLOP per clock (2.5 PFLOP/s at 2.4 GHz)
+        peak = 1024 * 1024 * mhz * 1e6 / 1e12
+        out["mfma_peak_at_clock_TFLOPs"] = round(peak, 1)
+        out["frac_at_clock"] = round(flops / (ms * 1e-3) / 1e12 / peak, 4)
+    return out
+
+
 def run_meank_256k(a, torch, kv, workloads) -> dict:
     """The 256K step with the reference's mean-K cosine scorer: per-block
     key sums are produced once (untimed warmup) and kept; a step sums the
@@ -519,7 +579,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="reselect_256k",
                     choices=["reselect_256k", "mixed_precision", "recall_1m", "copy_calibration",
-                             "cache_transform", "meank_256k"])
+                             "cache_transform", "meank_256k", "scorer_sustained"])
+    ap.add_argument("--seconds", type=float, default=8.0, help="scorer_sustained: loop length")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-pinned", action="store_true")
     a = ap.parse_args()
@@ -533,7 +594,8 @@ def main() -> int:
     from kvmem_amd import workloads
     run = {"reselect_256k": run_reselect_256k, "mixed_precision": run_mixed_precision,
            "recall_1m": run_recall_1m, "copy_calibration": run_copy_calibration,
-           "cache_transform": run_cache_transform, "meank_256k": run_meank_256k}[a.workload]
+           "cache_transform": run_cache_transform, "meank_256k": run_meank_256k,
+           "scorer_sustained": run_scorer_sustained}[a.workload]
     result = run(a, torch, kv, workloads)
     print(json.dumps(result), flush=True)
     return 0
