@@ -97,7 +97,7 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
         step()
         restore()
     ctx.perf_enable(True)
-    times, staged, score_ms, set_ms, sel_ms = [], [], 0.0, 0.0, 0.0
+    times, staged, moved, score_ms, set_ms, sel_ms, layout_ms = [], [], [], 0.0, 0.0, 0.0, 0.0
     for _ in range(steps):
         ctx.perf_reset()
         torch.cuda.synchronize()
@@ -109,12 +109,15 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
         score_ms += pf["score_ms"]
         set_ms += pf["set_ms"]
         sel_ms += pf["topk_ms"]
+        layout_ms += pf["layout_ms"]
         staged.append(st["n_staged"])
+        moved.append(st["n_moved"])
         restore()
     ctx.perf_enable(False)
     assert all(x == staged[0] for x in staged), staged
     return {"ms_step": 1e3 * sum(times) / steps, "score_ms": score_ms / steps,
-            "set_ms": set_ms / steps, "sel_ms": sel_ms / steps, "n_staged": staged[0]}
+            "set_ms": set_ms / steps, "sel_ms": sel_ms / steps, "n_staged": staged[0],
+            "layout_ms": layout_ms / steps, "n_moved": max(moved)}
 
 
 def stage_bytes(kv, n_blocks: int, type_k: int, type_v: int) -> int:
@@ -335,7 +338,30 @@ def run_reselect_256k(a, torch, kv, workloads) -> dict:
         log("cpu baseline (oracle restatement on host cores)")
         result["cpu_baseline"] = cpu_baseline(torch, k, v, q, sorted(set(sel) - set(prev)))
     eng.close()
+    result["canonical_layout"] = canonical_layout_mode(a, torch, kv, k, v, q, prev)
     return result
+
+
+def canonical_layout_mode(a, torch, kv, k, v, q, prev: list) -> dict:
+    """The same step with canonical slot order (window slot i holds the
+    i-th selected block, as layout_gpu_slots_by_orig_pos): the resident
+    blocks that change slot are moved on the device (gather to scratch, then
+    scatter) before the stage-in.  Reported beside the default step."""
+    log("canonical layout: the same step with slot i = i-th selected block")
+    eng = make_engine(kv, torch, k, v, canonical_layout=1)
+    ctx = kv.Context.borrow(eng.ctx_handle())
+    m = timed_steps(eng, ctx, torch, q, TQ, prev, a.steps, a.warmup)
+    eng.close()
+    row = kv.row_size(kv.TYPE_Q8_0, E)
+    moved_bytes = m["n_moved"] * L * 2 * T * row  # one copy of the moved blocks' K and V rows
+    out = {"ms_per_step": round(m["ms_step"], 4), "n_moved": m["n_moved"], "n_staged": m["n_staged"],
+           "layout_ms": round(m["layout_ms"], 4), "stagein_kernel_ms": round(m["set_ms"], 4),
+           "moved_bytes": moved_bytes,
+           "algorithmic_bytes": 2 * moved_bytes,  # read + write once
+           "device_bytes": 4 * moved_bytes}      # gather (read + write) and scatter (read + write)
+    if m["layout_ms"] > 0:
+        out["GBs_device"] = round(4 * moved_bytes / (m["layout_ms"] * 1e-3) / 1e9, 1)
+    return out
 
 
 def run_mixed_precision(a, torch, kv, workloads) -> dict:
