@@ -611,8 +611,8 @@ def main() -> int:
     ap.add_argument("--no-pinned", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: the reselect path runs on a single MI355X "
-              "(multi-GPU sharding is described in DESIGN.md, not run)", file=sys.stderr)
+        print("bench.py measures one GPU only: the reselect path runs on a single MI355X; "
+              "sharding it across GPUs is a design, not a run", file=sys.stderr)
         return 2
 
     import torch

@@ -1,5 +1,5 @@
 """Seeded synthetic workloads of the reselect path (shapes of the reselect
-benchmark configurations).  No checker logic lives here.
+benchmark configurations).  No parity logic lives here.
 
 Shapes (L layers, B history blocks, T = 128 tokens per block, Hkv = 4 KV
 heads, Hq = 24 query heads, D = 256):

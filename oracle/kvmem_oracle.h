@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product library links, loads or
  * calls this code: only tests/, __graft_entry__.smoke() and the cpu_baseline
- * leg of bench.py use it, and only as the checker.
+ * leg of bench.py use it, and only to check or time the product against.
  *
  * Every function cites the reference file:line whose behaviour it restates
  * (paths relative to the CrKcel/kvmem-llama.cpp tree).  The ggml quantizers
@@ -116,7 +116,8 @@ void ko_score_pertoken_max(const float *q, const uint16_t *k,
                            double *layer_scores);
 
 /* Same computation with fp32 accumulation, written for speed: the CPU
- * baseline of the scoring step (not a checker).  n_threads <= 0 = all. */
+ * baseline of the scoring step (parity rests on the fp64 version above).
+ * n_threads <= 0 = all. */
 void ko_score_pertoken_max_f32(const float *q, const uint16_t *k,
                                uint32_t L, uint32_t Tq, uint32_t Hq, uint32_t Hkv,
                                uint32_t D, uint32_t B, uint32_t T,

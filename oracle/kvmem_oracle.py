@@ -1,5 +1,5 @@
 """ctypes view of oracle/liboracle.so -- the CPU restatement of the reselect
-path used as the checker.
+path that the tests compare the product against.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
 cpu_baseline leg of bench.py, never by the product package.

@@ -1,8 +1,8 @@
 /*
  * kvmem_oracle_baseline.c -- fp32 CPU implementation of the per-token max
  * scorer, written to vectorise (K transposed per head so the inner loop runs
- * over keys).  It is the CPU baseline timed beside the GPU scorer, not a
- * checker: ko_score_pertoken_max (fp64) is the checker.
+ * over keys).  It is the CPU baseline timed beside the GPU scorer; the
+ * parity tests compare against ko_score_pertoken_max (fp64) instead.
  *
  * TEST INFRASTRUCTURE ONLY (see kvmem_oracle.h).
  */

@@ -1,6 +1,6 @@
 /*
  * kvmem_oracle_meank.c -- the reference's retrieval scorer (mean-K cosine)
- * and its mean-K producer, restated for the checker.
+ * and its mean-K producer, restated as the tests' reference.
  *
  * TEST INFRASTRUCTURE ONLY (see kvmem_oracle.h).  Compiled with
  * -ffp-contract=off: every product and sum below is one IEEE operation in

@@ -1,6 +1,7 @@
 /*
  * kvmem_oracle_quant.c -- half-precision conversion and the ggml q8_0 / q4_0 /
- * q5_0 reference quantizers, restated for the KVMem stage-in checker.
+ * q5_0 reference quantizers, restated as the tests' reference for the KVMem
+ * stage-in.
  *
  * TEST INFRASTRUCTURE ONLY (see kvmem_oracle.h).  Compiled with
  * -ffp-contract=off: ggml's reference quantizers are specified by their C

@@ -1,6 +1,7 @@
 /*
  * kvmem_oracle_select.c -- per-token max block scorer (fp64 truth), layer
- * combination and the KvMemStore top-k selection, restated for the checker.
+ * combination and the KvMemStore top-k selection, restated as the tests'
+ * reference.
  *
  * TEST INFRASTRUCTURE ONLY (see kvmem_oracle.h).
  */

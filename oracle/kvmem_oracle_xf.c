@@ -1,7 +1,7 @@
 /*
  * kvmem_oracle_xf.c -- the cache row transform of the raw-K stage-in
  * (NeoX RoPE at the block's positions, then the attn_rot Walsh-Hadamard
- * rotation), restated for the checker.
+ * rotation), restated as the tests' reference.
  *
  * TEST INFRASTRUCTURE ONLY (see kvmem_oracle.h).  Compiled with
  * -ffp-contract=off: every product and sum is one IEEE operation, and the

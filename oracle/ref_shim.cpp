@@ -1,6 +1,7 @@
 // C entry points over the reference's own host kvmem library (KvMemStore /
 // KvMemRuntime / RawKvStore compiled from kvmem/src/host/*.cpp where the
-// reference tree lies), so that ctypes can drive it as a second checker.
+// reference tree lies), so that the tests can drive it through ctypes as a
+// second reference.
 //
 // TEST INFRASTRUCTURE ONLY: built into oracle/_ref/ by `make ref`; used by
 // tests/golden/make_golden.py to write fixtures and by CPU tests when the
