@@ -58,6 +58,8 @@ __host__ __device__ constexpr uint32_t chunk_groups_of(int type, bool xf) {
     return 64u * static_cast<uint32_t>(rounds_of(type, xf));
 }
 constexpr int kTabMax = 4096;  // (row, rotary pair) entries per chunk
+// Layers of one block a workgroup takes when K is RoPE'd (one table build).
+constexpr uint32_t kRopeLayerGroup = 4;
 
 // Rows of `gpr` groups that one chunk of `cg` groups can touch.
 inline uint32_t chunk_rows_of(uint32_t gpr, uint32_t cg) {
@@ -149,11 +151,15 @@ struct BlockSource {
     uint32_t n_rot;                   // RoPE rotary dims (0 = none)
     uint32_t hadamard;                // Hadamard width (0 = none)
     float hscale;                     // 1 / sqrtf(hadamard)
+    uint32_t layer_group;             // layers per workgroup chunk index (RoPE'd K: 4; else 1)
     __device__ bool chunk(uint32_t c, Chunk &out) const {
         const uint32_t op = c / chunks_per_op;
         const uint32_t sub = c - op * chunks_per_op;
         const uint32_t item = op / n_layers;
-        const uint32_t layer = op - item * n_layers;
+        return chunk_at(item, op - item * n_layers, sub, out);
+    }
+    // Chunk `sub` of the run of (item, layer).
+    __device__ bool chunk_at(uint32_t item, uint32_t layer, uint32_t sub, Chunk &out) const {
         const uint32_t block = items[4 * item + 0];
         const uint32_t slot = items[4 * item + 1];
         const uint32_t ntok = items[4 * item + 2];
@@ -675,7 +681,7 @@ __device__ inline void quant_quarter_f<KVMEM_TYPE_F16>(const float x[8], uint32_
 template <int TYPE, class Source>
 __device__ inline void transform_rounds(const Source &s, const Chunk &c,
                                         const uint4 v[rounds_of(TYPE, true)], uint8_t *wl,
-                                        float2 *tab, uint32_t wg0, uint32_t lane) {
+                                        float2 *tab, uint32_t wg0, uint32_t lane, bool build_tab) {
     constexpr int kRounds = rounds_of(TYPE, true);
     constexpr int GB = Fmt<TYPE>::GB;
     const uint32_t quad = lane >> 2;
@@ -687,7 +693,7 @@ __device__ inline void transform_rounds(const Source &s, const Chunk &c,
     // as four 16-byte chunks pl*u + m, u < 4, so in each read the lanes of
     // a half-head take consecutive chunks (no bank conflicts).
     const uint32_t pl = half / 8u;
-    if (half != 0u) {
+    if (half != 0u && build_tab) {
         const uint32_t rows = (c.g0 + c.ng - 1u) / c.gpr - row0 + 1u;
         for (uint32_t i = threadIdx.x; i < rows * half; i += blockDim.x) {
             const uint32_t r = i / half;
@@ -747,16 +753,12 @@ __device__ inline void transform_rounds(const Source &s, const Chunk &c,
 // the source's transform and `tab` holds kTabMax cos/sin pairs.  The
 // source's chunk_groups is chunk_groups_of(TYPE, XF).
 template <int TYPE, class Source, bool XF>
-__device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8_t *lds,
-                                   float2 *tab) {
+__device__ inline void quant_chunk_body(const Source &source, const Chunk &c, uint8_t *lds,
+                                        float2 *tab, bool build_tab) {
     constexpr int GB = Fmt<TYPE>::GB;
     constexpr int kRounds = rounds_of(TYPE, XF);
     constexpr int kWaveGroups = 16 * kRounds;
     constexpr int kChunkGroups = 4 * kWaveGroups;
-    Chunk c;
-    if (!source.chunk(c_index, c)) {
-        return;  // uniform across the workgroup
-    }
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6;
     const uint32_t lane = tid & 63u;
@@ -791,7 +793,7 @@ __device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8
         }
     }
     if constexpr (XF) {
-        transform_rounds<TYPE>(source, c, v, wl, tab, wg0, lane);
+        transform_rounds<TYPE>(source, c, v, wl, tab, wg0, lane, build_tab);
     } else if (full_chunk) {
 #pragma unroll
         for (int r = 0; r < kRounds; ++r) {
@@ -820,6 +822,38 @@ __device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8
     }
     for (uint32_t off = full + lane * 2u; off < nb; off += 128u) {
         *reinterpret_cast<uint16_t *>(dst + off) = *reinterpret_cast<const uint16_t *>(wl + off);
+    }
+}
+
+template <int TYPE, class Source, bool XF>
+__device__ inline void quant_chunk(const Source &source, uint32_t c_index, uint8_t *lds,
+                                   float2 *tab) {
+    Chunk c;
+    if (!source.chunk(c_index, c)) {
+        return;  // uniform across the workgroup
+    }
+    quant_chunk_body<TYPE, Source, XF>(source, c, lds, tab, true);
+}
+
+// Workgroup chunk index `c` of a RoPE'd block source with layer grouping:
+// the same rows of layer_group consecutive layers of one block.  Their
+// positions, hence their cos/sin table, are the same, so the table is built
+// once for all of them.  (A separate kernel instantiation: the layer loop
+// costs registers that the other transformed sources do not pay.)
+template <int TYPE>
+__device__ inline void block_chunks(const BlockSource &s, uint32_t c, uint8_t *lds, float2 *tab) {
+    const uint32_t groups = (s.n_layers + s.layer_group - 1u) / s.layer_group;
+    const uint32_t og = c / s.chunks_per_op;
+    const uint32_t sub = c - og * s.chunks_per_op;
+    const uint32_t item = og / groups;
+    const uint32_t l0 = (og - item * groups) * s.layer_group;
+    const uint32_t l1 = min(s.n_layers, l0 + s.layer_group);
+    for (uint32_t l = l0; l < l1; ++l) {
+        Chunk ch;
+        if (!s.chunk_at(item, l, sub, ch)) {
+            return;  // uniform: no rows in this chunk for any layer
+        }
+        quant_chunk_body<TYPE, BlockSource, true>(s, ch, lds, tab, l == l0);
     }
 }
 
@@ -852,15 +886,20 @@ constexpr int stage_bytes() {
     return 4 * 16 * rounds_of(TYPE, XF) * Fmt<TYPE>::GB;
 }
 
-template <int TYPE, class Source, bool XF>
+template <int TYPE, class Source, bool XF, bool GROUP>
 __global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[stage_bytes<TYPE, XF>()];
-    quant_chunk<TYPE, Source, XF>(source, xcd_chunk(blockIdx.x, gridDim.x), lds, rope_tab);
+    const uint32_t c = xcd_chunk(blockIdx.x, gridDim.x);
+    if constexpr (GROUP) {
+        block_chunks<TYPE>(source, c, lds, rope_tab);
+    } else {
+        quant_chunk<TYPE, Source, XF>(source, c, lds, rope_tab);
+    }
 }
 
 // K and V of a block job in one launch: chunks [0, n_k) are K, the rest V
 // (the branch is uniform per workgroup).
-template <int TK, int TV, bool XF>
+template <int TK, int TV, bool XF, bool GROUP>
 __global__ __launch_bounds__(256) void quant_scatter_kv_kernel(BlockSource sk, BlockSource sv,
                                                                uint32_t n_k) {
     constexpr int SB = stage_bytes<TK, XF>() > stage_bytes<TV, XF>() ? stage_bytes<TK, XF>()
@@ -868,7 +907,11 @@ __global__ __launch_bounds__(256) void quant_scatter_kv_kernel(BlockSource sk, B
     __shared__ __attribute__((aligned(16))) uint8_t lds[SB];
     const uint32_t c = xcd_chunk(blockIdx.x, gridDim.x);
     if (c < n_k) {
-        quant_chunk<TK, BlockSource, XF>(sk, c, lds, rope_tab);
+        if constexpr (GROUP) {
+            block_chunks<TK>(sk, c, lds, rope_tab);
+        } else {
+            quant_chunk<TK, BlockSource, XF>(sk, c, lds, rope_tab);
+        }
     } else {
         quant_chunk<TV, BlockSource, XF>(sv, c - n_k, lds, rope_tab);
     }
@@ -880,7 +923,7 @@ size_t rope_tab_bytes(const Source &s) {
     return s.n_rot ? sizeof(float2) * chunk_rows_of(s.gpr, s.chunk_groups) * (s.n_rot / 2) : 0;
 }
 
-template <class Source, bool XF>
+template <class Source, bool XF, bool GROUP>
 bool launch_quant_x(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Source &s) {
     size_t tb = 0;
     if constexpr (XF) {
@@ -888,16 +931,16 @@ bool launch_quant_x(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Sourc
     }
     switch (type) {
         case KVMEM_TYPE_Q8_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q8_0, Source, XF><<<n_chunks, 256, tb, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_Q8_0, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s);
             break;
         case KVMEM_TYPE_Q4_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q4_0, Source, XF><<<n_chunks, 256, tb, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_Q4_0, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s);
             break;
         case KVMEM_TYPE_Q5_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q5_0, Source, XF><<<n_chunks, 256, tb, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_Q5_0, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s);
             break;
         case KVMEM_TYPE_F16:
-            quant_scatter_kernel<KVMEM_TYPE_F16, Source, XF><<<n_chunks, 256, tb, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_F16, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s);
             break;
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported type");
@@ -907,33 +950,36 @@ bool launch_quant_x(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Sourc
 }
 
 bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const OpListSource &s) {
-    return n_chunks == 0 || launch_quant_x<OpListSource, false>(ctx, type, n_chunks, s);
+    return n_chunks == 0 || launch_quant_x<OpListSource, false, false>(ctx, type, n_chunks, s);
 }
 
 bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const BlockSource &s, bool xf) {
     if (n_chunks == 0) {
         return true;
     }
-    return xf ? launch_quant_x<BlockSource, true>(ctx, type, n_chunks, s)
-              : launch_quant_x<BlockSource, false>(ctx, type, n_chunks, s);
+    if (!xf) {
+        return launch_quant_x<BlockSource, false, false>(ctx, type, n_chunks, s);
+    }
+    return s.layer_group > 1u ? launch_quant_x<BlockSource, true, true>(ctx, type, n_chunks, s)
+                              : launch_quant_x<BlockSource, true, false>(ctx, type, n_chunks, s);
 }
 
-template <int TK, bool XF>
+template <int TK, bool XF, bool GROUP>
 bool launch_kv_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, const BlockSource &sk,
                  const BlockSource &sv, uint32_t n_k) {
     const size_t tb = XF ? rope_tab_bytes(sk) : 0;  // only K is RoPE'd
     switch (tv) {
         case KVMEM_TYPE_Q8_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q8_0, XF><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q8_0, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
             break;
         case KVMEM_TYPE_Q4_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q4_0, XF><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q4_0, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
             break;
         case KVMEM_TYPE_Q5_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q5_0, XF><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q5_0, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
             break;
         case KVMEM_TYPE_F16:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_F16, XF><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_F16, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
             break;
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported V type");
@@ -942,28 +988,32 @@ bool launch_kv_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, const BlockSource &s
     return hip_ok(ctx, hipGetLastError(), "stage-in K/V kernel launch");
 }
 
-template <bool XF>
+template <bool XF, bool GROUP>
 bool launch_quant_kv_x(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_t n_v,
                        const BlockSource &sk, const BlockSource &sv) {
     const uint32_t grid = n_k + n_v;
     switch (tk) {
-        case KVMEM_TYPE_Q8_0: return launch_kv_v<KVMEM_TYPE_Q8_0, XF>(ctx, tv, grid, sk, sv, n_k);
-        case KVMEM_TYPE_Q4_0: return launch_kv_v<KVMEM_TYPE_Q4_0, XF>(ctx, tv, grid, sk, sv, n_k);
-        case KVMEM_TYPE_Q5_0: return launch_kv_v<KVMEM_TYPE_Q5_0, XF>(ctx, tv, grid, sk, sv, n_k);
-        case KVMEM_TYPE_F16: return launch_kv_v<KVMEM_TYPE_F16, XF>(ctx, tv, grid, sk, sv, n_k);
+        case KVMEM_TYPE_Q8_0: return launch_kv_v<KVMEM_TYPE_Q8_0, XF, GROUP>(ctx, tv, grid, sk, sv, n_k);
+        case KVMEM_TYPE_Q4_0: return launch_kv_v<KVMEM_TYPE_Q4_0, XF, GROUP>(ctx, tv, grid, sk, sv, n_k);
+        case KVMEM_TYPE_Q5_0: return launch_kv_v<KVMEM_TYPE_Q5_0, XF, GROUP>(ctx, tv, grid, sk, sv, n_k);
+        case KVMEM_TYPE_F16: return launch_kv_v<KVMEM_TYPE_F16, XF, GROUP>(ctx, tv, grid, sk, sv, n_k);
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported K type");
             return false;
     }
 }
 
+// The K source groups layers when it is RoPE'd (layer_group > 1); V never is.
 bool launch_quant_kv(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_t n_v,
                      const BlockSource &sk, const BlockSource &sv, bool xf) {
     if (n_k + n_v == 0) {
         return true;
     }
-    return xf ? launch_quant_kv_x<true>(ctx, tk, tv, n_k, n_v, sk, sv)
-              : launch_quant_kv_x<false>(ctx, tk, tv, n_k, n_v, sk, sv);
+    if (!xf) {
+        return launch_quant_kv_x<false, false>(ctx, tk, tv, n_k, n_v, sk, sv);
+    }
+    return sk.layer_group > 1u ? launch_quant_kv_x<true, true>(ctx, tk, tv, n_k, n_v, sk, sv)
+                               : launch_quant_kv_x<true, false>(ctx, tk, tv, n_k, n_v, sk, sv);
 }
 
 static bool aligned16(const void *p) {
@@ -1116,14 +1166,20 @@ static BlockSource make_block_source(int type, const uint8_t *base, uint64_t blo
     s.n_rot = is_k ? xp.n_rot : 0u;
     s.hadamard = is_k ? xp.had_k : xp.had_v;
     s.hscale = is_k ? xp.hscale_k : xp.hscale_v;
+    s.layer_group = (xp.on && s.n_rot) ? kRopeLayerGroup : 1u;
     return s;
 }
 
 // One launch for K (and V when sv is set): chunks of K first, then of V.
+static uint64_t block_job_chunks(const BlockSource &s, uint32_t n_items) {
+    const uint64_t groups = (s.n_layers + s.layer_group - 1u) / s.layer_group;
+    return static_cast<uint64_t>(n_items) * groups * s.chunks_per_op;
+}
+
 static int launch_block_job(kvmem_hip_ctx *ctx, int type_k, const BlockSource &sk, int type_v,
                             const BlockSource *sv, uint32_t n_items, bool xf) {
-    const uint64_t nk = static_cast<uint64_t>(n_items) * sk.n_layers * sk.chunks_per_op;
-    const uint64_t nv = sv ? static_cast<uint64_t>(n_items) * sv->n_layers * sv->chunks_per_op : 0;
+    const uint64_t nk = block_job_chunks(sk, n_items);
+    const uint64_t nv = sv ? block_job_chunks(*sv, n_items) : 0;
     if (nk + nv > 0x7fffffffu) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "stage-in: too many chunks in one call");
     }
