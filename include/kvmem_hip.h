@@ -441,7 +441,8 @@ KVMEM_HIP_API int kvmem_hip_meank_add(kvmem_hip_ctx *ctx, const void *k, int32_t
  *   q_sum       device [n_layers][n_head*head_dim] f32 (sums of query rows)
  *   q_count     host   [n_layers] rows summed (0 = layer not scored)
  *   k_sum, mean_tokens as produced by kvmem_hip_meank_sums
- *   scores      device [n_blocks] f32 */
+ *   scores      device [n_blocks] f32
+ * At most 256 layers (KVMEM_HIP_ERR_UNSUPPORTED beyond). */
 typedef struct kvmem_hip_meank_args {
     const float *q_sum;
     const uint32_t *q_count;

@@ -79,7 +79,23 @@ __global__ __launch_bounds__(256) void q_accumulate_kernel(const QT *q, const ui
     float *dst = q_sum + static_cast<uint64_t>(l) * E + e;
     float acc = reset ? 0.0f : *dst;
     const QT *src = q + static_cast<uint64_t>(l) * n_tokens * E + e;
-    for (uint32_t i = 0; i < n_list; ++i) {
+    // the rows of a batch are loaded before any is added (one memory latency
+    // per batch); they are added in list order as the sequential loop does
+    constexpr uint32_t kBatch = 16;
+    uint32_t i = 0;
+    for (; i + kBatch <= n_list; i += kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+            const uint32_t t = tokens ? tokens[i + j] : i + j;
+            v[j] = static_cast<float>(src[static_cast<uint64_t>(t) * E]);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+            acc += v[j];
+        }
+    }
+    for (; i < n_list; ++i) {
         const uint32_t t = tokens ? tokens[i] : i;
         acc += static_cast<float>(src[static_cast<uint64_t>(t) * E]);
     }
@@ -165,59 +181,68 @@ __device__ inline float row16_sum(float v) {
 }
 
 // 16 lanes per (layer, block) item, 16 items per 256-thread workgroup.  A
-// lane holds D/16 channels of each head as float4s; the next head's sums are
-// loaded before the current head is reduced.
+// lane holds D/16 channels of each head as float4s.  The key sums of every
+// head (up to kMaxHeads) are loaded before the first head is reduced, so an
+// item waits for memory once; the query vectors (shared by the layer's
+// blocks, cache hits) are loaded per head.
 template <int D>
 __global__ __launch_bounds__(256) void meank_cos_kernel(const float *k_sum, const uint32_t *mean_tokens,
                                                         const float *qv, const float *nq,
                                                         const float *invq, uint32_t L, uint32_t B,
                                                         uint32_t cap, uint32_t Hkv, double *layer_cos) {
     constexpr int P4 = D / 64;  // float4s per lane per head
+    constexpr int kMaxHeads = 4;  // heads whose key sums are in flight together
     const uint32_t item = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
     const uint32_t sub = threadIdx.x & 15u;
     const bool live = item < L * B;
     const uint32_t l = live ? item / B : 0u;
     const uint32_t b = live ? item - l * B : 0u;
-    const bool scored = live && invq[l] != 0.0f;  // layers without query rows are skipped
-    const uint32_t mt = scored ? mean_tokens[static_cast<uint64_t>(l) * cap + b] : 0u;
+    const float iq = invq[l];
+    const uint32_t mt_raw = mean_tokens[static_cast<uint64_t>(l) * cap + b];
+    const bool scored = live && iq != 0.0f;  // layers without query rows are skipped
+    const uint32_t mt = scored ? mt_raw : 0u;
     const float inv = mt ? 1.0f / static_cast<float>(mt) : 0.0f;
     const float4 *ks = reinterpret_cast<const float4 *>(k_sum + (static_cast<uint64_t>(l) * cap + b) * Hkv * D);
     const float4 *qs = reinterpret_cast<const float4 *>(qv + static_cast<uint64_t>(l) * Hkv * D);
     const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float4 kc[P4], qc[P4];
-#pragma unroll
-    for (int j = 0; j < P4; ++j) {
-        kc[j] = mt ? ks[j * 16 + sub] : zero;
-        qc[j] = scored ? qs[j * 16 + sub] : zero;
-    }
     double layer = 0.0;
-    for (uint32_t h = 0; h < Hkv; ++h) {
-        float4 kn[P4], qn[P4];
-        const bool more = h + 1 < Hkv;
+    for (uint32_t h0 = 0; h0 < Hkv; h0 += kMaxHeads) {
+        const uint32_t nh = min(Hkv - h0, static_cast<uint32_t>(kMaxHeads));
+        float4 kc[kMaxHeads][P4];
 #pragma unroll
-        for (int j = 0; j < P4; ++j) {
-            kn[j] = (more && mt) ? ks[(h + 1) * (D / 4) + j * 16 + sub] : zero;
-            qn[j] = (more && scored) ? qs[(h + 1) * (D / 4) + j * 16 + sub] : zero;
-        }
-        float dot = 0.0f, nk = 0.0f;
+        for (int hh = 0; hh < kMaxHeads; ++hh) {
 #pragma unroll
-        for (int j = 0; j < P4; ++j) {
-            const float m[4] = {kc[j].x * inv, kc[j].y * inv, kc[j].z * inv, kc[j].w * inv};
-            const float q[4] = {qc[j].x, qc[j].y, qc[j].z, qc[j].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                dot += q[e] * m[e];
-                nk += m[e] * m[e];
+            for (int j = 0; j < P4; ++j) {
+                // loaded whatever mt is (every row up to capacity is in bounds),
+                // chosen after: the load need not wait for mean_tokens
+                const float4 kv = static_cast<uint32_t>(hh) < nh ? ks[(h0 + hh) * (D / 4) + j * 16 + sub] : zero;
+                kc[hh][j] = mt ? kv : zero;
             }
         }
-        dot = row16_sum(dot);
-        nk = row16_sum(nk);
-        const float c = dot / (sqrtf(scored ? nq[l * Hkv + h] : 0.0f) * sqrtf(nk) + 1e-6f);
-        layer += static_cast<double>(c);
 #pragma unroll
-        for (int j = 0; j < P4; ++j) {
-            kc[j] = kn[j];
-            qc[j] = qn[j];
+        for (int hh = 0; hh < kMaxHeads; ++hh) {
+            if (static_cast<uint32_t>(hh) >= nh) {
+                break;
+            }
+            const uint32_t h = h0 + hh;
+            float dot = 0.0f, nk = 0.0f;
+#pragma unroll
+            for (int j = 0; j < P4; ++j) {
+                const float4 qv4 = qs[h * (D / 4) + j * 16 + sub];
+                const float4 qc = scored ? qv4 : zero;
+                const float m[4] = {kc[hh][j].x * inv, kc[hh][j].y * inv, kc[hh][j].z * inv, kc[hh][j].w * inv};
+                const float q[4] = {qc.x, qc.y, qc.z, qc.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dot += q[e] * m[e];
+                    nk += m[e] * m[e];
+                }
+            }
+            dot = row16_sum(dot);
+            nk = row16_sum(nk);
+            const float nqh = nq[l * Hkv + h];
+            const float c = dot / (sqrtf(scored ? nqh : 0.0f) * sqrtf(nk) + 1e-6f);
+            layer += static_cast<double>(c);
         }
     }
     if (scored && sub == 0u) {
@@ -225,30 +250,52 @@ __global__ __launch_bounds__(256) void meank_cos_kernel(const float *k_sum, cons
     }
 }
 
+// A block's score: the mean over scored layers of its layer cosine sum / Hkv
+// (in double, in layer order); 0 when no layer holds keys of the block.
+// Threads take (layer slice, block) pairs so every load is issued at once:
+// the workgroup covers 256 / kCombineLayers blocks, each thread its block's
+// layers l = slice, slice + kCombineLayers, ..., and one thread per block
+// adds the terms from LDS in layer order.
+constexpr uint32_t kCombineLayers = 16;
+constexpr uint32_t kCombineMaxL = 256;  // layers held in LDS per block
+
 __global__ __launch_bounds__(256) void meank_combine_kernel(const double *layer_cos,
                                                             const uint32_t *mean_tokens,
                                                             const float *invq, uint32_t L, uint32_t B,
                                                             uint32_t cap, uint32_t Hkv, float *scores) {
-    const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= B) {
-        return;
+    constexpr uint32_t kBlocks = 256 / kCombineLayers;
+    __shared__ double term[kBlocks][kCombineMaxL];
+    __shared__ uint32_t any_keys[kBlocks];
+    const uint32_t lb = threadIdx.x / kCombineLayers;  // block within the workgroup
+    const uint32_t slice = threadIdx.x - lb * kCombineLayers;
+    const uint32_t b = blockIdx.x * kBlocks + lb;
+    if (slice == 0) {
+        any_keys[lb] = 0u;
     }
-    bool has = false;
-    for (uint32_t l = 0; l < L; ++l) {
-        has |= mean_tokens[static_cast<uint64_t>(l) * cap + b] != 0;
+    __syncthreads();
+    if (b < B) {
+        uint32_t has = 0;
+        for (uint32_t l = slice; l < L; l += kCombineLayers) {
+            has |= mean_tokens[static_cast<uint64_t>(l) * cap + b] != 0 ? 1u : 0u;
+            term[lb][l] = invq[l] != 0.0f ? layer_cos[static_cast<uint64_t>(l) * B + b] : 0.0;
+        }
+        if (has) {
+            atomicOr(&any_keys[lb], 1u);
+        }
+    }
+    __syncthreads();
+    if (b >= B || slice != 0) {
+        return;
     }
     double acc = 0.0;
     uint32_t nlay = 0;
-    if (has) {
-        for (uint32_t l = 0; l < L; ++l) {
-            if (invq[l] == 0.0f) {
-                continue;
-            }
-            acc += layer_cos[static_cast<uint64_t>(l) * B + b] / static_cast<double>(Hkv ? Hkv : 1);
+    for (uint32_t l = 0; l < L; ++l) {
+        if (invq[l] != 0.0f) {
+            acc += term[lb][l] / static_cast<double>(Hkv ? Hkv : 1);
             ++nlay;
         }
     }
-    scores[b] = static_cast<float>(nlay ? acc / nlay : 0.0);
+    scores[b] = static_cast<float>((any_keys[lb] && nlay) ? acc / nlay : 0.0);
 }
 
 // Per-(layer, block) cosine sums in double, rounded up to 256 bytes so the
@@ -406,6 +453,9 @@ int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {
     if (reinterpret_cast<uintptr_t>(a->k_sum) & 15u) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "score_meank: k_sum must be 16-byte aligned");
     }
+    if (L > kCombineMaxL) {
+        return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "score_meank: more than 256 layers");
+    }
     if (L == 0 || B == 0) {
         return KVMEM_HIP_OK;
     }
@@ -445,7 +495,8 @@ int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {
         meank_cos_kernel<128><<<grid, 256, 0, ctx->stream>>>(a->k_sum, a->mean_tokens, qv, nq, invq_dev,
                                                              L, B, cap, a->n_head_kv, layer_cos);
     }
-    meank_combine_kernel<<<(B + 255) / 256, 256, 0, ctx->stream>>>(layer_cos, a->mean_tokens, invq_dev,
+    constexpr uint32_t kCombineBlocks = 256 / kCombineLayers;
+    meank_combine_kernel<<<(B + kCombineBlocks - 1) / kCombineBlocks, 256, 0, ctx->stream>>>(layer_cos, a->mean_tokens, invq_dev,
                                                                    L, B, cap, a->n_head_kv, a->scores);
     perf_end(ctx, kPerfScore);
     return hip_ok(ctx, hipGetLastError(), "score_meank launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
