@@ -598,6 +598,51 @@ def run_copy_calibration(a, torch, kv, workloads) -> dict:
             "pinned_link": link}
 
 
+def run_mfma_calibration(a, torch, kv, workloads) -> dict:
+    """The runtime's own dense GEMM (torch.matmul, i.e. hipBLASLt) on
+    8192 x 8192 x 8192 f16 and bf16 operands, each back to back for half of
+    `--seconds`, with socket power and GFX clocks sampled in the middle of
+    each loop: the dense MFMA rate a tuned library reaches on this chip under
+    the same power cap as the scorer, the reference point for the scorer's
+    TFLOP/s."""
+    import threading
+    n = 8192
+    flops = 2.0 * n * n * n
+    out = {"metric": "dense GEMM calibration (torch.matmul 8192^3)", "unit": "TFLOP/s",
+           "higher_is_better": True, "n_gpus": 1}
+    for name, dt in (("f16", torch.float16), ("bf16", torch.bfloat16)):
+        g = torch.Generator(device="cuda").manual_seed(5)
+        x = torch.randn(n, n, device="cuda", dtype=dt, generator=g)
+        w = torch.randn(n, n, device="cuda", dtype=dt, generator=g)
+        y = torch.empty(n, n, device="cuda", dtype=dt)
+        for _ in range(3):
+            torch.matmul(x, w, out=y)
+        torch.cuda.synchronize()
+        sample: dict = {}
+        secs = a.seconds / 2
+        timer = threading.Timer(secs / 2, lambda: sample.update(s=sample_power_clocks()))
+        timer.start()
+        calls, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < secs:
+            for _ in range(10):
+                torch.matmul(x, w, out=y)
+            torch.cuda.synchronize()
+            calls += 10
+        el = time.perf_counter() - t0
+        timer.join()
+        tf = flops * calls / el / 1e12
+        entry = {"ms_per_call": round(1e3 * el / calls, 4), "TFLOPs": round(tf, 1), "calls": calls,
+                 "frac_of_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "power_clocks": sample.get("s")}
+        pc = sample.get("s")
+        if pc and pc["gfx_clk_MHz"]:
+            mhz = sum(pc["gfx_clk_MHz"]) / len(pc["gfx_clk_MHz"])
+            entry["frac_at_clock"] = round(tf / (1024 * 1024 * mhz * 1e6 / 1e12), 4)
+        out[name] = entry
+        del x, w, y
+    out["value"] = out["f16"]["TFLOPs"]
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -605,8 +650,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="reselect_256k",
                     choices=["reselect_256k", "mixed_precision", "recall_1m", "copy_calibration",
-                             "cache_transform", "meank_256k", "scorer_sustained"])
-    ap.add_argument("--seconds", type=float, default=8.0, help="scorer_sustained: loop length")
+                             "cache_transform", "meank_256k", "scorer_sustained", "mfma_calibration"])
+    ap.add_argument("--seconds", type=float, default=8.0,
+                    help="scorer_sustained, mfma_calibration: loop length")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-pinned", action="store_true")
     a = ap.parse_args()
@@ -621,7 +667,7 @@ def main() -> int:
     run = {"reselect_256k": run_reselect_256k, "mixed_precision": run_mixed_precision,
            "recall_1m": run_recall_1m, "copy_calibration": run_copy_calibration,
            "cache_transform": run_cache_transform, "meank_256k": run_meank_256k,
-           "scorer_sustained": run_scorer_sustained}[a.workload]
+           "scorer_sustained": run_scorer_sustained, "mfma_calibration": run_mfma_calibration}[a.workload]
     result = run(a, torch, kv, workloads)
     print(json.dumps(result), flush=True)
     return 0
