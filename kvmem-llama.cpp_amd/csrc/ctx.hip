@@ -234,6 +234,10 @@ bool ensure_h2d_ring(kvmem_hip_ctx *ctx, size_t min_slot_bytes) {
     return true;
 }
 
+bool load_ctx_kernels() {
+    return load_kernel_object(&batched_copy_kernel);
+}
+
 }  // namespace kvmem_hip
 
 using namespace kvmem_hip;
@@ -256,7 +260,9 @@ int kvmem_hip_create(int device, kvmem_hip_ctx **out) {
     ctx->device = device;
     if (hipSetDevice(device) != hipSuccess ||
         hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess ||
-        hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking) != hipSuccess) {
+        hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking) != hipSuccess ||
+        !load_ctx_kernels() || !load_meank_kernels() || !load_score_kernels() ||
+        !load_stagein_kernels() || !load_topk_kernels()) {
         kvmem_hip_destroy(ctx);
         return KVMEM_HIP_ERR_RUNTIME;
     }

@@ -142,6 +142,22 @@ void perf_end(kvmem_hip_ctx *ctx, PerfStage s);
 // Harvest finished event pairs into the accumulators (blocking).
 void perf_collect(kvmem_hip_ctx *ctx);
 
+// Each .hip file's kernels make one code object, which HIP loads onto the
+// device at the first launch of any of them (about 5 ms for the stage-in
+// object).  Context creation asks each object for one kernel's attributes,
+// which loads it there, so no reselect step pays the load.
+bool load_ctx_kernels();
+bool load_meank_kernels();
+bool load_score_kernels();
+bool load_stagein_kernels();
+bool load_topk_kernels();
+
+template <typename K>
+inline bool load_kernel_object(K *kernel) {
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void *>(kernel)) == hipSuccess;
+}
+
 // 16-byte load that is not expected to be reused (streamed history data).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ inline uint4 load_stream16(const void *p) {

@@ -309,6 +309,10 @@ size_t meank_scratch_bytes(uint32_t L, uint32_t Hkv, uint32_t B, uint32_t D) {
     return meank_cos_bytes(L, B) + qv_bytes + 256;
 }
 
+bool load_meank_kernels() {
+    return load_kernel_object(&meank_cos_kernel<256>);
+}
+
 }  // namespace kvmem_hip
 
 using namespace kvmem_hip;

@@ -361,6 +361,10 @@ size_t score_partial_bytes(uint32_t L, uint32_t Hkv, uint32_t B, uint32_t n_q_to
     return sizeof(float) * slices * L * Hkv * B;
 }
 
+bool load_score_kernels() {
+    return load_kernel_object(&score_kernel<256>);
+}
+
 }  // namespace kvmem_hip
 
 using namespace kvmem_hip;

@@ -1193,6 +1193,10 @@ static int launch_block_job(kvmem_hip_ctx *ctx, int type_k, const BlockSource &s
     return ok ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
 }
 
+bool load_stagein_kernels() {
+    return load_kernel_object(&quant_scatter_kv_kernel<KVMEM_TYPE_Q8_0, KVMEM_TYPE_Q8_0, false, false>);
+}
+
 }  // namespace kvmem_hip
 
 using namespace kvmem_hip;

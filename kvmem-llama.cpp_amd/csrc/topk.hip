@@ -176,6 +176,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores,
     }
 }
 
+bool load_topk_kernels() {
+    return load_kernel_object(&topk_kernel);
+}
+
 }  // namespace kvmem_hip
 
 using namespace kvmem_hip;
