@@ -50,7 +50,7 @@ bool ensure_dev(kvmem_hip_ctx *ctx, DevBuf &b, size_t bytes, const char *what) {
     return true;
 }
 
-bool ensure_pin(kvmem_hip_ctx *ctx, PinBuf &b, size_t bytes, const char *what) {
+bool ensure_pin(kvmem_hip_ctx *ctx, PinBuf &b, size_t bytes, const char *what, unsigned flags) {
     if (b.ptr && b.bytes >= bytes) {
         return true;
     }
@@ -63,7 +63,7 @@ bool ensure_pin(kvmem_hip_ctx *ctx, PinBuf &b, size_t bytes, const char *what) {
         b.bytes = 0;
     }
     size_t want = bytes < 4096 ? 4096 : bytes;
-    if (!hip_ok(ctx, hipHostMalloc(&b.ptr, want, hipHostMallocDefault), what)) {
+    if (!hip_ok(ctx, hipHostMalloc(&b.ptr, want, flags), what)) {
         b.ptr = nullptr;
         return false;
     }
@@ -288,7 +288,7 @@ void kvmem_hip_destroy(kvmem_hip_ctx *ctx) {
         if (s.done) hipEventDestroy(s.done);
     }
     for (DevBuf *b : {&ctx->score_partial, &ctx->score_layers, &ctx->meank_scratch,
-                      &ctx->move_scratch, &ctx->topk_sel, &ctx->h2d_ring, &ctx->d2h_ring}) {
+                      &ctx->move_scratch, &ctx->h2d_ring, &ctx->d2h_ring}) {
         if (b->ptr) hipFree(b->ptr);
     }
     if (ctx->topk_sel_host.ptr) hipHostFree(ctx->topk_sel_host.ptr);
@@ -381,8 +381,8 @@ int kvmem_hip_reserve(kvmem_hip_ctx *ctx, const kvmem_hip_reserve_args *a) {
                     "reserve score_meank scratch")) {
         return nomem;
     }
-    if (B && (!ensure_dev(ctx, ctx->topk_sel, topk_out_bytes(B), "reserve topk output") ||
-              !ensure_pin(ctx, ctx->topk_sel_host, topk_out_bytes(B), "reserve topk pinned output"))) {
+    if (B && !ensure_pin(ctx, ctx->topk_sel_host, topk_out_bytes(B), "reserve topk host output",
+                         hipHostMallocCoherent | hipHostMallocMapped)) {
         return nomem;
     }
     if (a->max_items || L) {
@@ -421,7 +421,7 @@ int kvmem_hip_scratch_info(const kvmem_hip_ctx *ctx, kvmem_hip_scratch *out) {
         pin += s.host.bytes;
     }
     for (const DevBuf *b : {&ctx->score_partial, &ctx->score_layers, &ctx->meank_scratch,
-                            &ctx->move_scratch, &ctx->topk_sel, &ctx->h2d_ring, &ctx->d2h_ring}) {
+                            &ctx->move_scratch, &ctx->h2d_ring, &ctx->d2h_ring}) {
         dev += b->bytes;
     }
     pin += ctx->topk_sel_host.bytes;

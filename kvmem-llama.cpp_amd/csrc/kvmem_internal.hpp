@@ -56,8 +56,11 @@ struct kvmem_hip_ctx {
     kvmem_hip::DevBuf score_layers;     // [L][B] f32 when the caller passes none
     kvmem_hip::DevBuf meank_scratch;    // mean-K scorer: layer cosines, query vectors
     kvmem_hip::DevBuf move_scratch;     // gathered slots for kvmem_hip_move_slots
-    kvmem_hip::DevBuf topk_sel;         // device selection output
-    kvmem_hip::PinBuf topk_sel_host;    // pinned copy of the selection
+    // Selection written by the top-k kernel straight into coherent pinned
+    // host memory: [n] ids, [n] count, and a completion word the kernel
+    // sets to topk_epoch after the rest is visible (topk_flag_index).
+    kvmem_hip::PinBuf topk_sel_host;
+    uint32_t topk_epoch = 0;
 
     // pinned-host stage-in: device ring of block buffers + events
     kvmem_hip::DevBuf h2d_ring;
@@ -93,7 +96,8 @@ int fail(kvmem_hip_ctx *ctx, int code, const std::string &msg);
 bool hip_ok(kvmem_hip_ctx *ctx, hipError_t e, const char *what);
 
 bool ensure_dev(kvmem_hip_ctx *ctx, DevBuf &b, size_t bytes, const char *what);
-bool ensure_pin(kvmem_hip_ctx *ctx, PinBuf &b, size_t bytes, const char *what);
+bool ensure_pin(kvmem_hip_ctx *ctx, PinBuf &b, size_t bytes, const char *what,
+                unsigned flags = hipHostMallocDefault);
 
 // One device byte copy of the batched copy kernel.
 struct CopyOpDev {
@@ -122,7 +126,10 @@ size_t score_partial_bytes(uint32_t L, uint32_t Hkv, uint32_t B, uint32_t n_q_to
 // Mean-K scorer: query vectors and per-(layer, block) cosines.
 size_t meank_scratch_bytes(uint32_t L, uint32_t Hkv, uint32_t B, uint32_t D);
 // Selection output of kvmem_hip_topk over `n` blocks (device and pinned).
-inline size_t topk_out_bytes(uint32_t n) { return (static_cast<size_t>(n) + 1) * sizeof(uint32_t); }
+// Top-k host output: n ids, the count, then the completion word on its own
+// 64-byte line.
+inline size_t topk_flag_index(uint32_t n) { return (static_cast<size_t>(n) + 1 + 15) / 16 * 16; }
+inline size_t topk_out_bytes(uint32_t n) { return (topk_flag_index(n) + 16) * sizeof(uint32_t); }
 // Largest table one call with `items` ids / ops / blocks over `L` layers
 // uploads: 32-byte quantize ops, 24-byte copies of K and V per layer for a
 // block (packed stage-in/out, slot moves), or 16-byte block items after 2L

@@ -317,37 +317,69 @@ __global__ __launch_bounds__(kScoreThreads, 2) void score_kernel(ScoreParams p) 
     }
 }
 
-// layer_scores[l][b] = max_{slice, h} partial[slice][l][h][b]; one thread
-// per (layer, block).
-__global__ __launch_bounds__(256) void score_layer_kernel(const float *partial, uint32_t S,
-                                                          uint32_t L, uint32_t Hkv, uint32_t B,
-                                                          float *layer_scores) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= L * B) {
-        return;
-    }
-    const uint32_t l = i / B;
-    const uint32_t b = i - l * B;
-    float best = -FLT_MAX;
-    for (uint32_t s = 0; s < S; ++s) {
-        for (uint32_t h = 0; h < Hkv; ++h) {
-            best = fmaxf(best, partial[((static_cast<uint64_t>(s) * L + l) * Hkv + h) * B + b]);
+// The fold after the scorer, one launch:
+//   layer_scores[l][b] = max_{slice, h} partial[slice][l][h][b]
+//   scores[b]          = reduce over layers, in layer order, of layer_scores[l][b]
+//                        (sum then / L for the mean, or max).
+// A workgroup takes 16 blocks; 16 threads per block take the layers l,
+// l + 16, ... and issue a layer's partial maxima as one batch of loads.
+// After the barrier one thread per block reduces its layers in layer order,
+// again loading 16 layers per batch.  The arithmetic is the plain loops'
+// (a max chain in (slice, head) order, an ordered float sum), so batching
+// changes no bit.
+constexpr uint32_t kFoldBlocks = 16;
+constexpr uint32_t kFoldLanes = 256 / kFoldBlocks;
+constexpr uint32_t kFoldBatch = 16;
+
+__global__ __launch_bounds__(256) void score_fold_kernel(const float *partial, uint32_t S,
+                                                         uint32_t L, uint32_t Hkv, uint32_t B,
+                                                         float *layer_scores, int mode,
+                                                         float *scores) {
+    const uint32_t bl = threadIdx.x % kFoldBlocks;
+    const uint32_t lane = threadIdx.x / kFoldBlocks;
+    const uint32_t b = blockIdx.x * kFoldBlocks + bl;
+    const uint32_t per_layer = S * Hkv;
+    if (b < B) {
+        for (uint32_t l = lane; l < L; l += kFoldLanes) {
+            float best = -FLT_MAX;
+            for (uint32_t i0 = 0; i0 < per_layer; i0 += kFoldBatch) {
+                float v[kFoldBatch];
+#pragma unroll
+                for (uint32_t j = 0; j < kFoldBatch; ++j) {
+                    const uint32_t i = i0 + j;
+                    v[j] = -FLT_MAX;
+                    if (i < per_layer) {
+                        const uint32_t sl = i / Hkv;
+                        const uint32_t h = i - sl * Hkv;
+                        v[j] = partial[((static_cast<uint64_t>(sl) * L + l) * Hkv + h) * B + b];
+                    }
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < kFoldBatch; ++j) {
+                    best = fmaxf(best, v[j]);
+                }
+            }
+            layer_scores[static_cast<uint64_t>(l) * B + b] = best;
         }
     }
-    layer_scores[i] = best;
-}
-
-// scores[b] = reduce over layers (in layer order) of layer_scores[l][b].
-__global__ __launch_bounds__(256) void score_combine_kernel(const float *layer_scores, uint32_t L,
-                                                            uint32_t B, int mode, float *scores) {
-    const uint32_t b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= B) {
+    __syncthreads();
+    if (lane != 0 || b >= B) {
         return;
     }
-    float acc = mode == KVMEM_LAYER_MAX ? -FLT_MAX : 0.0f;
-    for (uint32_t l = 0; l < L; ++l) {
-        const float v = layer_scores[static_cast<uint64_t>(l) * B + b];
-        acc = mode == KVMEM_LAYER_MAX ? fmaxf(acc, v) : acc + v;
+    const bool max_mode = mode == KVMEM_LAYER_MAX;
+    float acc = max_mode ? -FLT_MAX : 0.0f;
+    for (uint32_t l0 = 0; l0 < L; l0 += kFoldBatch) {
+        float v[kFoldBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kFoldBatch; ++j) {
+            v[j] = l0 + j < L ? layer_scores[static_cast<uint64_t>(l0 + j) * B + b] : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kFoldBatch; ++j) {
+            if (l0 + j < L) {
+                acc = max_mode ? fmaxf(acc, v[j]) : acc + v[j];
+            }
+        }
     }
     if (mode == KVMEM_LAYER_MEAN && L > 0) {
         acc = acc / static_cast<float>(L);
@@ -463,15 +495,11 @@ extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist
         }
         layers = static_cast<float *>(ctx->score_layers.ptr);
     }
-    // the layer combination is timed with the selection stage
-    perf_begin(ctx, kPerfTopk);
-    const uint64_t lb = static_cast<uint64_t>(L) * B;
-    score_layer_kernel<<<static_cast<uint32_t>((lb + 255) / 256), 256, 0, ctx->stream>>>(
-        p.partial, slices, L, p.Hkv, B, layers);
-    score_combine_kernel<<<(B + 255) / 256, 256, 0, ctx->stream>>>(layers, L, B, args->layer_reduce,
-                                                                   args->scores);
-    perf_end(ctx, kPerfTopk);
-    if (!hip_ok(ctx, hipGetLastError(), "score finalize launch")) {
+    // the fold is not bracketed: a timing event costs the stream a few
+    // microseconds, as much as the fold itself
+    score_fold_kernel<<<(B + kFoldBlocks - 1) / kFoldBlocks, 256, 0, ctx->stream>>>(
+        p.partial, slices, L, p.Hkv, B, layers, args->layer_reduce, args->scores);
+    if (!hip_ok(ctx, hipGetLastError(), "score fold launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     return KVMEM_HIP_OK;

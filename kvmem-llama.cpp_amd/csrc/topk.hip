@@ -14,6 +14,15 @@
 // that threshold; they and the forced ids are compacted in ascending id
 // order with a workgroup prefix sum, which is the window order of
 // KvMemStore::pick_topk_ungrouped (kvmem_store.cpp:618-622).
+//
+// The selection goes straight to coherent pinned host memory: the ids are
+// compacted in LDS, one wave writes them out with coalesced stores, and a
+// completion word is set after its system-scope fence.  The host spins on that word
+// instead of sleeping in a stream synchronize: the wait spans the scorer
+// (milliseconds), long enough for a blocking wait to fall back to an
+// interrupt, whose wake-up cost tens of microseconds per step.  A few forced
+// ids (the sink) travel in the kernel arguments, so no upload precedes the
+// launch.
 #include "kvmem_internal.hpp"
 
 #include <algorithm>
@@ -24,6 +33,11 @@ namespace kvmem_hip {
 constexpr int kTopkThreads = 1024;
 constexpr int kTopkWaves = kTopkThreads / 64;
 constexpr int kTopkMaxN = 16384;
+constexpr int kTopkForcedInline = 64;  // forced ids passed by value
+
+struct TopkForced {
+    uint32_t id[kTopkForcedInline];
+};
 
 __device__ inline uint64_t rank_key(float s, uint32_t id, bool tie_lower) {
     if (s == 0.0f) {
@@ -67,11 +81,15 @@ __device__ inline uint32_t block_inclusive_scan(uint32_t v, uint32_t *wave_tot) 
     return v + (wave > 0 ? wave_tot[wave - 1] : 0u);
 }
 
+// `forced` is a device list, or null with the ids in `forced_inline`.
+// `out` (host-mapped) receives the ids at [0, count) and the count at [n];
+// `done` is set to `epoch` once both are visible to the host.
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores, uint32_t n,
                                                             const uint32_t *forced,
+                                                            TopkForced forced_inline,
                                                             uint32_t n_forced, uint32_t need,
-                                                            int tie_lower, uint32_t *sel,
-                                                            uint32_t *n_sel) {
+                                                            int tie_lower, uint32_t *out,
+                                                            uint32_t *done, uint32_t epoch) {
     __shared__ uint64_t keys[kTopkMaxN];
     __shared__ uint32_t forced_bits[kTopkMaxN / 32];
     __shared__ uint32_t hist[256];
@@ -90,8 +108,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores,
     }
     __syncthreads();
     for (uint32_t f = tid; f < n_forced; f += kTopkThreads) {
-        keys[forced[f]] = 0ull;  // out of the race
-        atomicOr(&forced_bits[forced[f] >> 5], 1u << (forced[f] & 31u));
+        const uint32_t id = forced ? forced[f] : forced_inline.id[f];
+        keys[id] = 0ull;  // out of the race
+        atomicOr(&forced_bits[id >> 5], 1u << (id & 31u));
     }
     __syncthreads();
 
@@ -161,18 +180,37 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores,
         return need > 0u && k >= threshold;
     };
     uint32_t cnt = 0;
-    for (uint32_t i = lo; i < hi; ++i) {
-        cnt += chosen(i) ? 1u : 0u;
-    }
-    const uint32_t incl = block_inclusive_scan(cnt, wave_tot);
-    uint32_t pos = incl - cnt;
+    uint32_t picked = 0;  // bit j: id lo + j chosen (seg <= 16)
     for (uint32_t i = lo; i < hi; ++i) {
         if (chosen(i)) {
-            sel[pos++] = i;
+            picked |= 1u << (i - lo);
+            ++cnt;
         }
     }
-    if (tid == kTopkThreads - 1) {
-        *n_sel = incl;
+    const uint32_t incl = block_inclusive_scan(cnt, wave_tot);
+    const uint32_t total = wave_tot[kTopkWaves - 1];
+    // the keys are no longer read: their LDS holds the compacted ids
+    uint32_t *ids = reinterpret_cast<uint32_t *>(keys);
+    uint32_t pos = incl - cnt;
+    for (uint32_t i = lo; i < hi; ++i) {
+        if ((picked >> (i - lo)) & 1u) {
+            ids[pos++] = i;
+        }
+    }
+    __syncthreads();
+    // one wave writes the host copy, so one fence covers it
+    if (tid >= 64u) {
+        return;
+    }
+    for (uint32_t i = tid; i < total; i += 64u) {
+        out[i] = ids[i];
+    }
+    if (tid == 0) {
+        out[n] = total;
+    }
+    __threadfence_system();
+    if (tid == 0) {
+        __hip_atomic_store(done, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 
@@ -183,6 +221,16 @@ bool load_topk_kernels() {
 }  // namespace kvmem_hip
 
 using namespace kvmem_hip;
+
+namespace {
+
+inline void cpu_relax() {
+#if defined(__x86_64__)
+    __builtin_ia32_pause();
+#endif
+}
+
+}  // namespace
 
 extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t n,
                               const uint32_t *forced, uint32_t n_forced, uint32_t need,
@@ -215,32 +263,56 @@ extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t 
     const uint32_t candidates = n - static_cast<uint32_t>(uniq.size());
     need = std::min(need, candidates);
     (void) hipSetDevice(ctx->device);
-    const size_t out_cap = static_cast<size_t>(n) + 1;
-    if (!ensure_dev(ctx, ctx->topk_sel, out_cap * sizeof(uint32_t), "topk output") ||
-        !ensure_pin(ctx, ctx->topk_sel_host, out_cap * sizeof(uint32_t), "topk pinned output")) {
+    if (!ensure_pin(ctx, ctx->topk_sel_host, topk_out_bytes(n), "topk host output",
+                    hipHostMallocCoherent | hipHostMallocMapped)) {
         return KVMEM_HIP_ERR_NOMEM;
     }
+    uint32_t *h = static_cast<uint32_t *>(ctx->topk_sel_host.ptr);
+    void *out_dev = nullptr;
+    if (!hip_ok(ctx, hipHostGetDevicePointer(&out_dev, h, 0), "topk host output mapping")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    const size_t flag = topk_flag_index(n);
+    TopkForced inl{};
     const uint32_t *forced_dev = nullptr;
-    if (!uniq.empty()) {
+    if (uniq.size() > static_cast<size_t>(kTopkForcedInline)) {
         forced_dev = static_cast<const uint32_t *>(
             upload(ctx, uniq.data(), uniq.size() * sizeof(uint32_t), "topk forced ids"));
         if (!forced_dev) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
+    } else {
+        std::copy(uniq.begin(), uniq.end(), inl.id);
     }
-    uint32_t *sel_dev = static_cast<uint32_t *>(ctx->topk_sel.ptr);
+    ctx->topk_epoch = ctx->topk_epoch + 1 == 0 ? 1 : ctx->topk_epoch + 1;
+    const uint32_t epoch = ctx->topk_epoch;
+    uint32_t *out = static_cast<uint32_t *>(out_dev);
     perf_begin(ctx, kPerfTopk);
-    topk_kernel<<<1, kTopkThreads, 0, ctx->stream>>>(scores, n, forced_dev,
+    topk_kernel<<<1, kTopkThreads, 0, ctx->stream>>>(scores, n, forced_dev, inl,
                                                      static_cast<uint32_t>(uniq.size()), need,
-                                                     tie_lower_index, sel_dev, sel_dev + n);
+                                                     tie_lower_index, out, out + flag, epoch);
     perf_end(ctx, kPerfTopk);
-    if (!hip_ok(ctx, hipGetLastError(), "topk launch") ||
-        !hip_ok(ctx, hipMemcpyAsync(ctx->topk_sel_host.ptr, sel_dev, out_cap * sizeof(uint32_t),
-                                    hipMemcpyDeviceToHost, ctx->stream), "topk D2H") ||
-        !hip_ok(ctx, hipStreamSynchronize(ctx->stream), "topk sync")) {
+    if (!hip_ok(ctx, hipGetLastError(), "topk launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
-    const uint32_t *h = static_cast<const uint32_t *>(ctx->topk_sel_host.ptr);
+    // Spin on the completion word; every few thousand rounds ask the stream
+    // whether it has drained (then the word must be set) or failed.
+    const uint32_t *done = h + flag;
+    for (uint32_t spin = 1; __atomic_load_n(done, __ATOMIC_ACQUIRE) != epoch; ++spin) {
+        cpu_relax();
+        if ((spin & 4095u) == 0) {
+            const hipError_t q = hipStreamQuery(ctx->stream);
+            if (q == hipErrorNotReady) {
+                continue;
+            }
+            if (!hip_ok(ctx, q, "topk wait")) {
+                return KVMEM_HIP_ERR_RUNTIME;
+            }
+            if (__atomic_load_n(done, __ATOMIC_ACQUIRE) != epoch) {
+                return fail(ctx, KVMEM_HIP_ERR_RUNTIME, "topk: kernel ended without its completion word");
+            }
+        }
+    }
     const uint32_t cnt = h[n];
     if (cnt > static_cast<uint32_t>(uniq.size()) + need) {
         return fail(ctx, KVMEM_HIP_ERR_RUNTIME, "topk: selection larger than requested");

@@ -73,6 +73,31 @@ def test_score_layer_reduce_modes(ctx, oracle, mode):
     assert_close(s, want, f"mode {mode}")
 
 
+@pytest.mark.parametrize("mode", [kv.LAYER_MEAN, kv.LAYER_MAX, kv.LAYER_SUM])
+def test_score_fold_many_layers_exact(ctx, oracle, mode):
+    """20 layers, 37 blocks (the last workgroup of the fold partly empty), an
+    80-token query (two 384-row slices: 32 partial maxima per layer).  The
+    block score is exactly the f32 reduction, in layer order, of the layer
+    scores the same call returns; the layer scores of two blocks match the
+    oracle."""
+    announce(f"fold: 20 layers x 37 blocks, Tq=80, mode {mode}")
+    L, B, Tq = 20, 37, 80
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=Tq, seed=29)
+    s, ls = run_score(ctx, k, q, kv.TYPE_BF16, 24, 4, 256, reduce=mode)
+    ls32 = ls.astype(np.float32)
+    if mode == kv.LAYER_MAX:
+        acc = ls32.max(axis=0)
+    else:
+        acc = np.zeros(B, dtype=np.float32)
+        for lay in range(L):
+            acc = (acc + ls32[lay]).astype(np.float32)
+        if mode == kv.LAYER_MEAN:
+            acc = (acc / np.float32(L)).astype(np.float32)
+    assert np.array_equal(s.astype(np.float32), acc)
+    want = oracle.score_pertoken_max(q_f32(q), workloads.to_bits(torch, k[:, :2].contiguous()))
+    assert_close(ls[:, :2], want, "layer scores")
+
+
 def test_score_invariants(ctx):
     """Permuting tokens inside a block and query heads inside a GQA group
     leaves scores unchanged; scaling Q by 2 scales them by 2."""

@@ -75,3 +75,22 @@ def test_topk_need_exceeds_candidates(ctx):
     assert ctx.topk(d.data_ptr(), 10, 0, forced=[3, 7]) == [3, 7]
     with pytest.raises(kv.KvMemError):
         ctx.topk(d.data_ptr(), 10, 1, forced=[10])
+
+
+@pytest.mark.parametrize("n_mand", [63, 64, 300])
+def test_topk_many_forced(ctx, oracle, n_mand):
+    """Up to 64 distinct forced ids travel in the kernel arguments, more go
+    through an upload: both sides of that limit, with repeated ids (which
+    count once)."""
+    announce(f"sink + {n_mand} mandatory ids, repeats included")
+    rng = np.random.default_rng(40 + n_mand)
+    n, fill = 5000, 200
+    s = rng.standard_normal(n).astype(np.float32)
+    mand = sorted(rng.choice(np.arange(1, n), n_mand, replace=False).tolist())
+    budget = 1 + n_mand + fill
+    want = oracle.pick_topk(s.astype(np.float64), budget, sink=1, mandatory=mand)
+    d = dev(s)
+    torch.cuda.synchronize()
+    got = ctx.topk(d.data_ptr(), n, fill, forced=[0] + mand + mand[:5])
+    assert got == want
+    assert len(got) == budget
