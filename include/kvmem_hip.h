@@ -255,12 +255,14 @@ KVMEM_HIP_API int kvmem_hip_stagein_blocks(kvmem_hip_ctx *ctx,
                                            const uint32_t *slots,
                                            uint32_t n);
 
-/* Host-resident history in pinned memory, block-major: block b occupies
- * one contiguous span of n_layers*(block_tokens*(n_embd_k+n_embd_v)) halves
- * laid out [layer][K rows then V rows].  Blocks are copied with
- * hipMemcpyAsync on a side stream into a device ring and quantized on the
- * context stream as each copy lands (copy/kernel overlap).  Replaces the
- * 32 MiB slab H2D of kvmem_stagein_flush (stagein.cu:632-753), which
+/* Host-resident history, block-major: block b occupies one contiguous span
+ * of n_layers*(block_tokens*(n_embd_k+n_embd_v)) halves laid out
+ * [layer][K rows then V rows].  When all n_blocks spans lie inside one
+ * pinned allocation (hipHostMalloc, torch pin_memory), the quantize kernel
+ * reads them over the link itself: one launch, no device staging.  Other
+ * host memory is copied with hipMemcpyAsync on a side stream into a device
+ * ring and quantized on the context stream as each copy lands.  Replaces
+ * the 32 MiB slab H2D of kvmem_stagein_flush (stagein.cu:632-753), which
  * event-synchronises every H2D. */
 typedef struct kvmem_hip_host_history {
     const void *base;           /* pinned host memory */
@@ -296,10 +298,11 @@ typedef struct kvmem_hip_packed_host {
 
 /* Stage-out: copy the packed rows of pool slot slots[i] (every layer, K and
  * V, n_tokens[i] rows) to block block_ids[i] of the packed host store.
- * The rows are gathered into a device ring in the host layout by one copy
- * launch per 128 MiB batch on the context stream, then copied device-to-
- * host on the side stream, so a later call's gathers overlap earlier
- * copies.
+ * A store inside one pinned allocation is written by one copy launch on the
+ * context stream.  Otherwise the rows are gathered into a device ring in
+ * the host layout by one copy launch per 128 MiB batch, then copied
+ * device-to-host on the side stream, so a later call's gathers overlap
+ * earlier copies.
  * Asynchronous: the host rows are complete after kvmem_hip_sync.  Replaces
  * kvmem_stageout_enqueue / submit / wait (llama-kvmem-stagein.h:40-47,
  * stagein.cu:842-963: gather kernel into a 32 MiB slab, D2H into two
@@ -312,10 +315,11 @@ KVMEM_HIP_API int kvmem_hip_stageout_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_
 
 /* Stage-in of packed rows, the reference's live path (write_block_to_gpu:
  * copy_k_gpu / copy_v_gpu into the slab, enqueue_v, flush,
- * llama-memory-kvmem.cpp:2726-2791): block spans go host-to-device into
- * the device ring on the side stream, and one copy launch per batch
- * scatters them into slot slots[i] of every layer (n_tokens[i] rows), no
- * quantization.  The pool transform (xf) does not apply: packed rows are
+ * llama-memory-kvmem.cpp:2726-2791): the rows go into slot slots[i] of
+ * every layer (n_tokens[i] rows), no quantization.  A store inside one
+ * pinned allocation is read by one copy launch; otherwise block spans go
+ * host-to-device into the device ring on the side stream and one copy
+ * launch per batch scatters them.  The pool transform (xf) does not apply: packed rows are
  * already in the cache's form. */
 KVMEM_HIP_API int kvmem_hip_stagein_packed_host(kvmem_hip_ctx *ctx,
                                                 const kvmem_hip_packed_host *src,

@@ -234,6 +234,30 @@ bool ensure_h2d_ring(kvmem_hip_ctx *ctx, size_t min_slot_bytes) {
     return true;
 }
 
+uint8_t *host_device_view(const void *p, uint64_t bytes) {
+    if (!p || bytes == 0) {
+        return nullptr;
+    }
+    hipPointerAttribute_t a{};
+    if (hipPointerGetAttributes(&a, p) != hipSuccess || a.type != hipMemoryTypeHost ||
+        !a.devicePointer) {
+        (void) hipGetLastError();
+        return nullptr;
+    }
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, static_cast<hipDeviceptr_t>(a.devicePointer)) != hipSuccess) {
+        (void) hipGetLastError();
+        return nullptr;
+    }
+    const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+    const uintptr_t v = reinterpret_cast<uintptr_t>(a.devicePointer);
+    if (v < b || v - b > size || bytes > size - (v - b)) {
+        return nullptr;
+    }
+    return static_cast<uint8_t *>(a.devicePointer);
+}
+
 bool load_ctx_kernels() {
     return load_kernel_object(&batched_copy_kernel);
 }

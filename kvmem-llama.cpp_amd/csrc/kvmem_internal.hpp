@@ -139,6 +139,12 @@ inline size_t upload_bytes_for(uint32_t items, uint32_t L) {
     return per_item * items + 16 * static_cast<size_t>(L) + 1024;
 }
 
+// The device's address for host memory [p, p + bytes) when the whole range
+// lies inside one pinned host allocation (kernels may then read or write it
+// directly over the link); nullptr otherwise (pageable memory, a range past
+// the allocation).  Clears the runtime error a failed query leaves behind.
+uint8_t *host_device_view(const void *p, uint64_t bytes);
+
 // Copy `bytes` of host data to device memory through the upload ring,
 // ordered on the context stream.  Returns the device address or nullptr.
 void *upload(kvmem_hip_ctx *ctx, const void *src, size_t bytes, const char *what);

@@ -4,7 +4,10 @@
 // (stage-out gather + D2H, llama-kvmem-stagein.cu:842-963; the live
 // write_block_to_gpu upload, llama-memory-kvmem.cpp:2726-2791).
 //
-// Both are copy pipelines over two streams.  Stage-out gathers a batch of
+// A store in pinned memory is read or written by the copy kernel itself:
+// one launch moves every row over the link at its full rate (runtime copies
+// of a few MB each leave ~10 us gaps between them).  A pageable store goes
+// through copy pipelines over two streams.  Stage-out gathers a batch of
 // blocks (every layer, K and V) into a 128 MiB device ring slot in the host
 // layout with one copy launch on the context stream, then copies the spans
 // device-to-host on the side stream (runs of consecutive blocks as one
@@ -124,6 +127,28 @@ int kvmem_hip_stageout_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool,
         return st;
     }
     (void) hipSetDevice(ctx->device);
+    // Pinned store: one copy launch writes the rows over the link.
+    if (uint8_t *view = host_device_view(dst->base, static_cast<uint64_t>(dst->n_blocks) * g.span)) {
+        std::vector<CopyOpDev> ops;
+        ops.reserve(static_cast<size_t>(n) * pool->n_layers * 2);
+        for (uint32_t i = 0; i < n; ++i) {
+            const uint32_t nt = n_tokens[i];
+            for (uint32_t l = 0; l < pool->n_layers && nt > 0; ++l) {
+                uint8_t *d = view + static_cast<uint64_t>(block_ids[i]) * g.span + l * g.layer_bytes;
+                ops.push_back({static_cast<const uint8_t *>(pool->k_layers[l]) + slots[i] * g.run_k, d,
+                               nt * g.row_k});
+                if (g.row_v) {
+                    ops.push_back({static_cast<const uint8_t *>(pool->v_layers[l]) + slots[i] * g.run_v,
+                                   d + g.run_k, nt * g.row_v});
+                }
+            }
+        }
+        perf_begin(ctx, kPerfCopy);
+        const bool ok = launch_copy_ops(ctx, ops, "stage-out to the pinned store");
+        perf_end(ctx, kPerfCopy);
+        return ok ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
+    }
+    // Pageable store: gather into the device ring, then runtime copies.
     if (!ensure_d2h_ring(ctx, g.span)) {
         return KVMEM_HIP_ERR_NOMEM;  // the failing call is in kvmem_hip_last_error
     }
@@ -224,6 +249,33 @@ int kvmem_hip_stagein_packed_host(kvmem_hip_ctx *ctx, const kvmem_hip_packed_hos
         return st;
     }
     (void) hipSetDevice(ctx->device);
+    // Pinned store: one copy launch reads the rows over the link.
+    if (const uint8_t *view = host_device_view(src->base, static_cast<uint64_t>(src->n_blocks) * g.span)) {
+        std::vector<CopyOpDev> ops;
+        ops.reserve(static_cast<size_t>(n) * pool->n_layers * 2);
+        uint64_t bytes = 0;
+        for (uint32_t i = 0; i < n; ++i) {
+            const uint32_t nt = n_tokens[i];
+            for (uint32_t l = 0; l < pool->n_layers && nt > 0; ++l) {
+                const uint8_t *s = view + static_cast<uint64_t>(block_ids[i]) * g.span + l * g.layer_bytes;
+                ops.push_back({s, static_cast<uint8_t *>(pool->k_layers[l]) + slots[i] * g.run_k, nt * g.row_k});
+                bytes += nt * g.row_k;
+                if (g.row_v) {
+                    ops.push_back({s + g.run_k, static_cast<uint8_t *>(pool->v_layers[l]) + slots[i] * g.run_v,
+                                   nt * g.row_v});
+                    bytes += nt * g.row_v;
+                }
+            }
+        }
+        perf_begin(ctx, kPerfSet);
+        const bool ok = launch_copy_ops(ctx, ops, "packed stage-in from the pinned store");
+        perf_end(ctx, kPerfSet);
+        if (ok) {
+            ctx->h2d_bytes += bytes;
+        }
+        return ok ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
+    }
+    // Pageable store: runtime copies into the stage-in ring, then a scatter.
     if (!ensure_h2d_ring(ctx, g.span)) {
         return KVMEM_HIP_ERR_NOMEM;  // the failing call is in kvmem_hip_last_error
     }

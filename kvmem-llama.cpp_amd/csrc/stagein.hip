@@ -1370,7 +1370,40 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
         return st;
     }
     (void) hipSetDevice(ctx->device);
-    // Device ring: kH2dRing slots of 32 MiB or more (at least one block each).
+    // Pinned history: the kernel reads the blocks over the link itself, one
+    // launch for every block, no ring and no copy calls (the copies cost the
+    // link ~10 us each between them).
+    if (const uint8_t *view = host_device_view(hist->base, span * hist->n_blocks)) {
+        std::vector<uint32_t> items(4 * static_cast<size_t>(n));
+        for (uint32_t i = 0; i < n; ++i) {
+            const uint32_t b = block_ids[i];
+            items[4 * i + 0] = b;
+            items[4 * i + 1] = slots[i];
+            items[4 * i + 2] = (b + 1 == hist->n_blocks && hist->last_block_tokens != 0)
+                                   ? std::min(hist->last_block_tokens, T) : T;
+            items[4 * i + 3] = item_pos0(pool, block_ids, i, T);
+        }
+        JobTables jt;
+        if (!upload_block_job(ctx, pool, want_v, items, xp, jt)) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        const BlockSource sk = make_block_source(pool->type_k, view, span, layer_bytes, jt.layers, L, T,
+                                                 hist->n_embd_k, jt.items, xp, true, jt.theta);
+        BlockSource sv{};
+        if (want_v) {
+            sv = make_block_source(pool->type_v, view + kbytes, span, layer_bytes, jt.layers + L, L, T,
+                                   hist->n_embd_v, jt.items, xp, false, jt.theta);
+        }
+        perf_begin(ctx, kPerfSet);
+        st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp.on);
+        perf_end(ctx, kPerfSet);
+        if (st == KVMEM_HIP_OK) {
+            ctx->h2d_bytes += static_cast<uint64_t>(n) * span;
+        }
+        return st;
+    }
+    // Pageable history: device ring of kH2dRing slots of 32 MiB or more (at
+    // least one block each), filled by runtime copies.
     if (!ensure_h2d_ring(ctx, span)) {
         return KVMEM_HIP_ERR_NOMEM;  // the failing call is in kvmem_hip_last_error
     }

@@ -181,18 +181,24 @@ def test_engine_pinned_host_history(oracle):
         check_pool(eng, oracle, k, v, sel.blocks, kv.TYPE_Q5_0, kv.TYPE_Q8_0)
 
 
-def test_stagein_host_many_ring_batches(ctx, oracle):
-    """Regression: a pinned-host stage-in spanning many device-ring batches
-    (per-call tables must stay valid through every batch)."""
-    announce("pinned-host stage-in, 4 layers, 47 blocks in 5 ring batches, K q8_0 / V q4_0")
+@pytest.mark.parametrize("memory", ["pinned", "pageable"])
+def test_stagein_host_many_ring_batches(ctx, oracle, memory):
+    """A host-history stage-in of 47 blocks, K q8_0 / V q4_0.  From pinned
+    memory the kernel reads the blocks itself in one launch; from pageable
+    memory they go through five device-ring batches (regression: the
+    per-call tables must stay valid through every batch)."""
+    announce(f"{memory} host stage-in, 4 layers, 47 blocks, K q8_0 / V q4_0")
     Lh, Ek, Ev, nb, n_slots = 4, 2048, 1024, 60, 64
     rng = np.random.default_rng(21)
     kh = workloads.heavy_tailed(22, (nb, Lh, T, Ek))
     vh = workloads.heavy_tailed(23, (nb, Lh, T, Ev))
     span = Lh * T * (Ek + Ev)
-    hb = torch.empty((nb, span), dtype=torch.int16, pin_memory=True)
-    hb.copy_(torch.from_numpy(np.concatenate([kh.reshape(nb, Lh, -1), vh.reshape(nb, Lh, -1)],
-                                             axis=2).reshape(nb, span).view(np.int16)))
+    rows = np.concatenate([kh.reshape(nb, Lh, -1), vh.reshape(nb, Lh, -1)], axis=2).reshape(nb, span)
+    if memory == "pinned":
+        hb = torch.empty((nb, span), dtype=torch.int16, pin_memory=True)
+        hb.copy_(torch.from_numpy(rows.view(np.int16)))
+    else:
+        hb = torch.from_numpy(np.ascontiguousarray(rows.view(np.int16)))
     ids = sorted(rng.choice(nb, 47, replace=False).tolist())
     slots = rng.permutation(n_slots)[:47].tolist()
     rbk, rbv = kv.row_size(kv.TYPE_Q8_0, Ek), kv.row_size(kv.TYPE_Q4_0, Ev)

@@ -94,10 +94,12 @@ def test_stageout_after_quantize_and_restore(ctx, oracle):
             assert (b_k[s2 * T + nt:(s2 + 1) * T] == 0x3C).all()
 
 
-def test_packed_many_ring_batches(ctx):
-    """Both directions over batches that fill several 32 MiB ring slots
-    (47 blocks of 5.5 MiB), with alternating ring slots reused."""
-    announce("4 layers, F16 K 2048 / q8_0 V 1024, 47 blocks in ~8 batches each way")
+@pytest.mark.parametrize("memory", ["pinned", "pageable"])
+def test_packed_many_ring_batches(ctx, memory):
+    """Both directions, 47 blocks of 5.5 MiB.  A pinned store is read and
+    written by one copy launch each way; a pageable one goes through batches
+    that fill several device-ring slots, with alternating slots reused."""
+    announce(f"{memory} store: 4 layers, F16 K 2048 / q8_0 V 1024, 47 blocks each way")
     L, Ek, Ev, n_slots, nb = 4, 2048, 1024, 64, 60
     tk, tv = kv.TYPE_F16, kv.TYPE_Q8_0
     g = torch.Generator(device="cuda").manual_seed(7)
@@ -108,7 +110,10 @@ def test_packed_many_ring_batches(ctx):
     ids = sorted(rng.choice(nb, 47, replace=False).tolist())
     slots = rng.permutation(n_slots)[:47].tolist()
     span = L * T * (rk + rv)
-    store = pinned(nb * span)
+    if memory == "pinned":
+        store = pinned(nb * span)
+    else:
+        store = torch.from_numpy(np.full(nb * span, SENT, dtype=np.uint8))
     ph = kv.PackedHost(store.data_ptr(), L, nb, T)
     torch.cuda.synchronize()
     ctx.stageout_blocks(pool, ph, ids, slots, [T] * 47)
