@@ -98,6 +98,7 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
         restore()
     ctx.perf_enable(True)
     times, staged, moved, score_ms, set_ms, sel_ms, layout_ms = [], [], [], 0.0, 0.0, 0.0, 0.0
+    d2d_bytes = 0
     for _ in range(steps):
         ctx.perf_reset()
         torch.cuda.synchronize()
@@ -110,6 +111,7 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
         set_ms += pf["set_ms"]
         sel_ms += pf["topk_ms"]
         layout_ms += pf["layout_ms"]
+        d2d_bytes += pf["d2d_bytes"]
         staged.append(st["n_staged"])
         moved.append(st["n_moved"])
         restore()
@@ -117,7 +119,7 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
     assert all(x == staged[0] for x in staged), staged
     return {"ms_step": 1e3 * sum(times) / steps, "score_ms": score_ms / steps,
             "set_ms": set_ms / steps, "sel_ms": sel_ms / steps, "n_staged": staged[0],
-            "layout_ms": layout_ms / steps, "n_moved": max(moved)}
+            "layout_ms": layout_ms / steps, "n_moved": max(moved), "d2d_bytes": d2d_bytes // steps}
 
 
 def stage_bytes(kv, n_blocks: int, type_k: int, type_v: int) -> int:
@@ -345,8 +347,9 @@ def run_reselect_256k(a, torch, kv, workloads) -> dict:
 def canonical_layout_mode(a, torch, kv, k, v, q, prev: list) -> dict:
     """The same step with canonical slot order (window slot i holds the
     i-th selected block, as layout_gpu_slots_by_orig_pos): the resident
-    blocks that change slot are moved on the device (gather to scratch, then
-    scatter) before the stage-in.  Reported beside the default step."""
+    blocks that change slot are moved on the device before the stage-in
+    (chains of moves walked backwards; the slots where chains are cut are
+    saved to scratch first).  Reported beside the default step."""
     log("canonical layout: the same step with slot i = i-th selected block")
     eng = make_engine(kv, torch, k, v, canonical_layout=1)
     ctx = kv.Context.borrow(eng.ctx_handle())
@@ -354,13 +357,15 @@ def canonical_layout_mode(a, torch, kv, k, v, q, prev: list) -> dict:
     eng.close()
     row = kv.row_size(kv.TYPE_Q8_0, E)
     moved_bytes = m["n_moved"] * L * 2 * T * row  # one copy of the moved blocks' K and V rows
+    device_bytes = 2 * m["d2d_bytes"]  # every byte the library copied, read + write
     out = {"ms_per_step": round(m["ms_step"], 4), "n_moved": m["n_moved"], "n_staged": m["n_staged"],
            "layout_ms": round(m["layout_ms"], 4), "stagein_kernel_ms": round(m["set_ms"], 4),
            "moved_bytes": moved_bytes,
            "algorithmic_bytes": 2 * moved_bytes,  # read + write once
-           "device_bytes": 4 * moved_bytes}      # gather (read + write) and scatter (read + write)
+           "device_bytes": device_bytes}
     if m["layout_ms"] > 0:
-        out["GBs_device"] = round(4 * moved_bytes / (m["layout_ms"] * 1e-3) / 1e9, 1)
+        out["GBs_algorithmic"] = round(2 * moved_bytes / (m["layout_ms"] * 1e-3) / 1e9, 1)
+        out["GBs_device"] = round(device_bytes / (m["layout_ms"] * 1e-3) / 1e9, 1)
     return out
 
 

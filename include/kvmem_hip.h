@@ -330,8 +330,12 @@ KVMEM_HIP_API int kvmem_hip_stagein_packed_host(kvmem_hip_ctx *ctx,
 /* Move slots inside the pool: the first n_tokens[i] rows of slot
  * src_slots[i] -> slot dst_slots[i] for every layer, K and V (quantized
  * bytes copied unchanged; the destination's rows past n_tokens[i] keep
- * their bytes).  n_tokens == NULL moves whole slots.  Overlapping moves are
- * hazard-free: sources are gathered to device scratch first.  Replaces the
+ * their bytes).  n_tokens == NULL moves whole slots.  The result is as if
+ * every source were read before any destination is written, whatever the
+ * overlap.  When sources are distinct and destinations are distinct (a
+ * canonical layout's moves), chains and cycles of moves are walked
+ * backwards and the bytes move once; other sets are gathered to device
+ * scratch and scattered, destinations in list order.  Replaces the
  * gather/scatter D2D of layout_gpu_slots_by_orig_pos, which moves each
  * block's n_tokens rows (llama-memory-kvmem.cpp:1003-1093). */
 KVMEM_HIP_API int kvmem_hip_move_slots(kvmem_hip_ctx *ctx,

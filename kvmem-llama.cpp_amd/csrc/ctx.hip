@@ -157,11 +157,13 @@ void perf_collect(kvmem_hip_ctx *ctx) {
 }
 
 // ------------------------------------------------------------------------
-// Batched byte copies: one workgroup per op, 16-byte vectors when both
-// addresses and the size are 16-byte aligned.
+// Batched byte copies: `pieces` workgroups per op, each a contiguous share
+// of it, 16-byte vectors when both addresses and the size are 16-byte
+// aligned.  A launch with few ops splits them so the chip fills.
 // ------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops, int n) {
-    const int i = blockIdx.x;
+__global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops, int n, int pieces) {
+    const int i = blockIdx.x / pieces;
+    const int piece = blockIdx.x - i * pieces;
     if (i >= n) {
         return;
     }
@@ -171,31 +173,43 @@ __global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops,
         const uint4 *s = reinterpret_cast<const uint4 *>(op.src);
         uint4 *d = reinterpret_cast<uint4 *>(op.dst);
         const uint64_t n16 = op.nbytes >> 4;
-        for (uint64_t j = threadIdx.x; j < n16; j += blockDim.x) {
+        const uint64_t j1 = n16 * (piece + 1) / pieces;
+        for (uint64_t j = n16 * piece / pieces + threadIdx.x; j < j1; j += blockDim.x) {
             d[j] = s[j];
         }
         return;
     }
-    for (uint64_t j = threadIdx.x; j < op.nbytes; j += blockDim.x) {
+    const uint64_t b1 = op.nbytes * (piece + 1) / pieces;
+    for (uint64_t j = op.nbytes * piece / pieces + threadIdx.x; j < b1; j += blockDim.x) {
         op.dst[j] = op.src[j];
     }
+}
+
+const CopyOpDev *upload_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, const char *what) {
+    if (ops.size() > 0x7fffffffu / 8u) {
+        fail(ctx, KVMEM_HIP_ERR_INVALID, std::string(what) + ": too many copies");
+        return nullptr;
+    }
+    return static_cast<const CopyOpDev *>(upload(ctx, ops.data(), ops.size() * sizeof(CopyOpDev), what));
+}
+
+bool launch_uploaded_copies(kvmem_hip_ctx *ctx, const CopyOpDev *dops, size_t n, const char *what) {
+    if (n == 0) {
+        return true;
+    }
+    // ~2048 workgroups fill the chip (256 CUs x 8); at most 8 pieces per op
+    const int pieces = static_cast<int>(std::min<size_t>(8, std::max<size_t>(1, 2048 / n)));
+    batched_copy_kernel<<<static_cast<uint32_t>(n * pieces), 256, 0, ctx->stream>>>(
+        dops, static_cast<int>(n), pieces);
+    return hip_ok(ctx, hipGetLastError(), what);
 }
 
 bool launch_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, const char *what) {
     if (ops.empty()) {
         return true;
     }
-    if (ops.size() > 0x7fffffffu) {
-        fail(ctx, KVMEM_HIP_ERR_INVALID, std::string(what) + ": too many copies");
-        return false;
-    }
-    void *dops = upload(ctx, ops.data(), ops.size() * sizeof(CopyOpDev), what);
-    if (!dops) {
-        return false;
-    }
-    batched_copy_kernel<<<static_cast<uint32_t>(ops.size()), 256, 0, ctx->stream>>>(
-        static_cast<const CopyOpDev *>(dops), static_cast<int>(ops.size()));
-    return hip_ok(ctx, hipGetLastError(), what);
+    const CopyOpDev *dops = upload_copy_ops(ctx, ops, what);
+    return dops && launch_uploaded_copies(ctx, dops, ops.size(), what);
 }
 
 bool ensure_h2d_ring(kvmem_hip_ctx *ctx, size_t min_slot_bytes) {
@@ -510,14 +524,14 @@ int kvmem_hip_d2d_batched(kvmem_hip_ctx *ctx, const void *const *src, void *cons
         total += nbytes[i];
     }
     (void) hipSetDevice(ctx->device);
-    void *dops = upload(ctx, ops.data(), ops.size() * sizeof(CopyOpDev), "d2d_batched ops");
+    const CopyOpDev *dops = upload_copy_ops(ctx, ops, "d2d_batched ops");
     if (!dops) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     perf_begin(ctx, kPerfLayout);
-    batched_copy_kernel<<<n, 256, 0, ctx->stream>>>(static_cast<const CopyOpDev *>(dops), n);
+    const bool ok = launch_uploaded_copies(ctx, dops, ops.size(), "d2d_batched launch");
     perf_end(ctx, kPerfLayout);
-    if (!hip_ok(ctx, hipGetLastError(), "d2d_batched launch")) {
+    if (!ok) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     ctx->d2d_bytes += total;

@@ -106,9 +106,13 @@ struct CopyOpDev {
     uint64_t nbytes;
 };
 
-// Upload `ops` and copy them in one launch on the context stream (one
-// workgroup per op, 16-byte vectors where aligned).
+// Upload `ops` and copy them in one launch on the context stream (each op
+// split over 1-8 workgroups so that a launch fills the chip, 16-byte
+// vectors where aligned).  The two halves apart: the upload, then launches
+// of the uploaded table (e.g. inside a timing bracket).
 bool launch_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, const char *what);
+const CopyOpDev *upload_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, const char *what);
+bool launch_uploaded_copies(kvmem_hip_ctx *ctx, const CopyOpDev *dops, size_t n, const char *what);
 
 // The pinned-host stage-in ring: kH2dRing device slots of at least
 // `min_slot_bytes` (32 MiB or more, grown only), with their events.
@@ -132,10 +136,11 @@ inline size_t topk_flag_index(uint32_t n) { return (static_cast<size_t>(n) + 1 +
 inline size_t topk_out_bytes(uint32_t n) { return (topk_flag_index(n) + 16) * sizeof(uint32_t); }
 // Largest table one call with `items` ids / ops / blocks over `L` layers
 // uploads: 32-byte quantize ops, 24-byte copies of K and V per layer for a
-// block (packed stage-in/out, slot moves), or 16-byte block items after 2L
-// pool pointers and up to 128 RoPE frequencies.
+// block (packed stage-in/out, slot moves), 16-byte block items after 2L
+// pool pointers and up to 128 RoPE frequencies, or 76-byte slot-move chain
+// segments after 2L pool pointers.
 inline size_t upload_bytes_for(uint32_t items, uint32_t L) {
-    const size_t per_item = std::max<size_t>(32, 48 * static_cast<size_t>(L));
+    const size_t per_item = std::max<size_t>(80, 48 * static_cast<size_t>(L));
     return per_item * items + 16 * static_cast<size_t>(L) + 1024;
 }
 

@@ -1193,6 +1193,175 @@ static int launch_block_job(kvmem_hip_ctx *ctx, int type_k, const BlockSource &s
     return ok ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
 }
 
+// ---------------------------------------------------------- slot moves
+//
+// A set of slot moves with distinct sources and distinct destinations is a
+// set of chains (s0 -> s1 -> ... -> sk) and cycles.  Chains are cut into
+// segments of at most kChainSeg moves; the first source of every segment
+// but a chain's first (and a cycle's first source) is saved to scratch
+// beforehand, since another segment overwrites it.  One thread then carries
+// one 16-byte column of a block through a whole segment with no
+// synchronisation: it reads all the segment's sources, then writes all its
+// destinations (straight-line code per segment length), and no other thread
+// reads or writes that column of those slots.  The bytes move once, plus the saved slots, where a gather to
+// scratch and a scatter back move them twice.
+constexpr int kChainSeg = 8;
+
+struct ChainSeg {
+    uint32_t slot[kChainSeg + 1];  // move j: slot[j] -> slot[j + 1]
+    uint32_t nt[kChainSeg];        // rows move j carries
+    uint32_t len;                  // moves in the segment
+    int32_t saved;                 // >= 0: slot[0]'s rows are this scratch entry
+};
+
+static_assert(sizeof(ChainSeg) == 76, "upload_bytes_for counts 76-byte chain segments");
+
+struct ChainParams {
+    const ChainSeg *segs;
+    uint8_t *const *k_layers;      // device [L]
+    uint8_t *const *v_layers;      // device [L], or null
+    const uint8_t *scratch;        // entry e: [layer][T rows of K][T rows of V]
+    uint64_t kspan, vspan;         // one slot of one layer
+    uint64_t entry_bytes;          // L * (kspan + vspan)
+    uint32_t krow16, vrow16;       // row bytes / 16
+    uint32_t L, T;
+    uint32_t vec_per_layer;        // T * (krow16 + vrow16)
+};
+
+// The N moves of one segment for one 16-byte column: N loads, then N stores
+// (rows at or past a move's n_tokens are inside the slot but not stored).
+template <int N>
+__device__ inline void seg_moves(const ChainSeg *seg, const uint8_t *first, uint8_t *base, uint64_t span,
+                                 uint64_t off, uint32_t r) {
+    u32x4_t val[N];
+    val[0] = *reinterpret_cast<const u32x4_t *>(first);
+#pragma unroll
+    for (int j = 1; j < N; ++j) {
+        val[j] = *reinterpret_cast<const u32x4_t *>(base + seg->slot[j] * span + off);
+    }
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        if (r < seg->nt[j]) {
+            *reinterpret_cast<u32x4_t *>(base + seg->slot[j + 1] * span + off) = val[j];
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void move_chain_kernel(ChainParams p) {
+    const ChainSeg *seg = p.segs + blockIdx.y;
+    const uint32_t x = blockIdx.x * 256u + threadIdx.x;
+    if (x >= p.L * p.vec_per_layer) {
+        return;
+    }
+    const uint32_t l = x / p.vec_per_layer;
+    uint32_t v = x - l * p.vec_per_layer;
+    const uint32_t kvecs = p.T * p.krow16;
+    const bool is_v = v >= kvecs;
+    if (is_v) {
+        v -= kvecs;
+    }
+    const uint32_t r = v / (is_v ? p.vrow16 : p.krow16);  // row within the slot
+    uint8_t *base = is_v ? p.v_layers[l] : p.k_layers[l];
+    const uint64_t span = is_v ? p.vspan : p.kspan;
+    const uint64_t off = static_cast<uint64_t>(v) * 16u;
+    const int32_t saved = seg->saved;
+    // Every slot of a segment is distinct (a cycle's closing source comes
+    // from scratch), so all the segment's loads go first, then its stores:
+    // up to kChainSeg loads in flight per thread.
+    const uint8_t *first = saved >= 0
+        ? p.scratch + static_cast<uint64_t>(saved) * p.entry_bytes + l * (p.kspan + p.vspan) +
+              (is_v ? p.kspan : 0u) + off
+        : base + seg->slot[0] * span + off;
+    static_assert(kChainSeg == 8, "one case per segment length");
+    switch (seg->len) {  // uniform per workgroup
+        case 1: seg_moves<1>(seg, first, base, span, off, r); break;
+        case 2: seg_moves<2>(seg, first, base, span, off, r); break;
+        case 3: seg_moves<3>(seg, first, base, span, off, r); break;
+        case 4: seg_moves<4>(seg, first, base, span, off, r); break;
+        case 5: seg_moves<5>(seg, first, base, span, off, r); break;
+        case 6: seg_moves<6>(seg, first, base, span, off, r); break;
+        case 7: seg_moves<7>(seg, first, base, span, off, r); break;
+        case 8: seg_moves<8>(seg, first, base, span, off, r); break;
+        default: break;
+    }
+}
+
+// Chains of the moves with rows to carry, cut into segments; `saved` gets
+// the slots to save first.  False when two such moves share a source or a
+// destination (self-moves included).  Self-moves are then dropped: their
+// slot is neither read nor written by any other move.
+static bool build_chains(const uint32_t *src, const uint32_t *dst, const uint32_t *n_tokens, uint32_t n,
+                         uint32_t T, uint32_t n_slots, std::vector<ChainSeg> &segs,
+                         std::vector<uint32_t> &saved) {
+    std::vector<int32_t> from(n_slots, -1), into(n_slots, -1);
+    std::vector<uint32_t> keep;
+    for (uint32_t i = 0; i < n; ++i) {
+        const uint32_t nt = n_tokens ? n_tokens[i] : T;
+        if (nt == 0) {
+            continue;
+        }
+        if (from[src[i]] >= 0 || into[dst[i]] >= 0) {
+            return false;
+        }
+        from[src[i]] = static_cast<int32_t>(i);
+        into[dst[i]] = static_cast<int32_t>(i);
+        if (src[i] != dst[i]) {
+            keep.push_back(i);
+        }
+    }
+    for (uint32_t i = 0; i < n; ++i) {  // self-moves leave the chain maps
+        const uint32_t nt = n_tokens ? n_tokens[i] : T;
+        if (nt != 0 && src[i] == dst[i]) {
+            from[src[i]] = -1;
+            into[dst[i]] = -1;
+        }
+    }
+    std::vector<uint8_t> done(n, 0);
+    std::vector<uint32_t> chain;
+    auto emit = [&](bool cycle) {
+        const uint32_t k = static_cast<uint32_t>(chain.size());
+        for (uint32_t g0 = 0; g0 < k; g0 += kChainSeg) {
+            ChainSeg sg{};
+            sg.len = std::min<uint32_t>(kChainSeg, k - g0);
+            for (uint32_t j = 0; j < sg.len; ++j) {
+                const uint32_t m = chain[g0 + j];
+                sg.slot[j] = src[m];
+                sg.slot[j + 1] = dst[m];
+                sg.nt[j] = n_tokens ? n_tokens[m] : T;
+            }
+            sg.saved = -1;
+            if (g0 > 0 || cycle) {
+                sg.saved = static_cast<int32_t>(saved.size());
+                saved.push_back(sg.slot[0]);
+            }
+            segs.push_back(sg);
+        }
+    };
+    for (uint32_t i : keep) {  // chains start at a source no move writes
+        if (into[src[i]] >= 0) {
+            continue;
+        }
+        chain.clear();
+        for (int32_t m = static_cast<int32_t>(i); m >= 0; m = from[dst[m]]) {
+            chain.push_back(static_cast<uint32_t>(m));
+            done[m] = 1;
+        }
+        emit(false);
+    }
+    for (uint32_t i : keep) {  // what is left are cycles
+        if (done[i]) {
+            continue;
+        }
+        chain.clear();
+        for (int32_t m = static_cast<int32_t>(i); !done[m]; m = from[dst[m]]) {
+            chain.push_back(static_cast<uint32_t>(m));
+            done[m] = 1;
+        }
+        emit(true);
+    }
+    return true;
+}
+
 bool load_stagein_kernels() {
     return load_kernel_object(&quant_scatter_kv_kernel<KVMEM_TYPE_Q8_0, KVMEM_TYPE_Q8_0, false, false>);
 }
@@ -1504,6 +1673,81 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
     }
     const uint64_t per_move = (kspan + vspan) * pool->n_layers;
     (void) hipSetDevice(ctx->device);
+    // distinct sources and destinations, 16-byte rows: chains, bytes moved once
+    std::vector<ChainSeg> segs;
+    std::vector<uint32_t> saved;
+    if (krow % 16 == 0 && vrow % 16 == 0 &&
+        build_chains(src_slots, dst_slots, n_tokens, n, pool->block_tokens, pool->n_slots, segs, saved) &&
+        segs.size() <= 65535) {
+        if (segs.empty()) {
+            return KVMEM_HIP_OK;
+        }
+        if (!saved.empty() && !ensure_dev(ctx, ctx->move_scratch, per_move * saved.size(), "move_slots scratch")) {
+            return KVMEM_HIP_ERR_NOMEM;
+        }
+        uint8_t *scratch = static_cast<uint8_t *>(ctx->move_scratch.ptr);
+        std::vector<CopyOpDev> ops;
+        for (size_t e = 0; e < saved.size(); ++e) {
+            uint8_t *sc = scratch + per_move * e;
+            for (uint32_t l = 0; l < pool->n_layers; ++l) {
+                ops.push_back({static_cast<const uint8_t *>(pool->k_layers[l]) + saved[e] * kspan, sc, kspan});
+                sc += kspan;
+                if (want_v) {
+                    ops.push_back({static_cast<const uint8_t *>(pool->v_layers[l]) + saved[e] * vspan, sc, vspan});
+                    sc += vspan;
+                }
+            }
+        }
+        // one upload: the K and V layer tables, then the segments
+        const uint32_t L = pool->n_layers;
+        const size_t ptr_bytes = 2 * L * sizeof(void *);
+        std::vector<uint8_t> table(ptr_bytes + segs.size() * sizeof(ChainSeg));
+        std::memcpy(table.data(), pool->k_layers, L * sizeof(void *));
+        if (want_v) {
+            std::memcpy(table.data() + L * sizeof(void *), pool->v_layers, L * sizeof(void *));
+        }
+        std::memcpy(table.data() + ptr_bytes, segs.data(), segs.size() * sizeof(ChainSeg));
+        uint8_t *tdev = static_cast<uint8_t *>(upload(ctx, table.data(), table.size(), "move_slots chains"));
+        if (!tdev) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        uint64_t moved = 0;
+        for (const ChainSeg &sg : segs) {
+            for (uint32_t j = 0; j < sg.len; ++j) {
+                moved += static_cast<uint64_t>(sg.nt[j]) * (krow + vrow) * L;
+            }
+        }
+        ChainParams cp{};
+        cp.k_layers = reinterpret_cast<uint8_t *const *>(tdev);
+        cp.v_layers = want_v ? cp.k_layers + L : nullptr;
+        cp.segs = reinterpret_cast<const ChainSeg *>(tdev + ptr_bytes);
+        cp.scratch = scratch;
+        cp.kspan = kspan;
+        cp.vspan = vspan;
+        cp.entry_bytes = per_move;
+        cp.krow16 = static_cast<uint32_t>(krow / 16);
+        cp.vrow16 = static_cast<uint32_t>(vrow / 16);
+        cp.L = L;
+        cp.T = pool->block_tokens;
+        cp.vec_per_layer = cp.T * (cp.krow16 + cp.vrow16);
+        const uint64_t nvec = static_cast<uint64_t>(L) * cp.vec_per_layer;
+        if (nvec > 0x7fffffffu) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "move_slots: slot too large");
+        }
+        const CopyOpDev *dops = ops.empty() ? nullptr : upload_copy_ops(ctx, ops, "move_slots save");
+        if (!ops.empty() && !dops) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        perf_begin(ctx, kPerfLayout);
+        if (!launch_uploaded_copies(ctx, dops, ops.size(), "move_slots save")) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        const dim3 grid(static_cast<uint32_t>((nvec + 255) / 256), static_cast<uint32_t>(segs.size()));
+        move_chain_kernel<<<grid, 256, 0, ctx->stream>>>(cp);
+        perf_end(ctx, kPerfLayout);
+        ctx->d2d_bytes += per_move * saved.size() + moved;
+        return hip_ok(ctx, hipGetLastError(), "move_slots chain launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
+    }
     if (!ensure_dev(ctx, ctx->move_scratch, per_move * n, "move_slots scratch")) {
         return KVMEM_HIP_ERR_NOMEM;
     }

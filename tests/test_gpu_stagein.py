@@ -219,6 +219,57 @@ def test_move_slots_overlapping(ctx):
             assert np.array_equal(got, want)
 
 
+def move_case(case: str, n_slots: int, rng):
+    """(src, dst) slot lists: long chains, cycles, or a set with a shared
+    source (which takes the gather/scatter path)."""
+    perm = rng.permutation(n_slots).tolist()
+    if case == "chains":      # one chain of 39 moves (five segments) and two short ones
+        chain = [(perm[i], perm[i + 1]) for i in range(39)]
+        chain += [(perm[41], perm[42]), (perm[42], perm[43]), (perm[45], perm[46])]
+        return [a for a, _ in chain], [b for _, b in chain]
+    if case == "cycles":      # cycles of 20, 3 and 2, and two self-moves
+        moves = [(perm[i], perm[(i + 1) % 20]) for i in range(20)]
+        moves += [(perm[20 + i], perm[20 + (i + 1) % 3]) for i in range(3)]
+        moves += [(perm[23], perm[24]), (perm[24], perm[23]), (perm[30], perm[30]), (perm[31], perm[31])]
+        order = rng.permutation(len(moves))
+        return [moves[i][0] for i in order], [moves[i][1] for i in order]
+    src = perm[:12] + [perm[0]]            # slot perm[0] copied to two places
+    dst = perm[12:24] + [perm[40]]
+    return src, dst
+
+
+@pytest.mark.parametrize("case", ["chains", "cycles", "shared_source"])
+def test_move_slots_chains_and_cycles(ctx, case):
+    """Slot moves equal gathering every source first and scattering in
+    order, for chains longer than one segment, cycles, self-moves and
+    partial token counts (K q8_0 and V q4_0 rows of different widths)."""
+    announce(f"move_slots {case}")
+    L, n_slots, T, E = 3, 64, 16, 256
+    rng = np.random.default_rng({"chains": 1, "cycles": 2, "shared_source": 3}[case])
+    tk, tv = kv.TYPE_Q8_0, kv.TYPE_Q4_0
+    rk, rv = kv.row_size(tk, E), kv.row_size(tv, E)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    pk = [torch.randint(0, 256, (n_slots * T * rk,), dtype=torch.uint8, device="cuda", generator=g)
+          for _ in range(L)]
+    pv = [torch.randint(0, 256, (n_slots * T * rv,), dtype=torch.uint8, device="cuda", generator=g)
+          for _ in range(L)]
+    pool = ctx.make_pool(L, n_slots, T, E, E, tk, tv, [p.data_ptr() for p in pk], [p.data_ptr() for p in pv])
+    src, dst = move_case(case, n_slots, rng)
+    ntok = [int(x) for x in rng.integers(0, T + 1, len(src))]
+    ntok[:3] = [T, T, 0]
+    before = [(p.cpu().numpy().reshape(n_slots, T, -1).copy()) for p in pk + pv]
+    torch.cuda.synchronize()
+    ctx.move_slots(pool, src, dst, ntok)
+    ctx.sync()
+    for b, p in zip(before, pk + pv):
+        want = b.copy()
+        gathered = [b[s_, :nt].copy() for s_, nt in zip(src, ntok)]
+        for d, nt, rows in zip(dst, ntok, gathered):
+            want[d, :nt] = rows
+        assert np.array_equal(p.cpu().numpy().reshape(n_slots, T, -1), want)
+
+
 def test_scale_shortcuts_exhaustive(ctx):
     """The quantizers' division-free scale arithmetic equals the IEEE
     quotients over every float of its range, on this device."""
