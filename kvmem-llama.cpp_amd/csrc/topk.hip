@@ -287,6 +287,9 @@ extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t 
     ctx->topk_epoch = ctx->topk_epoch + 1 == 0 ? 1 : ctx->topk_epoch + 1;
     const uint32_t epoch = ctx->topk_epoch;
     uint32_t *out = static_cast<uint32_t *>(out_dev);
+    // pinned memory comes uninitialised: clear the word before the kernel
+    // can set it (the previous call's write has landed; it was waited for)
+    __atomic_store_n(h + flag, 0u, __ATOMIC_RELEASE);
     perf_begin(ctx, kPerfTopk);
     topk_kernel<<<1, kTopkThreads, 0, ctx->stream>>>(scores, n, forced_dev, inl,
                                                      static_cast<uint32_t>(uniq.size()), need,
