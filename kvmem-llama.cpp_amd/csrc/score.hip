@@ -12,7 +12,8 @@
 // CU, so each SIMD runs two waves that cover each other's barrier and
 // load waits.  Each wave keeps 96 query rows resident in VGPRs as f16
 // A-fragments of v_mfma_f32_16x16x32_f16 (loaded once; bf16 queries are
-// converted to f16 on the way, exact for normal-range values), so every
+// converted to f16 on the way, exact for normal-range values, a wave's rows
+// scaled by a power of two first when they would overflow f16), so every
 // 16-byte B-fragment read from LDS feeds six MFMAs (two reads kept in
 // flight ahead of their MFMAs).  Half a block's K tile
 // (64 keys x head_dim halves of one KV head, 32 KiB) moves HBM -> LDS with
@@ -95,12 +96,37 @@ __device__ inline float wave_max(float m) {
     return __builtin_fmaxf(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
 }
 
-__device__ inline _Float16 q_elem_to_half(uint16_t bits, bool bf16) {
-    if (bf16) {
-        const float f = __uint_as_float(static_cast<uint32_t>(bits) << 16);
-        return static_cast<_Float16>(f);
+// A bf16 value (its bits in the top half of `f32_bits`, the rest zero) ->
+// f16, times qscale (a power of two, exact) before the rounding.
+__device__ inline _Float16 bf16_to_half(uint32_t f32_bits, float qscale) {
+    return static_cast<_Float16>(__uint_as_float(f32_bits) * qscale);
+}
+
+// A wave's query rows as raw 16-bit A fragments (bf16 or f16 bits, not yet
+// converted).  Returns the largest |q| bit pattern the lane loaded.
+template <int D, int KS>
+__device__ __forceinline__ uint32_t load_query_bits(const ScoreParams &p, half8_t (&a)[kRowTiles][KS],
+                                                    uint32_t l, uint32_t h, uint32_t rg, uint32_t wave,
+                                                    uint32_t lrow, uint32_t kgrp) {
+    uint32_t mx = 0;
+#pragma unroll
+    for (int rt = 0; rt < kRowTiles; ++rt) {
+        uint32_t r = rg * kRowsPerGroup + wave * kRowsPerWave + rt * 16 + lrow;
+        r = min(r, p.R - 1u);                       // duplicate the last valid row
+        const uint32_t t = r / p.g;
+        const uint32_t hq = h * p.g + (r - t * p.g);
+        const uint16_t *qrow = p.q + ((static_cast<uint64_t>(l) * p.Tq + t) * p.Hq + hq) * D;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const u32x4_t w = *reinterpret_cast<const u32x4_t *>(qrow + ks * 32 + kgrp * 8);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                mx = max(mx, max(w[i] & 0x7fffu, (w[i] >> 16) & 0x7fffu));
+            }
+            a[rt][ks] = __builtin_bit_cast(half8_t, w);
+        }
     }
-    return __builtin_bit_cast(_Float16, bits);
+    return mx;
 }
 
 template <int D>
@@ -206,28 +232,36 @@ __global__ __launch_bounds__(kScoreThreads, 2) void score_kernel(ScoreParams p) 
 
     issue_tile(0u, 0);
 
-    // ---- query rows -> A fragments (resident for the whole workgroup)
+    // ---- query rows -> A fragments (resident for the whole workgroup).  The
+    // raw bits are loaded first; bf16 rows are then converted to f16 in
+    // place.  A bf16 value past f16's range (|q| >= 65536, bf16 exponent
+    // >= 143) would turn infinite, so the wave's rows are converted times
+    // 2^-qexp, which brings its largest |q| below 65536, and its maxima are
+    // scaled back on the way out.  Both scalings are exact (qexp is 0 for
+    // rows in range), so scores do not change.
     half8_t a[kRowTiles][KS];
+    const uint32_t qmax = load_query_bits<D, KS>(p, a, l, h, rg, wave, lrow, kgrp);
+    int qexp = 0;
+    if (p.q_bf16 != 0) {
+        const uint32_t e = static_cast<uint32_t>(wave_max(static_cast<float>(qmax))) >> 7;
+        qexp = (e > 142u && e < 255u) ? static_cast<int>(e) - 142 : 0;
+        const float qscale = __builtin_ldexpf(1.0f, -qexp);
 #pragma unroll
-    for (int rt = 0; rt < kRowTiles; ++rt) {
-        uint32_t r = rg * kRowsPerGroup + wave * kRowsPerWave + rt * 16 + lrow;
-        r = min(r, p.R - 1u);                       // duplicate the last valid row
-        const uint32_t t = r / p.g;
-        const uint32_t hq = h * p.g + (r - t * p.g);
-        const uint16_t *qrow = p.q + ((static_cast<uint64_t>(l) * p.Tq + t) * p.Hq + hq) * D;
+        for (int rt = 0; rt < kRowTiles; ++rt) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const uint4 raw = *reinterpret_cast<const uint4 *>(qrow + ks * 32 + kgrp * 8);
-            const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-            half8_t v;
+            for (int ks = 0; ks < KS; ++ks) {
+                const u32x4_t w = __builtin_bit_cast(u32x4_t, a[rt][ks]);
+                half8_t v;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                v[2 * i] = q_elem_to_half(static_cast<uint16_t>(w[i] & 0xffffu), p.q_bf16 != 0);
-                v[2 * i + 1] = q_elem_to_half(static_cast<uint16_t>(w[i] >> 16), p.q_bf16 != 0);
+                for (int i = 0; i < 4; ++i) {  // two bf16 per word, the low one first
+                    v[2 * i] = bf16_to_half(w[i] << 16, qscale);
+                    v[2 * i + 1] = bf16_to_half(w[i] & 0xffff0000u, qscale);
+                }
+                a[rt][ks] = v;
             }
-            a[rt][ks] = v;
         }
     }
+    const float out_scale = __builtin_ldexpf(p.scale, qexp);
 
     // LDS byte address of B fragment (kt, ks) in buffer buf, i.e. of the
     // swizzled chunk (ks*4 + kgrp) ^ (key mod CH) of key kt*16 + lrow:
@@ -310,7 +344,7 @@ __global__ __launch_bounds__(kScoreThreads, 2) void score_kernel(ScoreParams p) 
         if (it & 1u) {  // both halves of the block are in m
             m = wave_max(m);
             if (lane == 0) {
-                out[b_begin + (it >> 1)] = m * p.scale;
+                out[b_begin + (it >> 1)] = m * out_scale;
             }
             m = -FLT_MAX;
         }

@@ -98,6 +98,26 @@ def test_score_fold_many_layers_exact(ctx, oracle, mode):
     assert_close(ls[:, :2], want, "layer scores")
 
 
+def test_score_bf16_query_past_f16_range(ctx, oracle):
+    """bf16 query values beyond f16's range (|q| >= 65536) in a few rows: the
+    waves holding them convert their rows scaled by a power of two and scale
+    their maxima back, so scores stay finite and match the oracle; waves
+    without them are untouched."""
+    announce("bf16 query rows past f16 range")
+    L, B, Tq = 2, 7, 16
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=Tq, seed=41)
+    qf = q.float()
+    g = torch.Generator(device="cuda").manual_seed(42)
+    qf[0, 3, 5] = 3.0e5 * torch.sign(torch.randn(256, device="cuda", generator=g))  # a whole row
+    qf[1, 10, 17, 7] = -2.0e6                                                           # one element
+    q = qf.to(torch.bfloat16)
+    s, ls = run_score(ctx, k, q, kv.TYPE_BF16, 24, 4, 256)
+    assert np.isfinite(s).all() and np.isfinite(ls).all()
+    want_ls = oracle.score_pertoken_max(q_f32(q), workloads.to_bits(torch, k))
+    assert_close(ls, want_ls, "layer scores")
+    assert ls.max() > 1e4  # the large rows decide some blocks' scores
+
+
 def test_score_invariants(ctx):
     """Permuting tokens inside a block and query heads inside a GQA group
     leaves scores unchanged; scaling Q by 2 scales them by 2."""
