@@ -391,7 +391,11 @@ KVMEM_HIP_API int kvmem_hip_score(kvmem_hip_ctx *ctx,
  * first as kvmem_store.cpp:602-609), and write the union in ascending id
  * order to sel_out (host array, capacity n_forced + need); *n_sel receives
  * its length.  Replaces the nth_element fill of pick_topk_ungrouped
- * (kvmem_store.cpp:594-622).  Synchronises the context stream.  n <= 16384. */
+ * (kvmem_store.cpp:594-622).  Returns once the selection is on the host:
+ * the kernel writes it to the context's coherent pinned buffer and sets a
+ * completion word there, on which the calling thread spins (work queued
+ * earlier on the context stream, e.g. the scorer, completes first).
+ * n <= 16384. */
 KVMEM_HIP_API int kvmem_hip_topk(kvmem_hip_ctx *ctx,
                                  const float *scores, uint32_t n,
                                  const uint32_t *forced, uint32_t n_forced,
