@@ -123,12 +123,16 @@ def test_engine_stale_selection():
         eng.apply(fresh)
 
 
-def test_engine_canonical_layout(oracle):
-    announce("canonical layout: selected block i in slot i")
+@pytest.mark.parametrize("budget,reserve", [(10, 4), (24, 8)])
+def test_engine_canonical_layout(oracle, budget, reserve):
+    """Selected block i in slot i after each reselection; with 24 of 30
+    blocks selected the resident blocks' moves form chains longer than one
+    segment of the chain walk."""
+    announce(f"canonical layout: selected block i in slot i (budget {budget})")
     cap, nb = 32, 30
     k, v, q1 = history(cap, seed=9)
     q2 = (q1.float() * -1.0).to(torch.bfloat16)
-    with make_engine(10, 4, canonical_layout=1) as eng:
+    with make_engine(budget, reserve, canonical_layout=1) as eng:
         eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
         for q in (q1, q2, q1):
             sel = eng.preview(q.data_ptr(), q.shape[1])
