@@ -175,6 +175,41 @@ def test_stagein_ops_strided_mixed_types(ctx, oracle):
         assert np.array_equal(got, w), first_diff(got, w)
 
 
+def test_stagein_full_256k_sampled(ctx, oracle):
+    """The benchmark's stage-in at full size: 77 random blocks of the 16-layer
+    x 2048-block history (16 GiB of F16 K and V on the device) into random
+    slots of a 384-slot q8_0 pool, one launch.  Eight sampled blocks are
+    checked bit for bit against the oracle quantizer in every layer, K and
+    V; every other staged block's rows must have been written (the pool
+    starts as a sentinel no q8_0 row of these values can equal)."""
+    announce("full-size stage-in: 77 of 2048 blocks x 16 layers, K/V q8_0 -> 384 slots")
+    L, B, T, E, n_slots = 16, 2048, 128, 1024, 384
+    k, v, _ = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=1, seed=12, with_v=True)
+    rng = np.random.default_rng(13)
+    ids = sorted(rng.choice(B, 77, replace=False).tolist())
+    slots = rng.permutation(n_slots)[:77].tolist()
+    rb = kv.row_size(kv.TYPE_Q8_0, E)
+    pk = [torch.full((n_slots * T * rb,), 0xFF, dtype=torch.uint8, device="cuda") for _ in range(L)]
+    pv = [torch.full((n_slots * T * rb,), 0xFF, dtype=torch.uint8, device="cuda") for _ in range(L)]
+    hist = ctx.make_history(k.data_ptr(), v.data_ptr(), L, B, T, E, E)
+    pool = ctx.make_pool(L, n_slots, T, E, E, kv.TYPE_Q8_0, kv.TYPE_Q8_0, [p.data_ptr() for p in pk],
+                         [p.data_ptr() for p in pv])
+    torch.cuda.synchronize()
+    ctx.stagein_blocks(hist, pool, ids, slots)
+    ctx.sync()
+    sample = set(rng.choice(77, 8, replace=False).tolist())
+    for l in range(L):
+        for src, p in ((k, pk[l]), (v, pv[l])):
+            got = p.cpu().numpy().reshape(n_slots, T, rb)
+            for i, (b, s_) in enumerate(zip(ids, slots)):
+                if i in sample:
+                    rows = src[l, b].reshape(T, E).cpu().view(torch.int16).numpy().view(np.uint16)
+                    assert np.array_equal(got[s_], oracle.quantize_rows_f16(kv.TYPE_Q8_0, rows)), (l, b)
+                else:
+                    assert not (got[s_] == 0xFF).all(axis=1).any(), (l, b)
+    del k, v
+
+
 def test_stagein_rejects_bad_arguments(ctx):
     announce("argument validation")
     a = torch.zeros(4096, dtype=torch.uint8, device="cuda")
