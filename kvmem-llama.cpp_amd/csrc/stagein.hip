@@ -184,10 +184,10 @@ struct BlockSource {
 
 // Quad exchange through DPP: lane i of each 4-lane quad reads lane i^1 / i^2.
 __device__ inline uint32_t quad_xor1(uint32_t v) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false));
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xB1, 0xF, 0xF, true));
 }
 __device__ inline uint32_t quad_xor2(uint32_t v) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false));
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x4E, 0xF, 0xF, true));
 }
 
 __device__ inline float half_bits_to_float(uint32_t h) {
@@ -457,13 +457,13 @@ __device__ inline float lane_xor(float v) {
     const int x = __float_as_int(v);
     int r;
     if constexpr (M == 1) {
-        r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
+        r = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true);
     } else if constexpr (M == 2) {
-        r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);
+        r = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);
     } else if constexpr (M == 4) {
         r = __builtin_amdgcn_ds_swizzle(x, 0x1F | (4 << 10));
     } else if constexpr (M == 8) {
-        r = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);  // row_ror:8
+        r = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true);  // row_ror:8
     } else if constexpr (M == 16) {
         r = __builtin_amdgcn_ds_swizzle(x, 0x1F | (16 << 10));
     } else {
