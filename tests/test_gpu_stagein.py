@@ -273,13 +273,16 @@ def move_case(case: str, n_slots: int, rng):
     return src, dst
 
 
+@pytest.mark.parametrize("E", [256, 32])
 @pytest.mark.parametrize("case", ["chains", "cycles", "shared_source"])
-def test_move_slots_chains_and_cycles(ctx, case):
+def test_move_slots_chains_and_cycles(ctx, case, E):
     """Slot moves equal gathering every source first and scattering in
     order, for chains longer than one segment, cycles, self-moves and
-    partial token counts (K q8_0 and V q4_0 rows of different widths)."""
-    announce(f"move_slots {case}")
-    L, n_slots, T, E = 3, 64, 16, 256
+    partial token counts (K q8_0 and V q4_0 rows of different widths; at
+    n_embd 32 the rows are 34 and 18 bytes, which takes the gather/scatter
+    path even for chains)."""
+    announce(f"move_slots {case}, n_embd {E}")
+    L, n_slots, T = 3, 64, 16
     rng = np.random.default_rng({"chains": 1, "cycles": 2, "shared_source": 3}[case])
     tk, tv = kv.TYPE_Q8_0, kv.TYPE_Q4_0
     rk, rv = kv.row_size(tk, E), kv.row_size(tv, E)
