@@ -285,3 +285,51 @@ def test_q8_scale_division_shortcut_exhaustive(oracle):
     that equals the IEEE quotient.  The reciprocal shortcut depends on the
     device's rcp and is checked on the GPU (test_gpu_stagein)."""
     assert oracle.lib().ko_div127_mismatches(0x00000000, 0x7F800000) == 0
+
+
+# ------------------------------------------------ q5_0 byte layout, literal
+from q5_literals import ggml_q5_0_decode_codes, q5_literal_failures  # noqa: E402
+
+
+def test_q5_0_literal_bytes(oracle):
+    assert q5_literal_failures(lambda r: oracle.quantize_rows_f16(Q5, r)) == []
+
+
+def test_q5_0_literal_checks_reject_planted_layouts(oracle):
+    """Plausible q5_0 layout mistakes, planted in the oracle's output, fail
+    the literal checks: qh stored big-endian, element j's bit 4 stored at
+    qh bit j + 16 (halves swapped), and the nibbles of qs swapped."""
+    def planted(mutate):
+        return lambda r: np.stack([mutate(bytearray(b.tobytes())) for b in
+                                   oracle.quantize_rows_f16(Q5, r)])
+
+    def qh_big_endian(b):
+        b[2:6] = b[2:6][::-1]
+        return np.frombuffer(bytes(b), np.uint8)
+
+    def qh_halves_swapped(b):
+        qh = int.from_bytes(b[2:6], "little")
+        b[2:6] = (((qh & 0xFFFF) << 16) | (qh >> 16)).to_bytes(4, "little")
+        return np.frombuffer(bytes(b), np.uint8)
+
+    def qs_nibbles_swapped(b):
+        for j in range(16):
+            b[6 + j] = ((b[6 + j] & 15) << 4) | (b[6 + j] >> 4)
+        return np.frombuffer(bytes(b), np.uint8)
+
+    for mutate in (qh_big_endian, qh_halves_swapped, qs_nibbles_swapped):
+        assert q5_literal_failures(planted(mutate)), mutate.__name__
+
+
+def test_q5_0_dequantizer_statement_round_trips_random_codes(oracle):
+    """Random groups of exact codes (d = 1 set by a -16 at a random first
+    position) round-trip through the published dequantizer bit for bit."""
+    rng = np.random.default_rng(21)
+    for _ in range(200):
+        pos = int(rng.integers(0, 32))
+        codes = rng.integers(-15, 16, 32)        # -15..15, so -16 at pos is the first max
+        codes[pos] = -16
+        g = codes.astype(np.float32)
+        blk = bytes(oracle.quantize_rows_f16(Q5, groups_f16(g))[0].tobytes())
+        assert blk[:2] == bytes([0x00, 0x3C])
+        assert ggml_q5_0_decode_codes(blk) == codes.tolist()

@@ -125,6 +125,9 @@ def special_rows(E: int = 1024) -> np.ndarray:
     g = (rng.standard_normal(32) * 1e-6).astype(np.float32); groups.append(g)        # tiny scale
     g = np.full(32, 0.75, np.float32); groups.append(g)                               # constant
     g = np.full(32, -1.0, np.float32); g[::2] = 1.0; groups.append(g)                 # +-1 alternating
+    groups.append(np.arange(-16, 16, dtype=np.float32))                               # every q5 code
+    g = np.full(32, -5.0, np.float32); g[0], g[3], g[20] = -16.0, 2.0, 7.0; groups.append(g)  # q5 qh bits 3, 20
+    g = np.zeros(32, np.float32); g[16], g[17], g[1] = 16.0, -15.0, -3.0; groups.append(g)    # q5 d < 0
     all_groups = [workloads.f16_bits(x) for x in groups] + gb_rows
     for i, gbits in enumerate(all_groups):
         r, c = divmod(i, E // 32)
@@ -148,6 +151,25 @@ def test_stagein_special_groups(ctx, oracle, type_):
     got = out.cpu().numpy().reshape(T, rb)
     want = oracle.quantize_rows_f16(type_, rows)
     assert np.array_equal(got, want), first_diff(got, want)
+
+
+def test_stagein_q5_0_literal_bytes(ctx):
+    """The kernel's q5_0 blocks equal literal bytes worked out from ggml's
+    published block_q5_0 layout and dequantizer (no oracle involved)."""
+    from q5_literals import q5_literal_failures
+    announce("q5_0 literal blocks (qh bit order, qs nibble pairing)")
+
+    def quantize(rows):
+        src = dev_bits(rows)
+        out = torch.full((rows.shape[0] * 22 * (rows.shape[1] // 32),), SENTINEL, dtype=torch.uint8,
+                         device="cuda")
+        torch.cuda.synchronize()
+        ctx.stagein_quant([(src.data_ptr(), out.data_ptr(), rows.shape[0], rows.shape[1],
+                            kv.TYPE_Q5_0)])
+        ctx.sync()
+        return out.cpu().numpy().reshape(rows.shape[0], -1)
+
+    assert q5_literal_failures(quantize) == []
 
 
 def test_stagein_ops_strided_mixed_types(ctx, oracle):
