@@ -675,6 +675,11 @@ def main() -> int:
            "scorer_sustained": run_scorer_sustained, "mfma_calibration": run_mfma_calibration}[a.workload]
     result = run(a, torch, kv, workloads)
     print(json.dumps(result), flush=True)
+    # every engine and context is released here, with the runtime fully up,
+    # not by finalizers during interpreter shutdown
+    torch.cuda.synchronize()
+    kv.close_all()
+    log("closed every engine and context")
     return 0
 
 

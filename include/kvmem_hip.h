@@ -482,6 +482,29 @@ KVMEM_HIP_API int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_mean
 KVMEM_HIP_API int kvmem_hip_check_scale_arith(kvmem_hip_ctx *ctx, uint64_t *div127_mismatches,
                                               uint64_t *recip_mismatches);
 
+/* ---------------------------------------------------- failure injection */
+
+/* Kinds of operation kvmem_hip_debug_fail_after can fail. */
+enum kvmem_hip_fail_kind {
+    KVMEM_HIP_FAIL_ALLOC = 1,  /* a device or pinned allocation */
+    KVMEM_HIP_FAIL_COPY = 2,   /* a host<->device copy (table uploads included) */
+    KVMEM_HIP_FAIL_LAUNCH = 4  /* a kernel launch */
+};
+
+/* Make the nth_op-th later operation of a kind in `kinds` (a mask of
+ * kvmem_hip_fail_kind) on this context fail before it is issued: the entry
+ * point that reaches it returns an error and kvmem_hip_last_error names
+ * it ("...: injected failure"); nothing is enqueued for that operation and
+ * injection then switches off.  nth_op = 0 or kinds = 0 switches it off.
+ * Host-side only, it never makes a kernel fault.  The reference's callers
+ * recover from a failed device call by falling back to host writes
+ * (llama-memory-kvmem.cpp:2752-2758, 993-998, 1094-1099); this is how such
+ * recovery is tested here.  No counterpart in the reference. */
+KVMEM_HIP_API int kvmem_hip_debug_fail_after(kvmem_hip_ctx *ctx, uint32_t kinds, uint64_t nth_op);
+/* Operations still to pass before the injected failure (0 = not armed:
+ * it fired, or was never set). */
+KVMEM_HIP_API uint64_t kvmem_hip_debug_fail_left(const kvmem_hip_ctx *ctx);
+
 /* ------------------------------------------------------------ profiling */
 
 /* Per-stage GPU time (hipEvent pairs on the context stream), the device

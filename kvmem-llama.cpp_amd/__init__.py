@@ -14,8 +14,11 @@ a call fails, an exception is raised.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
+import sys
+import weakref
 from pathlib import Path
 from typing import Iterable, Sequence
 
@@ -35,6 +38,9 @@ GROUP_BYTES = {TYPE_Q8_0: 34, TYPE_Q4_0: 18, TYPE_Q5_0: 22, TYPE_F16: 64}
 LAYER_MEAN, LAYER_MAX, LAYER_SUM = 0, 1, 2
 
 OK, ERR_INVALID, ERR_RUNTIME, ERR_NOMEM, ERR_STALE, ERR_UNSUPPORTED = range(6)
+
+# operation kinds of Context.debug_fail_after (kvmem_hip_fail_kind)
+FAIL_ALLOC, FAIL_COPY, FAIL_LAUNCH = 1, 2, 4
 
 
 def row_size(type_: int, n: int) -> int:
@@ -127,6 +133,32 @@ class Perf(C.Structure):
 
 _lib: C.CDLL | None = None
 
+# Every open handle (contexts, engines, stores).  They are closed at
+# interpreter exit by close_all(), an atexit hook, while the HIP runtime is
+# fully up; a finalizer running later, during interpreter shutdown, does
+# nothing (the process is ending and the runtime may already be tearing
+# down), so no HIP call is made from module teardown.
+_live: "weakref.WeakSet" = weakref.WeakSet()
+
+
+def track(obj) -> None:
+    """Register a handle owner (an object with close() and a _close_rank:
+    lower ranks close first) for close_all()."""
+    _live.add(obj)
+
+
+def close_all() -> None:
+    """Close every open engine, store and context: engines and stores
+    first (they destroy their own contexts), then stand-alone contexts."""
+    for obj in sorted(list(_live), key=lambda o: getattr(o, "_close_rank", 1)):
+        try:
+            obj.close()
+        except Exception:
+            pass
+
+
+atexit.register(close_all)
+
 
 def _sig(lib: C.CDLL, name: str, res, *args) -> None:
     f = getattr(lib, name)
@@ -173,6 +205,8 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_reserve", i32, vp, C.POINTER(ReserveArgs))
     _sig(lib, "kvmem_hip_scratch_info", i32, vp, C.POINTER(Scratch))
     _sig(lib, "kvmem_hip_h2d_async", i32, vp, vp, vp, sz)
+    _sig(lib, "kvmem_hip_debug_fail_after", i32, vp, u32, C.c_uint64)
+    _sig(lib, "kvmem_hip_debug_fail_left", C.c_uint64, vp)
     _sig(lib, "kvmem_hip_perf_enable", i32, vp, i32)
     _sig(lib, "kvmem_hip_perf_get", i32, vp, C.POINTER(Perf))
     _sig(lib, "kvmem_hip_perf_reset", None, vp)
@@ -201,6 +235,9 @@ class Context:
             raise KvMemError(rc, f"kvmem_hip_create(device={device}) failed")
         self.h = h
         self._keep: list = []
+        track(self)
+
+    _close_rank = 1
 
     @classmethod
     def borrow(cls, handle: int) -> "Context":
@@ -220,6 +257,8 @@ class Context:
             self.h = None
 
     def __del__(self):
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
@@ -407,6 +446,16 @@ class Context:
         a = MeanKArgs(q_sum_ptr, C.cast(qc, C.POINTER(C.c_uint32)), k_sum_ptr, mean_tokens_ptr,
                       n_layers, n_blocks, capacity_blocks, n_head, n_head_kv, head_dim, scores_ptr)
         self.check(self.lib.kvmem_hip_score_meank(self.h, C.byref(a)), "score_meank")
+
+    # -- failure injection (host side: nothing faults on the device)
+    def debug_fail_after(self, kinds: int, nth_op: int) -> None:
+        """The nth_op-th later operation of `kinds` (FAIL_* mask) fails before
+        it is issued; 0 switches injection off."""
+        self.check(self.lib.kvmem_hip_debug_fail_after(self.h, kinds, nth_op), "debug_fail_after")
+
+    def debug_fail_left(self) -> int:
+        """Operations left before the injected failure (0: fired or off)."""
+        return self.lib.kvmem_hip_debug_fail_left(self.h)
 
     # -- profiling
     def perf_enable(self, on: bool = True) -> None:

@@ -27,9 +27,26 @@ bool hip_ok(kvmem_hip_ctx *ctx, hipError_t e, const char *what) {
     return false;
 }
 
+bool injected_fail(kvmem_hip_ctx *ctx, uint32_t kind, const char *what) {
+    if (!ctx || !(ctx->fail_kinds & kind)) {
+        return false;
+    }
+    if (ctx->fail_countdown > 1) {
+        --ctx->fail_countdown;
+        return false;
+    }
+    ctx->fail_kinds = 0;
+    ctx->fail_countdown = 0;
+    ctx->last_error = std::string(what) + ": injected failure";
+    return true;
+}
+
 bool ensure_dev(kvmem_hip_ctx *ctx, DevBuf &b, size_t bytes, const char *what) {
     if (b.ptr && b.bytes >= bytes) {
         return true;
+    }
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_ALLOC, what)) {
+        return false;
     }
     if (b.ptr) {
         // the old buffer may still be read by enqueued work
@@ -53,6 +70,9 @@ bool ensure_dev(kvmem_hip_ctx *ctx, DevBuf &b, size_t bytes, const char *what) {
 bool ensure_pin(kvmem_hip_ctx *ctx, PinBuf &b, size_t bytes, const char *what, unsigned flags) {
     if (b.ptr && b.bytes >= bytes) {
         return true;
+    }
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_ALLOC, what)) {
+        return false;
     }
     if (b.ptr) {
         if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), what)) {
@@ -86,6 +106,9 @@ void *upload(kvmem_hip_ctx *ctx, const void *src, size_t bytes, const char *what
         return nullptr;
     }
     if (!s.done && !hip_ok(ctx, hipEventCreateWithFlags(&s.done, hipEventDisableTiming), what)) {
+        return nullptr;
+    }
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_COPY, what)) {
         return nullptr;
     }
     std::memcpy(s.host.ptr, src, bytes);
@@ -199,6 +222,9 @@ bool launch_uploaded_copies(kvmem_hip_ctx *ctx, const CopyOpDev *dops, size_t n,
     }
     // ~2048 workgroups fill the chip (256 CUs x 8); at most 8 pieces per op
     const int pieces = static_cast<int>(std::min<size_t>(8, std::max<size_t>(1, 2048 / n)));
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, what)) {
+        return false;
+    }
     batched_copy_kernel<<<static_cast<uint32_t>(n * pieces), 256, 0, ctx->stream>>>(
         dops, static_cast<int>(n), pieces);
     return hip_ok(ctx, hipGetLastError(), what);
@@ -480,6 +506,9 @@ int kvmem_hip_h2d_async(kvmem_hip_ctx *ctx, void *dst, const void *src, size_t n
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "h2d_async: null pointer");
     }
     (void) hipSetDevice(ctx->device);
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_COPY, "h2d_async")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
     perf_begin(ctx, kPerfCopy);
     const bool ok = hip_ok(ctx, hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, ctx->stream),
                            "h2d_async");
@@ -536,6 +565,23 @@ int kvmem_hip_d2d_batched(kvmem_hip_ctx *ctx, const void *const *src, void *cons
     }
     ctx->d2d_bytes += total;
     return KVMEM_HIP_OK;
+}
+
+int kvmem_hip_debug_fail_after(kvmem_hip_ctx *ctx, uint32_t kinds, uint64_t nth_op) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    const uint32_t all = KVMEM_HIP_FAIL_ALLOC | KVMEM_HIP_FAIL_COPY | KVMEM_HIP_FAIL_LAUNCH;
+    if (kinds & ~all) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "debug_fail_after: unknown operation kind");
+    }
+    ctx->fail_kinds = nth_op ? kinds : 0u;
+    ctx->fail_countdown = kinds ? nth_op : 0u;
+    return KVMEM_HIP_OK;
+}
+
+uint64_t kvmem_hip_debug_fail_left(const kvmem_hip_ctx *ctx) {
+    return ctx && ctx->fail_kinds ? ctx->fail_countdown : 0u;
 }
 
 int kvmem_hip_perf_enable(kvmem_hip_ctx *ctx, int on) {

@@ -86,6 +86,12 @@ struct kvmem_hip_ctx {
     uint64_t h2d_bytes = 0;
     uint64_t d2d_bytes = 0;
     uint64_t n_allocs = 0;  // device + pinned allocations since creation
+
+    // Host-side failure injection (kvmem_hip_debug_fail_after): the
+    // fail_countdown-th operation of a kind in fail_kinds fails before it
+    // is issued.
+    uint32_t fail_kinds = 0;
+    uint64_t fail_countdown = 0;
 };
 
 namespace kvmem_hip {
@@ -94,6 +100,12 @@ namespace kvmem_hip {
 int fail(kvmem_hip_ctx *ctx, int code, const std::string &msg);
 // Check a HIP call; on failure record "<what>: <hip error string>".
 bool hip_ok(kvmem_hip_ctx *ctx, hipError_t e, const char *what);
+
+// True when this operation (an allocation, a host<->device copy or a
+// kernel launch; kvmem_hip_fail_kind) is the one kvmem_hip_debug_fail_after
+// chose to fail: the error is recorded and the caller returns before
+// issuing anything.
+bool injected_fail(kvmem_hip_ctx *ctx, uint32_t kind, const char *what);
 
 bool ensure_dev(kvmem_hip_ctx *ctx, DevBuf &b, size_t bytes, const char *what);
 bool ensure_pin(kvmem_hip_ctx *ctx, PinBuf &b, size_t bytes, const char *what,

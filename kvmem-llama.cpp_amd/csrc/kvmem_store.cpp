@@ -267,6 +267,12 @@ void KvMemStore::clear_working_set() {
     }
 }
 
+void KvMemStore::drop_from_working_set(uint32_t id) {
+    if (id < block_count()) {
+        blocks_[id].in_working_set = false;
+    }
+}
+
 // ------------------------------------------------------------ slot pool
 
 SlotPool::SlotPool(uint32_t n_slots) : n_slots_(n_slots) {

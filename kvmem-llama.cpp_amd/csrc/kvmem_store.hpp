@@ -131,6 +131,9 @@ public:
     bool commit_resident_selection(const std::vector<uint32_t> &selected_ids);
     // kvmem_store.cpp:897-901.
     void clear_working_set();
+    // One block leaves the window (its pool rows can no longer be trusted);
+    // the next selection that keeps it stages it in again.
+    void drop_from_working_set(uint32_t id);
 
 private:
     StoreConfig cfg_;

@@ -352,6 +352,9 @@ int kvmem_hip_meank_sums(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
     if (!items) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "meank_sums launch")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
     meank_sum_kernel<<<static_cast<uint32_t>(jobs), E / 8, 0, ctx->stream>>>(
         static_cast<const uint8_t *>(hist->k), static_cast<const uint32_t *>(items), hist->n_layers,
         cap, hist->block_tokens, E, hist->n_blocks - 1, hist->last_block_tokens, k_sum, mean_tokens);
@@ -484,6 +487,9 @@ int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {
     const float *invq_dev = static_cast<const float *>(upload(ctx, invq.data(), sizeof(float) * L,
                                                               "score_meank invq"));
     if (!invq_dev) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "score_meank launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     perf_begin(ctx, kPerfScore);

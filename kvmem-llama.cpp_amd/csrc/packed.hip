@@ -203,6 +203,9 @@ int kvmem_hip_stageout_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool,
                 while (j + run < cnt && n_tokens[i + run] == T && block_ids[i + run] == block_ids[i] + run) {
                     ++run;
                 }
+                if (injected_fail(ctx, KVMEM_HIP_FAIL_COPY, "d2h block copy")) {
+                    return KVMEM_HIP_ERR_RUNTIME;
+                }
                 if (!hip_ok(ctx, hipMemcpyAsync(hb, db, run * g.span, hipMemcpyDeviceToHost, ctx->copy_stream),
                             "d2h block copy")) {
                     return KVMEM_HIP_ERR_RUNTIME;
@@ -298,6 +301,9 @@ int kvmem_hip_stagein_packed_host(kvmem_hip_ctx *ctx, const kvmem_hip_packed_hos
             uint32_t run = 1;
             while (j + run < cnt && block_ids[first + j + run] == b + run) {
                 ++run;
+            }
+            if (injected_fail(ctx, KVMEM_HIP_FAIL_COPY, "h2d packed block copy")) {
+                return KVMEM_HIP_ERR_RUNTIME;
             }
             if (!hip_ok(ctx, hipMemcpyAsync(slot_base + j * g.span, host + static_cast<uint64_t>(b) * g.span,
                                             run * g.span, hipMemcpyHostToDevice, ctx->copy_stream),

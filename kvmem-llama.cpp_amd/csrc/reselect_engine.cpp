@@ -74,6 +74,19 @@ void fill_stats(const Plan &p, uint32_t n_staged, uint32_t n_moved, uint32_t n_s
     st->total_window_tokens = p.total_window_tokens;
 }
 
+// admit_incoming gives a block no slot when the free list is empty
+// (alloc_gpu_slot returns -1, kvmem_runtime.cpp:294-328): such a plan
+// cannot be applied.
+bool every_stage_in_has_slot(const KvMemRuntime &rt, const Plan &p) {
+    for (uint32_t id : p.stage_in) {
+        const Block &b = rt.store().blocks()[id];
+        if (b.tier != Tier::GPU || b.gpu_slot < 0) {
+            return false;
+        }
+    }
+    return true;
+}
+
 StoreConfig store_config(uint32_t block_tokens, uint32_t budget_blocks, uint32_t sink,
                          uint32_t recent, bool tie_lower) {
     StoreConfig c;
@@ -170,8 +183,16 @@ int kvmem_store_apply(kvmem_store *s, const uint32_t *sel, uint32_t n_sel, uint3
     }
     s->slots.staged_ids.clear();
     s->slots.staged_slots.clear();
+    const KvMemRuntime rt_before = s->rt;
+    const RecordingSlots slots_before = s->slots;
     const Plan p = s->rt.prepare_selection(std::vector<uint32_t>(sel, sel + n_sel));
     s->rt.finish_reselect();
+    if (!every_stage_in_has_slot(s->rt, p)) {
+        // the pool ran out of slots: nothing was applied
+        s->rt = rt_before;
+        s->slots = slots_before;
+        return KVMEM_HIP_ERR_NOMEM;
+    }
     if (stage_in) {
         std::copy(p.stage_in.begin(), p.stage_in.end(), stage_in);
     }
@@ -375,6 +396,20 @@ static bool alloc_own_pool(kvmem_engine *e);
 
 namespace {
 
+// No block is in the pool any more: every block goes back to the host tier,
+// the working set is empty and every slot is free (the next apply stages
+// its whole selection).
+void drop_residency(kvmem_engine *e) {
+    for (const Block &b : e->rt.store().blocks()) {
+        if (b.tier == Tier::GPU) {
+            e->rt.store().set_block_tier(b.block_id, Tier::CPU);
+        }
+    }
+    e->rt.store().clear_working_set();
+    e->slots.reset_after(0);
+    e->dirty_tail = -1;
+}
+
 // The stage-in row transform from the engine parameters: RoPE frequencies
 // as rope.cpp:20-23 forms them, and the reference's attn_rot widths
 // (llama-kvmem-quant.h:22-38): on a quantized cache, K gets the largest
@@ -536,20 +571,27 @@ int kvmem_engine_set_device_history(kvmem_engine *e, const void *k, const void *
     if (n_tokens > cap_tokens) {
         return e->fail(KVMEM_HIP_ERR_INVALID, "set_device_history: n_tokens exceeds the capacity");
     }
-    e->hist_k = k;
-    e->hist_v = v;
-    e->hist_capacity = capacity_blocks;
-    e->meank_valid = 0;
-    std::fill(e->packed_valid.begin(), e->packed_valid.end(), 0);  // a new history
+    if (k != e->hist_k || v != e->hist_v || capacity_blocks != e->hist_capacity) {
+        // A new history: the pool rows, key sums and packed rows of every
+        // block were made from the old one.
+        if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {  // work reading the old one is done
+            return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "set_device_history");
+        }
+        e->hist_k = k;
+        e->hist_v = v;
+        e->hist_capacity = capacity_blocks;
+        drop_residency(e);
+        e->meank_valid = 0;
+        std::fill(e->packed_valid.begin(), e->packed_valid.end(), 0);
+    }
+    // The same history grown or cut: as append_tokens / truncate_to (a
+    // resident partial tail that grows is staged again, its key sums redone).
     const uint32_t have = e->rt.store().total_tokens();
     if (n_tokens < have) {
-        e->rt.truncate_to(n_tokens);
-    } else if (n_tokens > have) {
-        const uint32_t first_new = e->rt.store().block_count();
-        e->rt.register_append(n_tokens - have);
-        for (uint32_t id = first_new; id < e->rt.store().block_count(); ++id) {
-            e->rt.store().set_block_tier(id, Tier::CPU);
-        }
+        return kvmem_engine_truncate_to(e, n_tokens);
+    }
+    if (n_tokens > have) {
+        return kvmem_engine_append_tokens(e, n_tokens - have);
     }
     ++e->epoch;
     return KVMEM_HIP_OK;
@@ -697,15 +739,7 @@ int kvmem_engine_set_pool(kvmem_engine *e, void *const *k_layers, void *const *v
     } else if (!alloc_own_pool(e)) {
         return e->fail(KVMEM_HIP_ERR_NOMEM, "set_pool: pool allocation");
     }
-    // the new tensors hold none of the working set
-    for (const Block &b : e->rt.store().blocks()) {
-        if (b.tier == Tier::GPU) {
-            e->rt.store().set_block_tier(b.block_id, Tier::CPU);
-        }
-    }
-    e->rt.store().clear_working_set();
-    e->slots.reset_after(0);
-    e->dirty_tail = -1;
+    drop_residency(e);  // the new tensors hold none of the working set
     return KVMEM_HIP_OK;
 }
 
@@ -826,6 +860,47 @@ int meank_scores(kvmem_engine *e, const float *q_sum, const uint32_t *q_count) {
     a.scores = e->d_scores;
     const int rc = kvmem_hip_score_meank(e->ctx, &a);
     return rc == KVMEM_HIP_OK ? rc : e->fail_ctx(rc, "mean-K score");
+}
+
+// The store state before an apply, and the pool slots that apply's device
+// work has been asked to write so far.
+struct ApplyUndo {
+    KvMemRuntime rt;
+    RecordingSlots slots;
+    int64_t dirty_tail;
+    std::vector<uint8_t> packed_valid;
+    std::vector<uint32_t> written_slots;
+};
+
+// A failed apply leaves the store as before it, except that a block whose
+// slot the failed work may have written (a move destination or a stage-in
+// slot) is no longer trusted: it leaves the pool and the working set, so the
+// next apply that selects it stages it in again.  Packed rows copied out by
+// the failed apply are not marked kept.  The device error stays in the
+// engine's last error; the return value is `code`.
+int rollback(kvmem_engine *e, ApplyUndo &u, int code) {
+    e->rt = std::move(u.rt);
+    e->slots = std::move(u.slots);
+    e->dirty_tail = u.dirty_tail;
+    e->packed_valid = std::move(u.packed_valid);
+    if (!u.written_slots.empty()) {
+        std::vector<uint8_t> hit(e->n_slots, 0);
+        for (uint32_t s : u.written_slots) {
+            if (s < e->n_slots) hit[s] = 1;
+        }
+        for (const Block &b : e->rt.store().blocks()) {
+            if (b.tier == Tier::GPU && b.gpu_slot >= 0 && hit[static_cast<uint32_t>(b.gpu_slot)]) {
+                const uint32_t id = b.block_id;
+                e->slots.free_gpu_slot(b.gpu_slot);
+                e->rt.store().set_block_tier(id, Tier::CPU);
+                e->rt.store().drop_from_working_set(id);
+                if (e->dirty_tail == static_cast<int64_t>(id)) {
+                    e->dirty_tail = -1;
+                }
+            }
+        }
+    }
+    return code;
 }
 
 }  // namespace
@@ -953,10 +1028,18 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
     for (const Block &b : e->rt.store().blocks()) {
         old_slot[b.block_id] = b.tier == Tier::GPU ? b.gpu_slot : -1;
     }
+    // The plan is committed to the store before the device work it asks
+    // for; on any failure the store goes back to this state, minus the
+    // blocks whose pool slots the failed work may have written.
+    ApplyUndo undo{e->rt, e->slots, e->dirty_tail, e->packed_valid, {}};
     e->slots.staged_ids.clear();
     e->slots.staged_slots.clear();
     const Plan plan = e->rt.prepare_selection(ids);
     e->rt.finish_reselect();
+    if (!every_stage_in_has_slot(e->rt, plan)) {
+        e->fail(KVMEM_HIP_ERR_NOMEM, "apply: slot pool exhausted");
+        return rollback(e, undo, KVMEM_HIP_ERR_NOMEM);
+    }
     std::vector<uint32_t> stage_ids = e->slots.staged_ids;
     std::vector<uint32_t> stage_slots = e->slots.staged_slots;
     if (e->dirty_tail >= 0) {
@@ -977,7 +1060,8 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
     }
     for (uint32_t s : stage_slots) {
         if (s >= e->n_slots) {
-            return e->fail(KVMEM_HIP_ERR_RUNTIME, "apply: slot pool exhausted");
+            e->fail(KVMEM_HIP_ERR_RUNTIME, "apply: slot out of range");
+            return rollback(e, undo, KVMEM_HIP_ERR_RUNTIME);
         }
     }
     int rc = KVMEM_HIP_OK;
@@ -1002,7 +1086,8 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
             rc = kvmem_hip_stageout_blocks(e->ctx, &pool, &ph, sid.data(), sslot.data(), snt.data(),
                                            static_cast<uint32_t>(sid.size()));
             if (rc != KVMEM_HIP_OK) {
-                return e->fail_ctx(rc, "apply: stage-out");
+                e->fail_ctx(rc, "apply: stage-out");
+                return rollback(e, undo, rc);  // reads the pool only
             }
             for (uint32_t id : sid) e->packed_valid[id] = 1;
             n_saved = static_cast<uint32_t>(sid.size());
@@ -1029,22 +1114,26 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
         // staged ids come in ascending order, so stage_slots pairs with stage_ids
         e->slots.reset_after(static_cast<uint32_t>(ids.size()));
         if (!src.empty()) {
+            undo.written_slots.insert(undo.written_slots.end(), dst.begin(), dst.end());
             const kvmem_hip_pool pool = e->pool_desc();
             rc = kvmem_hip_move_slots(e->ctx, &pool, src.data(), dst.data(), ntok.data(),
                                       static_cast<uint32_t>(src.size()));
             if (rc != KVMEM_HIP_OK) {
-                return e->fail_ctx(rc, "apply: canonical layout");
+                e->fail_ctx(rc, "apply: canonical layout");
+                return rollback(e, undo, rc);
             }
             n_moved = static_cast<uint32_t>(src.size());
         }
     }
     uint32_t n_restored = 0;
+    undo.written_slots.insert(undo.written_slots.end(), stage_slots.begin(), stage_slots.end());
     rc = engine_stage(e, stage_ids, stage_slots, &n_restored);
     if (rc != KVMEM_HIP_OK) {
-        return rc;
+        return rollback(e, undo, rc);
     }
     if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
-        return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "apply sync");
+        e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "apply sync");
+        return rollback(e, undo, KVMEM_HIP_ERR_RUNTIME);
     }
     fill_stats(plan, static_cast<uint32_t>(stage_ids.size()), n_moved, n_saved, n_restored, stats);
     return KVMEM_HIP_OK;

@@ -511,6 +511,9 @@ extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist
     if (grid > 0x7fffffffu) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "score: problem too large for one launch");
     }
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "score kernel launch")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
     perf_begin(ctx, kPerfScore);
     if (D == 256) {
         score_kernel<256><<<static_cast<uint32_t>(grid), kScoreThreads, 0, ctx->stream>>>(p);

@@ -926,6 +926,9 @@ size_t rope_tab_bytes(const Source &s) {
 
 template <class Source, bool XF, bool GROUP>
 bool launch_quant_x(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Source &s) {
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "stage-in kernel launch")) {
+        return false;
+    }
     size_t tb = 0;
     if constexpr (XF) {
         tb = rope_tab_bytes(s);
@@ -968,6 +971,9 @@ bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const BlockSo
 template <int TK, bool XF, bool GROUP>
 bool launch_kv_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, const BlockSource &sk,
                  const BlockSource &sv, uint32_t n_k) {
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "stage-in K/V kernel launch")) {
+        return false;
+    }
     const size_t tb = XF ? rope_tab_bytes(sk) : 0;  // only K is RoPE'd
     switch (tv) {
         case KVMEM_TYPE_Q8_0:
@@ -1525,6 +1531,10 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
             while (j + run < cnt && block_ids[first + j + run] == b + run) {
                 ++run;
             }
+            if (injected_fail(ctx, KVMEM_HIP_FAIL_COPY, "h2d block copy")) {
+                perf_end(ctx, kPerfSet);
+                return KVMEM_HIP_ERR_RUNTIME;
+            }
             if (!hip_ok(ctx, hipMemcpyAsync(slot_base + j * span, host + static_cast<uint64_t>(b) * span,
                                             run * span, hipMemcpyHostToDevice, ctx->copy_stream),
                         "h2d block copy")) {
@@ -1654,9 +1664,14 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
         }
         perf_begin(ctx, kPerfLayout);
         if (!launch_uploaded_copies(ctx, dops, ops.size(), "move_slots save")) {
+            perf_end(ctx, kPerfLayout);
             return KVMEM_HIP_ERR_RUNTIME;
         }
         const dim3 grid(static_cast<uint32_t>((nvec + 255) / 256), static_cast<uint32_t>(segs.size()));
+        if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "move_slots chain launch")) {
+            perf_end(ctx, kPerfLayout);
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
         move_chain_kernel<<<grid, 256, 0, ctx->stream>>>(cp);
         perf_end(ctx, kPerfLayout);
         ctx->d2d_bytes += per_move * saved.size() + moved;

@@ -290,6 +290,9 @@ extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t 
     // pinned memory comes uninitialised: clear the word before the kernel
     // can set it (the previous call's write has landed; it was waited for)
     __atomic_store_n(h + flag, 0u, __ATOMIC_RELEASE);
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "topk launch")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
     perf_begin(ctx, kPerfTopk);
     topk_kernel<<<1, kTopkThreads, 0, ctx->stream>>>(scores, n, forced_dev, inl,
                                                      static_cast<uint32_t>(uniq.size()), need,

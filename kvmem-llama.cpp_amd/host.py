@@ -13,8 +13,10 @@ import ctypes as C
 from dataclasses import dataclass
 from typing import Sequence
 
+import sys
+
 from . import (ERR_STALE, OK, KvMemError, StaleSelection, TYPE_BF16, TYPE_Q8_0, LAYER_MEAN,
-               load_library)
+               load_library, track)
 
 
 class PlanStats(C.Structure):
@@ -119,6 +121,9 @@ class Store:
         if rc != OK:
             raise KvMemError(rc, "kvmem_store_create failed")
         self.h = h
+        track(self)
+
+    _close_rank = 0
 
     def close(self):
         if getattr(self, "h", None):
@@ -126,6 +131,8 @@ class Store:
             self.h = None
 
     def __del__(self):
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
@@ -196,6 +203,9 @@ class Engine:
         if rc != OK:
             raise KvMemError(rc, "kvmem_engine_create failed")
         self.h = h
+        track(self)
+
+    _close_rank = 0
 
     def close(self):
         if getattr(self, "h", None):
@@ -203,6 +213,8 @@ class Engine:
             self.h = None
 
     def __del__(self):
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:

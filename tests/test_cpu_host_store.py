@@ -238,3 +238,20 @@ def test_live_reference_random_sequences():
             b = st.blocks()
             assert b["gpu_slot"] == list(gs[:n]) and b["baked_pos"] == list(bk[:n])
         ref.kref_runtime_free(h)
+
+
+def test_apply_without_free_slots_changes_nothing():
+    """A selection the slot pool cannot hold (admit_incoming gets slot -1
+    from an empty free list) is refused as a whole: the block table is as
+    before the call."""
+    st = host.Store(block_tokens=16, budget_blocks=6, sink_blocks=1, recent_blocks=0,
+                    tie_lower_index=True, n_slots=4)
+    st.register_append(10 * 16)
+    st.apply([0, 1, 2])
+    before = st.blocks()
+    with pytest.raises(kv.KvMemError) as ex:
+        st.apply([0, 3, 4, 5, 6, 7])
+    assert ex.value.code == kv.ERR_NOMEM
+    assert st.blocks() == before
+    stage_in, _, _ = st.apply([0, 1, 5])
+    assert stage_in == [5]
