@@ -384,6 +384,22 @@ KVMEM_HIP_API int kvmem_hip_score(kvmem_hip_ctx *ctx,
                                   const kvmem_hip_history *hist,
                                   const kvmem_hip_score_args *args);
 
+/* kvmem_hip_score that allocates nothing: no counterpart in the reference.
+ * For callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments and the
+ * same scores, bit for bit.  The scorer's partial maxima (and the per-layer
+ * scores when args->layer_scores is NULL) live in a static device array of
+ * 8 MiB that every GPU the library runs on holds until the process ends;
+ * a call needing more returns KVMEM_HIP_ERR_INVALID before any work (the
+ * 256K workload -- 16 layers x 2048 blocks, 4 KV heads, 64 query tokens x
+ * 24 heads -- needs 2.1 MiB).  Every call on one GPU shares that GPU's
+ * array and overwrites it (nothing in it has to start at zero), so calls
+ * that overlap on one GPU -- two contexts or streams at once -- race; calls
+ * queued on one stream do not.  Not timed by kvmem_hip_perf_*. */
+KVMEM_HIP_API int kvmem_hip_score_noalloc(kvmem_hip_ctx *ctx,
+                                          const kvmem_hip_history *hist,
+                                          const kvmem_hip_score_args *args);
+
 /* Top-k block selection on device.  From scores[0..n) (device, finite),
  * keep every id in forced[] (host array, the sink / mandatory / recent
  * blocks already charged by the host), then the `need` best remaining ids

@@ -192,6 +192,7 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_move_slots", i32, vp, C.POINTER(Pool), pu32, pu32, pu32, u32)
     _sig(lib, "kvmem_hip_d2d_batched", i32, vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(sz), i32)
     _sig(lib, "kvmem_hip_score", i32, vp, C.POINTER(History), C.POINTER(ScoreArgs))
+    _sig(lib, "kvmem_hip_score_noalloc", i32, vp, C.POINTER(History), C.POINTER(ScoreArgs))
     _sig(lib, "kvmem_hip_topk", i32, vp, vp, u32, pu32, u32, u32, i32, pu32, pu32)
     _sig(lib, "kvmem_hip_meank_sums", i32, vp, C.POINTER(History), pu32, u32, vp, vp)
     _sig(lib, "kvmem_hip_score_meank", i32, vp, C.POINTER(MeanKArgs))
@@ -400,6 +401,14 @@ class Context:
         a = ScoreArgs(q_ptr, q_type, n_q_tokens, n_head, n_head_kv, head_dim, layer_reduce,
                       layer_scores_ptr or None, scores_ptr)
         self.check(self.lib.kvmem_hip_score(self.h, C.byref(hist), C.byref(a)), "score")
+
+    def score_noalloc(self, hist: History, q_ptr: int, q_type: int, n_q_tokens: int, n_head: int,
+                      n_head_kv: int, head_dim: int, scores_ptr: int, layer_scores_ptr: int = 0,
+                      layer_reduce: int = LAYER_MEAN) -> None:
+        """score() with the library's static per-GPU scratch (allocates nothing)."""
+        a = ScoreArgs(q_ptr, q_type, n_q_tokens, n_head, n_head_kv, head_dim, layer_reduce,
+                      layer_scores_ptr or None, scores_ptr)
+        self.check(self.lib.kvmem_hip_score_noalloc(self.h, C.byref(hist), C.byref(a)), "score_noalloc")
 
     def topk(self, scores_ptr: int, n: int, need: int, forced=(), tie_lower_index: bool = True) -> list[int]:
         f, nf = _u32_array(forced)

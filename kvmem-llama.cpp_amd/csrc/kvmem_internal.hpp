@@ -92,6 +92,10 @@ struct kvmem_hip_ctx {
     // is issued.
     uint32_t fail_kinds = 0;
     uint64_t fail_countdown = 0;
+
+    // Device address of the scorer's static scratch array on this device
+    // (kvmem_hip_score_noalloc), looked up when the context is created.
+    void *noalloc_scratch = nullptr;
 };
 
 namespace kvmem_hip {
@@ -181,6 +185,10 @@ bool load_meank_kernels();
 bool load_score_kernels();
 bool load_stagein_kernels();
 bool load_topk_kernels();
+// Looks up, once per device (the context's, made current by the caller),
+// the device address of the static scratch array of
+// kvmem_hip_score_noalloc and keeps it in ctx->noalloc_scratch.
+bool score_scratch_setup(kvmem_hip_ctx *ctx);
 
 template <typename K>
 inline bool load_kernel_object(K *kernel) {

@@ -43,6 +43,8 @@
 #include <algorithm>
 #include <cfloat>
 #include <cmath>
+#include <mutex>
+#include <string>
 
 namespace kvmem_hip {
 
@@ -435,11 +437,13 @@ bool load_score_kernels() {
 
 using namespace kvmem_hip;
 
-extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
-                               const kvmem_hip_score_args *args) {
-    if (!ctx) {
-        return KVMEM_HIP_ERR_INVALID;
-    }
+namespace {
+
+// Validates a scorer call and fills its launch shape (everything but the
+// partial-maxima buffer).  Sets *empty when there is nothing to score.
+int score_setup(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist, const kvmem_hip_score_args *args,
+                ScoreParams &p, uint64_t &grid, bool *empty) {
+    *empty = false;
     if (!hist || !args || !hist->k || !args->q || !args->scores) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "score: null argument");
     }
@@ -469,9 +473,10 @@ extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist
     const uint32_t L = hist->n_layers;
     const uint32_t B = hist->n_blocks;
     if (L == 0 || B == 0) {
+        *empty = true;
         return KVMEM_HIP_OK;
     }
-    ScoreParams p{};
+    p = ScoreParams{};
     p.q = static_cast<const uint16_t *>(args->q);
     p.k = static_cast<const uint8_t *>(hist->k);
     p.L = L;
@@ -499,45 +504,137 @@ extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist
     p.blocks_per_chunk = (B + p.n_chunks - 1) / p.n_chunks;
     p.n_chunks = (B + p.blocks_per_chunk - 1) / p.blocks_per_chunk;
     p.xcd_major = (pairs % 8u) == 0;
-
-    (void) hipSetDevice(ctx->device);
-    const uint32_t slices = p.RG * kScoreWaves;
-    const size_t partial_bytes = score_partial_bytes(L, p.Hkv, B, p.Tq, p.g);
-    if (!ensure_dev(ctx, ctx->score_partial, partial_bytes, "score partial")) {
-        return KVMEM_HIP_ERR_NOMEM;
-    }
-    p.partial = static_cast<float *>(ctx->score_partial.ptr);
-    const uint64_t grid = static_cast<uint64_t>(pairs) * p.RG * p.n_chunks;
+    grid = static_cast<uint64_t>(pairs) * p.RG * p.n_chunks;
     if (grid > 0x7fffffffu) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "score: problem too large for one launch");
     }
+    return KVMEM_HIP_OK;
+}
+
+// The scorer and the fold on the context stream: p.partial receives the
+// per-slice maxima, `layers` the per-layer scores.  `timed` brackets the
+// scorer with the profiling events of kPerfScore.
+int score_launch(kvmem_hip_ctx *ctx, const kvmem_hip_score_args *args, const ScoreParams &p,
+                 uint64_t grid, float *layers, bool timed) {
     if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "score kernel launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
-    perf_begin(ctx, kPerfScore);
-    if (D == 256) {
+    if (timed) {
+        perf_begin(ctx, kPerfScore);
+    }
+    if (args->head_dim == 256) {
         score_kernel<256><<<static_cast<uint32_t>(grid), kScoreThreads, 0, ctx->stream>>>(p);
     } else {
         score_kernel<128><<<static_cast<uint32_t>(grid), kScoreThreads, 0, ctx->stream>>>(p);
     }
-    perf_end(ctx, kPerfScore);
+    if (timed) {
+        perf_end(ctx, kPerfScore);
+    }
     if (!hip_ok(ctx, hipGetLastError(), "score kernel launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
+    // the fold is not bracketed: a timing event costs the stream a few
+    // microseconds, as much as the fold itself
+    score_fold_kernel<<<(p.B + kFoldBlocks - 1) / kFoldBlocks, 256, 0, ctx->stream>>>(
+        p.partial, p.RG * kScoreWaves, p.L, p.Hkv, p.B, layers, args->layer_reduce, args->scores);
+    if (!hip_ok(ctx, hipGetLastError(), "score fold launch")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    return KVMEM_HIP_OK;
+}
+
+// Scratch of kvmem_hip_score_noalloc, one copy per GPU for the life of the
+// process: the per-slice maxima, then (when the caller passes no
+// layer_scores) the per-layer scores.  The 256K workload (16 layers x 2048
+// blocks, 4 KV heads, a 64-token query of 24 heads) needs 2 MiB + 128 KiB.
+constexpr size_t kNoAllocScratchBytes = size_t{8} << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+// Device address of `scratch` on each GPU, looked up once per device.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_addr[kMaxDevices] = {};
+
+}  // namespace
+
+namespace kvmem_hip {
+
+bool score_scratch_setup(kvmem_hip_ctx *ctx) {
+    if (ctx->device < 0 || ctx->device >= kMaxDevices) {
+        fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "score scratch: device ordinal beyond 63");
+        return false;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[ctx->device]) {
+        // the caller made ctx->device current
+        void *addr = nullptr;
+        if (!hip_ok(ctx, hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)), "score scratch address")) {
+            return false;
+        }
+        g_scratch_addr[ctx->device] = addr;
+    }
+    ctx->noalloc_scratch = g_scratch_addr[ctx->device];
+    return true;
+}
+
+}  // namespace kvmem_hip
+
+extern "C" int kvmem_hip_score(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
+                               const kvmem_hip_score_args *args) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    ScoreParams p;
+    uint64_t grid = 0;
+    bool empty = false;
+    int st = score_setup(ctx, hist, args, p, grid, &empty);
+    if (st != KVMEM_HIP_OK || empty) {
+        return st;
+    }
+    (void) hipSetDevice(ctx->device);
+    const size_t partial_bytes = score_partial_bytes(p.L, p.Hkv, p.B, p.Tq, p.g);
+    if (!ensure_dev(ctx, ctx->score_partial, partial_bytes, "score partial")) {
+        return KVMEM_HIP_ERR_NOMEM;
+    }
+    p.partial = static_cast<float *>(ctx->score_partial.ptr);
     float *layers = args->layer_scores;
     if (!layers) {
-        if (!ensure_dev(ctx, ctx->score_layers, sizeof(float) * static_cast<size_t>(L) * B,
+        if (!ensure_dev(ctx, ctx->score_layers, sizeof(float) * static_cast<size_t>(p.L) * p.B,
                         "score layer buffer")) {
             return KVMEM_HIP_ERR_NOMEM;
         }
         layers = static_cast<float *>(ctx->score_layers.ptr);
     }
-    // the fold is not bracketed: a timing event costs the stream a few
-    // microseconds, as much as the fold itself
-    score_fold_kernel<<<(B + kFoldBlocks - 1) / kFoldBlocks, 256, 0, ctx->stream>>>(
-        p.partial, slices, L, p.Hkv, B, layers, args->layer_reduce, args->scores);
-    if (!hip_ok(ctx, hipGetLastError(), "score fold launch")) {
-        return KVMEM_HIP_ERR_RUNTIME;
+    return score_launch(ctx, args, p, grid, layers, true);
+}
+
+extern "C" int kvmem_hip_score_noalloc(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
+                                       const kvmem_hip_score_args *args) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
     }
-    return KVMEM_HIP_OK;
+    ScoreParams p;
+    uint64_t grid = 0;
+    bool empty = false;
+    int st = score_setup(ctx, hist, args, p, grid, &empty);
+    if (st != KVMEM_HIP_OK || empty) {
+        return st;
+    }
+    if (!ctx->noalloc_scratch) {
+        return fail(ctx, KVMEM_HIP_ERR_RUNTIME, "score_noalloc: no scratch address for this device");
+    }
+    const size_t partial_bytes = score_partial_bytes(p.L, p.Hkv, p.B, p.Tq, p.g);
+    const size_t layer_off = (partial_bytes + 255) / 256 * 256;
+    const size_t need = args->layer_scores ? partial_bytes
+                                           : layer_off + sizeof(float) * static_cast<size_t>(p.L) * p.B;
+    if (need > kNoAllocScratchBytes) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID,
+                    "score_noalloc: " + std::to_string(need) + " bytes of scratch needed, the maximum is " +
+                        std::to_string(kNoAllocScratchBytes) + " (use kvmem_hip_score)");
+    }
+    (void) hipSetDevice(ctx->device);
+    uint8_t *base = static_cast<uint8_t *>(ctx->noalloc_scratch);
+    p.partial = reinterpret_cast<float *>(base);
+    float *layers = args->layer_scores ? args->layer_scores : reinterpret_cast<float *>(base + layer_off);
+    return score_launch(ctx, args, p, grid, layers, false);
 }

@@ -1,0 +1,84 @@
+"""kvmem_hip_score_noalloc: the per-token max scorer with the library's
+static per-GPU scratch instead of allocated buffers.
+
+Two calls in a row through the C ABI -- the 256K workload (16 layers x 2048
+blocks, 64-token bf16 query x 24 heads) and then a smaller one (2 layers x
+300 blocks with a partial last block, 8-token f16 query, per-layer scores
+left to the scratch) -- each equal bit for bit to kvmem_hip_score on the
+same inputs, with no allocation by the context in between.  A call that
+needs more scratch than the array holds is refused before any work.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from conftest import load_pkg  # noqa: E402
+
+kv = load_pkg()
+from kvmem_amd import workloads  # noqa: E402
+
+T, HKV, HQ, D = 128, 4, 24, 256
+E = HKV * D
+
+
+def announce(msg: str) -> None:
+    print(f"[no_alloc] {msg}", flush=True)
+
+
+def both_scores(ctx, L, B, Tq, q_type, last_T, seed):
+    """(scores, layer scores) of kvmem_hip_score and of
+    kvmem_hip_score_noalloc on the same seeded inputs."""
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=Tq, seed=seed)
+    if q_type == kv.TYPE_F16:
+        q = q.to(torch.float16)
+    torch.cuda.synchronize()
+    hist = ctx.make_history(k.data_ptr(), None, L, B, T, E, 0, last_T)
+    want = torch.empty(B, dtype=torch.float32, device="cuda")
+    want_l = torch.empty((L, B), dtype=torch.float32, device="cuda")
+    ctx.score(hist, q.data_ptr(), q_type, Tq, HQ, HKV, D, want.data_ptr(), want_l.data_ptr())
+    ctx.sync()
+    got = torch.full((B,), float("nan"), dtype=torch.float32, device="cuda")
+    got_l = torch.full((L, B), float("nan"), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    before = ctx.scratch_info()["allocations"]
+    ctx.score_noalloc(hist, q.data_ptr(), q_type, Tq, HQ, HKV, D, got.data_ptr(), got_l.data_ptr())
+    ctx.sync()
+    # the layer scores left to the static scratch: same final scores
+    got2 = torch.full((B,), float("nan"), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.score_noalloc(hist, q.data_ptr(), q_type, Tq, HQ, HKV, D, got2.data_ptr())
+    ctx.sync()
+    assert ctx.scratch_info()["allocations"] == before
+    return [t.cpu().numpy() for t in (want, want_l, got, got_l, got2)]
+
+
+def test_score_noalloc_equals_score_two_calls():
+    with kv.Context(0) as ctx:
+        for L, B, Tq, q_type, last_T, seed in ((16, 2048, 64, kv.TYPE_BF16, 0, 2),
+                                               (2, 300, 8, kv.TYPE_F16, 37, 5)):
+            announce(f"L={L} B={B} Tq={Tq} q_type={q_type} last_T={last_T}")
+            want, want_l, got, got_l, got2 = both_scores(ctx, L, B, Tq, q_type, last_T, seed)
+            assert np.isfinite(want).all()
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+            assert np.array_equal(got_l.view(np.uint32), want_l.view(np.uint32))
+            assert np.array_equal(got2.view(np.uint32), want.view(np.uint32))
+
+
+def test_score_noalloc_refuses_past_its_scratch():
+    """16 layers x 8192 blocks with a 512-token query needs 64 MiB of
+    partial maxima: refused on the host, nothing launched."""
+    announce("oversized call refused")
+    with kv.Context(0) as ctx:
+        buf = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+        out = torch.zeros(8192, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        hist = ctx.make_history(buf.data_ptr(), None, 16, 8192, T, E, 0)
+        with pytest.raises(kv.KvMemError) as ex:
+            ctx.score_noalloc(hist, buf.data_ptr(), kv.TYPE_BF16, 512, HQ, HKV, D, out.data_ptr())
+        assert ex.value.code == kv.ERR_INVALID and "maximum" in str(ex.value)
+        ctx.sync()
