@@ -14,7 +14,12 @@ Each timed step starts from the same previous selection: between timed
 steps an untimed restore re-applies it (the same stage-in path).
 
 Prints ONE JSON line.  `value` is ms per agent step (lower is better) with
-history and query resident in HBM.  `roofline` is the MFMA block scorer
+history and query resident in HBM, the pool laid out as the reference lays
+it out (slot i = i-th selected block); `lifo_layout` is the same step
+without the slot moves.  `mixed_precision` (Student-t history, K q8_0 +
+V q4_0, then K and V q5_0) and `recall_1m` (8192 blocks, 512-token query,
+32 planted blocks, budget 512) are the other workloads' steps, in the same
+line unless --no-configs.  `roofline` is the MFMA block scorer
 (the dominant kernel); `stagein_roofline` the q8_0 stage-in kernel against
 HBM; `pinned_host` the same stage-in fed over PCIe from pinned host memory,
 and the same blocks as packed q8_0 rows copied out to (`packed_stageout`)
@@ -126,17 +131,6 @@ def stage_bytes(kv, n_blocks: int, type_k: int, type_v: int) -> int:
     """Algorithmic HBM bytes of a stage-in: F16 K and V read once, packed
     rows written once."""
     return n_blocks * L * T * (2 * E * 2 + kv.row_size(type_k, E) + kv.row_size(type_v, E))
-
-
-def make_previous(sel: list[int], seed: int = 7) -> list[int]:
-    """The previous step's selection: N_CHANGED seeded blocks of `sel`
-    (never the sink) swapped for seeded blocks outside it."""
-    rng = np.random.default_rng(seed)
-    cur = np.array(sel)
-    drop = rng.choice(cur[cur != 0], N_CHANGED, replace=False)
-    outside = np.setdiff1d(np.arange(B), cur)
-    add = rng.choice(outside, N_CHANGED, replace=False)
-    return sorted(set(sel) - set(drop.tolist()) | set(add.tolist()))
 
 
 # ------------------------------------------------------------ cpu baseline
@@ -288,21 +282,24 @@ def run_reselect_256k(a, torch, kv, workloads) -> dict:
     log("generating history K/V [16][2048][128][4][256] f16 and query [16][64][24][256] bf16")
     k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=TQ, seed=2, with_v=True)
     torch.cuda.synchronize()
-    eng = make_engine(kv, torch, k, v)
+    eng = make_engine(kv, torch, k, v)   # canonical layout: slot i = i-th selected block
     ctx = kv.Context.borrow(eng.ctx_handle())
     sel = eng.preview(q.data_ptr(), TQ).blocks
-    prev = make_previous(sel)
+    prev = workloads.previous_selection(sel, B, N_CHANGED)
     log(f"selection {len(sel)} blocks, {len(set(sel) - set(prev))} changed vs previous step")
     m = timed_steps(eng, ctx, torch, q, TQ, prev, a.steps, a.warmup)
     n_staged = m["n_staged"]
     log(f"step {m['ms_step']:.3f} ms: score kernel {m['score_ms']:.3f} ms, top-k "
-        f"{m['sel_ms']:.3f} ms, stage-in kernel {m['set_ms']:.3f} ms ({n_staged} blocks)")
+        f"{m['sel_ms']:.3f} ms, slot moves {m['layout_ms']:.3f} ms ({m['n_moved']} blocks), "
+        f"stage-in kernel {m['set_ms']:.3f} ms ({n_staged} blocks)")
 
     flops = 2.0 * TQ * HQ * D * (B * T) * L
     k_bytes = L * B * T * E * 2
     score_tflops = flops / (m["score_ms"] * 1e-3) / 1e12
     sbytes = stage_bytes(kv, n_staged, kv.TYPE_Q8_0, kv.TYPE_Q8_0)
     stage_gbs = sbytes / (m["set_ms"] * 1e-3) / 1e9
+    row = kv.row_size(kv.TYPE_Q8_0, E)
+    moved_bytes = m["n_moved"] * L * 2 * T * row  # one copy of the moved blocks' K and V rows
     result = {
         "metric": "reselect latency ms/agent-step @256K ctx; stage-in GB/s vs HBM peak",
         "value": round(m["ms_step"], 4),
@@ -318,7 +315,8 @@ def run_reselect_256k(a, torch, kv, workloads) -> dict:
         "data": "synthetic (seeded N(0,1) keys with per-block offsets, bf16 query)",
         "config": {"workload": "full reselect step @256K: 16 layers x 2048 blocks x 128 tokens, "
                                "4 KV heads x 256, 64-token query x 24 heads (GQA 6), top-256 + sink, "
-                               f"{n_staged} changed blocks -> q8_0 K/V pool of 256+128 slots",
+                               f"{n_staged} changed blocks -> q8_0 K/V pool of 256+128 slots, "
+                               "canonical layout (slot i = i-th selected block)",
                    "history": "device-resident", "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": "score_kernel<256>",
                      "achieved": round(score_tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
@@ -329,10 +327,13 @@ def run_reselect_256k(a, torch, kv, workloads) -> dict:
                              "achieved": round(stage_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(stage_gbs / HBM_PEAK_GBS, 4), "traffic": STAGEIN_TRAFFIC_BYTES,
                              "algorithmic_bytes": sbytes, "kernel_ms": round(m["set_ms"], 4)},
+        "layout": {"n_moved": m["n_moved"], "layout_ms": round(m["layout_ms"], 4),
+                   "algorithmic_bytes": 2 * moved_bytes, "device_bytes": 2 * m["d2d_bytes"],
+                   "GBs_algorithmic": (round(2 * moved_bytes / (m["layout_ms"] * 1e-3) / 1e9, 1)
+                                       if m["layout_ms"] > 0 else None)},
         "parts_ms": {"score_kernel": round(m["score_ms"], 4), "topk_kernel": round(m["sel_ms"], 4),
-                     "stagein_kernel": round(m["set_ms"], 4)},
+                     "layout_kernels": round(m["layout_ms"], 4), "stagein_kernel": round(m["set_ms"], 4)},
     }
-    ctx = kv.Context.borrow(eng.ctx_handle())
     if not a.no_pinned:
         incoming = sorted(set(sel) - set(prev))
         result["pinned_host"] = pinned_host_mode(kv, ctx, torch, k, v, eng, incoming)
@@ -340,33 +341,28 @@ def run_reselect_256k(a, torch, kv, workloads) -> dict:
         log("cpu baseline (oracle restatement on host cores)")
         result["cpu_baseline"] = cpu_baseline(torch, k, v, q, sorted(set(sel) - set(prev)))
     eng.close()
-    result["canonical_layout"] = canonical_layout_mode(a, torch, kv, k, v, q, prev)
+    result["lifo_layout"] = lifo_layout_mode(a, torch, kv, k, v, q, prev)
+    del k, v, q
+    torch.cuda.empty_cache()
+    if not a.no_configs:
+        result["mixed_precision"] = run_mixed_precision(a, torch, kv, workloads)["runs"]
+        torch.cuda.empty_cache()
+        result["recall_1m"] = run_recall_1m(a, torch, kv, workloads)
+        torch.cuda.empty_cache()
     return result
 
 
-def canonical_layout_mode(a, torch, kv, k, v, q, prev: list) -> dict:
-    """The same step with canonical slot order (window slot i holds the
-    i-th selected block, as layout_gpu_slots_by_orig_pos): the resident
-    blocks that change slot are moved on the device before the stage-in
-    (chains of moves walked backwards; the slots where chains are cut are
-    saved to scratch first).  Reported beside the default step."""
-    log("canonical layout: the same step with slot i = i-th selected block")
-    eng = make_engine(kv, torch, k, v, canonical_layout=1)
+def lifo_layout_mode(a, torch, kv, k, v, q, prev: list) -> dict:
+    """The same step with the LIFO slot plan alone (canonical_layout = 0):
+    incoming blocks take the slots the outgoing ones free and resident
+    blocks never move.  Reported beside the default step."""
+    log("LIFO layout: the same step without the canonical slot moves")
+    eng = make_engine(kv, torch, k, v, canonical_layout=0)
     ctx = kv.Context.borrow(eng.ctx_handle())
     m = timed_steps(eng, ctx, torch, q, TQ, prev, a.steps, a.warmup)
     eng.close()
-    row = kv.row_size(kv.TYPE_Q8_0, E)
-    moved_bytes = m["n_moved"] * L * 2 * T * row  # one copy of the moved blocks' K and V rows
-    device_bytes = 2 * m["d2d_bytes"]  # every byte the library copied, read + write
-    out = {"ms_per_step": round(m["ms_step"], 4), "n_moved": m["n_moved"], "n_staged": m["n_staged"],
-           "layout_ms": round(m["layout_ms"], 4), "stagein_kernel_ms": round(m["set_ms"], 4),
-           "moved_bytes": moved_bytes,
-           "algorithmic_bytes": 2 * moved_bytes,  # read + write once
-           "device_bytes": device_bytes}
-    if m["layout_ms"] > 0:
-        out["GBs_algorithmic"] = round(2 * moved_bytes / (m["layout_ms"] * 1e-3) / 1e9, 1)
-        out["GBs_device"] = round(device_bytes / (m["layout_ms"] * 1e-3) / 1e9, 1)
-    return out
+    return {"ms_per_step": round(m["ms_step"], 4), "n_moved": m["n_moved"], "n_staged": m["n_staged"],
+            "score_kernel_ms": round(m["score_ms"], 4), "stagein_kernel_ms": round(m["set_ms"], 4)}
 
 
 def run_mixed_precision(a, torch, kv, workloads) -> dict:
@@ -381,7 +377,7 @@ def run_mixed_precision(a, torch, kv, workloads) -> dict:
         eng = make_engine(kv, torch, k, v, reserve=reserve, type_k=tk, type_v=tv)
         ctx = kv.Context.borrow(eng.ctx_handle())
         sel = eng.preview(q.data_ptr(), TQ).blocks
-        prev = make_previous(sel)
+        prev = workloads.previous_selection(sel, B, N_CHANGED)
         m = timed_steps(eng, ctx, torch, q, TQ, prev, a.steps, a.warmup)
         sb = stage_bytes(kv, m["n_staged"], tk, tv)
         runs[name] = {"ms_per_step": round(m["ms_step"], 4), "score_kernel_ms": round(m["score_ms"], 4),
@@ -389,9 +385,11 @@ def run_mixed_precision(a, torch, kv, workloads) -> dict:
                       "stagein_algorithmic_bytes": sb,
                       "stagein_GBs": round(sb / (m["set_ms"] * 1e-3) / 1e9, 1),
                       "stagein_frac_hbm": round(sb / (m["set_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                      "layout_ms": round(m["layout_ms"], 4), "n_moved": m["n_moved"],
                       "pool_slots": BUDGET + reserve}
         log(f"{name}: {runs[name]}")
         eng.close()
+    del k, v, q
     return {"metric": "mixed-precision reselect @256K (Student-t nu=4 history)", "unit": "ms/step",
             "higher_is_better": False, "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
             "data": "synthetic (seeded Student-t nu=4 K/V, bf16 query)", "runs": runs}
@@ -407,7 +405,7 @@ def run_cache_transform(a, torch, kv, workloads) -> dict:
     eng = make_engine(kv, torch, k, v, n_rot=256, rope_freq_base=1e6, attn_rot=1)
     ctx = kv.Context.borrow(eng.ctx_handle())
     sel = eng.preview(q.data_ptr(), TQ).blocks
-    prev = make_previous(sel)
+    prev = workloads.previous_selection(sel, B, N_CHANGED)
     m = timed_steps(eng, ctx, torch, q, TQ, prev, a.steps, a.warmup)
     eng.close()
     sb = stage_bytes(kv, m["n_staged"], kv.TYPE_Q8_0, kv.TYPE_Q8_0)
@@ -493,7 +491,7 @@ def run_meank_256k(a, torch, kv, workloads) -> dict:
     eng = make_engine(kv, torch, k, v, scorer=1)
     ctx = kv.Context.borrow(eng.ctx_handle())
     sel = eng.preview(q.data_ptr(), TQ).blocks
-    prev = make_previous(sel)
+    prev = workloads.previous_selection(sel, B, N_CHANGED)
     m = timed_steps(eng, ctx, torch, q, TQ, prev, a.steps, a.warmup)
     eng.close()
     sums_bytes = L * B * E * 4
@@ -510,10 +508,12 @@ def run_meank_256k(a, torch, kv, workloads) -> dict:
 
 def run_recall_1m(a, torch, kv, workloads) -> dict:
     """1M-token workspace: 8192 blocks x 16 layers, 512-token query, 32
-    planted blocks (Zipf relevance), budget 512.  A cold step (empty pool)
-    then warm steps with the same query; reports recall of the planted
-    blocks."""
+    planted blocks (Zipf relevance), budget 512.  A cold step (empty pool,
+    every selected block staged), the recall of the planted blocks, then
+    reselect steps that each start from a previous selection with 30 % of
+    the 512 blocks different (154 staged)."""
     nb, tq, budget = 8192, 512, 512
+    n_changed = round(0.3 * budget)
     log("generating history K/V [16][8192][128][4][256] f16 (64 GiB) and query [16][512][24][256]")
     k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=nb, Tq=tq, seed=6, with_v=True)
     planted = workloads.plant_blocks(torch, k, q, n_planted=32, seed=5)
@@ -528,28 +528,30 @@ def run_recall_1m(a, torch, kv, workloads) -> dict:
     torch.cuda.synchronize()
     cold_ms = 1e3 * (time.perf_counter() - t0)
     pf_cold = ctx.perf()
-    sel = set(eng.preview(q.data_ptr(), tq).blocks)
-    recall = sum(int(b) in sel for b in planted) / len(planted)
-    warm = []
-    for _ in range(max(1, a.steps // 2)):
-        ctx.perf_reset()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        eng.apply_retrieval(q.data_ptr(), tq)
-        torch.cuda.synchronize()
-        warm.append(1e3 * (time.perf_counter() - t0))
-    pf = ctx.perf()
-    flops = 2.0 * tq * HQ * D * (nb * T) * L
+    ctx.perf_enable(False)
+    sel = eng.preview(q.data_ptr(), tq).blocks
+    recall = sum(int(b) in set(sel) for b in planted) / len(planted)
+    prev = workloads.previous_selection(sel, nb, n_changed)
+    m = timed_steps(eng, ctx, torch, q, tq, prev, max(2, a.steps // 2), 1)
     eng.close()
+    del k, v, q
+    flops = 2.0 * tq * HQ * D * (nb * T) * L
+    sb = stage_bytes(kv, m["n_staged"], kv.TYPE_Q8_0, kv.TYPE_Q8_0)
+    log(f"1M: reselect step {m['ms_step']:.3f} ms, cold step {cold_ms:.3f} ms, recall {recall:.3f}")
     return {"metric": "1M-workspace reselect step + planted-block recall", "unit": "ms/step",
             "higher_is_better": False, "n_gpus": 1,
-            "config": {"workload": "16 layers x 8192 blocks x 128 tokens, 512-token query, budget 512, "
-                                   "32 planted blocks"},
+            "config": {"workload": "16 layers x 8192 blocks x 128 tokens, 512-token query, budget 512 "
+                                   "(+128 reserve), 32 planted blocks, q8_0 K/V, canonical layout",
+                       "changed_per_step": n_changed},
+            "ms_per_step": round(m["ms_step"], 3), "n_staged": m["n_staged"], "n_moved": m["n_moved"],
+            "score_kernel_ms": round(m["score_ms"], 3),
+            "score_TFLOPs": round(flops / (m["score_ms"] * 1e-3) / 1e12, 1),
+            "score_frac_mfma": round(flops / (m["score_ms"] * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+            "topk_kernel_ms": round(m["sel_ms"], 4), "layout_ms": round(m["layout_ms"], 4),
+            "stagein_kernel_ms": round(m["set_ms"], 4),
+            "stagein_frac_hbm": round(sb / (m["set_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "cold_step_ms": round(cold_ms, 3), "cold_staged": st["n_staged"],
             "cold_stagein_kernel_ms": round(pf_cold["set_ms"], 4),
-            "warm_step_ms": round(sum(warm) / len(warm), 3),
-            "score_kernel_ms": round(pf["score_ms"], 3),
-            "score_TFLOPs": round(flops / (pf["score_ms"] * 1e-3) / 1e12, 1),
             "recall_planted": recall, "n_planted": len(planted)}
 
 
@@ -660,6 +662,8 @@ def main() -> int:
                     help="scorer_sustained, mfma_calibration: loop length")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-pinned", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="reselect_256k: leave out the mixed-precision and 1M-workspace sub-objects")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the reselect path runs on a single MI355X; "

@@ -120,10 +120,13 @@ typedef struct kvmem_engine_params {
     int32_t type_v;            /* (-ctv) */
     int32_t tie_lower_index;   /* 1: equal scores -> lower id first */
     int32_t layer_reduce;      /* kvmem_hip_layer_reduce */
-    int32_t canonical_layout;  /* 1: selected block i (ascending) lives in
-                                  slot i after apply, as
+    int32_t canonical_layout;  /* 1 (default): selected block i (ascending)
+                                  lives in slot i after every apply, as
+                                  apply_selection lays the window out with
                                   layout_gpu_slots_by_orig_pos
-                                  (llama-memory-kvmem.cpp:931-1254) */
+                                  (llama-memory-kvmem.cpp:3209, 931-1254);
+                                  0: blocks keep the slot the LIFO free list
+                                  gave them (resident blocks never move) */
     int32_t scorer;            /* kvmem_engine_scorer used by preview */
     /* Cache row transform of the stage-in (kvmem_hip_transform), for a
      * history of pre-RoPE keys and a cache that holds RoPE'd, rotated rows: */
@@ -148,8 +151,9 @@ enum kvmem_engine_scorer {
 
 /* Defaults: 16 layers, 128-token blocks, 24/4 heads x 256, budget 256 +
  * reserve 128 blocks, sink 1, recent 0, q8_0 K and V, lower-id ties, mean
- * layer reduce, free-list (non-canonical) layout, per-token max scorer, no
- * row transform (RoPE base 10000, scale 1 when n_rot is set). */
+ * layer reduce, canonical layout (slot i = i-th selected block), per-token
+ * max scorer, no row transform (RoPE base 10000, scale 1 when n_rot is
+ * set). */
 KVMEM_HIP_API kvmem_engine_params kvmem_engine_default_params(void);
 
 /* Create the engine: its kvmem_hip_ctx, the slot pool of

@@ -471,7 +471,7 @@ kvmem_engine_params kvmem_engine_default_params(void) {
     p.type_v = KVMEM_TYPE_Q8_0;
     p.tie_lower_index = 1;
     p.layer_reduce = KVMEM_LAYER_MEAN;
-    p.canonical_layout = 0;
+    p.canonical_layout = 1;
     p.scorer = KVMEM_SCORER_TOKEN_MAX;
     p.n_rot = 0;
     p.rope_freq_base = 10000.0f;

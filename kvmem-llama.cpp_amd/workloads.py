@@ -124,6 +124,18 @@ def plant_blocks(torch, k, q, n_planted: int = 32, seed: int = 5, alpha: float =
     return ids.astype(np.uint32)
 
 
+def previous_selection(sel, n_blocks: int, n_changed: int, seed: int = 7) -> list[int]:
+    """The previous agent step's selection for a reselect workload:
+    `n_changed` seeded blocks of `sel` (never block 0, the sink) swapped for
+    seeded blocks outside it, so the next step stages exactly those."""
+    rng = np.random.default_rng(seed)
+    cur = np.array(sel)
+    drop = rng.choice(cur[cur != 0], n_changed, replace=False)
+    outside = np.setdiff1d(np.arange(n_blocks), cur)
+    add = rng.choice(outside, n_changed, replace=False)
+    return sorted(set(int(x) for x in sel) - set(drop.tolist()) | set(add.tolist()))
+
+
 def to_bits(torch, t) -> np.ndarray:
     """Device f16/bf16 tensor -> numpy uint16 bits on the host."""
     return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)

@@ -36,7 +36,7 @@ def test_engine_two_steps_vs_oracle(oracle):
     cap, nb = 48, 40
     k, v, q1 = history(cap, seed=31)
     q2 = (q1.float() * -1.0).to(torch.bfloat16)     # a different query direction
-    with make_engine(8, 4, kv.TYPE_Q8_0, kv.TYPE_Q4_0) as eng:
+    with make_engine(8, 4, kv.TYPE_Q8_0, kv.TYPE_Q4_0, canonical_layout=0) as eng:
         eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
         assert eng.block_count() == nb
         sel1 = eng.preview(q1.data_ptr(), q1.shape[1])
