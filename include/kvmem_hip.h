@@ -411,7 +411,8 @@ KVMEM_HIP_API int kvmem_hip_score_noalloc(kvmem_hip_ctx *ctx,
  * the kernel writes it to the context's coherent pinned buffer and sets a
  * completion word there, on which the calling thread spins (work queued
  * earlier on the context stream, e.g. the scorer, completes first).
- * n <= 16384. */
+ * n <= 1048576 (more than 16384 blocks take a kernel that recomputes
+ * the keys from the scores in every radix pass). */
 KVMEM_HIP_API int kvmem_hip_topk(kvmem_hip_ctx *ctx,
                                  const float *scores, uint32_t n,
                                  const uint32_t *forced, uint32_t n_forced,

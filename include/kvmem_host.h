@@ -58,6 +58,13 @@ typedef struct kvmem_plan_stats {
     uint32_t n_restored;               /* staged blocks restored from packed rows */
 } kvmem_plan_stats;
 
+/* A half-open range [begin, end) of history rows (token positions);
+ * llama_kvmem_row_range (src/adapter/llama-kvmem-hooks.h:123-126). */
+typedef struct kvmem_row_range {
+    int32_t begin;
+    int32_t end;
+} kvmem_row_range;
+
 /* ----------------------------------------------------------- host store */
 
 typedef struct kvmem_store kvmem_store;
@@ -99,6 +106,15 @@ KVMEM_HIP_API int kvmem_store_blocks(const kvmem_store *s, int32_t *gpu_slot, ui
 /* KvMemStore::commit_resident_selection (kvmem_store.cpp:884-895):
  * 1 if committed, 0 if refused. */
 KVMEM_HIP_API int kvmem_store_commit_resident(kvmem_store *s, const uint32_t *sel, uint32_t n);
+/* The block ids the adapter's retrieval_mandatory derives from row ranges
+ * (llama-memory-kvmem.cpp:3026-3045): in block order every block
+ * overlapping one of the n_ranges ranges, then the block holding force_pos
+ * (KvMemStore::block_id_containing, kvmem_store.cpp:158-176; -1 = none).
+ * out holds `capacity` ids; *n_out receives the count (ERR_INVALID when it
+ * exceeds capacity, or for a range with begin < 0 or end < begin). */
+KVMEM_HIP_API int kvmem_store_blocks_overlapping(const kvmem_store *s, const kvmem_row_range *ranges,
+                                                 uint32_t n_ranges, int32_t force_pos,
+                                                 uint32_t *out, uint32_t capacity, uint32_t *n_out);
 
 /* ------------------------------------------------------ reselect engine */
 
@@ -220,11 +236,33 @@ KVMEM_HIP_API int kvmem_engine_pool_layer(const kvmem_engine *e, uint32_t layer,
 /* Slot of every block (-1 = not in the pool), block count entries. */
 KVMEM_HIP_API int kvmem_engine_block_slots(const kvmem_engine *e, int32_t *slots);
 
+/* Request span (llama_kvmem_set_request_span, llama-kvmem-hooks.h:112):
+ * the query rows [query_begin, query_end) (query_end <= 0: to the end of
+ * the history; query_begin < 0: no span) and force_pos, a row whose block
+ * every selection keeps (-1 = none).  Drops explicit turn spans. */
+KVMEM_HIP_API int kvmem_engine_set_request_span(kvmem_engine *e, int32_t query_begin,
+                                                int32_t query_end, int32_t force_pos);
+/* Explicit turn spans (llama_kvmem_set_turn_spans, llama-kvmem-hooks.h:
+ * 133-137, 154): query ranges and mandatory ranges replace the request
+ * span; ERR_INVALID for a range with begin < 0 or end < begin (the
+ * reference throws std::invalid_argument, llama-memory-kvmem.cpp:2936-2944). */
+KVMEM_HIP_API int kvmem_engine_set_turn_spans(kvmem_engine *e, const kvmem_row_range *query,
+                                              uint32_t n_query, const kvmem_row_range *mandatory,
+                                              uint32_t n_mandatory);
+/* The blocks every preview keeps (retrieval_mandatory,
+ * llama-memory-kvmem.cpp:3026-3045): with turn spans, the blocks
+ * overlapping their mandatory ranges; else those overlapping the request
+ * span's query rows; then the block holding force_pos.  Block order; out
+ * holds `capacity` ids. */
+KVMEM_HIP_API int kvmem_engine_retrieval_mandatory(const kvmem_engine *e, uint32_t *out,
+                                                   uint32_t capacity, uint32_t *n_out);
+
 /* Phase 1 (preview_retrieval): score every block over q (device
  * [n_layers][n_q_tokens][n_head][head_dim], bf16 or f16) with the engine's
  * scorer -- the per-token max, or mean-K cosine over the sum of the
  * n_q_tokens rows (q_count_ = n_q_tokens in every layer) -- then top-k
- * with sink / mandatory (host ids, newest last) / recent charged first.
+ * with sink / mandatory / recent charged first: mandatory is the caller's
+ * host ids (newest last) followed by kvmem_engine_retrieval_mandatory's.
  * Writes the ascending selection (capacity block count), its epoch and rows
  * (history tokens). */
 KVMEM_HIP_API int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type,

@@ -81,6 +81,44 @@ void KvMemStore::set_block_gpu_slot(uint32_t id, int32_t slot) {
     }
 }
 
+int32_t KvMemStore::block_id_containing(uint32_t pos) const {
+    if (blocks_.empty() || pos >= total_tokens_) {
+        return -1;
+    }
+    const uint32_t guess = std::min(pos / cfg_.block_tokens, block_count() - 1);
+    const Block &g = blocks_[guess];
+    if (pos >= g.orig_pos_start && pos < g.orig_pos_end()) {
+        return static_cast<int32_t>(guess);
+    }
+    for (const Block &b : blocks_) {
+        if (pos >= b.orig_pos_start && pos < b.orig_pos_end()) {
+            return static_cast<int32_t>(b.block_id);
+        }
+    }
+    return -1;
+}
+
+std::vector<uint32_t> KvMemStore::blocks_overlapping(
+    const std::vector<std::pair<int32_t, int32_t>> &ranges, int32_t force_pos) const {
+    std::vector<uint32_t> out;
+    for (const Block &b : blocks_) {
+        for (const auto &r : ranges) {
+            if (static_cast<int64_t>(b.orig_pos_end()) > r.first &&
+                static_cast<int64_t>(b.orig_pos_start) < r.second) {
+                out.push_back(b.block_id);
+                break;
+            }
+        }
+    }
+    if (force_pos >= 0) {
+        const int32_t id = block_id_containing(static_cast<uint32_t>(force_pos));
+        if (id >= 0) {
+            out.push_back(static_cast<uint32_t>(id));
+        }
+    }
+    return out;
+}
+
 // ---------------------------------------------------------------- top-k
 
 TopkCharge KvMemStore::charge_topk(const std::vector<uint32_t> &mandatory) const {

@@ -17,6 +17,7 @@
 #include <cstdint>
 #include <functional>
 #include <stdexcept>
+#include <utility>
 #include <vector>
 
 namespace kvmem_amd {
@@ -119,6 +120,15 @@ public:
                                            const Ranker &ranker = nullptr) const;
     // The charge phase of pick_topk_blocks alone.
     TopkCharge charge_topk(const std::vector<uint32_t> &mandatory) const;
+
+    // kvmem_store.cpp:158-176: the block holding token position pos, -1 if
+    // none.
+    int32_t block_id_containing(uint32_t pos) const;
+    // The adapter's retrieval_mandatory (llama-memory-kvmem.cpp:3026-3045):
+    // in block order, every block overlapping one of the half-open row
+    // ranges [begin, end), then the block holding force_pos (>= 0).
+    std::vector<uint32_t> blocks_overlapping(const std::vector<std::pair<int32_t, int32_t>> &ranges,
+                                             int32_t force_pos) const;
 
     // kvmem_store.cpp:250-277 with optimize_stage_out: leaving the GPU
     // clears the slot.

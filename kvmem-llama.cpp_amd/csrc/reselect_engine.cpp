@@ -17,6 +17,7 @@
 #include <exception>
 #include <new>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "kvmem_host.h"
@@ -83,6 +84,19 @@ bool every_stage_in_has_slot(const KvMemRuntime &rt, const Plan &p) {
         if (b.tier != Tier::GPU || b.gpu_slot < 0) {
             return false;
         }
+    }
+    return true;
+}
+
+// Row ranges from the ABI; false for a range with begin < 0 or end < begin
+// (the reference's std::invalid_argument, llama-memory-kvmem.cpp:2938-2944).
+bool copy_ranges(const kvmem_row_range *r, uint32_t n, std::vector<std::pair<int32_t, int32_t>> &out) {
+    out.clear();
+    for (uint32_t i = 0; i < n; ++i) {
+        if (r[i].begin < 0 || r[i].end < r[i].begin) {
+            return false;
+        }
+        out.emplace_back(r[i].begin, r[i].end);
     }
     return true;
 }
@@ -231,6 +245,23 @@ int kvmem_store_commit_resident(kvmem_store *s, const uint32_t *sel, uint32_t n)
     return s->rt.commit_resident_selection(std::vector<uint32_t>(sel, sel + n)) ? 1 : 0;
 }
 
+int kvmem_store_blocks_overlapping(const kvmem_store *s, const kvmem_row_range *ranges,
+                                   uint32_t n_ranges, int32_t force_pos, uint32_t *out,
+                                   uint32_t capacity, uint32_t *n_out) {
+    std::vector<std::pair<int32_t, int32_t>> rr;
+    if (!s || !n_out || (n_ranges && !ranges) || (capacity && !out) ||
+        !copy_ranges(ranges, n_ranges, rr)) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    const std::vector<uint32_t> ids = s->rt.store().blocks_overlapping(rr, force_pos);
+    *n_out = static_cast<uint32_t>(ids.size());
+    if (ids.size() > capacity) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    std::copy(ids.begin(), ids.end(), out);
+    return KVMEM_HIP_OK;
+}
+
 }  // extern "C"
 
 // =============================================================== engine
@@ -266,6 +297,37 @@ struct kvmem_engine {
     bool has_xf = false;
     uint64_t epoch = 1;
     std::string err;
+    // request span / turn spans (llama-memory-kvmem.h:164-170, .cpp:2938-2948)
+    int32_t query_begin = -1;
+    int32_t query_end = 0;
+    int32_t force_pos = -1;
+    bool explicit_spans = false;
+    std::vector<std::pair<int32_t, int32_t>> span_query, span_mandatory;
+
+    // retrieval_mandatory (llama-memory-kvmem.cpp:3026-3045)
+    std::vector<uint32_t> retrieval_mandatory() const {
+        std::vector<std::pair<int32_t, int32_t>> ranges;
+        if (explicit_spans) {
+            ranges = span_mandatory;
+        } else if (query_begin >= 0) {
+            ranges.emplace_back(query_begin, query_end > 0
+                                                 ? query_end
+                                                 : static_cast<int32_t>(rt.store().total_tokens()));
+        }
+        return rt.store().blocks_overlapping(ranges, force_pos);
+    }
+    // query_contains (llama-memory-kvmem.cpp:2950-2955): a row of the query
+    bool query_contains(int32_t row) const {
+        if (!explicit_spans) {
+            return query_begin >= 0 && row >= query_begin && (query_end <= 0 || row < query_end);
+        }
+        for (const auto &r : span_query) {
+            if (row >= r.first && row < r.second) {
+                return true;
+            }
+        }
+        return false;
+    }
 
     kvmem_engine(const kvmem_engine_params &pp, uint32_t n)
         : p(pp),
@@ -907,6 +969,48 @@ int rollback(kvmem_engine *e, ApplyUndo &u, int code) {
 
 extern "C" {
 
+int kvmem_engine_set_request_span(kvmem_engine *e, int32_t query_begin, int32_t query_end,
+                                  int32_t force_pos) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    e->explicit_spans = false;
+    e->query_begin = query_begin;
+    e->query_end = query_end;
+    e->force_pos = force_pos;
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_set_turn_spans(kvmem_engine *e, const kvmem_row_range *query, uint32_t n_query,
+                                const kvmem_row_range *mandatory, uint32_t n_mandatory) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    std::vector<std::pair<int32_t, int32_t>> q, m;
+    if ((n_query && !query) || (n_mandatory && !mandatory) || !copy_ranges(query, n_query, q) ||
+        !copy_ranges(mandatory, n_mandatory, m)) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "set_turn_spans: invalid KVMem row range");
+    }
+    e->span_query.swap(q);
+    e->span_mandatory.swap(m);
+    e->explicit_spans = true;
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_retrieval_mandatory(const kvmem_engine *e, uint32_t *out, uint32_t capacity,
+                                     uint32_t *n_out) {
+    if (!e || !n_out || (capacity && !out)) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    const std::vector<uint32_t> ids = e->retrieval_mandatory();
+    *n_out = static_cast<uint32_t>(ids.size());
+    if (ids.size() > capacity) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    std::copy(ids.begin(), ids.end(), out);
+    return KVMEM_HIP_OK;
+}
+
 int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_t n_q_tokens,
                          const uint32_t *mandatory, uint32_t n_mandatory, uint32_t *sel,
                          uint32_t *n_sel, uint64_t *epoch, uint32_t *rows) {
@@ -930,6 +1034,8 @@ int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_
         return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: score buffer");
     }
     std::vector<uint32_t> mand(mandatory, mandatory + n_mandatory);
+    const std::vector<uint32_t> spans = e->retrieval_mandatory();
+    mand.insert(mand.end(), spans.begin(), spans.end());
     if (!e->rt.store().charge_topk(mand).all_fit && e->p.scorer == KVMEM_SCORER_MEAN_K) {
         // the reference's scorer over the sum of the query rows
         const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
@@ -991,6 +1097,8 @@ int kvmem_engine_preview_meank(kvmem_engine *e, const float *q_sum, const uint32
         return e->fail(KVMEM_HIP_ERR_NOMEM, "preview_meank: score buffer");
     }
     std::vector<uint32_t> mand(mandatory, mandatory + n_mandatory);
+    const std::vector<uint32_t> spans = e->retrieval_mandatory();
+    mand.insert(mand.end(), spans.begin(), spans.end());
     if (!e->rt.store().charge_topk(mand).all_fit) {
         const int rc = meank_scores(e, q_sum, q_count);
         if (rc != KVMEM_HIP_OK) {

@@ -1,4 +1,6 @@
-// Top-k block selection in one workgroup.
+// Top-k block selection in one workgroup.  Up to 16384 blocks the keys sit
+// in LDS (topk_kernel); beyond, up to 2^20, they are recomputed from the
+// scores in every pass (topk_stream_kernel).
 //
 // Keys are 64-bit: the high word is the score mapped to an unsigned order
 // (negative floats bit-inverted, positive floats with the sign bit set,
@@ -214,8 +216,119 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores,
     }
 }
 
+// More blocks than the keys LDS holds (n > kTopkMaxN, up to kTopkStreamMaxN):
+// the same radix select and ordered compaction, but no key is kept -- each
+// pass recomputes the keys it needs from the scores (L2-resident: 4 bytes a
+// block) and only the forced-id bitmask lives in LDS.  The ids go straight
+// from each thread's segment to the host buffer.
+constexpr uint32_t kTopkStreamMaxN = 1u << 20;
+
+__global__ __launch_bounds__(kTopkThreads) void topk_stream_kernel(
+    const float *scores, uint32_t n, const uint32_t *forced, TopkForced forced_inline,
+    uint32_t n_forced, uint32_t need, int tie_lower, uint32_t *out, uint32_t *done, uint32_t epoch) {
+    __shared__ uint32_t forced_bits[kTopkStreamMaxN / 32];
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t wave_tot[kTopkWaves];
+    __shared__ uint64_t s_prefix;
+    __shared__ uint32_t s_rank;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const bool tl = tie_lower != 0;
+    for (uint32_t w = tid; w < (n + 31u) / 32u; w += kTopkThreads) {
+        forced_bits[w] = 0u;
+    }
+    __syncthreads();
+    for (uint32_t f = tid; f < n_forced; f += kTopkThreads) {
+        const uint32_t id = forced ? forced[f] : forced_inline.id[f];
+        atomicOr(&forced_bits[id >> 5], 1u << (id & 31u));
+    }
+    __syncthreads();
+    auto is_forced = [&](uint32_t i) -> bool { return (forced_bits[i >> 5] >> (i & 31u)) & 1u; };
+    auto key_of = [&](uint32_t i) -> uint64_t { return is_forced(i) ? 0ull : rank_key(scores[i], i, tl); };
+
+    uint64_t prefix = 0ull;
+    uint64_t mask = 0ull;
+    uint32_t rank = need;
+    if (need > 0u) {
+        for (int shift = 56; shift >= 0; shift -= 8) {
+            if (tid < 256u) {
+                hist[tid] = 0u;
+            }
+            __syncthreads();
+            for (uint32_t i = tid; i < n; i += kTopkThreads) {
+                const uint64_t k = key_of(i);
+                if (k != 0ull && (k & mask) == prefix) {
+                    atomicAdd(&hist[static_cast<uint32_t>(k >> shift) & 255u], 1u);
+                }
+            }
+            __syncthreads();
+            if (tid < 64u) {
+                uint32_t c[4];
+                uint32_t own = 0u;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    c[j] = hist[4u * lane + j];
+                    own += c[j];
+                }
+                uint32_t suffix = own;
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1) {
+                    const uint32_t t = __shfl_down(suffix, off, 64);
+                    if (lane + off < 64u) {
+                        suffix += t;
+                    }
+                }
+                uint32_t above = suffix - own;
+#pragma unroll
+                for (int j = 3; j >= 0; --j) {
+                    if (above < rank && rank <= above + c[j]) {
+                        s_prefix = prefix | (static_cast<uint64_t>(4u * lane + j) << shift);
+                        s_rank = rank - above;
+                    }
+                    above += c[j];
+                }
+            }
+            __syncthreads();
+            prefix = s_prefix;
+            rank = s_rank;
+            mask |= 0xffull << shift;
+            __syncthreads();
+        }
+    }
+    const uint64_t threshold = prefix;
+    auto chosen = [&](uint32_t i) -> bool {
+        if (is_forced(i)) {
+            return true;
+        }
+        return need > 0u && rank_key(scores[i], i, tl) >= threshold;
+    };
+    const uint32_t seg = (n + kTopkThreads - 1) / kTopkThreads;
+    const uint32_t lo = min(n, tid * seg);
+    const uint32_t hi = min(n, lo + seg);
+    uint32_t cnt = 0;
+    for (uint32_t i = lo; i < hi; ++i) {
+        cnt += chosen(i) ? 1u : 0u;
+    }
+    const uint32_t incl = block_inclusive_scan(cnt, wave_tot);
+    const uint32_t total = wave_tot[kTopkWaves - 1];
+    uint32_t pos = incl - cnt;
+    for (uint32_t i = lo; i < hi; ++i) {
+        if (chosen(i)) {
+            out[pos++] = i;
+        }
+    }
+    if (tid == 0) {
+        out[n] = total;
+    }
+    __threadfence_system();  // every thread's ids are visible to the host ...
+    __syncthreads();
+    if (tid == 0) {          // ... before the completion word
+        __hip_atomic_store(done, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
 bool load_topk_kernels() {
-    return load_kernel_object(&topk_kernel);
+    return load_kernel_object(&topk_kernel) && load_kernel_object(&topk_stream_kernel);
 }
 
 }  // namespace kvmem_hip
@@ -245,8 +358,8 @@ extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t 
     if (n == 0) {
         return KVMEM_HIP_OK;
     }
-    if (n > static_cast<uint32_t>(kTopkMaxN)) {
-        return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "topk: more than 16384 blocks");
+    if (n > kTopkStreamMaxN) {
+        return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "topk: more than 1048576 blocks");
     }
     std::vector<uint8_t> seen(n, 0);
     std::vector<uint32_t> uniq;
@@ -294,9 +407,15 @@ extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t 
         return KVMEM_HIP_ERR_RUNTIME;
     }
     perf_begin(ctx, kPerfTopk);
-    topk_kernel<<<1, kTopkThreads, 0, ctx->stream>>>(scores, n, forced_dev, inl,
-                                                     static_cast<uint32_t>(uniq.size()), need,
-                                                     tie_lower_index, out, out + flag, epoch);
+    if (n <= static_cast<uint32_t>(kTopkMaxN)) {
+        topk_kernel<<<1, kTopkThreads, 0, ctx->stream>>>(scores, n, forced_dev, inl,
+                                                         static_cast<uint32_t>(uniq.size()), need,
+                                                         tie_lower_index, out, out + flag, epoch);
+    } else {
+        topk_stream_kernel<<<1, kTopkThreads, 0, ctx->stream>>>(
+            scores, n, forced_dev, inl, static_cast<uint32_t>(uniq.size()), need, tie_lower_index, out,
+            out + flag, epoch);
+    }
     perf_end(ctx, kPerfTopk);
     if (!hip_ok(ctx, hipGetLastError(), "topk launch")) {
         return KVMEM_HIP_ERR_RUNTIME;

@@ -30,6 +30,16 @@ class PlanStats(C.Structure):
         return {name: getattr(self, name) for name, _ in self._fields_}
 
 
+class RowRange(C.Structure):
+    """kvmem_row_range: rows [begin, end) (llama_kvmem_row_range)."""
+    _fields_ = [("begin", C.c_int32), ("end", C.c_int32)]
+
+
+def _ranges(rs):
+    rs = list(rs)
+    return (RowRange * max(1, len(rs)))(*[RowRange(int(b), int(e)) for b, e in rs]), len(rs)
+
+
 class EngineParams(C.Structure):
     _fields_ = [("device", C.c_int32), ("n_layers", C.c_uint32), ("block_tokens", C.c_uint32),
                 ("n_head", C.c_uint32), ("n_head_kv", C.c_uint32), ("head_dim", C.c_uint32),
@@ -68,6 +78,10 @@ def bind(lib: C.CDLL) -> C.CDLL:
     sig("kvmem_store_apply", i32, vp, pu32, u32, pu32, pu32, pu32, pu32, C.POINTER(PlanStats))
     sig("kvmem_store_blocks", i32, vp, pi32, pu8, pu8, pi64)
     sig("kvmem_store_commit_resident", i32, vp, pu32, u32)
+    sig("kvmem_store_blocks_overlapping", i32, vp, C.POINTER(RowRange), u32, C.c_int32, pu32, u32, pu32)
+    sig("kvmem_engine_set_request_span", i32, vp, C.c_int32, C.c_int32, C.c_int32)
+    sig("kvmem_engine_set_turn_spans", i32, vp, C.POINTER(RowRange), u32, C.POINTER(RowRange), u32)
+    sig("kvmem_engine_retrieval_mandatory", i32, vp, pu32, u32, pu32)
     sig("kvmem_engine_default_params", EngineParams)
     sig("kvmem_engine_create", i32, C.POINTER(EngineParams), C.POINTER(vp))
     sig("kvmem_engine_destroy", None, vp)
@@ -186,6 +200,17 @@ class Store:
         s, n = _u32(sel)
         return bool(self.lib.kvmem_store_commit_resident(self.h, s, n))
 
+    def blocks_overlapping(self, ranges, force_pos: int = -1) -> list:
+        """retrieval_mandatory's mapping of row ranges (+ force_pos) to ids."""
+        r, nr = _ranges(ranges)
+        cap = max(1, self.block_count() + 1)
+        out = (C.c_uint32 * cap)()
+        n = C.c_uint32(0)
+        rc = self.lib.kvmem_store_blocks_overlapping(self.h, r, nr, force_pos, out, cap, C.byref(n))
+        if rc != OK:
+            raise KvMemError(rc, "kvmem_store_blocks_overlapping failed")
+        return list(out[: n.value])
+
 
 class Engine:
     """The reselect engine on one GPU (owns its context, pool and store)."""
@@ -283,6 +308,23 @@ class Engine:
         va = (C.c_void_p * len(v_ptrs))(*v_ptrs)
         self._pool_keep = (ka, va)
         self.check(self.lib.kvmem_engine_set_pool(self.h, ka, va), "set_pool")
+
+    def set_request_span(self, query_begin: int, query_end: int = 0, force_pos: int = -1) -> None:
+        self.check(self.lib.kvmem_engine_set_request_span(self.h, query_begin, query_end, force_pos),
+                   "set_request_span")
+
+    def set_turn_spans(self, query=(), mandatory=()) -> None:
+        q, nq = _ranges(query)
+        m, nm = _ranges(mandatory)
+        self.check(self.lib.kvmem_engine_set_turn_spans(self.h, q, nq, m, nm), "set_turn_spans")
+
+    def retrieval_mandatory(self) -> list:
+        cap = max(1, self.block_count() + 1)
+        out = (C.c_uint32 * cap)()
+        n = C.c_uint32(0)
+        self.check(self.lib.kvmem_engine_retrieval_mandatory(self.h, out, cap, C.byref(n)),
+                   "retrieval_mandatory")
+        return list(out[: n.value])
 
     def block_slots(self) -> list:
         n = self.block_count()

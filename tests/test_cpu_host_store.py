@@ -255,3 +255,45 @@ def test_apply_without_free_slots_changes_nothing():
     assert st.blocks() == before
     stage_in, _, _ = st.apply([0, 1, 5])
     assert stage_in == [5]
+
+
+def test_blocks_overlapping_closed_forms():
+    """retrieval_mandatory's row-range mapping (llama-memory-kvmem.cpp:
+    3026-3045) on 10 blocks of 16 tokens with a 5-token tail (149 rows):
+    half-open ranges, straddles, the tail, several ranges (each block once,
+    block order), force_pos appended last (even when already listed), and
+    the reference's overlap test, under which an empty range [20, 20) still
+    names the block holding row 20."""
+    st = host.Store(block_tokens=16, budget_blocks=4, n_slots=8)
+    st.register_append(9 * 16 + 5)
+    assert st.blocks_overlapping([(0, 1)]) == [0]
+    assert st.blocks_overlapping([(15, 17)]) == [0, 1]
+    assert st.blocks_overlapping([(16, 32)]) == [1]
+    assert st.blocks_overlapping([(144, 1000)]) == [9]
+    assert st.blocks_overlapping([(149, 1000)]) == []
+    assert st.blocks_overlapping([(100, 120), (0, 20), (110, 130)]) == [0, 1, 6, 7, 8]
+    assert st.blocks_overlapping([(20, 20)]) == [1]
+    assert st.blocks_overlapping([(32, 48)], force_pos=40) == [2, 2]
+    assert st.blocks_overlapping([], force_pos=148) == [9]
+    assert st.blocks_overlapping([], force_pos=149) == []
+    assert st.blocks_overlapping([], force_pos=-1) == []
+    for bad in ([(-1, 5)], [(8, 7)]):
+        with pytest.raises(kv.KvMemError):
+            st.blocks_overlapping(bad)
+
+
+def test_mandatory_blocks_feed_pick_topk_like_the_reference():
+    """The mapped ids go to pick_topk_blocks as its mandatory list: with a
+    budget of 5, sink 1 and the query rows [100, 130) (blocks 6, 7, 8), the
+    selection is the sink, the three query blocks and the best other block
+    (2); a force_pos block is listed last, hence charged first, so it
+    survives a tight budget."""
+    st = host.Store(block_tokens=16, budget_blocks=5, sink_blocks=1, n_slots=8)
+    st.register_append(9 * 16 + 5)
+    st.set_retrieval_scores([0.0, 0.1, 0.9, 0.2, 0.3, 0.4, 0.0, 0.0, 0.0, 0.5])
+    assert st.pick_topk_blocks(st.blocks_overlapping([(100, 130)])) == [0, 2, 6, 7, 8]
+    tight = host.Store(block_tokens=16, budget_blocks=3, sink_blocks=1, n_slots=8)
+    tight.register_append(9 * 16 + 5)
+    tight.set_retrieval_scores([0.0] * 10)
+    # charged newest-listed first: force block 3, then blocks 8, 7 ... until full
+    assert tight.pick_topk_blocks(tight.blocks_overlapping([(100, 130)], force_pos=50)) == [0, 3, 8]

@@ -167,3 +167,33 @@ def test_stagein_host_many_ring_batches(ctx, oracle, memory):
         for b, s in zip(ids, slots):
             assert np.array_equal(gk[s * T:(s + 1) * T], oracle.quantize_rows_f16(kv.TYPE_Q8_0, kh[b, layer]))
             assert np.array_equal(gv[s * T:(s + 1) * T], oracle.quantize_rows_f16(kv.TYPE_Q4_0, vh[b, layer]))
+
+
+def test_engine_request_and_turn_spans(oracle):
+    """Mandatory blocks from the request span / turn spans and force_pos
+    (retrieval_mandatory) are charged in preview: the selection equals the
+    oracle's top-k with those ids as the mandatory list."""
+    announce("request span, turn spans and force_pos -> mandatory blocks")
+    cap, nb, budget = 40, 40, 8
+    k, v, q = history(cap, seed=37)
+    with make_engine(budget, 4) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        cases = [
+            (lambda: eng.set_request_span(20 * T + 5, 23 * T, 3 * T + 1), [20, 21, 22, 3]),
+            (lambda: eng.set_request_span(37 * T, 0, -1), [37, 38, 39]),
+            (lambda: eng.set_turn_spans(query=[(0, 10)], mandatory=[(35 * T, 36 * T + 1), (2, 3)]),
+             [0, 35, 36]),
+            (lambda: eng.set_request_span(-1, 0, -1), []),
+        ]
+        for set_span, want_mand in cases:
+            set_span()
+            mand = eng.retrieval_mandatory()
+            assert mand == want_mand
+            sel = eng.preview(q.data_ptr(), q.shape[1])
+            s = np.array(eng.scores(), dtype=np.float64).astype(np.float32).astype(np.float64)
+            assert sel.blocks == oracle.pick_topk(s, budget, sink=1, mandatory=mand)
+            assert set(want_mand) <= set(sel.blocks)
+            eng.apply(sel)
+            check_pool(eng, oracle, k, v, sel.blocks, kv.TYPE_Q8_0, kv.TYPE_Q8_0)
+        with pytest.raises(kv.KvMemError):
+            eng.set_turn_spans(query=[(5, 4)])

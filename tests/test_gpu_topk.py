@@ -94,3 +94,42 @@ def test_topk_many_forced(ctx, oracle, n_mand):
     got = ctx.topk(d.data_ptr(), n, fill, forced=[0] + mand + mand[:5])
     assert got == want
     assert len(got) == budget
+
+
+@pytest.mark.parametrize("n,budget,tie_lower", [(16385, 512, True), (20000, 512, False),
+                                                (65536, 4096, True), (300000, 2048, False)])
+def test_topk_beyond_lds_keys(ctx, oracle, n, budget, tie_lower):
+    """More blocks than the keys LDS holds: the keys are recomputed from the
+    scores in every radix pass.  Ties (a coarse score grid), a sink and 100
+    mandatory ids (the upload path), both tie rules."""
+    announce(f"n={n} budget={budget} tie_lower={tie_lower}")
+    rng = np.random.default_rng(n)
+    s = (rng.integers(-400, 400, n) * 0.25).astype(np.float32)
+    mand = sorted(rng.choice(np.arange(1, n), 100, replace=False).tolist())
+    want = oracle.pick_topk(s.astype(np.float64), budget, sink=1, mandatory=mand,
+                            tie_lower_index=tie_lower)
+    d = dev(s)
+    torch.cuda.synchronize()
+    got = ctx.topk(d.data_ptr(), n, budget - 101, forced=[0] + mand, tie_lower_index=tie_lower)
+    assert got == want
+
+
+def test_engine_selects_over_20000_blocks(oracle):
+    """The engine's preview over 20000 blocks of 32 tokens (a 640K-token
+    history at --kvmem-block-tokens 32): the device top-k equals the
+    oracle's over the same scores."""
+    from kvmem_amd import host, workloads
+    announce("engine preview over 20000 blocks of 32 tokens")
+    L, nb, bt, tq = 1, 20000, 32, 8
+    k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=nb, Tq=tq, seed=12, T=bt, with_v=True)
+    torch.cuda.synchronize()
+    with host.Engine(n_layers=L, block_tokens=bt, n_head=24, n_head_kv=4, head_dim=256,
+                     budget_blocks=512, reserve_blocks=64) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), nb, nb * bt)
+        sel = eng.preview(q.data_ptr(), tq)
+        s = np.array(eng.scores(), dtype=np.float64)
+        assert sel.blocks == oracle.pick_topk(s.astype(np.float32).astype(np.float64), 512, sink=1)
+        st = eng.apply(sel)
+        assert st["n_staged"] == 512
+    del k, v, q
+    torch.cuda.empty_cache()
