@@ -431,6 +431,19 @@ KVMEM_HIP_API int kvmem_hip_meank_sums(kvmem_hip_ctx *ctx, const kvmem_hip_histo
                                        const uint32_t *block_ids, uint32_t n,
                                        float *k_sum, uint32_t *mean_tokens);
 
+/* The same producer over a pinned host history (kvmem_hip_host_history,
+ * block-major), for a deployment that keeps the history on the host only,
+ * as the reference's RawKvStore does (its key sums are made on the host,
+ * raw_kv_store.cpp:674-694, 976-1043): the kernel reads the listed blocks'
+ * K rows over the link itself.  The whole history must lie inside one
+ * pinned allocation (KVMEM_HIP_ERR_UNSUPPORTED otherwise).  k_sum /
+ * mean_tokens are [n_layers][capacity_blocks] (0 = hist->n_blocks) as
+ * kvmem_hip_meank_sums writes them; the sums are bit-identical. */
+KVMEM_HIP_API int kvmem_hip_meank_sums_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_history *hist,
+                                            const uint32_t *block_ids, uint32_t n,
+                                            uint32_t capacity_blocks, float *k_sum,
+                                            uint32_t *mean_tokens);
+
 /* Query-sum producer (the reference's Q harvest into q_sum_,
  * src/adapter/llama-memory-kvmem.cpp:2164-2172 and :2206-2219): for every
  * layer and channel, q_sum[l][e] += q[l][t][e] over the listed tokens in

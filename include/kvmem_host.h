@@ -189,7 +189,12 @@ KVMEM_HIP_API int kvmem_engine_set_device_history(kvmem_engine *e, const void *k
                                                   uint32_t capacity_blocks, uint32_t n_tokens);
 /* Pinned host history, block-major (see kvmem_hip_host_history): when
  * set, stage-in reads changed blocks from it over PCIe instead of from the
- * device history.  NULL clears it. */
+ * device history.  It may also be the only history, as the reference keeps
+ * every block in host RAM (RawKvStore): then append_tokens registers its
+ * blocks, and preview runs the mean-K scorer (scorer = KVMEM_SCORER_MEAN_K;
+ * the per-token scorer needs keys in HBM) on key sums the device reads from
+ * the pinned blocks once per block (kvmem_hip_meank_sums_host).  NULL
+ * clears it. */
 KVMEM_HIP_API int kvmem_engine_set_host_history(kvmem_engine *e, const void *pinned_base,
                                                 uint32_t capacity_blocks);
 /* Packed host store (see kvmem_hip_packed_host), pinned, capacity_blocks

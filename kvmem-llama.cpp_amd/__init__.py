@@ -195,6 +195,7 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_score_noalloc", i32, vp, C.POINTER(History), C.POINTER(ScoreArgs))
     _sig(lib, "kvmem_hip_topk", i32, vp, vp, u32, pu32, u32, u32, i32, pu32, pu32)
     _sig(lib, "kvmem_hip_meank_sums", i32, vp, C.POINTER(History), pu32, u32, vp, vp)
+    _sig(lib, "kvmem_hip_meank_sums_host", i32, vp, C.POINTER(HostHistory), pu32, u32, u32, vp, vp)
     _sig(lib, "kvmem_hip_score_meank", i32, vp, C.POINTER(MeanKArgs))
     _sig(lib, "kvmem_hip_q_accumulate", i32, vp, vp, i32, u32, u32, u32, pu32, u32, i32, vp)
     _sig(lib, "kvmem_hip_meank_add", i32, vp, vp, i32, u32, u32, sz, sz, sz, u32, u32, i32, vp, vp)
@@ -423,6 +424,13 @@ class Context:
         ids, n = _u32_array(block_ids)
         self.check(self.lib.kvmem_hip_meank_sums(self.h, C.byref(hist), ids, n, k_sum_ptr,
                                                  mean_tokens_ptr), "meank_sums")
+
+    def meank_sums_host(self, hist: HostHistory, block_ids, k_sum_ptr: int, mean_tokens_ptr: int,
+                        capacity_blocks: int = 0) -> None:
+        """Key sums of pinned host blocks (block-major history)."""
+        ids, n = _u32_array(block_ids)
+        self.check(self.lib.kvmem_hip_meank_sums_host(self.h, C.byref(hist), ids, n, capacity_blocks,
+                                                      k_sum_ptr, mean_tokens_ptr), "meank_sums_host")
 
     def meank_add(self, k_ptr: int, k_type: int, n_embd: int, head_dim: int, nb0: int, nb1: int,
                   nb2: int, tok0: int, n_keep: int, acc_ptr: int, count_ptr: int = 0,

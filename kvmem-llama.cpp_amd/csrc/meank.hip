@@ -27,8 +27,12 @@
 
 namespace kvmem_hip {
 
-// grid: (items * L) workgroups of E/8 threads; item i = block_ids[i].
-__global__ __launch_bounds__(256) void meank_sum_kernel(const uint8_t *k, const uint32_t *items,
+// grid: (items * L) workgroups of E/8 threads; item i = block_ids[i].  The
+// keys of (block b, layer l) are T rows of E halves at k + b*block_stride +
+// l*layer_stride: a device history [L][cap][T][E] or the K rows of a
+// block-major pinned host history.
+__global__ __launch_bounds__(256) void meank_sum_kernel(const uint8_t *k, uint64_t block_stride,
+                                                        uint64_t layer_stride, const uint32_t *items,
                                                         uint32_t L, uint32_t cap, uint32_t T,
                                                         uint32_t E, uint32_t last_block,
                                                         uint32_t last_tokens, float *k_sum,
@@ -42,7 +46,7 @@ __global__ __launch_bounds__(256) void meank_sum_kernel(const uint8_t *k, const 
         return;
     }
     const uint32_t nt = (b == last_block && last_tokens != 0) ? last_tokens : T;
-    const uint8_t *base = k + ((static_cast<uint64_t>(l) * cap + b) * T) * E * 2u + e0 * 2u;
+    const uint8_t *base = k + b * block_stride + l * layer_stride + e0 * 2u;
     float s[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     for (uint32_t t = 0; t < nt; ++t) {
         const uint4 raw = *reinterpret_cast<const uint4 *>(base + static_cast<uint64_t>(t) * E * 2u);
@@ -355,10 +359,68 @@ int kvmem_hip_meank_sums(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
     if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "meank_sums launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
+    const uint64_t block_stride = static_cast<uint64_t>(hist->block_tokens) * E * 2u;
     meank_sum_kernel<<<static_cast<uint32_t>(jobs), E / 8, 0, ctx->stream>>>(
-        static_cast<const uint8_t *>(hist->k), static_cast<const uint32_t *>(items), hist->n_layers,
-        cap, hist->block_tokens, E, hist->n_blocks - 1, hist->last_block_tokens, k_sum, mean_tokens);
+        static_cast<const uint8_t *>(hist->k), block_stride, block_stride * cap,
+        static_cast<const uint32_t *>(items), hist->n_layers, cap, hist->block_tokens, E,
+        hist->n_blocks - 1, hist->last_block_tokens, k_sum, mean_tokens);
     return hip_ok(ctx, hipGetLastError(), "meank_sums launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
+}
+
+int kvmem_hip_meank_sums_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_history *hist,
+                              const uint32_t *block_ids, uint32_t n, uint32_t capacity_blocks,
+                              float *k_sum, uint32_t *mean_tokens) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (n == 0) {
+        return KVMEM_HIP_OK;
+    }
+    if (!hist || !hist->base || !block_ids || !k_sum || !mean_tokens) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "meank_sums_host: null argument");
+    }
+    const uint32_t E = hist->n_embd_k;
+    const uint32_t T = hist->block_tokens;
+    const uint32_t cap = capacity_blocks ? capacity_blocks : hist->n_blocks;
+    if (E == 0 || E % 8 != 0 || E / 8 > 256 || T == 0 || cap < hist->n_blocks ||
+        hist->last_block_tokens > T || (reinterpret_cast<uintptr_t>(hist->base) & 15u) ||
+        (reinterpret_cast<uintptr_t>(k_sum) & 15u) || (hist->n_embd_v % 8 != 0)) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID,
+                    "meank_sums_host: n_embd_k must be a multiple of 8 and at most 2048, 16-byte aligned");
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        if (block_ids[i] >= hist->n_blocks) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "meank_sums_host: block id out of range");
+        }
+    }
+    const uint64_t jobs = static_cast<uint64_t>(n) * hist->n_layers;
+    if (jobs > 0x7fffffffu) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "meank_sums_host: too many blocks in one call");
+    }
+    const uint64_t layer_bytes = static_cast<uint64_t>(T) * (hist->n_embd_k + hist->n_embd_v) * 2u;
+    const uint64_t span = layer_bytes * hist->n_layers;
+    (void) hipSetDevice(ctx->device);
+    // the kernel reads the pinned rows over the link itself
+    const uint8_t *view = host_device_view(hist->base, span * hist->n_blocks);
+    if (!view) {
+        return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED,
+                    "meank_sums_host: the history must lie inside one pinned host allocation");
+    }
+    const void *items = upload(ctx, block_ids, sizeof(uint32_t) * n, "meank_sums_host ids");
+    if (!items) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "meank_sums_host launch")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    meank_sum_kernel<<<static_cast<uint32_t>(jobs), E / 8, 0, ctx->stream>>>(
+        view, span, layer_bytes, static_cast<const uint32_t *>(items), hist->n_layers, cap, T, E,
+        hist->n_blocks - 1, hist->last_block_tokens, k_sum, mean_tokens);
+    if (!hip_ok(ctx, hipGetLastError(), "meank_sums_host launch")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    ctx->h2d_bytes += static_cast<uint64_t>(n) * hist->n_layers * T * E * 2u;
+    return KVMEM_HIP_OK;
 }
 
 int kvmem_hip_meank_add(kvmem_hip_ctx *ctx, const void *k, int32_t k_type, uint32_t n_embd,

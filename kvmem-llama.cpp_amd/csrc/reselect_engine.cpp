@@ -369,6 +369,22 @@ struct kvmem_engine {
         return bl.back().n_tokens;
     }
 
+    // Blocks the key-sum arrays are laid out for: the device history's
+    // capacity, or the pinned host history's when there is no device one.
+    uint32_t sums_capacity() const { return hist_k ? hist_capacity : host_capacity; }
+
+    kvmem_hip_host_history host_history() const {
+        kvmem_hip_host_history h{};
+        h.base = host_base;
+        h.n_layers = p.n_layers;
+        h.n_blocks = rt.store().block_count();
+        h.block_tokens = p.block_tokens;
+        h.n_embd_k = n_embd_k;
+        h.n_embd_v = n_embd_v;
+        h.last_block_tokens = last_block_tokens();
+        return h;
+    }
+
     kvmem_hip_history device_history() const {
         kvmem_hip_history h{};
         h.k = hist_k;
@@ -405,8 +421,6 @@ int engine_stage(kvmem_engine *e, const std::vector<uint32_t> &ids,
         return KVMEM_HIP_OK;
     }
     const kvmem_hip_pool pool = e->pool_desc();
-    const uint32_t n_blocks = e->rt.store().block_count();
-    const uint32_t last = e->last_block_tokens();
     std::vector<uint32_t> q_ids, q_slots;
     std::vector<uint32_t> p_ids, p_slots, p_nt;
     for (size_t i = 0; i < ids.size(); ++i) {
@@ -434,14 +448,7 @@ int engine_stage(kvmem_engine *e, const std::vector<uint32_t> &ids,
         return KVMEM_HIP_OK;
     }
     if (e->host_base) {
-        kvmem_hip_host_history h{};
-        h.base = e->host_base;
-        h.n_layers = e->p.n_layers;
-        h.n_blocks = n_blocks;
-        h.block_tokens = e->p.block_tokens;
-        h.n_embd_k = e->n_embd_k;
-        h.n_embd_v = e->n_embd_v;
-        h.last_block_tokens = last;
+        const kvmem_hip_host_history h = e->host_history();
         rc = kvmem_hip_stagein_blocks_host(e->ctx, &h, &pool, q_ids.data(), q_slots.data(),
                                            static_cast<uint32_t>(q_ids.size()));
     } else {
@@ -670,6 +677,9 @@ int kvmem_engine_set_host_history(kvmem_engine *e, const void *pinned_base,
     e->host_base = pinned_base;
     e->host_capacity = pinned_base ? capacity_blocks : 0;
     std::fill(e->packed_valid.begin(), e->packed_valid.end(), 0);  // a new history
+    if (!e->hist_k) {
+        e->meank_valid = 0;  // the key sums come from this history
+    }
     return KVMEM_HIP_OK;
 }
 
@@ -695,7 +705,8 @@ int kvmem_engine_append_tokens(kvmem_engine *e, uint32_t n_new_tokens) {
         return KVMEM_HIP_ERR_INVALID;
     }
     const uint64_t want = static_cast<uint64_t>(e->rt.store().total_tokens()) + n_new_tokens;
-    if (want > static_cast<uint64_t>(e->hist_capacity) * e->p.block_tokens ||
+    if ((!e->hist_k && !e->host_base) ||
+        (e->hist_k && want > static_cast<uint64_t>(e->hist_capacity) * e->p.block_tokens) ||
         (e->host_base && want > static_cast<uint64_t>(e->host_capacity) * e->p.block_tokens)) {
         return e->fail(KVMEM_HIP_ERR_INVALID, "append_tokens: history capacity exceeded");
     }
@@ -879,7 +890,8 @@ int select_topk(kvmem_engine *e, const std::vector<uint32_t> &mand, uint32_t *se
 // call (a partial tail block is summed again once it grows).
 int meank_scores(kvmem_engine *e, const float *q_sum, const uint32_t *q_count) {
     const uint32_t n = e->rt.store().block_count();
-    if (e->meank_cap != e->hist_capacity) {
+    const uint32_t cap = e->sums_capacity();
+    if (e->meank_cap != cap) {
         if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
             return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "mean-K scorer");
         }
@@ -887,21 +899,29 @@ int meank_scores(kvmem_engine *e, const float *q_sum, const uint32_t *q_count) {
         if (e->d_mt) (void) hipFree(e->d_mt);
         e->d_ksum = nullptr;
         e->d_mt = nullptr;
-        const size_t lc = static_cast<size_t>(e->p.n_layers) * e->hist_capacity;
+        const size_t lc = static_cast<size_t>(e->p.n_layers) * cap;
         if (hipMalloc(&e->d_ksum, sizeof(float) * lc * e->n_embd_k) != hipSuccess ||
             hipMalloc(&e->d_mt, sizeof(uint32_t) * lc) != hipSuccess) {
             e->meank_cap = 0;
             return e->fail(KVMEM_HIP_ERR_NOMEM, "mean-K scorer: key sums");
         }
-        e->meank_cap = e->hist_capacity;
+        e->meank_cap = cap;
         e->meank_valid = 0;
     }
-    const kvmem_hip_history h = e->device_history();
     if (e->meank_valid < n) {
         std::vector<uint32_t> ids;
         for (uint32_t b = e->meank_valid; b < n; ++b) ids.push_back(b);
-        const int rc = kvmem_hip_meank_sums(e->ctx, &h, ids.data(), static_cast<uint32_t>(ids.size()),
-                                            e->d_ksum, e->d_mt);
+        int rc;
+        if (e->hist_k) {
+            const kvmem_hip_history h = e->device_history();
+            rc = kvmem_hip_meank_sums(e->ctx, &h, ids.data(), static_cast<uint32_t>(ids.size()), e->d_ksum,
+                                      e->d_mt);
+        } else {
+            // host-only history: the sums are read from the pinned blocks
+            const kvmem_hip_host_history h = e->host_history();
+            rc = kvmem_hip_meank_sums_host(e->ctx, &h, ids.data(), static_cast<uint32_t>(ids.size()), cap,
+                                           e->d_ksum, e->d_mt);
+        }
         if (rc != KVMEM_HIP_OK) {
             return e->fail_ctx(rc, "mean-K key sums");
         }
@@ -915,7 +935,7 @@ int meank_scores(kvmem_engine *e, const float *q_sum, const uint32_t *q_count) {
     a.mean_tokens = e->d_mt;
     a.n_layers = e->p.n_layers;
     a.n_blocks = n;
-    a.capacity_blocks = e->hist_capacity;
+    a.capacity_blocks = cap;
     a.n_head = e->p.n_head;
     a.n_head_kv = e->p.n_head_kv;
     a.head_dim = e->p.head_dim;
@@ -1020,7 +1040,9 @@ int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_
     if (!q || !sel || !n_sel || (n_mandatory && !mandatory)) {
         return e->fail(KVMEM_HIP_ERR_INVALID, "preview: null argument");
     }
-    if (!e->hist_k) {
+    if (!e->hist_k && (e->p.scorer != KVMEM_SCORER_MEAN_K || !e->host_base)) {
+        // the per-token scorer reads every key in HBM; the mean-K scorer
+        // also runs from a pinned host history's key sums
         return e->fail(KVMEM_HIP_ERR_INVALID, "preview: no device history (the scorer reads keys in HBM)");
     }
     const uint32_t n = e->rt.store().block_count();
@@ -1083,8 +1105,8 @@ int kvmem_engine_preview_meank(kvmem_engine *e, const float *q_sum, const uint32
     if (!q_sum || !q_count || !sel || !n_sel || (n_mandatory && !mandatory)) {
         return e->fail(KVMEM_HIP_ERR_INVALID, "preview_meank: null argument");
     }
-    if (!e->hist_k) {
-        return e->fail(KVMEM_HIP_ERR_INVALID, "preview_meank: no device history");
+    if (!e->hist_k && !e->host_base) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "preview_meank: no history");
     }
     const uint32_t n = e->rt.store().block_count();
     *n_sel = 0;

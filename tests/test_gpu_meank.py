@@ -203,3 +203,100 @@ def test_meank_add_decode_running_sum(ctx, oracle, dtype):
     want = oracle.q_accumulate(rows)[0]            # every token in order from zero
     assert np.array_equal(acc.cpu().numpy().view(np.uint32), want.view(np.uint32))
     assert int(cnt.item()) == n_tok
+
+
+def pinned_block_major(k, v):
+    """Host history [block][layer][K rows, V rows] halves in one pinned
+    allocation, from CPU tensors k, v [L][B][T][Hkv][D]."""
+    L_, nb = k.shape[0], k.shape[1]
+    kk = k.permute(1, 0, 2, 3, 4).reshape(nb, L_, -1)
+    vv = v.permute(1, 0, 2, 3, 4).reshape(nb, L_, -1)
+    hb = torch.empty((nb, L_ * (kk.shape[2] + vv.shape[2])), dtype=torch.float16, pin_memory=True)
+    hb.copy_(torch.cat([kk, vv], dim=2).reshape(nb, -1))
+    return hb
+
+
+def test_meank_sums_from_pinned_host_bit_exact(ctx, oracle):
+    """Key sums read by the device from a pinned block-major host history
+    (partial last block, capacity above the block count) equal the
+    oracle's token-order sums bit for bit."""
+    announce("key sums from pinned host blocks: 3 layers x 21 blocks, 50-token tail")
+    L, nb, cap, last = 3, 21, 24, 50
+    k, v, _ = workloads.scoring_tensors(torch, "cpu", L=L, B=nb, Tq=1, seed=61, with_v=True)
+    hb = pinned_block_major(k, v)
+    hh = kv.HostHistory(hb.data_ptr(), L, nb, T, E, E, last)
+    ks = torch.full((L, cap, E), float("nan"), dtype=torch.float32, device="cuda")
+    mt = torch.zeros((L, cap), dtype=torch.int32, device="cuda")
+    ids = [20, 0, 7, 13]
+    torch.cuda.synchronize()
+    ctx.meank_sums_host(hh, ids, ks.data_ptr(), mt.data_ptr(), capacity_blocks=cap)
+    ctx.sync()
+    kb = workloads.to_bits(torch, k)
+    got, got_t = ks.cpu().numpy(), mt.cpu().numpy()
+    for l in range(L):
+        for b in ids:
+            nt = last if b == nb - 1 else T
+            want = oracle.meank_sum_f16(kb[l, b].reshape(T, E)[:nt])
+            assert np.array_equal(got[l, b].view(np.uint32), want.view(np.uint32)), (l, b)
+            assert got_t[l, b] == nt
+
+
+def test_engine_host_only_history_meank(oracle):
+    """The reference's deployment shape: every block in pinned host memory
+    and no key mirror in HBM.  The mean-K scorer runs on key sums the device
+    reads from the pinned blocks; stage-in reads the same blocks.  Scores
+    within 1e-5 of the oracle chain, the selection equal to the oracle's
+    top-k over those scores, pool rows bit-exact -- then the partial tail
+    grows and is summed and staged again."""
+    announce("host-only history: mean-K scorer, 2 layers x 40 blocks")
+    L, nb, cap, Tq, budget = 2, 40, 48, 16, 8
+    k, v, q = workloads.scoring_tensors(torch, "cpu", L=L, B=cap, Tq=Tq, seed=62, with_v=True)
+    hb = pinned_block_major(k, v)
+    qd = q.cuda()
+    kb = workloads.to_bits(torch, k)
+    vb = workloads.to_bits(torch, v)
+    q_sum = oracle.q_accumulate(q.float().numpy().reshape(L, Tq, HQ * D))
+    with host.Engine(n_layers=L, block_tokens=T, n_head=HQ, n_head_kv=HKV, head_dim=D,
+                     budget_blocks=budget, reserve_blocks=4, scorer=1, recent_blocks=1) as eng:
+        eng.set_host_history(hb.data_ptr(), cap)
+        for n_tok in (nb * T - 70, nb * T - 20):
+            if eng.total_tokens() == 0:
+                eng.append_tokens(n_tok)
+            else:
+                eng.append_tokens(n_tok - eng.total_tokens())   # the tail grows by 50 rows
+            last = n_tok - (nb - 1) * T
+            announce(f"{n_tok} tokens, tail block of {last}")
+            sel = eng.preview(qd.data_ptr(), Tq)
+            got = np.array(eng.scores(), dtype=np.float64)
+            sums = np.stack([[oracle.meank_sum_f16(kb[l, b].reshape(T, E)[:(T if b < nb - 1 else last)])
+                              for b in range(nb)] for l in range(L)])
+            mt = np.full((L, nb), T, np.uint32)
+            mt[:, nb - 1] = last
+            want = oracle.score_meank(q_sum, [Tq] * L, sums, mt, HQ, HKV, D)
+            assert np.max(np.abs(got - want)) <= 1e-5
+            assert sel.blocks == oracle.pick_topk(got.astype(np.float32).astype(np.float64), budget,
+                                                  sink=1, recent=1)
+            eng.apply(sel)
+            slots = eng.block_slots()
+            for l in range(L):
+                for which, src in ((0, kb), (1, vb)):
+                    ptr = eng.pool_layer(l)[which]
+                    n = eng.n_slots() * T * 1088
+                    buf = torch.empty(n, dtype=torch.uint8, device="cuda")
+                    c = kv.Context(0)
+                    c.d2d_batched([ptr], [buf.data_ptr()], [n])
+                    c.sync()
+                    c.close()
+                    pool = buf.cpu().numpy().reshape(-1, 1088)
+                    for b in sel.blocks:
+                        nt = T if b < nb - 1 else last
+                        s = slots[b]
+                        want_rows = oracle.quantize_rows_f16(kv.TYPE_Q8_0, src[l, b].reshape(T, E)[:nt])
+                        assert np.array_equal(pool[s * T:s * T + nt], want_rows), (l, which, b)
+        # the per-token scorer needs keys in HBM
+        with pytest.raises(kv.KvMemError):
+            with host.Engine(n_layers=L, block_tokens=T, n_head=HQ, n_head_kv=HKV, head_dim=D,
+                             budget_blocks=budget, reserve_blocks=4) as e2:
+                e2.set_host_history(hb.data_ptr(), cap)
+                e2.append_tokens(nb * T)
+                e2.preview(qd.data_ptr(), Tq)
