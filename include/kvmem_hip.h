@@ -474,6 +474,27 @@ KVMEM_HIP_API int kvmem_hip_meank_add(kvmem_hip_ctx *ctx, const void *k, int32_t
                                       size_t nb2, uint32_t tok0, uint32_t n_keep, int reset,
                                       float *acc, uint32_t *count);
 
+/* Per-token query window (the rows the per-token scorer reads; the
+ * reference keeps only their sum, q_sum_, from the pre-RoPE post-q_norm
+ * query rows of its query span, llama-memory-kvmem.cpp:2157-2172,
+ * 2206-2219).  Write: for i < n, row rows[i] of `window` (device
+ * [capacity][n_head*head_dim] f32, one layer) receives token tokens[i] of
+ * the strided device view q (element (d, h, t) at d*nb0 + h*nb1 + t*nb2
+ * bytes, as ggml lays Qcur out and the reference reads it,
+ * bytes_to_f32_token_major :2066-2090), widened exactly to f32 from F32,
+ * F16 or BF16.  Rows must be distinct within a call. */
+KVMEM_HIP_API int kvmem_hip_q_window_write(kvmem_hip_ctx *ctx, const void *q, int32_t q_type,
+                                           uint32_t n_head, uint32_t head_dim, size_t nb0, size_t nb1,
+                                           size_t nb2, const uint32_t *tokens, const uint32_t *rows,
+                                           uint32_t n, float *window);
+/* Gather: out[l][i][:] = window[l][rows[i]][:] for every layer (window
+ * device [n_layers][capacity][n_embd_q] f32), converted to out_type (BF16
+ * and F16 round to nearest even; F32 copies) -- the [n_layers][n][n_head]
+ * [head_dim] query kvmem_hip_score reads. */
+KVMEM_HIP_API int kvmem_hip_q_window_gather(kvmem_hip_ctx *ctx, const float *window, uint32_t n_layers,
+                                            uint32_t capacity, uint32_t n_embd_q, const uint32_t *rows,
+                                            uint32_t n, int32_t out_type, void *out);
+
 /* The reference's retrieval scorer (llama_memory_kvmem::score_retrieval,
  * src/adapter/llama-memory-kvmem.cpp:2869-2916): per block the mean over
  * layers with query rows of the mean over KV heads of

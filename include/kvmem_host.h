@@ -155,6 +155,13 @@ typedef struct kvmem_engine_params {
                                   22-38): a quantized K (V) cache gets the
                                   Walsh-Hadamard rotation of width
                                   kvmem_hadamard_nrot_k(head_dim) (64) */
+    uint32_t query_max_tokens; /* query window: rows kept per layer, the newest
+                                  (--kvmem-query-max-tokens, default 512,
+                                  tools/llama-kvmem-server.cpp:226, 1089-1096) */
+    uint32_t query_last;       /* with no request / turn span: rows the
+                                  preview takes, the newest captured
+                                  (--kvmem-query-last, default 64,
+                                  tools/llama-kvmem-server.cpp:225, 1032-1038) */
 } kvmem_engine_params;
 
 /* Block scorer of kvmem_engine_preview / apply_retrieval. */
@@ -262,12 +269,36 @@ KVMEM_HIP_API int kvmem_engine_set_turn_spans(kvmem_engine *e, const kvmem_row_r
 KVMEM_HIP_API int kvmem_engine_retrieval_mandatory(const kvmem_engine *e, uint32_t *out,
                                                    uint32_t capacity, uint32_t *n_out);
 
+/* Query capture (the reference's Q harvest, harvest_capture('q') /
+ * harvest_from_host('q'), llama-memory-kvmem.cpp:2157-2172, 2206-2219):
+ * the rows of the strided device view q (pre-RoPE, post-q_norm Qcur of
+ * `layer`: element (d, h, t) at d*nb0 + h*nb1 + t*nb2 bytes, F32 / F16 /
+ * BF16; n_head x head_dim per token) whose position positions[t] (host) is
+ * a query row (query_contains, llama-memory-kvmem.cpp:2950-2955; every row
+ * when no span is set) are widened to f32 into the engine's query window,
+ * a ring of the newest query_max_tokens rows per layer in HBM.  Enqueued on
+ * the engine stream: q stays valid until the next preview / apply returns
+ * or kvmem_hip_sync(kvmem_engine_ctx(e)) does.  Layers are captured
+ * independently but must end up with the same number of rows. */
+KVMEM_HIP_API int kvmem_engine_capture_q(kvmem_engine *e, uint32_t layer, const void *q,
+                                         int32_t q_type, size_t nb0, size_t nb1, size_t nb2,
+                                         uint32_t n_tokens, const int32_t *positions);
+/* Empty the query window (llama_kvmem_reset_query, llama-kvmem-hooks.h:71;
+ * reset_query_acc, llama-memory-kvmem.cpp:2059-2064). */
+KVMEM_HIP_API int kvmem_engine_reset_query(kvmem_engine *e);
+/* Query rows a window preview would read: the newest query_max_tokens
+ * captured rows, or the newest query_last with no span set. */
+KVMEM_HIP_API int kvmem_engine_query_rows(kvmem_engine *e, uint32_t *n_rows);
+
 /* Phase 1 (preview_retrieval): score every block over q (device
  * [n_layers][n_q_tokens][n_head][head_dim], bf16 or f16) with the engine's
  * scorer -- the per-token max, or mean-K cosine over the sum of the
  * n_q_tokens rows (q_count_ = n_q_tokens in every layer) -- then top-k
  * with sink / mandatory / recent charged first: mandatory is the caller's
  * host ids (newest last) followed by kvmem_engine_retrieval_mandatory's.
+ * q = NULL scores the captured query window instead (kvmem_engine_capture_q,
+ * n_q_tokens and q_type ignored): its rows in token order, as bf16 for the
+ * per-token scorer and summed in f32 for mean-K (q_count_ = the rows).
  * Writes the ascending selection (capacity block count), its epoch and rows
  * (history tokens). */
 KVMEM_HIP_API int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type,

@@ -326,7 +326,8 @@ int kvmem_hip_create(int device, kvmem_hip_ctx **out) {
         hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess ||
         hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking) != hipSuccess ||
         !load_ctx_kernels() || !load_meank_kernels() || !load_score_kernels() ||
-        !load_stagein_kernels() || !load_topk_kernels() || !score_scratch_setup(ctx)) {
+        !load_stagein_kernels() || !load_topk_kernels() || !load_qwindow_kernels() ||
+        !score_scratch_setup(ctx)) {
         kvmem_hip_destroy(ctx);
         return KVMEM_HIP_ERR_RUNTIME;
     }

@@ -185,6 +185,7 @@ bool load_meank_kernels();
 bool load_score_kernels();
 bool load_stagein_kernels();
 bool load_topk_kernels();
+bool load_qwindow_kernels();
 // Looks up, once per device (the context's, made current by the caller),
 // the device address of the static scratch array of
 // kvmem_hip_score_noalloc and keeps it in ctx->noalloc_scratch.

@@ -289,6 +289,10 @@ struct kvmem_engine {
     uint32_t meank_cap = 0;    // capacity the sums are allocated for
     uint32_t meank_valid = 0;  // leading blocks whose sums are current
     float *d_qsum = nullptr;   // query sums [L][n_head*head_dim] (mean-K scorer)
+    float *d_qwin = nullptr;   // query window [L][qwin_cap][n_head*head_dim] f32
+    void *d_qgather = nullptr; // its rows in token order for the scorer, bf16
+    uint32_t qwin_cap = 0;
+    std::vector<uint64_t> qwin_count;  // rows captured per layer since the reset
     void *packed_base = nullptr;        // pinned packed host store (may be null)
     uint32_t packed_capacity = 0;       // blocks it holds
     std::vector<uint8_t> packed_valid;  // block's packed rows are in the store
@@ -316,6 +320,7 @@ struct kvmem_engine {
         }
         return rt.store().blocks_overlapping(ranges, force_pos);
     }
+    bool spans_set() const { return explicit_spans || query_begin >= 0; }
     // query_contains (llama-memory-kvmem.cpp:2950-2955): a row of the query
     bool query_contains(int32_t row) const {
         if (!explicit_spans) {
@@ -546,6 +551,8 @@ kvmem_engine_params kvmem_engine_default_params(void) {
     p.rope_freq_base = 10000.0f;
     p.rope_freq_scale = 1.0f;
     p.attn_rot = 0;
+    p.query_max_tokens = 512;
+    p.query_last = 64;
     return p;
 }
 
@@ -568,6 +575,10 @@ int kvmem_engine_create(const kvmem_engine_params *pp, kvmem_engine **out) {
     }
     e->n_embd_k = p.n_head_kv * p.head_dim;
     e->n_embd_v = p.n_embd_v ? p.n_embd_v : e->n_embd_k;
+    if (e->p.query_max_tokens == 0) e->p.query_max_tokens = 512;  // zero-initialised params
+    if (e->p.query_last == 0) e->p.query_last = 64;
+    e->qwin_cap = e->p.query_max_tokens;
+    e->qwin_count.assign(p.n_layers, 0);
     if (e->n_embd_v % 32 != 0) {
         delete e;
         return KVMEM_HIP_ERR_INVALID;
@@ -615,6 +626,12 @@ void kvmem_engine_destroy(kvmem_engine *e) {
     }
     if (e->d_mt) {
         (void) hipFree(e->d_mt);
+    }
+    if (e->d_qwin) {
+        (void) hipFree(e->d_qwin);
+    }
+    if (e->d_qgather) {
+        (void) hipFree(e->d_qgather);
     }
     kvmem_hip_destroy(e->ctx);
     delete e;
@@ -985,6 +1002,29 @@ int rollback(kvmem_engine *e, ApplyUndo &u, int code) {
     return code;
 }
 
+// The query window rows a preview reads, oldest first: the newest
+// query_max_tokens captured rows (query_last when no span is set; the
+// server's clamp and fallback, tools/llama-kvmem-server.cpp:1032-1038,
+// 1089-1096).  Every layer must hold the same number of rows.
+int window_rows(kvmem_engine *e, std::vector<uint32_t> &rows) {
+    rows.clear();
+    const uint64_t c = e->qwin_count.empty() ? 0 : e->qwin_count[0];
+    for (uint64_t x : e->qwin_count) {
+        if (x != c) {
+            return e->fail(KVMEM_HIP_ERR_INVALID, "query window: layers hold different numbers of rows");
+        }
+    }
+    const uint64_t limit = e->spans_set() ? e->qwin_cap : std::min<uint32_t>(e->qwin_cap, e->p.query_last);
+    const uint64_t n = std::min<uint64_t>(c, limit);
+    if (n == 0) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "query window: no query rows captured");
+    }
+    for (uint64_t i = c - n; i < c; ++i) {
+        rows.push_back(static_cast<uint32_t>(i % e->qwin_cap));
+    }
+    return KVMEM_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1037,7 +1077,7 @@ int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_
     if (!e) {
         return KVMEM_HIP_ERR_INVALID;
     }
-    if (!q || !sel || !n_sel || (n_mandatory && !mandatory)) {
+    if (!sel || !n_sel || (n_mandatory && !mandatory)) {
         return e->fail(KVMEM_HIP_ERR_INVALID, "preview: null argument");
     }
     if (!e->hist_k && (e->p.scorer != KVMEM_SCORER_MEAN_K || !e->host_base)) {
@@ -1049,6 +1089,15 @@ int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_
     *n_sel = 0;
     if (epoch) *epoch = e->epoch;
     if (rows) *rows = e->rt.store().total_tokens();
+    // no query pointer: the captured query window, its newest rows in token order
+    std::vector<uint32_t> win_rows;
+    if (!q) {
+        const int rc = window_rows(e, win_rows);
+        if (rc != KVMEM_HIP_OK) {
+            return rc;
+        }
+        n_q_tokens = static_cast<uint32_t>(win_rows.size());
+    }
     if (n == 0) {
         return KVMEM_HIP_OK;
     }
@@ -1058,16 +1107,19 @@ int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_
     std::vector<uint32_t> mand(mandatory, mandatory + n_mandatory);
     const std::vector<uint32_t> spans = e->retrieval_mandatory();
     mand.insert(mand.end(), spans.begin(), spans.end());
+    const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
     if (!e->rt.store().charge_topk(mand).all_fit && e->p.scorer == KVMEM_SCORER_MEAN_K) {
         // the reference's scorer over the sum of the query rows
-        const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
         if (!e->d_qsum &&
             hipMalloc(&e->d_qsum, sizeof(float) * e->p.n_layers * n_embd_q) != hipSuccess) {
             e->d_qsum = nullptr;
             return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: query sums");
         }
-        int rc = kvmem_hip_q_accumulate(e->ctx, q, q_type, e->p.n_layers, n_q_tokens, n_embd_q,
-                                        nullptr, 0, 1, e->d_qsum);
+        int rc = q ? kvmem_hip_q_accumulate(e->ctx, q, q_type, e->p.n_layers, n_q_tokens, n_embd_q, nullptr,
+                                            0, 1, e->d_qsum)
+                   // the window's rows summed in token order, as the harvest adds them
+                   : kvmem_hip_q_accumulate(e->ctx, e->d_qwin, KVMEM_TYPE_F32, e->p.n_layers, e->qwin_cap,
+                                            n_embd_q, win_rows.data(), n_q_tokens, 1, e->d_qsum);
         if (rc != KVMEM_HIP_OK) {
             return e->fail_ctx(rc, "preview query sums");
         }
@@ -1077,6 +1129,22 @@ int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_
             return rc;
         }
     } else if (!e->rt.store().charge_topk(mand).all_fit) {
+        if (!q) {
+            // the window's rows in token order, as the bf16 query the scorer reads
+            const size_t bytes = 2u * static_cast<size_t>(e->p.n_layers) * e->qwin_cap * n_embd_q;
+            if (!e->d_qgather && hipMalloc(&e->d_qgather, bytes) != hipSuccess) {
+                e->d_qgather = nullptr;
+                return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: query window gather buffer");
+            }
+            const int rc = kvmem_hip_q_window_gather(e->ctx, e->d_qwin, e->p.n_layers, e->qwin_cap, n_embd_q,
+                                                     win_rows.data(), n_q_tokens, KVMEM_TYPE_BF16,
+                                                     e->d_qgather);
+            if (rc != KVMEM_HIP_OK) {
+                return e->fail_ctx(rc, "preview query window");
+            }
+            q = e->d_qgather;
+            q_type = KVMEM_TYPE_BF16;
+        }
         const kvmem_hip_history h = e->device_history();
         kvmem_hip_score_args a{};
         a.q = q;
@@ -1094,6 +1162,69 @@ int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_
         }
     }
     return select_topk(e, mand, sel, n_sel);
+}
+
+int kvmem_engine_capture_q(kvmem_engine *e, uint32_t layer, const void *q, int32_t q_type, size_t nb0,
+                           size_t nb1, size_t nb2, uint32_t n_tokens, const int32_t *positions) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (layer >= e->p.n_layers || (n_tokens && (!q || !positions))) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "capture_q: bad layer or null argument");
+    }
+    // the rows of the query (all of them when no span is set: the preview
+    // then takes the newest query_last)
+    std::vector<uint32_t> kept;
+    for (uint32_t i = 0; i < n_tokens; ++i) {
+        if (!e->spans_set() || e->query_contains(positions[i])) {
+            kept.push_back(i);
+        }
+    }
+    if (kept.empty()) {
+        return KVMEM_HIP_OK;
+    }
+    const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
+    if (!e->d_qwin) {
+        const size_t bytes = sizeof(float) * static_cast<size_t>(e->p.n_layers) * e->qwin_cap * n_embd_q;
+        if (hipMalloc(&e->d_qwin, bytes) != hipSuccess) {
+            e->d_qwin = nullptr;
+            return e->fail(KVMEM_HIP_ERR_NOMEM, "capture_q: query window");
+        }
+    }
+    // ring of qwin_cap rows: only the newest qwin_cap of this call are written
+    uint64_t &count = e->qwin_count[layer];
+    const size_t skip = kept.size() > e->qwin_cap ? kept.size() - e->qwin_cap : 0;
+    std::vector<uint32_t> tokens, rows;
+    for (size_t j = skip; j < kept.size(); ++j) {
+        tokens.push_back(kept[j]);
+        rows.push_back(static_cast<uint32_t>((count + j) % e->qwin_cap));
+    }
+    const int rc = kvmem_hip_q_window_write(e->ctx, q, q_type, e->p.n_head, e->p.head_dim, nb0, nb1, nb2,
+                                            tokens.data(), rows.data(), static_cast<uint32_t>(tokens.size()),
+                                            e->d_qwin + static_cast<size_t>(layer) * e->qwin_cap * n_embd_q);
+    if (rc != KVMEM_HIP_OK) {
+        return e->fail_ctx(rc, "capture_q");
+    }
+    count += kept.size();
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_reset_query(kvmem_engine *e) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    std::fill(e->qwin_count.begin(), e->qwin_count.end(), 0);
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_query_rows(kvmem_engine *e, uint32_t *n_rows) {
+    if (!e || !n_rows) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    std::vector<uint32_t> r;
+    const int rc = window_rows(e, r);
+    *n_rows = static_cast<uint32_t>(r.size());
+    return rc;
 }
 
 int kvmem_engine_preview_meank(kvmem_engine *e, const float *q_sum, const uint32_t *q_count,

@@ -48,7 +48,8 @@ class EngineParams(C.Structure):
                 ("recent_blocks", C.c_uint32), ("type_k", C.c_int32), ("type_v", C.c_int32),
                 ("tie_lower_index", C.c_int32), ("layer_reduce", C.c_int32),
                 ("canonical_layout", C.c_int32), ("scorer", C.c_int32), ("n_rot", C.c_uint32),
-                ("rope_freq_base", C.c_float), ("rope_freq_scale", C.c_float), ("attn_rot", C.c_int32)]
+                ("rope_freq_base", C.c_float), ("rope_freq_scale", C.c_float), ("attn_rot", C.c_int32),
+                ("query_max_tokens", C.c_uint32), ("query_last", C.c_uint32)]
 
 
 _bound = set()
@@ -82,6 +83,9 @@ def bind(lib: C.CDLL) -> C.CDLL:
     sig("kvmem_engine_set_request_span", i32, vp, C.c_int32, C.c_int32, C.c_int32)
     sig("kvmem_engine_set_turn_spans", i32, vp, C.POINTER(RowRange), u32, C.POINTER(RowRange), u32)
     sig("kvmem_engine_retrieval_mandatory", i32, vp, pu32, u32, pu32)
+    sig("kvmem_engine_capture_q", i32, vp, u32, vp, i32, C.c_size_t, C.c_size_t, C.c_size_t, u32, pi32)
+    sig("kvmem_engine_reset_query", i32, vp)
+    sig("kvmem_engine_query_rows", i32, vp, pu32)
     sig("kvmem_engine_default_params", EngineParams)
     sig("kvmem_engine_create", i32, C.POINTER(EngineParams), C.POINTER(vp))
     sig("kvmem_engine_destroy", None, vp)
@@ -325,6 +329,31 @@ class Engine:
         self.check(self.lib.kvmem_engine_retrieval_mandatory(self.h, out, cap, C.byref(n)),
                    "retrieval_mandatory")
         return list(out[: n.value])
+
+    def capture_q(self, layer: int, q_ptr: int, q_type: int, nb0: int, nb1: int, nb2: int,
+                  positions: Sequence[int]) -> None:
+        """Query rows of one layer's strided Qcur view, at these positions."""
+        pos = (C.c_int32 * max(1, len(positions)))(*[int(p) for p in positions])
+        self.check(self.lib.kvmem_engine_capture_q(self.h, layer, q_ptr, q_type, nb0, nb1, nb2,
+                                                   len(positions), pos), "capture_q")
+
+    def reset_query(self) -> None:
+        self.check(self.lib.kvmem_engine_reset_query(self.h), "reset_query")
+
+    def query_rows(self) -> int:
+        n = C.c_uint32(0)
+        self.check(self.lib.kvmem_engine_query_rows(self.h, C.byref(n)), "query_rows")
+        return n.value
+
+    def preview_window(self, mandatory: Sequence[int] = ()) -> Selection:
+        """Preview over the captured query window (q = NULL)."""
+        m, nm = _u32(mandatory)
+        out = (C.c_uint32 * max(1, self.block_count()))()
+        n, rows = C.c_uint32(0), C.c_uint32(0)
+        ep = C.c_uint64(0)
+        self.check(self.lib.kvmem_engine_preview(self.h, None, TYPE_BF16, 0, m, nm, out, C.byref(n),
+                                                 C.byref(ep), C.byref(rows)), "preview (query window)")
+        return Selection(ep.value, rows.value, list(out[: n.value]))
 
     def block_slots(self) -> list:
         n = self.block_count()

@@ -1,0 +1,165 @@
+"""The engine's per-token query window on the GPU.
+
+Query rows of strided Qcur views (F32 / F16 / BF16, padded head stride)
+are captured per layer over several ubatches, kept by the request span
+(the reference's query_contains), capped to the newest query_max_tokens
+rows, or the newest query_last when no span is set.  A preview over the
+window must equal a preview over the same rows passed explicitly (bit for
+bit: the same scorer input), and the oracle chain: per-token max scores
+within 1e-3 relative of the fp64 oracle on the bf16-rounded rows; mean-K
+scores within 1e-5 of the oracle over the f32 row sums in token order.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from conftest import load_pkg  # noqa: E402
+
+kv = load_pkg()
+from kvmem_amd import host, workloads  # noqa: E402
+
+L, T, HKV, HQ, D = 2, 128, 4, 24, 256
+E = HKV * D
+EQ = HQ * D
+PAD = 8
+DTYPES = {"f32": (torch.float32, kv.TYPE_F32), "f16": (torch.float16, kv.TYPE_F16),
+          "bf16": (torch.bfloat16, kv.TYPE_BF16)}
+
+
+def announce(msg: str) -> None:
+    print(f"[qwindow] {msg}", flush=True)
+
+
+def engine(**kw):
+    p = dict(n_layers=L, block_tokens=T, n_head=HQ, n_head_kv=HKV, head_dim=D, budget_blocks=8,
+             reserve_blocks=4)
+    p.update(kw)
+    return host.Engine(**p)
+
+
+class Capture:
+    """Seeded Qcur ubatches: per layer a padded [n][HQ][D + PAD] tensor of
+    `dtype`; `rows(layer, positions)` gives the captured rows as f32."""
+
+    def __init__(self, dtype: str, seed: int):
+        self.tdt, self.code = DTYPES[dtype]
+        self.g = torch.Generator(device="cpu").manual_seed(seed)
+        self.by_pos = {}
+
+    def ubatch(self, eng, pos0: int, n: int):
+        positions = list(range(pos0, pos0 + n))
+        for layer in range(L):
+            x = (torch.randn((n, HQ, D + PAD), generator=self.g) * 2).to(self.tdt)
+            for i, p in enumerate(positions):
+                self.by_pos[(layer, p)] = x[i, :, :D].float().reshape(EQ).numpy()
+            xd = x.cuda()
+            esz = xd.element_size()
+            torch.cuda.synchronize()
+            eng.capture_q(layer, xd.data_ptr(), self.code, esz, (D + PAD) * esz, HQ * (D + PAD) * esz,
+                          positions)
+            kv.Context.borrow(eng.ctx_handle()).sync()   # the view is freed after this
+
+    def rows(self, positions) -> np.ndarray:
+        """[L][len][HQ][D] f32 rows at these positions."""
+        return np.stack([[self.by_pos[(layer, p)] for p in positions] for layer in range(L)]).reshape(
+            L, len(positions), HQ, D)
+
+
+def explicit_q(rows_f32: np.ndarray):
+    """The same rows as the bf16 device query kvmem_engine_preview takes."""
+    return torch.from_numpy(np.ascontiguousarray(rows_f32)).to(torch.bfloat16).cuda()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_window_span_per_token_scorer(oracle, dtype):
+    announce(f"request span [100, 160) over 3 ubatches of {dtype} Qcur")
+    cap, nb = 40, 40
+    k, v, _ = workloads.scoring_tensors(torch, "cuda", L=L, B=cap, Tq=1, seed=71, with_v=True)
+    with engine() as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        eng.set_request_span(100, 160, -1)
+        cp = Capture(dtype, 72)
+        for p0, n in ((64, 64), (128, 64), (192, 8)):
+            cp.ubatch(eng, p0, n)
+        assert eng.query_rows() == 60
+        sel = eng.preview_window()
+        got = np.array(eng.scores(), dtype=np.float64)
+        rows = cp.rows(range(100, 160))
+        qe = explicit_q(rows)
+        torch.cuda.synchronize()
+        sel2 = eng.preview(qe.data_ptr(), 60)
+        got2 = np.array(eng.scores(), dtype=np.float64)
+        assert sel.blocks == sel2.blocks and np.array_equal(got, got2)
+        qb = qe.float().cpu().numpy()                      # the bf16-rounded rows
+        want = oracle.combine_layers(oracle.score_pertoken_max(qb, workloads.to_bits(torch, k)), 0)
+        assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-6)) <= 1e-3
+        mand = eng.retrieval_mandatory()
+        assert mand == [0, 1]
+        assert sel.blocks == oracle.pick_topk(got.astype(np.float32).astype(np.float64), 8, sink=1,
+                                              mandatory=mand)
+
+
+def test_window_meank_scorer_sums_in_token_order(oracle):
+    announce("mean-K scorer over the window: f32 sums in token order")
+    cap, nb = 40, 40
+    k, v, _ = workloads.scoring_tensors(torch, "cuda", L=L, B=cap, Tq=1, seed=73, with_v=True)
+    with engine(scorer=1) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        eng.set_turn_spans(query=[(10, 30), (50, 70)], mandatory=[])
+        cp = Capture("f32", 74)
+        cp.ubatch(eng, 0, 40)
+        cp.ubatch(eng, 40, 40)
+        assert eng.query_rows() == 40
+        sel = eng.preview_window()
+        got = np.array(eng.scores(), dtype=np.float64)
+        pos = list(range(10, 30)) + list(range(50, 70))
+        q_sum = oracle.q_accumulate(cp.rows(pos).reshape(L, 40, EQ))
+        kb = workloads.to_bits(torch, k)
+        sums = np.stack([[oracle.meank_sum_f16(kb[l, b].reshape(T, E)) for b in range(nb)]
+                         for l in range(L)])
+        want = oracle.score_meank(q_sum, [40] * L, sums, np.full((L, nb), T, np.uint32), HQ, HKV, D)
+        assert np.max(np.abs(got - want)) <= 1e-5
+        assert sel.blocks == oracle.pick_topk(got.astype(np.float32).astype(np.float64), 8, sink=1)
+
+
+def test_window_cap_and_query_last_fallback(oracle):
+    announce("cap 32 keeps the newest rows; no span: the newest query_last = 24")
+    cap, nb = 40, 40
+    k, v, _ = workloads.scoring_tensors(torch, "cuda", L=L, B=cap, Tq=1, seed=75, with_v=True)
+    with engine(query_max_tokens=32, query_last=24) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        cp = Capture("bf16", 76)
+        for p0 in (0, 20, 40):                              # no span: every row captured
+            cp.ubatch(eng, p0, 20)
+        assert eng.query_rows() == 24
+        sel = eng.preview_window()
+        got = np.array(eng.scores(), dtype=np.float64)
+        qe = explicit_q(cp.rows(range(36, 60)))
+        torch.cuda.synchronize()
+        assert eng.preview(qe.data_ptr(), 24).blocks == sel.blocks
+        assert np.array_equal(np.array(eng.scores(), dtype=np.float64), got)
+        eng.reset_query()
+        eng.set_request_span(5, 0, -1)                      # open-ended span: rows 5.. (then capped)
+        for p0 in (0, 20):
+            cp.ubatch(eng, p0, 20)
+        assert eng.query_rows() == 32                       # 35 rows kept, the newest 32 read
+        sel = eng.preview_window()
+        got = np.array(eng.scores(), dtype=np.float64)
+        qe = explicit_q(cp.rows(range(8, 40)))
+        torch.cuda.synchronize()
+        assert eng.preview(qe.data_ptr(), 32).blocks == sel.blocks
+        assert np.array_equal(np.array(eng.scores(), dtype=np.float64), got)
+        # one layer ahead of the other, then an empty window: refused
+        x = torch.zeros((1, HQ, D), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        eng.capture_q(0, x.data_ptr(), kv.TYPE_F32, 4, D * 4, HQ * D * 4, [39])
+        with pytest.raises(kv.KvMemError):
+            eng.preview_window()
+        eng.reset_query()
+        with pytest.raises(kv.KvMemError):
+            eng.query_rows()
