@@ -258,8 +258,10 @@ class Context:
                 self.lib.kvmem_hip_destroy(self.h)
             self.h = None
 
-    def __del__(self):
-        if sys.is_finalizing():
+    def __del__(self, _finalizing=sys.is_finalizing):
+        # bound at definition: module globals (sys among them) may already be
+        # gone when an object is collected during interpreter shutdown
+        if _finalizing():
             return
         try:
             self.close()

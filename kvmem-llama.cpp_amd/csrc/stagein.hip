@@ -918,6 +918,465 @@ __global__ __launch_bounds__(256) void quant_scatter_kv_kernel(BlockSource sk, B
     }
 }
 
+// ------------------------------------------ transformed rows, 64 per lane
+//
+// The transformed path above gives each lane 8 elements, so most butterfly
+// stages and every quantization group span lanes, and each cross-lane step
+// costs an exchange, a sign and an add per element.  This path gives each
+// lane 64 consecutive elements of a row (two quantization groups) and a
+// wave a unit of 4096 consecutive elements of an operation; a workgroup
+// takes one unit of one block for every layer, wave w the layers w, w + 4,
+// ... (four workgroups per CU hide each other's load latency).  Loads
+// stay coalesced (16 bytes per lane, 1 KiB per wave-wide load) and are
+// redistributed through the wave's LDS with a lane stride of 136 bytes
+// (8-byte halves of consecutive lanes fall on distinct banks on both sides,
+// and every address is one base plus an immediate offset).  Then:
+//  - Hadamard spans 1 .. 32 are butterflies inside the lane; spans 64, 128
+//    and 256 pair lane l with l ^ 1, ^ 2, ^ 4.  A cross-lane stage is one
+//    fused multiply-add per element, y = fma(partner, t, own) with t = -1
+//    in the lane that holds the upper element: fma(p, +-1, y) rounds y +- p
+//    once, as the IEEE sum does, and the upper lane then holds the negation
+//    of its value (round to nearest even is odd-symmetric).  After the
+//    stages a lane holds sigma * x with sigma = (-1)^(its cross-lane bits),
+//    folded into the quantizer: the scale reads |x| and the codes are
+//    y * (sigma * id) = x * id.  Only the sign of an exact zero can differ,
+//    which q8_0, q4_0 and q5_0 never show; F16 rows with cross-lane stages
+//    take the path above.
+//  - A Hadamard scale that is a power of two (widths 64 and 256: 1/8,
+//    1/16) is not applied to the elements.  Every nonzero value of the
+//    transform lies between 2^-100 and 2^40 in magnitude (f16 inputs,
+//    products with cos/sin rounded to 24 bits, rounded sums of those), so
+//    scaling by a power of two commutes with every rounded operation; the
+//    quantizer scales amax (exactly) and multiplies id by the scale
+//    (exactly) instead.  1/sqrtf(128) and 1/sqrtf(512) are inexact and
+//    scale the elements first, as the reference does.
+//  - RoPE (n_rot 128 and 256): a rotary pair lies in lanes l and
+//    l ^ n_rot/128, and an element becomes fma(partner * sin, t, own * cos),
+//    t = -1 in the first half: the two rounded products and the one rounded
+//    sum of x0*c - x1*s and x0*s + x1*c.  Partners (here and for the
+//    butterflies) come through ds_bpermute, off the vector ALU.
+//  - The cos/sin table of the unit's rows is built once per workgroup for
+//    all the layers.
+constexpr uint32_t kX64Lane = 136;              // LDS bytes per lane: 128 + 8
+constexpr uint32_t kX64Wave = 64u * kX64Lane;   // LDS bytes of one wave
+constexpr uint32_t kX64Groups = 128; // groups of 32 elements in a unit
+
+// cos/sin table of rotary pairs (n_rot = 2 * half, half 64 or 128) in
+// 16-byte units of two pairs (c_j, s_j, c_j+1, s_j+1).  A lane reads P = 64
+// consecutive pairs; a row holds half / P runs of P/2 units, each followed
+// by one unused unit, so that the rows and runs one wave-wide read touches
+// fall on distinct banks.
+struct X64Tab {
+    uint32_t P, JS, RS;  // pairs per run, units per run (+1), units per row
+};
+__host__ __device__ inline X64Tab x64_tab_geom(uint32_t half) {
+    const uint32_t P = half < 64u ? half : 64u;
+    const uint32_t JS = P / 2u + 1u;
+    return {P, JS, (half / P) * JS};
+}
+
+// A unit's 16-byte loads: load k of lane i holds elements 512k + 8i .. +7
+// of the 4096, owned by lane 8k + i/8.  Loads owned by lanes past the
+// operation's end are not issued.
+__device__ inline void x64_load(const Chunk &c, uint32_t lane, uint32_t nvl, uint4 v[8]) {
+    const uint8_t *base = c.src + static_cast<uint64_t>(c.g0) * 64u + lane * 16u;
+    if (nvl == 64u) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            v[k] = load_stream16(base + k * 1024);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            v[k] = make_uint4(0u, 0u, 0u, 0u);
+            if (8u * k + (lane >> 3) < nvl) {
+                v[k] = load_stream16(base + k * 1024);
+            }
+        }
+    }
+}
+
+__device__ inline void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The value of lane ^ m (m uniform) through ds_bpermute, on the LDS pipe.
+__device__ inline float x64_partner(float v, uint32_t src_addr) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(static_cast<int>(src_addr), __float_as_int(v)));
+}
+
+// v_fma_mix_f32 on the f16 halves of a packed pair: an f16 operand is
+// widened exactly, so fma(lo, 1, hi) rounds lo + hi once (the IEEE sum of
+// the widened values), fma(hi, -1, lo) is lo - hi and fma(h, c, -0) is the
+// product h * c rounded once (-0 keeps the sign of a zero product).  The
+// widening then costs no instruction of its own.
+__device__ inline float mix_sum(uint32_t w) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, 1.0, %1 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(w));
+    return r;
+}
+__device__ inline float mix_diff(uint32_t w) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %1 op_sel:[1,0,0] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(w));
+    return r;
+}
+template <int HI>
+__device__ inline float mix_mul(uint32_t w, float c, float nz) {
+    float r;
+    if constexpr (HI) {
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(c), "v"(nz));
+    } else {
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(c), "v"(nz));
+    }
+    return r;
+}
+
+// RoPE of pairs across lanes (src_addr = 4 * the partner lane) straight from
+// the packed f16 words (word u: elements 2u, 2u + 1), one exchange per word.
+__device__ inline void x64_rope_f16(float x[64], const uint32_t w[32], const float4 *t, float tr,
+                                    uint32_t src_addr) {
+    const float nz = -0.0f;
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+        const float4 cs = t[u];  // pairs of elements 2u (x: cos, y: sin) and 2u + 1 (z, w)
+        const uint32_t pw = static_cast<uint32_t>(
+            __builtin_amdgcn_ds_bpermute(static_cast<int>(src_addr), static_cast<int>(w[u])));
+        const float p0 = mix_mul<0>(pw, cs.y, nz);
+        const float p1 = mix_mul<1>(pw, cs.w, nz);
+        const float a0 = mix_mul<0>(w[u], cs.x, nz);
+        const float a1 = mix_mul<1>(w[u], cs.z, nz);
+        x[2 * u] = __builtin_fmaf(p0, tr, a0);
+        x[2 * u + 1] = __builtin_fmaf(p1, tr, a1);
+    }
+}
+
+// vmax of q4_0 / q5_0 (first element of largest magnitude, ggml's strict
+// scan) of group y[0..31] as held: +0 for an all-zero group.
+__device__ inline float x64_vmax(const float *y) {
+    float mx = 0.0f, mn = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        mx = fmaxf(mx, y[i]);
+        mn = fminf(mn, y[i]);
+    }
+    const float a = fmaxf(mx, -mn);
+    if (a == 0.0f) {
+        return 0.0f;
+    }
+    if (mx == a && -mn == a) {  // both signs reach amax: the first one wins
+        uint32_t neg = 0u;
+#pragma unroll
+        for (int i = 31; i >= 0; --i) {
+            if (fabsf(y[i]) == a) {
+                neg = __float_as_uint(y[i]) >> 31;
+            }
+        }
+        return neg ? -a : a;
+    }
+    return mx == a ? a : -a;
+}
+
+// Codes of one q4_0 / q5_0 group as bytes: word m holds codes 4m .. 4m+3
+// (lo) and 16+4m .. 16+4m+3 (hi).
+template <int TOP>
+__device__ inline void x64_trunc_codes(const float *y, float idf, float bias, uint32_t lo[4],
+                                       uint32_t hi[4]) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        lo[m] = 0u;
+        hi[m] = 0u;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            lo[m] |= trunc_code<TOP>(y[4 * m + b], idf, bias) << (8 * b);
+            hi[m] |= trunc_code<TOP>(y[16 + 4 * m + b], idf, bias) << (8 * b);
+        }
+    }
+}
+
+// Quantize one group (32 values y held as sigma * x / scale; f = sigma *
+// scale, sf = scale) into its f16 scale bits and P payload words.
+template <int TYPE> struct X64Q;
+
+template <> struct X64Q<KVMEM_TYPE_Q8_0> {
+    static constexpr int P = 8;
+    __device__ static inline uint32_t group(const float *y, float f, float sf, uint32_t w[P]) {
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            a = fmaxf(a, fabsf(y[i]));
+        }
+        const float d = scale_div127(a * sf);
+        const float id = d != 0.0f ? scale_recip(d) : 0.0f;
+        const float idf = id * f;
+#pragma unroll
+        for (int m = 0; m < P; ++m) {
+            w[m] = 0u;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                w[m] |= (static_cast<uint32_t>(round_q8(y[4 * m + b] * idf)) & 0xffu) << (8 * b);
+            }
+        }
+        return float_to_half_bits(d);
+    }
+};
+
+template <> struct X64Q<KVMEM_TYPE_Q4_0> {
+    static constexpr int P = 4;
+    __device__ static inline uint32_t group(const float *y, float f, float, uint32_t w[P]) {
+        const float vm = x64_vmax(y);
+        const float d = (vm != 0.0f ? vm * f : 0.0f) * -0.125f;  // vmax of x / -8, both exact
+        const float id = d != 0.0f ? scale_recip(d) : 0.0f;
+        uint32_t lo[4], hi[4];
+        x64_trunc_codes<15>(y, id * f, 8.5f, lo, hi);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            w[m] = lo[m] | (hi[m] << 4);
+        }
+        return float_to_half_bits(d);
+    }
+};
+
+template <> struct X64Q<KVMEM_TYPE_Q5_0> {
+    static constexpr int P = 5;
+    __device__ static inline uint32_t group(const float *y, float f, float, uint32_t w[P]) {
+        const float vm = x64_vmax(y);
+        const float d = (vm != 0.0f ? vm * f : 0.0f) * -0.0625f;  // vmax of x / -16, both exact
+        const float id = d != 0.0f ? scale_recip(d) : 0.0f;
+        uint32_t lo[4], hi[4];
+        x64_trunc_codes<31>(y, id * f, 16.5f, lo, hi);
+        uint32_t qh = 0u;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            qh |= (bit4_of_bytes(lo[m]) << (4 * m)) | (bit4_of_bytes(hi[m]) << (16 + 4 * m));
+            w[1 + m] = (lo[m] & 0x0f0f0f0fu) | ((hi[m] & 0x0f0f0f0fu) << 4);
+        }
+        w[0] = qh;
+        return float_to_half_bits(d);
+    }
+};
+
+// The lane's two groups in ggml's byte layout as 2 * GB / 4 words (GB is 2
+// mod 4: the second group starts two bytes into a word).
+template <int TYPE>
+__device__ inline void x64_quant_lane(const float x[64], float f, float sf, uint32_t *dst) {
+    if constexpr (TYPE == KVMEM_TYPE_F16) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            dst[i] = float_to_half_bits(x[2 * i]) | (float_to_half_bits(x[2 * i + 1]) << 16);
+        }
+    } else {
+        constexpr int P = X64Q<TYPE>::P;
+        uint32_t w0[P], w1[P];
+        const uint32_t d0 = X64Q<TYPE>::group(x, f, sf, w0);
+        const uint32_t d1 = X64Q<TYPE>::group(x + 32, f, sf, w1);
+        dst[0] = d0 | (w0[0] << 16);
+#pragma unroll
+        for (int m = 1; m < P; ++m) {
+            dst[m] = __builtin_amdgcn_alignbit(w0[m], w0[m - 1], 16);
+        }
+        dst[P] = (w0[P - 1] >> 16) | (d1 << 16);
+#pragma unroll
+        for (int m = 0; m < P; ++m) {
+            dst[P + 1 + m] = w1[m];
+        }
+    }
+}
+
+// Workgroup `c` of a block source on this path: unit `sub` (groups g0 ..
+// g0+ng, ng <= 128) of one block, wave w taking layers w, w + 4, ...
+template <int TYPE>
+__device__ inline void x64_unit_layers(const BlockSource &s, uint32_t c, uint8_t *lds, uint8_t *tab) {
+    constexpr int GB = Fmt<TYPE>::GB;
+    const uint32_t item = c / s.chunks_per_op;
+    const uint32_t sub = c - item * s.chunks_per_op;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
+    const uint32_t lane = tid & 63u;
+    // the item's fields, read once (uniform): block, slot, tokens, position
+    const uint32_t block = s.items[4 * item + 0];
+    const uint32_t slot = s.items[4 * item + 1];
+    Chunk ch;
+    ch.pos0 = static_cast<int32_t>(s.items[4 * item + 3]);
+    ch.gpr = s.gpr;
+    ch.src_stride = s.gpr * 64u;
+    ch.g0 = sub * kX64Groups;
+    const uint32_t total = s.items[4 * item + 2] * s.gpr;
+    if (ch.g0 >= total) {
+        return;  // uniform: no rows in this unit
+    }
+    ch.ng = min(kX64Groups, total - ch.g0);
+    const uint8_t *src0 = s.base + block * s.block_stride;
+    const uint64_t dst_off = static_cast<uint64_t>(slot) * s.block_tokens * s.row_bytes;
+    const uint32_t nvl = min(64u, ch.ng / 2u);  // lanes with elements (ng is even)
+    uint8_t *wl = lds + wave * kX64Wave;
+
+    // the lane's place: row, offset in its head
+    const uint32_t E = s.gpr * 32u;
+    const uint32_t e = (ch.g0 + 2u * lane) * 32u;
+    const uint32_t row = e / E;
+    const uint32_t d0 = (e - row * E) & (s.head_dim - 1u);
+    const uint32_t row0 = ch.g0 / ch.gpr;
+    const uint32_t half = s.n_rot / 2u;
+    const X64Tab tg = x64_tab_geom(half);
+    if (half != 0u) {
+        const uint32_t rows = (ch.g0 + ch.ng - 1u) / ch.gpr - row0 + 1u;
+        for (uint32_t i = tid; i < rows * half; i += blockDim.x) {
+            const uint32_t r = i / half;
+            const uint32_t j = i - r * half;
+            const float pos = static_cast<float>(ch.pos0 + static_cast<int32_t>(row0 + r));
+            float sn, cs;
+            rope_sincos(pos * s.theta[j], sn, cs);
+            const uint32_t off = (r * tg.RS + (j / tg.P) * tg.JS + (j % tg.P) / 2u) * 16u + (j & 1u) * 8u;
+            *reinterpret_cast<float2 *>(tab + off) = make_float2(cs, sn);
+        }
+        __syncthreads();
+    }
+    // RoPE (n_rot 128 or 256): the pair of element d0 + k is element
+    // d0 + k +- half of lane ^ half/64, the cos/sin of pairs j0 .. j0 + 63
+    const bool first = d0 < half;
+    const bool rot = lane < nvl && d0 < s.n_rot;
+    const uint32_t j0 = first ? d0 : d0 - half;
+    const float4 *trow = reinterpret_cast<const float4 *>(tab + ((row - row0) * tg.RS + (j0 / 64u) * tg.JS) * 16u);
+    const float tr = first ? -1.0f : 1.0f;
+    const uint32_t rope_src = 4u * (lane ^ (half / 64u));
+    // cross-lane butterflies: stages on lane bits 0 .. nx-1, and the sign
+    // they leave
+    const uint32_t W = s.hadamard;
+    const uint32_t nx = W >= 512u ? 3u : W >= 256u ? 2u : W >= 128u ? 1u : 0u;
+    const float sigma = (__popc(lane & ((1u << nx) - 1u)) & 1u) ? -1.0f : 1.0f;
+    // a power-of-two scale is carried into the quantizer (never for F16)
+    const bool fold = TYPE != KVMEM_TYPE_F16 && (__float_as_uint(s.hscale) & 0x007fffffu) == 0u;
+    const float sf = (W != 0u && fold) ? s.hscale : 1.0f;
+    const float f = sigma * sf;
+    // without RoPE the first operation is the Hadamard's span-1 butterfly
+    // (scale carried) or its scale
+    const bool first_sum = half == 0u && W != 0u && fold;
+    const bool first_scale = half == 0u && W != 0u && !fold;
+    // LDS places: chunk lane % 8 of load k belongs to lane 8k + lane/8
+    uint8_t *wr = wl + (lane >> 3) * kX64Lane + (lane & 7u) * 16u;
+    const uint8_t *rd = wl + lane * kX64Lane;
+
+    for (uint32_t l = wave; l < s.n_layers; l += 4u) {
+        ch.src = src0 + l * s.layer_stride;  // the same rows of layer l
+        ch.dst = const_cast<uint8_t *>(s.layer_dst[l]) + dst_off;
+        uint4 v[8];
+        x64_load(ch, lane, nvl, v);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            uint2 *q = reinterpret_cast<uint2 *>(wr + k * 8u * kX64Lane);
+            q[0] = make_uint2(v[k].x, v[k].y);
+            q[1] = make_uint2(v[k].z, v[k].w);
+        }
+        wave_lds_order();
+        uint32_t w[32];  // packed f16 pairs: word m holds elements 2m, 2m + 1
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint2 lo = reinterpret_cast<const uint2 *>(rd + 16u * j)[0];
+            const uint2 hi = reinterpret_cast<const uint2 *>(rd + 16u * j)[1];
+            w[4 * j + 0] = lo.x;
+            w[4 * j + 1] = lo.y;
+            w[4 * j + 2] = hi.x;
+            w[4 * j + 3] = hi.y;
+        }
+        // the first operation on each element widens it
+        float x[64];
+        if (half != 0u && rot) {
+            x64_rope_f16(x, w, trow, tr, rope_src);
+        } else if (first_sum) {  // Hadamard span 1 with the scale carried to the quantizer
+#pragma unroll
+            for (int m = 0; m < 32; ++m) {
+                x[2 * m] = mix_sum(w[m]);
+                x[2 * m + 1] = mix_diff(w[m]);
+            }
+        } else if (first_scale) {  // the inexact Hadamard scale
+#pragma unroll
+            for (int m = 0; m < 32; ++m) {
+                x[2 * m] = mix_mul<0>(w[m], s.hscale, -0.0f);
+                x[2 * m + 1] = mix_mul<1>(w[m], s.hscale, -0.0f);
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < 32; ++m) {
+                x[2 * m] = half_bits_to_float(w[m] & 0xffffu);
+                x[2 * m + 1] = half_bits_to_float(w[m] >> 16);
+            }
+        }
+        if (W != 0u) {
+            if (!fold && half != 0u) {
+#pragma unroll
+                for (int i = 0; i < 64; ++i) {
+                    x[i] = x[i] * s.hscale;
+                }
+            }
+            if (!first_sum) {
+#pragma unroll
+                for (int i = 0; i < 64; i += 2) {
+                    const float a = x[i];
+                    const float b = x[i + 1];
+                    x[i] = a + b;
+                    x[i + 1] = a - b;
+                }
+            }
+#pragma unroll
+            for (int h = 2; h < 64; h <<= 1) {
+#pragma unroll
+                for (int i = 0; i < 64; i += 2 * h) {
+#pragma unroll
+                    for (int j = 0; j < h; ++j) {
+                        const float a = x[i + j];
+                        const float b = x[i + j + h];
+                        x[i + j] = a + b;
+                        x[i + j + h] = a - b;
+                    }
+                }
+            }
+            for (uint32_t st = 0; st < nx; ++st) {
+                // y = own + t * partner, t = -1 where the lane holds the upper element
+                const uint32_t src = 4u * (lane ^ (1u << st));
+                const float t = ((lane >> st) & 1u) ? -1.0f : 1.0f;
+#pragma unroll
+                for (int i = 0; i < 64; ++i) {
+                    x[i] = __builtin_fmaf(x64_partner(x[i], src), t, x[i]);
+                }
+            }
+        }
+        wave_lds_order();  // every lane's input is read before outputs overwrite it
+        x64_quant_lane<TYPE>(x, f, sf, reinterpret_cast<uint32_t *>(wl + lane * (2u * GB)));
+        wave_lds_order();
+        const uint32_t nb = nvl * 2u * GB;
+        uint8_t *out = ch.dst + static_cast<uint64_t>(ch.g0) * GB;
+        const uint32_t full = nb & ~15u;
+        for (uint32_t off = lane * 16u; off < full; off += 1024u) {
+            const u32x4_t w = *reinterpret_cast<const u32x4_t *>(wl + off);
+            __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t *>(out + off));
+        }
+        for (uint32_t off = full + lane * 4u; off < nb; off += 256u) {
+            *reinterpret_cast<uint32_t *>(out + off) = *reinterpret_cast<const uint32_t *>(wl + off);
+        }
+        wave_lds_order();  // the copy-out reads finish before the next layer's rows land
+    }
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void x64_kernel(BlockSource s) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kX64Wave];
+    x64_unit_layers<TYPE>(s, xcd_chunk(blockIdx.x, gridDim.x), lds, reinterpret_cast<uint8_t *>(rope_tab4));
+}
+
+template <int TK, int TV>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void x64_kv_kernel(BlockSource sk, BlockSource sv, uint32_t n_k) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kX64Wave];
+    const uint32_t c = xcd_chunk(blockIdx.x, gridDim.x);
+    uint8_t *tab = reinterpret_cast<uint8_t *>(rope_tab4);
+    if (c < n_k) {
+        x64_unit_layers<TK>(sk, c, lds, tab);
+    } else {
+        x64_unit_layers<TV>(sv, c - n_k, lds, tab);
+    }
+}
+
 // Dynamic LDS bytes of the RoPE table for chunks of `s`.
 template <class Source>
 size_t rope_tab_bytes(const Source &s) {
@@ -1051,6 +1510,7 @@ static int check_pool(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, uint32_t n
 // A pool's transform, checked and resolved per kind.
 struct XfParams {
     bool on = false;
+    bool lane64 = false;  // the 64-elements-per-lane kernels take the job
     uint32_t head_dim = 32;
     uint32_t n_rot = 0;
     uint32_t had_k = 0;
@@ -1101,6 +1561,15 @@ static int resolve_xf(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, uint32_t e
     // the reference's scale, 1.0f / sqrtf((float) nrot) (stagein.cu:557)
     out.hscale_k = out.had_k ? 1.0f / sqrtf(static_cast<float>(out.had_k)) : 1.0f;
     out.hscale_v = out.had_v ? 1.0f / sqrtf(static_cast<float>(out.had_v)) : 1.0f;
+    // The 64-elements-per-lane kernels hold a rotary pair in lanes l and
+    // l ^ n_rot/128 (n_rot 128, 256), and F16 rows only without cross-lane
+    // butterflies (width 64); other shapes take the 8-elements-per-lane
+    // kernels.
+    const uint32_t half = out.n_rot / 2;
+    out.lane64 = (half == 0 || half == 64 || half == 128) &&
+                 ek % 64 == 0 && (!want_v || ev % 64 == 0) &&
+                 (pool->type_k != KVMEM_TYPE_F16 || out.had_k <= 64) &&
+                 (!want_v || pool->type_v != KVMEM_TYPE_F16 || out.had_v <= 64);
     return KVMEM_HIP_OK;
 }
 
@@ -1173,7 +1642,13 @@ static BlockSource make_block_source(int type, const uint8_t *base, uint64_t blo
     s.n_rot = is_k ? xp.n_rot : 0u;
     s.hadamard = is_k ? xp.had_k : xp.had_v;
     s.hscale = is_k ? xp.hscale_k : xp.hscale_v;
-    s.layer_group = (xp.on && s.n_rot) ? kRopeLayerGroup : 1u;
+    if (xp.lane64) {  // one workgroup per unit of 128 groups, every layer
+        s.chunk_groups = kX64Groups;
+        s.chunks_per_op = (block_tokens * s.gpr + kX64Groups - 1) / kX64Groups;
+        s.layer_group = n_layers;
+    } else {
+        s.layer_group = (xp.on && s.n_rot) ? kRopeLayerGroup : 1u;
+    }
     return s;
 }
 
@@ -1183,15 +1658,71 @@ static uint64_t block_job_chunks(const BlockSource &s, uint32_t n_items) {
     return static_cast<uint64_t>(n_items) * groups * s.chunks_per_op;
 }
 
+// Dynamic LDS bytes of the 64-per-lane RoPE table for chunks of `s`.
+static size_t x64_tab_bytes(const BlockSource &s) {
+    if (!s.n_rot) {
+        return 0;
+    }
+    return static_cast<size_t>(chunk_rows_of(s.gpr, s.chunk_groups)) * x64_tab_geom(s.n_rot / 2).RS * 16u;
+}
+
+template <int TK>
+static bool launch_x64_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, size_t tb, const BlockSource &sk,
+                         const BlockSource &sv, uint32_t n_k) {
+    switch (tv) {
+        case KVMEM_TYPE_Q8_0: x64_kv_kernel<TK, KVMEM_TYPE_Q8_0><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k); break;
+        case KVMEM_TYPE_Q4_0: x64_kv_kernel<TK, KVMEM_TYPE_Q4_0><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k); break;
+        case KVMEM_TYPE_Q5_0: x64_kv_kernel<TK, KVMEM_TYPE_Q5_0><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k); break;
+        case KVMEM_TYPE_F16: x64_kv_kernel<TK, KVMEM_TYPE_F16><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k); break;
+        default: fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported V type"); return false;
+    }
+    return true;
+}
+
+// The job on the 64-elements-per-lane kernels (K chunks first, then V).
+static bool launch_x64(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_t n_v,
+                       const BlockSource &sk, const BlockSource *sv) {
+    if (n_k + n_v == 0) {
+        return true;
+    }
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "stage-in transform kernel launch")) {
+        return false;
+    }
+    const size_t tb = x64_tab_bytes(sk);  // only K is RoPE'd
+    const uint32_t grid = n_k + n_v;
+    bool ok = true;
+    if (sv) {
+        switch (tk) {
+            case KVMEM_TYPE_Q8_0: ok = launch_x64_v<KVMEM_TYPE_Q8_0>(ctx, tv, grid, tb, sk, *sv, n_k); break;
+            case KVMEM_TYPE_Q4_0: ok = launch_x64_v<KVMEM_TYPE_Q4_0>(ctx, tv, grid, tb, sk, *sv, n_k); break;
+            case KVMEM_TYPE_Q5_0: ok = launch_x64_v<KVMEM_TYPE_Q5_0>(ctx, tv, grid, tb, sk, *sv, n_k); break;
+            case KVMEM_TYPE_F16: ok = launch_x64_v<KVMEM_TYPE_F16>(ctx, tv, grid, tb, sk, *sv, n_k); break;
+            default: fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported K type"); return false;
+        }
+    } else {
+        switch (tk) {
+            case KVMEM_TYPE_Q8_0: x64_kernel<KVMEM_TYPE_Q8_0><<<grid, 256, tb, ctx->stream>>>(sk); break;
+            case KVMEM_TYPE_Q4_0: x64_kernel<KVMEM_TYPE_Q4_0><<<grid, 256, tb, ctx->stream>>>(sk); break;
+            case KVMEM_TYPE_Q5_0: x64_kernel<KVMEM_TYPE_Q5_0><<<grid, 256, tb, ctx->stream>>>(sk); break;
+            case KVMEM_TYPE_F16: x64_kernel<KVMEM_TYPE_F16><<<grid, 256, tb, ctx->stream>>>(sk); break;
+            default: fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported K type"); return false;
+        }
+    }
+    return ok && hip_ok(ctx, hipGetLastError(), "stage-in transform kernel launch");
+}
+
 static int launch_block_job(kvmem_hip_ctx *ctx, int type_k, const BlockSource &sk, int type_v,
-                            const BlockSource *sv, uint32_t n_items, bool xf) {
+                            const BlockSource *sv, uint32_t n_items, const XfParams &xp) {
     const uint64_t nk = block_job_chunks(sk, n_items);
     const uint64_t nv = sv ? block_job_chunks(*sv, n_items) : 0;
     if (nk + nv > 0x7fffffffu) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "stage-in: too many chunks in one call");
     }
+    const bool xf = xp.on;
     bool ok;
-    if (sv) {
+    if (xp.lane64) {
+        ok = launch_x64(ctx, type_k, type_v, static_cast<uint32_t>(nk), static_cast<uint32_t>(nv), sk, sv);
+    } else if (sv) {
         ok = launch_quant_kv(ctx, type_k, type_v, static_cast<uint32_t>(nk),
                              static_cast<uint32_t>(nv), sk, *sv, xf);
     } else {
@@ -1417,7 +1948,7 @@ int kvmem_hip_stagein_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
                                hist->n_embd_v, jt.items, xp, false, jt.theta);
     }
     perf_begin(ctx, kPerfSet);
-    st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp.on);
+    st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp);
     perf_end(ctx, kPerfSet);
     return st;
 }
@@ -1484,7 +2015,7 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
                                    hist->n_embd_v, jt.items, xp, false, jt.theta);
         }
         perf_begin(ctx, kPerfSet);
-        st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp.on);
+        st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp);
         perf_end(ctx, kPerfSet);
         if (st == KVMEM_HIP_OK) {
             ctx->h2d_bytes += static_cast<uint64_t>(n) * span;
@@ -1555,7 +2086,7 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
             sv = make_block_source(pool->type_v, slot_base + kbytes, span, layer_bytes, jt.layers + L, L,
                                    T, hist->n_embd_v, batch_items, xp, false, jt.theta);
         }
-        st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, cnt, xp.on);
+        st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, cnt, xp);
         if (st != KVMEM_HIP_OK) {
             return st;
         }

@@ -148,8 +148,10 @@ class Store:
             self.lib.kvmem_store_destroy(self.h)
             self.h = None
 
-    def __del__(self):
-        if sys.is_finalizing():
+    def __del__(self, _finalizing=sys.is_finalizing):
+        # bound at definition: module globals (sys among them) may already be
+        # gone when an object is collected during interpreter shutdown
+        if _finalizing():
             return
         try:
             self.close()
@@ -241,8 +243,10 @@ class Engine:
             self.lib.kvmem_engine_destroy(self.h)
             self.h = None
 
-    def __del__(self):
-        if sys.is_finalizing():
+    def __del__(self, _finalizing=sys.is_finalizing):
+        # bound at definition: module globals (sys among them) may already be
+        # gone when an object is collected during interpreter shutdown
+        if _finalizing():
             return
         try:
             self.close()

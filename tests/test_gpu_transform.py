@@ -113,6 +113,33 @@ def test_transform_partial_rotary_128_positions(ctx, oracle):
              pos0=[1 << 20, 5, 262_016], seed=41)
 
 
+# Shapes of both stage-in kernels: the 64-elements-per-lane one (rotary
+# pairs across lanes l ^ 1 and l ^ 2 or inside a lane, Hadamard stages
+# across lanes ^ 1, ^ 2, ^ 4, inexact scales 1/sqrtf(128) and 1/sqrtf(512),
+# rotary dims short of head_dim, an untransformed V) and the
+# 8-elements-per-lane one it leaves to (n_rot 48 and 512; F16 with
+# cross-lane butterflies is covered above).
+SHAPES = [
+    # D, Hkv, n_rot, had_k, had_v, type_k, type_v
+    (128, 8, 128, 128, 128, kv.TYPE_Q8_0, kv.TYPE_Q5_0),
+    (256, 4, 128, 256, 256, kv.TYPE_Q4_0, kv.TYPE_Q8_0),
+    (512, 2, 256, 512, 512, kv.TYPE_Q8_0, kv.TYPE_Q4_0),
+    (128, 8, 32, 64, 0, kv.TYPE_Q5_0, kv.TYPE_Q8_0),
+    (64, 16, 64, 64, 64, kv.TYPE_Q8_0, kv.TYPE_F16),
+    (256, 4, 256, 256, 64, kv.TYPE_Q8_0, kv.TYPE_F16),
+    (256, 4, 48, 256, 64, kv.TYPE_Q8_0, kv.TYPE_Q8_0),
+    (512, 2, 512, 512, 128, kv.TYPE_Q5_0, kv.TYPE_Q8_0),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"D{s[0]}-rot{s[2]}-h{s[3]}-{s[4]}-k{s[5]}-v{s[6]}")
+def test_transform_shapes(ctx, oracle, shape):
+    D, hkv, n_rot, hk, hv, tk, tv = shape
+    announce(f"head_dim {D} x {hkv}, n_rot {n_rot}, Hadamard {hk}/{hv}, K={tk} V={tv}, partial last")
+    run_case(ctx, oracle, L=3, B=5, Hkv=hkv, D=D, type_k=tk, type_v=tv, n_rot=n_rot, had_k=hk, had_v=hv,
+             ids=[4, 1, 3], slots=[2, 0, 1], n_slots=3, last=45, pos0=[70_000, 3, 1 << 19], seed=D + n_rot + hk)
+
+
 def test_transform_rope_only_f16(ctx, oracle):
     announce("RoPE only into an F16 pool (RNE of the rotated values)")
     run_case(ctx, oracle, L=1, B=4, Hkv=4, D=256, type_k=kv.TYPE_F16, type_v=kv.TYPE_F16,
