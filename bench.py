@@ -398,7 +398,9 @@ def run_mixed_precision(a, torch, kv, workloads) -> dict:
 def run_cache_transform(a, torch, kv, workloads) -> dict:
     """The 256K step with the cache row transform on: the 77 changed blocks
     are RoPE'd at their original positions (256 rotary dims, base 1e6) and
-    Walsh-Hadamard rotated (K width 256, V width 64) before q8_0."""
+    Walsh-Hadamard rotated (K width 256, V width 64) before q8_0.  Beside it,
+    `transform_parts`: the stage-in alone (no scorer before it), 77 distinct
+    random blocks per call, with each part of the transform on its own."""
     log("generating history K/V [16][2048][128][4][256] f16 and query")
     k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=TQ, seed=2, with_v=True)
     torch.cuda.synchronize()
@@ -410,14 +412,56 @@ def run_cache_transform(a, torch, kv, workloads) -> dict:
     eng.close()
     sb = stage_bytes(kv, m["n_staged"], kv.TYPE_Q8_0, kv.TYPE_Q8_0)
     gbs = sb / (m["set_ms"] * 1e-3) / 1e9
+    parts = transform_parts(kv, torch, k, v, sb)
     return {"metric": "reselect @256K with RoPE + attn_rot stage-in", "unit": "ms/step",
             "value": round(m["ms_step"], 4), "higher_is_better": False, "n_gpus": 1,
             "steps": a.steps, "warmup": a.warmup, "data": "synthetic (seeded N(0,1) keys, bf16 query)",
-            "stagein_roofline": {"bound": "hbm", "kernel": "quant_scatter_kv_kernel<q8_0,q8_0,xf>",
+            "stagein_roofline": {"bound": "hbm", "kernel": "x64_kv_kernel<q8_0,q8_0>",
                                  "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                  "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": sb,
                                  "kernel_ms": round(m["set_ms"], 4), "n_staged": m["n_staged"]},
-            "parts_ms": {"score_kernel": round(m["score_ms"], 4), "stagein_kernel": round(m["set_ms"], 4)}}
+            "parts_ms": {"score_kernel": round(m["score_ms"], 4), "stagein_kernel": round(m["set_ms"], 4)},
+            "transform_parts": parts}
+
+
+def transform_parts(kv, torch, k, v, sb: int, calls: int = 12) -> dict:
+    """Stage-in device ms (events on the library stream) of 77 random blocks
+    x 16 layers into a q8_0 pool, per transform: none, RoPE only (K), K
+    Hadamard 256 only, V Hadamard 64 only, and all of them."""
+    import numpy as np
+    # RoPE frequencies base^(-2i/n_rot) (the timing does not depend on their last bits)
+    theta = (1e6 ** (-2.0 * np.arange(128) / 256)).astype(np.float32)
+    ctx = kv.Context(0)
+    rb = kv.row_size(kv.TYPE_Q8_0, E)
+    n_slots = N_CHANGED
+    pk = [torch.empty(n_slots * T * rb, dtype=torch.uint8, device="cuda") for _ in range(L)]
+    pv = [torch.empty(n_slots * T * rb, dtype=torch.uint8, device="cuda") for _ in range(L)]
+    hist = ctx.make_history(k.data_ptr(), v.data_ptr(), L, B, T, E, E)
+    rng = np.random.default_rng(5)
+    sets = [sorted(rng.choice(B, N_CHANGED, replace=False).tolist()) for _ in range(calls + 2)]
+    slots = list(range(n_slots))
+    variants = {"none": None, "rope_k": (D, 256, theta, 0, 0), "hadamard_k256": (D, 0, None, 256, 0),
+                "hadamard_v64": (D, 0, None, 0, 64), "all": (D, 256, theta, 256, 64)}
+    out = {}
+    ctx.perf_enable(True)
+    for name, xf in variants.items():
+        x = ctx.make_transform(*xf) if xf else None
+        pool = ctx.make_pool(L, n_slots, T, E, E, kv.TYPE_Q8_0, kv.TYPE_Q8_0, [p.data_ptr() for p in pk],
+                             [p.data_ptr() for p in pv], x)
+        for ids in sets[:2]:
+            ctx.stagein_blocks(hist, pool, ids, slots)
+        ctx.sync()
+        ctx.perf_reset()
+        for ids in sets[2:]:
+            ctx.stagein_blocks(hist, pool, ids, slots)
+        ctx.sync()
+        ms = ctx.perf()["set_ms"] / calls
+        out[name] = {"kernel_ms": round(ms, 4), "GBps": round(sb / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    ctx.perf_enable(False)
+    ctx.close()
+    del pk, pv
+    return out
 
 
 def sample_power_clocks() -> dict | None:
