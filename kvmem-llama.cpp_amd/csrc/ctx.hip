@@ -184,13 +184,15 @@ void perf_collect(kvmem_hip_ctx *ctx) {
 // of it, 16-byte vectors when both addresses and the size are 16-byte
 // aligned.  A launch with few ops splits them so the chip fills.
 // ------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops, int n, int pieces) {
+__global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops_dev, ArgTables t, int n,
+                                                           int pieces) {
     const int i = blockIdx.x / pieces;
     const int piece = blockIdx.x - i * pieces;
     if (i >= n) {
         return;
     }
-    const CopyOpDev op = ops[i];
+    const CopyOpDev op = reinterpret_cast<const CopyOpDev *>(
+        table_base(reinterpret_cast<const uint8_t *>(ops_dev), t))[i];
     const uintptr_t a = reinterpret_cast<uintptr_t>(op.src) | reinterpret_cast<uintptr_t>(op.dst);
     if ((a & 15u) == 0 && (op.nbytes & 15u) == 0) {
         const uint4 *s = reinterpret_cast<const uint4 *>(op.src);
@@ -208,15 +210,25 @@ __global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops,
     }
 }
 
-const CopyOpDev *upload_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, const char *what) {
-    if (ops.size() > 0x7fffffffu / 8u) {
-        fail(ctx, KVMEM_HIP_ERR_INVALID, std::string(what) + ": too many copies");
-        return nullptr;
+bool stage_tables(kvmem_hip_ctx *ctx, const void *src, size_t bytes, LaunchTables &out, const char *what) {
+    if (bytes <= kArgTableBytes) {
+        out.dev = nullptr;
+        std::memcpy(out.args.bytes, src, bytes);
+        return true;
     }
-    return static_cast<const CopyOpDev *>(upload(ctx, ops.data(), ops.size() * sizeof(CopyOpDev), what));
+    out.dev = static_cast<const uint8_t *>(upload(ctx, src, bytes, what));
+    return out.dev != nullptr;
 }
 
-bool launch_uploaded_copies(kvmem_hip_ctx *ctx, const CopyOpDev *dops, size_t n, const char *what) {
+bool stage_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, LaunchTables &out, const char *what) {
+    if (ops.size() > 0x7fffffffu / 8u) {
+        fail(ctx, KVMEM_HIP_ERR_INVALID, std::string(what) + ": too many copies");
+        return false;
+    }
+    return stage_tables(ctx, ops.data(), ops.size() * sizeof(CopyOpDev), out, what);
+}
+
+bool launch_staged_copies(kvmem_hip_ctx *ctx, const LaunchTables &tables, size_t n, const char *what) {
     if (n == 0) {
         return true;
     }
@@ -226,7 +238,7 @@ bool launch_uploaded_copies(kvmem_hip_ctx *ctx, const CopyOpDev *dops, size_t n,
         return false;
     }
     batched_copy_kernel<<<static_cast<uint32_t>(n * pieces), 256, 0, ctx->stream>>>(
-        dops, static_cast<int>(n), pieces);
+        reinterpret_cast<const CopyOpDev *>(tables.dev), tables.args, static_cast<int>(n), pieces);
     return hip_ok(ctx, hipGetLastError(), what);
 }
 
@@ -234,8 +246,8 @@ bool launch_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, cons
     if (ops.empty()) {
         return true;
     }
-    const CopyOpDev *dops = upload_copy_ops(ctx, ops, what);
-    return dops && launch_uploaded_copies(ctx, dops, ops.size(), what);
+    LaunchTables tables;
+    return stage_copy_ops(ctx, ops, tables, what) && launch_staged_copies(ctx, tables, ops.size(), what);
 }
 
 bool ensure_h2d_ring(kvmem_hip_ctx *ctx, size_t min_slot_bytes) {
@@ -554,12 +566,12 @@ int kvmem_hip_d2d_batched(kvmem_hip_ctx *ctx, const void *const *src, void *cons
         total += nbytes[i];
     }
     (void) hipSetDevice(ctx->device);
-    const CopyOpDev *dops = upload_copy_ops(ctx, ops, "d2d_batched ops");
-    if (!dops) {
+    LaunchTables tables;
+    if (!stage_copy_ops(ctx, ops, tables, "d2d_batched ops")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     perf_begin(ctx, kPerfLayout);
-    const bool ok = launch_uploaded_copies(ctx, dops, ops.size(), "d2d_batched launch");
+    const bool ok = launch_staged_copies(ctx, tables, ops.size(), "d2d_batched launch");
     perf_end(ctx, kPerfLayout);
     if (!ok) {
         return KVMEM_HIP_ERR_RUNTIME;

@@ -122,13 +122,34 @@ struct CopyOpDev {
     uint64_t nbytes;
 };
 
+// Launch tables small enough travel in the kernel's arguments instead of an
+// upload (a pinned copy, an H2D transfer and a blit on the stream before the
+// kernel): the kernel reads them in place from its argument segment.  A
+// kernel that takes ArgTables binds its table pointers to `dev` when the
+// tables were uploaded (too large for the arguments), else to the bytes.
+constexpr size_t kArgTableBytes = 3072;
+struct ArgTables {
+    alignas(16) uint8_t bytes[kArgTableBytes];
+};
+__device__ inline const uint8_t *table_base(const uint8_t *dev, const ArgTables &t) {
+    return dev ? dev : t.bytes;
+}
+
+// Tables for one launch: copied into `args` when they fit (dev = null),
+// else uploaded (dev = the device copy).  False on an upload failure.
+struct LaunchTables {
+    const uint8_t *dev = nullptr;
+    ArgTables args;
+};
+bool stage_tables(kvmem_hip_ctx *ctx, const void *src, size_t bytes, LaunchTables &out, const char *what);
+
 // Upload `ops` and copy them in one launch on the context stream (each op
 // split over 1-8 workgroups so that a launch fills the chip, 16-byte
 // vectors where aligned).  The two halves apart: the upload, then launches
 // of the uploaded table (e.g. inside a timing bracket).
 bool launch_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, const char *what);
-const CopyOpDev *upload_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, const char *what);
-bool launch_uploaded_copies(kvmem_hip_ctx *ctx, const CopyOpDev *dops, size_t n, const char *what);
+bool stage_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, LaunchTables &out, const char *what);
+bool launch_staged_copies(kvmem_hip_ctx *ctx, const LaunchTables &tables, size_t n, const char *what);
 
 // The pinned-host stage-in ring: kH2dRing device slots of at least
 // `min_slot_bytes` (32 MiB or more, grown only), with their events.

@@ -122,6 +122,7 @@ struct OpListSource {
         out.pos0 = 0;
         return true;
     }
+    __device__ void bind(const ArgTables &) {}  // the op list is always uploaded
     // rows may be strided; no row transform on this source
     static constexpr bool kContiguous = false;
     static constexpr uint32_t head_dim = 32, n_rot = 0, hadamard = 0;
@@ -137,9 +138,12 @@ struct OpListSource {
 struct BlockSource {
     static constexpr bool kContiguous = true;  // group g of an operation at src + 64 g
     const uint8_t *base;
-    const uint8_t *const *layer_dst;  // device array [n_layers]
-    const uint32_t *items;            // device [n_items][4]: block, slot, n_tokens, pos0
-    const float *theta;               // device [n_rot/2] (RoPE)
+    // set by bind() from the job's tables:
+    const uint8_t *const *layer_dst;  // [n_layers]
+    const uint32_t *items;            // [n_items][4]: block, slot, n_tokens, pos0
+    const float *theta;               // [n_rot/2] (RoPE)
+    const uint8_t *tables;            // the job's uploaded tables, or null: in the kernel's ArgTables
+    uint32_t layer_off, items_off, theta_off;  // byte offsets of the three tables in them
     uint64_t block_stride;
     uint64_t layer_stride;
     uint32_t n_layers;
@@ -153,6 +157,12 @@ struct BlockSource {
     uint32_t hadamard;                // Hadamard width (0 = none)
     float hscale;                     // 1 / sqrtf(hadamard)
     uint32_t layer_group;             // layers per workgroup chunk index (RoPE'd K: 4; else 1)
+    __device__ void bind(const ArgTables &t) {
+        const uint8_t *b = table_base(tables, t);
+        layer_dst = reinterpret_cast<const uint8_t *const *>(b + layer_off);
+        items = reinterpret_cast<const uint32_t *>(b + items_off);
+        theta = reinterpret_cast<const float *>(b + theta_off);
+    }
     __device__ bool chunk(uint32_t c, Chunk &out) const {
         const uint32_t op = c / chunks_per_op;
         const uint32_t sub = c - op * chunks_per_op;
@@ -888,8 +898,10 @@ constexpr int stage_bytes() {
 }
 
 template <int TYPE, class Source, bool XF, bool GROUP>
-__global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
+__global__ __launch_bounds__(256) void quant_scatter_kernel(Source arg, ArgTables t) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[stage_bytes<TYPE, XF>()];
+    Source source = arg;
+    source.bind(t);
     const uint32_t c = xcd_chunk(blockIdx.x, gridDim.x);
     if constexpr (GROUP) {
         block_chunks<TYPE>(source, c, lds, rope_tab);
@@ -901,8 +913,11 @@ __global__ __launch_bounds__(256) void quant_scatter_kernel(Source source) {
 // K and V of a block job in one launch: chunks [0, n_k) are K, the rest V
 // (the branch is uniform per workgroup).
 template <int TK, int TV, bool XF, bool GROUP>
-__global__ __launch_bounds__(256) void quant_scatter_kv_kernel(BlockSource sk, BlockSource sv,
-                                                               uint32_t n_k) {
+__global__ __launch_bounds__(256) void quant_scatter_kv_kernel(BlockSource ak, BlockSource av, uint32_t n_k,
+                                                               ArgTables t) {
+    BlockSource sk = ak, sv = av;
+    sk.bind(t);
+    sv.bind(t);
     constexpr int SB = stage_bytes<TK, XF>() > stage_bytes<TV, XF>() ? stage_bytes<TK, XF>()
                                                                      : stage_bytes<TV, XF>();
     __shared__ __attribute__((aligned(16))) uint8_t lds[SB];
@@ -1360,13 +1375,19 @@ __device__ inline void x64_unit_layers(const BlockSource &s, uint32_t c, uint8_t
 }
 
 template <int TYPE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void x64_kernel(BlockSource s) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void x64_kernel(BlockSource a,
+                                                                                            ArgTables t) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kX64Wave];
+    BlockSource s = a;
+    s.bind(t);
     x64_unit_layers<TYPE>(s, xcd_chunk(blockIdx.x, gridDim.x), lds, reinterpret_cast<uint8_t *>(rope_tab4));
 }
 
 template <int TK, int TV>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void x64_kv_kernel(BlockSource sk, BlockSource sv, uint32_t n_k) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void x64_kv_kernel(BlockSource ak, BlockSource av, uint32_t n_k, ArgTables t) {
+    BlockSource sk = ak, sv = av;
+    sk.bind(t);
+    sv.bind(t);
     __shared__ __attribute__((aligned(16))) uint8_t lds[4 * kX64Wave];
     const uint32_t c = xcd_chunk(blockIdx.x, gridDim.x);
     uint8_t *tab = reinterpret_cast<uint8_t *>(rope_tab4);
@@ -1384,7 +1405,7 @@ size_t rope_tab_bytes(const Source &s) {
 }
 
 template <class Source, bool XF, bool GROUP>
-bool launch_quant_x(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Source &s) {
+bool launch_quant_x(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Source &s, const ArgTables &args) {
     if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "stage-in kernel launch")) {
         return false;
     }
@@ -1394,16 +1415,16 @@ bool launch_quant_x(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Sourc
     }
     switch (type) {
         case KVMEM_TYPE_Q8_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q8_0, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_Q8_0, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s, args);
             break;
         case KVMEM_TYPE_Q4_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q4_0, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_Q4_0, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s, args);
             break;
         case KVMEM_TYPE_Q5_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q5_0, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_Q5_0, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s, args);
             break;
         case KVMEM_TYPE_F16:
-            quant_scatter_kernel<KVMEM_TYPE_F16, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s);
+            quant_scatter_kernel<KVMEM_TYPE_F16, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s, args);
             break;
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported type");
@@ -1412,40 +1433,43 @@ bool launch_quant_x(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Sourc
     return hip_ok(ctx, hipGetLastError(), "stage-in kernel launch");
 }
 
+static const ArgTables kNoArgTables{};
+
 bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const OpListSource &s) {
-    return n_chunks == 0 || launch_quant_x<OpListSource, false, false>(ctx, type, n_chunks, s);
+    return n_chunks == 0 || launch_quant_x<OpListSource, false, false>(ctx, type, n_chunks, s, kNoArgTables);
 }
 
-bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const BlockSource &s, bool xf) {
+bool launch_quant(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const BlockSource &s, bool xf,
+                  const ArgTables &args) {
     if (n_chunks == 0) {
         return true;
     }
     if (!xf) {
-        return launch_quant_x<BlockSource, false, false>(ctx, type, n_chunks, s);
+        return launch_quant_x<BlockSource, false, false>(ctx, type, n_chunks, s, args);
     }
-    return s.layer_group > 1u ? launch_quant_x<BlockSource, true, true>(ctx, type, n_chunks, s)
-                              : launch_quant_x<BlockSource, true, false>(ctx, type, n_chunks, s);
+    return s.layer_group > 1u ? launch_quant_x<BlockSource, true, true>(ctx, type, n_chunks, s, args)
+                              : launch_quant_x<BlockSource, true, false>(ctx, type, n_chunks, s, args);
 }
 
 template <int TK, bool XF, bool GROUP>
 bool launch_kv_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, const BlockSource &sk,
-                 const BlockSource &sv, uint32_t n_k) {
+                 const BlockSource &sv, uint32_t n_k, const ArgTables &args) {
     if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "stage-in K/V kernel launch")) {
         return false;
     }
     const size_t tb = XF ? rope_tab_bytes(sk) : 0;  // only K is RoPE'd
     switch (tv) {
         case KVMEM_TYPE_Q8_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q8_0, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q8_0, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args);
             break;
         case KVMEM_TYPE_Q4_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q4_0, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q4_0, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args);
             break;
         case KVMEM_TYPE_Q5_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q5_0, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q5_0, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args);
             break;
         case KVMEM_TYPE_F16:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_F16, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k);
+            quant_scatter_kv_kernel<TK, KVMEM_TYPE_F16, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args);
             break;
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported V type");
@@ -1456,13 +1480,13 @@ bool launch_kv_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, const BlockSource &s
 
 template <bool XF, bool GROUP>
 bool launch_quant_kv_x(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_t n_v,
-                       const BlockSource &sk, const BlockSource &sv) {
+                       const BlockSource &sk, const BlockSource &sv, const ArgTables &args) {
     const uint32_t grid = n_k + n_v;
     switch (tk) {
-        case KVMEM_TYPE_Q8_0: return launch_kv_v<KVMEM_TYPE_Q8_0, XF, GROUP>(ctx, tv, grid, sk, sv, n_k);
-        case KVMEM_TYPE_Q4_0: return launch_kv_v<KVMEM_TYPE_Q4_0, XF, GROUP>(ctx, tv, grid, sk, sv, n_k);
-        case KVMEM_TYPE_Q5_0: return launch_kv_v<KVMEM_TYPE_Q5_0, XF, GROUP>(ctx, tv, grid, sk, sv, n_k);
-        case KVMEM_TYPE_F16: return launch_kv_v<KVMEM_TYPE_F16, XF, GROUP>(ctx, tv, grid, sk, sv, n_k);
+        case KVMEM_TYPE_Q8_0: return launch_kv_v<KVMEM_TYPE_Q8_0, XF, GROUP>(ctx, tv, grid, sk, sv, n_k, args);
+        case KVMEM_TYPE_Q4_0: return launch_kv_v<KVMEM_TYPE_Q4_0, XF, GROUP>(ctx, tv, grid, sk, sv, n_k, args);
+        case KVMEM_TYPE_Q5_0: return launch_kv_v<KVMEM_TYPE_Q5_0, XF, GROUP>(ctx, tv, grid, sk, sv, n_k, args);
+        case KVMEM_TYPE_F16: return launch_kv_v<KVMEM_TYPE_F16, XF, GROUP>(ctx, tv, grid, sk, sv, n_k, args);
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported K type");
             return false;
@@ -1471,15 +1495,15 @@ bool launch_quant_kv_x(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_
 
 // The K source groups layers when it is RoPE'd (layer_group > 1); V never is.
 bool launch_quant_kv(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_t n_v,
-                     const BlockSource &sk, const BlockSource &sv, bool xf) {
+                     const BlockSource &sk, const BlockSource &sv, bool xf, const ArgTables &args) {
     if (n_k + n_v == 0) {
         return true;
     }
     if (!xf) {
-        return launch_quant_kv_x<false, false>(ctx, tk, tv, n_k, n_v, sk, sv);
+        return launch_quant_kv_x<false, false>(ctx, tk, tv, n_k, n_v, sk, sv, args);
     }
-    return sk.layer_group > 1u ? launch_quant_kv_x<true, true>(ctx, tk, tv, n_k, n_v, sk, sv)
-                               : launch_quant_kv_x<true, false>(ctx, tk, tv, n_k, n_v, sk, sv);
+    return sk.layer_group > 1u ? launch_quant_kv_x<true, true>(ctx, tk, tv, n_k, n_v, sk, sv, args)
+                               : launch_quant_kv_x<true, false>(ctx, tk, tv, n_k, n_v, sk, sv, args);
 }
 
 static bool aligned16(const void *p) {
@@ -1579,14 +1603,13 @@ static int resolve_xf(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, uint32_t e
 // per call keeps them inside one upload-ring slot for as long as the
 // call's kernels need them.
 struct JobTables {
-    const void *const *layers = nullptr;
-    const uint32_t *items = nullptr;
-    const float *theta = nullptr;
+    LaunchTables tables;  // [2L] layer pointers (K, then V), the items, the RoPE frequencies
+    uint32_t items_off = 0;
+    uint32_t theta_off = 0;
 };
 
-static bool upload_block_job(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, bool want_v,
-                             const std::vector<uint32_t> &items, const XfParams &xp,
-                             JobTables &out) {
+static bool stage_block_job(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, bool want_v,
+                            const std::vector<uint32_t> &items, const XfParams &xp, JobTables &out) {
     const size_t L = pool->n_layers;
     const size_t n_theta = xp.n_rot / 2;
     const size_t words = items.size() + n_theta;  // 4-byte words after the pointers
@@ -1600,14 +1623,9 @@ static bool upload_block_job(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, boo
     if (n_theta) {
         std::memcpy(tail + items.size() * sizeof(uint32_t), pool->xf->theta, n_theta * sizeof(float));
     }
-    void *dev = upload(ctx, buf.data(), buf.size() * sizeof(uint64_t), "stage-in job tables");
-    if (!dev) {
-        return false;
-    }
-    out.layers = static_cast<const void *const *>(dev);
-    out.items = reinterpret_cast<const uint32_t *>(static_cast<const uint64_t *>(dev) + 2 * L);
-    out.theta = n_theta ? reinterpret_cast<const float *>(out.items + items.size()) : nullptr;
-    return true;
+    out.items_off = static_cast<uint32_t>(2 * L * sizeof(uint64_t));
+    out.theta_off = static_cast<uint32_t>(out.items_off + items.size() * sizeof(uint32_t));
+    return stage_tables(ctx, buf.data(), buf.size() * sizeof(uint64_t), out.tables, "stage-in job tables");
 }
 
 // Position of token 0 of staged block i (item order of the call).
@@ -1619,17 +1637,18 @@ static uint32_t item_pos0(const kvmem_hip_pool *pool, const uint32_t *block_ids,
     return block_ids[i] * block_tokens;
 }
 
-// Source of one kind (K or V) of a block job.  items_dev: device [n][4].
+// Source of one kind (K or V) of a block job over the job's tables, its
+// items starting at `first_item`.
 static BlockSource make_block_source(int type, const uint8_t *base, uint64_t block_stride,
-                                     uint64_t layer_stride, const void *layer_table_dev,
-                                     uint32_t n_layers, uint32_t block_tokens, uint32_t n_embd,
-                                     const uint32_t *items_dev, const XfParams &xp, bool is_k,
-                                     const float *theta_dev) {
-    BlockSource s;
+                                     uint64_t layer_stride, const JobTables &jt, uint32_t n_layers,
+                                     uint32_t block_tokens, uint32_t n_embd, uint32_t first_item,
+                                     const XfParams &xp, bool is_k) {
+    BlockSource s{};
     s.base = base;
-    s.layer_dst = static_cast<const uint8_t *const *>(layer_table_dev);
-    s.items = items_dev;
-    s.theta = theta_dev;
+    s.tables = jt.tables.dev;
+    s.layer_off = is_k ? 0u : static_cast<uint32_t>(n_layers * sizeof(uint64_t));
+    s.items_off = jt.items_off + 16u * first_item;
+    s.theta_off = jt.theta_off;
     s.block_stride = block_stride;
     s.layer_stride = layer_stride;
     s.n_layers = n_layers;
@@ -1668,12 +1687,12 @@ static size_t x64_tab_bytes(const BlockSource &s) {
 
 template <int TK>
 static bool launch_x64_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, size_t tb, const BlockSource &sk,
-                         const BlockSource &sv, uint32_t n_k) {
+                         const BlockSource &sv, uint32_t n_k, const ArgTables &args) {
     switch (tv) {
-        case KVMEM_TYPE_Q8_0: x64_kv_kernel<TK, KVMEM_TYPE_Q8_0><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k); break;
-        case KVMEM_TYPE_Q4_0: x64_kv_kernel<TK, KVMEM_TYPE_Q4_0><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k); break;
-        case KVMEM_TYPE_Q5_0: x64_kv_kernel<TK, KVMEM_TYPE_Q5_0><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k); break;
-        case KVMEM_TYPE_F16: x64_kv_kernel<TK, KVMEM_TYPE_F16><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k); break;
+        case KVMEM_TYPE_Q8_0: x64_kv_kernel<TK, KVMEM_TYPE_Q8_0><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args); break;
+        case KVMEM_TYPE_Q4_0: x64_kv_kernel<TK, KVMEM_TYPE_Q4_0><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args); break;
+        case KVMEM_TYPE_Q5_0: x64_kv_kernel<TK, KVMEM_TYPE_Q5_0><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args); break;
+        case KVMEM_TYPE_F16: x64_kv_kernel<TK, KVMEM_TYPE_F16><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args); break;
         default: fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported V type"); return false;
     }
     return true;
@@ -1681,7 +1700,7 @@ static bool launch_x64_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, size_t tb, c
 
 // The job on the 64-elements-per-lane kernels (K chunks first, then V).
 static bool launch_x64(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_t n_v,
-                       const BlockSource &sk, const BlockSource *sv) {
+                       const BlockSource &sk, const BlockSource *sv, const ArgTables &args) {
     if (n_k + n_v == 0) {
         return true;
     }
@@ -1693,18 +1712,18 @@ static bool launch_x64(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_
     bool ok = true;
     if (sv) {
         switch (tk) {
-            case KVMEM_TYPE_Q8_0: ok = launch_x64_v<KVMEM_TYPE_Q8_0>(ctx, tv, grid, tb, sk, *sv, n_k); break;
-            case KVMEM_TYPE_Q4_0: ok = launch_x64_v<KVMEM_TYPE_Q4_0>(ctx, tv, grid, tb, sk, *sv, n_k); break;
-            case KVMEM_TYPE_Q5_0: ok = launch_x64_v<KVMEM_TYPE_Q5_0>(ctx, tv, grid, tb, sk, *sv, n_k); break;
-            case KVMEM_TYPE_F16: ok = launch_x64_v<KVMEM_TYPE_F16>(ctx, tv, grid, tb, sk, *sv, n_k); break;
+            case KVMEM_TYPE_Q8_0: ok = launch_x64_v<KVMEM_TYPE_Q8_0>(ctx, tv, grid, tb, sk, *sv, n_k, args); break;
+            case KVMEM_TYPE_Q4_0: ok = launch_x64_v<KVMEM_TYPE_Q4_0>(ctx, tv, grid, tb, sk, *sv, n_k, args); break;
+            case KVMEM_TYPE_Q5_0: ok = launch_x64_v<KVMEM_TYPE_Q5_0>(ctx, tv, grid, tb, sk, *sv, n_k, args); break;
+            case KVMEM_TYPE_F16: ok = launch_x64_v<KVMEM_TYPE_F16>(ctx, tv, grid, tb, sk, *sv, n_k, args); break;
             default: fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported K type"); return false;
         }
     } else {
         switch (tk) {
-            case KVMEM_TYPE_Q8_0: x64_kernel<KVMEM_TYPE_Q8_0><<<grid, 256, tb, ctx->stream>>>(sk); break;
-            case KVMEM_TYPE_Q4_0: x64_kernel<KVMEM_TYPE_Q4_0><<<grid, 256, tb, ctx->stream>>>(sk); break;
-            case KVMEM_TYPE_Q5_0: x64_kernel<KVMEM_TYPE_Q5_0><<<grid, 256, tb, ctx->stream>>>(sk); break;
-            case KVMEM_TYPE_F16: x64_kernel<KVMEM_TYPE_F16><<<grid, 256, tb, ctx->stream>>>(sk); break;
+            case KVMEM_TYPE_Q8_0: x64_kernel<KVMEM_TYPE_Q8_0><<<grid, 256, tb, ctx->stream>>>(sk, args); break;
+            case KVMEM_TYPE_Q4_0: x64_kernel<KVMEM_TYPE_Q4_0><<<grid, 256, tb, ctx->stream>>>(sk, args); break;
+            case KVMEM_TYPE_Q5_0: x64_kernel<KVMEM_TYPE_Q5_0><<<grid, 256, tb, ctx->stream>>>(sk, args); break;
+            case KVMEM_TYPE_F16: x64_kernel<KVMEM_TYPE_F16><<<grid, 256, tb, ctx->stream>>>(sk, args); break;
             default: fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported K type"); return false;
         }
     }
@@ -1712,7 +1731,8 @@ static bool launch_x64(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_
 }
 
 static int launch_block_job(kvmem_hip_ctx *ctx, int type_k, const BlockSource &sk, int type_v,
-                            const BlockSource *sv, uint32_t n_items, const XfParams &xp) {
+                            const BlockSource *sv, uint32_t n_items, const XfParams &xp,
+                            const ArgTables &args) {
     const uint64_t nk = block_job_chunks(sk, n_items);
     const uint64_t nv = sv ? block_job_chunks(*sv, n_items) : 0;
     if (nk + nv > 0x7fffffffu) {
@@ -1721,12 +1741,13 @@ static int launch_block_job(kvmem_hip_ctx *ctx, int type_k, const BlockSource &s
     const bool xf = xp.on;
     bool ok;
     if (xp.lane64) {
-        ok = launch_x64(ctx, type_k, type_v, static_cast<uint32_t>(nk), static_cast<uint32_t>(nv), sk, sv);
+        ok = launch_x64(ctx, type_k, type_v, static_cast<uint32_t>(nk), static_cast<uint32_t>(nv), sk, sv,
+                        args);
     } else if (sv) {
         ok = launch_quant_kv(ctx, type_k, type_v, static_cast<uint32_t>(nk),
-                             static_cast<uint32_t>(nv), sk, *sv, xf);
+                             static_cast<uint32_t>(nv), sk, *sv, xf, args);
     } else {
-        ok = launch_quant(ctx, type_k, static_cast<uint32_t>(nk), sk, xf);
+        ok = launch_quant(ctx, type_k, static_cast<uint32_t>(nk), sk, xf, args);
     }
     return ok ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
 }
@@ -1744,9 +1765,8 @@ static int launch_block_job(kvmem_hip_ctx *ctx, int type_k, const BlockSource &s
 // reads or writes that column of those slots.  The bytes move once, plus the saved slots, where a gather to
 // scratch and a scatter back move them twice.
 struct ChainParams {
-    const ChainSeg *segs;
-    uint8_t *const *k_layers;      // device [L]
-    uint8_t *const *v_layers;      // device [L], or null
+    const uint8_t *tables;         // uploaded tables, or null: in the kernel's ArgTables
+                                   // (K layer pointers [L], V layer pointers [L], segments)
     const uint8_t *scratch;        // entry e: [layer][T rows of K][T rows of V]
     uint64_t kspan, vspan;         // one slot of one layer
     uint64_t entry_bytes;          // L * (kspan + vspan)
@@ -1755,27 +1775,47 @@ struct ChainParams {
     uint32_t vec_per_layer;        // T * (krow16 + vrow16)
 };
 
+// A chain segment as the kernel reads it: after the layer pointers, one
+// header per segment, then a pool of slot / row-count entries (16-bit when
+// the pool's slots and tokens fit, else 32-bit) where the segment's run is
+// slot[0 .. len] followed by nt[0 .. len-1].  About 2.5 entries per move
+// instead of a fixed 19 words per segment, so a step's table fits in the
+// kernel arguments.
+struct SegHdr {
+    uint32_t off_len;  // run offset in the pool << 4 | len (1 .. kChainSeg)
+    int32_t saved;     // >= 0: slot[0]'s rows are this scratch entry
+};
+
 // The N moves of one segment for one 16-byte column: N loads, then N stores
 // (rows at or past a move's n_tokens are inside the slot but not stored).
-template <int N>
-__device__ inline void seg_moves(const ChainSeg *seg, const uint8_t *first, uint8_t *base, uint64_t span,
-                                 uint64_t off, uint32_t r) {
+template <int N, typename IdxT>
+__device__ inline void seg_moves(const IdxT *slot, const IdxT *nt, const uint8_t *first, uint8_t *base,
+                                 uint64_t span, uint64_t off, uint32_t r) {
     u32x4_t val[N];
     val[0] = *reinterpret_cast<const u32x4_t *>(first);
 #pragma unroll
     for (int j = 1; j < N; ++j) {
-        val[j] = *reinterpret_cast<const u32x4_t *>(base + seg->slot[j] * span + off);
+        val[j] = *reinterpret_cast<const u32x4_t *>(base + static_cast<uint64_t>(slot[j]) * span + off);
     }
 #pragma unroll
     for (int j = 0; j < N; ++j) {
-        if (r < seg->nt[j]) {
-            *reinterpret_cast<u32x4_t *>(base + seg->slot[j + 1] * span + off) = val[j];
+        if (r < nt[j]) {
+            *reinterpret_cast<u32x4_t *>(base + static_cast<uint64_t>(slot[j + 1]) * span + off) = val[j];
         }
     }
 }
 
-__global__ __launch_bounds__(256) void move_chain_kernel(ChainParams p) {
-    const ChainSeg *seg = p.segs + blockIdx.y;
+// grid (column blocks, segments)
+template <typename IdxT>
+__global__ __launch_bounds__(256) void move_chain_kernel(ChainParams p, ArgTables t) {
+    const uint8_t *tb = table_base(p.tables, t);
+    uint8_t *const *k_layers = reinterpret_cast<uint8_t *const *>(tb);
+    uint8_t *const *v_layers = k_layers + p.L;
+    const SegHdr *hdr = reinterpret_cast<const SegHdr *>(tb + 2u * p.L * sizeof(void *));
+    const SegHdr h = hdr[blockIdx.y];
+    const uint32_t len = h.off_len & 15u;
+    const IdxT *slot = reinterpret_cast<const IdxT *>(hdr + gridDim.y) + (h.off_len >> 4);
+    const IdxT *nt = slot + len + 1u;
     const uint32_t x = blockIdx.x * 256u + threadIdx.x;
     if (x >= p.L * p.vec_per_layer) {
         return;
@@ -1788,28 +1828,58 @@ __global__ __launch_bounds__(256) void move_chain_kernel(ChainParams p) {
         v -= kvecs;
     }
     const uint32_t r = v / (is_v ? p.vrow16 : p.krow16);  // row within the slot
-    uint8_t *base = is_v ? p.v_layers[l] : p.k_layers[l];
+    uint8_t *base = is_v ? v_layers[l] : k_layers[l];
     const uint64_t span = is_v ? p.vspan : p.kspan;
     const uint64_t off = static_cast<uint64_t>(v) * 16u;
-    const int32_t saved = seg->saved;
     // Every slot of a segment is distinct (a cycle's closing source comes
     // from scratch), so all the segment's loads go first, then its stores:
     // up to kChainSeg loads in flight per thread.
-    const uint8_t *first = saved >= 0
-        ? p.scratch + static_cast<uint64_t>(saved) * p.entry_bytes + l * (p.kspan + p.vspan) +
+    const uint8_t *first = h.saved >= 0
+        ? p.scratch + static_cast<uint64_t>(h.saved) * p.entry_bytes + l * (p.kspan + p.vspan) +
               (is_v ? p.kspan : 0u) + off
-        : base + seg->slot[0] * span + off;
+        : base + static_cast<uint64_t>(slot[0]) * span + off;
     static_assert(kChainSeg == 8, "one case per segment length");
-    switch (seg->len) {  // uniform per workgroup
-        case 1: seg_moves<1>(seg, first, base, span, off, r); break;
-        case 2: seg_moves<2>(seg, first, base, span, off, r); break;
-        case 3: seg_moves<3>(seg, first, base, span, off, r); break;
-        case 4: seg_moves<4>(seg, first, base, span, off, r); break;
-        case 5: seg_moves<5>(seg, first, base, span, off, r); break;
-        case 6: seg_moves<6>(seg, first, base, span, off, r); break;
-        case 7: seg_moves<7>(seg, first, base, span, off, r); break;
-        case 8: seg_moves<8>(seg, first, base, span, off, r); break;
+    switch (len) {  // uniform per workgroup
+        case 1: seg_moves<1>(slot, nt, first, base, span, off, r); break;
+        case 2: seg_moves<2>(slot, nt, first, base, span, off, r); break;
+        case 3: seg_moves<3>(slot, nt, first, base, span, off, r); break;
+        case 4: seg_moves<4>(slot, nt, first, base, span, off, r); break;
+        case 5: seg_moves<5>(slot, nt, first, base, span, off, r); break;
+        case 6: seg_moves<6>(slot, nt, first, base, span, off, r); break;
+        case 7: seg_moves<7>(slot, nt, first, base, span, off, r); break;
+        case 8: seg_moves<8>(slot, nt, first, base, span, off, r); break;
         default: break;
+    }
+}
+
+// The kernel's table for `segs`: layer pointers, headers, the entry pool.
+template <typename IdxT>
+static void chain_table(const kvmem_hip_pool *pool, bool want_v, const std::vector<ChainSeg> &segs,
+                        std::vector<uint8_t> &table) {
+    const uint32_t L = pool->n_layers;
+    const size_t ptr_bytes = 2 * L * sizeof(void *);
+    size_t entries = 0;
+    for (const ChainSeg &sg : segs) {
+        entries += 2 * sg.len + 1;
+    }
+    table.assign(ptr_bytes + segs.size() * sizeof(SegHdr) + entries * sizeof(IdxT), 0);
+    std::memcpy(table.data(), pool->k_layers, L * sizeof(void *));
+    if (want_v) {
+        std::memcpy(table.data() + L * sizeof(void *), pool->v_layers, L * sizeof(void *));
+    }
+    SegHdr *hdr = reinterpret_cast<SegHdr *>(table.data() + ptr_bytes);
+    IdxT *ent = reinterpret_cast<IdxT *>(hdr + segs.size());
+    uint32_t off = 0;
+    for (size_t i = 0; i < segs.size(); ++i) {
+        const ChainSeg &sg = segs[i];
+        hdr[i].off_len = (off << 4) | sg.len;
+        hdr[i].saved = sg.saved;
+        for (uint32_t j = 0; j <= sg.len; ++j) {
+            ent[off++] = static_cast<IdxT>(sg.slot[j]);
+        }
+        for (uint32_t j = 0; j < sg.len; ++j) {
+            ent[off++] = static_cast<IdxT>(sg.nt[j]);
+        }
     }
 }
 
@@ -1933,22 +2003,22 @@ int kvmem_hip_stagein_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
     }
     (void) hipSetDevice(ctx->device);
     JobTables jt;
-    if (!upload_block_job(ctx, pool, want_v, items, xp, jt)) {
+    if (!stage_block_job(ctx, pool, want_v, items, xp, jt)) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     const uint64_t bk = static_cast<uint64_t>(T) * hist->n_embd_k * 2u;
     const BlockSource sk = make_block_source(pool->type_k, static_cast<const uint8_t *>(hist->k), bk,
-                                             bk * cap, jt.layers, hist->n_layers, T,
-                                             hist->n_embd_k, jt.items, xp, true, jt.theta);
+                                             bk * cap, jt, hist->n_layers, T,
+                                             hist->n_embd_k, 0, xp, true);
     BlockSource sv{};
     if (want_v) {
         const uint64_t bv = static_cast<uint64_t>(T) * hist->n_embd_v * 2u;
         sv = make_block_source(pool->type_v, static_cast<const uint8_t *>(hist->v), bv,
-                               bv * cap, jt.layers + hist->n_layers, hist->n_layers, T,
-                               hist->n_embd_v, jt.items, xp, false, jt.theta);
+                               bv * cap, jt, hist->n_layers, T,
+                               hist->n_embd_v, 0, xp, false);
     }
     perf_begin(ctx, kPerfSet);
-    st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp);
+    st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp, jt.tables.args);
     perf_end(ctx, kPerfSet);
     return st;
 }
@@ -2004,18 +2074,18 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
             items[4 * i + 3] = item_pos0(pool, block_ids, i, T);
         }
         JobTables jt;
-        if (!upload_block_job(ctx, pool, want_v, items, xp, jt)) {
+        if (!stage_block_job(ctx, pool, want_v, items, xp, jt)) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
-        const BlockSource sk = make_block_source(pool->type_k, view, span, layer_bytes, jt.layers, L, T,
-                                                 hist->n_embd_k, jt.items, xp, true, jt.theta);
+        const BlockSource sk = make_block_source(pool->type_k, view, span, layer_bytes, jt, L, T,
+                                                 hist->n_embd_k, 0, xp, true);
         BlockSource sv{};
         if (want_v) {
-            sv = make_block_source(pool->type_v, view + kbytes, span, layer_bytes, jt.layers + L, L, T,
-                                   hist->n_embd_v, jt.items, xp, false, jt.theta);
+            sv = make_block_source(pool->type_v, view + kbytes, span, layer_bytes, jt, L, T,
+                                   hist->n_embd_v, 0, xp, false);
         }
         perf_begin(ctx, kPerfSet);
-        st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp);
+        st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp, jt.tables.args);
         perf_end(ctx, kPerfSet);
         if (st == KVMEM_HIP_OK) {
             ctx->h2d_bytes += static_cast<uint64_t>(n) * span;
@@ -2041,7 +2111,7 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
         items[4 * i + 3] = item_pos0(pool, block_ids, i, T);
     }
     JobTables jt;
-    if (!upload_block_job(ctx, pool, want_v, items, xp, jt)) {
+    if (!stage_block_job(ctx, pool, want_v, items, xp, jt)) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     perf_begin(ctx, kPerfSet);
@@ -2078,15 +2148,14 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
             !hip_ok(ctx, hipStreamWaitEvent(ctx->stream, ctx->h2d_copied[r], 0), "h2d wait copied")) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
-        const uint32_t *batch_items = jt.items + 4 * static_cast<size_t>(first);
-        const BlockSource sk = make_block_source(pool->type_k, slot_base, span, layer_bytes, jt.layers,
-                                                 L, T, hist->n_embd_k, batch_items, xp, true, jt.theta);
+        const BlockSource sk = make_block_source(pool->type_k, slot_base, span, layer_bytes, jt,
+                                                 L, T, hist->n_embd_k, first, xp, true);
         BlockSource sv{};
         if (want_v) {
-            sv = make_block_source(pool->type_v, slot_base + kbytes, span, layer_bytes, jt.layers + L, L,
-                                   T, hist->n_embd_v, batch_items, xp, false, jt.theta);
+            sv = make_block_source(pool->type_v, slot_base + kbytes, span, layer_bytes, jt, L,
+                                   T, hist->n_embd_v, first, xp, false);
         }
-        st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, cnt, xp);
+        st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, cnt, xp, jt.tables.args);
         if (st != KVMEM_HIP_OK) {
             return st;
         }
@@ -2153,17 +2222,17 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
                 }
             }
         }
-        // one upload: the K and V layer tables, then the segments
+        // the K and V layer tables, then the segments (in the kernel arguments when they fit)
         const uint32_t L = pool->n_layers;
-        const size_t ptr_bytes = 2 * L * sizeof(void *);
-        std::vector<uint8_t> table(ptr_bytes + segs.size() * sizeof(ChainSeg));
-        std::memcpy(table.data(), pool->k_layers, L * sizeof(void *));
-        if (want_v) {
-            std::memcpy(table.data() + L * sizeof(void *), pool->v_layers, L * sizeof(void *));
+        const bool narrow = pool->n_slots <= 65536u && pool->block_tokens <= 65535u;
+        std::vector<uint8_t> table;
+        if (narrow) {
+            chain_table<uint16_t>(pool, want_v, segs, table);
+        } else {
+            chain_table<uint32_t>(pool, want_v, segs, table);
         }
-        std::memcpy(table.data() + ptr_bytes, segs.data(), segs.size() * sizeof(ChainSeg));
-        uint8_t *tdev = static_cast<uint8_t *>(upload(ctx, table.data(), table.size(), "move_slots chains"));
-        if (!tdev) {
+        LaunchTables chain_tables;
+        if (!stage_tables(ctx, table.data(), table.size(), chain_tables, "move_slots chains")) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
         uint64_t moved = 0;
@@ -2173,9 +2242,7 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
             }
         }
         ChainParams cp{};
-        cp.k_layers = reinterpret_cast<uint8_t *const *>(tdev);
-        cp.v_layers = want_v ? cp.k_layers + L : nullptr;
-        cp.segs = reinterpret_cast<const ChainSeg *>(tdev + ptr_bytes);
+        cp.tables = chain_tables.dev;
         cp.scratch = scratch;
         cp.kspan = kspan;
         cp.vspan = vspan;
@@ -2189,12 +2256,12 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
         if (nvec > 0x7fffffffu) {
             return fail(ctx, KVMEM_HIP_ERR_INVALID, "move_slots: slot too large");
         }
-        const CopyOpDev *dops = ops.empty() ? nullptr : upload_copy_ops(ctx, ops, "move_slots save");
-        if (!ops.empty() && !dops) {
+        LaunchTables save_tables;
+        if (!ops.empty() && !stage_copy_ops(ctx, ops, save_tables, "move_slots save")) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
         perf_begin(ctx, kPerfLayout);
-        if (!launch_uploaded_copies(ctx, dops, ops.size(), "move_slots save")) {
+        if (!launch_staged_copies(ctx, save_tables, ops.size(), "move_slots save")) {
             perf_end(ctx, kPerfLayout);
             return KVMEM_HIP_ERR_RUNTIME;
         }
@@ -2203,7 +2270,11 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
             perf_end(ctx, kPerfLayout);
             return KVMEM_HIP_ERR_RUNTIME;
         }
-        move_chain_kernel<<<grid, 256, 0, ctx->stream>>>(cp);
+        if (narrow) {
+            move_chain_kernel<uint16_t><<<grid, 256, 0, ctx->stream>>>(cp, chain_tables.args);
+        } else {
+            move_chain_kernel<uint32_t><<<grid, 256, 0, ctx->stream>>>(cp, chain_tables.args);
+        }
         perf_end(ctx, kPerfLayout);
         ctx->d2d_bytes += per_move * saved.size() + moved;
         return hip_ok(ctx, hipGetLastError(), "move_slots chain launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;

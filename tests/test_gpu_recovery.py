@@ -42,25 +42,31 @@ def test_failed_apply_is_recovered_bit_exact(oracle, mode):
     cap, nb, budget = 40, 40, 8
     k, v, q1 = history(cap, seed=41)
     q2 = (q1.float() * -1.0).to(torch.bfloat16)
-    with make_engine(budget, 4, kv.TYPE_Q8_0, kv.TYPE_Q4_0,
-                     canonical_layout=int(mode == "canonical")) as eng:
+    hb = store = None
+    span = L * T * (kv.row_size(kv.TYPE_Q8_0, E) + kv.row_size(kv.TYPE_Q4_0, E))
+    if mode == "pinned_packed":
+        hb = block_major_pinned(k, v, nb)
+        store = torch.zeros(nb * span, dtype=torch.uint8, pin_memory=True)
+
+    def fresh_engine():
+        """The same starting state for every injection point: sel1 applied."""
+        eng = make_engine(budget, 4, kv.TYPE_Q8_0, kv.TYPE_Q4_0, canonical_layout=int(mode == "canonical"))
         eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
-        keep = []
         if mode == "pinned_packed":
-            hb = block_major_pinned(k, v, nb)
-            span = L * T * (kv.row_size(kv.TYPE_Q8_0, E) + kv.row_size(kv.TYPE_Q4_0, E))
-            store = torch.zeros(nb * span, dtype=torch.uint8, pin_memory=True)
-            keep = [hb, store]
+            store.zero_()
             eng.set_host_history(hb.data_ptr(), nb)
             eng.set_packed_host(store.data_ptr(), nb)
-        ctx = kv.Context.borrow(eng.ctx_handle())
-        sel1 = eng.preview(q1.data_ptr(), q1.shape[1])
-        sel2 = eng.preview(q2.data_ptr(), q2.shape[1])
-        assert set(sel1.blocks) != set(sel2.blocks)
-        eng.apply(sel1)
-        check_pool(eng, oracle, k, v, sel1.blocks, kv.TYPE_Q8_0, kv.TYPE_Q4_0)
-        n_failed = 0
-        for nth in range(1, 64):
+        return eng
+
+    n_failed = 0
+    for nth in range(1, 64):
+        with fresh_engine() as eng:
+            ctx = kv.Context.borrow(eng.ctx_handle())
+            sel1 = eng.preview(q1.data_ptr(), q1.shape[1])
+            sel2 = eng.preview(q2.data_ptr(), q2.shape[1])
+            assert set(sel1.blocks) != set(sel2.blocks)
+            eng.apply(sel1)
+            check_pool(eng, oracle, k, v, sel1.blocks, kv.TYPE_Q8_0, kv.TYPE_Q4_0)
             ctx.debug_fail_after(ALL_KINDS, nth)
             try:
                 eng.apply(sel2)
@@ -88,10 +94,13 @@ def test_failed_apply_is_recovered_bit_exact(oracle, mode):
                 assert [slots[b] for b in sel2.blocks] == list(range(len(sel2.blocks)))
             eng.apply(sel1)
             check_pool(eng, oracle, k, v, sel1.blocks, kv.TYPE_Q8_0, kv.TYPE_Q4_0)
-        else:
-            raise AssertionError("apply never ran to completion")
-        assert n_failed >= 2, n_failed
-        del keep
+    else:
+        raise AssertionError("apply never ran to completion")
+    # a device-history apply is one launch (its tables travel in the kernel
+    # arguments); slot moves add the chain launch (and saves), the pinned
+    # packed store the stage-out of evicted blocks
+    assert n_failed >= {"device": 1, "canonical": 2, "pinned_packed": 2}[mode], n_failed
+    del hb, store
 
 
 def test_set_device_history_grows_resident_tail(oracle):
