@@ -195,12 +195,26 @@ __global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops_
         table_base(reinterpret_cast<const uint8_t *>(ops_dev), t))[i];
     const uintptr_t a = reinterpret_cast<uintptr_t>(op.src) | reinterpret_cast<uintptr_t>(op.dst);
     if ((a & 15u) == 0 && (op.nbytes & 15u) == 0) {
-        const uint4 *s = reinterpret_cast<const uint4 *>(op.src);
-        uint4 *d = reinterpret_cast<uint4 *>(op.dst);
+        // four 16-byte loads in flight per thread, nontemporal both ways (a
+        // copy streams at ~6.0 TB/s so, against ~4.5-5.4 with one load)
+        const u32x4_t *s = reinterpret_cast<const u32x4_t *>(op.src);
+        u32x4_t *d = reinterpret_cast<u32x4_t *>(op.dst);
         const uint64_t n16 = op.nbytes >> 4;
         const uint64_t j1 = n16 * (piece + 1) / pieces;
-        for (uint64_t j = n16 * piece / pieces + threadIdx.x; j < j1; j += blockDim.x) {
-            d[j] = s[j];
+        uint64_t j = n16 * piece / pieces + threadIdx.x;
+        for (; j + 3u * blockDim.x < j1; j += 4u * blockDim.x) {
+            u32x4_t v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                v[u] = __builtin_nontemporal_load(s + j + u * blockDim.x);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                __builtin_nontemporal_store(v[u], d + j + u * blockDim.x);
+            }
+        }
+        for (; j < j1; j += blockDim.x) {
+            __builtin_nontemporal_store(__builtin_nontemporal_load(s + j), d + j);
         }
         return;
     }

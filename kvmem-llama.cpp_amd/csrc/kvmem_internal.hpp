@@ -134,6 +134,32 @@ struct ArgTables {
 __device__ inline const uint8_t *table_base(const uint8_t *dev, const ArgTables &t) {
     return dev ? dev : t.bytes;
 }
+// Table pointers stay generic: a pointer into a kernel's ArgTables must never
+// go through an integer (its parameter would be copied to private memory and
+// the integer would hold a private-aperture address).  tab_read() reads a
+// value at a byte offset of a launch's tables without forming one: from an
+// uploaded table through the constant address space (a scalar load when the
+// offset is uniform), else from the argument bytes by direct indexing (a
+// scalar load from the argument segment).
+template <typename T>
+__device__ inline T tab_read(const uint8_t *dev, const ArgTables &t, uint32_t off) {
+    if (dev) {
+        return *reinterpret_cast<const __attribute__((address_space(4))) T *>(
+            reinterpret_cast<uintptr_t>(dev) + off);
+    }
+    T v;
+    __builtin_memcpy(&v, &t.bytes[off], sizeof(T));
+    return v;
+}
+
+// A device-memory address (an allocation, never a kernel parameter) in the
+// global address space: global_load / global_store instead of flat ones.
+template <typename T>
+using global_ptr = __attribute__((address_space(1))) T *;
+template <typename T>
+__device__ inline global_ptr<T> as_global(T *p) {
+    return reinterpret_cast<global_ptr<T>>(reinterpret_cast<uintptr_t>(p));
+}
 
 // Tables for one launch: copied into `args` when they fit (dev = null),
 // else uploaded (dev = the device copy).  False on an upload failure.

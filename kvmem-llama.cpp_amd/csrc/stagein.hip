@@ -1775,67 +1775,92 @@ struct ChainParams {
     uint32_t vec_per_layer;        // T * (krow16 + vrow16)
 };
 
-// A chain segment as the kernel reads it: after the layer pointers, one
-// header per segment, then a pool of slot / row-count entries (16-bit when
-// the pool's slots and tokens fit, else 32-bit) where the segment's run is
-// slot[0 .. len] followed by nt[0 .. len-1].  About 2.5 entries per move
-// instead of a fixed 19 words per segment, so a step's table fits in the
-// kernel arguments.
-struct SegHdr {
-    uint32_t off_len;  // run offset in the pool << 4 | len (1 .. kChainSeg)
-    int32_t saved;     // >= 0: slot[0]'s rows are this scratch entry
-};
+// A chain segment as the kernel reads it, after the layer pointers: a
+// fixed-size record of IdxT entries (16-bit when the pool's slots and
+// tokens fit, else 32-bit): [len, saved + 1 (0: none), slot[0 .. 8],
+// nt[0 .. 7]], padded to whole 4-byte words.  40 bytes per segment in
+// 16-bit entries, so a step's table fits in the kernel arguments; one
+// unconditional read of the record per workgroup.
+template <typename IdxT>
+constexpr uint32_t seg_record_words() {
+    return (static_cast<uint32_t>(sizeof(IdxT)) * (2 * kChainSeg + 3) + 3) / 4;
+}
 
 // The N moves of one segment for one 16-byte column: N loads, then N stores
 // (rows at or past a move's n_tokens are inside the slot but not stored).
-template <int N, typename IdxT>
-__device__ inline void seg_moves(const IdxT *slot, const IdxT *nt, const uint8_t *first, uint8_t *base,
-                                 uint64_t span, uint64_t off, uint32_t r) {
+// Streamed bytes: nontemporal loads and stores.
+template <int N>
+__device__ inline void seg_moves(const uint32_t (&slot)[kChainSeg + 1], const uint32_t (&nt)[kChainSeg],
+                                 const uint8_t *first, uint8_t *base, uint64_t span, uint64_t off,
+                                 uint32_t r) {
     u32x4_t val[N];
-    val[0] = *reinterpret_cast<const u32x4_t *>(first);
+    val[0] = __builtin_nontemporal_load(as_global(reinterpret_cast<const u32x4_t *>(first)));
 #pragma unroll
     for (int j = 1; j < N; ++j) {
-        val[j] = *reinterpret_cast<const u32x4_t *>(base + static_cast<uint64_t>(slot[j]) * span + off);
+        val[j] = __builtin_nontemporal_load(
+            as_global(reinterpret_cast<const u32x4_t *>(base + static_cast<uint64_t>(slot[j]) * span + off)));
     }
 #pragma unroll
     for (int j = 0; j < N; ++j) {
         if (r < nt[j]) {
-            *reinterpret_cast<u32x4_t *>(base + static_cast<uint64_t>(slot[j + 1]) * span + off) = val[j];
+            __builtin_nontemporal_store(val[j], as_global(reinterpret_cast<u32x4_t *>(
+                                                    base + static_cast<uint64_t>(slot[j + 1]) * span + off)));
         }
     }
 }
 
-// grid (column blocks, segments)
+// grid (column blocks, segments): one 16-byte column per thread.  (Slot-
+// scattered copies measured 5.9 TB/s with one column per thread and
+// nontemporal accesses, 5.2 with four or eight.)  The segment's header and
+// run are read once per workgroup into scalar registers.
 template <typename IdxT>
 __global__ __launch_bounds__(256) void move_chain_kernel(ChainParams p, ArgTables t) {
-    const uint8_t *tb = table_base(p.tables, t);
-    uint8_t *const *k_layers = reinterpret_cast<uint8_t *const *>(tb);
-    uint8_t *const *v_layers = k_layers + p.L;
-    const SegHdr *hdr = reinterpret_cast<const SegHdr *>(tb + 2u * p.L * sizeof(void *));
-    const SegHdr h = hdr[blockIdx.y];
-    const uint32_t len = h.off_len & 15u;
-    const IdxT *slot = reinterpret_cast<const IdxT *>(hdr + gridDim.y) + (h.off_len >> 4);
-    const IdxT *nt = slot + len + 1u;
-    const uint32_t x = blockIdx.x * 256u + threadIdx.x;
-    if (x >= p.L * p.vec_per_layer) {
+    constexpr uint32_t W = seg_record_words<IdxT>();
+    const uint32_t rec = 2u * p.L * static_cast<uint32_t>(sizeof(void *)) + blockIdx.y * W * 4u;
+    uint32_t w[W];
+#pragma unroll
+    for (uint32_t i = 0; i < W; ++i) {
+        w[i] = tab_read<uint32_t>(p.tables, t, rec + 4u * i);
+    }
+    auto entry = [&](uint32_t e) -> uint32_t {  // e is a constant after unrolling
+        if constexpr (sizeof(IdxT) == 2) {
+            return (w[e >> 1] >> (16u * (e & 1u))) & 0xffffu;
+        } else {
+            return w[e];
+        }
+    };
+    const uint32_t len = entry(0);
+    const int32_t saved = static_cast<int32_t>(entry(1)) - 1;
+    uint32_t slot[kChainSeg + 1], nt[kChainSeg];
+#pragma unroll
+    for (uint32_t j = 0; j <= kChainSeg; ++j) {
+        slot[j] = entry(2u + j);
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kChainSeg; ++j) {
+        nt[j] = entry(3u + kChainSeg + j);
+    }
+    const uint64_t total = static_cast<uint64_t>(p.L) * p.vec_per_layer;  // < 2^31
+    const uint64_t x = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+    if (x >= total) {
         return;
     }
-    const uint32_t l = x / p.vec_per_layer;
-    uint32_t v = x - l * p.vec_per_layer;
     const uint32_t kvecs = p.T * p.krow16;
+    const uint32_t l = static_cast<uint32_t>(x) / p.vec_per_layer;
+    uint32_t v = static_cast<uint32_t>(x) - l * p.vec_per_layer;
     const bool is_v = v >= kvecs;
     if (is_v) {
         v -= kvecs;
     }
     const uint32_t r = v / (is_v ? p.vrow16 : p.krow16);  // row within the slot
-    uint8_t *base = is_v ? v_layers[l] : k_layers[l];
+    uint8_t *base = reinterpret_cast<uint8_t *>(
+        tab_read<uint64_t>(p.tables, t, (is_v ? p.L + l : l) * static_cast<uint32_t>(sizeof(void *))));
     const uint64_t span = is_v ? p.vspan : p.kspan;
     const uint64_t off = static_cast<uint64_t>(v) * 16u;
     // Every slot of a segment is distinct (a cycle's closing source comes
-    // from scratch), so all the segment's loads go first, then its stores:
-    // up to kChainSeg loads in flight per thread.
-    const uint8_t *first = h.saved >= 0
-        ? p.scratch + static_cast<uint64_t>(h.saved) * p.entry_bytes + l * (p.kspan + p.vspan) +
+    // from scratch), so all the segment's loads go first, then its stores.
+    const uint8_t *first = saved >= 0
+        ? p.scratch + static_cast<uint64_t>(saved) * p.entry_bytes + l * (p.kspan + p.vspan) +
               (is_v ? p.kspan : 0u) + off
         : base + static_cast<uint64_t>(slot[0]) * span + off;
     static_assert(kChainSeg == 8, "one case per segment length");
@@ -1852,33 +1877,28 @@ __global__ __launch_bounds__(256) void move_chain_kernel(ChainParams p, ArgTable
     }
 }
 
-// The kernel's table for `segs`: layer pointers, headers, the entry pool.
+// The kernel's table for `segs`: layer pointers, then one record per segment.
 template <typename IdxT>
 static void chain_table(const kvmem_hip_pool *pool, bool want_v, const std::vector<ChainSeg> &segs,
                         std::vector<uint8_t> &table) {
     const uint32_t L = pool->n_layers;
     const size_t ptr_bytes = 2 * L * sizeof(void *);
-    size_t entries = 0;
-    for (const ChainSeg &sg : segs) {
-        entries += 2 * sg.len + 1;
-    }
-    table.assign(ptr_bytes + segs.size() * sizeof(SegHdr) + entries * sizeof(IdxT), 0);
+    const size_t rec_bytes = 4 * seg_record_words<IdxT>();
+    table.assign(ptr_bytes + segs.size() * rec_bytes, 0);
     std::memcpy(table.data(), pool->k_layers, L * sizeof(void *));
     if (want_v) {
         std::memcpy(table.data() + L * sizeof(void *), pool->v_layers, L * sizeof(void *));
     }
-    SegHdr *hdr = reinterpret_cast<SegHdr *>(table.data() + ptr_bytes);
-    IdxT *ent = reinterpret_cast<IdxT *>(hdr + segs.size());
-    uint32_t off = 0;
     for (size_t i = 0; i < segs.size(); ++i) {
         const ChainSeg &sg = segs[i];
-        hdr[i].off_len = (off << 4) | sg.len;
-        hdr[i].saved = sg.saved;
-        for (uint32_t j = 0; j <= sg.len; ++j) {
-            ent[off++] = static_cast<IdxT>(sg.slot[j]);
+        IdxT *r = reinterpret_cast<IdxT *>(table.data() + ptr_bytes + i * rec_bytes);
+        r[0] = static_cast<IdxT>(sg.len);
+        r[1] = static_cast<IdxT>(sg.saved + 1);
+        for (int j = 0; j <= kChainSeg; ++j) {
+            r[2 + j] = static_cast<IdxT>(sg.slot[j]);
         }
-        for (uint32_t j = 0; j < sg.len; ++j) {
-            ent[off++] = static_cast<IdxT>(sg.nt[j]);
+        for (int j = 0; j < kChainSeg; ++j) {
+            r[3 + kChainSeg + j] = static_cast<IdxT>(sg.nt[j]);
         }
     }
 }
@@ -2224,7 +2244,8 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
         }
         // the K and V layer tables, then the segments (in the kernel arguments when they fit)
         const uint32_t L = pool->n_layers;
-        const bool narrow = pool->n_slots <= 65536u && pool->block_tokens <= 65535u;
+        // 16-bit records when every slot, row count and saved entry fits
+        const bool narrow = pool->n_slots <= 65536u && pool->block_tokens <= 65535u && saved.size() < 65535u;
         std::vector<uint8_t> table;
         if (narrow) {
             chain_table<uint16_t>(pool, want_v, segs, table);
