@@ -814,6 +814,9 @@ int kvmem_engine_set_pool(kvmem_engine *e, void *const *k_layers, void *const *v
     if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
         return e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "set_pool");
     }
+    // the old tensors go: no block is resident in the pool from here on,
+    // also when the new pool cannot be allocated
+    drop_residency(e);
     if (e->own_pool) {
         for (void *ptr : e->pool_k) {
             if (ptr) (void) hipFree(ptr);
@@ -827,9 +830,10 @@ int kvmem_engine_set_pool(kvmem_engine *e, void *const *k_layers, void *const *v
         e->pool_v.assign(v_layers, v_layers + e->p.n_layers);
         e->own_pool = false;
     } else if (!alloc_own_pool(e)) {
+        // the layers allocated before the failure are freed with the
+        // engine; the null ones make every apply fail until a pool is set
         return e->fail(KVMEM_HIP_ERR_NOMEM, "set_pool: pool allocation");
     }
-    drop_residency(e);  // the new tensors hold none of the working set
     return KVMEM_HIP_OK;
 }
 
@@ -1274,6 +1278,11 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
     }
     if (!e->hist_k && !e->host_base) {
         return e->fail(KVMEM_HIP_ERR_INVALID, "apply: no history");
+    }
+    for (uint32_t l = 0; l < e->p.n_layers; ++l) {
+        if (!e->pool_k[l] || !e->pool_v[l]) {
+            return e->fail(KVMEM_HIP_ERR_INVALID, "apply: no pool (a failed set_pool)");
+        }
     }
     std::vector<uint32_t> ids(sel, sel + n_sel);
     const uint32_t n = e->rt.store().block_count();

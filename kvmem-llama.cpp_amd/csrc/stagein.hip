@@ -2215,12 +2215,21 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
             return fail(ctx, KVMEM_HIP_ERR_INVALID, "move_slots: n_tokens above block_tokens");
         }
     }
+    // every layer tensor the moves touch; the chain walk's 16-byte accesses
+    // also need them 16-byte aligned (else the moves gather and scatter)
+    bool aligned = true;
+    for (uint32_t l = 0; l < pool->n_layers; ++l) {
+        if (!pool->k_layers[l] || (want_v && !pool->v_layers[l])) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "move_slots: null layer tensor");
+        }
+        aligned = aligned && aligned16(pool->k_layers[l]) && (!want_v || aligned16(pool->v_layers[l]));
+    }
     const uint64_t per_move = (kspan + vspan) * pool->n_layers;
     (void) hipSetDevice(ctx->device);
     // distinct sources and destinations, 16-byte rows: chains, bytes moved once
     std::vector<ChainSeg> segs;
     std::vector<uint32_t> saved;
-    if (krow % 16 == 0 && vrow % 16 == 0 &&
+    if (aligned && krow % 16 == 0 && vrow % 16 == 0 &&
         build_chains(src_slots, dst_slots, n_tokens, n, pool->block_tokens, pool->n_slots, segs, saved) &&
         segs.size() <= 65535) {
         if (segs.empty()) {

@@ -276,6 +276,33 @@ def test_move_slots_overlapping(ctx):
             assert np.array_equal(got, want)
 
 
+def test_move_slots_null_layer_refused_unaligned_layers_moved(ctx):
+    announce("move_slots: a null V layer is refused; layers at 2-byte offsets move by gather/scatter")
+    L, n_slots, T, E = 2, 8, 16, 256
+    rb = kv.row_size(kv.TYPE_Q8_0, E)
+    span = n_slots * T * rb
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+    raw = [torch.randint(0, 256, (span + 16,), dtype=torch.uint8, device="cuda", generator=g)
+           for _ in range(2 * L)]
+    ptrs = [r.data_ptr() + 2 for r in raw]  # every layer tensor 2 bytes past 16-byte alignment
+    null_v = ctx.make_pool(L, n_slots, T, E, E, kv.TYPE_Q8_0, kv.TYPE_Q8_0, ptrs[:L], [ptrs[L], 0])
+    torch.cuda.synchronize()
+    with pytest.raises(kv.KvMemError):
+        ctx.move_slots(null_v, [1], [0])
+    before = [r.cpu().numpy()[2:2 + span].reshape(n_slots, -1).copy() for r in raw]
+    pool = ctx.make_pool(L, n_slots, T, E, E, kv.TYPE_Q8_0, kv.TYPE_Q8_0, ptrs[:L], ptrs[L:])
+    src, dst = [1, 2, 3, 5, 0], [0, 1, 2, 3, 5]     # a chain and a cycle through slot 0
+    ctx.move_slots(pool, src, dst)
+    ctx.sync()
+    for i, r in enumerate(raw):
+        out = r.cpu().numpy()
+        want = before[i].copy()
+        for s, d in zip(src, dst):
+            want[d] = before[i][s]
+        assert np.array_equal(out[2:2 + span].reshape(n_slots, -1), want)
+
+
 def move_case(case: str, n_slots: int, rng):
     """(src, dst) slot lists: long chains, cycles, or a set with a shared
     source (which takes the gather/scatter path)."""
