@@ -333,9 +333,11 @@ KVMEM_HIP_API int kvmem_hip_stagein_packed_host(kvmem_hip_ctx *ctx,
  * their bytes).  n_tokens == NULL moves whole slots.  The result is as if
  * every source were read before any destination is written, whatever the
  * overlap.  When sources are distinct and destinations are distinct (a
- * canonical layout's moves), chains and cycles of moves are walked
- * backwards and the bytes move once; other sets are gathered to device
- * scratch and scattered, destinations in list order.  Replaces the
+ * canonical layout's moves) and the layer tensors and rows are 16-byte
+ * aligned, chains and cycles of moves are walked in segments and the bytes
+ * move once; other sets are gathered to device scratch and scattered,
+ * destinations in list order.  Every layer tensor of the pool must be
+ * non-null (KVMEM_HIP_ERR_INVALID otherwise, nothing issued).  Replaces the
  * gather/scatter D2D of layout_gpu_slots_by_orig_pos, which moves each
  * block's n_tokens rows (llama-memory-kvmem.cpp:1003-1093). */
 KVMEM_HIP_API int kvmem_hip_move_slots(kvmem_hip_ctx *ctx,
