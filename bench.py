@@ -8,8 +8,9 @@ Workload (the full reselect step at 256K, 16 attention layers):
   pool     256 + 128 slots of 128 cells per layer, K and V q8_0
   step     score every block (per-token max of q.k/16, mean over layers) ->
            top-256 with block 0 kept as sink, ascending -> diff against the
-           resident selection -> stage-in of the changed blocks (77 of 256,
-           ~30 %) quantized to q8_0 into the slots the outgoing blocks free.
+           resident selection and slot plan on the device -> slot moves
+           (slot i = i-th selected block) -> stage-in of the changed blocks
+           (77 of 256, ~30 %) quantized to q8_0.
 Each timed step starts from the same previous selection: between timed
 steps an untimed restore re-applies it (the same stage-in path).
 
@@ -17,7 +18,8 @@ Prints ONE JSON line.  `value` is ms per agent step (lower is better) with
 history and query resident in HBM, the pool laid out as the reference lays
 it out (slot i = i-th selected block), with the HIP timing events of the
 rooflines on; `ms_per_step_no_timing_events` is the same steps timed again
-without them; `lifo_layout` is the same step without the slot moves.  `mixed_precision` (Student-t history, K q8_0 +
+without them; `host_planned` is the same step with the diff and slot plan
+on the host, `lifo_layout` the same step without the slot moves.  `mixed_precision` (Student-t history, K q8_0 +
 V q4_0, then K and V q5_0) and `recall_1m` (8192 blocks, 512-token query,
 32 planted blocks, budget 512) are the other workloads' steps, in the same
 line unless --no-configs.  `roofline` is the MFMA block scorer
@@ -105,6 +107,7 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
         step()
         restore()
     times, bare, staged, moved, score_ms, set_ms, sel_ms, layout_ms = [], [], [], [], 0.0, 0.0, 0.0, 0.0
+    planned = []
     d2d_bytes = 0
     for _ in range(steps):
         ctx.perf_enable(True)
@@ -123,6 +126,7 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
         d2d_bytes += pf["d2d_bytes"]
         staged.append(st["n_staged"])
         moved.append(st["n_moved"])
+        planned.append(st.get("device_planned", 0))
         restore()
         # the same step without the timing events (each event is a packet of
         # its own on the stream), interleaved so that both see the same
@@ -137,7 +141,8 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
     return {"ms_step": 1e3 * sum(times) / steps, "ms_step_no_events": 1e3 * sum(bare) / steps,
             "score_ms": score_ms / steps,
             "set_ms": set_ms / steps, "sel_ms": sel_ms / steps, "n_staged": staged[0],
-            "layout_ms": layout_ms / steps, "n_moved": max(moved), "d2d_bytes": d2d_bytes // steps}
+            "layout_ms": layout_ms / steps, "n_moved": max(moved), "d2d_bytes": d2d_bytes // steps,
+            "device_planned": min(planned)}
 
 
 def stage_bytes(kv, n_blocks: int, type_k: int, type_v: int) -> int:
@@ -374,6 +379,7 @@ def run_reselect_256k(a, torch, kv, workloads) -> dict:
                                        if m["layout_ms"] > 0 else None)},
         "parts_ms": {"score_kernel": round(m["score_ms"], 4), "topk_kernel": round(m["sel_ms"], 4),
                      "layout_kernels": round(m["layout_ms"], 4), "stagein_kernel": round(m["set_ms"], 4)},
+        "beside_scorer_ms": round(m["ms_step"] - m["score_ms"], 4),
     }
     if not a.no_pinned:
         incoming = sorted(set(sel) - set(prev))
@@ -382,6 +388,8 @@ def run_reselect_256k(a, torch, kv, workloads) -> dict:
         log("cpu baseline (oracle restatement on host cores)")
         result["cpu_baseline"] = cpu_baseline(torch, k, v, q, sorted(set(sel) - set(prev)))
     eng.close()
+    result["device_planned"] = m["device_planned"]
+    result["host_planned"] = host_planned_mode(a, torch, kv, k, v, q, prev)
     result["lifo_layout"] = lifo_layout_mode(a, torch, kv, k, v, q, prev)
     if not a.no_pinned:
         result["pinned_host"]["step"] = pinned_host_step(a, torch, kv, k, v, q, prev)
@@ -393,6 +401,24 @@ def run_reselect_256k(a, torch, kv, workloads) -> dict:
         result["recall_1m"] = run_recall_1m(a, torch, kv, workloads)
         torch.cuda.empty_cache()
     return result
+
+
+def host_planned_mode(a, torch, kv, k, v, q, prev: list) -> dict:
+    """The same step planned on the host (device_plan = 0): the host waits
+    for the selection, plans the diff and the slot moves and launches them.
+    `beside_scorer_ms` is the step less its scorer, the part the plan
+    changes (the scorer's own duration follows the power-capped clock)."""
+    log("host-planned: the same step with the diff and slot plan on the host")
+    eng = make_engine(kv, torch, k, v, device_plan=0)
+    ctx = kv.Context.borrow(eng.ctx_handle())
+    m = timed_steps(eng, ctx, torch, q, TQ, prev, a.steps, a.warmup)
+    eng.close()
+    assert m["device_planned"] == 0
+    return {"ms_per_step": round(m["ms_step"], 4),
+            "ms_per_step_no_timing_events": round(m["ms_step_no_events"], 4),
+            "beside_scorer_ms": round(m["ms_step"] - m["score_ms"], 4),
+            "score_kernel_ms": round(m["score_ms"], 4), "layout_ms": round(m["layout_ms"], 4),
+            "stagein_kernel_ms": round(m["set_ms"], 4), "n_moved": m["n_moved"], "n_staged": m["n_staged"]}
 
 
 def lifo_layout_mode(a, torch, kv, k, v, q, prev: list) -> dict:
@@ -589,8 +615,10 @@ def run_meank_256k(a, torch, kv, workloads) -> dict:
                                "achieved": round(sums_bytes / (m["score_ms"] * 1e-3) / 1e9, 1),
                                "peak": HBM_PEAK_GBS, "unit": "GB/s", "algorithmic_bytes": sums_bytes,
                                "score_ms": round(m["score_ms"], 4)},
+            "ms_per_step_no_timing_events": round(m["ms_step_no_events"], 4),
             "parts_ms": {"score": round(m["score_ms"], 4), "stagein_kernel": round(m["set_ms"], 4),
-                         "topk": round(m["sel_ms"], 4)}}
+                         "topk": round(m["sel_ms"], 4), "layout_kernels": round(m["layout_ms"], 4)},
+            "n_staged": m["n_staged"], "n_moved": m["n_moved"]}
 
 
 def run_recall_1m(a, torch, kv, workloads) -> dict:

@@ -56,6 +56,8 @@ typedef struct kvmem_plan_stats {
     uint32_t total_window_tokens;
     uint32_t n_saved;                  /* evicted blocks copied to the packed host store */
     uint32_t n_restored;               /* staged blocks restored from packed rows */
+    uint32_t device_planned;           /* 1: the diff and slot plan ran on the device
+                                          (kvmem_engine_params.device_plan) */
 } kvmem_plan_stats;
 
 /* A half-open range [begin, end) of history rows (token positions);
@@ -162,6 +164,19 @@ typedef struct kvmem_engine_params {
                                   preview takes, the newest captured
                                   (--kvmem-query-last, default 64,
                                   tools/llama-kvmem-server.cpp:225, 1032-1038) */
+    int32_t device_plan;       /* 1 (default): apply_retrieval diffs the
+                                  selection and plans the slot moves on the
+                                  device, behind the top-k, so scoring,
+                                  top-k, the plan, the slot saves and the
+                                  chain walk run back to back with no host
+                                  round trip; the host meanwhile takes the
+                                  selection, commits the same plan to its
+                                  store and queues the stage-in behind the
+                                  walk (canonical layout, device-resident
+                                  history, no row transform or packed store,
+                                  budget <= 1024 blocks, pool <= 4096
+                                  slots, 16-byte rows).  0, or outside those
+                                  bounds: the host plans, as apply */
 } kvmem_engine_params;
 
 /* Block scorer of kvmem_engine_preview / apply_retrieval. */

@@ -184,15 +184,8 @@ void perf_collect(kvmem_hip_ctx *ctx) {
 // of it, 16-byte vectors when both addresses and the size are 16-byte
 // aligned.  A launch with few ops splits them so the chip fills.
 // ------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops_dev, ArgTables t, int n,
-                                                           int pieces) {
-    const int i = blockIdx.x / pieces;
-    const int piece = blockIdx.x - i * pieces;
-    if (i >= n) {
-        return;
-    }
-    const CopyOpDev op = reinterpret_cast<const CopyOpDev *>(
-        table_base(reinterpret_cast<const uint8_t *>(ops_dev), t))[i];
+// Piece `piece` of `pieces` of one copy op, by the calling workgroup.
+__device__ inline void copy_piece(const CopyOpDev &op, int piece, int pieces) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(op.src) | reinterpret_cast<uintptr_t>(op.dst);
     if ((a & 15u) == 0 && (op.nbytes & 15u) == 0) {
         // four 16-byte loads in flight per thread, nontemporal both ways (a
@@ -222,6 +215,44 @@ __global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops_
     for (uint64_t j = op.nbytes * piece / pieces + threadIdx.x; j < b1; j += blockDim.x) {
         op.dst[j] = op.src[j];
     }
+}
+
+__global__ __launch_bounds__(256) void batched_copy_kernel(const CopyOpDev *ops_dev, ArgTables t, int n,
+                                                           int pieces) {
+    const int i = blockIdx.x / pieces;
+    const int piece = blockIdx.x - i * pieces;
+    if (i >= n) {
+        return;
+    }
+    const CopyOpDev op = reinterpret_cast<const CopyOpDev *>(
+        table_base(reinterpret_cast<const uint8_t *>(ops_dev), t))[i];
+    copy_piece(op, piece, pieces);
+}
+
+// The same copies with their count in device memory (written by an earlier
+// kernel on the stream): min(*count, max_ops) ops of a device table, the
+// grid's workgroups taking (op, piece) pairs in turn.
+__global__ __launch_bounds__(256) void batched_copy_dev_kernel(const CopyOpDev *ops, const uint32_t *count,
+                                                               uint32_t max_ops, uint32_t pieces) {
+    const uint32_t n = min(*count, max_ops) * pieces;
+    for (uint32_t v = blockIdx.x; v < n; v += gridDim.x) {
+        const uint32_t i = v / pieces;
+        copy_piece(ops[i], static_cast<int>(v - i * pieces), static_cast<int>(pieces));
+    }
+}
+
+bool launch_dev_copies(kvmem_hip_ctx *ctx, const CopyOpDev *ops, const uint32_t *count, uint32_t max_ops,
+                       const char *what) {
+    if (max_ops == 0) {
+        return true;
+    }
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, what)) {
+        return false;
+    }
+    constexpr uint32_t kPieces = 8;
+    const uint32_t grid = static_cast<uint32_t>(std::min<uint64_t>(1024, uint64_t{max_ops} * kPieces));
+    batched_copy_dev_kernel<<<grid, 256, 0, ctx->stream>>>(ops, count, max_ops, kPieces);
+    return hip_ok(ctx, hipGetLastError(), what);
 }
 
 bool stage_tables(kvmem_hip_ctx *ctx, const void *src, size_t bytes, LaunchTables &out, const char *what) {
@@ -379,10 +410,11 @@ void kvmem_hip_destroy(kvmem_hip_ctx *ctx) {
         if (s.done) hipEventDestroy(s.done);
     }
     for (DevBuf *b : {&ctx->score_partial, &ctx->score_layers, &ctx->meank_scratch,
-                      &ctx->move_scratch, &ctx->h2d_ring, &ctx->d2h_ring}) {
+                      &ctx->move_scratch, &ctx->h2d_ring, &ctx->d2h_ring, &ctx->topk_dev, &ctx->plan}) {
         if (b->ptr) hipFree(b->ptr);
     }
     if (ctx->topk_sel_host.ptr) hipHostFree(ctx->topk_sel_host.ptr);
+    if (ctx->plan_counts.ptr) hipHostFree(ctx->plan_counts.ptr);
     for (int i = 0; i < 8; ++i) {
         if (ctx->h2d_copied[i]) hipEventDestroy(ctx->h2d_copied[i]);
         if (ctx->h2d_consumed[i]) hipEventDestroy(ctx->h2d_consumed[i]);

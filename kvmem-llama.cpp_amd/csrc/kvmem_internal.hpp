@@ -61,6 +61,21 @@ struct kvmem_hip_ctx {
     // sets to topk_epoch after the rest is visible (topk_flag_index).
     kvmem_hip::PinBuf topk_sel_host;
     uint32_t topk_epoch = 0;
+    // a launched top-k not yet waited for: its block count and largest
+    // selection; with a device copy of the selection in topk_dev ([0] =
+    // count, then the ids) for the device reselect plan
+    bool topk_pending = false;
+    uint32_t topk_n = 0;
+    uint32_t topk_limit = 0;
+    kvmem_hip::DevBuf topk_dev;
+    // device reselect plan: its tables (stage items, chain segments, slot
+    // saves) and counts, and the counts in host-mapped memory
+    kvmem_hip::DevBuf plan;
+    kvmem_hip::PinBuf plan_counts;
+    size_t plan_stage_off = 0;     // the stage table's offset in `plan`
+    uint32_t plan_max_sel = 0;     // stage entries the last plan wrote
+    uint64_t plan_row_bytes = 0;   // one moved row over every layer, K and V
+    uint64_t plan_save_bytes = 0;  // one saved slot over every layer, K and V
 
     // pinned-host stage-in: device ring of block buffers + events
     kvmem_hip::DevBuf h2d_ring;
@@ -152,6 +167,15 @@ __device__ inline T tab_read(const uint8_t *dev, const ArgTables &t, uint32_t of
     return v;
 }
 
+// A value at byte offset `off` of a table in device memory (an allocation,
+// never a kernel parameter), read through the constant address space: a
+// scalar load when the offset is uniform.  The table is not written by the
+// reading kernel.
+template <typename T>
+__device__ inline T cload(const uint8_t *dev, uint32_t off) {
+    return *reinterpret_cast<const __attribute__((address_space(4))) T *>(reinterpret_cast<uintptr_t>(dev) + off);
+}
+
 // A device-memory address (an allocation, never a kernel parameter) in the
 // global address space: global_load / global_store instead of flat ones.
 template <typename T>
@@ -176,6 +200,10 @@ bool stage_tables(kvmem_hip_ctx *ctx, const void *src, size_t bytes, LaunchTable
 bool launch_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, const char *what);
 bool stage_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, LaunchTables &out, const char *what);
 bool launch_staged_copies(kvmem_hip_ctx *ctx, const LaunchTables &tables, size_t n, const char *what);
+// Copies whose count an earlier kernel on the stream writes: min(*count,
+// max_ops) ops of the device table `ops` (a grid sized for max_ops).
+bool launch_dev_copies(kvmem_hip_ctx *ctx, const CopyOpDev *ops, const uint32_t *count, uint32_t max_ops,
+                       const char *what);
 
 // The pinned-host stage-in ring: kH2dRing device slots of at least
 // `min_slot_bytes` (32 MiB or more, grown only), with their events.
@@ -216,6 +244,13 @@ uint8_t *host_device_view(const void *p, uint64_t bytes);
 // Copy `bytes` of host data to device memory through the upload ring,
 // ordered on the context stream.  Returns the device address or nullptr.
 void *upload(kvmem_hip_ctx *ctx, const void *src, size_t bytes, const char *what);
+
+// Top-k in two halves (kvmem_hip_topk is both): topk_launch enqueues the
+// selection kernel (with `to_device`, also writing the selection to
+// ctx->topk_dev); topk_wait spins until the selection is on the host.
+int topk_launch(kvmem_hip_ctx *ctx, const float *scores, uint32_t n, const uint32_t *forced,
+                uint32_t n_forced, uint32_t need, int tie_lower_index, bool to_device);
+int topk_wait(kvmem_hip_ctx *ctx, uint32_t *sel_out, uint32_t *n_sel);
 
 // Profiling brackets around a stage's launches on the context stream.
 void perf_begin(kvmem_hip_ctx *ctx, PerfStage s);

@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "kvmem_host.h"
+#include "device_reselect.h"
 #include "kvmem_store.hpp"
 
 using kvmem_amd::Block;
@@ -73,6 +74,7 @@ void fill_stats(const Plan &p, uint32_t n_staged, uint32_t n_moved, uint32_t n_s
     st->retained_position_stable = p.retained_position_stable;
     st->retained_position_moved = p.retained_position_moved;
     st->total_window_tokens = p.total_window_tokens;
+    st->device_planned = 0;
 }
 
 // admit_incoming gives a block no slot when the free list is empty
@@ -553,6 +555,7 @@ kvmem_engine_params kvmem_engine_default_params(void) {
     p.attn_rot = 0;
     p.query_max_tokens = 512;
     p.query_last = 64;
+    p.device_plan = 1;
     return p;
 }
 
@@ -882,9 +885,8 @@ bool ensure_scores(kvmem_engine *e, uint32_t n) {
 
 // The store's charge (sink, mandatory, recent) then the device top-k over
 // d_scores for the remaining budget; ascending selection into sel.
-int select_topk(kvmem_engine *e, const std::vector<uint32_t> &mand, uint32_t *sel, uint32_t *n_sel) {
+int select_topk(kvmem_engine *e, const kvmem_amd::TopkCharge &charge, uint32_t *sel, uint32_t *n_sel) {
     const uint32_t n = e->rt.store().block_count();
-    const kvmem_amd::TopkCharge charge = e->rt.store().charge_topk(mand);
     std::vector<uint32_t> out;
     if (charge.all_fit) {
         out.resize(n);
@@ -1029,6 +1031,250 @@ int window_rows(kvmem_engine *e, std::vector<uint32_t> &rows) {
     return KVMEM_HIP_OK;
 }
 
+// The scoring half of a preview: the mandatory ids (the caller's, then the
+// spans'), the store's charge, and, unless every block fits the budget, the
+// scores of every block launched into d_scores (not waited for).  *empty:
+// the store has no block.
+int preview_scores(kvmem_engine *e, const void *q, int32_t q_type, uint32_t n_q_tokens,
+                   const uint32_t *mandatory, uint32_t n_mandatory, kvmem_amd::TopkCharge &charge,
+                   bool *empty) {
+    *empty = false;
+    if (!e->hist_k && (e->p.scorer != KVMEM_SCORER_MEAN_K || !e->host_base)) {
+        // the per-token scorer reads every key in HBM; the mean-K scorer
+        // also runs from a pinned host history's key sums
+        return e->fail(KVMEM_HIP_ERR_INVALID, "preview: no device history (the scorer reads keys in HBM)");
+    }
+    const uint32_t n = e->rt.store().block_count();
+    // no query pointer: the captured query window, its newest rows in token order
+    std::vector<uint32_t> win_rows;
+    if (!q) {
+        const int rc = window_rows(e, win_rows);
+        if (rc != KVMEM_HIP_OK) {
+            return rc;
+        }
+        n_q_tokens = static_cast<uint32_t>(win_rows.size());
+    }
+    if (n == 0) {
+        *empty = true;
+        return KVMEM_HIP_OK;
+    }
+    if (!ensure_scores(e, n)) {
+        return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: score buffer");
+    }
+    std::vector<uint32_t> mand(mandatory, mandatory + n_mandatory);
+    const std::vector<uint32_t> spans = e->retrieval_mandatory();
+    mand.insert(mand.end(), spans.begin(), spans.end());
+    charge = e->rt.store().charge_topk(mand);
+    if (charge.all_fit) {
+        return KVMEM_HIP_OK;
+    }
+    const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
+    if (e->p.scorer == KVMEM_SCORER_MEAN_K) {
+        // the reference's scorer over the sum of the query rows
+        if (!e->d_qsum &&
+            hipMalloc(&e->d_qsum, sizeof(float) * e->p.n_layers * n_embd_q) != hipSuccess) {
+            e->d_qsum = nullptr;
+            return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: query sums");
+        }
+        int rc = q ? kvmem_hip_q_accumulate(e->ctx, q, q_type, e->p.n_layers, n_q_tokens, n_embd_q, nullptr,
+                                            0, 1, e->d_qsum)
+                   // the window's rows summed in token order, as the harvest adds them
+                   : kvmem_hip_q_accumulate(e->ctx, e->d_qwin, KVMEM_TYPE_F32, e->p.n_layers, e->qwin_cap,
+                                            n_embd_q, win_rows.data(), n_q_tokens, 1, e->d_qsum);
+        if (rc != KVMEM_HIP_OK) {
+            return e->fail_ctx(rc, "preview query sums");
+        }
+        const std::vector<uint32_t> q_count(e->p.n_layers, n_q_tokens);
+        return meank_scores(e, e->d_qsum, q_count.data());
+    }
+    if (!q) {
+        // the window's rows in token order, as the bf16 query the scorer reads
+        const size_t bytes = 2u * static_cast<size_t>(e->p.n_layers) * e->qwin_cap * n_embd_q;
+        if (!e->d_qgather && hipMalloc(&e->d_qgather, bytes) != hipSuccess) {
+            e->d_qgather = nullptr;
+            return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: query window gather buffer");
+        }
+        const int rc = kvmem_hip_q_window_gather(e->ctx, e->d_qwin, e->p.n_layers, e->qwin_cap, n_embd_q,
+                                                 win_rows.data(), n_q_tokens, KVMEM_TYPE_BF16,
+                                                 e->d_qgather);
+        if (rc != KVMEM_HIP_OK) {
+            return e->fail_ctx(rc, "preview query window");
+        }
+        q = e->d_qgather;
+        q_type = KVMEM_TYPE_BF16;
+    }
+    const kvmem_hip_history h = e->device_history();
+    kvmem_hip_score_args a{};
+    a.q = q;
+    a.q_type = q_type;
+    a.n_q_tokens = n_q_tokens;
+    a.n_head = e->p.n_head;
+    a.n_head_kv = e->p.n_head_kv;
+    a.head_dim = e->p.head_dim;
+    a.layer_reduce = e->p.layer_reduce;
+    a.layer_scores = nullptr;
+    a.scores = e->d_scores;
+    const int rc = kvmem_hip_score(e->ctx, &h, &a);
+    return rc == KVMEM_HIP_OK ? rc : e->fail_ctx(rc, "preview score");
+}
+
+// The store's side of a canonical-layout apply of `ids` (ascending, unique,
+// in range): the plan committed (prepare_selection + finish_reselect), the
+// grown partial tail staged again, window slot i given to the i-th id.
+// Counts the blocks staged and the resident blocks that change slot.
+void commit_canonical(kvmem_engine *e, const std::vector<uint32_t> &ids, Plan &plan, uint32_t *n_staged,
+                      uint32_t *n_moved) {
+    const uint32_t n = e->rt.store().block_count();
+    std::vector<int32_t> old_slot(n, -1);
+    for (const Block &b : e->rt.store().blocks()) {
+        old_slot[b.block_id] = b.tier == Tier::GPU ? b.gpu_slot : -1;
+    }
+    e->slots.staged_ids.clear();
+    e->slots.staged_slots.clear();
+    plan = e->rt.prepare_selection(ids);
+    e->rt.finish_reselect();
+    std::vector<uint8_t> staged(n, 0);
+    for (uint32_t id : e->slots.staged_ids) staged[id] = 1;
+    if (e->dirty_tail >= 0) {
+        const uint32_t id = static_cast<uint32_t>(e->dirty_tail);
+        if (id < n && e->rt.store().blocks()[id].tier == Tier::GPU && e->rt.store().blocks()[id].gpu_slot >= 0) {
+            staged[id] = 1;
+        }
+        e->dirty_tail = -1;
+    }
+    *n_staged = 0;
+    *n_moved = 0;
+    for (uint32_t i = 0; i < ids.size(); ++i) {
+        const uint32_t id = ids[i];
+        if (staged[id]) {
+            ++*n_staged;
+        } else if (old_slot[id] >= 0 && static_cast<uint32_t>(old_slot[id]) != i) {
+            ++*n_moved;
+        }
+        e->rt.store().set_block_gpu_slot(id, static_cast<int32_t>(i));
+    }
+    e->slots.reset_after(static_cast<uint32_t>(ids.size()));
+}
+
+// Whether apply_retrieval can take the device plan: the parameters and the
+// pool it covers (the resident blocks' order is checked per call).
+bool device_plan_ok(const kvmem_engine *e) {
+    if (!e->p.device_plan || !e->p.canonical_layout || !e->hist_k || !e->hist_v || e->host_base ||
+        e->packed_base || e->has_xf || e->n_slots > KVMEM_PLAN_MAX_SLOTS || e->p.block_tokens > 65535u ||
+        kvmem_hip_row_size(e->p.type_k, e->n_embd_k) % 16 != 0 ||
+        kvmem_hip_row_size(e->p.type_v, e->n_embd_v) % 16 != 0) {
+        return false;
+    }
+    for (uint32_t l = 0; l < e->p.n_layers; ++l) {
+        if (!e->pool_k[l] || !e->pool_v[l]) {
+            return false;
+        }
+    }
+    return true;
+}
+
+// A device plan that failed part way may have moved or written any slot of
+// the window: nothing in the pool is trusted any more.
+int device_plan_failed(kvmem_engine *e, int code, const char *what) {
+    e->fail_ctx(code, what);
+    (void) kvmem_hip_sync(e->ctx);
+    drop_residency(e);
+    return code;
+}
+
+// apply_retrieval as one device pipeline: scorer, top-k, then (queued
+// behind it, sized on the device) the diff and slot plan, the slot saves
+// and the chain walk.  The host meanwhile waits for the selection, commits
+// the same plan to the store and queues the stage-in of the blocks it
+// stages while the walk runs, then checks the device's counts against its
+// own.  KVMEM_HIP_ERR_UNSUPPORTED (nothing issued):
+// take the host path.
+int apply_retrieval_device(kvmem_engine *e, const void *q, int32_t q_type, uint32_t n_q_tokens,
+                           const uint32_t *mandatory, uint32_t n_mandatory, kvmem_plan_stats *stats) {
+    const uint32_t n = e->rt.store().block_count();
+    if (n == 0 || (!e->hist_k && !e->host_base)) {
+        return KVMEM_HIP_ERR_UNSUPPORTED;
+    }
+    // the blocks whose pool rows are valid, ascending in id; a canonical
+    // pool holds them at ascending slots
+    std::vector<uint32_t> res_block, res_slot;
+    for (const Block &b : e->rt.store().blocks()) {
+        if (b.tier == Tier::GPU && b.gpu_slot >= 0) {
+            if (!res_slot.empty() && static_cast<uint32_t>(b.gpu_slot) <= res_slot.back()) {
+                return KVMEM_HIP_ERR_UNSUPPORTED;  // not a canonical pool
+            }
+            res_block.push_back(b.block_id);
+            res_slot.push_back(static_cast<uint32_t>(b.gpu_slot));
+        }
+    }
+    kvmem_amd::TopkCharge charge;
+    bool empty = false;
+    int rc = preview_scores(e, q, q_type, n_q_tokens, mandatory, n_mandatory, charge, &empty);
+    if (rc != KVMEM_HIP_OK) {
+        return rc;
+    }
+    const uint32_t max_sel = static_cast<uint32_t>(charge.forced.size()) + charge.need;
+    if (empty || charge.all_fit || max_sel == 0 || max_sel > KVMEM_PLAN_MAX_SEL || max_sel > e->n_slots) {
+        // outside the device plan: the host selects over the scores on the
+        // stream and plans
+        std::vector<uint32_t> sel(std::max<uint32_t>(1, n));
+        uint32_t n_sel = 0;
+        if (!empty) {
+            rc = select_topk(e, charge, sel.data(), &n_sel);
+            if (rc != KVMEM_HIP_OK) {
+                return rc;
+            }
+        }
+        return kvmem_engine_apply(e, e->epoch, e->rt.store().total_tokens(), sel.data(), n_sel, stats);
+    }
+    rc = kvmem_hip_topk_launch_dev(e->ctx, e->d_scores, n, charge.forced.data(),
+                                   static_cast<uint32_t>(charge.forced.size()), charge.need,
+                                   e->p.tie_lower_index);
+    if (rc != KVMEM_HIP_OK) {
+        return e->fail_ctx(rc, "apply_retrieval: top-k");
+    }
+    const uint32_t dirty = e->dirty_tail >= 0 ? static_cast<uint32_t>(e->dirty_tail) : UINT32_MAX;
+    const kvmem_hip_history h = e->device_history();
+    const kvmem_hip_pool pool = e->pool_desc();
+    rc = kvmem_hip_reselect_device(e->ctx, &h, &pool, res_block.data(), res_slot.data(),
+                                   static_cast<uint32_t>(res_block.size()), dirty, max_sel);
+    std::vector<uint32_t> sel(max_sel);
+    uint32_t n_sel = 0;
+    const int wrc = kvmem_hip_topk_wait(e->ctx, sel.data(), &n_sel);
+    if (rc != KVMEM_HIP_OK) {
+        return device_plan_failed(e, rc, "apply_retrieval: device plan");
+    }
+    if (wrc != KVMEM_HIP_OK) {
+        return device_plan_failed(e, wrc, "apply_retrieval: top-k");
+    }
+    sel.resize(n_sel);
+    Plan plan;
+    uint32_t n_staged = 0, n_moved = 0;
+    commit_canonical(e, sel, plan, &n_staged, &n_moved);
+    // queued while the chain walk runs: the stage-in of the blocks the
+    // device plan listed, as many as the store stages
+    rc = kvmem_hip_reselect_device_stagein(e->ctx, &h, &pool, n_staged);
+    if (rc != KVMEM_HIP_OK) {
+        return device_plan_failed(e, rc, "apply_retrieval: stage-in");
+    }
+    if (kvmem_hip_sync(e->ctx) != KVMEM_HIP_OK) {
+        return device_plan_failed(e, KVMEM_HIP_ERR_RUNTIME, "apply_retrieval sync");
+    }
+    uint32_t c[KVMEM_PLAN_N_COUNTS] = {};
+    (void) kvmem_hip_reselect_device_counts(e->ctx, c, KVMEM_PLAN_N_COUNTS);
+    if (c[KVMEM_PLAN_ERROR] != 0 || c[KVMEM_PLAN_SEL] != n_sel || c[KVMEM_PLAN_STAGE] != n_staged ||
+        c[KVMEM_PLAN_MOVES] != n_moved) {
+        e->fail(KVMEM_HIP_ERR_RUNTIME, "apply_retrieval: the device plan differs from the store's");
+        drop_residency(e);
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    fill_stats(plan, n_staged, n_moved, 0, 0, stats);
+    if (stats) {
+        stats->device_planned = 1;
+    }
+    return KVMEM_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1084,88 +1330,16 @@ int kvmem_engine_preview(kvmem_engine *e, const void *q, int32_t q_type, uint32_
     if (!sel || !n_sel || (n_mandatory && !mandatory)) {
         return e->fail(KVMEM_HIP_ERR_INVALID, "preview: null argument");
     }
-    if (!e->hist_k && (e->p.scorer != KVMEM_SCORER_MEAN_K || !e->host_base)) {
-        // the per-token scorer reads every key in HBM; the mean-K scorer
-        // also runs from a pinned host history's key sums
-        return e->fail(KVMEM_HIP_ERR_INVALID, "preview: no device history (the scorer reads keys in HBM)");
-    }
-    const uint32_t n = e->rt.store().block_count();
     *n_sel = 0;
     if (epoch) *epoch = e->epoch;
     if (rows) *rows = e->rt.store().total_tokens();
-    // no query pointer: the captured query window, its newest rows in token order
-    std::vector<uint32_t> win_rows;
-    if (!q) {
-        const int rc = window_rows(e, win_rows);
-        if (rc != KVMEM_HIP_OK) {
-            return rc;
-        }
-        n_q_tokens = static_cast<uint32_t>(win_rows.size());
+    kvmem_amd::TopkCharge charge;
+    bool empty = false;
+    const int rc = preview_scores(e, q, q_type, n_q_tokens, mandatory, n_mandatory, charge, &empty);
+    if (rc != KVMEM_HIP_OK || empty) {
+        return rc;
     }
-    if (n == 0) {
-        return KVMEM_HIP_OK;
-    }
-    if (!ensure_scores(e, n)) {
-        return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: score buffer");
-    }
-    std::vector<uint32_t> mand(mandatory, mandatory + n_mandatory);
-    const std::vector<uint32_t> spans = e->retrieval_mandatory();
-    mand.insert(mand.end(), spans.begin(), spans.end());
-    const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
-    if (!e->rt.store().charge_topk(mand).all_fit && e->p.scorer == KVMEM_SCORER_MEAN_K) {
-        // the reference's scorer over the sum of the query rows
-        if (!e->d_qsum &&
-            hipMalloc(&e->d_qsum, sizeof(float) * e->p.n_layers * n_embd_q) != hipSuccess) {
-            e->d_qsum = nullptr;
-            return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: query sums");
-        }
-        int rc = q ? kvmem_hip_q_accumulate(e->ctx, q, q_type, e->p.n_layers, n_q_tokens, n_embd_q, nullptr,
-                                            0, 1, e->d_qsum)
-                   // the window's rows summed in token order, as the harvest adds them
-                   : kvmem_hip_q_accumulate(e->ctx, e->d_qwin, KVMEM_TYPE_F32, e->p.n_layers, e->qwin_cap,
-                                            n_embd_q, win_rows.data(), n_q_tokens, 1, e->d_qsum);
-        if (rc != KVMEM_HIP_OK) {
-            return e->fail_ctx(rc, "preview query sums");
-        }
-        const std::vector<uint32_t> q_count(e->p.n_layers, n_q_tokens);
-        rc = meank_scores(e, e->d_qsum, q_count.data());
-        if (rc != KVMEM_HIP_OK) {
-            return rc;
-        }
-    } else if (!e->rt.store().charge_topk(mand).all_fit) {
-        if (!q) {
-            // the window's rows in token order, as the bf16 query the scorer reads
-            const size_t bytes = 2u * static_cast<size_t>(e->p.n_layers) * e->qwin_cap * n_embd_q;
-            if (!e->d_qgather && hipMalloc(&e->d_qgather, bytes) != hipSuccess) {
-                e->d_qgather = nullptr;
-                return e->fail(KVMEM_HIP_ERR_NOMEM, "preview: query window gather buffer");
-            }
-            const int rc = kvmem_hip_q_window_gather(e->ctx, e->d_qwin, e->p.n_layers, e->qwin_cap, n_embd_q,
-                                                     win_rows.data(), n_q_tokens, KVMEM_TYPE_BF16,
-                                                     e->d_qgather);
-            if (rc != KVMEM_HIP_OK) {
-                return e->fail_ctx(rc, "preview query window");
-            }
-            q = e->d_qgather;
-            q_type = KVMEM_TYPE_BF16;
-        }
-        const kvmem_hip_history h = e->device_history();
-        kvmem_hip_score_args a{};
-        a.q = q;
-        a.q_type = q_type;
-        a.n_q_tokens = n_q_tokens;
-        a.n_head = e->p.n_head;
-        a.n_head_kv = e->p.n_head_kv;
-        a.head_dim = e->p.head_dim;
-        a.layer_reduce = e->p.layer_reduce;
-        a.layer_scores = nullptr;
-        a.scores = e->d_scores;
-        const int rc = kvmem_hip_score(e->ctx, &h, &a);
-        if (rc != KVMEM_HIP_OK) {
-            return e->fail_ctx(rc, "preview score");
-        }
-    }
-    return select_topk(e, mand, sel, n_sel);
+    return select_topk(e, charge, sel, n_sel);
 }
 
 int kvmem_engine_capture_q(kvmem_engine *e, uint32_t layer, const void *q, int32_t q_type, size_t nb0,
@@ -1256,13 +1430,14 @@ int kvmem_engine_preview_meank(kvmem_engine *e, const float *q_sum, const uint32
     std::vector<uint32_t> mand(mandatory, mandatory + n_mandatory);
     const std::vector<uint32_t> spans = e->retrieval_mandatory();
     mand.insert(mand.end(), spans.begin(), spans.end());
-    if (!e->rt.store().charge_topk(mand).all_fit) {
+    const kvmem_amd::TopkCharge charge = e->rt.store().charge_topk(mand);
+    if (!charge.all_fit) {
         const int rc = meank_scores(e, q_sum, q_count);
         if (rc != KVMEM_HIP_OK) {
             return rc;
         }
     }
-    return select_topk(e, mand, sel, n_sel);
+    return select_topk(e, charge, sel, n_sel);
 }
 
 int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uint32_t *sel,
@@ -1414,6 +1589,15 @@ int kvmem_engine_apply_retrieval(kvmem_engine *e, const void *q, int32_t q_type,
                                  uint32_t n_mandatory, kvmem_plan_stats *stats) {
     if (!e) {
         return KVMEM_HIP_ERR_INVALID;
+    }
+    if ((n_mandatory && !mandatory)) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "apply_retrieval: null mandatory list");
+    }
+    if (device_plan_ok(e)) {
+        const int drc = apply_retrieval_device(e, q, q_type, n_q_tokens, mandatory, n_mandatory, stats);
+        if (drc != KVMEM_HIP_ERR_UNSUPPORTED) {
+            return drc;
+        }
     }
     std::vector<uint32_t> sel(std::max<uint32_t>(1, e->rt.store().block_count()));
     uint32_t n_sel = 0, rows = 0;

@@ -35,6 +35,7 @@
 // 8 .. width/2 exchange with lane ^ span/8.  The cos/sin of every (row,
 // rotary pair) of a chunk are computed once per workgroup into LDS.
 #include "kvmem_internal.hpp"
+#include "device_reselect.h"
 #include "move_plan.hpp"
 
 #include <algorithm>
@@ -169,12 +170,27 @@ struct BlockSource {
         const uint32_t item = op / n_layers;
         return chunk_at(item, op - item * n_layers, sub, out);
     }
-    // Chunk `sub` of the run of (item, layer).
+    // Chunk `sub` of the run of (item, layer).  Tables in device memory
+    // (uploaded, or written by an earlier kernel) are read through the
+    // constant address space: uniform scalar loads, as the argument bytes
+    // are, instead of vector loads the chunk's addresses would wait on.
     __device__ bool chunk_at(uint32_t item, uint32_t layer, uint32_t sub, Chunk &out) const {
-        const uint32_t block = items[4 * item + 0];
-        const uint32_t slot = items[4 * item + 1];
-        const uint32_t ntok = items[4 * item + 2];
-        out.pos0 = static_cast<int32_t>(items[4 * item + 3]);
+        uint32_t block, slot, ntok;
+        const uint8_t *ldst;
+        if (tables) {
+            const u32x4_t it = cload<u32x4_t>(tables, items_off + 16u * item);
+            block = it[0];
+            slot = it[1];
+            ntok = it[2];
+            out.pos0 = static_cast<int32_t>(it[3]);
+            ldst = reinterpret_cast<const uint8_t *>(cload<uint64_t>(tables, layer_off + 8u * layer));
+        } else {
+            block = items[4 * item + 0];
+            slot = items[4 * item + 1];
+            ntok = items[4 * item + 2];
+            out.pos0 = static_cast<int32_t>(items[4 * item + 3]);
+            ldst = layer_dst[layer];
+        }
         const uint32_t total = ntok * gpr;
         out.g0 = sub * chunk_groups;
         if (out.g0 >= total) {
@@ -182,8 +198,7 @@ struct BlockSource {
         }
         out.ng = min(chunk_groups, total - out.g0);
         out.src = base + block * block_stride + layer * layer_stride;
-        out.dst = const_cast<uint8_t *>(layer_dst[layer]) +
-                  static_cast<uint64_t>(slot) * block_tokens * row_bytes;
+        out.dst = const_cast<uint8_t *>(ldst) + static_cast<uint64_t>(slot) * block_tokens * row_bytes;
         out.gpr = gpr;
         out.src_stride = gpr * 64u;
         return true;
@@ -1768,11 +1783,14 @@ struct ChainParams {
     const uint8_t *tables;         // uploaded tables, or null: in the kernel's ArgTables
                                    // (K layer pointers [L], V layer pointers [L], segments)
     const uint8_t *scratch;        // entry e: [layer][T rows of K][T rows of V]
+    const uint32_t *dcount;        // segment count in device memory (a device plan), or
+                                   // null: one segment per grid row
     uint64_t kspan, vspan;         // one slot of one layer
     uint64_t entry_bytes;          // L * (kspan + vspan)
     uint32_t krow16, vrow16;       // row bytes / 16
     uint32_t L, T;
     uint32_t vec_per_layer;        // T * (krow16 + vrow16)
+    uint32_t max_segs;             // with dcount: segments the table holds
 };
 
 // A chain segment as the kernel reads it, after the layer pointers: a
@@ -1814,9 +1832,9 @@ __device__ inline void seg_moves(const uint32_t (&slot)[kChainSeg + 1], const ui
 // nontemporal accesses, 5.2 with four or eight.)  The segment's header and
 // run are read once per workgroup into scalar registers.
 template <typename IdxT>
-__global__ __launch_bounds__(256) void move_chain_kernel(ChainParams p, ArgTables t) {
+__device__ inline void chain_segment(const ChainParams &p, const ArgTables &t, uint32_t seg) {
     constexpr uint32_t W = seg_record_words<IdxT>();
-    const uint32_t rec = 2u * p.L * static_cast<uint32_t>(sizeof(void *)) + blockIdx.y * W * 4u;
+    const uint32_t rec = 2u * p.L * static_cast<uint32_t>(sizeof(void *)) + seg * W * 4u;
     uint32_t w[W];
 #pragma unroll
     for (uint32_t i = 0; i < W; ++i) {
@@ -1877,6 +1895,18 @@ __global__ __launch_bounds__(256) void move_chain_kernel(ChainParams p, ArgTable
     }
 }
 
+template <typename IdxT>
+__global__ __launch_bounds__(256) void move_chain_kernel(ChainParams p, ArgTables t) {
+    if (p.dcount) {  // a device plan: the grid's rows take the segments in turn
+        const uint32_t n = min(*p.dcount, p.max_segs);
+        for (uint32_t seg = blockIdx.y; seg < n; seg += gridDim.y) {
+            chain_segment<IdxT>(p, t, seg);
+        }
+        return;
+    }
+    chain_segment<IdxT>(p, t, blockIdx.y);
+}
+
 // The kernel's table for `segs`: layer pointers, then one record per segment.
 template <typename IdxT>
 static void chain_table(const kvmem_hip_pool *pool, bool want_v, const std::vector<ChainSeg> &segs,
@@ -1899,6 +1929,287 @@ static void chain_table(const kvmem_hip_pool *pool, bool want_v, const std::vect
         }
         for (int j = 0; j < kChainSeg; ++j) {
             r[3 + kChainSeg + j] = static_cast<IdxT>(sg.nt[j]);
+        }
+    }
+}
+
+// ------------------------------------------------ device reselect plan
+//
+// apply_retrieval as one device pipeline: the top-k kernel leaves the
+// selection in device memory, and plan_kernel (one workgroup) diffs it
+// against the pool's resident blocks and writes the job tables of the
+// kernels queued behind it: the stage-in items, the chain segments of the
+// slot moves and the copies that save cut slots first.  Window slot i takes
+// the i-th selected block (canonical layout).  A selected block resident at
+// slot s moves s -> i when s != i, unless it is the grown partial tail,
+// which is staged again; a selected block not resident is staged into slot
+// i.  Moves then have distinct sources and distinct destinations.  With the
+// resident blocks at slots ascending with their ids (a canonical pool)
+// sources and destinations both ascend with the block id, so the moves
+// form chains and never a cycle.
+//
+// A chain starts at a move whose source no move writes; pred(m) is the move
+// that writes m's source, which m must read first (inside a segment the walk
+// reads every source before it writes; across segments the cut slot is
+// read from its saved copy).  Each move's rank along its chain comes from pointer jumping on pred
+// (11 rounds cover kPlanMaxSel moves).  Segments of kChainSeg moves start at
+// ranks 0, kChainSeg, ...; the first source of every segment but a chain's
+// first is saved to scratch beforehand, as build_chains (move_plan.cpp)
+// does on the host.
+constexpr uint32_t kPlanThreads = 1024;
+constexpr uint32_t kChainRows = 64;  // chain segments the device plan's walk runs side by side
+constexpr uint32_t kPlanMaxSel = KVMEM_PLAN_MAX_SEL;    // selected blocks per step (one per thread)
+constexpr uint32_t kPlanMaxSlots = KVMEM_PLAN_MAX_SLOTS;  // pool slots
+constexpr uint16_t kNoMove = 0xffffu;
+constexpr uint32_t kPlanJumpRounds = 11;  // 2^11 > kPlanMaxSel
+constexpr uint32_t kPlanSaveOpsPer(uint32_t L) { return 2u * L; }
+static_assert(kChainSeg == 8, "plan segments are the chain kernel's");
+
+// Counts at the start of the plan buffer (and in host-mapped memory).
+enum PlanCount : uint32_t {
+    kPlanStage = 0,   // blocks staged
+    kPlanMoves = 1,   // slot moves
+    kPlanSegs = 2,    // chain segments
+    kPlanSaves = 3,   // slots saved before the walk
+    kPlanSaveOps = 4, // their copies (K and V of every layer)
+    kPlanSel = 5,     // selected blocks
+    kPlanError = 6,   // nonzero: the plan was refused (nothing moves)
+    kPlanRows = 7,    // rows the moves carry (sum over moves of n_tokens)
+    kPlanCounts = 16
+};
+
+struct PlanParams {
+    const uint32_t *sel;     // [0] = selected count, then the ascending ids
+    uint8_t *plan;           // counts, stage table, chain table, save copies
+    uint32_t *counts_host;   // the counts again, host-mapped
+    const uint8_t *scratch;  // saved slot e at scratch + e * entry_bytes
+    const uint8_t *tables;   // uploaded pool/resident table, or null: in the ArgTables
+    uint64_t kspan, vspan;   // one slot of one layer
+    uint64_t entry_bytes;    // L * (kspan + vspan)
+    uint32_t off_stage, off_chain, off_saves;
+    uint32_t n_res, n_slots, n_blocks, T, last_T, dirty, L, max_sel, max_saves;
+    uint32_t first_T;        // tokens of block 0
+};
+
+// Exclusive prefix over the workgroup's threads of `v`; `total` gets the sum.
+__device__ inline uint32_t plan_scan(uint32_t v, uint32_t *wave_tot, uint32_t &total) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    constexpr uint32_t kWaves = kPlanThreads / 64u;
+    uint32_t x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off, 64);
+        if (lane >= static_cast<uint32_t>(off)) {
+            x += y;
+        }
+    }
+    if (lane == 63u) {
+        wave_tot[wave] = x;
+    }
+    __syncthreads();
+    uint32_t before = 0;
+    total = 0;
+    for (uint32_t w = 0; w < kWaves; ++w) {
+        const uint32_t tw = wave_tot[w];
+        before += w < wave ? tw : 0u;
+        total += tw;
+    }
+    __syncthreads();  // wave_tot is rewritten by the next scan
+    return before + x - v;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p, ArgTables t) {
+    __shared__ uint32_t res_block[kPlanMaxSlots];
+    __shared__ uint16_t res_slot[kPlanMaxSlots];
+    __shared__ uint16_t at_src[kPlanMaxSlots];  // move reading slot s
+    __shared__ uint16_t at_dst[kPlanMaxSlots];  // move writing slot s
+    __shared__ uint16_t msrc[kPlanMaxSel], mdst[kPlanMaxSel], mnt[kPlanMaxSel], mnext[kPlanMaxSel];
+    __shared__ uint16_t jump[kPlanMaxSel];
+    __shared__ uint32_t rank[kPlanMaxSel];
+    __shared__ uint32_t wave_tot[kPlanThreads / 64u];
+    __shared__ uint32_t s_bad;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t L = p.L;
+    // the pool's layer pointers head the stage and chain tables
+    for (uint32_t j = tid; j < 2u * L; j += kPlanThreads) {
+        const uint64_t v = tab_read<uint64_t>(p.tables, t, 8u * j);
+        *reinterpret_cast<uint64_t *>(p.plan + p.off_stage + 8u * j) = v;
+        *reinterpret_cast<uint64_t *>(p.plan + p.off_chain + 8u * j) = v;
+    }
+    const uint32_t rb_off = 16u * L;
+    const uint32_t rs_off = rb_off + 4u * p.n_res;
+    for (uint32_t r = tid; r < p.n_res; r += kPlanThreads) {
+        res_block[r] = tab_read<uint32_t>(p.tables, t, rb_off + 4u * r);
+        res_slot[r] = static_cast<uint16_t>(tab_read<uint32_t>(p.tables, t, rs_off + 4u * r));
+    }
+    for (uint32_t q = tid; q < p.n_slots; q += kPlanThreads) {
+        at_src[q] = kNoMove;
+        at_dst[q] = kNoMove;
+    }
+    if (tid == 0) {
+        s_bad = 0;
+    }
+    __syncthreads();
+
+    // ---- selected index i = tid: stays, moves or is staged
+    const uint32_t k = min(p.sel[0], p.max_sel);
+    const uint32_t i = tid;
+    uint32_t b = 0;
+    int32_t src = -1;
+    if (i < k) {
+        b = p.sel[1u + i];
+        uint32_t lo = 0, hi = p.n_res;  // first resident id >= b
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (res_block[mid] < b) {
+                lo = mid + 1u;
+            } else {
+                hi = mid;
+            }
+        }
+        if (lo < p.n_res && res_block[lo] == b && b != p.dirty) {
+            src = res_slot[lo];
+        }
+        if (b >= p.n_blocks) {
+            atomicOr(&s_bad, 1u);
+        }
+    }
+    const bool stage = i < k && src < 0;
+    const bool move = i < k && src >= 0 && static_cast<uint32_t>(src) != i;
+    const uint32_t nt = (b + 1u == p.n_blocks && p.last_T != 0u) ? p.last_T : p.T;
+    uint32_t n_stage, n_moves;
+    const uint32_t at_stage = plan_scan(stage ? 1u : 0u, wave_tot, n_stage);
+    const uint32_t m_own = plan_scan(move ? 1u : 0u, wave_tot, n_moves);
+    if (stage) {
+        uint32_t *item = reinterpret_cast<uint32_t *>(p.plan + p.off_stage + 16u * L + 16u * at_stage);
+        const bool ok = b < p.n_blocks;
+        item[0] = ok ? b : 0u;
+        item[1] = i;
+        item[2] = ok ? nt : p.first_T;
+        item[3] = ok ? b * p.T : 0u;
+    }
+    // the host launches the stage-in with its own count, at most max_sel:
+    // every entry up to there holds an in-bounds item (block 0 to slot 0),
+    // whatever the two plans make of the selection; a disagreement is
+    // caught afterwards and drops the window
+    if (tid >= n_stage && tid < p.max_sel) {
+        uint32_t *item = reinterpret_cast<uint32_t *>(p.plan + p.off_stage + 16u * L + 16u * tid);
+        item[0] = 0u;
+        item[1] = 0u;
+        item[2] = p.first_T;
+        item[3] = 0u;
+    }
+    if (move) {
+        msrc[m_own] = static_cast<uint16_t>(src);
+        mdst[m_own] = static_cast<uint16_t>(i);
+        mnt[m_own] = static_cast<uint16_t>(nt);
+        at_src[src] = static_cast<uint16_t>(m_own);
+        at_dst[i] = static_cast<uint16_t>(m_own);
+    }
+    __syncthreads();
+
+    // ---- chains: rank of move m = tid along its chain
+    const uint32_t m = tid;
+    uint16_t jm = kNoMove;
+    uint32_t rm = 0;
+    if (m < n_moves) {
+        jm = at_dst[msrc[m]];             // pred: the move writing m's source
+        mnext[m] = at_src[mdst[m]];       // next: the move reading m's destination
+        rm = jm != kNoMove ? 1u : 0u;
+        jump[m] = jm;
+        rank[m] = rm;
+    }
+    __syncthreads();
+    for (uint32_t round = 0; round < kPlanJumpRounds; ++round) {
+        uint16_t j2 = kNoMove;
+        uint32_t r2 = 0;
+        if (m < n_moves && jm != kNoMove) {
+            j2 = jump[jm];
+            r2 = rank[jm];
+        }
+        __syncthreads();
+        if (m < n_moves && jm != kNoMove) {
+            rm += r2;
+            jm = j2;
+            jump[m] = jm;
+            rank[m] = rm;
+        }
+        __syncthreads();
+    }
+    if (m < n_moves && jm != kNoMove) {
+        atomicOr(&s_bad, 2u);  // a cycle: this plan is refused
+    }
+
+    // ---- segments from ranks 0, kChainSeg, ...; the non-first ones save
+    const bool seg_start = m < n_moves && (rm % kChainSeg) == 0u;
+    const bool saves = seg_start && rm > 0u;
+    uint32_t n_segs, n_saves;
+    const uint32_t g = plan_scan(seg_start ? 1u : 0u, wave_tot, n_segs);
+    const uint32_t e = plan_scan(saves ? 1u : 0u, wave_tot, n_saves);
+    uint32_t rows = 0, n_rows = 0;
+    if (m < n_moves) {
+        rows = mnt[m];
+    }
+    (void) plan_scan(rows, wave_tot, n_rows);
+    if (seg_start) {
+        // the record [len, saved + 1, slot[0 .. 8], nt[0 .. 7]] of 16-bit
+        // entries, padded to whole words; every index is a constant after
+        // unrolling, so the entries stay in registers
+        uint32_t rec[2 * kChainSeg + 4];
+#pragma unroll
+        for (uint32_t q = 0; q < 2 * kChainSeg + 4; ++q) {
+            rec[q] = 0u;
+        }
+        uint32_t len = 0;
+        uint32_t j = m;
+        rec[2] = msrc[m];
+#pragma unroll
+        for (uint32_t q = 0; q < kChainSeg; ++q) {
+            if (j != kNoMove) {
+                rec[3 + q] = mdst[j];
+                rec[3 + kChainSeg + q] = mnt[j];
+                len = q + 1u;
+                j = mnext[j];
+            }
+        }
+        rec[0] = len;
+        rec[1] = saves ? e + 1u : 0u;
+        constexpr uint32_t W = seg_record_words<uint16_t>();
+        static_assert(2 * W <= 2 * kChainSeg + 4, "record entries");
+        uint32_t *dst = reinterpret_cast<uint32_t *>(p.plan + p.off_chain + 16u * L + 4u * W * g);
+#pragma unroll
+        for (uint32_t w = 0; w < W; ++w) {
+            dst[w] = (rec[2 * w] & 0xffffu) | (rec[2 * w + 1] << 16);
+        }
+        if (saves && e < p.max_saves) {
+            CopyOpDev *ops = reinterpret_cast<CopyOpDev *>(p.plan + p.off_saves) + kPlanSaveOpsPer(L) * e;
+            const uint8_t *entry = p.scratch + e * p.entry_bytes;
+            for (uint32_t l = 0; l < L; ++l) {
+                const uint8_t *kl = reinterpret_cast<const uint8_t *>(tab_read<uint64_t>(p.tables, t, 8u * l));
+                const uint8_t *vl = reinterpret_cast<const uint8_t *>(tab_read<uint64_t>(p.tables, t, 8u * (L + l)));
+                uint8_t *at = const_cast<uint8_t *>(entry) + l * (p.kspan + p.vspan);
+                ops[2 * l] = CopyOpDev{kl + msrc[m] * p.kspan, at, p.kspan};
+                ops[2 * l + 1] = CopyOpDev{vl + msrc[m] * p.vspan, at + p.kspan, p.vspan};
+            }
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t bad = s_bad | (n_saves > p.max_saves ? 4u : 0u);
+        uint32_t c[kPlanCounts] = {};
+        c[kPlanStage] = bad ? 0u : n_stage;
+        c[kPlanMoves] = n_moves;
+        c[kPlanSegs] = bad ? 0u : n_segs;
+        c[kPlanSaves] = n_saves;
+        c[kPlanSaveOps] = bad ? 0u : n_saves * kPlanSaveOpsPer(L);
+        c[kPlanSel] = k;
+        c[kPlanError] = bad;
+        c[kPlanRows] = n_rows;
+        uint32_t *dc = reinterpret_cast<uint32_t *>(p.plan);
+        for (uint32_t q = 0; q < kPlanCounts; ++q) {
+            dc[q] = c[q];
+            p.counts_host[q] = c[q];
         }
     }
 }
@@ -2350,6 +2661,213 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
         st = kvmem_hip_d2d_batched(ctx, ss.data(), sd.data(), nb.data(), nops);
     }
     return st;
+}
+
+
+// Internal to the library (the reselect engine's device pipeline): the plan
+// kernel over the selection the last topk_launch(to_device) leaves in
+// ctx->topk_dev, then the slot saves, the chain walk and the stage-in, all
+// sized on the device.  res_block / res_slot: the blocks whose pool rows are
+// valid, ascending in id and in slot; dirty: a resident block to stage again
+// (UINT32_MAX: none); max_sel: the largest selection the top-k can return.
+int kvmem_hip_reselect_device(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist, const kvmem_hip_pool *pool,
+                              const uint32_t *res_block, const uint32_t *res_slot, uint32_t n_res,
+                              uint32_t dirty, uint32_t max_sel) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!hist || !hist->k || !hist->v || !pool || !pool->v_layers || (n_res && (!res_block || !res_slot))) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "reselect_device: null argument");
+    }
+    if (!ctx->topk_pending || !ctx->topk_dev.ptr) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "reselect_device: no top-k launched to device memory");
+    }
+    const uint32_t T = hist->block_tokens;
+    const uint32_t L = hist->n_layers;
+    int st = check_pool(ctx, pool, L, T, hist->n_embd_k, hist->n_embd_v, true);
+    if (st != KVMEM_HIP_OK) {
+        return st;
+    }
+    const uint64_t krow = kvmem_hip_row_size(pool->type_k, pool->n_embd_k);
+    const uint64_t vrow = kvmem_hip_row_size(pool->type_v, pool->n_embd_v);
+    const uint32_t cap = hist->capacity_blocks ? hist->capacity_blocks : hist->n_blocks;
+    if (pool->xf || pool->n_slots > kPlanMaxSlots || max_sel == 0 || max_sel > kPlanMaxSel ||
+        max_sel > pool->n_slots || n_res > pool->n_slots || T == 0 || T > 65535u || krow % 16 || vrow % 16 ||
+        hist->n_embd_k % 32 || hist->n_embd_v % 32 || !aligned16(hist->k) || !aligned16(hist->v) ||
+        cap < hist->n_blocks) {
+        return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "reselect_device: pool or history outside the device plan");
+    }
+    for (uint32_t r = 0; r < n_res; ++r) {
+        if (res_slot[r] >= pool->n_slots || res_block[r] >= hist->n_blocks ||
+            (r > 0 && (res_block[r] <= res_block[r - 1] || res_slot[r] <= res_slot[r - 1]))) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "reselect_device: resident blocks must ascend in id and slot");
+        }
+    }
+    const uint32_t max_segs = max_sel;  // a move per segment at most
+    const uint32_t max_saves = max_sel / kChainSeg + 1;
+    const uint32_t ops_per = kPlanSaveOpsPer(L);
+    auto up256 = [](size_t x) { return (x + 255) & ~size_t{255}; };
+    const size_t off_stage = 256;
+    const size_t off_chain = up256(off_stage + 16 * size_t{L} + 16 * size_t{max_sel});
+    const size_t off_saves = up256(off_chain + 16 * size_t{L} + 4 * size_t{seg_record_words<uint16_t>()} * max_segs);
+    const size_t plan_bytes = off_saves + sizeof(CopyOpDev) * size_t{ops_per} * max_saves;
+    const uint64_t kspan = krow * T;
+    const uint64_t vspan = vrow * T;
+    const uint64_t per_move = (kspan + vspan) * L;
+    (void) hipSetDevice(ctx->device);
+    if (!ensure_dev(ctx, ctx->plan, plan_bytes, "reselect_device plan") ||
+        !ensure_pin(ctx, ctx->plan_counts, sizeof(uint32_t) * kPlanCounts, "reselect_device counts",
+                    hipHostMallocCoherent | hipHostMallocMapped) ||
+        !ensure_dev(ctx, ctx->move_scratch, per_move * max_saves, "reselect_device scratch")) {
+        return KVMEM_HIP_ERR_NOMEM;
+    }
+    void *counts_dev = nullptr;
+    if (!hip_ok(ctx, hipHostGetDevicePointer(&counts_dev, ctx->plan_counts.ptr, 0), "reselect_device counts mapping")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    std::memset(ctx->plan_counts.ptr, 0, sizeof(uint32_t) * kPlanCounts);
+    // the pool's layer pointers (K, then V), then the resident table
+    std::vector<uint8_t> tab(16 * size_t{L} + 8 * size_t{n_res});
+    std::memcpy(tab.data(), pool->k_layers, 8 * size_t{L});
+    std::memcpy(tab.data() + 8 * size_t{L}, pool->v_layers, 8 * size_t{L});
+    if (n_res) {
+        std::memcpy(tab.data() + 16 * size_t{L}, res_block, 4 * size_t{n_res});
+        std::memcpy(tab.data() + 16 * size_t{L} + 4 * size_t{n_res}, res_slot, 4 * size_t{n_res});
+    }
+    LaunchTables lt;
+    if (!stage_tables(ctx, tab.data(), tab.size(), lt, "reselect_device resident table")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    uint8_t *plan = static_cast<uint8_t *>(ctx->plan.ptr);
+    uint8_t *scratch = static_cast<uint8_t *>(ctx->move_scratch.ptr);
+    PlanParams pp{};
+    pp.sel = static_cast<const uint32_t *>(ctx->topk_dev.ptr);
+    pp.plan = plan;
+    pp.counts_host = static_cast<uint32_t *>(counts_dev);
+    pp.scratch = scratch;
+    pp.tables = lt.dev;
+    pp.kspan = kspan;
+    pp.vspan = vspan;
+    pp.entry_bytes = per_move;
+    pp.off_stage = static_cast<uint32_t>(off_stage);
+    pp.off_chain = static_cast<uint32_t>(off_chain);
+    pp.off_saves = static_cast<uint32_t>(off_saves);
+    pp.n_res = n_res;
+    pp.n_slots = pool->n_slots;
+    pp.n_blocks = hist->n_blocks;
+    pp.T = T;
+    pp.last_T = hist->last_block_tokens;
+    pp.first_T = (hist->n_blocks == 1 && hist->last_block_tokens) ? hist->last_block_tokens : T;
+    pp.dirty = dirty;
+    pp.L = L;
+    pp.max_sel = max_sel;
+    pp.max_saves = max_saves;
+    ctx->plan_row_bytes = (krow + vrow) * L;
+    ctx->plan_save_bytes = per_move;
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "reselect_device plan launch")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    plan_kernel<<<1, kPlanThreads, 0, ctx->stream>>>(pp, lt.args);
+    if (!hip_ok(ctx, hipGetLastError(), "reselect_device plan launch")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    const uint32_t *counts = reinterpret_cast<const uint32_t *>(plan);
+    // slot saves, then the chain walk
+    perf_begin(ctx, kPerfLayout);
+    if (!launch_dev_copies(ctx, reinterpret_cast<const CopyOpDev *>(plan + off_saves), counts + kPlanSaveOps,
+                           ops_per * max_saves, "reselect_device saves")) {
+        perf_end(ctx, kPerfLayout);
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    ChainParams cp{};
+    cp.tables = plan + off_chain;
+    cp.scratch = scratch;
+    cp.dcount = counts + kPlanSegs;
+    cp.kspan = kspan;
+    cp.vspan = vspan;
+    cp.entry_bytes = per_move;
+    cp.krow16 = static_cast<uint32_t>(krow / 16);
+    cp.vrow16 = static_cast<uint32_t>(vrow / 16);
+    cp.L = L;
+    cp.T = T;
+    cp.vec_per_layer = T * (cp.krow16 + cp.vrow16);
+    cp.max_segs = max_segs;
+    const uint64_t nvec = static_cast<uint64_t>(L) * cp.vec_per_layer;
+    if (nvec > 0x7fffffffu) {
+        perf_end(ctx, kPerfLayout);
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "reselect_device: slot too large");
+    }
+    if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "reselect_device chain launch")) {
+        perf_end(ctx, kPerfLayout);
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    // up to kChainRows segments run side by side, one per grid row; more
+    // take turns (a row's next segment waits for its stores)
+    const dim3 cgrid(static_cast<uint32_t>((nvec + 255) / 256), std::min<uint32_t>(kChainRows, max_segs));
+    move_chain_kernel<uint16_t><<<cgrid, 256, 0, ctx->stream>>>(cp, kNoArgTables);
+    perf_end(ctx, kPerfLayout);
+    if (!hip_ok(ctx, hipGetLastError(), "reselect_device chain launch")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    ctx->plan_stage_off = off_stage;
+    ctx->plan_max_sel = max_sel;
+    return KVMEM_HIP_OK;
+}
+
+// The stage-in of the last device plan's n_staged blocks, launched by the
+// host once it knows the count (the plan kernel wrote their items to the
+// plan's stage table on the device): one workgroup per chunk, as the other
+// stage-ins.
+int kvmem_hip_reselect_device_stagein(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
+                                      const kvmem_hip_pool *pool, uint32_t n_staged) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!hist || !hist->k || !hist->v || !pool || !pool->v_layers || pool->xf || !ctx->plan.ptr ||
+        !ctx->plan_stage_off) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "reselect_device_stagein: no device plan");
+    }
+    if (n_staged > ctx->plan_max_sel || ctx->plan_max_sel > pool->n_slots) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "reselect_device_stagein: more blocks than the plan holds");
+    }
+    if (n_staged == 0) {
+        return KVMEM_HIP_OK;
+    }
+    const uint32_t T = hist->block_tokens;
+    const uint32_t L = hist->n_layers;
+    const uint32_t cap = hist->capacity_blocks ? hist->capacity_blocks : hist->n_blocks;
+    JobTables jt;
+    jt.tables.dev = static_cast<const uint8_t *>(ctx->plan.ptr) + ctx->plan_stage_off;
+    jt.items_off = 16u * L;
+    jt.theta_off = 16u * L;
+    const XfParams xp{};
+    const uint64_t bk = static_cast<uint64_t>(T) * hist->n_embd_k * 2u;
+    const uint64_t bv = static_cast<uint64_t>(T) * hist->n_embd_v * 2u;
+    const BlockSource sk = make_block_source(pool->type_k, static_cast<const uint8_t *>(hist->k), bk, bk * cap, jt,
+                                             L, T, hist->n_embd_k, 0, xp, true);
+    const BlockSource sv = make_block_source(pool->type_v, static_cast<const uint8_t *>(hist->v), bv, bv * cap, jt,
+                                             L, T, hist->n_embd_v, 0, xp, false);
+    (void) hipSetDevice(ctx->device);
+    perf_begin(ctx, kPerfSet);
+    const int st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, &sv, n_staged, xp, kNoArgTables);
+    perf_end(ctx, kPerfSet);
+    return st;
+}
+
+// The last device plan's counts (kPlanCounts words: staged, moves,
+// segments, saves, save copies, selected, error, moved rows), once the
+// stream has drained; its moved and saved bytes join the copy counter.
+int kvmem_hip_reselect_device_counts(kvmem_hip_ctx *ctx, uint32_t *out, uint32_t n) {
+    if (!ctx || !out || !ctx->plan_counts.ptr) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    const uint32_t *c = static_cast<const uint32_t *>(ctx->plan_counts.ptr);
+    for (uint32_t i = 0; i < n && i < kPlanCounts; ++i) {
+        out[i] = __atomic_load_n(c + i, __ATOMIC_ACQUIRE);
+    }
+    ctx->d2d_bytes += static_cast<uint64_t>(c[kPlanRows]) * ctx->plan_row_bytes +
+                      static_cast<uint64_t>(c[kPlanSaves]) * ctx->plan_save_bytes;
+    return KVMEM_HIP_OK;
 }
 
 }  // extern "C"

@@ -26,6 +26,7 @@
 // ids (the sink) travel in the kernel arguments, so no upload precedes the
 // launch.
 #include "kvmem_internal.hpp"
+#include "device_reselect.h"
 
 #include <algorithm>
 #include <vector>
@@ -85,13 +86,16 @@ __device__ inline uint32_t block_inclusive_scan(uint32_t v, uint32_t *wave_tot) 
 
 // `forced` is a device list, or null with the ids in `forced_inline`.
 // `out` (host-mapped) receives the ids at [0, count) and the count at [n];
-// `done` is set to `epoch` once both are visible to the host.
+// `done` is set to `epoch` once both are visible to the host.  `dev_out`,
+// when set, receives the count at [0] and the ids at [1, 1 + count) in
+// device memory, for kernels that follow on the stream.
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores, uint32_t n,
                                                             const uint32_t *forced,
                                                             TopkForced forced_inline,
                                                             uint32_t n_forced, uint32_t need,
                                                             int tie_lower, uint32_t *out,
-                                                            uint32_t *done, uint32_t epoch) {
+                                                            uint32_t *done, uint32_t epoch,
+                                                            uint32_t *dev_out) {
     __shared__ uint64_t keys[kTopkMaxN];
     __shared__ uint32_t forced_bits[kTopkMaxN / 32];
     __shared__ uint32_t hist[256];
@@ -206,9 +210,15 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores,
     }
     for (uint32_t i = tid; i < total; i += 64u) {
         out[i] = ids[i];
+        if (dev_out) {
+            dev_out[1u + i] = ids[i];
+        }
     }
     if (tid == 0) {
         out[n] = total;
+        if (dev_out) {
+            dev_out[0] = total;
+        }
     }
     __threadfence_system();
     if (tid == 0) {
@@ -225,7 +235,8 @@ constexpr uint32_t kTopkStreamMaxN = 1u << 20;
 
 __global__ __launch_bounds__(kTopkThreads) void topk_stream_kernel(
     const float *scores, uint32_t n, const uint32_t *forced, TopkForced forced_inline,
-    uint32_t n_forced, uint32_t need, int tie_lower, uint32_t *out, uint32_t *done, uint32_t epoch) {
+    uint32_t n_forced, uint32_t need, int tie_lower, uint32_t *out, uint32_t *done, uint32_t epoch,
+    uint32_t *dev_out) {
     __shared__ uint32_t forced_bits[kTopkStreamMaxN / 32];
     __shared__ uint32_t hist[256];
     __shared__ uint32_t wave_tot[kTopkWaves];
@@ -314,11 +325,17 @@ __global__ __launch_bounds__(kTopkThreads) void topk_stream_kernel(
     uint32_t pos = incl - cnt;
     for (uint32_t i = lo; i < hi; ++i) {
         if (chosen(i)) {
+            if (dev_out) {
+                dev_out[1u + pos] = i;
+            }
             out[pos++] = i;
         }
     }
     if (tid == 0) {
         out[n] = total;
+        if (dev_out) {
+            dev_out[0] = total;
+        }
     }
     __threadfence_system();  // every thread's ids are visible to the host ...
     __syncthreads();
@@ -345,18 +362,17 @@ inline void cpu_relax() {
 
 }  // namespace
 
-extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t n,
-                              const uint32_t *forced, uint32_t n_forced, uint32_t need,
-                              int tie_lower_index, uint32_t *sel_out, uint32_t *n_sel) {
-    if (!ctx) {
-        return KVMEM_HIP_ERR_INVALID;
-    }
-    if (!sel_out || !n_sel || (n > 0 && !scores) || (n_forced > 0 && !forced)) {
+namespace kvmem_hip {
+
+// Launch half of kvmem_hip_topk: validates, uploads nothing but an overlong
+// forced list, and enqueues the kernel.  With `to_device` the selection is
+// also written to ctx->topk_dev ([0] = count, then the ids) for kernels
+// that follow on the stream.  topk_wait() collects the selection.
+int topk_launch(kvmem_hip_ctx *ctx, const float *scores, uint32_t n, const uint32_t *forced,
+                uint32_t n_forced, uint32_t need, int tie_lower_index, bool to_device) {
+    ctx->topk_pending = false;
+    if (!scores || (n_forced > 0 && !forced)) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "topk: null argument");
-    }
-    *n_sel = 0;
-    if (n == 0) {
-        return KVMEM_HIP_OK;
     }
     if (n > kTopkStreamMaxN) {
         return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "topk: more than 1048576 blocks");
@@ -380,6 +396,10 @@ extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t 
                     hipHostMallocCoherent | hipHostMallocMapped)) {
         return KVMEM_HIP_ERR_NOMEM;
     }
+    if (to_device && !ensure_dev(ctx, ctx->topk_dev, sizeof(uint32_t) * (static_cast<size_t>(n) + 1),
+                                 "topk device output")) {
+        return KVMEM_HIP_ERR_NOMEM;
+    }
     uint32_t *h = static_cast<uint32_t *>(ctx->topk_sel_host.ptr);
     void *out_dev = nullptr;
     if (!hip_ok(ctx, hipHostGetDevicePointer(&out_dev, h, 0), "topk host output mapping")) {
@@ -400,6 +420,7 @@ extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t 
     ctx->topk_epoch = ctx->topk_epoch + 1 == 0 ? 1 : ctx->topk_epoch + 1;
     const uint32_t epoch = ctx->topk_epoch;
     uint32_t *out = static_cast<uint32_t *>(out_dev);
+    uint32_t *dev_out = to_device ? static_cast<uint32_t *>(ctx->topk_dev.ptr) : nullptr;
     // pinned memory comes uninitialised: clear the word before the kernel
     // can set it (the previous call's write has landed; it was waited for)
     __atomic_store_n(h + flag, 0u, __ATOMIC_RELEASE);
@@ -410,19 +431,34 @@ extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t 
     if (n <= static_cast<uint32_t>(kTopkMaxN)) {
         topk_kernel<<<1, kTopkThreads, 0, ctx->stream>>>(scores, n, forced_dev, inl,
                                                          static_cast<uint32_t>(uniq.size()), need,
-                                                         tie_lower_index, out, out + flag, epoch);
+                                                         tie_lower_index, out, out + flag, epoch, dev_out);
     } else {
         topk_stream_kernel<<<1, kTopkThreads, 0, ctx->stream>>>(
             scores, n, forced_dev, inl, static_cast<uint32_t>(uniq.size()), need, tie_lower_index, out,
-            out + flag, epoch);
+            out + flag, epoch, dev_out);
     }
     perf_end(ctx, kPerfTopk);
     if (!hip_ok(ctx, hipGetLastError(), "topk launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
-    // Spin on the completion word; every few thousand rounds ask the stream
-    // whether it has drained (then the word must be set) or failed.
-    const uint32_t *done = h + flag;
+    ctx->topk_pending = true;
+    ctx->topk_n = n;
+    ctx->topk_limit = static_cast<uint32_t>(uniq.size()) + need;
+    return KVMEM_HIP_OK;
+}
+
+// Wait half: spin on the completion word of the last topk_launch; every few
+// thousand rounds ask the stream whether it has drained (then the word must
+// be set) or failed.
+int topk_wait(kvmem_hip_ctx *ctx, uint32_t *sel_out, uint32_t *n_sel) {
+    if (!ctx->topk_pending) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "topk: no launch to wait for");
+    }
+    ctx->topk_pending = false;
+    const uint32_t n = ctx->topk_n;
+    const uint32_t epoch = ctx->topk_epoch;
+    const uint32_t *h = static_cast<const uint32_t *>(ctx->topk_sel_host.ptr);
+    const uint32_t *done = h + topk_flag_index(n);
     for (uint32_t spin = 1; __atomic_load_n(done, __ATOMIC_ACQUIRE) != epoch; ++spin) {
         cpu_relax();
         if ((spin & 4095u) == 0) {
@@ -439,10 +475,52 @@ extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t 
         }
     }
     const uint32_t cnt = h[n];
-    if (cnt > static_cast<uint32_t>(uniq.size()) + need) {
+    if (cnt > ctx->topk_limit) {
         return fail(ctx, KVMEM_HIP_ERR_RUNTIME, "topk: selection larger than requested");
     }
     std::copy(h, h + cnt, sel_out);
     *n_sel = cnt;
     return KVMEM_HIP_OK;
+}
+
+}  // namespace kvmem_hip
+
+extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t n,
+                              const uint32_t *forced, uint32_t n_forced, uint32_t need,
+                              int tie_lower_index, uint32_t *sel_out, uint32_t *n_sel) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!sel_out || !n_sel || (n > 0 && !scores) || (n_forced > 0 && !forced)) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "topk: null argument");
+    }
+    *n_sel = 0;
+    if (n == 0) {
+        return KVMEM_HIP_OK;
+    }
+    const int rc = topk_launch(ctx, scores, n, forced, n_forced, need, tie_lower_index, false);
+    if (rc != KVMEM_HIP_OK) {
+        return rc;
+    }
+    return topk_wait(ctx, sel_out, n_sel);
+}
+
+extern "C" int kvmem_hip_topk_launch_dev(kvmem_hip_ctx *ctx, const float *scores, uint32_t n,
+                                         const uint32_t *forced, uint32_t n_forced, uint32_t need,
+                                         int tie_lower_index) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (n == 0) {
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "topk: no blocks");
+    }
+    return topk_launch(ctx, scores, n, forced, n_forced, need, tie_lower_index, true);
+}
+
+extern "C" int kvmem_hip_topk_wait(kvmem_hip_ctx *ctx, uint32_t *sel_out, uint32_t *n_sel) {
+    if (!ctx || !sel_out || !n_sel) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    *n_sel = 0;
+    return topk_wait(ctx, sel_out, n_sel);
 }

@@ -24,7 +24,7 @@ class PlanStats(C.Structure):
                 ("n_moved", C.c_uint32), ("selection_overlap_blocks", C.c_uint32),
                 ("gpu_reused_blocks", C.c_uint32), ("retained_position_stable", C.c_uint32),
                 ("retained_position_moved", C.c_uint32), ("total_window_tokens", C.c_uint32),
-                ("n_saved", C.c_uint32), ("n_restored", C.c_uint32)]
+                ("n_saved", C.c_uint32), ("n_restored", C.c_uint32), ("device_planned", C.c_uint32)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -49,7 +49,7 @@ class EngineParams(C.Structure):
                 ("tie_lower_index", C.c_int32), ("layer_reduce", C.c_int32),
                 ("canonical_layout", C.c_int32), ("scorer", C.c_int32), ("n_rot", C.c_uint32),
                 ("rope_freq_base", C.c_float), ("rope_freq_scale", C.c_float), ("attn_rot", C.c_int32),
-                ("query_max_tokens", C.c_uint32), ("query_last", C.c_uint32)]
+                ("query_max_tokens", C.c_uint32), ("query_last", C.c_uint32), ("device_plan", C.c_int32)]
 
 
 _bound = set()

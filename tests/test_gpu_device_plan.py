@@ -1,0 +1,189 @@
+"""apply_retrieval's device plan: the selection diff and the slot moves
+sized on the device behind the top-k, and the stage-in of the items the
+plan kernel wrote (kvmem_engine_params.device_plan).  Two engines over the
+same history, one planning on the device and one on the host, must leave
+the same pool bytes, the same slots and the same plan counts after every
+step, and both must equal the oracle's quantization of every selected
+block; a failure anywhere in the device pipeline leaves no block called
+resident with wrong bytes."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+from engine_helpers import E, HQ, L, T, check_pool, history, kv, make_engine  # noqa: E402
+
+
+def announce(msg: str) -> None:
+    print(f"[test_gpu_device_plan] {msg}", flush=True)
+
+ALL_KINDS = kv.FAIL_ALLOC | kv.FAIL_COPY | kv.FAIL_LAUNCH
+
+
+def queries(seed: int, n: int, tq: int = 8):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return [torch.randn((L, tq, HQ, 256), generator=g, device="cuda").to(torch.bfloat16) for _ in range(n)]
+
+
+def window(eng, type_k, type_v, ntok_of):
+    """Bytes of every selected block's rows, slot by slot, both tensors."""
+    out = {}
+    slots = eng.block_slots()
+    c = kv.Context(0)
+    for layer in range(L):
+        for which, ty in ((0, type_k), (1, type_v)):
+            rb = kv.row_size(ty, E)
+            n = eng.n_slots() * T * rb
+            buf = torch.empty(n, dtype=torch.uint8, device="cuda")
+            c.d2d_batched([eng.pool_layer(layer)[which]], [buf.data_ptr()], [n])
+            c.sync()
+            pool = buf.cpu().numpy().reshape(eng.n_slots() * T, rb)
+            for b, s in enumerate(slots):
+                if s >= 0:
+                    out[(layer, which, b)] = pool[s * T: s * T + ntok_of(b)].copy()
+    c.close()
+    return out
+
+
+def same_step(dev, ref, q, mandatory, types, ntok_of, oracle, k, v):
+    sd = dev.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=mandatory)
+    sr = ref.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=mandatory)
+    assert sd["device_planned"] == 1 and sr["device_planned"] == 0
+    sd.pop("device_planned")
+    sr.pop("device_planned")
+    assert sd == sr
+    slots = dev.block_slots()
+    assert slots == ref.block_slots()
+    sel = [b for b, s in enumerate(slots) if s >= 0]
+    assert sorted(slots[b] for b in sel) == list(range(len(sel)))  # canonical: slot i = i-th block
+    wd, wr = window(dev, *types, ntok_of), window(ref, *types, ntok_of)
+    assert wd.keys() == wr.keys()
+    for key in wd:
+        assert np.array_equal(wd[key], wr[key]), key
+    check_pool(dev, oracle, k, v, sel, *types, ntok_of=ntok_of)
+    return sd
+
+
+TYPES = [(kv.TYPE_Q8_0, kv.TYPE_Q8_0), (kv.TYPE_Q8_0, kv.TYPE_Q4_0), (kv.TYPE_Q5_0, kv.TYPE_Q5_0),
+         (kv.TYPE_F16, kv.TYPE_Q8_0)]
+
+
+@pytest.mark.parametrize("types", TYPES, ids=["q8q8", "q8q4", "q5q5", "f16q8"])
+def test_device_plan_equals_host_plan(oracle, types):
+    announce(f"device plan vs host plan: 6 steps, 48-block history with a growing partial tail, types {types}")
+    cap = 48
+    k, v, _ = history(cap, seed=61)
+    tail = {"n": 77}
+    n_tok = 47 * T + tail["n"]
+    ntok_of = lambda b: tail["n"] if b == 47 else T  # noqa: E731
+    with make_engine(24, 8, *types, recent_blocks=1) as dev, \
+            make_engine(24, 8, *types, recent_blocks=1, device_plan=0) as ref:
+        for eng in (dev, ref):
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, n_tok)
+        moved = 0
+        for step, q in enumerate(queries(62, 6)):
+            if step == 3:  # the resident tail grows: it is staged again
+                for eng in (dev, ref):
+                    eng.append_tokens(30)
+                tail["n"] = 107
+            st = same_step(dev, ref, q, (), types, ntok_of, oracle, k, v)
+            moved += st["n_moved"]
+        assert moved > 0
+
+
+@pytest.mark.parametrize("types", [(kv.TYPE_Q8_0, kv.TYPE_Q4_0), (kv.TYPE_Q5_0, kv.TYPE_F16)],
+                         ids=["q8q4", "q5f16"])
+def test_device_plan_many_staged_blocks(oracle, types):
+    """64 blocks staged at once, K and V in different formats: the stage-in
+    reads the plan kernel's items, as many as the store stages."""
+    announce(f"device plan: 64 staged blocks, several chunks per workgroup, types {types}")
+    cap = 160
+    k, v, _ = history(cap, seed=69)
+    with make_engine(64, 16, *types) as dev, make_engine(64, 16, *types, device_plan=0) as ref:
+        for eng in (dev, ref):
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, cap * T)
+        staged = 0
+        for q in queries(70, 3):
+            st = same_step(dev, ref, q, (), types, lambda b: T, oracle, k, v)
+            staged = max(staged, st["n_staged"])
+        assert staged == 64
+
+
+def test_device_plan_long_chains_and_saves(oracle):
+    announce("device plan: forced selections whose slot moves form chains longer than a segment")
+    cap = 64
+    k, v, q = history(cap, seed=63)
+    types = (kv.TYPE_Q8_0, kv.TYPE_Q4_0)
+    steps = [
+        [0] + list(range(10, 33)),                             # 24 blocks
+        [0, 1, 2] + list(range(10, 31)),                       # 10..30 shift right by 2: chains of 10
+        [0] + list(range(3, 12)) + list(range(20, 34)),        # shifts both ways
+        [0] + list(range(40, 63)),                             # everything new
+        [0] + list(range(39, 62)),                             # every block one slot right
+        [0] + list(range(41, 64)),                             # and two slots left
+    ]
+    with make_engine(24, 8, *types) as dev, make_engine(24, 8, *types, device_plan=0) as ref:
+        for eng in (dev, ref):
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, cap * T)
+        longest = 0
+        for sel in steps:
+            st = same_step(dev, ref, q, sel, types, lambda b: T, oracle, k, v)
+            assert sorted(b for b, s in enumerate(dev.block_slots()) if s >= 0) == sel
+            longest = max(longest, st["n_moved"])
+        assert longest >= 20
+
+
+def test_device_plan_budget_edges(oracle):
+    announce("device plan: every block fits (host path), then a selection of one block past the sink")
+    cap = 20
+    k, v, q = history(cap, seed=65)
+    types = (kv.TYPE_Q8_0, kv.TYPE_Q8_0)
+    with make_engine(24, 4, *types) as dev:
+        dev.set_device_history(k.data_ptr(), v.data_ptr(), cap, 12 * T)
+        st = dev.apply_retrieval(q.data_ptr(), q.shape[1])  # 12 blocks <= budget 24
+        assert st["device_planned"] == 0 and st["n_staged"] == 12
+        check_pool(dev, oracle, k, v, list(range(12)), *types)
+    with make_engine(2, 2, *types) as dev, make_engine(2, 2, *types, device_plan=0) as ref:
+        for eng in (dev, ref):
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, cap * T)
+        for q2 in queries(66, 3):
+            same_step(dev, ref, q2, (), types, lambda b: T, oracle, k, v)
+
+
+def test_device_plan_failure_leaves_exact_pool(oracle):
+    announce("device plan: every allocation / copy / launch of an apply_retrieval failed in turn")
+    cap = 40
+    k, v, q = history(cap, seed=67)
+    types = (kv.TYPE_Q8_0, kv.TYPE_Q4_0)
+    first = [0] + list(range(5, 28))
+    second = [0, 1] + list(range(8, 30))
+    n_failed = 0
+    for nth in range(1, 64):
+        with make_engine(24, 8, *types) as eng:
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, cap * T)
+            eng.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=first)
+            ctx = kv.Context.borrow(eng.ctx_handle())
+            ctx.debug_fail_after(ALL_KINDS, nth)
+            try:
+                st = eng.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=second)
+            except kv.KvMemError:
+                n_failed += 1
+                ctx.debug_fail_after(0, 0)
+                slots = eng.block_slots()
+                resident = [b for b, s in enumerate(slots) if s >= 0]
+                check_pool(eng, oracle, k, v, resident, *types)
+                st = eng.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=second)
+                assert st["device_planned"] == 1
+                check_pool(eng, oracle, k, v, second, *types)
+                continue
+            ctx.debug_fail_after(0, 0)
+            assert st["device_planned"] == 1
+            check_pool(eng, oracle, k, v, second, *types)
+            break
+    else:
+        raise AssertionError("apply_retrieval never ran to completion")
+    assert n_failed >= 4, n_failed  # scorer, top-k, plan, saves, chain walk, stage-in
