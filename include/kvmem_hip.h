@@ -564,7 +564,10 @@ KVMEM_HIP_API uint64_t kvmem_hip_debug_fail_left(const kvmem_hip_ctx *ctx);
  * analogue of the KVMEM_RETR_SUM buckets (llama-memory-kvmem.cpp:2918-2936):
  * score = scoring kernels, topk = selection kernel, set = stage-in kernels,
  * copy = H2D of host blocks, layout = slot moves.  Milliseconds summed over
- * calls since the last reset; counts are numbers of timed calls. */
+ * calls since the last reset; counts are numbers of timed calls.
+ * after_score_ms: from the end of a call's scoring to the end of the last
+ * stage-in before the next scoring (top-k, the slot plan, moves, stage-in
+ * and the idle stream between them); n_after_score such spans. */
 typedef struct kvmem_hip_perf {
     double score_ms;
     double topk_ms;
@@ -578,6 +581,8 @@ typedef struct kvmem_hip_perf {
     uint64_t n_layout;
     uint64_t h2d_bytes;
     uint64_t d2d_bytes;
+    double after_score_ms;
+    uint64_t n_after_score;
 } kvmem_hip_perf;
 
 KVMEM_HIP_API int kvmem_hip_perf_enable(kvmem_hip_ctx *ctx, int on);

@@ -125,7 +125,8 @@ class Perf(C.Structure):
     _fields_ = [("score_ms", C.c_double), ("topk_ms", C.c_double), ("set_ms", C.c_double),
                 ("copy_ms", C.c_double), ("layout_ms", C.c_double), ("n_score", C.c_uint64),
                 ("n_topk", C.c_uint64), ("n_set", C.c_uint64), ("n_copy", C.c_uint64),
-                ("n_layout", C.c_uint64), ("h2d_bytes", C.c_uint64), ("d2d_bytes", C.c_uint64)]
+                ("n_layout", C.c_uint64), ("h2d_bytes", C.c_uint64), ("d2d_bytes", C.c_uint64),
+                ("after_score_ms", C.c_double), ("n_after_score", C.c_uint64)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}

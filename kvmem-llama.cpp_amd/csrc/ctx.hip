@@ -146,6 +146,16 @@ void perf_begin(kvmem_hip_ctx *ctx, PerfStage s) {
     }
 }
 
+// The open scorer-to-stage-in span, if it reached a stage-in, joins the
+// done list; either way a new one may start.
+static void span_close(kvmem_hip_ctx *ctx) {
+    if (ctx->span_score_end && ctx->span_set_end) {
+        ctx->span_done.emplace_back(ctx->span_score_end, ctx->span_set_end);
+    }
+    ctx->span_score_end = nullptr;
+    ctx->span_set_end = nullptr;
+}
+
 void perf_end(kvmem_hip_ctx *ctx, PerfStage s) {
     hipEvent_t start = ctx->perf_open[s];
     if (!start) {
@@ -155,6 +165,12 @@ void perf_end(kvmem_hip_ctx *ctx, PerfStage s) {
     hipEvent_t end = perf_event(ctx);
     if (end && hipEventRecord(end, ctx->stream) == hipSuccess) {
         ctx->perf_done[s].emplace_back(start, end);
+        if (s == kPerfScore) {
+            span_close(ctx);
+            ctx->span_score_end = end;
+        } else if (s == kPerfSet && ctx->span_score_end) {
+            ctx->span_set_end = end;
+        }
         return;
     }
     ctx->perf_free.push_back(start);
@@ -164,6 +180,17 @@ void perf_end(kvmem_hip_ctx *ctx, PerfStage s) {
 }
 
 void perf_collect(kvmem_hip_ctx *ctx) {
+    // the spans first: their events belong to the stage pairs freed below
+    span_close(ctx);
+    for (auto &pr : ctx->span_done) {
+        float ms = 0.0f;
+        if (hipEventSynchronize(pr.second) == hipSuccess &&
+            hipEventElapsedTime(&ms, pr.first, pr.second) == hipSuccess) {
+            ctx->after_score_ms += ms;
+            ctx->n_after_score += 1;
+        }
+    }
+    ctx->span_done.clear();
     for (int s = 0; s < kPerfStages; ++s) {
         for (auto &pr : ctx->perf_done[s]) {
             float ms = 0.0f;
@@ -668,6 +695,8 @@ int kvmem_hip_perf_get(kvmem_hip_ctx *ctx, kvmem_hip_perf *out) {
     out->n_layout = ctx->perf_n[kPerfLayout];
     out->h2d_bytes = ctx->h2d_bytes;
     out->d2d_bytes = ctx->d2d_bytes;
+    out->after_score_ms = ctx->after_score_ms;
+    out->n_after_score = ctx->n_after_score;
     return KVMEM_HIP_OK;
 }
 
@@ -682,6 +711,8 @@ void kvmem_hip_perf_reset(kvmem_hip_ctx *ctx) {
     }
     ctx->h2d_bytes = 0;
     ctx->d2d_bytes = 0;
+    ctx->after_score_ms = 0.0;
+    ctx->n_after_score = 0;
 }
 
 }  // extern "C"

@@ -98,6 +98,12 @@ struct kvmem_hip_ctx {
     std::vector<std::pair<hipEvent_t, hipEvent_t>> perf_done[kvmem_hip::kPerfStages];
     double perf_ms[kvmem_hip::kPerfStages] = {};
     uint64_t perf_n[kvmem_hip::kPerfStages] = {};
+    // from a scoring stage's end event to the end event of the last
+    // stage-in after it (events owned by their stages' pairs)
+    hipEvent_t span_score_end = nullptr, span_set_end = nullptr;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> span_done;
+    double after_score_ms = 0.0;
+    uint64_t n_after_score = 0;
     uint64_t h2d_bytes = 0;
     uint64_t d2d_bytes = 0;
     uint64_t n_allocs = 0;  // device + pinned allocations since creation

@@ -71,7 +71,8 @@ __global__ __launch_bounds__(256) void meank_sum_kernel(const uint8_t *k, uint64
 // tokens' values in list order onto (or from zero into) q_sum, as the
 // reference's harvest loop does per layer (llama-memory-kvmem.cpp:2164-2172).
 template <typename QT>
-__global__ __launch_bounds__(256) void q_accumulate_kernel(const QT *q, const uint32_t *tokens,
+__global__ __launch_bounds__(256) void q_accumulate_kernel(const QT *q, const uint8_t *tok_dev,
+                                                           ArgTables tok_args, int listed,
                                                            uint32_t n_list, uint32_t n_tokens,
                                                            uint32_t E, uint32_t L, int reset,
                                                            float *q_sum) {
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(256) void q_accumulate_kernel(const QT *q, const ui
         float v[kBatch];
 #pragma unroll
         for (uint32_t j = 0; j < kBatch; ++j) {
-            const uint32_t t = tokens ? tokens[i + j] : i + j;
+            const uint32_t t = listed ? tab_read<uint32_t>(tok_dev, tok_args, 4u * (i + j)) : i + j;
             v[j] = static_cast<float>(src[static_cast<uint64_t>(t) * E]);
         }
 #pragma unroll
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(256) void q_accumulate_kernel(const QT *q, const ui
         }
     }
     for (; i < n_list; ++i) {
-        const uint32_t t = tokens ? tokens[i] : i;
+        const uint32_t t = listed ? tab_read<uint32_t>(tok_dev, tok_args, 4u * i) : i;
         acc += static_cast<float>(src[static_cast<uint64_t>(t) * E]);
     }
     *dst = acc;
@@ -130,25 +131,37 @@ __global__ __launch_bounds__(256) void meank_add_kernel(const uint8_t *k, uint32
     acc[e] = s;
 }
 
+// Per-layer 1 / (query rows x group size), 0 for a layer without query
+// rows, carried in the query kernel's arguments (no upload before it).
+constexpr uint32_t kMeankMaxL = 256;
+struct LayerScales {
+    float v[kMeankMaxL];
+};
+
 // One workgroup per (layer, KV head), one thread per channel: the group's
 // query sum (heads added in group order) scaled by invq, and its squared
-// norm reduced over the channels.
-__global__ __launch_bounds__(256) void meank_query_kernel(const float *q_sum, const float *invq,
-                                                          uint32_t L, uint32_t Hq, uint32_t Hkv,
-                                                          uint32_t D, float *qv, float *nq) {
+// norm reduced over the channels.  The (layer, 0) workgroups also copy the
+// layer's scale to invq_out in device memory for the kernels after it.
+__global__ __launch_bounds__(256) void meank_query_kernel(const float *q_sum, LayerScales invq,
+                                                          float *invq_out, uint32_t L, uint32_t Hq,
+                                                          uint32_t Hkv, uint32_t D, float *qv, float *nq) {
     __shared__ float part[4];
     const uint32_t i = blockIdx.x;  // l * Hkv + h
     const uint32_t d = threadIdx.x;
     const uint32_t l = i / Hkv;
     const uint32_t h = i - l * Hkv;
     const uint32_t g = Hq / Hkv;
+    const float scale = invq.v[l];  // uniform index: read from the argument bytes
+    if (h == 0 && d == 0) {
+        invq_out[l] = scale;
+    }
     float v = 0.0f;
     if (d < D) {
         float acc = 0.0f;
         for (uint32_t gi = 0; gi < g; ++gi) {
             acc += q_sum[(static_cast<uint64_t>(l) * Hq + h * g + gi) * D + d];
         }
-        v = acc * invq[l];
+        v = acc * scale;
         qv[static_cast<uint64_t>(i) * D + d] = v;
     }
     float n = v * v;
@@ -310,7 +323,7 @@ static size_t meank_cos_bytes(uint32_t L, uint32_t B) {
 
 size_t meank_scratch_bytes(uint32_t L, uint32_t Hkv, uint32_t B, uint32_t D) {
     const size_t qv_bytes = sizeof(float) * static_cast<size_t>(L) * Hkv * (D + 1);
-    return meank_cos_bytes(L, B) + qv_bytes + 256;
+    return meank_cos_bytes(L, B) + qv_bytes + sizeof(float) * static_cast<size_t>(L) + 256;
 }
 
 bool load_meank_kernels() {
@@ -485,24 +498,26 @@ int kvmem_hip_q_accumulate(kvmem_hip_ctx *ctx, const void *q, int32_t q_type, ui
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "q_accumulate: too many layers");
     }
     (void) hipSetDevice(ctx->device);
-    const uint32_t *dev_tokens = nullptr;
-    if (tokens && n_list) {
-        dev_tokens = static_cast<const uint32_t *>(upload(ctx, tokens, sizeof(uint32_t) * n_list,
-                                                          "q_accumulate tokens"));
-        if (!dev_tokens) {
-            return KVMEM_HIP_ERR_RUNTIME;
-        }
+    // the token list travels in the kernel arguments when it fits (768
+    // rows), else it is uploaded
+    LaunchTables lt;
+    const int listed = tokens && n_list ? 1 : 0;
+    if (listed && !stage_tables(ctx, tokens, sizeof(uint32_t) * n_list, lt, "q_accumulate tokens")) {
+        return KVMEM_HIP_ERR_RUNTIME;
     }
     const dim3 grid((n_embd_q + 255) / 256, n_layers);
     if (q_type == KVMEM_TYPE_F32) {
         q_accumulate_kernel<float><<<grid, 256, 0, ctx->stream>>>(
-            static_cast<const float *>(q), dev_tokens, n_list, n_tokens, n_embd_q, n_layers, reset, q_sum);
+            static_cast<const float *>(q), lt.dev, lt.args, listed, n_list, n_tokens, n_embd_q, n_layers, reset,
+            q_sum);
     } else if (q_type == KVMEM_TYPE_F16) {
         q_accumulate_kernel<_Float16><<<grid, 256, 0, ctx->stream>>>(
-            static_cast<const _Float16 *>(q), dev_tokens, n_list, n_tokens, n_embd_q, n_layers, reset, q_sum);
+            static_cast<const _Float16 *>(q), lt.dev, lt.args, listed, n_list, n_tokens, n_embd_q, n_layers,
+            reset, q_sum);
     } else {
         q_accumulate_kernel<__bf16><<<grid, 256, 0, ctx->stream>>>(
-            static_cast<const __bf16 *>(q), dev_tokens, n_list, n_tokens, n_embd_q, n_layers, reset, q_sum);
+            static_cast<const __bf16 *>(q), lt.dev, lt.args, listed, n_list, n_tokens, n_embd_q, n_layers,
+            reset, q_sum);
     }
     return hip_ok(ctx, hipGetLastError(), "q_accumulate launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
 }
@@ -522,7 +537,8 @@ int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {
     if (reinterpret_cast<uintptr_t>(a->k_sum) & 15u) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "score_meank: k_sum must be 16-byte aligned");
     }
-    if (L > kCombineMaxL) {
+    static_assert(kMeankMaxL == kCombineMaxL, "layer bound");
+    if (L > kMeankMaxL) {
         return fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "score_meank: more than 256 layers");
     }
     if (L == 0 || B == 0) {
@@ -531,9 +547,9 @@ int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {
     const uint32_t g = a->n_head / a->n_head_kv;
     // per-layer 1 / (q_count * g) as the reference computes it in fp32; 0
     // marks a layer without query rows
-    std::vector<float> invq(L);
+    LayerScales invq{};
     for (uint32_t l = 0; l < L; ++l) {
-        invq[l] = a->q_count[l] ? 1.0f / static_cast<float>(a->q_count[l] * g) : 0.0f;
+        invq.v[l] = a->q_count[l] ? 1.0f / static_cast<float>(a->q_count[l] * g) : 0.0f;
     }
     (void) hipSetDevice(ctx->device);
     // the fp32 query vectors start 256-byte aligned (read as float4)
@@ -546,17 +562,13 @@ int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {
     double *layer_cos = reinterpret_cast<double *>(scratch);
     float *qv = reinterpret_cast<float *>(scratch + cos_bytes);
     float *nq = qv + static_cast<size_t>(L) * a->n_head_kv * D;
-    const float *invq_dev = static_cast<const float *>(upload(ctx, invq.data(), sizeof(float) * L,
-                                                              "score_meank invq"));
-    if (!invq_dev) {
-        return KVMEM_HIP_ERR_RUNTIME;
-    }
+    float *invq_dev = nq + static_cast<size_t>(L) * a->n_head_kv;
     if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "score_meank launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     perf_begin(ctx, kPerfScore);
     const uint32_t lh = L * a->n_head_kv;
-    meank_query_kernel<<<lh, D, 0, ctx->stream>>>(a->q_sum, invq_dev, L, a->n_head, a->n_head_kv, D,
+    meank_query_kernel<<<lh, D, 0, ctx->stream>>>(a->q_sum, invq, invq_dev, L, a->n_head, a->n_head_kv, D,
                                                   qv, nq);
     const uint64_t items = static_cast<uint64_t>(L) * B;  // 16 lanes each
     const uint32_t grid = static_cast<uint32_t>((items * 16 + 255) / 256);

@@ -48,11 +48,12 @@ __device__ inline uint16_t f32_to_bf16_rne(float f) {
 
 // grid (n, L): out[l][i][:] = window[l][rows[i]][:] in the output type.
 __global__ __launch_bounds__(256) void qwin_gather_kernel(const float *window, uint32_t cap, uint32_t E,
-                                                          const uint32_t *rows, uint32_t n, int out_type,
-                                                          uint8_t *out) {
+                                                          const uint8_t *rows_dev, ArgTables rows_args,
+                                                          uint32_t n, int out_type, uint8_t *out) {
     const uint32_t i = blockIdx.x;
     const uint32_t l = blockIdx.y;
-    const float *src = window + (static_cast<uint64_t>(l) * cap + rows[i]) * E;
+    const uint32_t row = tab_read<uint32_t>(rows_dev, rows_args, 4u * i);
+    const float *src = window + (static_cast<uint64_t>(l) * cap + row) * E;
     const uint64_t o = (static_cast<uint64_t>(l) * n + i) * E;
     for (uint32_t e = threadIdx.x; e < E; e += 256u) {
         const float v = src[e];
@@ -152,16 +153,16 @@ int kvmem_hip_q_window_gather(kvmem_hip_ctx *ctx, const float *window, uint32_t 
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "q_window_gather: too many layers");
     }
     (void) hipSetDevice(ctx->device);
-    const uint32_t *dr = static_cast<const uint32_t *>(
-        upload(ctx, rows, sizeof(uint32_t) * n, "q_window_gather rows"));
-    if (!dr) {
+    // the row list travels in the kernel arguments when it fits (768 rows)
+    LaunchTables lt;
+    if (!stage_tables(ctx, rows, sizeof(uint32_t) * n, lt, "q_window_gather rows")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "q_window_gather launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
-    qwin_gather_kernel<<<dim3(n, n_layers), 256, 0, ctx->stream>>>(window, capacity, n_embd_q, dr, n, out_type,
-                                                                  static_cast<uint8_t *>(out));
+    qwin_gather_kernel<<<dim3(n, n_layers), 256, 0, ctx->stream>>>(window, capacity, n_embd_q, lt.dev, lt.args, n,
+                                                                  out_type, static_cast<uint8_t *>(out));
     return hip_ok(ctx, hipGetLastError(), "q_window_gather launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
 }
 

@@ -1195,26 +1195,29 @@ int apply_retrieval_device(kvmem_engine *e, const void *q, int32_t q_type, uint3
     if (n == 0 || (!e->hist_k && !e->host_base)) {
         return KVMEM_HIP_ERR_UNSUPPORTED;
     }
-    // the blocks whose pool rows are valid, ascending in id; a canonical
-    // pool holds them at ascending slots
-    std::vector<uint32_t> res_block, res_slot;
-    for (const Block &b : e->rt.store().blocks()) {
-        if (b.tier == Tier::GPU && b.gpu_slot >= 0) {
-            if (!res_slot.empty() && static_cast<uint32_t>(b.gpu_slot) <= res_slot.back()) {
-                return KVMEM_HIP_ERR_UNSUPPORTED;  // not a canonical pool
-            }
-            res_block.push_back(b.block_id);
-            res_slot.push_back(static_cast<uint32_t>(b.gpu_slot));
-        }
-    }
     kvmem_amd::TopkCharge charge;
     bool empty = false;
     int rc = preview_scores(e, q, q_type, n_q_tokens, mandatory, n_mandatory, charge, &empty);
     if (rc != KVMEM_HIP_OK) {
         return rc;
     }
+    // while the scorer runs: the blocks whose pool rows are valid,
+    // ascending in id; a canonical pool holds them at ascending slots
+    std::vector<uint32_t> res_block, res_slot;
+    bool canonical = true;
+    for (const Block &b : e->rt.store().blocks()) {
+        if (b.tier == Tier::GPU && b.gpu_slot >= 0) {
+            if (!res_slot.empty() && static_cast<uint32_t>(b.gpu_slot) <= res_slot.back()) {
+                canonical = false;
+                break;
+            }
+            res_block.push_back(b.block_id);
+            res_slot.push_back(static_cast<uint32_t>(b.gpu_slot));
+        }
+    }
     const uint32_t max_sel = static_cast<uint32_t>(charge.forced.size()) + charge.need;
-    if (empty || charge.all_fit || max_sel == 0 || max_sel > KVMEM_PLAN_MAX_SEL || max_sel > e->n_slots) {
+    if (!canonical || empty || charge.all_fit || max_sel == 0 || max_sel > KVMEM_PLAN_MAX_SEL ||
+        max_sel > e->n_slots) {
         // outside the device plan: the host selects over the scores on the
         // stream and plans
         std::vector<uint32_t> sel(std::max<uint32_t>(1, n));
