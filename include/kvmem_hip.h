@@ -586,6 +586,17 @@ typedef struct kvmem_hip_perf {
 } kvmem_hip_perf;
 
 KVMEM_HIP_API int kvmem_hip_perf_enable(kvmem_hip_ctx *ctx, int on);
+/* Which stages perf_enable times (default all): a mask of
+ * KVMEM_PERF_STAGE_* bits.  Each timed stage records two events on the
+ * stream, and each event holds the stream idle for a few microseconds, so
+ * timing fewer stages perturbs a call less.  after_score_ms needs SCORE and
+ * SET. */
+#define KVMEM_PERF_STAGE_SCORE 1u
+#define KVMEM_PERF_STAGE_TOPK 2u
+#define KVMEM_PERF_STAGE_SET 4u
+#define KVMEM_PERF_STAGE_COPY 8u
+#define KVMEM_PERF_STAGE_LAYOUT 16u
+KVMEM_HIP_API int kvmem_hip_perf_stages(kvmem_hip_ctx *ctx, uint32_t mask);
 KVMEM_HIP_API int kvmem_hip_perf_get(kvmem_hip_ctx *ctx, kvmem_hip_perf *out);
 KVMEM_HIP_API void kvmem_hip_perf_reset(kvmem_hip_ctx *ctx);
 

@@ -39,6 +39,10 @@ LAYER_MEAN, LAYER_MAX, LAYER_SUM = 0, 1, 2
 
 OK, ERR_INVALID, ERR_RUNTIME, ERR_NOMEM, ERR_STALE, ERR_UNSUPPORTED = range(6)
 
+# stage bits of Context.perf_stages (KVMEM_PERF_STAGE_*)
+PERF_STAGE_SCORE, PERF_STAGE_TOPK, PERF_STAGE_SET, PERF_STAGE_COPY, PERF_STAGE_LAYOUT = 1, 2, 4, 8, 16
+PERF_STAGE_ALL = 0xffffffff
+
 # operation kinds of Context.debug_fail_after (kvmem_hip_fail_kind)
 FAIL_ALLOC, FAIL_COPY, FAIL_LAUNCH = 1, 2, 4
 
@@ -211,6 +215,7 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_debug_fail_after", i32, vp, u32, C.c_uint64)
     _sig(lib, "kvmem_hip_debug_fail_left", C.c_uint64, vp)
     _sig(lib, "kvmem_hip_perf_enable", i32, vp, i32)
+    _sig(lib, "kvmem_hip_perf_stages", i32, vp, C.c_uint32)
     _sig(lib, "kvmem_hip_perf_get", i32, vp, C.POINTER(Perf))
     _sig(lib, "kvmem_hip_perf_reset", None, vp)
     if path is None:
@@ -480,6 +485,10 @@ class Context:
     # -- profiling
     def perf_enable(self, on: bool = True) -> None:
         self.check(self.lib.kvmem_hip_perf_enable(self.h, int(on)), "perf_enable")
+
+    def perf_stages(self, mask: int) -> None:
+        """Time only the stages in `mask` (PERF_STAGE_* bits) while enabled."""
+        self.check(self.lib.kvmem_hip_perf_stages(self.h, mask), "perf_stages")
 
     def perf(self) -> dict:
         p = Perf()

@@ -135,8 +135,8 @@ static hipEvent_t perf_event(kvmem_hip_ctx *ctx) {
 }
 
 void perf_begin(kvmem_hip_ctx *ctx, PerfStage s) {
-    if (!ctx->perf_on || ctx->perf_open[s]) {
-        return;  // off, or already inside this stage
+    if (!ctx->perf_on || !(ctx->perf_mask & (1u << s)) || ctx->perf_open[s]) {
+        return;  // off, not timed, or already inside this stage
     }
     hipEvent_t e = perf_event(ctx);
     if (e && hipEventRecord(e, ctx->stream) == hipSuccess) {
@@ -675,6 +675,14 @@ int kvmem_hip_perf_enable(kvmem_hip_ctx *ctx, int on) {
         return KVMEM_HIP_ERR_INVALID;
     }
     ctx->perf_on = on != 0;
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_hip_perf_stages(kvmem_hip_ctx *ctx, uint32_t mask) {
+    if (!ctx) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    ctx->perf_mask = mask;
     return KVMEM_HIP_OK;
 }
 

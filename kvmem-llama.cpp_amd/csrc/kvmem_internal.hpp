@@ -93,6 +93,7 @@ struct kvmem_hip_ctx {
 
     // profiling: start/end event pairs per stage, harvested when read
     bool perf_on = false;
+    uint32_t perf_mask = 0xffffffffu;  // stages timed while perf_on (bit = PerfStage)
     std::vector<hipEvent_t> perf_free;                       // reusable events
     hipEvent_t perf_open[kvmem_hip::kPerfStages] = {};       // started, not ended
     std::vector<std::pair<hipEvent_t, hipEvent_t>> perf_done[kvmem_hip::kPerfStages];

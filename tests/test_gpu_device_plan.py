@@ -187,3 +187,39 @@ def test_device_plan_failure_leaves_exact_pool(oracle):
     else:
         raise AssertionError("apply_retrieval never ran to completion")
     assert n_failed >= 4, n_failed  # scorer, top-k, plan, saves, chain walk, stage-in
+
+
+def test_perf_stage_mask_and_after_score_span():
+    """kvmem_hip_perf_stages: with SCORE | SET only the scorer and the
+    stage-in are timed, and after_score_ms spans the scorer's end to the
+    stage-in's end; with every stage the top-k and the slot moves are timed
+    too."""
+    announce("perf stage mask: scorer + stage-in only, then every stage")
+    cap = 40
+    k, v, q = history(cap, seed=71)
+    types = (kv.TYPE_Q8_0, kv.TYPE_Q8_0)
+    first = [0] + list(range(10, 33))
+    second = [0, 1, 2] + list(range(10, 31))   # 2 staged, the rest move right by 2
+    with make_engine(24, 8, *types) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, cap * T)
+        ctx = kv.Context.borrow(eng.ctx_handle())
+        eng.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=first)
+        ctx.perf_stages(kv.PERF_STAGE_SCORE | kv.PERF_STAGE_SET)
+        ctx.perf_enable(True)
+        ctx.perf_reset()
+        st = eng.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=second)
+        pf = ctx.perf()
+        assert st["n_staged"] == 2 and st["n_moved"] > 0 and st["device_planned"] == 1
+        assert pf["n_score"] == 1 and pf["n_set"] == 1
+        assert pf["n_topk"] == 0 and pf["n_layout"] == 0
+        assert pf["n_after_score"] == 1
+        assert pf["after_score_ms"] >= pf["set_ms"] > 0.0
+        ctx.perf_stages(kv.PERF_STAGE_ALL)
+        ctx.perf_reset()
+        st = eng.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=first)
+        pf = ctx.perf()
+        ctx.perf_enable(False)
+        assert st["n_moved"] > 0
+        assert pf["n_score"] == 1 and pf["n_topk"] == 1 and pf["n_layout"] == 1
+        assert pf["n_set"] == (1 if st["n_staged"] else 0)
+        assert pf["after_score_ms"] >= pf["topk_ms"] + pf["layout_ms"] + pf["set_ms"]
