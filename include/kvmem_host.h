@@ -173,10 +173,11 @@ typedef struct kvmem_engine_params {
                                   selection, commits the same plan to its
                                   store and queues the stage-in behind the
                                   walk (canonical layout, device-resident
-                                  history, no row transform or packed store,
-                                  budget <= 1024 blocks, pool <= 4096
-                                  slots, 16-byte rows).  0, or outside those
-                                  bounds: the host plans, as apply */
+                                  history, no packed store, budget <= 1024
+                                  blocks, pool <= 4096 slots, 16-byte rows;
+                                  a row transform is carried).  0, or
+                                  outside those bounds: the host plans, as
+                                  apply */
 } kvmem_engine_params;
 
 /* Block scorer of kvmem_engine_preview / apply_retrieval. */

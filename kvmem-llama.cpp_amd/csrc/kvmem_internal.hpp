@@ -74,6 +74,7 @@ struct kvmem_hip_ctx {
     kvmem_hip::PinBuf plan_counts;
     size_t plan_stage_off = 0;     // the stage table's offset in `plan`
     uint32_t plan_max_sel = 0;     // stage entries the last plan wrote
+    uint32_t plan_theta_off = 0;   // RoPE frequencies in the stage table
     uint64_t plan_row_bytes = 0;   // one moved row over every layer, K and V
     uint64_t plan_save_bytes = 0;  // one saved slot over every layer, K and V
 

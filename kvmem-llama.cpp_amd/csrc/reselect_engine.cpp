@@ -1160,7 +1160,7 @@ void commit_canonical(kvmem_engine *e, const std::vector<uint32_t> &ids, Plan &p
 // pool it covers (the resident blocks' order is checked per call).
 bool device_plan_ok(const kvmem_engine *e) {
     if (!e->p.device_plan || !e->p.canonical_layout || !e->hist_k || !e->hist_v || e->host_base ||
-        e->packed_base || e->has_xf || e->n_slots > KVMEM_PLAN_MAX_SLOTS || e->p.block_tokens > 65535u ||
+        e->packed_base || e->n_slots > KVMEM_PLAN_MAX_SLOTS || e->p.block_tokens > 65535u ||
         kvmem_hip_row_size(e->p.type_k, e->n_embd_k) % 16 != 0 ||
         kvmem_hip_row_size(e->p.type_v, e->n_embd_v) % 16 != 0) {
         return false;

@@ -1989,6 +1989,9 @@ struct PlanParams {
     uint32_t off_stage, off_chain, off_saves;
     uint32_t n_res, n_slots, n_blocks, T, last_T, dirty, L, max_sel, max_saves;
     uint32_t first_T;        // tokens of block 0
+    uint32_t n_theta;        // RoPE frequencies copied from the tables to the stage table
+    uint32_t theta_src;      // their byte offset in the tables
+    uint32_t theta_dst;      // and in the stage table
 };
 
 // Exclusive prefix over the workgroup's threads of `v`; `total` gets the sum.
@@ -2036,6 +2039,11 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanParams p, ArgTab
         const uint64_t v = tab_read<uint64_t>(p.tables, t, 8u * j);
         *reinterpret_cast<uint64_t *>(p.plan + p.off_stage + 8u * j) = v;
         *reinterpret_cast<uint64_t *>(p.plan + p.off_chain + 8u * j) = v;
+    }
+    // the RoPE frequencies of a transformed stage-in follow its items
+    for (uint32_t j = tid; j < p.n_theta; j += kPlanThreads) {
+        *reinterpret_cast<float *>(p.plan + p.off_stage + p.theta_dst + 4u * j) =
+            tab_read<float>(p.tables, t, p.theta_src + 4u * j);
     }
     const uint32_t rb_off = 16u * L;
     const uint32_t rs_off = rb_off + 4u * p.n_res;
@@ -2691,7 +2699,13 @@ int kvmem_hip_reselect_device(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
     const uint64_t krow = kvmem_hip_row_size(pool->type_k, pool->n_embd_k);
     const uint64_t vrow = kvmem_hip_row_size(pool->type_v, pool->n_embd_v);
     const uint32_t cap = hist->capacity_blocks ? hist->capacity_blocks : hist->n_blocks;
-    if (pool->xf || pool->n_slots > kPlanMaxSlots || max_sel == 0 || max_sel > kPlanMaxSel ||
+    XfParams xp;
+    st = resolve_xf(ctx, pool, hist->n_embd_k, hist->n_embd_v, true, xp);
+    if (st != KVMEM_HIP_OK) {
+        return st;
+    }
+    const uint32_t n_theta = xp.n_rot / 2;
+    if ((pool->xf && pool->xf->pos0) || pool->n_slots > kPlanMaxSlots || max_sel == 0 || max_sel > kPlanMaxSel ||
         max_sel > pool->n_slots || n_res > pool->n_slots || T == 0 || T > 65535u || krow % 16 || vrow % 16 ||
         hist->n_embd_k % 32 || hist->n_embd_v % 32 || !aligned16(hist->k) || !aligned16(hist->v) ||
         cap < hist->n_blocks) {
@@ -2708,7 +2722,8 @@ int kvmem_hip_reselect_device(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
     const uint32_t ops_per = kPlanSaveOpsPer(L);
     auto up256 = [](size_t x) { return (x + 255) & ~size_t{255}; };
     const size_t off_stage = 256;
-    const size_t off_chain = up256(off_stage + 16 * size_t{L} + 16 * size_t{max_sel});
+    const size_t theta_dst = 16 * size_t{L} + 16 * size_t{max_sel};  // in the stage table
+    const size_t off_chain = up256(off_stage + theta_dst + 4 * size_t{n_theta});
     const size_t off_saves = up256(off_chain + 16 * size_t{L} + 4 * size_t{seg_record_words<uint16_t>()} * max_segs);
     const size_t plan_bytes = off_saves + sizeof(CopyOpDev) * size_t{ops_per} * max_saves;
     const uint64_t kspan = krow * T;
@@ -2726,13 +2741,18 @@ int kvmem_hip_reselect_device(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
         return KVMEM_HIP_ERR_RUNTIME;
     }
     std::memset(ctx->plan_counts.ptr, 0, sizeof(uint32_t) * kPlanCounts);
-    // the pool's layer pointers (K, then V), then the resident table
-    std::vector<uint8_t> tab(16 * size_t{L} + 8 * size_t{n_res});
+    // the pool's layer pointers (K, then V), the resident table, then the
+    // RoPE frequencies of a transformed pool
+    const size_t theta_src = 16 * size_t{L} + 8 * size_t{n_res};
+    std::vector<uint8_t> tab(theta_src + 4 * size_t{n_theta});
     std::memcpy(tab.data(), pool->k_layers, 8 * size_t{L});
     std::memcpy(tab.data() + 8 * size_t{L}, pool->v_layers, 8 * size_t{L});
     if (n_res) {
         std::memcpy(tab.data() + 16 * size_t{L}, res_block, 4 * size_t{n_res});
         std::memcpy(tab.data() + 16 * size_t{L} + 4 * size_t{n_res}, res_slot, 4 * size_t{n_res});
+    }
+    if (n_theta) {
+        std::memcpy(tab.data() + theta_src, pool->xf->theta, 4 * size_t{n_theta});
     }
     LaunchTables lt;
     if (!stage_tables(ctx, tab.data(), tab.size(), lt, "reselect_device resident table")) {
@@ -2758,6 +2778,9 @@ int kvmem_hip_reselect_device(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
     pp.T = T;
     pp.last_T = hist->last_block_tokens;
     pp.first_T = (hist->n_blocks == 1 && hist->last_block_tokens) ? hist->last_block_tokens : T;
+    pp.n_theta = n_theta;
+    pp.theta_src = static_cast<uint32_t>(theta_src);
+    pp.theta_dst = static_cast<uint32_t>(theta_dst);
     pp.dirty = dirty;
     pp.L = L;
     pp.max_sel = max_sel;
@@ -2810,6 +2833,7 @@ int kvmem_hip_reselect_device(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
         return KVMEM_HIP_ERR_RUNTIME;
     }
     ctx->plan_stage_off = off_stage;
+    ctx->plan_theta_off = static_cast<uint32_t>(theta_dst);
     ctx->plan_max_sel = max_sel;
     return KVMEM_HIP_OK;
 }
@@ -2823,8 +2847,8 @@ int kvmem_hip_reselect_device_stagein(kvmem_hip_ctx *ctx, const kvmem_hip_histor
     if (!ctx) {
         return KVMEM_HIP_ERR_INVALID;
     }
-    if (!hist || !hist->k || !hist->v || !pool || !pool->v_layers || pool->xf || !ctx->plan.ptr ||
-        !ctx->plan_stage_off) {
+    if (!hist || !hist->k || !hist->v || !pool || !pool->v_layers || (pool->xf && pool->xf->pos0) ||
+        !ctx->plan.ptr || !ctx->plan_stage_off) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "reselect_device_stagein: no device plan");
     }
     if (n_staged > ctx->plan_max_sel || ctx->plan_max_sel > pool->n_slots) {
@@ -2836,11 +2860,15 @@ int kvmem_hip_reselect_device_stagein(kvmem_hip_ctx *ctx, const kvmem_hip_histor
     const uint32_t T = hist->block_tokens;
     const uint32_t L = hist->n_layers;
     const uint32_t cap = hist->capacity_blocks ? hist->capacity_blocks : hist->n_blocks;
+    XfParams xp;
+    const int xst = resolve_xf(ctx, pool, hist->n_embd_k, hist->n_embd_v, true, xp);
+    if (xst != KVMEM_HIP_OK) {
+        return xst;
+    }
     JobTables jt;
     jt.tables.dev = static_cast<const uint8_t *>(ctx->plan.ptr) + ctx->plan_stage_off;
     jt.items_off = 16u * L;
-    jt.theta_off = 16u * L;
-    const XfParams xp{};
+    jt.theta_off = ctx->plan_theta_off;  // the plan kernel copied the RoPE frequencies there
     const uint64_t bk = static_cast<uint64_t>(T) * hist->n_embd_k * 2u;
     const uint64_t bv = static_cast<uint64_t>(T) * hist->n_embd_v * 2u;
     const BlockSource sk = make_block_source(pool->type_k, static_cast<const uint8_t *>(hist->k), bk, bk * cap, jt,

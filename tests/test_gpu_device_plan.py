@@ -14,7 +14,7 @@ import pytest
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-from engine_helpers import E, HQ, L, T, check_pool, history, kv, make_engine  # noqa: E402
+from engine_helpers import D, E, HQ, L, T, check_pool, history, kv, make_engine, workloads  # noqa: E402
 
 
 def announce(msg: str) -> None:
@@ -223,3 +223,52 @@ def test_perf_stage_mask_and_after_score_span():
         assert pf["n_score"] == 1 and pf["n_topk"] == 1 and pf["n_layout"] == 1
         assert pf["n_set"] == (1 if st["n_staged"] else 0)
         assert pf["after_score_ms"] >= pf["topk_ms"] + pf["layout_ms"] + pf["set_ms"]
+
+
+XF_CASES = [
+    # (n_rot, type_k, type_v): RoPE 256 + attn_rot on the 64-elements-per-lane kernel,
+    # RoPE 64 + attn_rot on the 8-per-lane kernel, attn_rot alone
+    (256, kv.TYPE_Q8_0, kv.TYPE_Q4_0),
+    (64, kv.TYPE_Q5_0, kv.TYPE_Q5_0),
+    (0, kv.TYPE_Q8_0, kv.TYPE_Q8_0),
+]
+
+
+@pytest.mark.parametrize("case", XF_CASES, ids=["rope256_q8q4", "rope64_q5q5", "hadamard_q8q8"])
+def test_device_plan_with_row_transform(oracle, case):
+    """A transformed pool (RoPE at the original positions, then attn_rot)
+    through the device plan: the plan kernel carries the RoPE frequencies
+    to the stage-in; pools equal the host-planned engine's byte for byte,
+    and with RoPE 256 every selected block equals the oracle's transform
+    and quantization."""
+    from test_gpu_transform import expected_rows
+    n_rot, tk, tv = case
+    announce(f"device plan with the row transform: n_rot {n_rot} + attn_rot, types {(tk, tv)}, 4 steps")
+    cap = 48
+    k, v, _ = history(cap, seed=73)
+    xf = dict(n_rot=n_rot, rope_freq_base=1e6, attn_rot=1)
+    with make_engine(24, 8, tk, tv, **xf) as dev, make_engine(24, 8, tk, tv, device_plan=0, **xf) as ref:
+        for eng in (dev, ref):
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, cap * T)
+        moved = 0
+        for q in queries(74, 4):
+            sd = dev.apply_retrieval(q.data_ptr(), q.shape[1])
+            sr = ref.apply_retrieval(q.data_ptr(), q.shape[1])
+            assert sd.pop("device_planned") == 1 and sr.pop("device_planned") == 0
+            assert sd == sr
+            assert dev.block_slots() == ref.block_slots()
+            wd, wr = window(dev, tk, tv, lambda b: T), window(ref, tk, tv, lambda b: T)
+            assert wd.keys() == wr.keys()
+            for key in wd:
+                assert np.array_equal(wd[key], wr[key]), key
+            moved += sd["n_moved"]
+        assert moved > 0
+        if n_rot == 256:
+            theta = oracle.rope_theta(256, 1e6)
+            kb = workloads.to_bits(torch, k)
+            vb = workloads.to_bits(torch, v)
+            for (layer, which, b), got in wd.items():
+                src, ty, nr, width = (kb, tk, 256, 256) if which == 0 else (vb, tv, 0, 64)
+                want = expected_rows(oracle, ty, src[layer, b].reshape(T, E), D, nr,
+                                     theta if nr else None, b * T, width)
+                assert np.array_equal(got, want), (layer, which, b)
