@@ -272,3 +272,44 @@ def test_device_plan_with_row_transform(oracle, case):
                 want = expected_rows(oracle, ty, src[layer, b].reshape(T, E), D, nr,
                                      theta if nr else None, b * T, width)
                 assert np.array_equal(got, want), (layer, which, b)
+
+
+def test_device_plan_random_selections():
+    """40 seeded random selections of 24 blocks (sink kept) over 64 blocks,
+    some steps with a grown tail: the device plan's diff, chain ranks, cut
+    slots and stage items leave the same pool bytes and slots as the host
+    plan after every step."""
+    announce("device plan: 40 random selections vs the host plan, q8_0 K / q5_0 V")
+    cap = 64
+    k, v, q = history(cap, seed=75)
+    types = (kv.TYPE_Q8_0, kv.TYPE_Q5_0)
+    rng = np.random.default_rng(76)
+    tail = {"n": 60}
+    ntok_of = lambda b: tail["n"] if b == cap - 1 else T  # noqa: E731
+    with make_engine(24, 8, *types) as dev, make_engine(24, 8, *types, device_plan=0) as ref:
+        for eng in (dev, ref):
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, (cap - 1) * T + tail["n"])
+        moved = staged = 0
+        for step in range(40):
+            if step in (13, 29):  # the partial tail grows: staged again if resident
+                for eng in (dev, ref):
+                    eng.append_tokens(20)
+                tail["n"] += 20
+            # runs of neighbours as well as scattered ids, so chains of every length occur
+            start = int(rng.integers(1, cap - 30))
+            pool_ids = np.concatenate([np.arange(start, start + 30), rng.choice(np.arange(1, cap), 20)])
+            sel = sorted({0, *rng.choice(np.unique(pool_ids), 23, replace=False).tolist()})
+            sel = sel[:24]
+            sd = dev.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=sel)
+            sr = ref.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=sel)
+            assert sd.pop("device_planned") == 1 and sr.pop("device_planned") == 0, step
+            assert sd == sr, step
+            slots = dev.block_slots()
+            assert slots == ref.block_slots(), step
+            assert sorted(b for b, s in enumerate(slots) if s >= 0) == sel, step
+            wd, wr = window(dev, *types, ntok_of), window(ref, *types, ntok_of)
+            for key in wd:
+                assert np.array_equal(wd[key], wr[key]), (step, key)
+            moved += sd["n_moved"]
+            staged += sd["n_staged"]
+        assert moved > 100 and staged > 100, (moved, staged)
