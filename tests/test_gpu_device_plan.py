@@ -276,9 +276,10 @@ def test_device_plan_with_row_transform(oracle, case):
 
 def test_device_plan_random_selections():
     """40 seeded random selections of 24 blocks (sink kept) over 64 blocks,
-    some steps with a grown tail: the device plan's diff, chain ranks, cut
-    slots and stage items leave the same pool bytes and slots as the host
-    plan after every step."""
+    some steps with a grown tail, every tenth step a repeat (nothing to
+    stage or move): the device plan's diff, chain ranks, cut slots and stage
+    items leave the same pool bytes and slots as the host plan after every
+    step."""
     announce("device plan: 40 random selections vs the host plan, q8_0 K / q5_0 V")
     cap = 64
     k, v, q = history(cap, seed=75)
@@ -291,15 +292,15 @@ def test_device_plan_random_selections():
             eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, (cap - 1) * T + tail["n"])
         moved = staged = 0
         for step in range(40):
-            if step in (13, 29):  # the partial tail grows: staged again if resident
+            if step in (13, 27):  # the partial tail grows: staged again if resident
                 for eng in (dev, ref):
                     eng.append_tokens(20)
                 tail["n"] += 20
             # runs of neighbours as well as scattered ids, so chains of every length occur
             start = int(rng.integers(1, cap - 30))
             pool_ids = np.concatenate([np.arange(start, start + 30), rng.choice(np.arange(1, cap), 20)])
-            sel = sorted({0, *rng.choice(np.unique(pool_ids), 23, replace=False).tolist()})
-            sel = sel[:24]
+            if step % 10 != 9:  # every tenth step repeats the last: nothing staged or moved
+                sel = sorted({0, *rng.choice(np.unique(pool_ids), 23, replace=False).tolist()})
             sd = dev.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=sel)
             sr = ref.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=sel)
             assert sd.pop("device_planned") == 1 and sr.pop("device_planned") == 0, step
@@ -310,6 +311,8 @@ def test_device_plan_random_selections():
             wd, wr = window(dev, *types, ntok_of), window(ref, *types, ntok_of)
             for key in wd:
                 assert np.array_equal(wd[key], wr[key]), (step, key)
+            if step % 10 == 9:
+                assert sd["n_staged"] == 0 and sd["n_moved"] == 0, step
             moved += sd["n_moved"]
             staged += sd["n_staged"]
         assert moved > 100 and staged > 100, (moved, staged)
