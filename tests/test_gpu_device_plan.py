@@ -316,3 +316,70 @@ def test_device_plan_random_selections():
             moved += sd["n_moved"]
             staged += sd["n_staged"]
         assert moved > 100 and staged > 100, (moved, staged)
+
+
+GEOMETRIES = [
+    # (block_tokens, n_head, n_head_kv, head_dim, type_k, type_v)
+    (32, 8, 2, 128, kv.TYPE_Q8_0, kv.TYPE_Q4_0),
+    (64, 16, 2, 128, kv.TYPE_Q5_0, kv.TYPE_Q8_0),
+]
+
+
+@pytest.mark.parametrize("geom", GEOMETRIES, ids=["T32_d128", "T64_d128"])
+def test_device_plan_other_block_sizes(oracle, geom):
+    """32- and 64-token blocks over 128-wide heads (256-element rows): 16
+    random selections through the device and the host plan leave the same
+    pool bytes and slots, and the last window equals the oracle's
+    quantization of every selected block."""
+    from kvmem_amd import host
+    bt, hq, hkv, hd, tk, tv = geom
+    nl, cap, budget = 2, 48, 16
+    e = hkv * hd
+    announce(f"device plan: {bt}-token blocks, {hkv} KV heads x {hd}, types {(tk, tv)}, 16 steps")
+    k, v, q = workloads.scoring_tensors(torch, "cuda", L=nl, B=cap, Tq=8, seed=77, T=bt, Hkv=hkv, Hq=hq,
+                                        D=hd, with_v=True)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(78)
+
+    def engine(**kw):
+        return host.Engine(n_layers=nl, block_tokens=bt, n_head=hq, n_head_kv=hkv, head_dim=hd,
+                           budget_blocks=budget, reserve_blocks=4, type_k=tk, type_v=tv, **kw)
+
+    def pool_rows(eng, layer, which, ty):
+        rb = kv.row_size(ty, e)
+        n = eng.n_slots() * bt * rb
+        buf = torch.empty(n, dtype=torch.uint8, device="cuda")
+        c = kv.Context(0)
+        c.d2d_batched([eng.pool_layer(layer)[which]], [buf.data_ptr()], [n])
+        c.sync()
+        c.close()
+        return buf.cpu().numpy().reshape(eng.n_slots() * bt, rb)
+
+    with engine() as dev, engine(device_plan=0) as ref:
+        for eng in (dev, ref):
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, cap * bt)
+        moved = 0
+        for step in range(16):
+            sel = sorted({0, *rng.choice(np.arange(1, cap), budget - 1, replace=False).tolist()})
+            sd = dev.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=sel)
+            sr = ref.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=sel)
+            assert sd.pop("device_planned") == 1 and sr.pop("device_planned") == 0, step
+            assert sd == sr, step
+            slots = dev.block_slots()
+            assert slots == ref.block_slots(), step
+            for layer in range(nl):
+                for which, ty in ((0, tk), (1, tv)):
+                    pd, pr = pool_rows(dev, layer, which, ty), pool_rows(ref, layer, which, ty)
+                    for b in sel:
+                        s = slots[b]
+                        assert np.array_equal(pd[s * bt:(s + 1) * bt], pr[s * bt:(s + 1) * bt]), (step, b)
+            moved += sd["n_moved"]
+        assert moved > 0
+        kb, vb = workloads.to_bits(torch, k), workloads.to_bits(torch, v)
+        for layer in range(nl):
+            for which, src, ty in ((0, kb, tk), (1, vb, tv)):
+                pd = pool_rows(dev, layer, which, ty)
+                for b in sel:
+                    s = slots[b]
+                    want = oracle.quantize_rows_f16(ty, src[layer, b].reshape(bt, e))
+                    assert np.array_equal(pd[s * bt:(s + 1) * bt], want), (layer, which, b)
