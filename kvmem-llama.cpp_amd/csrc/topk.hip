@@ -29,6 +29,7 @@
 #include "device_reselect.h"
 
 #include <algorithm>
+#include <chrono>
 #include <vector>
 
 namespace kvmem_hip {
@@ -447,9 +448,15 @@ int topk_launch(kvmem_hip_ctx *ctx, const float *scores, uint32_t n, const uint3
     return KVMEM_HIP_OK;
 }
 
-// Wait half: spin on the completion word of the last topk_launch; every few
-// thousand rounds ask the stream whether it has drained (then the word must
-// be set) or failed.
+// Wait half: spin on the completion word of the last topk_launch.  Once the
+// wait has lasted kTopkQueryAfterUs, every few thousand rounds ask the
+// stream whether it has drained (then the word must be set) or failed.  The
+// query is held back because the runtime answers it by attaching a
+// completion signal, with a system-scope cache release, to the last command
+// queued: in a device-planned apply that is the chain walk, and its release
+// would then stall the stage-in queued behind it by several microseconds.
+constexpr int64_t kTopkQueryAfterUs = 20000;
+
 int topk_wait(kvmem_hip_ctx *ctx, uint32_t *sel_out, uint32_t *n_sel) {
     if (!ctx->topk_pending) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "topk: no launch to wait for");
@@ -459,9 +466,14 @@ int topk_wait(kvmem_hip_ctx *ctx, uint32_t *sel_out, uint32_t *n_sel) {
     const uint32_t epoch = ctx->topk_epoch;
     const uint32_t *h = static_cast<const uint32_t *>(ctx->topk_sel_host.ptr);
     const uint32_t *done = h + topk_flag_index(n);
+    const auto t0 = std::chrono::steady_clock::now();
+    bool query = false;
     for (uint32_t spin = 1; __atomic_load_n(done, __ATOMIC_ACQUIRE) != epoch; ++spin) {
         cpu_relax();
-        if ((spin & 4095u) == 0) {
+        if ((spin & 4095u) == 0 && !query) {
+            query = std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(kTopkQueryAfterUs);
+        }
+        if (query && (spin & 4095u) == 0) {
             const hipError_t q = hipStreamQuery(ctx->stream);
             if (q == hipErrorNotReady) {
                 continue;
