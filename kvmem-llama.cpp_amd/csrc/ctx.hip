@@ -53,7 +53,7 @@ bool ensure_dev(kvmem_hip_ctx *ctx, DevBuf &b, size_t bytes, const char *what) {
         if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), what)) {
             return false;
         }
-        hipFree(b.ptr);
+        (void) hipFree(b.ptr);
         b.ptr = nullptr;
         b.bytes = 0;
     }
@@ -78,7 +78,7 @@ bool ensure_pin(kvmem_hip_ctx *ctx, PinBuf &b, size_t bytes, const char *what, u
         if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), what)) {
             return false;
         }
-        hipHostFree(b.ptr);
+        (void) hipHostFree(b.ptr);
         b.ptr = nullptr;
         b.bytes = 0;
     }
@@ -426,42 +426,42 @@ void kvmem_hip_destroy(kvmem_hip_ctx *ctx) {
     }
     (void) hipSetDevice(ctx->device);
     if (ctx->stream) {
-        hipStreamSynchronize(ctx->stream);
+        (void) hipStreamSynchronize(ctx->stream);
     }
     if (ctx->copy_stream) {
-        hipStreamSynchronize(ctx->copy_stream);
+        (void) hipStreamSynchronize(ctx->copy_stream);
     }
     for (auto &s : ctx->upload) {
-        if (s.host.ptr) hipHostFree(s.host.ptr);
-        if (s.dev.ptr) hipFree(s.dev.ptr);
-        if (s.done) hipEventDestroy(s.done);
+        if (s.host.ptr) (void) hipHostFree(s.host.ptr);
+        if (s.dev.ptr) (void) hipFree(s.dev.ptr);
+        if (s.done) (void) hipEventDestroy(s.done);
     }
     for (DevBuf *b : {&ctx->score_partial, &ctx->score_layers, &ctx->meank_scratch,
                       &ctx->move_scratch, &ctx->h2d_ring, &ctx->d2h_ring, &ctx->topk_dev, &ctx->plan}) {
-        if (b->ptr) hipFree(b->ptr);
+        if (b->ptr) (void) hipFree(b->ptr);
     }
-    if (ctx->topk_sel_host.ptr) hipHostFree(ctx->topk_sel_host.ptr);
-    if (ctx->plan_counts.ptr) hipHostFree(ctx->plan_counts.ptr);
+    if (ctx->topk_sel_host.ptr) (void) hipHostFree(ctx->topk_sel_host.ptr);
+    if (ctx->plan_counts.ptr) (void) hipHostFree(ctx->plan_counts.ptr);
     for (int i = 0; i < 8; ++i) {
-        if (ctx->h2d_copied[i]) hipEventDestroy(ctx->h2d_copied[i]);
-        if (ctx->h2d_consumed[i]) hipEventDestroy(ctx->h2d_consumed[i]);
+        if (ctx->h2d_copied[i]) (void) hipEventDestroy(ctx->h2d_copied[i]);
+        if (ctx->h2d_consumed[i]) (void) hipEventDestroy(ctx->h2d_consumed[i]);
     }
     for (int i = 0; i < 2; ++i) {
-        if (ctx->d2h_gathered[i]) hipEventDestroy(ctx->d2h_gathered[i]);
-        if (ctx->d2h_done[i]) hipEventDestroy(ctx->d2h_done[i]);
+        if (ctx->d2h_gathered[i]) (void) hipEventDestroy(ctx->d2h_gathered[i]);
+        if (ctx->d2h_done[i]) (void) hipEventDestroy(ctx->d2h_done[i]);
     }
     for (int s = 0; s < kPerfStages; ++s) {
-        if (ctx->perf_open[s]) hipEventDestroy(ctx->perf_open[s]);
+        if (ctx->perf_open[s]) (void) hipEventDestroy(ctx->perf_open[s]);
         for (auto &pr : ctx->perf_done[s]) {
-            hipEventDestroy(pr.first);
-            hipEventDestroy(pr.second);
+            (void) hipEventDestroy(pr.first);
+            (void) hipEventDestroy(pr.second);
         }
     }
     for (hipEvent_t e : ctx->perf_free) {
-        hipEventDestroy(e);
+        (void) hipEventDestroy(e);
     }
-    if (ctx->own_stream) hipStreamDestroy(ctx->own_stream);
-    if (ctx->copy_stream) hipStreamDestroy(ctx->copy_stream);
+    if (ctx->own_stream) (void) hipStreamDestroy(ctx->own_stream);
+    if (ctx->copy_stream) (void) hipStreamDestroy(ctx->copy_stream);
     delete ctx;
 }
 
