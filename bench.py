@@ -64,6 +64,7 @@ SCORE_TRAFFIC_BYTES = 8.597e9 + 2.10e6
 STAGEIN_TRAFFIC_BYTES = 6.458e8 + 3.431e8
 MFMA_F16_PEAK_TFLOPS = 2500.0
 PCIE_PEAK_GBS = 64.0
+HOST_CPU_SHARE = 16           # host cores a one-GPU job may use, whatever the node shows
 
 
 def log(msg: str) -> None:
@@ -182,7 +183,8 @@ def cpu_baseline(torch, k, v, q, sel_ids: list[int], budget_s: float = 12.0) -> 
     sys.path.insert(0, str(ROOT / "oracle"))
     import kvmem_oracle as oracle
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    visible = len(os.sched_getaffinity(0))
+    threads = min(HOST_CPU_SHARE, visible)  # a one-GPU job's share of the host's cores
     os.environ.setdefault("OMP_NUM_THREADS", str(threads))
     qf = q.float().cpu().numpy()
 
@@ -244,6 +246,7 @@ def cpu_baseline(torch, k, v, q, sel_ids: list[int], budget_s: float = 12.0) -> 
         memcpy_s = dt if memcpy_s is None else min(memcpy_s, dt)
     return {
         "value": round(total_ms, 1), "unit": "ms/step", "cores": threads, "kind": "port",
+        "host_cpus_visible": visible, "cpu_share_per_gpu": HOST_CPU_SHARE,
         "sample": (f"fp32 per-token max scorer on {len(sample_ids)} of {B} blocks x {L} layers "
                    f"(OpenMP, {threads} threads) scaled x{B / len(sample_ids):.1f}; top-256 over "
                    f"{B} scores; q8_0 quantize of {n_q} of {N_CHANGED} staged blocks x {L} layers "
