@@ -103,6 +103,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores,
     __shared__ uint32_t wave_tot[kTopkWaves];
     __shared__ uint64_t s_prefix;
     __shared__ uint32_t s_rank;
+    __shared__ uint32_t s_alone;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const bool tl = tie_lower != 0;
@@ -121,7 +122,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores,
     }
     __syncthreads();
 
-    // ---- radix select: threshold = the need-th largest candidate key
+    // ---- radix select: threshold = the need-th largest candidate key.
+    // Keys are unique, so once the digit holding that rank has a single key
+    // it is the threshold, and the digits decided so far (`mask`) order
+    // every other key against it: the later passes are skipped.
     uint64_t prefix = 0ull;
     uint64_t mask = 0ull;
     uint32_t rank = need;  // rank still to find among keys matching `prefix`
@@ -129,6 +133,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores,
         for (int shift = 56; shift >= 0; shift -= 8) {
             if (tid < 256u) {
                 hist[tid] = 0u;
+            }
+            if (tid == 0u) {
+                s_alone = 0u;
             }
             __syncthreads();
             for (uint32_t i = tid; i < n; i += kTopkThreads) {
@@ -162,6 +169,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores,
                     if (above < rank && rank <= above + c[j]) {
                         s_prefix = prefix | (static_cast<uint64_t>(4u * lane + j) << shift);
                         s_rank = rank - above;
+                        s_alone = c[j] == 1u ? 1u : 0u;
                     }
                     above += c[j];
                 }
@@ -170,10 +178,16 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores,
             prefix = s_prefix;
             rank = s_rank;
             mask |= 0xffull << shift;
-            __syncthreads();  // s_prefix / hist are rewritten by the next pass
+            const bool alone = s_alone != 0u;
+            __syncthreads();  // s_prefix / s_alone / hist are rewritten by the next pass
+            if (alone) {
+                break;
+            }
         }
     }
-    const uint64_t threshold = prefix;  // unique key of rank `need`
+    // the key of rank `need`, on the bits decided (all 64 unless it stood
+    // alone earlier): a candidate wins when its key on those bits is >= it
+    const uint64_t threshold = prefix;
 
     // ---- ordered compaction: thread t owns ids [t*seg, (t+1)*seg)
     const uint32_t seg = (n + kTopkThreads - 1) / kTopkThreads;
@@ -184,7 +198,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float *scores,
         if (k == 0ull) {
             return (forced_bits[i >> 5] >> (i & 31u)) & 1u;
         }
-        return need > 0u && k >= threshold;
+        return need > 0u && (k & mask) >= threshold;
     };
     uint32_t cnt = 0;
     uint32_t picked = 0;  // bit j: id lo + j chosen (seg <= 16)
