@@ -257,6 +257,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_stream_kernel(
     __shared__ uint32_t wave_tot[kTopkWaves];
     __shared__ uint64_t s_prefix;
     __shared__ uint32_t s_rank;
+    __shared__ uint32_t s_alone;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const bool tl = tie_lower != 0;
@@ -272,6 +273,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_stream_kernel(
     auto is_forced = [&](uint32_t i) -> bool { return (forced_bits[i >> 5] >> (i & 31u)) & 1u; };
     auto key_of = [&](uint32_t i) -> uint64_t { return is_forced(i) ? 0ull : rank_key(scores[i], i, tl); };
 
+    // the same radix select as topk_kernel's, its passes skipped once the
+    // threshold key stands alone in its digit
     uint64_t prefix = 0ull;
     uint64_t mask = 0ull;
     uint32_t rank = need;
@@ -279,6 +282,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_stream_kernel(
         for (int shift = 56; shift >= 0; shift -= 8) {
             if (tid < 256u) {
                 hist[tid] = 0u;
+            }
+            if (tid == 0u) {
+                s_alone = 0u;
             }
             __syncthreads();
             for (uint32_t i = tid; i < n; i += kTopkThreads) {
@@ -310,6 +316,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_stream_kernel(
                     if (above < rank && rank <= above + c[j]) {
                         s_prefix = prefix | (static_cast<uint64_t>(4u * lane + j) << shift);
                         s_rank = rank - above;
+                        s_alone = c[j] == 1u ? 1u : 0u;
                     }
                     above += c[j];
                 }
@@ -318,15 +325,19 @@ __global__ __launch_bounds__(kTopkThreads) void topk_stream_kernel(
             prefix = s_prefix;
             rank = s_rank;
             mask |= 0xffull << shift;
+            const bool alone = s_alone != 0u;
             __syncthreads();
+            if (alone) {
+                break;
+            }
         }
     }
-    const uint64_t threshold = prefix;
+    const uint64_t threshold = prefix;  // on the bits in `mask`
     auto chosen = [&](uint32_t i) -> bool {
         if (is_forced(i)) {
             return true;
         }
-        return need > 0u && rank_key(scores[i], i, tl) >= threshold;
+        return need > 0u && (rank_key(scores[i], i, tl) & mask) >= threshold;
     };
     const uint32_t seg = (n + kTopkThreads - 1) / kTopkThreads;
     const uint32_t lo = min(n, tid * seg);

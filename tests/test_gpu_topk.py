@@ -114,6 +114,22 @@ def test_topk_beyond_lds_keys(ctx, oracle, n, budget, tie_lower):
     assert got == want
 
 
+@pytest.mark.parametrize("n,budget,tie_lower", [(2048, 257, True), (16384, 1024, False),
+                                                (50000, 2048, True), (300000, 512, False)])
+def test_topk_distinct_scores_early_exit(ctx, oracle, n, budget, tie_lower):
+    """Continuous scores (no ties but the forced ids): the radix select
+    stops once the threshold key stands alone in its digit, in the LDS
+    kernel (n <= 16384) and in the streaming one."""
+    announce(f"distinct scores n={n} budget={budget} tie_lower={tie_lower}")
+    rng = np.random.default_rng(n + 7)
+    s = rng.standard_normal(n).astype(np.float32)
+    want = oracle.pick_topk(s.astype(np.float64), budget, sink=1, tie_lower_index=tie_lower)
+    d = dev(s)
+    torch.cuda.synchronize()
+    got = ctx.topk(d.data_ptr(), n, budget - 1, forced=[0], tie_lower_index=tie_lower)
+    assert got == want
+
+
 def test_engine_selects_over_20000_blocks(oracle):
     """The engine's preview over 20000 blocks of 32 tokens (a 640K-token
     history at --kvmem-block-tokens 32): the device top-k equals the
