@@ -383,3 +383,36 @@ def test_device_plan_other_block_sizes(oracle, geom):
                     s = slots[b]
                     want = oracle.quantize_rows_f16(ty, src[layer, b].reshape(bt, e))
                     assert np.array_equal(pd[s * bt:(s + 1) * bt], want), (layer, which, b)
+
+
+@pytest.mark.parametrize("scorer", [0, 1], ids=["per_token_max", "mean_k"])
+def test_device_plan_query_window_both_scorers(scorer):
+    """apply_retrieval through the device plan from the captured query
+    window (q = NULL: the newest 64 captured rows) with either scorer: 5
+    steps, each after a fresh ubatch of Qcur, leave the same slots, counts
+    and pool bytes as the host-planned engine fed the same rows."""
+    from test_gpu_qwindow import Capture
+    announce(f"device plan from the query window, scorer {scorer}, 5 steps")
+    cap = 40
+    k, v, _ = history(cap, seed=79)
+    types = (kv.TYPE_Q8_0, kv.TYPE_Q4_0)
+    with make_engine(16, 4, *types, scorer=scorer) as dev, \
+            make_engine(16, 4, *types, scorer=scorer, device_plan=0) as ref:
+        caps = (Capture("bf16", 80), Capture("bf16", 80))   # the same rows for both
+        for eng in (dev, ref):
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, cap * T)
+        moved = 0
+        for step in range(5):
+            for eng, cp in zip((dev, ref), caps):
+                cp.ubatch(eng, 64 * step, 64)
+            sd = dev.apply_retrieval(0, 0)
+            sr = ref.apply_retrieval(0, 0)
+            assert sd.pop("device_planned") == 1 and sr.pop("device_planned") == 0, step
+            assert sd == sr, step
+            assert dev.block_slots() == ref.block_slots(), step
+            wd, wr = window(dev, *types, lambda b: T), window(ref, *types, lambda b: T)
+            assert wd.keys() == wr.keys()
+            for key in wd:
+                assert np.array_equal(wd[key], wr[key]), (step, key)
+            moved += sd["n_moved"] + sd["n_staged"]
+        assert moved > 0
