@@ -416,3 +416,47 @@ def test_device_plan_query_window_both_scorers(scorer):
                 assert np.array_equal(wd[key], wr[key]), (step, key)
             moved += sd["n_moved"] + sd["n_staged"]
         assert moved > 0
+
+
+def test_device_plan_transform_growing_tail(oracle):
+    """RoPE 256 + attn_rot through the device plan while the last block is
+    partial and grows between steps: the re-staged tail is RoPE'd at its
+    original positions on its valid rows only; pools equal the host-planned
+    engine's, and the tail equals the oracle's transform of its rows."""
+    from test_gpu_transform import expected_rows
+    announce("device plan, RoPE 256 + attn_rot, partial tail growing 50 -> 90 -> 128 tokens")
+    cap = 32
+    k, v, _ = history(cap, seed=81)
+    types = (kv.TYPE_Q8_0, kv.TYPE_Q4_0)
+    xf = dict(n_rot=256, rope_freq_base=1e6, attn_rot=1)
+    tail = {"n": 50}
+    ntok_of = lambda b: tail["n"] if b == cap - 1 else T  # noqa: E731
+    mand = [0, cap - 1] + list(range(8, 20))   # the tail is always selected
+    with make_engine(16, 4, *types, **xf) as dev, make_engine(16, 4, *types, device_plan=0, **xf) as ref:
+        for eng in (dev, ref):
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, (cap - 1) * T + tail["n"])
+        for step, q in enumerate(queries(82, 3)):
+            if step:
+                for eng in (dev, ref):
+                    eng.append_tokens(40 if step == 1 else 38)
+                tail["n"] = 90 if step == 1 else 128
+            sd = dev.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=mand)
+            sr = ref.apply_retrieval(q.data_ptr(), q.shape[1], mandatory=mand)
+            assert sd.pop("device_planned") == 1 and sr.pop("device_planned") == 0, step
+            assert sd == sr, step
+            if step:
+                assert sd["n_staged"] >= 1  # the grown tail
+            wd, wr = window(dev, *types, ntok_of), window(ref, *types, ntok_of)
+            for key in wd:
+                assert np.array_equal(wd[key], wr[key]), (step, key)
+            theta = oracle.rope_theta(256, 1e6)
+            kb = workloads.to_bits(torch, k)
+            vb = workloads.to_bits(torch, v)
+            b = cap - 1
+            nt = tail["n"]
+            for layer in range(L):
+                want_k = expected_rows(oracle, types[0], kb[layer, b].reshape(T, E)[:nt], D, 256, theta,
+                                       b * T, 256)
+                want_v = expected_rows(oracle, types[1], vb[layer, b].reshape(T, E)[:nt], D, 0, None, b * T, 64)
+                assert np.array_equal(wd[(layer, 0, b)], want_k), (step, layer, "K")
+                assert np.array_equal(wd[(layer, 1, b)], want_v), (step, layer, "V")
