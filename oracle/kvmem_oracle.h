@@ -20,6 +20,10 @@
  *                                   special groups, dequantisation bounds.
  *   ko_score_pertoken_max         : brute force fp64 numpy on tiny shapes,
  *                                   permutation / scaling invariants.
+ *   ko_score_pertoken_max_f32     : the fp64 scorer above and an independent
+ *                                   numpy brute force (1e-5 relative), over
+ *                                   block sub-ranges, thread counts, head
+ *                                   widths, GQA groups, partial tails.
  *   ko_pick_topk                  : the reference kvmem library compiled from
  *                                   its own sources (oracle/_ref), the
  *                                   reference's own unit-test cases, sort-based
@@ -116,11 +120,13 @@ void ko_score_pertoken_max(const float *q, const uint16_t *k,
                            double *layer_scores);
 
 /* Same computation with fp32 accumulation, written for speed: the CPU
- * baseline of the scoring step (parity rests on the fp64 version above).
- * n_threads <= 0 = all. */
+ * baseline of the scoring step and the checker of the full-size scoring
+ * tests.  Fills columns [b_begin, b_end) of layer_scores; block B-1 has
+ * last_block_tokens keys when nonzero.  n_threads <= 0 = all. */
 void ko_score_pertoken_max_f32(const float *q, const uint16_t *k,
                                uint32_t L, uint32_t Tq, uint32_t Hq, uint32_t Hkv,
                                uint32_t D, uint32_t B, uint32_t T,
+                               uint32_t last_block_tokens,
                                uint32_t b_begin, uint32_t b_end,
                                float *layer_scores, int n_threads);
 

@@ -58,7 +58,7 @@ def lib() -> C.CDLL:
                                         C.c_void_p, u32, f64p]
     L.ko_score_pertoken_max_f32.restype = None
     L.ko_score_pertoken_max_f32.argtypes = [f32p, u16p, u32, u32, u32, u32, u32, u32, u32,
-                                            u32, u32, f32p, C.c_int]
+                                            u32, u32, u32, f32p, C.c_int]
     L.ko_combine_layers.restype = None
     L.ko_combine_layers.argtypes = [f64p, u32, u32, C.c_int, f64p]
     L.ko_pick_topk.restype = None
@@ -164,13 +164,19 @@ def score_pertoken_max(q: np.ndarray, k: np.ndarray, last_block_tokens: int = 0,
     return out
 
 
-def score_pertoken_max_f32(q, k, b_begin: int, b_end: int, n_threads: int = 0) -> np.ndarray:
+def score_pertoken_max_f32(q, k, b_begin: int, b_end: int, n_threads: int = 0,
+                           last_block_tokens: int = 0) -> np.ndarray:
+    """fp32 per-token max scorer: q [L,Tq,Hq,D] f32, k [L,B,T,Hkv,D] f16 bits
+    -> [L,B] f32 with columns [b_begin, b_end) filled (the rest NaN)."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     k = np.ascontiguousarray(k, dtype=np.uint16)
     L, Tq, Hq, D = q.shape
-    _, B, T, Hkv, _ = k.shape
+    L2, B, T, Hkv, D2 = k.shape
+    if L != L2 or D != D2 or Hq % Hkv or not 0 <= b_begin <= b_end <= B or last_block_tokens > T:
+        raise ValueError("score_pertoken_max_f32: shapes or block range do not match")
     out = np.full((L, B), np.nan, dtype=np.float32)
-    lib().ko_score_pertoken_max_f32(q, k, L, Tq, Hq, Hkv, D, B, T, b_begin, b_end, out, n_threads)
+    lib().ko_score_pertoken_max_f32(q, k, L, Tq, Hq, Hkv, D, B, T, last_block_tokens, b_begin, b_end,
+                                    out, n_threads)
     return out
 
 

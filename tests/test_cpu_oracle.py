@@ -12,7 +12,11 @@ oracle/kvmem_oracle_quant.c):
 Half precision: f16 -> f32 over all 65536 codes and f32 -> f16 on edge and
 random values against numpy's IEEE conversion.
 Per-token max scorer (fp64): numpy brute force on tiny shapes, permutation
-and scaling invariants.
+and scaling invariants.  Its fp32 twin (the full-size tests' checker): the
+fp64 scorer and the brute force within 1e-5, over block sub-ranges, thread
+counts, head_dim 128 / 256, GQA groups and partial last blocks; GQA-map,
+block-offset, layer-stride and partial-tail slips planted through its inputs
+fail the same comparison.
 Top-k: the reference library's selections (tests/golden/select_sequences
 .json, ties to the higher id) and a sort-based brute force (both tie rules).
 """
@@ -224,6 +228,83 @@ def test_scorer_invariants(oracle):
     assert np.allclose(oracle.score_pertoken_max(q * 2, k), 2 * base, rtol=1e-12)
     swapped = q[:, :, [1, 0, 3, 2]].copy()        # heads swapped inside each group
     assert np.allclose(oracle.score_pertoken_max(swapped, k), base, rtol=1e-12)
+
+
+# ------------------------------------------------ fp32 scorer (full-size checker)
+def _f32_inputs(seed, L, Tq, Hq, Hkv, D, B, T):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((L, Tq, Hq, D)).astype(np.float32)
+    k = (rng.standard_normal((L, B, T, Hkv, D)) + rng.normal(0, 0.3, (L, B, 1, 1, D)))
+    return q, k.astype(np.float16).view(np.uint16)
+
+
+def _f32_close(got, want, rtol=1e-5):
+    """fp32 accumulation over D <= 256 products: 1e-5 of the score's scale."""
+    scale = np.maximum(np.abs(want), 1e-3)
+    return bool(np.all(np.abs(got.astype(np.float64) - want) <= rtol * scale))
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,last", [(256, 24, 4, 0), (256, 24, 4, 37), (128, 8, 2, 0),
+                                          (128, 6, 6, 91)])
+def test_scorer_f32_vs_fp64_and_brute_force(oracle, D, Hq, Hkv, last):
+    """The fp32 scorer the full-size tests check the device against equals
+    the fp64 scorer and a numpy brute force to fp32 accumulation error, on
+    128-token blocks with a partial last block."""
+    L, Tq, B, T = 2, 4, 5, 128
+    q, k = _f32_inputs(21 + D + last, L, Tq, Hq, Hkv, D, B, T)
+    got = oracle.score_pertoken_max_f32(q, k, 0, B, last_block_tokens=last)
+    assert not np.isnan(got).any()
+    assert _f32_close(got, oracle.score_pertoken_max(q, k, last))
+    assert _f32_close(got, brute_scores(q, k, last))
+
+
+def test_scorer_f32_block_range_and_threads(oracle):
+    """Columns outside [b_begin, b_end) stay untouched; inside they equal the
+    full-range call bit for bit, for 1, 3 and all threads (one block is one
+    thread's work, so the sums never depend on the split)."""
+    L, Tq, Hq, Hkv, D, B, T = 3, 3, 24, 4, 256, 7, 128
+    q, k = _f32_inputs(5, L, Tq, Hq, Hkv, D, B, T)
+    full = oracle.score_pertoken_max_f32(q, k, 0, B, n_threads=1, last_block_tokens=50)
+    for threads in (1, 3, 0):
+        assert np.array_equal(oracle.score_pertoken_max_f32(q, k, 0, B, threads, 50), full)
+        part = oracle.score_pertoken_max_f32(q, k, 2, 6, threads, 50)
+        assert np.isnan(part[:, :2]).all() and np.isnan(part[:, 6:]).all()
+        assert np.array_equal(part[:, 2:6], full[:, 2:6])
+        tail = oracle.score_pertoken_max_f32(q, k, 6, 7, threads, 50)
+        assert np.array_equal(tail[:, 6], full[:, 6])
+    assert np.isnan(oracle.score_pertoken_max_f32(q, k, 3, 3)).all()
+    with pytest.raises(ValueError):
+        oracle.score_pertoken_max_f32(q, k, 4, 8)
+
+
+def test_scorer_f32_checks_reject_planted_slips(oracle):
+    """The comparison the fp32 scorer passes above fails for the slips a
+    rewrite of it could make.  Each slip is planted by feeding the correct
+    scorer the inputs that make it compute the wrong thing:
+      - GQA map hq -> hq % Hkv instead of hq // g;
+      - keys read one block further on (a block-offset slip);
+      - the layer stride off by one block (layer l reads layer l's keys
+        starting one block early);
+      - the partial last block scored over all T rows."""
+    L, Tq, Hq, Hkv, D, B, T, last = 2, 4, 24, 4, 256, 5, 128, 40
+    g = Hq // Hkv
+    q, k = _f32_inputs(77, L, Tq, Hq, Hkv, D, B, T)
+    kf = k.view(np.float16).copy()
+    kf[:, B - 1, last:] = 8.0          # rows past the tail: large, never to be scored
+    k = kf.view(np.uint16)
+    want = oracle.score_pertoken_max(q, k, last)
+    assert _f32_close(oracle.score_pertoken_max_f32(q, k, 0, B, last_block_tokens=last), want)
+
+    perm = [gi * Hkv + h for h in range(Hkv) for gi in range(g)]
+    slips = {
+        "gqa": (q[:, :, perm].copy(), k, last),
+        "block_offset": (q, np.roll(k, -1, axis=1).copy(), last),
+        "layer_stride": (q, np.roll(k.reshape(L * B, T, Hkv, D), 1, axis=0).reshape(k.shape).copy(), last),
+        "partial_tail": (q, k, 0),
+    }
+    for name, (qq, kk, lt) in slips.items():
+        got = oracle.score_pertoken_max_f32(qq, kk, 0, B, last_block_tokens=lt)
+        assert not _f32_close(got, want), name
 
 
 def test_combine_layers_modes(oracle):
