@@ -67,6 +67,26 @@ typedef struct kvmem_row_range {
     int32_t end;
 } kvmem_row_range;
 
+/* An attention view (llama_kvmem_attention_view, src/adapter/
+ * llama-kvmem-hooks.h:143-148): the blocks attention reads -- every block
+ * holding a pool slot, ascending -- with the attention epoch and the history
+ * rows it was taken at.  valid = 1 when every one of them has all its rows
+ * in the pool (and, for a canonical view, the i-th of them sits in slot i).
+ * The attention epoch moves whenever pool contents or residency change (an
+ * apply that stages, moves or evicts, a truncate, a new pool or history, a
+ * failed apply); rows appended do not move it (the adapter's
+ * attention_epoch_, llama-memory-kvmem.cpp:630-1495, 2735).  The caller
+ * owns `blocks` (capacity entries); calls that fill a view set n_blocks
+ * always and the ids when they fit. */
+typedef struct kvmem_attention_view {
+    uint64_t epoch;
+    uint32_t rows;
+    int32_t valid;
+    uint32_t n_blocks;
+    uint32_t capacity;
+    uint32_t *blocks;
+} kvmem_attention_view;
+
 /* ----------------------------------------------------------- host store */
 
 typedef struct kvmem_store kvmem_store;
@@ -117,6 +137,48 @@ KVMEM_HIP_API int kvmem_store_commit_resident(kvmem_store *s, const uint32_t *se
 KVMEM_HIP_API int kvmem_store_blocks_overlapping(const kvmem_store *s, const kvmem_row_range *ranges,
                                                  uint32_t n_ranges, int32_t force_pos,
                                                  uint32_t *out, uint32_t capacity, uint32_t *n_out);
+
+/* Continuation checks of the two-phase API over the store alone, where a
+ * block holding a slot counts as complete (no device).  The store's
+ * attention epoch moves with every apply that changes the working set and
+ * every truncate that cuts rows; kvmem_store_register_append and
+ * kvmem_store_append_resident leave it.  These restate the adapter's
+ * attention_view / selection_fits / commit_unchanged / can_append
+ * (llama-memory-kvmem.cpp:2982-3024, 3069-3096), which the engine calls
+ * below exports with the pool's own state. */
+KVMEM_HIP_API uint64_t kvmem_store_epoch(const kvmem_store *s);
+/* Rows that enter the pool as they are written (llama.cpp's decode writing
+ * K/V cells): register_append, and every block the rows touch that has no
+ * slot takes one from the LIFO free list (prepare_working_set with the
+ * working set pinned, llama-memory-kvmem.cpp:1256-1337).  ERR_NOMEM (no
+ * change) when the free list is short. */
+KVMEM_HIP_API int kvmem_store_append_resident(kvmem_store *s, uint32_t n_tokens);
+KVMEM_HIP_API int kvmem_store_attention_view(const kvmem_store *s, int canonical,
+                                             kvmem_attention_view *view);
+/* 1 when the selection (epoch, rows, ids) is current, keeps every listed
+ * mandatory id, and the rows up to end plus generation_rows fit the slot
+ * pool beside it; else 0 (llama_kvmem_selection_fits, llama-kvmem-hooks.h:
+ * 158; llama-memory-kvmem.cpp:3069-3084). */
+KVMEM_HIP_API int kvmem_store_selection_fits(const kvmem_store *s, const uint32_t *mandatory,
+                                             uint32_t n_mandatory, uint64_t epoch, uint32_t rows,
+                                             const uint32_t *sel, uint32_t n_sel, uint32_t end,
+                                             uint32_t generation_rows);
+/* 1 and the selection committed as the working set when the view taken
+ * before is still current, the canonical view now equals the selection and
+ * keeps every block of the view before; else 0, nothing changed
+ * (llama_kvmem_commit_unchanged, llama-kvmem-hooks.h:159;
+ * llama-memory-kvmem.cpp:3086-3096). */
+KVMEM_HIP_API int kvmem_store_commit_unchanged(kvmem_store *s, const kvmem_attention_view *before,
+                                               uint64_t epoch, uint32_t rows, const uint32_t *sel,
+                                               uint32_t n_sel);
+/* 1 when rows up to end plus generation_rows can be decoded onto the pool
+ * as it is; *reason (static string) gets the adapter's reason: "same_query"
+ * / "all_resident" or "invalid_boundary", "coverage_or_layout",
+ * "partial_tail_missing", "history_not_resident", "selection_budget",
+ * "prefill_pressure", "insufficient_slots" (llama_kvmem_can_append,
+ * llama-kvmem-hooks.h:156; llama-memory-kvmem.cpp:3002-3024). */
+KVMEM_HIP_API int kvmem_store_can_append(const kvmem_store *s, uint32_t end, uint32_t generation_rows,
+                                         int all_history, const char **reason);
 
 /* ------------------------------------------------------ reselect engine */
 
@@ -343,6 +405,62 @@ KVMEM_HIP_API int kvmem_engine_preview_meank(kvmem_engine *e, const float *q_sum
 KVMEM_HIP_API int kvmem_engine_apply_retrieval(kvmem_engine *e, const void *q, int32_t q_type,
                                                uint32_t n_q_tokens, const uint32_t *mandatory,
                                                uint32_t n_mandatory, kvmem_plan_stats *stats);
+/* ------------------------------------------- continuation (two-phase API)
+ * The calls a caller makes between preview and apply to skip or check an
+ * apply (llama-kvmem-hooks.h:155-161; the multimodal server's cached-query
+ * and unchanged-selection paths, tools/kvmem-multimodal-server.h:309-389).
+ * Selections are checked against the engine's epoch and rows as apply
+ * checks them; views against the attention epoch. */
+
+/* Rows the caller's decode writes into the pool itself, as llama.cpp writes
+ * a batch's K/V cells (the adapter's prepare_working_set with the working
+ * set pinned, llama-memory-kvmem.cpp:1256-1337): the history grows by
+ * n_new_tokens (the caller writes them there too), and every block they
+ * touch that holds no slot takes the next one of the free list --
+ * kvmem_engine_block_slots tells where; row t of block b goes to cell
+ * slot*block_tokens + (t - b*block_tokens) of every layer's K and V pool
+ * tensor, in the pool's row format.  In canonical layout the new blocks
+ * continue the window's slot order.  A partial tail that held no slot gets
+ * one but its older rows are not in the pool: the next apply stages it
+ * again.  Moves the selection epoch, not the attention epoch.  ERR_NOMEM
+ * (nothing changed) when the free list is short. */
+KVMEM_HIP_API int kvmem_engine_append_resident(kvmem_engine *e, uint32_t n_new_tokens);
+KVMEM_HIP_API uint64_t kvmem_engine_attention_epoch(const kvmem_engine *e);
+/* llama_kvmem_get_attention_view (llama-kvmem-hooks.h:155;
+ * llama-memory-kvmem.cpp:2982-3000): a block holding a slot is complete
+ * unless it is a partial tail whose newer rows wait to be staged.  The
+ * pool has no cells outside blocks, so the reference's check of extra live
+ * cells has nothing to count here. */
+KVMEM_HIP_API int kvmem_engine_attention_view(const kvmem_engine *e, int canonical,
+                                              kvmem_attention_view *view);
+/* llama_kvmem_selection_fits (llama-kvmem-hooks.h:158; llama-memory-kvmem.cpp:
+ * 3069-3084): 1 when the selection is current (epoch, rows), end >= rows,
+ * it keeps every block kvmem_engine_retrieval_mandatory names (a selector
+ * that trimmed a mandatory range to its budget made a plan unfit for
+ * continuation), and its blocks plus those rows [rows, end +
+ * generation_rows) still need fit the slot pool; else 0. */
+KVMEM_HIP_API int kvmem_engine_selection_fits(const kvmem_engine *e, uint64_t epoch, uint32_t rows,
+                                              const uint32_t *sel, uint32_t n_sel, uint32_t end,
+                                              uint32_t generation_rows);
+/* llama_kvmem_commit_unchanged (llama-kvmem-hooks.h:159; llama-memory-kvmem.cpp:
+ * 3086-3096): when the view taken before is valid and still current (same
+ * attention epoch, no more rows than now), the selection is current, the
+ * canonical view now is valid and equals it and keeps every block of the
+ * view before, the selection becomes the working set with no device work
+ * (commit_resident_selection) and 1 is returned; else 0 and nothing
+ * changes.  A caller that gets 1 skips kvmem_engine_apply. */
+KVMEM_HIP_API int kvmem_engine_commit_unchanged(kvmem_engine *e, const kvmem_attention_view *before,
+                                                uint64_t epoch, uint32_t rows, const uint32_t *sel,
+                                                uint32_t n_sel);
+/* llama_kvmem_commit_resident (llama-kvmem-hooks.h:161; llama-memory-kvmem.cpp:
+ * 3098-3102): commit the blocks now in the pool as the working set when the
+ * view (canonical or not) is valid; 1 on success, 0 otherwise. */
+KVMEM_HIP_API int kvmem_engine_commit_resident(kvmem_engine *e, int canonical);
+/* llama_kvmem_can_append (llama-kvmem-hooks.h:156; llama-memory-kvmem.cpp:
+ * 3002-3024): as kvmem_store_can_append, over the engine's pool. */
+KVMEM_HIP_API int kvmem_engine_can_append(const kvmem_engine *e, uint32_t end, uint32_t generation_rows,
+                                          int all_history, const char **reason);
+
 /* Scores of the last preview (host copy, block count entries). */
 KVMEM_HIP_API int kvmem_engine_scores(kvmem_engine *e, float *out, uint32_t n);
 

@@ -299,6 +299,23 @@ bool KvMemStore::commit_resident_selection(const std::vector<uint32_t> &ids) {
     return true;
 }
 
+bool KvMemStore::prefill_needs_offload(uint32_t resident_tokens, uint32_t incoming_tokens,
+                                       uint32_t pool_tokens) const {
+    if (incoming_tokens == 0 || pool_tokens == 0) {
+        return false;
+    }
+    const uint64_t next = static_cast<uint64_t>(resident_tokens) + incoming_tokens;
+    if (next > pool_tokens) {
+        return true;
+    }
+    double r = cfg_.gpu_high_watermark;
+    if (r <= 0.0 || r > 1.0) {
+        r = 1.0;
+    }
+    const uint32_t high = std::max(static_cast<uint32_t>(pool_tokens * r), cfg_.block_tokens);
+    return next > high;
+}
+
 void KvMemStore::clear_working_set() {
     for (Block &b : blocks_) {
         b.in_working_set = false;
@@ -385,6 +402,46 @@ bool KvMemRuntime::commit_resident_selection(const std::vector<uint32_t> &select
     return true;
 }
 
+bool KvMemRuntime::append_resident(uint32_t n_tokens, std::vector<uint32_t> *placed) {
+    if (placed) {
+        placed->clear();
+    }
+    if (pending_) {
+        return false;
+    }
+    if (n_tokens == 0) {
+        return true;
+    }
+    // blocks the new rows [t0, t0 + n_tokens) touch: the partial tail, then
+    // the new ones
+    const uint32_t bt = store_.config().block_tokens;
+    const uint32_t t0 = store_.total_tokens();
+    const auto &bl = store_.blocks();
+    uint32_t need = 0;
+    const bool tail_partial = !bl.empty() && bl.back().n_tokens < bt;
+    if (tail_partial && bl.back().gpu_slot < 0) {
+        ++need;
+    }
+    const uint32_t into_tail = tail_partial ? std::min(bt - bl.back().n_tokens, n_tokens) : 0u;
+    need += (n_tokens - into_tail + bt - 1) / bt;
+    if (need > backend_->free_slot_count()) {
+        return false;
+    }
+    store_.register_append(n_tokens);
+    for (const Block &b : store_.blocks()) {
+        if (b.orig_pos_end() <= t0 || b.gpu_slot >= 0) {
+            continue;
+        }
+        const int32_t slot = backend_->alloc_gpu_slot();
+        store_.set_block_tier(b.block_id, Tier::GPU);
+        store_.set_block_gpu_slot(b.block_id, slot);
+        if (placed) {
+            placed->push_back(b.block_id);
+        }
+    }
+    return true;
+}
+
 void KvMemRuntime::spill_outgoing() {
     if (!pending_) {
         return;
@@ -425,6 +482,143 @@ void KvMemRuntime::admit_incoming() {
 void KvMemRuntime::finish_reselect() {
     spill_outgoing();
     admit_incoming();
+}
+
+// ------------------------------------------------- continuation checks
+
+namespace {
+
+bool holds(const std::vector<uint32_t> &sorted, uint32_t id) {
+    return std::binary_search(sorted.begin(), sorted.end(), id);
+}
+
+// gpu_kv_complete (llama-memory-kvmem.cpp:2964-2980) for block id.
+bool block_complete(const KvMemStore &s, const PoolState &p, uint64_t id) {
+    if (id >= s.block_count()) {
+        return false;
+    }
+    const Block &b = s.blocks()[id];
+    return b.gpu_slot >= 0 && b.tier == Tier::GPU && b.n_tokens > 0 && p.complete && p.complete(b);
+}
+
+}  // namespace
+
+AttentionView attention_view(const KvMemStore &s, const PoolState &p, bool canonical) {
+    AttentionView v;
+    v.epoch = p.epoch;
+    v.rows = s.total_tokens();
+    v.valid = s.config().optimize_stage_in;
+    for (const Block &b : s.blocks()) {
+        if (b.gpu_slot < 0 || b.n_tokens == 0) {
+            continue;
+        }
+        if ((canonical && b.gpu_slot != static_cast<int32_t>(v.blocks.size())) ||
+            !block_complete(s, p, b.block_id)) {
+            v.valid = false;
+        }
+        v.blocks.push_back(b.block_id);
+    }
+    return v;
+}
+
+bool selection_fits(const KvMemStore &s, const PoolState &p, const std::vector<uint32_t> &mandatory,
+                    uint64_t sel_epoch, uint32_t sel_rows, const std::vector<uint32_t> &sel,
+                    uint32_t end, uint32_t generation_rows) {
+    if (sel_epoch != p.epoch || sel_rows != s.total_tokens() || end < sel_rows) {
+        return false;
+    }
+    std::vector<uint32_t> ids(sel);
+    std::sort(ids.begin(), ids.end());
+    // a selector that trimmed a mandatory range to its budget made a plan
+    // unfit for continuation
+    for (uint32_t id : mandatory) {
+        if (!holds(ids, id)) {
+            return false;
+        }
+    }
+    const uint64_t bt = s.config().block_tokens;
+    const uint64_t final_block = (static_cast<uint64_t>(end) + generation_rows + bt - 1) / bt;
+    const uint64_t first = sel_rows / bt;
+    if (final_block < first || final_block - first > p.n_slots) {
+        return false;
+    }
+    uint64_t count = ids.size();
+    for (uint64_t id = first; id < final_block; ++id) {
+        if (!holds(ids, static_cast<uint32_t>(id))) {
+            ++count;
+        }
+    }
+    return count <= p.n_slots;
+}
+
+bool commit_unchanged(KvMemRuntime &rt, const PoolState &p, const AttentionView &before,
+                      uint64_t sel_epoch, uint32_t sel_rows, const std::vector<uint32_t> &sel) {
+    const KvMemStore &s = rt.store();
+    if (!before.valid || before.epoch != p.epoch || before.rows > s.total_tokens() ||
+        sel_epoch != p.epoch || sel_rows != s.total_tokens()) {
+        return false;
+    }
+    const AttentionView after = attention_view(s, p, true);
+    if (!after.valid || after.blocks != sel) {
+        return false;
+    }
+    for (uint32_t id : before.blocks) {
+        if (!holds(after.blocks, id)) {
+            return false;
+        }
+    }
+    return rt.commit_resident_selection(sel);
+}
+
+bool commit_resident(KvMemRuntime &rt, const PoolState &p, bool canonical) {
+    const AttentionView v = attention_view(rt.store(), p, canonical);
+    return v.valid && rt.commit_resident_selection(v.blocks);
+}
+
+bool can_append(const KvMemStore &s, const PoolState &p, uint32_t end, uint32_t generation_rows,
+                bool all_history, const char **reason) {
+    const char *why = nullptr;
+    const uint64_t bt = s.config().block_tokens;
+    const AttentionView v = attention_view(s, p, all_history);
+    uint32_t resident_tokens = 0;
+    for (const Block &b : s.blocks()) {
+        if (b.gpu_slot >= 0) {
+            resident_tokens += b.n_tokens;
+        }
+    }
+    const uint64_t end_blocks = (static_cast<uint64_t>(end) + bt - 1) / bt;
+    const uint64_t final_blocks = (static_cast<uint64_t>(end) + generation_rows + bt - 1) / bt;
+    if (end < s.total_tokens()) {
+        why = "invalid_boundary";
+    } else if (!v.valid) {
+        why = "coverage_or_layout";
+    } else if (v.rows % bt && !block_complete(s, p, v.rows / bt)) {
+        why = "partial_tail_missing";
+    } else if (all_history && v.blocks.size() != s.block_count()) {
+        why = "history_not_resident";
+    } else if (all_history && s.budget_blocks() && end_blocks > s.budget_blocks()) {
+        why = "selection_budget";
+    } else if (all_history &&
+               s.prefill_needs_offload(resident_tokens, end - v.rows,
+                                       static_cast<uint32_t>(static_cast<uint64_t>(p.n_slots) * bt))) {
+        why = "prefill_pressure";
+    } else if (final_blocks > static_cast<uint64_t>(p.n_slots) + s.block_count()) {
+        why = "insufficient_slots";
+    } else {
+        uint64_t needed = 0;
+        for (uint64_t id = v.rows / bt; id < final_blocks; ++id) {
+            if (id >= s.block_count() || s.blocks()[id].gpu_slot < 0) {
+                ++needed;
+            }
+        }
+        if (needed > p.n_free) {
+            why = "insufficient_slots";
+        }
+    }
+    if (reason) {
+        *reason = why ? why : (all_history ? "all_resident" : "same_query");
+    }
+    return why == nullptr;
 }
 
 }  // namespace kvmem_amd

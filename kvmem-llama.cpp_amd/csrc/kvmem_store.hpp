@@ -73,6 +73,9 @@ struct StoreConfig {
     // false forces every selected block to be staged in again
     // (optimize_stage_in, kvmem_store.hpp:229-231).
     bool optimize_stage_in = true;
+    // Share of the pool's tokens above which a prefill must offload
+    // (gpu_high_watermark, kvmem_store.hpp:311).
+    double gpu_high_watermark = 0.95;
 };
 
 // Blocks charged before the score fill of pick_topk: sink, mandatory
@@ -130,6 +133,12 @@ public:
     std::vector<uint32_t> blocks_overlapping(const std::vector<std::pair<int32_t, int32_t>> &ranges,
                                              int32_t force_pos) const;
 
+    // kvmem_store.cpp:340-351 with gpu_high_watermark_tokens (:320-327):
+    // whether incoming_tokens more rows over resident_tokens overflow the
+    // pool's pool_tokens or its high watermark.
+    bool prefill_needs_offload(uint32_t resident_tokens, uint32_t incoming_tokens,
+                               uint32_t pool_tokens) const;
+
     // kvmem_store.cpp:250-277 with optimize_stage_out: leaving the GPU
     // clears the slot.
     void set_block_tier(uint32_t id, Tier tier);
@@ -158,6 +167,9 @@ public:
     virtual ~KvMemBackend() = default;
     virtual int32_t alloc_gpu_slot() { return -1; }
     virtual void free_gpu_slot(int32_t /*slot*/) {}
+    // Slots alloc_gpu_slot can still hand out (the adapter's
+    // free_slots_.size()).
+    virtual uint32_t free_slot_count() const { return 0; }
     // A block entered `slot` (called once per staged block, ascending ids).
     virtual void block_staged_in(uint32_t /*block_id*/, int32_t /*slot*/) {}
 };
@@ -170,6 +182,7 @@ public:
     explicit SlotPool(uint32_t n_slots);
     int32_t alloc_gpu_slot() override;
     void free_gpu_slot(int32_t slot) override;
+    uint32_t free_slot_count() const override { return n_free(); }
     uint32_t n_slots() const { return n_slots_; }
     uint32_t n_free() const { return static_cast<uint32_t>(free_.size()); }
     void reset();
@@ -198,6 +211,14 @@ public:
                                            const Ranker &ranker = nullptr) const;
     Plan prepare_selection(const std::vector<uint32_t> &selected);
     bool commit_resident_selection(const std::vector<uint32_t> &selected);
+    // Rows the caller writes into the pool itself, as llama.cpp's decode
+    // writes the K/V cells of a batch: register_append, then every block
+    // the new rows touch that has no slot gets one from the free list
+    // (prepare_working_set with the working set pinned,
+    // llama-memory-kvmem.cpp:1256-1337).  Refused (false, nothing changed)
+    // while a plan is pending or when the free list is short; `placed`
+    // receives the blocks given a slot.
+    bool append_resident(uint32_t n_tokens, std::vector<uint32_t> *placed);
     void spill_outgoing();
     void admit_incoming();
     void finish_reselect();
@@ -209,5 +230,52 @@ private:
     bool pending_ = false;
     std::vector<int32_t> pending_frees_;
 };
+
+// ------------------------------------------------- continuation checks
+
+// llama_kvmem_attention_view (src/adapter/llama-kvmem-hooks.h:143-148): the
+// blocks attention reads (every block holding a pool slot, in block order),
+// the attention epoch and history rows it was taken at, and whether every
+// one of them has all its rows in the pool (and, canonical, block i of the
+// view in slot i).
+struct AttentionView {
+    uint64_t epoch = 0;
+    uint32_t rows = 0;
+    bool valid = false;
+    std::vector<uint32_t> blocks;
+};
+
+// What the checks need of the pool beside the store: the attention epoch
+// (bumped whenever pool contents or residency change, never by appended
+// rows: the adapter's attention_epoch_), the slot count and free slots, and
+// whether a block's rows are all in the pool (gpu_kv_complete,
+// llama-memory-kvmem.cpp:2964-2980; called for blocks holding a slot).
+struct PoolState {
+    uint64_t epoch = 0;
+    uint32_t n_slots = 0;
+    uint32_t n_free = 0;
+    std::function<bool(const Block &)> complete;
+};
+
+// attention_view (llama-memory-kvmem.cpp:2982-3000).
+AttentionView attention_view(const KvMemStore &s, const PoolState &p, bool canonical);
+// selection_fits (llama-memory-kvmem.cpp:3069-3084): the selection is
+// current, keeps every mandatory block, and with the rows up to end plus
+// generation_rows fits the slot pool.
+bool selection_fits(const KvMemStore &s, const PoolState &p, const std::vector<uint32_t> &mandatory,
+                    uint64_t sel_epoch, uint32_t sel_rows, const std::vector<uint32_t> &sel,
+                    uint32_t end, uint32_t generation_rows);
+// commit_unchanged (llama-memory-kvmem.cpp:3086-3096): the attention view
+// taken before (same epoch, no more rows) is kept by the current one, which
+// equals the selection; then commit_resident_selection.
+bool commit_unchanged(KvMemRuntime &rt, const PoolState &p, const AttentionView &before,
+                      uint64_t sel_epoch, uint32_t sel_rows, const std::vector<uint32_t> &sel);
+// commit_resident (llama-memory-kvmem.cpp:3098-3102).
+bool commit_resident(KvMemRuntime &rt, const PoolState &p, bool canonical);
+// can_append (llama-memory-kvmem.cpp:3002-3024): whether rows up to end
+// plus generation_rows can be decoded onto the current pool without a
+// reselect; *reason receives the adapter's reason string.
+bool can_append(const KvMemStore &s, const PoolState &p, uint32_t end, uint32_t generation_rows,
+                bool all_history, const char **reason);
 
 }  // namespace kvmem_amd

@@ -39,6 +39,8 @@ public:
     explicit RecordingSlots(uint32_t n) : pool_(n) {}
     int32_t alloc_gpu_slot() override { return pool_.alloc_gpu_slot(); }
     void free_gpu_slot(int32_t s) override { pool_.free_gpu_slot(s); }
+    uint32_t free_slot_count() const override { return pool_.n_free(); }
+    uint32_t n_slots() const { return pool_.n_slots(); }
     void block_staged_in(uint32_t id, int32_t slot) override {
         staged_ids.push_back(id);
         staged_slots.push_back(static_cast<uint32_t>(slot));
@@ -103,6 +105,33 @@ bool copy_ranges(const kvmem_row_range *r, uint32_t n, std::vector<std::pair<int
     return true;
 }
 
+// An attention view into the ABI struct: header fields always, the block
+// ids when they fit the caller's capacity (ERR_INVALID otherwise).
+int export_view(const kvmem_amd::AttentionView &v, kvmem_attention_view *out) {
+    out->epoch = v.epoch;
+    out->rows = v.rows;
+    out->valid = v.valid ? 1 : 0;
+    out->n_blocks = static_cast<uint32_t>(v.blocks.size());
+    if (v.blocks.size() > out->capacity || (!v.blocks.empty() && !out->blocks)) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    std::copy(v.blocks.begin(), v.blocks.end(), out->blocks);
+    return KVMEM_HIP_OK;
+}
+
+// The ABI struct back into a view (its first n_blocks ids); false when the
+// ids cannot be read.
+bool import_view(const kvmem_attention_view *in, kvmem_amd::AttentionView &v) {
+    if (!in || (in->n_blocks && !in->blocks) || in->n_blocks > in->capacity) {
+        return false;
+    }
+    v.epoch = in->epoch;
+    v.rows = in->rows;
+    v.valid = in->valid != 0;
+    v.blocks.assign(in->blocks, in->blocks + in->n_blocks);
+    return true;
+}
+
 StoreConfig store_config(uint32_t block_tokens, uint32_t budget_blocks, uint32_t sink,
                          uint32_t recent, bool tie_lower) {
     StoreConfig c;
@@ -121,7 +150,19 @@ StoreConfig store_config(uint32_t block_tokens, uint32_t budget_blocks, uint32_t
 struct kvmem_store {
     RecordingSlots slots;
     KvMemRuntime rt;
+    // attention epoch: bumped by applies that change the working set and by
+    // cuts, never by appended rows (the adapter's attention_epoch_)
+    uint64_t epoch = 1;
     kvmem_store(const StoreConfig &c, uint32_t n_slots) : slots(n_slots), rt(c, &slots) {}
+    // The store alone has no device: a block holding a slot is complete.
+    kvmem_amd::PoolState pool_state() const {
+        kvmem_amd::PoolState p;
+        p.epoch = epoch;
+        p.n_slots = slots.n_slots();
+        p.n_free = slots.n_free();
+        p.complete = [](const Block &b) { return b.tier == Tier::GPU; };
+        return p;
+    }
 };
 
 extern "C" {
@@ -159,8 +200,66 @@ int kvmem_store_truncate_to(kvmem_store *s, uint32_t token_pos) {
     if (!s) {
         return KVMEM_HIP_ERR_INVALID;
     }
+    if (token_pos < s->rt.store().total_tokens()) {
+        ++s->epoch;
+    }
     s->rt.truncate_to(token_pos);
     return KVMEM_HIP_OK;
+}
+
+int kvmem_store_append_resident(kvmem_store *s, uint32_t n_tokens) {
+    if (!s) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    return s->rt.append_resident(n_tokens, nullptr) ? KVMEM_HIP_OK : KVMEM_HIP_ERR_NOMEM;
+}
+
+uint64_t kvmem_store_epoch(const kvmem_store *s) {
+    return s ? s->epoch : 0;
+}
+
+int kvmem_store_attention_view(const kvmem_store *s, int canonical, kvmem_attention_view *view) {
+    if (!s || !view) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    return export_view(kvmem_amd::attention_view(s->rt.store(), s->pool_state(), canonical != 0), view);
+}
+
+int kvmem_store_selection_fits(const kvmem_store *s, const uint32_t *mandatory, uint32_t n_mandatory,
+                               uint64_t epoch, uint32_t rows, const uint32_t *sel, uint32_t n_sel,
+                               uint32_t end, uint32_t generation_rows) {
+    if (!s || (n_mandatory && !mandatory) || (n_sel && !sel)) {
+        return 0;
+    }
+    return kvmem_amd::selection_fits(s->rt.store(), s->pool_state(),
+                                     std::vector<uint32_t>(mandatory, mandatory + n_mandatory), epoch,
+                                     rows, std::vector<uint32_t>(sel, sel + n_sel), end, generation_rows)
+               ? 1
+               : 0;
+}
+
+int kvmem_store_commit_unchanged(kvmem_store *s, const kvmem_attention_view *before, uint64_t epoch,
+                                 uint32_t rows, const uint32_t *sel, uint32_t n_sel) {
+    kvmem_amd::AttentionView v;
+    if (!s || (n_sel && !sel) || !import_view(before, v)) {
+        return 0;
+    }
+    return kvmem_amd::commit_unchanged(s->rt, s->pool_state(), v, epoch, rows,
+                                       std::vector<uint32_t>(sel, sel + n_sel))
+               ? 1
+               : 0;
+}
+
+int kvmem_store_can_append(const kvmem_store *s, uint32_t end, uint32_t generation_rows, int all_history,
+                           const char **reason) {
+    if (!s) {
+        if (reason) *reason = "invalid_boundary";
+        return 0;
+    }
+    return kvmem_amd::can_append(s->rt.store(), s->pool_state(), end, generation_rows, all_history != 0,
+                                 reason)
+               ? 1
+               : 0;
 }
 
 uint32_t kvmem_store_block_count(const kvmem_store *s) {
@@ -208,6 +307,9 @@ int kvmem_store_apply(kvmem_store *s, const uint32_t *sel, uint32_t n_sel, uint3
         s->rt = rt_before;
         s->slots = slots_before;
         return KVMEM_HIP_ERR_NOMEM;
+    }
+    if (!p.stage_in.empty() || !p.stage_out.empty()) {
+        ++s->epoch;  // the working set changed (apply_plan_to_kv, llama-memory-kvmem.cpp:785)
     }
     if (stage_in) {
         std::copy(p.stage_in.begin(), p.stage_in.end(), stage_in);
@@ -301,7 +403,8 @@ struct kvmem_engine {
     kvmem_hip_transform xf{};  // cache row transform (unused when has_xf is false)
     std::vector<float> theta;  // RoPE pair frequencies
     bool has_xf = false;
-    uint64_t epoch = 1;
+    uint64_t epoch = 1;        // selection epoch: history rows or contents changed
+    uint64_t attn_epoch = 1;   // attention epoch: pool contents or residency changed
     std::string err;
     // request span / turn spans (llama-memory-kvmem.h:164-170, .cpp:2938-2948)
     int32_t query_begin = -1;
@@ -351,6 +454,20 @@ struct kvmem_engine {
     int fail_ctx(int code, const char *what) {
         err = std::string(what) + ": " + kvmem_hip_last_error(ctx);
         return code;
+    }
+
+    // The pool as the continuation checks see it: a block holding a slot is
+    // complete unless it is a partial tail whose newer rows are not staged.
+    kvmem_amd::PoolState pool_state() const {
+        kvmem_amd::PoolState ps;
+        ps.epoch = attn_epoch;
+        ps.n_slots = n_slots;
+        ps.n_free = slots.n_free();
+        const int64_t dirty = dirty_tail;
+        ps.complete = [dirty](const Block &b) {
+            return b.tier == Tier::GPU && static_cast<int64_t>(b.block_id) != dirty;
+        };
+        return ps;
     }
 
     kvmem_hip_pool pool_desc() const {
@@ -484,6 +601,7 @@ void drop_residency(kvmem_engine *e) {
     e->rt.store().clear_working_set();
     e->slots.reset_after(0);
     e->dirty_tail = -1;
+    ++e->attn_epoch;
 }
 
 // The stage-in row transform from the engine parameters: RoPE frequencies
@@ -754,6 +872,9 @@ int kvmem_engine_truncate_to(kvmem_engine *e, uint32_t token_pos) {
     if (!e) {
         return KVMEM_HIP_ERR_INVALID;
     }
+    if (token_pos < e->rt.store().total_tokens()) {
+        ++e->attn_epoch;  // rows attention read are gone
+    }
     e->rt.truncate_to(token_pos);
     // blocks from the one holding token_pos on are cut short or gone
     for (uint32_t id = token_pos / e->p.block_tokens; id < e->packed_capacity; ++id) {
@@ -984,6 +1105,7 @@ struct ApplyUndo {
 // the failed apply are not marked kept.  The device error stays in the
 // engine's last error; the return value is `code`.
 int rollback(kvmem_engine *e, ApplyUndo &u, int code) {
+    ++e->attn_epoch;  // the failed work may have changed pool rows
     e->rt = std::move(u.rt);
     e->slots = std::move(u.slots);
     e->dirty_tail = u.dirty_tail;
@@ -1270,6 +1392,9 @@ int apply_retrieval_device(kvmem_engine *e, const void *q, int32_t q_type, uint3
         e->fail(KVMEM_HIP_ERR_RUNTIME, "apply_retrieval: the device plan differs from the store's");
         drop_residency(e);
         return KVMEM_HIP_ERR_RUNTIME;
+    }
+    if (!plan.stage_in.empty() || !plan.stage_out.empty() || n_staged || n_moved) {
+        ++e->attn_epoch;
     }
     fill_stats(plan, n_staged, n_moved, 0, 0, stats);
     if (stats) {
@@ -1583,6 +1708,9 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
         e->fail_ctx(KVMEM_HIP_ERR_RUNTIME, "apply sync");
         return rollback(e, undo, KVMEM_HIP_ERR_RUNTIME);
     }
+    if (!plan.stage_in.empty() || !plan.stage_out.empty() || !stage_ids.empty() || n_moved) {
+        ++e->attn_epoch;  // apply_plan_to_kv / layout / write_block_to_gpu (llama-memory-kvmem.cpp:785, 964, 2735)
+    }
     fill_stats(plan, static_cast<uint32_t>(stage_ids.size()), n_moved, n_saved, n_restored, stats);
     return KVMEM_HIP_OK;
 }
@@ -1611,6 +1739,99 @@ int kvmem_engine_apply_retrieval(kvmem_engine *e, const void *q, int32_t q_type,
         return rc;
     }
     return kvmem_engine_apply(e, epoch, rows, sel.data(), n_sel, stats);
+}
+
+int kvmem_engine_append_resident(kvmem_engine *e, uint32_t n_new_tokens) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    const uint64_t want = static_cast<uint64_t>(e->rt.store().total_tokens()) + n_new_tokens;
+    if ((!e->hist_k && !e->host_base) ||
+        (e->hist_k && want > static_cast<uint64_t>(e->hist_capacity) * e->p.block_tokens) ||
+        (e->host_base && want > static_cast<uint64_t>(e->host_capacity) * e->p.block_tokens)) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "append_resident: history capacity exceeded");
+    }
+    if (n_new_tokens == 0) {
+        return KVMEM_HIP_OK;
+    }
+    const auto &bl = e->rt.store().blocks();
+    const uint32_t first_new = e->rt.store().block_count();
+    const bool tail_partial = first_new > 0 && bl.back().n_tokens < e->p.block_tokens;
+    // A partial tail without a slot gets one, but its older rows are not in
+    // the pool: it is staged again by the next apply.  One such block at a
+    // time (the engine tracks a single stale tail).
+    const bool tail_gets_slot = tail_partial && !(bl.back().tier == Tier::GPU && bl.back().gpu_slot >= 0);
+    if (tail_gets_slot && e->dirty_tail >= 0 && e->dirty_tail != static_cast<int64_t>(first_new - 1)) {
+        return e->fail(KVMEM_HIP_ERR_UNSUPPORTED, "append_resident: another block still waits to be staged again");
+    }
+    const uint32_t tail_id = first_new - 1;
+    std::vector<uint32_t> placed;
+    if (!e->rt.append_resident(n_new_tokens, &placed)) {
+        return e->fail(KVMEM_HIP_ERR_NOMEM, "append_resident: no free pool slot for the new rows");
+    }
+    if (tail_partial) {
+        e->meank_valid = std::min(e->meank_valid, tail_id);  // the tail grows: its sums are redone
+    }
+    if (tail_gets_slot) {
+        e->dirty_tail = tail_id;
+    }
+    ++e->epoch;  // the history grew: earlier selections are stale (their rows differ)
+    return KVMEM_HIP_OK;
+}
+
+uint64_t kvmem_engine_attention_epoch(const kvmem_engine *e) {
+    return e ? e->attn_epoch : 0;
+}
+
+int kvmem_engine_attention_view(const kvmem_engine *e, int canonical, kvmem_attention_view *view) {
+    if (!e || !view) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    return export_view(kvmem_amd::attention_view(e->rt.store(), e->pool_state(), canonical != 0), view);
+}
+
+int kvmem_engine_selection_fits(const kvmem_engine *e, uint64_t epoch, uint32_t rows, const uint32_t *sel,
+                                uint32_t n_sel, uint32_t end, uint32_t generation_rows) {
+    if (!e || (n_sel && !sel) || epoch != e->epoch) {
+        return 0;
+    }
+    kvmem_amd::PoolState ps = e->pool_state();
+    ps.epoch = epoch;  // the selection's own staleness is checked above
+    return kvmem_amd::selection_fits(e->rt.store(), ps, e->retrieval_mandatory(), epoch, rows,
+                                     std::vector<uint32_t>(sel, sel + n_sel), end, generation_rows)
+               ? 1
+               : 0;
+}
+
+int kvmem_engine_commit_unchanged(kvmem_engine *e, const kvmem_attention_view *before, uint64_t epoch,
+                                  uint32_t rows, const uint32_t *sel, uint32_t n_sel) {
+    kvmem_amd::AttentionView v;
+    if (!e || (n_sel && !sel) || !import_view(before, v) || epoch != e->epoch) {
+        return 0;
+    }
+    // the view against the attention epoch, the selection against its own
+    kvmem_amd::PoolState ps = e->pool_state();
+    return kvmem_amd::commit_unchanged(e->rt, ps, v, ps.epoch, rows, std::vector<uint32_t>(sel, sel + n_sel))
+               ? 1
+               : 0;
+}
+
+int kvmem_engine_commit_resident(kvmem_engine *e, int canonical) {
+    if (!e) {
+        return 0;
+    }
+    return kvmem_amd::commit_resident(e->rt, e->pool_state(), canonical != 0) ? 1 : 0;
+}
+
+int kvmem_engine_can_append(const kvmem_engine *e, uint32_t end, uint32_t generation_rows, int all_history,
+                            const char **reason) {
+    if (!e) {
+        if (reason) *reason = "invalid_boundary";
+        return 0;
+    }
+    return kvmem_amd::can_append(e->rt.store(), e->pool_state(), end, generation_rows, all_history != 0, reason)
+               ? 1
+               : 0;
 }
 
 int kvmem_engine_scores(kvmem_engine *e, float *out, uint32_t n) {

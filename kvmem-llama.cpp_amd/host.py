@@ -35,6 +35,36 @@ class RowRange(C.Structure):
     _fields_ = [("begin", C.c_int32), ("end", C.c_int32)]
 
 
+class AttentionViewC(C.Structure):
+    """kvmem_attention_view (llama_kvmem_attention_view)."""
+    _fields_ = [("epoch", C.c_uint64), ("rows", C.c_uint32), ("valid", C.c_int32),
+                ("n_blocks", C.c_uint32), ("capacity", C.c_uint32), ("blocks", C.POINTER(C.c_uint32))]
+
+
+@dataclass
+class AttentionView:
+    """llama_kvmem_attention_view (src/adapter/llama-kvmem-hooks.h:143-148)."""
+    epoch: int
+    rows: int
+    valid: bool
+    blocks: list
+
+    def to_c(self):
+        arr = (C.c_uint32 * max(1, len(self.blocks)))(*self.blocks)
+        v = AttentionViewC(self.epoch, self.rows, int(self.valid), len(self.blocks), len(self.blocks),
+                           C.cast(arr, C.POINTER(C.c_uint32)))
+        return v, arr
+
+
+def _get_view(fn, h, canonical: bool, cap: int) -> AttentionView:
+    arr = (C.c_uint32 * max(1, cap))()
+    v = AttentionViewC(0, 0, 0, 0, max(1, cap), C.cast(arr, C.POINTER(C.c_uint32)))
+    rc = fn(h, int(canonical), C.byref(v))
+    if rc != OK:
+        raise KvMemError(rc, "attention view failed")
+    return AttentionView(v.epoch, v.rows, bool(v.valid), list(arr[: v.n_blocks]))
+
+
 def _ranges(rs):
     rs = list(rs)
     return (RowRange * max(1, len(rs)))(*[RowRange(int(b), int(e)) for b, e in rs]), len(rs)
@@ -80,6 +110,20 @@ def bind(lib: C.CDLL) -> C.CDLL:
     sig("kvmem_store_blocks", i32, vp, pi32, pu8, pu8, pi64)
     sig("kvmem_store_commit_resident", i32, vp, pu32, u32)
     sig("kvmem_store_blocks_overlapping", i32, vp, C.POINTER(RowRange), u32, C.c_int32, pu32, u32, pu32)
+    pview, pstr = C.POINTER(AttentionViewC), C.POINTER(C.c_char_p)
+    sig("kvmem_store_epoch", u64, vp)
+    sig("kvmem_store_append_resident", i32, vp, u32)
+    sig("kvmem_store_attention_view", i32, vp, i32, pview)
+    sig("kvmem_store_selection_fits", i32, vp, pu32, u32, u64, u32, pu32, u32, u32, u32)
+    sig("kvmem_store_commit_unchanged", i32, vp, pview, u64, u32, pu32, u32)
+    sig("kvmem_store_can_append", i32, vp, u32, u32, i32, pstr)
+    sig("kvmem_engine_append_resident", i32, vp, u32)
+    sig("kvmem_engine_attention_epoch", u64, vp)
+    sig("kvmem_engine_attention_view", i32, vp, i32, pview)
+    sig("kvmem_engine_selection_fits", i32, vp, u64, u32, pu32, u32, u32, u32)
+    sig("kvmem_engine_commit_unchanged", i32, vp, pview, u64, u32, pu32, u32)
+    sig("kvmem_engine_commit_resident", i32, vp, i32)
+    sig("kvmem_engine_can_append", i32, vp, u32, u32, i32, pstr)
     sig("kvmem_engine_set_request_span", i32, vp, C.c_int32, C.c_int32, C.c_int32)
     sig("kvmem_engine_set_turn_spans", i32, vp, C.POINTER(RowRange), u32, C.POINTER(RowRange), u32)
     sig("kvmem_engine_retrieval_mandatory", i32, vp, pu32, u32, pu32)
@@ -205,6 +249,37 @@ class Store:
     def commit_resident_selection(self, sel: Sequence[int]) -> bool:
         s, n = _u32(sel)
         return bool(self.lib.kvmem_store_commit_resident(self.h, s, n))
+
+    # ---- continuation checks (the store alone: a block holding a slot is complete)
+    def epoch(self) -> int:
+        """Attention epoch: moves with applies that change the working set and cuts."""
+        return self.lib.kvmem_store_epoch(self.h)
+
+    def append_resident(self, n_tokens: int) -> None:
+        """Rows written into the pool as they are decoded (new blocks take slots)."""
+        rc = self.lib.kvmem_store_append_resident(self.h, n_tokens)
+        if rc != OK:
+            raise KvMemError(rc, "kvmem_store_append_resident failed")
+
+    def attention_view(self, canonical: bool = True) -> AttentionView:
+        return _get_view(self.lib.kvmem_store_attention_view, self.h, canonical, self.block_count())
+
+    def selection_fits(self, sel: Selection, end: int, generation_rows: int,
+                       mandatory: Sequence[int] = ()) -> bool:
+        m, nm = _u32(mandatory)
+        s, ns = _u32(sel.blocks)
+        return bool(self.lib.kvmem_store_selection_fits(self.h, m, nm, sel.epoch, sel.rows, s, ns, end,
+                                                        generation_rows))
+
+    def commit_unchanged(self, before: AttentionView, sel: Selection) -> bool:
+        v, keep = before.to_c()
+        s, ns = _u32(sel.blocks)
+        return bool(self.lib.kvmem_store_commit_unchanged(self.h, C.byref(v), sel.epoch, sel.rows, s, ns))
+
+    def can_append(self, end: int, generation_rows: int, all_history: bool) -> tuple[bool, str]:
+        why = C.c_char_p()
+        ok = self.lib.kvmem_store_can_append(self.h, end, generation_rows, int(all_history), C.byref(why))
+        return bool(ok), why.value.decode()
 
     def blocks_overlapping(self, ranges, force_pos: int = -1) -> list:
         """retrieval_mandatory's mapping of row ranges (+ force_pos) to ids."""
@@ -402,6 +477,35 @@ class Engine:
                                                          C.byref(st)), "apply_retrieval")
         return st.as_dict()
 
+    # ---- continuation (two-phase API)
+    def append_resident(self, n: int) -> None:
+        """Rows the caller's decode writes into the pool itself (see block_slots)."""
+        self.check(self.lib.kvmem_engine_append_resident(self.h, n), "append_resident")
+
+    def attention_epoch(self) -> int:
+        return self.lib.kvmem_engine_attention_epoch(self.h)
+
+    def attention_view(self, canonical: bool = True) -> AttentionView:
+        return _get_view(self.lib.kvmem_engine_attention_view, self.h, canonical, self.block_count())
+
+    def selection_fits(self, sel: Selection, end: int, generation_rows: int) -> bool:
+        s, ns = _u32(sel.blocks)
+        return bool(self.lib.kvmem_engine_selection_fits(self.h, sel.epoch, sel.rows, s, ns, end,
+                                                         generation_rows))
+
+    def commit_unchanged(self, before: AttentionView, sel: Selection) -> bool:
+        v, keep = before.to_c()
+        s, ns = _u32(sel.blocks)
+        return bool(self.lib.kvmem_engine_commit_unchanged(self.h, C.byref(v), sel.epoch, sel.rows, s, ns))
+
+    def commit_resident(self, canonical: bool = True) -> bool:
+        return bool(self.lib.kvmem_engine_commit_resident(self.h, int(canonical)))
+
+    def can_append(self, end: int, generation_rows: int, all_history: bool) -> tuple[bool, str]:
+        why = C.c_char_p()
+        ok = self.lib.kvmem_engine_can_append(self.h, end, generation_rows, int(all_history), C.byref(why))
+        return bool(ok), why.value.decode()
+
     def scores(self) -> list:
         n = self.block_count()
         out = (C.c_float * max(1, n))()
@@ -409,5 +513,5 @@ class Engine:
         return list(out[:n])
 
 
-__all__ = ["Store", "Engine", "Selection", "PlanStats", "EngineParams", "bind",
+__all__ = ["Store", "Engine", "Selection", "AttentionView", "PlanStats", "EngineParams", "bind",
            "TYPE_Q8_0", "LAYER_MEAN"]

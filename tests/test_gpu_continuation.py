@@ -1,0 +1,207 @@
+"""Continuation calls of the engine on the GPU (include/kvmem_host.h):
+attention_view, selection_fits, commit_unchanged, commit_resident,
+can_append and append_resident over the engine's own pool.
+
+- The reference GPU test's expectations (tests/mtp-kv-test.cpp:300-361):
+  prefill to the query start with the rows written into the pool as they
+  are decoded, take the view, decode the query rows, preview with the query
+  span mandatory; the identical view is accepted, a trimmed mandatory tail
+  does not fit, an oversized generation reserve cannot append, and after a
+  restore (truncate to the query start) the old view and selection are
+  stale.  Every pool row stays the oracle's quantization of the history.
+- An identical preview after an apply commits with no device work: the
+  pool is byte for byte the same and no stage-in or slot move is timed.
+- A changed selection or a changed pool is refused; commit_resident and
+  canonical / LIFO views.
+- Rows appended resident in canonical mode continue the slot order and are
+  not staged again by the next apply.
+"""
+from __future__ import annotations
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from conftest import load_pkg  # noqa: E402
+
+kv = load_pkg()
+from kvmem_amd import host  # noqa: E402
+
+from engine_helpers import E, L, T, check_pool, history, make_engine  # noqa: E402
+
+
+def announce(msg: str) -> None:
+    print(f"[continuation] {msg}", flush=True)
+
+
+def pool_bytes(eng) -> list:
+    out = []
+    for layer in range(L):
+        for ptr, ty in zip(eng.pool_layer(layer), (eng.params.type_k, eng.params.type_v)):
+            n = eng.n_slots() * T * kv.row_size(ty, E)
+            buf = torch.empty(n, dtype=torch.uint8, device="cuda")
+            c = kv.Context(0)
+            c.d2d_batched([ptr], [buf.data_ptr()], [n])
+            c.sync()
+            c.close()
+            out.append(buf.cpu())
+    return out
+
+
+def decode_rows(eng, k, v, begin: int, end: int) -> None:
+    """The caller's decode of rows [begin, end): append them resident, then
+    write the pool cells of every block they touch (whole blocks, from the
+    history that already holds the rows), as llama.cpp writes a batch's
+    K/V cells."""
+    eng.append_resident(end - begin)
+    slots = eng.block_slots()
+    ids = list(range(begin // T, (end + T - 1) // T))
+    n_blocks = eng.block_count()
+    last = eng.total_tokens() - (n_blocks - 1) * T
+    c = kv.Context(0)
+    hist = c.make_history(k.data_ptr(), v.data_ptr(), L, n_blocks, T, E, E, 0 if last == T else last,
+                          k.shape[1])
+    pk = [eng.pool_layer(layer)[0] for layer in range(L)]
+    pv = [eng.pool_layer(layer)[1] for layer in range(L)]
+    pool = c.make_pool(L, eng.n_slots(), T, E, E, eng.params.type_k, eng.params.type_v, pk, pv)
+    c.stagein_blocks(hist, pool, ids, [slots[b] for b in ids])
+    c.sync()
+    c.close()
+
+
+def test_reference_logits_fixture_flow(oracle):
+    announce("mtp-kv-test flow: prefill 576 rows, 24 query rows, all blocks fit the budget")
+    cap, end = 8, 600
+    query = end - 24
+    k, v, q = history(cap, seed=41)
+    with make_engine(16, 4) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, 0)
+        decode_rows(eng, k, v, 0, query)
+        before = eng.attention_view()
+        assert before.valid and before.rows == query and before.blocks == [0, 1, 2, 3, 4]
+        decode_rows(eng, k, v, query, end)
+        eng.set_request_span(query, end)
+        sel = eng.preview(q.data_ptr(), q.shape[1])
+        assert sel.blocks == [0, 1, 2, 3, 4] and sel.rows == end
+        snap = pool_bytes(eng)
+        assert eng.commit_unchanged(before, sel), "identical attention view rejected"
+        assert all(torch.equal(a, b) for a, b in zip(snap, pool_bytes(eng)))
+        last = end - 4 * T
+        check_pool(eng, oracle, k, v, sel.blocks, kv.TYPE_Q8_0, kv.TYPE_Q8_0,
+                   ntok_of=lambda b: last if b == 4 else T)
+        trimmed = host.Selection(sel.epoch, sel.rows, sel.blocks[:-1])
+        assert not eng.selection_fits(trimmed, end, 0), "trimmed mandatory tail accepted"
+        assert eng.selection_fits(sel, end, 0)
+        ok, why = eng.can_append(end, eng.n_slots() * T, True)
+        assert not ok and why == "insufficient_slots", "oversized generation reserve accepted"
+        assert eng.can_append(end, T, False) == (True, "same_query")
+        eng.truncate_to(query)                  # restore the checkpoint at the query start
+        assert not eng.commit_unchanged(before, sel), "stale attention view accepted after restore"
+        with pytest.raises(kv.StaleSelection):
+            eng.apply(sel)
+        decode_rows(eng, k, v, query, end)      # replay the query rows
+        again = eng.preview(q.data_ptr(), q.shape[1])
+        assert again.blocks == sel.blocks
+        assert eng.commit_unchanged(eng.attention_view(), again)
+        check_pool(eng, oracle, k, v, again.blocks, kv.TYPE_Q8_0, kv.TYPE_Q8_0,
+                   ntok_of=lambda b: last if b == 4 else T)
+
+
+def test_commit_unchanged_after_identical_preview(oracle):
+    announce("apply, then an identical preview: commit_unchanged moves no byte")
+    cap, nb = 40, 40
+    k, v, q = history(cap, seed=43)
+    q2 = (q.float() * -1.0).to(torch.bfloat16)
+    with make_engine(8, 4) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        sel1 = eng.preview(q.data_ptr(), q.shape[1])
+        eng.apply(sel1)
+        view = eng.attention_view()
+        assert view.valid and view.blocks == sel1.blocks
+        assert eng.commit_resident(True)
+        snap = pool_bytes(eng)
+        ctx = kv.Context.borrow(eng.ctx_handle())
+        ctx.perf_enable(True)
+        ctx.perf_reset()
+        same = eng.preview(q.data_ptr(), q.shape[1])
+        assert same.blocks == sel1.blocks
+        assert eng.commit_unchanged(view, same)
+        ctx.sync()
+        perf = ctx.perf()
+        ctx.perf_enable(False)
+        assert perf["n_set"] == 0 and perf["n_layout"] == 0, perf
+        assert all(torch.equal(a, b) for a, b in zip(snap, pool_bytes(eng)))
+        st = eng.apply(host.Selection(eng.epoch(), eng.total_tokens(), same.blocks))
+        assert st["n_staged"] == 0 and st["n_moved"] == 0 and st["n_stage_in"] == 0
+        # a different selection is refused and leaves the working set alone
+        other = eng.preview(q2.data_ptr(), q2.shape[1])
+        assert other.blocks != sel1.blocks
+        assert not eng.commit_unchanged(view, other)
+        assert not eng.selection_fits(host.Selection(other.epoch + 1, other.rows, other.blocks),
+                                      other.rows, 0)
+        eng.apply(other)
+        # the pool changed: the old view is stale even for the new resident set
+        assert eng.attention_epoch() != view.epoch
+        assert not eng.commit_unchanged(view, host.Selection(eng.epoch(), eng.total_tokens(),
+                                                             other.blocks))
+        check_pool(eng, oracle, k, v, other.blocks, kv.TYPE_Q8_0, kv.TYPE_Q8_0)
+
+
+def test_views_in_lifo_layout(oracle):
+    announce("LIFO slots: the canonical view breaks, the plain one holds")
+    cap, nb = 24, 24
+    k, v, q = history(cap, seed=47)
+    q2 = (q.float() * -1.0).to(torch.bfloat16)
+    with make_engine(6, 2, canonical_layout=0) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        eng.apply(eng.preview(q.data_ptr(), q.shape[1]))
+        eng.apply(eng.preview(q2.data_ptr(), q2.shape[1]))
+        slots = eng.block_slots()
+        resident = [b for b in range(nb) if slots[b] >= 0]
+        canonical = all(slots[b] == i for i, b in enumerate(resident))
+        plain = eng.attention_view(canonical=False)
+        assert plain.valid and plain.blocks == resident
+        assert eng.attention_view(canonical=True).valid == canonical
+        assert eng.commit_resident(False)
+        assert eng.commit_resident(True) == canonical
+        ok, why = eng.can_append(nb * T, 0, True)
+        assert not ok and why in ("coverage_or_layout", "history_not_resident")
+
+
+def test_append_resident_in_canonical_layout(oracle):
+    announce("rows appended resident continue the window and are not staged again")
+    cap, nb = 20, 16
+    k, v, q = history(cap, seed=53)
+    with make_engine(8, 4) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        sel = eng.preview(q.data_ptr(), q.shape[1])
+        eng.apply(sel)
+        view = eng.attention_view()
+        decode_rows(eng, k, v, nb * T, nb * T + 70)     # block 16, 70 rows
+        assert eng.block_slots()[nb] == len(sel.blocks)
+        after = eng.attention_view()
+        assert after.valid and after.blocks == sel.blocks + [nb]
+        assert after.epoch == view.epoch                # appended rows leave the attention epoch
+        # the selection now needs the new block: with it mandatory, it is kept
+        eng.set_request_span(nb * T, 0)
+        sel2 = eng.preview(q.data_ptr(), q.shape[1])
+        assert nb in sel2.blocks
+        st = eng.apply(sel2)
+        assert st["n_staged"] == len(set(sel2.blocks) - set(sel.blocks) - {nb})
+        check_pool(eng, oracle, k, v, sel2.blocks, kv.TYPE_Q8_0, kv.TYPE_Q8_0,
+                   ntok_of=lambda b: 70 if b == nb else T)
+        # a partial tail without a slot gets one, but is staged again by the next apply
+        eng.set_request_span(-1)
+        far = [b for b in range(nb) if b not in sel2.blocks][:1]
+        eng.apply(host.Selection(eng.epoch(), eng.total_tokens(), sorted(set(sel2.blocks[:4]) | set(far))))
+        assert eng.block_slots()[nb] == -1
+        eng.append_resident(10)                         # the tail (80 rows) takes a slot
+        assert eng.block_slots()[nb] >= 0
+        assert not eng.attention_view(canonical=False).valid
+        st = eng.apply(host.Selection(eng.epoch(), eng.total_tokens(), [0, nb]))
+        assert st["n_staged"] >= 1
+        check_pool(eng, oracle, k, v, [0, nb], kv.TYPE_Q8_0, kv.TYPE_Q8_0,
+                   ntok_of=lambda b: 80 if b == nb else T)
+        assert eng.attention_view().valid
