@@ -49,7 +49,8 @@ enum kvmem_hip_status {
     KVMEM_HIP_ERR_RUNTIME = 2,    /* a HIP runtime call failed */
     KVMEM_HIP_ERR_NOMEM = 3,      /* device or pinned allocation failed */
     KVMEM_HIP_ERR_STALE = 4,      /* selection epoch/rows mismatch */
-    KVMEM_HIP_ERR_UNSUPPORTED = 5 /* type / head_dim not built */
+    KVMEM_HIP_ERR_UNSUPPORTED = 5, /* type / head_dim not built */
+    KVMEM_HIP_ERR_BUSY = 6         /* a shared resource is in use by overlapping work */
 };
 
 /* ggml_type codes (ggml.h) for the formats on this path. */
@@ -387,17 +388,21 @@ KVMEM_HIP_API int kvmem_hip_score(kvmem_hip_ctx *ctx,
                                   const kvmem_hip_score_args *args);
 
 /* kvmem_hip_score that allocates nothing: no counterpart in the reference.
- * For callers that cannot allocate (code under HIP graph capture, tight
- * serving loops, harnesses that forbid hipMalloc).  Same arguments and the
- * same scores, bit for bit.  The scorer's partial maxima (and the per-layer
- * scores when args->layer_scores is NULL) live in a static device array of
- * 8 MiB that every GPU the library runs on holds until the process ends;
- * a call needing more returns KVMEM_HIP_ERR_INVALID before any work (the
- * 256K workload -- 16 layers x 2048 blocks, 4 KV heads, 64 query tokens x
- * 24 heads -- needs 2.1 MiB).  Every call on one GPU shares that GPU's
- * array and overwrites it (nothing in it has to start at zero), so calls
- * that overlap on one GPU -- two contexts or streams at once -- race; calls
- * queued on one stream do not.  Not timed by kvmem_hip_perf_*. */
+ * For callers that cannot allocate (tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and the same scores, bit for bit.
+ * The scorer's partial maxima (and the per-layer scores when
+ * args->layer_scores is NULL) live in a static device array of 8 MiB that
+ * every GPU the library runs on holds until the process ends; a call
+ * needing more returns KVMEM_HIP_ERR_INVALID before any work (the 256K
+ * workload -- 16 layers x 2048 blocks, 4 KV heads, 64 query tokens x 24
+ * heads -- needs 2.1 MiB).  Every call on one GPU shares that GPU's array
+ * and overwrites it (nothing in it has to start at zero).  Calls queued on
+ * one context's stream follow each other; a call from another context, or
+ * from the same context on another stream, while the last call on the
+ * array has not finished returns KVMEM_HIP_ERR_BUSY with nothing issued
+ * (the caller synchronises, or uses kvmem_hip_score).  The array's last
+ * user is tracked on the host: two processes on one GPU each have their
+ * own array.  Not timed by kvmem_hip_perf_*. */
 KVMEM_HIP_API int kvmem_hip_score_noalloc(kvmem_hip_ctx *ctx,
                                           const kvmem_hip_history *hist,
                                           const kvmem_hip_score_args *args);
@@ -484,11 +489,12 @@ KVMEM_HIP_API int kvmem_hip_meank_add(kvmem_hip_ctx *ctx, const void *k, int32_t
  * the strided device view q (element (d, h, t) at d*nb0 + h*nb1 + t*nb2
  * bytes, as ggml lays Qcur out and the reference reads it,
  * bytes_to_f32_token_major :2066-2090), widened exactly to f32 from F32,
- * F16 or BF16.  Rows must be distinct within a call. */
+ * F16 or BF16.  Rows must be distinct within a call and below capacity
+ * (KVMEM_HIP_ERR_INVALID, nothing issued, otherwise). */
 KVMEM_HIP_API int kvmem_hip_q_window_write(kvmem_hip_ctx *ctx, const void *q, int32_t q_type,
                                            uint32_t n_head, uint32_t head_dim, size_t nb0, size_t nb1,
                                            size_t nb2, const uint32_t *tokens, const uint32_t *rows,
-                                           uint32_t n, float *window);
+                                           uint32_t n, float *window, uint32_t capacity);
 /* Gather: out[l][i][:] = window[l][rows[i]][:] for every layer (window
  * device [n_layers][capacity][n_embd_q] f32), converted to out_type (BF16
  * and F16 round to nearest even; F32 copies) -- the [n_layers][n][n_head]
@@ -562,12 +568,18 @@ KVMEM_HIP_API uint64_t kvmem_hip_debug_fail_left(const kvmem_hip_ctx *ctx);
 
 /* Per-stage GPU time (hipEvent pairs on the context stream), the device
  * analogue of the KVMEM_RETR_SUM buckets (llama-memory-kvmem.cpp:2918-2936):
- * score = scoring kernels, topk = selection kernel, set = stage-in kernels,
- * copy = H2D of host blocks, layout = slot moves.  Milliseconds summed over
- * calls since the last reset; counts are numbers of timed calls.
+ * score = scoring kernels, topk = selection kernel, set = stage-in kernels
+ * (quantizing or packed), copy = kvmem_hip_h2d_async, layout = slot moves
+ * and their slot saves, stage_out = packed rows gathered and copied to the
+ * host (kvmem_hip_stageout_blocks), plan = the slot plan (the device plan
+ * kernel of the engine's apply_retrieval, or the host time of the engine's
+ * own diff and slot plan when it plans on the host).  Milliseconds summed
+ * over calls since the last reset; counts are numbers of timed calls; a
+ * call that fails is not timed.
  * after_score_ms: from the end of a call's scoring to the end of the last
  * stage-in before the next scoring (top-k, the slot plan, moves, stage-in
- * and the idle stream between them); n_after_score such spans. */
+ * and the idle stream between them); n_after_score such spans.
+ * h2d_bytes / d2h_bytes / d2d_bytes: the bytes of kvmem_hip_transfer_get. */
 typedef struct kvmem_hip_perf {
     double score_ms;
     double topk_ms;
@@ -583,7 +595,32 @@ typedef struct kvmem_hip_perf {
     uint64_t d2d_bytes;
     double after_score_ms;
     uint64_t n_after_score;
+    double stage_out_ms;
+    double plan_ms;
+    uint64_t n_stage_out;
+    uint64_t n_plan;
+    uint64_t d2h_bytes;
 } kvmem_hip_perf;
+
+/* Data this context moved, per direction: [0] host to device, [1] device
+ * to host, [2] device to device -- llama_kvmem_transfer_stats
+ * (src/adapter/llama-kvmem-hooks.h:127-132), whose copy call sites
+ * kvmem_copy_async / kvmem_tensor_set / _get count the same way
+ * (src/adapter/llama-kvmem-transfer.h:9-31).  A call is one copy launch or
+ * one runtime copy: a stage-in kernel reading pinned host blocks over the
+ * link is one host-to-device call of the F16 (or packed) bytes it reads; a
+ * slot-move chain walk and its slot saves are one device-to-device call
+ * each; a stage-out through the device ring is its gather launches (device
+ * to device) and its runtime copies (device to host).  Quantizing kernels
+ * reading a device-resident history are compute, not transfers, and launch
+ * tables are not counted.  Always counted (perf_enable not needed); cleared
+ * by kvmem_hip_perf_reset. */
+typedef struct kvmem_hip_transfer_stats {
+    uint64_t bytes[3];
+    uint64_t calls[3];
+} kvmem_hip_transfer_stats;
+
+KVMEM_HIP_API int kvmem_hip_transfer_get(const kvmem_hip_ctx *ctx, kvmem_hip_transfer_stats *out);
 
 KVMEM_HIP_API int kvmem_hip_perf_enable(kvmem_hip_ctx *ctx, int on);
 /* Which stages perf_enable times (default all): a mask of
@@ -596,8 +633,12 @@ KVMEM_HIP_API int kvmem_hip_perf_enable(kvmem_hip_ctx *ctx, int on);
 #define KVMEM_PERF_STAGE_SET 4u
 #define KVMEM_PERF_STAGE_COPY 8u
 #define KVMEM_PERF_STAGE_LAYOUT 16u
+#define KVMEM_PERF_STAGE_STAGE_OUT 32u
+#define KVMEM_PERF_STAGE_PLAN 64u
 KVMEM_HIP_API int kvmem_hip_perf_stages(kvmem_hip_ctx *ctx, uint32_t mask);
 KVMEM_HIP_API int kvmem_hip_perf_get(kvmem_hip_ctx *ctx, kvmem_hip_perf *out);
+/* Zero every bucket, count and transfer counter; a stage a failed call
+ * left open is dropped. */
 KVMEM_HIP_API void kvmem_hip_perf_reset(kvmem_hip_ctx *ctx);
 
 #ifdef __cplusplus

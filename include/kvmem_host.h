@@ -58,6 +58,10 @@ typedef struct kvmem_plan_stats {
     uint32_t n_restored;               /* staged blocks restored from packed rows */
     uint32_t device_planned;           /* 1: the diff and slot plan ran on the device
                                           (kvmem_engine_params.device_plan) */
+    uint32_t n_skip;                   /* window blocks whose baked position equals
+                                          their window position (KvMemRemap.skip,
+                                          the reference's n_skip,
+                                          llama-memory-kvmem.cpp:3152-3158) */
 } kvmem_plan_stats;
 
 /* A half-open range [begin, end) of history rows (token positions);

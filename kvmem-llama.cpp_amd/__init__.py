@@ -37,10 +37,11 @@ GROUP_BYTES = {TYPE_Q8_0: 34, TYPE_Q4_0: 18, TYPE_Q5_0: 22, TYPE_F16: 64}
 
 LAYER_MEAN, LAYER_MAX, LAYER_SUM = 0, 1, 2
 
-OK, ERR_INVALID, ERR_RUNTIME, ERR_NOMEM, ERR_STALE, ERR_UNSUPPORTED = range(6)
+OK, ERR_INVALID, ERR_RUNTIME, ERR_NOMEM, ERR_STALE, ERR_UNSUPPORTED, ERR_BUSY = range(7)
 
 # stage bits of Context.perf_stages (KVMEM_PERF_STAGE_*)
 PERF_STAGE_SCORE, PERF_STAGE_TOPK, PERF_STAGE_SET, PERF_STAGE_COPY, PERF_STAGE_LAYOUT = 1, 2, 4, 8, 16
+PERF_STAGE_STAGE_OUT, PERF_STAGE_PLAN = 32, 64
 PERF_STAGE_ALL = 0xffffffff
 
 # operation kinds of Context.debug_fail_after (kvmem_hip_fail_kind)
@@ -125,12 +126,24 @@ class Scratch(C.Structure):
     _fields_ = [("device_bytes", C.c_uint64), ("pinned_bytes", C.c_uint64), ("allocations", C.c_uint64)]
 
 
+class TransferStats(C.Structure):
+    """kvmem_hip_transfer_stats: bytes / calls per direction (H2D, D2H, D2D)."""
+    _fields_ = [("bytes", C.c_uint64 * 3), ("calls", C.c_uint64 * 3)]
+
+    def as_dict(self) -> dict:
+        names = ("h2d", "d2h", "d2d")
+        return {f"{n}_{what}": int(getattr(self, what)[i]) for i, n in enumerate(names)
+                for what in ("bytes", "calls")}
+
+
 class Perf(C.Structure):
     _fields_ = [("score_ms", C.c_double), ("topk_ms", C.c_double), ("set_ms", C.c_double),
                 ("copy_ms", C.c_double), ("layout_ms", C.c_double), ("n_score", C.c_uint64),
                 ("n_topk", C.c_uint64), ("n_set", C.c_uint64), ("n_copy", C.c_uint64),
                 ("n_layout", C.c_uint64), ("h2d_bytes", C.c_uint64), ("d2d_bytes", C.c_uint64),
-                ("after_score_ms", C.c_double), ("n_after_score", C.c_uint64)]
+                ("after_score_ms", C.c_double), ("n_after_score", C.c_uint64),
+                ("stage_out_ms", C.c_double), ("plan_ms", C.c_double), ("n_stage_out", C.c_uint64),
+                ("n_plan", C.c_uint64), ("d2h_bytes", C.c_uint64)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}
@@ -218,6 +231,9 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_perf_stages", i32, vp, C.c_uint32)
     _sig(lib, "kvmem_hip_perf_get", i32, vp, C.POINTER(Perf))
     _sig(lib, "kvmem_hip_perf_reset", None, vp)
+    _sig(lib, "kvmem_hip_q_window_write", i32, vp, vp, i32, C.c_uint32, C.c_uint32, C.c_size_t, C.c_size_t,
+         C.c_size_t, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.c_uint32, vp, C.c_uint32)
+    _sig(lib, "kvmem_hip_transfer_get", i32, vp, C.POINTER(TransferStats))
     if path is None:
         _lib = lib
     return lib
@@ -497,3 +513,18 @@ class Context:
 
     def perf_reset(self) -> None:
         self.lib.kvmem_hip_perf_reset(self.h)
+
+    def q_window_write(self, q_ptr: int, q_type: int, n_head: int, head_dim: int, nb0: int, nb1: int,
+                       nb2: int, tokens, rows, window_ptr: int, capacity: int) -> None:
+        """Tokens of a strided query view into rows of a [capacity][n_head*head_dim] f32 window."""
+        t, n = _u32_array(tokens)
+        r, m = _u32_array(rows)
+        assert n == m
+        self.check(self.lib.kvmem_hip_q_window_write(self.h, q_ptr, q_type, n_head, head_dim, nb0, nb1, nb2,
+                                                     t, r, n, window_ptr, capacity), "q_window_write")
+
+    def transfers(self) -> dict:
+        """Bytes and calls per direction since the last perf_reset."""
+        t = TransferStats()
+        self.check(self.lib.kvmem_hip_transfer_get(self.h, C.byref(t)), "transfer_get")
+        return t.as_dict()

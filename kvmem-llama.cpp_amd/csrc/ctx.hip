@@ -1,6 +1,7 @@
 // Context lifetime, error reporting, streams, upload ring, profiling and the
 // batched device copy of libkvmem_hip.so.
 #include "kvmem_internal.hpp"
+#include "device_reselect.h"
 
 #include <algorithm>
 
@@ -144,6 +145,18 @@ void perf_begin(kvmem_hip_ctx *ctx, PerfStage s) {
     } else if (e) {
         ctx->perf_free.push_back(e);
     }
+}
+
+void perf_drop(kvmem_hip_ctx *ctx, PerfStage s) {
+    if (ctx->perf_open[s]) {
+        ctx->perf_free.push_back(ctx->perf_open[s]);
+        ctx->perf_open[s] = nullptr;
+    }
+}
+
+void note_xfer(kvmem_hip_ctx *ctx, XferKind k, uint64_t bytes, uint64_t calls) {
+    ctx->xfer_bytes[k] += bytes;
+    ctx->xfer_calls[k] += calls;
 }
 
 // The open scorer-to-stage-in span, if it reached a stage-in, joins the
@@ -460,6 +473,8 @@ void kvmem_hip_destroy(kvmem_hip_ctx *ctx) {
     for (hipEvent_t e : ctx->perf_free) {
         (void) hipEventDestroy(e);
     }
+    score_scratch_release(ctx);
+    if (ctx->noalloc_done) (void) hipEventDestroy(ctx->noalloc_done);
     if (ctx->own_stream) (void) hipStreamDestroy(ctx->own_stream);
     if (ctx->copy_stream) (void) hipStreamDestroy(ctx->copy_stream);
     delete ctx;
@@ -595,14 +610,12 @@ int kvmem_hip_h2d_async(kvmem_hip_ctx *ctx, void *dst, const void *src, size_t n
     if (injected_fail(ctx, KVMEM_HIP_FAIL_COPY, "h2d_async")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
-    perf_begin(ctx, kPerfCopy);
-    const bool ok = hip_ok(ctx, hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, ctx->stream),
-                           "h2d_async");
-    perf_end(ctx, kPerfCopy);
-    if (!ok) {
+    PerfScope timed(ctx, kPerfCopy);
+    if (!hip_ok(ctx, hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, ctx->stream), "h2d_async")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
-    ctx->h2d_bytes += n;
+    timed.ok();
+    note_xfer(ctx, kXferH2D, n);
     return KVMEM_HIP_OK;
 }
 
@@ -643,13 +656,12 @@ int kvmem_hip_d2d_batched(kvmem_hip_ctx *ctx, const void *const *src, void *cons
     if (!stage_copy_ops(ctx, ops, tables, "d2d_batched ops")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
-    perf_begin(ctx, kPerfLayout);
-    const bool ok = launch_staged_copies(ctx, tables, ops.size(), "d2d_batched launch");
-    perf_end(ctx, kPerfLayout);
-    if (!ok) {
+    PerfScope timed(ctx, kPerfLayout);
+    if (!launch_staged_copies(ctx, tables, ops.size(), "d2d_batched launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
-    ctx->d2d_bytes += total;
+    timed.ok();
+    note_xfer(ctx, kXferD2D, total);
     return KVMEM_HIP_OK;
 }
 
@@ -701,10 +713,33 @@ int kvmem_hip_perf_get(kvmem_hip_ctx *ctx, kvmem_hip_perf *out) {
     out->n_set = ctx->perf_n[kPerfSet];
     out->n_copy = ctx->perf_n[kPerfCopy];
     out->n_layout = ctx->perf_n[kPerfLayout];
-    out->h2d_bytes = ctx->h2d_bytes;
-    out->d2d_bytes = ctx->d2d_bytes;
+    out->h2d_bytes = ctx->xfer_bytes[kXferH2D];
+    out->d2d_bytes = ctx->xfer_bytes[kXferD2D];
     out->after_score_ms = ctx->after_score_ms;
     out->n_after_score = ctx->n_after_score;
+    out->stage_out_ms = ctx->perf_ms[kPerfStageOut];
+    out->plan_ms = ctx->perf_ms[kPerfPlan];
+    out->n_stage_out = ctx->perf_n[kPerfStageOut];
+    out->n_plan = ctx->perf_n[kPerfPlan];
+    out->d2h_bytes = ctx->xfer_bytes[kXferD2H];
+    return KVMEM_HIP_OK;
+}
+
+void kvmem_hip_perf_add_plan_ms(kvmem_hip_ctx *ctx, double ms) {
+    if (ctx && ctx->perf_on && (ctx->perf_mask & (1u << kPerfPlan))) {
+        ctx->perf_ms[kPerfPlan] += ms;
+        ctx->perf_n[kPerfPlan] += 1;
+    }
+}
+
+int kvmem_hip_transfer_get(const kvmem_hip_ctx *ctx, kvmem_hip_transfer_stats *out) {
+    if (!ctx || !out) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    for (int k = 0; k < 3; ++k) {
+        out->bytes[k] = ctx->xfer_bytes[k];
+        out->calls[k] = ctx->xfer_calls[k];
+    }
     return KVMEM_HIP_OK;
 }
 
@@ -714,11 +749,15 @@ void kvmem_hip_perf_reset(kvmem_hip_ctx *ctx) {
     }
     perf_collect(ctx);
     for (int s = 0; s < kPerfStages; ++s) {
+        // a stage a failed or unfinished call left open starts no later span
+        perf_drop(ctx, static_cast<PerfStage>(s));
         ctx->perf_ms[s] = 0.0;
         ctx->perf_n[s] = 0;
     }
-    ctx->h2d_bytes = 0;
-    ctx->d2d_bytes = 0;
+    for (int k = 0; k < 3; ++k) {
+        ctx->xfer_bytes[k] = 0;
+        ctx->xfer_calls[k] = 0;
+    }
     ctx->after_score_ms = 0.0;
     ctx->n_after_score = 0;
 }

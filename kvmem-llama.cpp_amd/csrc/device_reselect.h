@@ -60,6 +60,10 @@ int kvmem_hip_reselect_device_stagein(kvmem_hip_ctx *ctx, const kvmem_hip_histor
  * once the stream has drained. */
 int kvmem_hip_reselect_device_counts(kvmem_hip_ctx *ctx, uint32_t *out, uint32_t n);
 
+/* Host time of the engine's own diff and slot plan, added to the plan
+ * bucket of kvmem_hip_perf when that stage is timed. */
+void kvmem_hip_perf_add_plan_ms(kvmem_hip_ctx *ctx, double ms);
+
 #ifdef __cplusplus
 }
 #endif

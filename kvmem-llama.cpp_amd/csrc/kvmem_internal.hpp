@@ -37,8 +37,18 @@ struct UploadSlot {
 };
 
 constexpr int kUploadRing = 4;
-constexpr int kPerfStages = 5;  // score, topk, set, copy, layout
-enum PerfStage { kPerfScore = 0, kPerfTopk = 1, kPerfSet = 2, kPerfCopy = 3, kPerfLayout = 4 };
+constexpr int kPerfStages = 7;  // score, topk, set, copy, layout, stage-out, plan
+enum PerfStage {
+    kPerfScore = 0,
+    kPerfTopk = 1,
+    kPerfSet = 2,
+    kPerfCopy = 3,
+    kPerfLayout = 4,
+    kPerfStageOut = 5,
+    kPerfPlan = 6
+};
+// Directions of the transfer counters (llama_kvmem_transfer_stats order).
+enum XferKind { kXferH2D = 0, kXferD2H = 1, kXferD2D = 2 };
 
 }  // namespace kvmem_hip
 
@@ -106,8 +116,10 @@ struct kvmem_hip_ctx {
     std::vector<std::pair<hipEvent_t, hipEvent_t>> span_done;
     double after_score_ms = 0.0;
     uint64_t n_after_score = 0;
-    uint64_t h2d_bytes = 0;
-    uint64_t d2d_bytes = 0;
+    // bytes and calls per direction (kXferH2D, kXferD2H, kXferD2D) of the
+    // data this context moved: one call = one copy launch or runtime copy
+    uint64_t xfer_bytes[3] = {};
+    uint64_t xfer_calls[3] = {};
     uint64_t n_allocs = 0;  // device + pinned allocations since creation
 
     // Host-side failure injection (kvmem_hip_debug_fail_after): the
@@ -119,6 +131,9 @@ struct kvmem_hip_ctx {
     // Device address of the scorer's static scratch array on this device
     // (kvmem_hip_score_noalloc), looked up when the context is created.
     void *noalloc_scratch = nullptr;
+    // Completion of this context's last kvmem_hip_score_noalloc, recorded on
+    // the stream it ran on; the device's scratch owner record points here.
+    hipEvent_t noalloc_done = nullptr;
 };
 
 namespace kvmem_hip {
@@ -255,14 +270,46 @@ void *upload(kvmem_hip_ctx *ctx, const void *src, size_t bytes, const char *what
 
 // Top-k in two halves (kvmem_hip_topk is both): topk_launch enqueues the
 // selection kernel (with `to_device`, also writing the selection to
-// ctx->topk_dev); topk_wait spins until the selection is on the host.
+// ctx->topk_dev); topk_wait spins until the selection is on the host,
+// asking the stream for a failure once hold_off_us have passed.
 int topk_launch(kvmem_hip_ctx *ctx, const float *scores, uint32_t n, const uint32_t *forced,
                 uint32_t n_forced, uint32_t need, int tie_lower_index, bool to_device);
-int topk_wait(kvmem_hip_ctx *ctx, uint32_t *sel_out, uint32_t *n_sel);
+int topk_wait(kvmem_hip_ctx *ctx, uint32_t *sel_out, uint32_t *n_sel, int64_t hold_off_us);
 
 // Profiling brackets around a stage's launches on the context stream.
 void perf_begin(kvmem_hip_ctx *ctx, PerfStage s);
 void perf_end(kvmem_hip_ctx *ctx, PerfStage s);
+// Forget a started stage without timing it (the call failed).
+void perf_drop(kvmem_hip_ctx *ctx, PerfStage s);
+
+// A timed stage over a scope: started on construction, ended by ok() once
+// the work is enqueued, dropped on destruction otherwise, so that no
+// return path leaves the stage open.
+class PerfScope {
+public:
+    PerfScope(kvmem_hip_ctx *ctx, PerfStage s) : ctx_(ctx), s_(s) { perf_begin(ctx_, s_); }
+    ~PerfScope() {
+        if (!done_) {
+            perf_drop(ctx_, s_);
+        }
+    }
+    void ok() {
+        if (!done_) {
+            perf_end(ctx_, s_);
+            done_ = true;
+        }
+    }
+    PerfScope(const PerfScope &) = delete;
+    PerfScope &operator=(const PerfScope &) = delete;
+
+private:
+    kvmem_hip_ctx *ctx_;
+    PerfStage s_;
+    bool done_ = false;
+};
+
+// Count `bytes` moved in direction k by `calls` copy operations.
+void note_xfer(kvmem_hip_ctx *ctx, XferKind k, uint64_t bytes, uint64_t calls = 1);
 // Harvest finished event pairs into the accumulators (blocking).
 void perf_collect(kvmem_hip_ctx *ctx);
 
@@ -280,6 +327,8 @@ bool load_qwindow_kernels();
 // the device address of the static scratch array of
 // kvmem_hip_score_noalloc and keeps it in ctx->noalloc_scratch.
 bool score_scratch_setup(kvmem_hip_ctx *ctx);
+// Forgets ctx as the owner of its device's scratch (the context goes away).
+void score_scratch_release(kvmem_hip_ctx *ctx);
 
 template <typename K>
 inline bool load_kernel_object(K *kernel) {

@@ -432,7 +432,12 @@ int kvmem_hip_meank_sums_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_history *
     if (!hip_ok(ctx, hipGetLastError(), "meank_sums_host launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
-    ctx->h2d_bytes += static_cast<uint64_t>(n) * hist->n_layers * T * E * 2u;
+    // the kernel reads the listed blocks' K rows over the link
+    uint64_t rows = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        rows += (block_ids[i] + 1 == hist->n_blocks && hist->last_block_tokens) ? hist->last_block_tokens : T;
+    }
+    note_xfer(ctx, kXferH2D, rows * hist->n_layers * E * 2u);
     return KVMEM_HIP_OK;
 }
 

@@ -143,10 +143,15 @@ int kvmem_hip_stageout_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool,
                 }
             }
         }
-        perf_begin(ctx, kPerfCopy);
-        const bool ok = launch_copy_ops(ctx, ops, "stage-out to the pinned store");
-        perf_end(ctx, kPerfCopy);
-        return ok ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
+        uint64_t bytes = 0;
+        for (const CopyOpDev &op : ops) bytes += op.nbytes;
+        PerfScope timed(ctx, kPerfStageOut);
+        if (!launch_copy_ops(ctx, ops, "stage-out to the pinned store")) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        timed.ok();
+        note_xfer(ctx, kXferD2H, bytes);
+        return KVMEM_HIP_OK;
     }
     // Pageable store: gather into the device ring, then runtime copies.
     if (!ensure_d2h_ring(ctx, g.span)) {
@@ -157,7 +162,7 @@ int kvmem_hip_stageout_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool,
     const uint32_t T = pool->block_tokens;
     uint8_t *host = static_cast<uint8_t *>(dst->base);
     uint8_t *ring = static_cast<uint8_t *>(ctx->d2h_ring.ptr);
-    perf_begin(ctx, kPerfCopy);
+    PerfScope timed(ctx, kPerfStageOut);
     int r = ctx->d2h_next;
     for (uint32_t first = 0; first < n; first += per_slot) {
         const uint32_t cnt = std::min(per_slot, n - first);
@@ -187,6 +192,9 @@ int kvmem_hip_stageout_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool,
         if (!launch_copy_ops(ctx, ops, "stage-out gather")) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
+        uint64_t gathered = 0;
+        for (const CopyOpDev &op : ops) gathered += op.nbytes;
+        note_xfer(ctx, kXferD2D, gathered);
         if (!hip_ok(ctx, hipEventRecord(ctx->d2h_gathered[r], ctx->stream), "d2h record") ||
             !hip_ok(ctx, hipStreamWaitEvent(ctx->copy_stream, ctx->d2h_gathered[r], 0), "d2h wait gathered")) {
             return KVMEM_HIP_ERR_RUNTIME;
@@ -210,6 +218,7 @@ int kvmem_hip_stageout_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool,
                             "d2h block copy")) {
                     return KVMEM_HIP_ERR_RUNTIME;
                 }
+                note_xfer(ctx, kXferD2H, run * g.span);
                 j += run - 1;
                 continue;
             }
@@ -220,10 +229,14 @@ int kvmem_hip_stageout_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool,
                                                 ctx->copy_stream), "d2h rows copy")) {
                     return KVMEM_HIP_ERR_RUNTIME;
                 }
+                note_xfer(ctx, kXferD2H, nt * g.row_k);
                 if (g.row_v &&
                     !hip_ok(ctx, hipMemcpyAsync(hb + o + g.run_k, db + o + g.run_k, nt * g.row_v,
                                                 hipMemcpyDeviceToHost, ctx->copy_stream), "d2h rows copy")) {
                     return KVMEM_HIP_ERR_RUNTIME;
+                }
+                if (g.row_v) {
+                    note_xfer(ctx, kXferD2H, nt * g.row_v);
                 }
             }
         }
@@ -233,7 +246,7 @@ int kvmem_hip_stageout_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool,
         r ^= 1;
     }
     ctx->d2h_next = r;
-    perf_end(ctx, kPerfCopy);
+    timed.ok();
     return KVMEM_HIP_OK;
 }
 
@@ -270,13 +283,13 @@ int kvmem_hip_stagein_packed_host(kvmem_hip_ctx *ctx, const kvmem_hip_packed_hos
                 }
             }
         }
-        perf_begin(ctx, kPerfSet);
-        const bool ok = launch_copy_ops(ctx, ops, "packed stage-in from the pinned store");
-        perf_end(ctx, kPerfSet);
-        if (ok) {
-            ctx->h2d_bytes += bytes;
+        PerfScope timed(ctx, kPerfSet);
+        if (!launch_copy_ops(ctx, ops, "packed stage-in from the pinned store")) {
+            return KVMEM_HIP_ERR_RUNTIME;
         }
-        return ok ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
+        timed.ok();
+        note_xfer(ctx, kXferH2D, bytes);
+        return KVMEM_HIP_OK;
     }
     // Pageable store: runtime copies into the stage-in ring, then a scatter.
     if (!ensure_h2d_ring(ctx, g.span)) {
@@ -286,7 +299,7 @@ int kvmem_hip_stagein_packed_host(kvmem_hip_ctx *ctx, const kvmem_hip_packed_hos
     const uint32_t per_slot = static_cast<uint32_t>(slot_bytes / g.span);
     const uint8_t *host = static_cast<const uint8_t *>(src->base);
     uint8_t *ring = static_cast<uint8_t *>(ctx->h2d_ring.ptr);
-    perf_begin(ctx, kPerfSet);
+    PerfScope timed(ctx, kPerfSet);
     int r = 0;
     for (uint32_t first = 0; first < n; first += per_slot) {
         const uint32_t cnt = std::min(per_slot, n - first);
@@ -310,7 +323,7 @@ int kvmem_hip_stagein_packed_host(kvmem_hip_ctx *ctx, const kvmem_hip_packed_hos
                         "h2d packed block copy")) {
                 return KVMEM_HIP_ERR_RUNTIME;
             }
-            ctx->h2d_bytes += run * g.span;
+            note_xfer(ctx, kXferH2D, run * g.span);
             j += run - 1;
         }
         if (!hip_ok(ctx, hipEventRecord(ctx->h2d_copied[r], ctx->copy_stream), "h2d record") ||
@@ -337,12 +350,15 @@ int kvmem_hip_stagein_packed_host(kvmem_hip_ctx *ctx, const kvmem_hip_packed_hos
         if (!launch_copy_ops(ctx, ops, "packed stage-in scatter")) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
+        uint64_t scattered = 0;
+        for (const CopyOpDev &op : ops) scattered += op.nbytes;
+        note_xfer(ctx, kXferD2D, scattered);
         if (!hip_ok(ctx, hipEventRecord(ctx->h2d_consumed[r], ctx->stream), "h2d record consumed")) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
         r = (r + 1) % kH2dRing;
     }
-    perf_end(ctx, kPerfSet);
+    timed.ok();
     return KVMEM_HIP_OK;
 }
 

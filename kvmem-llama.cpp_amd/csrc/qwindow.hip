@@ -79,7 +79,8 @@ extern "C" {
 
 int kvmem_hip_q_window_write(kvmem_hip_ctx *ctx, const void *q, int32_t q_type, uint32_t n_head,
                              uint32_t head_dim, size_t nb0, size_t nb1, size_t nb2,
-                             const uint32_t *tokens, const uint32_t *rows, uint32_t n, float *window) {
+                             const uint32_t *tokens, const uint32_t *rows, uint32_t n, float *window,
+                             uint32_t capacity) {
     if (!ctx) {
         return KVMEM_HIP_ERR_INVALID;
     }
@@ -99,12 +100,15 @@ int kvmem_hip_q_window_write(kvmem_hip_ctx *ctx, const void *q, int32_t q_type, 
     }
     const uint32_t E = n_head * head_dim;
     std::vector<uint32_t> pairs(2 * static_cast<size_t>(n));
+    std::vector<uint8_t> seen(capacity, 0);
     for (uint32_t i = 0; i < n; ++i) {
-        for (uint32_t j = 0; j < i; ++j) {
-            if (rows[j] == rows[i]) {
-                return fail(ctx, KVMEM_HIP_ERR_INVALID, "q_window_write: a row is written twice");
-            }
+        if (rows[i] >= capacity) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "q_window_write: row beyond the window's capacity");
         }
+        if (seen[rows[i]]) {
+            return fail(ctx, KVMEM_HIP_ERR_INVALID, "q_window_write: a row is written twice");
+        }
+        seen[rows[i]] = 1;
         pairs[2 * i] = tokens[i];
         pairs[2 * i + 1] = rows[i];
     }

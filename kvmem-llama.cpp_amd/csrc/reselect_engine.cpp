@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstddef>
 #include <cstring>
@@ -77,6 +78,10 @@ void fill_stats(const Plan &p, uint32_t n_staged, uint32_t n_moved, uint32_t n_s
     st->retained_position_moved = p.retained_position_moved;
     st->total_window_tokens = p.total_window_tokens;
     st->device_planned = 0;
+    st->n_skip = 0;
+    for (const kvmem_amd::Remap &r : p.remaps) {
+        st->n_skip += r.skip ? 1u : 0u;
+    }
 }
 
 // admit_incoming gives a block no slot when the free list is empty
@@ -774,6 +779,10 @@ int kvmem_engine_set_device_history(kvmem_engine *e, const void *k, const void *
     if (!k || !v) {
         return e->fail(KVMEM_HIP_ERR_INVALID, "set_device_history: null K or V");
     }
+    if ((reinterpret_cast<uintptr_t>(k) & 15u) || (reinterpret_cast<uintptr_t>(v) & 15u)) {
+        // the scorer, the key sums and every stage-in read it in 16-byte words
+        return e->fail(KVMEM_HIP_ERR_INVALID, "set_device_history: K and V must be 16-byte aligned");
+    }
     const uint64_t cap_tokens = static_cast<uint64_t>(capacity_blocks) * e->p.block_tokens;
     if (n_tokens > cap_tokens) {
         return e->fail(KVMEM_HIP_ERR_INVALID, "set_device_history: n_tokens exceeds the capacity");
@@ -1278,13 +1287,19 @@ void commit_canonical(kvmem_engine *e, const std::vector<uint32_t> &ids, Plan &p
     e->slots.reset_after(static_cast<uint32_t>(ids.size()));
 }
 
-// Whether apply_retrieval can take the device plan: the parameters and the
-// pool it covers (the resident blocks' order is checked per call).
+// Whether apply_retrieval can take the device plan: the parameters, the
+// history and the pool it covers -- every condition under which
+// kvmem_hip_reselect_device refuses a plan, so that a refusal never comes
+// after the top-k is launched (the selection size and the resident blocks'
+// order are checked per call).
 bool device_plan_ok(const kvmem_engine *e) {
     if (!e->p.device_plan || !e->p.canonical_layout || !e->hist_k || !e->hist_v || e->host_base ||
         e->packed_base || e->n_slots > KVMEM_PLAN_MAX_SLOTS || e->p.block_tokens > 65535u ||
         kvmem_hip_row_size(e->p.type_k, e->n_embd_k) % 16 != 0 ||
-        kvmem_hip_row_size(e->p.type_v, e->n_embd_v) % 16 != 0) {
+        kvmem_hip_row_size(e->p.type_v, e->n_embd_v) % 16 != 0 || e->n_embd_k % 32 != 0 ||
+        e->n_embd_v % 32 != 0 || (reinterpret_cast<uintptr_t>(e->hist_k) & 15u) ||
+        (reinterpret_cast<uintptr_t>(e->hist_v) & 15u) || e->hist_capacity < e->rt.store().block_count() ||
+        (e->has_xf && e->xf.pos0)) {
         return false;
     }
     for (uint32_t l = 0; l < e->p.n_layers; ++l) {
@@ -1507,7 +1522,8 @@ int kvmem_engine_capture_q(kvmem_engine *e, uint32_t layer, const void *q, int32
     }
     const int rc = kvmem_hip_q_window_write(e->ctx, q, q_type, e->p.n_head, e->p.head_dim, nb0, nb1, nb2,
                                             tokens.data(), rows.data(), static_cast<uint32_t>(tokens.size()),
-                                            e->d_qwin + static_cast<size_t>(layer) * e->qwin_cap * n_embd_q);
+                                            e->d_qwin + static_cast<size_t>(layer) * e->qwin_cap * n_embd_q,
+                                            e->qwin_cap);
     if (rc != KVMEM_HIP_OK) {
         return e->fail_ctx(rc, "capture_q");
     }
@@ -1605,6 +1621,7 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
     // for; on any failure the store goes back to this state, minus the
     // blocks whose pool slots the failed work may have written.
     ApplyUndo undo{e->rt, e->slots, e->dirty_tail, e->packed_valid, {}};
+    const auto t_plan = std::chrono::steady_clock::now();
     e->slots.staged_ids.clear();
     e->slots.staged_slots.clear();
     const Plan plan = e->rt.prepare_selection(ids);
@@ -1638,6 +1655,9 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
         }
     }
     int rc = KVMEM_HIP_OK;
+    // the diff and slot plan so far, plus the canonical layout's slot
+    // assignment below, are the host's plan
+    double plan_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_plan).count();
     // Evicted full blocks whose packed rows the host store lacks are copied
     // out first: the copies are ordered before the moves and stage-ins that
     // reuse their slots on the same stream.
@@ -1669,6 +1689,7 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
     uint32_t n_moved = 0;
     if (e->p.canonical_layout) {
         // window slot i holds the i-th selected block
+        const auto t_layout = std::chrono::steady_clock::now();
         std::vector<uint32_t> src, dst, ntok;
         std::vector<uint8_t> staged(n, 0);
         for (uint32_t id : stage_ids) staged[id] = 1;
@@ -1686,6 +1707,7 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
         }
         // staged ids come in ascending order, so stage_slots pairs with stage_ids
         e->slots.reset_after(static_cast<uint32_t>(ids.size()));
+        plan_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_layout).count();
         if (!src.empty()) {
             undo.written_slots.insert(undo.written_slots.end(), dst.begin(), dst.end());
             const kvmem_hip_pool pool = e->pool_desc();
@@ -1711,6 +1733,7 @@ int kvmem_engine_apply(kvmem_engine *e, uint64_t epoch, uint32_t rows, const uin
     if (!plan.stage_in.empty() || !plan.stage_out.empty() || !stage_ids.empty() || n_moved) {
         ++e->attn_epoch;  // apply_plan_to_kv / layout / write_block_to_gpu (llama-memory-kvmem.cpp:785, 964, 2735)
     }
+    kvmem_hip_perf_add_plan_ms(e->ctx, plan_ms);
     fill_stats(plan, static_cast<uint32_t>(stage_ids.size()), n_moved, n_saved, n_restored, stats);
     return KVMEM_HIP_OK;
 }

@@ -550,10 +550,19 @@ int score_launch(kvmem_hip_ctx *ctx, const kvmem_hip_score_args *args, const Sco
 constexpr size_t kNoAllocScratchBytes = size_t{8} << 20;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
-// Device address of `scratch` on each GPU, looked up once per device.
+// Device address of `scratch` on each GPU, looked up once per device, and
+// its owner: the context and stream of the last call, whose completion
+// event tells when the array is free again.  A call from another context,
+// or from the same context on another stream, while that event is pending
+// would race on the array and is refused instead.
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void *g_scratch_addr[kMaxDevices] = {};
+struct ScratchOwner {
+    const kvmem_hip_ctx *ctx = nullptr;
+    hipStream_t stream = nullptr;
+};
+ScratchOwner g_scratch_owner[kMaxDevices];
 
 }  // namespace
 
@@ -574,7 +583,18 @@ bool score_scratch_setup(kvmem_hip_ctx *ctx) {
         g_scratch_addr[ctx->device] = addr;
     }
     ctx->noalloc_scratch = g_scratch_addr[ctx->device];
-    return true;
+    // the owner record's completion event (no timing: cheap to record)
+    return hip_ok(ctx, hipEventCreateWithFlags(&ctx->noalloc_done, hipEventDisableTiming), "score scratch event");
+}
+
+void score_scratch_release(kvmem_hip_ctx *ctx) {
+    if (ctx->device < 0 || ctx->device >= kMaxDevices) {
+        return;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_owner[ctx->device].ctx == ctx) {
+        g_scratch_owner[ctx->device] = ScratchOwner{};
+    }
 }
 
 }  // namespace kvmem_hip
@@ -633,8 +653,35 @@ extern "C" int kvmem_hip_score_noalloc(kvmem_hip_ctx *ctx, const kvmem_hip_histo
                         std::to_string(kNoAllocScratchBytes) + " (use kvmem_hip_score)");
     }
     (void) hipSetDevice(ctx->device);
+    // Take the device's array: free when no call is recorded, when the last
+    // one came from this context on this stream (queued behind it), or when
+    // the last call's completion event has fired.
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ScratchOwner &own = g_scratch_owner[ctx->device];
+    if (own.ctx && !(own.ctx == ctx && own.stream == ctx->stream)) {
+        const hipError_t q = hipEventQuery(own.ctx->noalloc_done);
+        if (q == hipErrorNotReady) {
+            return fail(ctx, KVMEM_HIP_ERR_BUSY,
+                        "score_noalloc: another context or stream is still using this GPU's scratch");
+        }
+        if (q != hipSuccess) {
+            return fail(ctx, KVMEM_HIP_ERR_RUNTIME,
+                        std::string("score_noalloc: owner event: ") + hipGetErrorString(q));
+        }
+    }
     uint8_t *base = static_cast<uint8_t *>(ctx->noalloc_scratch);
     p.partial = reinterpret_cast<float *>(base);
     float *layers = args->layer_scores ? args->layer_scores : reinterpret_cast<float *>(base + layer_off);
-    return score_launch(ctx, args, p, grid, layers, false);
+    st = score_launch(ctx, args, p, grid, layers, false);
+    if (st != KVMEM_HIP_OK) {
+        return st;
+    }
+    if (!hip_ok(ctx, hipEventRecord(ctx->noalloc_done, ctx->stream), "score_noalloc completion event")) {
+        own = ScratchOwner{};  // nothing tells when the launched work ends: no owner to wait for
+        (void) hipStreamSynchronize(ctx->stream);
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    own.ctx = ctx;
+    own.stream = ctx->stream;
+    return KVMEM_HIP_OK;
 }

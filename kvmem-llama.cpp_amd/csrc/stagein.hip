@@ -2259,7 +2259,7 @@ int kvmem_hip_stagein_quant(kvmem_hip_ctx *ctx, const kvmem_hip_quant_op *ops, i
                         "stagein_quant: op needs 16-byte aligned src/dst/stride and n_embd % 32 == 0");
         }
     }
-    perf_begin(ctx, kPerfSet);
+    PerfScope timed(ctx, kPerfSet);
     for (int type : types) {
         std::vector<QuantOpDev> dev;
         uint64_t chunks = 0;
@@ -2294,7 +2294,7 @@ int kvmem_hip_stagein_quant(kvmem_hip_ctx *ctx, const kvmem_hip_quant_op *ops, i
             return KVMEM_HIP_ERR_RUNTIME;
         }
     }
-    perf_end(ctx, kPerfSet);
+    timed.ok();
     return KVMEM_HIP_OK;
 }
 
@@ -2356,9 +2356,11 @@ int kvmem_hip_stagein_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
                                bv * cap, jt, hist->n_layers, T,
                                hist->n_embd_v, 0, xp, false);
     }
-    perf_begin(ctx, kPerfSet);
+    PerfScope timed(ctx, kPerfSet);
     st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp, jt.tables.args);
-    perf_end(ctx, kPerfSet);
+    if (st == KVMEM_HIP_OK) {
+        timed.ok();
+    }
     return st;
 }
 
@@ -2423,11 +2425,14 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
             sv = make_block_source(pool->type_v, view + kbytes, span, layer_bytes, jt, L, T,
                                    hist->n_embd_v, 0, xp, false);
         }
-        perf_begin(ctx, kPerfSet);
+        PerfScope timed(ctx, kPerfSet);
         st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp, jt.tables.args);
-        perf_end(ctx, kPerfSet);
         if (st == KVMEM_HIP_OK) {
-            ctx->h2d_bytes += static_cast<uint64_t>(n) * span;
+            timed.ok();
+            // the kernel reads each block's rows of every layer over the link
+            uint64_t rows = 0;
+            for (uint32_t i = 0; i < n; ++i) rows += items[4 * i + 2];
+            note_xfer(ctx, kXferH2D, rows * L * (want_v ? kbytes + vbytes : kbytes) / T);
         }
         return st;
     }
@@ -2453,7 +2458,7 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
     if (!stage_block_job(ctx, pool, want_v, items, xp, jt)) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
-    perf_begin(ctx, kPerfSet);
+    PerfScope timed(ctx, kPerfSet);
     const uint8_t *host = static_cast<const uint8_t *>(hist->base);
     uint8_t *ring = static_cast<uint8_t *>(ctx->h2d_ring.ptr);
     int r = 0;
@@ -2472,7 +2477,6 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
                 ++run;
             }
             if (injected_fail(ctx, KVMEM_HIP_FAIL_COPY, "h2d block copy")) {
-                perf_end(ctx, kPerfSet);
                 return KVMEM_HIP_ERR_RUNTIME;
             }
             if (!hip_ok(ctx, hipMemcpyAsync(slot_base + j * span, host + static_cast<uint64_t>(b) * span,
@@ -2480,7 +2484,7 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
                         "h2d block copy")) {
                 return KVMEM_HIP_ERR_RUNTIME;
             }
-            ctx->h2d_bytes += run * span;
+            note_xfer(ctx, kXferH2D, run * span);
             j += run - 1;
         }
         if (!hip_ok(ctx, hipEventRecord(ctx->h2d_copied[r], ctx->copy_stream), "h2d record") ||
@@ -2503,7 +2507,7 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
         }
         r = (r + 1) % kRing;
     }
-    perf_end(ctx, kPerfSet);
+    timed.ok();
     return KVMEM_HIP_OK;
 }
 
@@ -2609,14 +2613,15 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
         if (!ops.empty() && !stage_copy_ops(ctx, ops, save_tables, "move_slots save")) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
-        perf_begin(ctx, kPerfLayout);
+        PerfScope timed(ctx, kPerfLayout);
         if (!launch_staged_copies(ctx, save_tables, ops.size(), "move_slots save")) {
-            perf_end(ctx, kPerfLayout);
             return KVMEM_HIP_ERR_RUNTIME;
+        }
+        if (!ops.empty()) {
+            note_xfer(ctx, kXferD2D, per_move * saved.size());
         }
         const dim3 grid(static_cast<uint32_t>((nvec + 255) / 256), static_cast<uint32_t>(segs.size()));
         if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "move_slots chain launch")) {
-            perf_end(ctx, kPerfLayout);
             return KVMEM_HIP_ERR_RUNTIME;
         }
         if (narrow) {
@@ -2624,9 +2629,12 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
         } else {
             move_chain_kernel<uint32_t><<<grid, 256, 0, ctx->stream>>>(cp, chain_tables.args);
         }
-        perf_end(ctx, kPerfLayout);
-        ctx->d2d_bytes += per_move * saved.size() + moved;
-        return hip_ok(ctx, hipGetLastError(), "move_slots chain launch") ? KVMEM_HIP_OK : KVMEM_HIP_ERR_RUNTIME;
+        if (!hip_ok(ctx, hipGetLastError(), "move_slots chain launch")) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        timed.ok();
+        note_xfer(ctx, kXferD2D, moved);
+        return KVMEM_HIP_OK;
     }
     if (!ensure_dev(ctx, ctx->move_scratch, per_move * n, "move_slots scratch")) {
         return KVMEM_HIP_ERR_NOMEM;
@@ -2790,16 +2798,19 @@ int kvmem_hip_reselect_device(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
     if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "reselect_device plan launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
-    plan_kernel<<<1, kPlanThreads, 0, ctx->stream>>>(pp, lt.args);
-    if (!hip_ok(ctx, hipGetLastError(), "reselect_device plan launch")) {
-        return KVMEM_HIP_ERR_RUNTIME;
+    {
+        PerfScope planned(ctx, kPerfPlan);
+        plan_kernel<<<1, kPlanThreads, 0, ctx->stream>>>(pp, lt.args);
+        if (!hip_ok(ctx, hipGetLastError(), "reselect_device plan launch")) {
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
+        planned.ok();
     }
     const uint32_t *counts = reinterpret_cast<const uint32_t *>(plan);
     // slot saves, then the chain walk
-    perf_begin(ctx, kPerfLayout);
+    PerfScope timed(ctx, kPerfLayout);
     if (!launch_dev_copies(ctx, reinterpret_cast<const CopyOpDev *>(plan + off_saves), counts + kPlanSaveOps,
                            ops_per * max_saves, "reselect_device saves")) {
-        perf_end(ctx, kPerfLayout);
         return KVMEM_HIP_ERR_RUNTIME;
     }
     ChainParams cp{};
@@ -2817,21 +2828,19 @@ int kvmem_hip_reselect_device(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
     cp.max_segs = max_segs;
     const uint64_t nvec = static_cast<uint64_t>(L) * cp.vec_per_layer;
     if (nvec > 0x7fffffffu) {
-        perf_end(ctx, kPerfLayout);
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "reselect_device: slot too large");
     }
     if (injected_fail(ctx, KVMEM_HIP_FAIL_LAUNCH, "reselect_device chain launch")) {
-        perf_end(ctx, kPerfLayout);
         return KVMEM_HIP_ERR_RUNTIME;
     }
     // up to kChainRows segments run side by side, one per grid row; more
     // take turns (a row's next segment waits for its stores)
     const dim3 cgrid(static_cast<uint32_t>((nvec + 255) / 256), std::min<uint32_t>(kChainRows, max_segs));
     move_chain_kernel<uint16_t><<<cgrid, 256, 0, ctx->stream>>>(cp, kNoArgTables);
-    perf_end(ctx, kPerfLayout);
     if (!hip_ok(ctx, hipGetLastError(), "reselect_device chain launch")) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
+    timed.ok();
     ctx->plan_stage_off = off_stage;
     ctx->plan_theta_off = static_cast<uint32_t>(theta_dst);
     ctx->plan_max_sel = max_sel;
@@ -2876,9 +2885,11 @@ int kvmem_hip_reselect_device_stagein(kvmem_hip_ctx *ctx, const kvmem_hip_histor
     const BlockSource sv = make_block_source(pool->type_v, static_cast<const uint8_t *>(hist->v), bv, bv * cap, jt,
                                              L, T, hist->n_embd_v, 0, xp, false);
     (void) hipSetDevice(ctx->device);
-    perf_begin(ctx, kPerfSet);
+    PerfScope timed(ctx, kPerfSet);
     const int st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, &sv, n_staged, xp, kNoArgTables);
-    perf_end(ctx, kPerfSet);
+    if (st == KVMEM_HIP_OK) {
+        timed.ok();
+    }
     return st;
 }
 
@@ -2893,8 +2904,9 @@ int kvmem_hip_reselect_device_counts(kvmem_hip_ctx *ctx, uint32_t *out, uint32_t
     for (uint32_t i = 0; i < n && i < kPlanCounts; ++i) {
         out[i] = __atomic_load_n(c + i, __ATOMIC_ACQUIRE);
     }
-    ctx->d2d_bytes += static_cast<uint64_t>(c[kPlanRows]) * ctx->plan_row_bytes +
-                      static_cast<uint64_t>(c[kPlanSaves]) * ctx->plan_save_bytes;
+    // the saves' copy launch and the chain walk
+    note_xfer(ctx, kXferD2D, static_cast<uint64_t>(c[kPlanSaves]) * ctx->plan_save_bytes, c[kPlanSaves] ? 1 : 0);
+    note_xfer(ctx, kXferD2D, static_cast<uint64_t>(c[kPlanRows]) * ctx->plan_row_bytes, c[kPlanRows] ? 1 : 0);
     return KVMEM_HIP_OK;
 }
 

@@ -474,15 +474,18 @@ int topk_launch(kvmem_hip_ctx *ctx, const float *scores, uint32_t n, const uint3
 }
 
 // Wait half: spin on the completion word of the last topk_launch.  Once the
-// wait has lasted kTopkQueryAfterUs, every few thousand rounds ask the
-// stream whether it has drained (then the word must be set) or failed.  The
-// query is held back because the runtime answers it by attaching a
-// completion signal, with a system-scope cache release, to the last command
-// queued: in a device-planned apply that is the chain walk, and its release
-// would then stall the stage-in queued behind it by several microseconds.
+// wait has lasted hold_off_us, every few thousand rounds ask the stream
+// whether it has drained (then the word must be set) or failed.  A caller
+// with work queued behind the top-k holds the query back: the runtime
+// answers it by attaching a completion signal, with a system-scope cache
+// release, to the last command queued -- in a device-planned apply the
+// chain walk, whose release would then stall the stage-in queued behind it
+// by several microseconds.  There a failed stream is seen after
+// kTopkQueryAfterUs; kvmem_hip_topk, with nothing behind the top-k, asks
+// from the first round.
 constexpr int64_t kTopkQueryAfterUs = 20000;
 
-int topk_wait(kvmem_hip_ctx *ctx, uint32_t *sel_out, uint32_t *n_sel) {
+int topk_wait(kvmem_hip_ctx *ctx, uint32_t *sel_out, uint32_t *n_sel, int64_t hold_off_us) {
     if (!ctx->topk_pending) {
         return fail(ctx, KVMEM_HIP_ERR_INVALID, "topk: no launch to wait for");
     }
@@ -492,11 +495,11 @@ int topk_wait(kvmem_hip_ctx *ctx, uint32_t *sel_out, uint32_t *n_sel) {
     const uint32_t *h = static_cast<const uint32_t *>(ctx->topk_sel_host.ptr);
     const uint32_t *done = h + topk_flag_index(n);
     const auto t0 = std::chrono::steady_clock::now();
-    bool query = false;
+    bool query = hold_off_us <= 0;
     for (uint32_t spin = 1; __atomic_load_n(done, __ATOMIC_ACQUIRE) != epoch; ++spin) {
         cpu_relax();
         if ((spin & 4095u) == 0 && !query) {
-            query = std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(kTopkQueryAfterUs);
+            query = std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(hold_off_us);
         }
         if (query && (spin & 4095u) == 0) {
             const hipError_t q = hipStreamQuery(ctx->stream);
@@ -539,7 +542,7 @@ extern "C" int kvmem_hip_topk(kvmem_hip_ctx *ctx, const float *scores, uint32_t 
     if (rc != KVMEM_HIP_OK) {
         return rc;
     }
-    return topk_wait(ctx, sel_out, n_sel);
+    return topk_wait(ctx, sel_out, n_sel, 0);
 }
 
 extern "C" int kvmem_hip_topk_launch_dev(kvmem_hip_ctx *ctx, const float *scores, uint32_t n,
@@ -559,5 +562,5 @@ extern "C" int kvmem_hip_topk_wait(kvmem_hip_ctx *ctx, uint32_t *sel_out, uint32
         return KVMEM_HIP_ERR_INVALID;
     }
     *n_sel = 0;
-    return topk_wait(ctx, sel_out, n_sel);
+    return topk_wait(ctx, sel_out, n_sel, kTopkQueryAfterUs);
 }

@@ -24,7 +24,8 @@ class PlanStats(C.Structure):
                 ("n_moved", C.c_uint32), ("selection_overlap_blocks", C.c_uint32),
                 ("gpu_reused_blocks", C.c_uint32), ("retained_position_stable", C.c_uint32),
                 ("retained_position_moved", C.c_uint32), ("total_window_tokens", C.c_uint32),
-                ("n_saved", C.c_uint32), ("n_restored", C.c_uint32), ("device_planned", C.c_uint32)]
+                ("n_saved", C.c_uint32), ("n_restored", C.c_uint32), ("device_planned", C.c_uint32),
+                ("n_skip", C.c_uint32)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}

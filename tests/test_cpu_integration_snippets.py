@@ -29,7 +29,7 @@ STRUCTS = {
     "kvmem_hip_score_args": kv.ScoreArgs, "kvmem_hip_meank_args": kv.MeanKArgs,
     "kvmem_hip_perf": kv.Perf, "kvmem_plan_stats": host.PlanStats,
     "kvmem_engine_params": host.EngineParams, "kvmem_row_range": host.RowRange,
-    "kvmem_attention_view": host.AttentionViewC,
+    "kvmem_attention_view": host.AttentionViewC, "kvmem_hip_transfer_stats": kv.TransferStats,
 }
 
 

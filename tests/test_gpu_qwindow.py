@@ -163,3 +163,40 @@ def test_window_cap_and_query_last_fallback(oracle):
         eng.reset_query()
         with pytest.raises(kv.KvMemError):
             eng.query_rows()
+
+
+def test_window_write_checks_rows_against_capacity():
+    """kvmem_hip_q_window_write refuses a row at or past the window's
+    capacity, and a row written twice, before anything is issued; rows in
+    range receive their tokens widened exactly."""
+    announce("q_window_write: rows checked against the capacity")
+    cap, nt = 6, 4
+    q = torch.randn((nt, HQ, D), dtype=torch.float32, device="cuda").to(torch.bfloat16)
+    win = torch.full((cap, EQ), -7.0, dtype=torch.float32, device="cuda")
+    nb0, nb1, nb2 = 2, D * 2, HQ * D * 2
+    with kv.Context(0) as ctx:
+        for rows in ([0, 6], [5, 5]):
+            with pytest.raises(kv.KvMemError):
+                ctx.q_window_write(q.data_ptr(), kv.TYPE_BF16, HQ, D, nb0, nb1, nb2, [0, 1], rows,
+                                   win.data_ptr(), cap)
+        ctx.sync()
+        assert bool((win == -7.0).all())
+        ctx.q_window_write(q.data_ptr(), kv.TYPE_BF16, HQ, D, nb0, nb1, nb2, [3, 1], [5, 0], win.data_ptr(), cap)
+        ctx.sync()
+    assert torch.equal(win[5], q[3].float().reshape(-1)) and torch.equal(win[0], q[1].float().reshape(-1))
+    assert bool((win[1:5] == -7.0).all())
+
+
+def test_misaligned_device_history_is_refused():
+    """Every reader of the device history (scorer, key sums, stage-in)
+    loads 16-byte words: set_device_history refuses a misaligned K or V
+    and keeps the history it had."""
+    announce("set_device_history: 16-byte alignment")
+    k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=4, Tq=4, seed=9, with_v=True)
+    with engine() as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), 4, 4 * T)
+        with pytest.raises(kv.KvMemError):
+            eng.set_device_history(k.data_ptr() + 8, v.data_ptr(), 4, 4 * T)
+        assert eng.block_count() == 4
+        st = eng.apply_retrieval(q.data_ptr(), 4)
+        assert st["n_staged"] == 4

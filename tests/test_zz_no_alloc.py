@@ -6,7 +6,10 @@ blocks, 64-token bf16 query x 24 heads) and then a smaller one (2 layers x
 300 blocks with a partial last block, 8-token f16 query, per-layer scores
 left to the scratch) -- each equal bit for bit to kvmem_hip_score on the
 same inputs, with no allocation by the context in between.  A call that
-needs more scratch than the array holds is refused before any work.
+needs more scratch than the array holds is refused before any work.  Two
+contexts on one GPU share the array in turn; a call from the second while
+the first one's call is still queued -- or from the first on another
+stream -- is refused with KVMEM_HIP_ERR_BUSY and writes nothing.
 """
 from __future__ import annotations
 
@@ -82,3 +85,59 @@ def test_score_noalloc_refuses_past_its_scratch():
             ctx.score_noalloc(hist, buf.data_ptr(), kv.TYPE_BF16, 512, HQ, HKV, D, out.data_ptr())
         assert ex.value.code == kv.ERR_INVALID and "maximum" in str(ex.value)
         ctx.sync()
+
+
+def test_score_noalloc_two_contexts_share_then_refuse_overlap():
+    announce("two contexts on one GPU: in turn, then overlapping")
+    L, B, Tq = 2, 300, 8
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=Tq, seed=7)
+    busy = torch.cuda.Stream()
+    torch.cuda.synchronize()
+
+    def out():
+        t = torch.full((B,), float("nan"), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        return t
+
+    def occupy():
+        # about 10 ms of matrix products queued on `busy` ahead of the next call
+        with torch.cuda.stream(busy):
+            x = torch.ones((4096, 4096), dtype=torch.float16, device="cuda")
+            for _ in range(64):
+                x = (x @ x) * 1e-3
+
+    with kv.Context(0) as a, kv.Context(0) as b:
+        ha = a.make_history(k.data_ptr(), None, L, B, T, E, 0)
+        hb = b.make_history(k.data_ptr(), None, L, B, T, E, 0)
+        want = out()
+        a.score(ha, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, want.data_ptr())
+        a.sync()
+        want = want.cpu().numpy()
+        # in turn: each call waited for before the other context's
+        for ctx, h in ((a, ha), (b, hb), (a, ha)):
+            got = out()
+            ctx.score_noalloc(h, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, got.data_ptr())
+            ctx.sync()
+            assert np.array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
+        # overlapping: a's call is queued behind the products, b's is refused
+        a.set_stream(busy.cuda_stream)
+        occupy()
+        got_a, got_b = out(), out()
+        a.score_noalloc(ha, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, got_a.data_ptr())
+        with pytest.raises(kv.KvMemError) as ex:
+            b.score_noalloc(hb, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, got_b.data_ptr())
+        assert ex.value.code == kv.ERR_BUSY, str(ex.value)
+        # the same context on another stream is refused as well
+        occupy()
+        a.score_noalloc(ha, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, got_a.data_ptr())
+        a.set_stream(None)
+        with pytest.raises(kv.KvMemError) as ex:
+            a.score_noalloc(ha, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, got_b.data_ptr())
+        assert ex.value.code == kv.ERR_BUSY, str(ex.value)
+        busy.synchronize()
+        assert np.isnan(got_b.cpu().numpy()).all()          # the refused calls wrote nothing
+        assert np.array_equal(got_a.cpu().numpy().view(np.uint32), want.view(np.uint32))
+        # once the work is done, b takes the array
+        b.score_noalloc(hb, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, got_b.data_ptr())
+        b.sync()
+        assert np.array_equal(got_b.cpu().numpy().view(np.uint32), want.view(np.uint32))
