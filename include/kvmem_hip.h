@@ -396,11 +396,11 @@ KVMEM_HIP_API int kvmem_hip_score(kvmem_hip_ctx *ctx,
  * needing more returns KVMEM_HIP_ERR_INVALID before any work (the 256K
  * workload -- 16 layers x 2048 blocks, 4 KV heads, 64 query tokens x 24
  * heads -- needs 2.1 MiB).  Every call on one GPU shares that GPU's array
- * and overwrites it (nothing in it has to start at zero).  Calls queued on
- * one context's stream follow each other; a call from another context, or
- * from the same context on another stream, while the last call on the
- * array has not finished returns KVMEM_HIP_ERR_BUSY with nothing issued
- * (the caller synchronises, or uses kvmem_hip_score).  The array's last
+ * and overwrites it (nothing in it has to start at zero).  One context's
+ * calls follow each other (kvmem_hip_set_stream waits for the old stream);
+ * a call from another context while the last call on the array has not
+ * finished returns KVMEM_HIP_ERR_BUSY with nothing issued (the caller
+ * synchronises, or uses kvmem_hip_score).  The array's last
  * user is tracked on the host: two processes on one GPU each have their
  * own array.  Not timed by kvmem_hip_perf_*. */
 KVMEM_HIP_API int kvmem_hip_score_noalloc(kvmem_hip_ctx *ctx,

@@ -552,9 +552,10 @@ static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 // Device address of `scratch` on each GPU, looked up once per device, and
 // its owner: the context and stream of the last call, whose completion
-// event tells when the array is free again.  A call from another context,
-// or from the same context on another stream, while that event is pending
-// would race on the array and is refused instead.
+// event tells when the array is free again.  A call from another context
+// while that event is pending would race on the array and is refused
+// instead (a context's own calls are ordered: set_stream waits for the old
+// stream).
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void *g_scratch_addr[kMaxDevices] = {};
