@@ -23,8 +23,11 @@ the same steps timed again without any event, and
 top-k and slot-move parts); `host_planned` is the same step with the diff and slot plan
 on the host, `lifo_layout` the same step without the slot moves.  `mixed_precision` (Student-t history, K q8_0 +
 V q4_0, then K and V q5_0) and `recall_1m` (8192 blocks, 512-token query,
-32 planted blocks, budget 512) are the other workloads' steps, in the same
-line unless --no-configs.  `roofline` is the MFMA block scorer
+32 planted blocks, budget 512) are the other workloads' steps, and
+`meank_256k` (the reference's own mean-K scorer) and `cache_transform` (RoPE +
+attn_rot before q8_0) the same 256K step in its other modes, in the same
+line unless --no-configs.  `transfers_per_step` is one step's data movement
+per direction (kvmem_hip_transfer_get).  `roofline` is the MFMA block scorer
 (the dominant kernel); `stagein_roofline` the q8_0 stage-in kernel against
 HBM; `pinned_host` the same stage-in fed over PCIe from pinned host memory,
 and the same blocks as packed q8_0 rows copied out to (`packed_stageout`)
@@ -32,7 +35,7 @@ and restored from (`packed_stagein`) a pinned packed store, and `step` the
 whole reselect step with the F16 history staged from pinned host memory
 (the keys also in HBM for the scorer), again with a packed host store
 (`with_packed_store`: incoming blocks restored from their q8_0 rows); `cpu_baseline`
-the oracle's restatement of the step on the host cores.
+the oracle's restatement of the whole step measured on the host cores.
 """
 from __future__ import annotations
 
@@ -128,6 +131,7 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
         torch.cuda.synchronize()
         times.append(time.perf_counter() - t0)
         pf = ctx.perf()
+        xfer = ctx.transfers()  # this step's data movement, per direction
         ctx.perf_enable(False)
         score_ms += pf["score_ms"]
         set_ms += pf["set_ms"]
@@ -165,7 +169,7 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
             "score_ms": score_ms / steps,
             "set_ms": set_ms / steps, "sel_ms": sel_ms / steps, "n_staged": staged[0],
             "layout_ms": layout_ms / steps, "n_moved": max(moved), "d2d_bytes": d2d_bytes // steps,
-            "device_planned": min(planned), "after_score_ms": after_ms / steps}
+            "device_planned": min(planned), "after_score_ms": after_ms / steps, "transfers": xfer}
 
 
 def stage_bytes(kv, n_blocks: int, type_k: int, type_v: int) -> int:
@@ -175,11 +179,15 @@ def stage_bytes(kv, n_blocks: int, type_k: int, type_v: int) -> int:
 
 
 # ------------------------------------------------------------ cpu baseline
-def cpu_baseline(torch, k, v, q, sel_ids: list[int], budget_s: float = 12.0) -> dict:
-    """The oracle's restatement of the step on the host cores: fp32 per-token
-    max scorer (OpenMP) on a sample of blocks, sort-based top-k, and the
-    reference q8_0 quantizer over a sample of the staged blocks (thread
-    pool), each scaled to the full step."""
+def cpu_baseline(torch, k, v, q, sel_ids: list[int]) -> dict:
+    """The oracle's restatement of the whole step on the host cores, over
+    the same inputs, measured in full: the fp32 per-token max scorer
+    (OpenMP) on every block of every layer, the sort-based top-k over the
+    2048 scores, and the reference q8_0 quantizer on every staged block's K
+    and V rows of every layer (thread pool).  Beside it, measured in full
+    too: the reference's own mean-K scorer (one thread, as the adapter runs
+    it) over every block's key sums, the q8_0 quantizer on one thread, and
+    the host memcpy of the staged blocks' packed rows."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import kvmem_oracle as oracle
 
@@ -192,50 +200,43 @@ def cpu_baseline(torch, k, v, q, sel_ids: list[int], budget_s: float = 12.0) -> 
         idx = torch.tensor(ids, dtype=torch.long, device=t.device)
         return t[:, idx].contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
 
-    # scoring: probe 8 blocks, then a sample sized to ~budget_s * 0.8
-    probe = host_blocks(k, list(range(8)))
+    # scoring: every block of every layer (the keys copied to the host first, untimed)
+    kh = k.cpu().view(torch.int16).numpy().view(np.uint16)
     t0 = time.perf_counter()
-    oracle.score_pertoken_max_f32(qf, probe, 0, 8, threads)
-    per_block = (time.perf_counter() - t0) / 8
-    n_sample = int(min(B, max(16, (0.8 * budget_s) / max(per_block, 1e-6))))
-    sample_ids = list(range(0, B, max(1, B // n_sample)))[:n_sample]
-    ks = host_blocks(k, sample_ids)
-    t0 = time.perf_counter()
-    ls = oracle.score_pertoken_max_f32(qf, ks, 0, len(sample_ids), threads)
-    score_s = (time.perf_counter() - t0) * B / len(sample_ids)
-    del ks
-    # top-k over a full score vector (the sampled ones tiled)
-    sc = np.resize(ls.mean(axis=0).astype(np.float64), B)
+    ls = oracle.score_pertoken_max_f32(qf, kh, 0, B, threads)
+    score_s = time.perf_counter() - t0
+    del kh
+    sc = ls.astype(np.float64).mean(axis=0)
     t0 = time.perf_counter()
     oracle.pick_topk(sc, BUDGET, sink=1)
     topk_s = time.perf_counter() - t0
-    # stage-in quantize: 8 staged blocks x 16 layers x K/V, thread pool
-    n_q = min(8, len(sel_ids))
-    kb = host_blocks(k, sel_ids[:n_q])
-    vb = host_blocks(v, sel_ids[:n_q])
+    # stage-in quantize: every staged block x 16 layers x K/V, thread pool
+    n_q = len(sel_ids)
+    kb = host_blocks(k, sel_ids)
+    vb = host_blocks(v, sel_ids)
     jobs = [(src[l, i].reshape(T, E)) for src in (kb, vb) for l in range(L) for i in range(n_q)]
     t0 = time.perf_counter()
     with cf.ThreadPoolExecutor(threads) as ex:
         list(ex.map(lambda r: oracle.quantize_rows_f16(oracle.TYPE_Q8_0, r), jobs))
-    quant_s = (time.perf_counter() - t0) * N_CHANGED / n_q
+    quant_s = time.perf_counter() - t0
     total_ms = (score_s + topk_s + quant_s) * 1e3
-    # the reference's own scorer (mean-K cosine, single thread as in the
-    # adapter) over key sums of 256 sampled blocks, scaled to every block
-    rng = np.random.default_rng(1)
-    n_mk = 256
-    k_sum = rng.standard_normal((L, n_mk, E)).astype(np.float32)
+    # the reference's own scorer (mean-K cosine, one thread as in the
+    # adapter) over the real key sums of every block (made on the device,
+    # untimed: they are kept per block, not made per step)
+    k_sum = k.float().sum(dim=2).reshape(L, B, E).cpu().numpy()
     q_sum = qf.sum(axis=1).reshape(L, HQ * D).astype(np.float32)
     t0 = time.perf_counter()
-    oracle.score_meank(q_sum, [TQ] * L, k_sum, np.full((L, n_mk), T, np.uint32), HQ, HKV, D)
-    meank_s = (time.perf_counter() - t0) * B / n_mk
+    oracle.score_meank(q_sum, [TQ] * L, k_sum, np.full((L, B), T, np.uint32), HQ, HKV, D)
+    meank_s = time.perf_counter() - t0
+    del k_sum
     # q8_0 quantize on one thread (the same jobs, serial)
     t0 = time.perf_counter()
-    for r in jobs[: 2 * L]:
+    for r in jobs:
         oracle.quantize_rows_f16(oracle.TYPE_Q8_0, r)
-    quant1_s = (time.perf_counter() - t0) * len(jobs) / (2 * L) * N_CHANGED / n_q
+    quant1_s = time.perf_counter() - t0
     # the reference's live stage-in on the host: a memcpy of the changed
     # blocks' packed q8_0 rows into the staging slab (write_block_to_gpu)
-    packed = np.ones(N_CHANGED * L * 2 * T * 1088, dtype=np.uint8)
+    packed = np.ones(n_q * L * 2 * T * 1088, dtype=np.uint8)
     slab = np.zeros_like(packed)
     slab.fill(2)  # the slab's pages are resident, as the reference's pinned slab
     memcpy_s = None
@@ -247,15 +248,14 @@ def cpu_baseline(torch, k, v, q, sel_ids: list[int], budget_s: float = 12.0) -> 
     return {
         "value": round(total_ms, 1), "unit": "ms/step", "cores": threads, "kind": "port",
         "host_cpus_visible": visible, "cpu_share_per_gpu": HOST_CPU_SHARE,
-        "sample": (f"fp32 per-token max scorer on {len(sample_ids)} of {B} blocks x {L} layers "
-                   f"(OpenMP, {threads} threads) scaled x{B / len(sample_ids):.1f}; top-256 over "
-                   f"{B} scores; q8_0 quantize of {n_q} of {N_CHANGED} staged blocks x {L} layers "
-                   f"x K/V ({threads} threads) scaled x{N_CHANGED / n_q:.2f}"),
+        "sample": (f"the whole step measured, no scaling: fp32 per-token max scorer on all {B} blocks "
+                   f"x {L} layers (OpenMP, {threads} threads); top-{BUDGET} over {B} scores; q8_0 "
+                   f"quantize of all {n_q} staged blocks x {L} layers x K/V ({threads} threads)"),
         "parts_ms": {"score": round(score_s * 1e3, 1), "topk": round(topk_s * 1e3, 3),
                      "quantize": round(quant_s * 1e3, 1)},
         "other_legs": {
             "meank_score_ms": round(meank_s * 1e3, 2),
-            "meank_sample": f"mean-K cosine scorer (1 thread) on {n_mk} of {B} blocks x {L} layers, scaled",
+            "meank_sample": f"mean-K cosine scorer (1 thread) on all {B} blocks x {L} layers",
             "quantize_1thread_ms": round(quant1_s * 1e3, 1),
             "packed_memcpy_ms": round(memcpy_s * 1e3, 2),
             "packed_memcpy_GBs": round(packed.nbytes / memcpy_s / 1e9, 2),
@@ -422,6 +422,7 @@ def run_reselect_256k(a, torch, kv, workloads) -> dict:
         "parts_ms": {"score_kernel": round(m["score_ms"], 4), "topk_kernel": round(m["sel_ms"], 4),
                      "layout_kernels": round(m["layout_ms"], 4), "stagein_kernel": round(m["set_ms"], 4)},
         "after_score_ms": round(m["after_score_ms"], 4),
+        "transfers_per_step": m["transfers"],
     }
     if not a.no_pinned:
         incoming = sorted(set(sel) - set(prev))
@@ -433,6 +434,9 @@ def run_reselect_256k(a, torch, kv, workloads) -> dict:
     result["device_planned"] = m["device_planned"]
     result["host_planned"] = host_planned_mode(a, torch, kv, k, v, q, prev)
     result["lifo_layout"] = lifo_layout_mode(a, torch, kv, k, v, q, prev)
+    if not a.no_configs:
+        result["meank_256k"] = run_meank_256k(a, torch, kv, workloads, (k, v, q))
+        result["cache_transform"] = run_cache_transform(a, torch, kv, workloads, (k, v, q))
     if not a.no_pinned:
         result["pinned_host"]["step"] = pinned_host_step(a, torch, kv, k, v, q, prev)
     del k, v, q
@@ -507,15 +511,20 @@ def run_mixed_precision(a, torch, kv, workloads) -> dict:
             "data": "synthetic (seeded Student-t nu=4 K/V, bf16 query)", "runs": runs}
 
 
-def run_cache_transform(a, torch, kv, workloads) -> dict:
+def run_cache_transform(a, torch, kv, workloads, tensors=None) -> dict:
     """The 256K step with the cache row transform on: the 77 changed blocks
     are RoPE'd at their original positions (256 rotary dims, base 1e6) and
     Walsh-Hadamard rotated (K width 256, V width 64) before q8_0.  Beside it,
     `transform_parts`: the stage-in alone (no scorer before it), 77 distinct
-    random blocks per call, with each part of the transform on its own."""
-    log("generating history K/V [16][2048][128][4][256] f16 and query")
-    k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=TQ, seed=2, with_v=True)
-    torch.cuda.synchronize()
+    random blocks per call, with each part of the transform on its own.
+    `tensors` = (k, v, q) of the 256K workload when the caller has them."""
+    if tensors is None:
+        log("generating history K/V [16][2048][128][4][256] f16 and query")
+        k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=TQ, seed=2, with_v=True)
+        torch.cuda.synchronize()
+    else:
+        k, v, q = tensors
+    log("cache transform step: RoPE 256 + attn_rot before q8_0")
     eng = make_engine(kv, torch, k, v, n_rot=256, rope_freq_base=1e6, attn_rot=1)
     ctx = kv.Context.borrow(eng.ctx_handle())
     sel = eng.preview(q.data_ptr(), TQ).blocks
@@ -636,14 +645,19 @@ def run_scorer_sustained(a, torch, kv, workloads) -> dict:
     return out
 
 
-def run_meank_256k(a, torch, kv, workloads) -> dict:
+def run_meank_256k(a, torch, kv, workloads, tensors=None) -> dict:
     """The 256K step with the reference's mean-K cosine scorer: per-block
     key sums are produced once (untimed warmup) and kept; a step sums the
     query rows, scores every block from the sums (128 MiB of fp32) and
-    stages the changed blocks."""
-    log("generating history K/V [16][2048][128][4][256] f16 and query")
-    k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=TQ, seed=2, with_v=True)
-    torch.cuda.synchronize()
+    stages the changed blocks.  `tensors` = (k, v, q) of the 256K workload
+    when the caller has them."""
+    if tensors is None:
+        log("generating history K/V [16][2048][128][4][256] f16 and query")
+        k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=TQ, seed=2, with_v=True)
+        torch.cuda.synchronize()
+    else:
+        k, v, q = tensors
+    log("mean-K step: the reference's scorer over kept key sums")
     eng = make_engine(kv, torch, k, v, scorer=1)
     ctx = kv.Context.borrow(eng.ctx_handle())
     sel = eng.preview(q.data_ptr(), TQ).blocks
@@ -657,6 +671,7 @@ def run_meank_256k(a, torch, kv, workloads) -> dict:
             "score_roofline": {"bound": "hbm", "kernel": "meank_cos_kernel<256>",
                                "achieved": round(sums_bytes / (m["score_ms"] * 1e-3) / 1e9, 1),
                                "peak": HBM_PEAK_GBS, "unit": "GB/s", "algorithmic_bytes": sums_bytes,
+                               "frac": round(sums_bytes / (m["score_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                "score_ms": round(m["score_ms"], 4)},
             "ms_per_step_no_timing_events": round(m["ms_step_no_events"], 4),
             "parts_ms": {"score": round(m["score_ms"], 4), "stagein_kernel": round(m["set_ms"], 4),

@@ -8,6 +8,11 @@
 - The full reselect step @256K through the engine (canonical layout, 77 of
   256 blocks changed): every staged block and a sample of the moved ones
   bit-exact in their slots, slot i holding the i-th selected block.
+- The same step with the history in pinned host memory, block-major as the
+  reference keeps it in host RAM (16 GiB, every block): the 77 changed
+  blocks read over the link and quantized, every one bit-exact; then with a
+  pinned packed host store, the evicted blocks' q8_0 rows saved bit-exact
+  and the 77 blocks restored from them bit-exact.
 - Mixed precision @256K (Student-t nu = 4): K q8_0 + V q4_0, then K and V
   q5_0 with a 96-block reserve; every staged block bit-exact.
 - 1M workspace (16 layers x 8192 blocks, 512-token query, 32 planted
@@ -154,6 +159,51 @@ def test_reselect_256k_engine_step_bit_exact(oracle):
         sample = sorted(rng.choice(moved, 16, replace=False).tolist()) if len(moved) > 16 else moved
         check_blocks_in_pool(eng, oracle, k, v, staged + sample, kv.TYPE_Q8_0, kv.TYPE_Q8_0)
     del k, v, q
+    torch.cuda.empty_cache()
+
+
+def test_reselect_256k_pinned_host_step_bit_exact(oracle):
+    announce("pinned-host step @256K: 77 changed blocks read over the link from 16 GiB of block-major "
+             "pinned history, then saved to and restored from a pinned packed store")
+    B, Tq = 2048, 64
+    k, v, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=Tq, seed=2, with_v=True)
+    span_el = L * 2 * T * E
+    hist = torch.empty((B, span_el), dtype=torch.float16, pin_memory=True)
+    hv = hist.view(B, L, 2, T * E)
+    for layer in range(L):
+        hv[:, layer, 0].copy_(k[layer].reshape(B, T * E))
+        hv[:, layer, 1].copy_(v[layer].reshape(B, T * E))
+    torch.cuda.synchronize()
+    row = kv.row_size(kv.TYPE_Q8_0, E)
+    with engine() as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), B, B * T)   # the scorer's keys
+        eng.set_host_history(hist.data_ptr(), B)                        # the stage-in's source
+        sel = eng.preview(q.data_ptr(), Tq)
+        prev = workloads.previous_selection(sel.blocks, B, 77)
+        eng.apply(host.Selection(eng.epoch(), eng.total_tokens(), prev))
+        st = eng.apply_retrieval(q.data_ptr(), Tq)
+        assert st["n_staged"] == 77 and st["n_restored"] == 0
+        staged = sorted(set(sel.blocks) - set(prev))
+        check_blocks_in_pool(eng, oracle, k, v, staged, kv.TYPE_Q8_0, kv.TYPE_Q8_0)
+        announce("packed host store: the 77 blocks evicted (saved), then restored from their rows")
+        packed = torch.zeros((B, L * 2 * T * row), dtype=torch.uint8, pin_memory=True)
+        eng.set_packed_host(packed.data_ptr(), B)
+        back = eng.apply(host.Selection(eng.epoch(), eng.total_tokens(), prev))
+        assert back["n_saved"] == 77 and back["n_staged"] == 77
+        assert all(eng.packed_valid(b) for b in staged)
+        idx = torch.tensor(staged, dtype=torch.long, device="cuda")
+        kb = workloads.to_bits(torch, k[:, idx])
+        vb = workloads.to_bits(torch, v[:, idx])
+        pk = packed.numpy()[staged].reshape(len(staged), L, 2, T, row)
+        for layer in range(L):
+            for j in range(len(staged)):
+                for which, src in ((0, kb), (1, vb)):
+                    want = oracle.quantize_rows_f16(kv.TYPE_Q8_0, src[layer, j].reshape(T, E))
+                    assert np.array_equal(pk[j, layer, which], want), (layer, "KV"[which], staged[j])
+        fwd = eng.apply_retrieval(q.data_ptr(), Tq)
+        assert fwd["n_staged"] == 77 and fwd["n_restored"] == 77
+        check_blocks_in_pool(eng, oracle, k, v, staged, kv.TYPE_Q8_0, kv.TYPE_Q8_0)
+    del k, v, q, hist, hv, packed
     torch.cuda.empty_cache()
 
 
