@@ -183,6 +183,16 @@ KVMEM_HIP_API int kvmem_store_commit_unchanged(kvmem_store *s, const kvmem_atten
  * llama-kvmem-hooks.h:156; llama-memory-kvmem.cpp:3002-3024). */
 KVMEM_HIP_API int kvmem_store_can_append(const kvmem_store *s, uint32_t end, uint32_t generation_rows,
                                          int all_history, const char **reason);
+/* 1 when replaying the query rows [query_begin, prompt_end) fits the
+ * selection budget beside the sink blocks (the blocks from query_begin's on
+ * plus the sink; 1 with no budget or an empty range) -- the adapter's
+ * query_replay_fits (llama_kvmem_query_replay_fits, llama-kvmem-hooks.h:103;
+ * llama-memory-kvmem.cpp:3502-3524). */
+KVMEM_HIP_API int kvmem_store_query_replay_fits(const kvmem_store *s, uint32_t query_begin,
+                                                uint32_t prompt_end);
+/* Slots the LIFO free list still holds (llama_kvmem_free_slots,
+ * llama-kvmem-hooks.h:85). */
+KVMEM_HIP_API uint32_t kvmem_store_free_slots(const kvmem_store *s);
 
 /* ------------------------------------------------------ reselect engine */
 
@@ -365,8 +375,9 @@ KVMEM_HIP_API int kvmem_engine_retrieval_mandatory(const kvmem_engine *e, uint32
 KVMEM_HIP_API int kvmem_engine_capture_q(kvmem_engine *e, uint32_t layer, const void *q,
                                          int32_t q_type, size_t nb0, size_t nb1, size_t nb2,
                                          uint32_t n_tokens, const int32_t *positions);
-/* Empty the query window (llama_kvmem_reset_query, llama-kvmem-hooks.h:71;
- * reset_query_acc, llama-memory-kvmem.cpp:2059-2064). */
+/* Empty the query window and drop a state set by kvmem_engine_set_query
+ * (llama_kvmem_reset_query, llama-kvmem-hooks.h:71; reset_query_acc,
+ * llama-memory-kvmem.cpp:2059-2064); a frozen query stays frozen. */
 KVMEM_HIP_API int kvmem_engine_reset_query(kvmem_engine *e);
 /* Query rows a window preview would read: the newest query_max_tokens
  * captured rows, or the newest query_last with no span set. */
@@ -464,6 +475,30 @@ KVMEM_HIP_API int kvmem_engine_commit_resident(kvmem_engine *e, int canonical);
  * 3002-3024): as kvmem_store_can_append, over the engine's pool. */
 KVMEM_HIP_API int kvmem_engine_can_append(const kvmem_engine *e, uint32_t end, uint32_t generation_rows,
                                           int all_history, const char **reason);
+/* As kvmem_store_query_replay_fits / kvmem_store_free_slots, over the
+ * engine's store and pool (llama-kvmem-hooks.h:85, 103). */
+KVMEM_HIP_API int kvmem_engine_query_replay_fits(const kvmem_engine *e, uint32_t query_begin,
+                                                 uint32_t prompt_end);
+KVMEM_HIP_API uint32_t kvmem_engine_free_slots(const kvmem_engine *e);
+
+/* Query state (llama_kvmem_query_state {sum, count}, llama-kvmem-hooks.h:
+ * 139-142, 162-164): per layer the sum of the query rows (n_head*head_dim
+ * f32) and their count, the input of the reference's mean-K scorer.
+ * get: host q_sum [n_layers][n_head*head_dim], q_count [n_layers] receive
+ * the state a preview with q = NULL would use -- the rows of the query
+ * window summed in token order, or the state set_query set (ERR_INVALID
+ * with no captured rows; llama-memory-kvmem.cpp:3104-3119).
+ * set: the caller's state replaces the window for previews with q = NULL
+ * and freezes the query (capture_q keeps no rows) until reset_query or
+ * freeze_query(0) (llama-memory-kvmem.cpp:3121-3137); sums must be finite
+ * and the counts equal and nonzero (ERR_INVALID, nothing changed).  The
+ * per-token scorer reads the rows themselves, not their sum:
+ * ERR_UNSUPPORTED on an engine with scorer = KVMEM_SCORER_TOKEN_MAX.
+ * freeze: while frozen, capture_q keeps no rows (query_contains is false,
+ * llama-memory-kvmem.cpp:2950-2951). */
+KVMEM_HIP_API int kvmem_engine_get_query(kvmem_engine *e, float *q_sum, uint32_t *q_count);
+KVMEM_HIP_API int kvmem_engine_set_query(kvmem_engine *e, const float *q_sum, const uint32_t *q_count);
+KVMEM_HIP_API int kvmem_engine_freeze_query(kvmem_engine *e, int frozen);
 
 /* Scores of the last preview (host copy, block count entries). */
 KVMEM_HIP_API int kvmem_engine_scores(kvmem_engine *e, float *out, uint32_t n);

@@ -575,6 +575,26 @@ bool commit_resident(KvMemRuntime &rt, const PoolState &p, bool canonical) {
     return v.valid && rt.commit_resident_selection(v.blocks);
 }
 
+bool query_replay_fits(const KvMemStore &s, uint32_t query_begin, uint32_t prompt_end) {
+    if (query_begin >= prompt_end) {
+        return true;
+    }
+    const uint64_t bt = std::max(1u, s.config().block_tokens);
+    const uint64_t budget = s.budget_blocks();
+    if (budget == 0) {
+        return true;
+    }
+    const uint64_t total_blocks = (static_cast<uint64_t>(prompt_end) + bt - 1) / bt;
+    const uint64_t boundary = query_begin / bt;
+    if (boundary >= total_blocks) {
+        return true;
+    }
+    const uint64_t sink = std::min<uint64_t>(s.config().sink_blocks, total_blocks);
+    // the query blocks from the boundary on, plus the sink ahead of them
+    const uint64_t required = boundary < sink ? total_blocks : sink + (total_blocks - boundary);
+    return required <= budget;
+}
+
 bool can_append(const KvMemStore &s, const PoolState &p, uint32_t end, uint32_t generation_rows,
                 bool all_history, const char **reason) {
     const char *why = nullptr;

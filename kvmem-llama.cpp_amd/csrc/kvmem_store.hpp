@@ -272,6 +272,10 @@ bool commit_unchanged(KvMemRuntime &rt, const PoolState &p, const AttentionView 
                       uint64_t sel_epoch, uint32_t sel_rows, const std::vector<uint32_t> &sel);
 // commit_resident (llama-memory-kvmem.cpp:3098-3102).
 bool commit_resident(KvMemRuntime &rt, const PoolState &p, bool canonical);
+// query_replay_fits (llama-memory-kvmem.cpp:3502-3524): whether replaying
+// the query rows [query_begin, prompt_end) fits the selection budget beside
+// the sink blocks (true with no budget or an empty query).
+bool query_replay_fits(const KvMemStore &s, uint32_t query_begin, uint32_t prompt_end);
 // can_append (llama-memory-kvmem.cpp:3002-3024): whether rows up to end
 // plus generation_rows can be decoded onto the current pool without a
 // reselect; *reason receives the adapter's reason string.

@@ -255,6 +255,14 @@ int kvmem_store_commit_unchanged(kvmem_store *s, const kvmem_attention_view *bef
                : 0;
 }
 
+int kvmem_store_query_replay_fits(const kvmem_store *s, uint32_t query_begin, uint32_t prompt_end) {
+    return !s || kvmem_amd::query_replay_fits(s->rt.store(), query_begin, prompt_end) ? 1 : 0;
+}
+
+uint32_t kvmem_store_free_slots(const kvmem_store *s) {
+    return s ? s->slots.n_free() : 0u;
+}
+
 int kvmem_store_can_append(const kvmem_store *s, uint32_t end, uint32_t generation_rows, int all_history,
                            const char **reason) {
     if (!s) {
@@ -402,6 +410,9 @@ struct kvmem_engine {
     void *d_qgather = nullptr; // its rows in token order for the scorer, bf16
     uint32_t qwin_cap = 0;
     std::vector<uint64_t> qwin_count;  // rows captured per layer since the reset
+    bool query_frozen = false;         // capture_q keeps no rows (freeze_query, set_query)
+    bool query_imported = false;       // d_qsum holds sums set by set_query
+    std::vector<uint32_t> imp_count;   // their row counts per layer
     void *packed_base = nullptr;        // pinned packed host store (may be null)
     uint32_t packed_capacity = 0;       // blocks it holds
     std::vector<uint8_t> packed_valid;  // block's packed rows are in the store
@@ -1176,9 +1187,14 @@ int preview_scores(kvmem_engine *e, const void *q, int32_t q_type, uint32_t n_q_
         return e->fail(KVMEM_HIP_ERR_INVALID, "preview: no device history (the scorer reads keys in HBM)");
     }
     const uint32_t n = e->rt.store().block_count();
-    // no query pointer: the captured query window, its newest rows in token order
+    // no query pointer: the sums set by set_query, or the captured query
+    // window, its newest rows in token order
     std::vector<uint32_t> win_rows;
-    if (!q) {
+    const bool imported = !q && e->query_imported;
+    if (imported && e->p.scorer != KVMEM_SCORER_MEAN_K) {
+        return e->fail(KVMEM_HIP_ERR_UNSUPPORTED, "preview: a set query holds row sums; the per-token scorer needs rows");
+    }
+    if (!q && !imported) {
         const int rc = window_rows(e, win_rows);
         if (rc != KVMEM_HIP_OK) {
             return rc;
@@ -1200,6 +1216,10 @@ int preview_scores(kvmem_engine *e, const void *q, int32_t q_type, uint32_t n_q_
         return KVMEM_HIP_OK;
     }
     const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
+    if (imported) {
+        // the set query's sums and counts, as q_sum_ / q_count_ after set_query
+        return meank_scores(e, e->d_qsum, e->imp_count.data());
+    }
     if (e->p.scorer == KVMEM_SCORER_MEAN_K) {
         // the reference's scorer over the sum of the query rows
         if (!e->d_qsum &&
@@ -1494,9 +1514,10 @@ int kvmem_engine_capture_q(kvmem_engine *e, uint32_t layer, const void *q, int32
         return e->fail(KVMEM_HIP_ERR_INVALID, "capture_q: bad layer or null argument");
     }
     // the rows of the query (all of them when no span is set: the preview
-    // then takes the newest query_last)
+    // then takes the newest query_last); none while the query is frozen
+    // (query_contains is false then, llama-memory-kvmem.cpp:2950-2951)
     std::vector<uint32_t> kept;
-    for (uint32_t i = 0; i < n_tokens; ++i) {
+    for (uint32_t i = 0; i < n_tokens && !e->query_frozen; ++i) {
         if (!e->spans_set() || e->query_contains(positions[i])) {
             kept.push_back(i);
         }
@@ -1536,6 +1557,7 @@ int kvmem_engine_reset_query(kvmem_engine *e) {
         return KVMEM_HIP_ERR_INVALID;
     }
     std::fill(e->qwin_count.begin(), e->qwin_count.end(), 0);
+    e->query_imported = false;  // reset_query_acc zeroes q_sum_ / q_count_
     return KVMEM_HIP_OK;
 }
 
@@ -1799,6 +1821,99 @@ int kvmem_engine_append_resident(kvmem_engine *e, uint32_t n_new_tokens) {
         e->dirty_tail = tail_id;
     }
     ++e->epoch;  // the history grew: earlier selections are stale (their rows differ)
+    return KVMEM_HIP_OK;
+}
+
+uint32_t kvmem_engine_free_slots(const kvmem_engine *e) {
+    return e ? e->slots.n_free() : 0u;
+}
+
+int kvmem_engine_query_replay_fits(const kvmem_engine *e, uint32_t query_begin, uint32_t prompt_end) {
+    return !e || kvmem_amd::query_replay_fits(e->rt.store(), query_begin, prompt_end) ? 1 : 0;
+}
+
+int kvmem_engine_get_query(kvmem_engine *e, float *q_sum, uint32_t *q_count) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!q_sum || !q_count) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "get_query: null argument");
+    }
+    const uint32_t L = e->p.n_layers;
+    const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
+    const size_t bytes = sizeof(float) * static_cast<size_t>(L) * n_embd_q;
+    if (!e->d_qsum && hipMalloc(&e->d_qsum, bytes) != hipSuccess) {
+        e->d_qsum = nullptr;
+        return e->fail(KVMEM_HIP_ERR_NOMEM, "get_query: query sums");
+    }
+    if (!e->query_imported) {
+        // the rows a preview would read, summed in token order
+        std::vector<uint32_t> rows;
+        const int rc = window_rows(e, rows);
+        if (rc != KVMEM_HIP_OK) {
+            return rc;
+        }
+        const int arc = kvmem_hip_q_accumulate(e->ctx, e->d_qwin, KVMEM_TYPE_F32, L, e->qwin_cap, n_embd_q,
+                                               rows.data(), static_cast<uint32_t>(rows.size()), 1, e->d_qsum);
+        if (arc != KVMEM_HIP_OK) {
+            return e->fail_ctx(arc, "get_query: sums");
+        }
+        std::fill(q_count, q_count + L, static_cast<uint32_t>(rows.size()));
+    } else {
+        std::copy(e->imp_count.begin(), e->imp_count.end(), q_count);
+    }
+    hipStream_t st = static_cast<hipStream_t>(kvmem_hip_get_stream(e->ctx));
+    if (hipMemcpyAsync(q_sum, e->d_qsum, bytes, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+        return e->fail(KVMEM_HIP_ERR_RUNTIME, "get_query: copy");
+    }
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_set_query(kvmem_engine *e, const float *q_sum, const uint32_t *q_count) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    if (!q_sum || !q_count) {
+        return e->fail(KVMEM_HIP_ERR_INVALID, "set_query: null argument");
+    }
+    if (e->p.scorer != KVMEM_SCORER_MEAN_K) {
+        return e->fail(KVMEM_HIP_ERR_UNSUPPORTED,
+                       "set_query: the state holds row sums, which only the mean-K scorer reads");
+    }
+    const uint32_t L = e->p.n_layers;
+    const size_t n = static_cast<size_t>(L) * e->p.n_head * e->p.head_dim;
+    // llama-memory-kvmem.cpp:3124-3137: finite sums, one nonzero row count
+    for (size_t i = 0; i < n; ++i) {
+        if (!std::isfinite(q_sum[i])) {
+            return e->fail(KVMEM_HIP_ERR_INVALID, "set_query: a sum is not finite");
+        }
+    }
+    for (uint32_t l = 0; l < L; ++l) {
+        if (q_count[l] == 0 || q_count[l] != q_count[0]) {
+            return e->fail(KVMEM_HIP_ERR_INVALID, "set_query: row counts must be equal and nonzero");
+        }
+    }
+    if (!e->d_qsum && hipMalloc(&e->d_qsum, sizeof(float) * n) != hipSuccess) {
+        e->d_qsum = nullptr;
+        return e->fail(KVMEM_HIP_ERR_NOMEM, "set_query: query sums");
+    }
+    hipStream_t st = static_cast<hipStream_t>(kvmem_hip_get_stream(e->ctx));
+    if (hipMemcpyAsync(e->d_qsum, q_sum, sizeof(float) * n, hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+        return e->fail(KVMEM_HIP_ERR_RUNTIME, "set_query: copy");
+    }
+    e->imp_count.assign(q_count, q_count + L);
+    e->query_imported = true;
+    e->query_frozen = true;
+    return KVMEM_HIP_OK;
+}
+
+int kvmem_engine_freeze_query(kvmem_engine *e, int frozen) {
+    if (!e) {
+        return KVMEM_HIP_ERR_INVALID;
+    }
+    e->query_frozen = frozen != 0;
     return KVMEM_HIP_OK;
 }
 

@@ -125,6 +125,14 @@ def bind(lib: C.CDLL) -> C.CDLL:
     sig("kvmem_engine_commit_unchanged", i32, vp, pview, u64, u32, pu32, u32)
     sig("kvmem_engine_commit_resident", i32, vp, i32)
     sig("kvmem_engine_can_append", i32, vp, u32, u32, i32, pstr)
+    sig("kvmem_store_query_replay_fits", i32, vp, u32, u32)
+    sig("kvmem_store_free_slots", u32, vp)
+    sig("kvmem_engine_query_replay_fits", i32, vp, u32, u32)
+    sig("kvmem_engine_free_slots", u32, vp)
+    pf32 = C.POINTER(C.c_float)
+    sig("kvmem_engine_get_query", i32, vp, pf32, pu32)
+    sig("kvmem_engine_set_query", i32, vp, pf32, pu32)
+    sig("kvmem_engine_freeze_query", i32, vp, i32)
     sig("kvmem_engine_set_request_span", i32, vp, C.c_int32, C.c_int32, C.c_int32)
     sig("kvmem_engine_set_turn_spans", i32, vp, C.POINTER(RowRange), u32, C.POINTER(RowRange), u32)
     sig("kvmem_engine_retrieval_mandatory", i32, vp, pu32, u32, pu32)
@@ -281,6 +289,12 @@ class Store:
         why = C.c_char_p()
         ok = self.lib.kvmem_store_can_append(self.h, end, generation_rows, int(all_history), C.byref(why))
         return bool(ok), why.value.decode()
+
+    def query_replay_fits(self, query_begin: int, prompt_end: int) -> bool:
+        return bool(self.lib.kvmem_store_query_replay_fits(self.h, query_begin, prompt_end))
+
+    def free_slots(self) -> int:
+        return self.lib.kvmem_store_free_slots(self.h)
 
     def blocks_overlapping(self, ranges, force_pos: int = -1) -> list:
         """retrieval_mandatory's mapping of row ranges (+ force_pos) to ids."""
@@ -506,6 +520,32 @@ class Engine:
         why = C.c_char_p()
         ok = self.lib.kvmem_engine_can_append(self.h, end, generation_rows, int(all_history), C.byref(why))
         return bool(ok), why.value.decode()
+
+    def query_replay_fits(self, query_begin: int, prompt_end: int) -> bool:
+        return bool(self.lib.kvmem_engine_query_replay_fits(self.h, query_begin, prompt_end))
+
+    def free_slots(self) -> int:
+        return self.lib.kvmem_engine_free_slots(self.h)
+
+    def get_query(self):
+        """(sums [n_layers][n_head*head_dim] f32, counts [n_layers]) a window preview uses."""
+        import numpy as np
+        L = self.params.n_layers
+        sums = np.zeros((L, self.params.n_head * self.params.head_dim), np.float32)
+        cnt = (C.c_uint32 * L)()
+        self.check(self.lib.kvmem_engine_get_query(self.h, sums.ctypes.data_as(C.POINTER(C.c_float)), cnt),
+                   "get_query")
+        return sums, list(cnt)
+
+    def set_query(self, sums, counts) -> None:
+        import numpy as np
+        a = np.ascontiguousarray(sums, dtype=np.float32)
+        cnt = (C.c_uint32 * len(counts))(*counts)
+        self.check(self.lib.kvmem_engine_set_query(self.h, a.ctypes.data_as(C.POINTER(C.c_float)), cnt),
+                   "set_query")
+
+    def freeze_query(self, frozen: bool) -> None:
+        self.check(self.lib.kvmem_engine_freeze_query(self.h, int(frozen)), "freeze_query")
 
     def scores(self) -> list:
         n = self.block_count()

@@ -207,3 +207,33 @@ def test_can_append_reasons():
     lay.apply([0, 1, 2])                        # block 1 in slot 2, block 2 in slot 1
     assert lay.can_append(16, 0, True) == (False, "coverage_or_layout")
     assert lay.can_append(16, 0, False) == (True, "same_query")
+
+
+def test_query_replay_fits_closed_forms():
+    """query_replay_fits (llama-memory-kvmem.cpp:3502-3524): the blocks from
+    the query's first block to the prompt's end plus the sink must fit the
+    budget; a query starting inside the sink needs every block."""
+    bt = 4
+    st = make_store(bt=bt, budget=5, n_slots=8)     # sink 1
+    assert st.query_replay_fits(40, 40) and st.query_replay_fits(41, 40)   # empty
+    assert st.query_replay_fits(32, 40)             # blocks 8, 9 + sink = 3
+    assert st.query_replay_fits(24, 40)             # 6..9 + sink = 5
+    assert not st.query_replay_fits(20, 40)         # 5..9 + sink = 6
+    assert st.query_replay_fits(39, 40)             # block 9 + sink
+    assert not st.query_replay_fits(0, 40)          # inside the sink: all 10 blocks
+    assert st.query_replay_fits(0, 20)              # all 5 blocks
+    assert st.query_replay_fits(3, 17)              # inside the sink: 17 rows = 5 blocks
+    assert not st.query_replay_fits(3, 21)          # 21 rows = 6 blocks
+    assert make_store(bt=bt, budget=0, n_slots=8).query_replay_fits(0, 400)   # no budget
+
+
+def test_free_slots_follow_the_lifo_list():
+    st = make_store(bt=4, budget=3, n_slots=5)
+    assert st.free_slots() == 5
+    st.register_append(20)
+    st.apply([0, 1, 2])
+    assert st.free_slots() == 2
+    st.append_resident(4)                           # block 5 takes a slot
+    assert st.free_slots() == 1
+    st.truncate_to(12)                              # blocks 3.. gone, block 5's slot freed
+    assert st.free_slots() == 2

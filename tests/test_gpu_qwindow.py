@@ -200,3 +200,59 @@ def test_misaligned_device_history_is_refused():
         assert eng.block_count() == 4
         st = eng.apply_retrieval(q.data_ptr(), 4)
         assert st["n_staged"] == 4
+
+
+def test_query_state_get_set_freeze(oracle):
+    """The query state {sum, count} (llama_kvmem_get_query / set_query /
+    freeze_query, llama-memory-kvmem.cpp:3104-3137): get returns the window
+    rows summed in token order, bit-exact against the oracle's ordered sum;
+    set on a second engine makes its window preview score from the given
+    sums (the same scores and selection as the first engine's window) and
+    freezes the query, so later captures keep no rows; reset_query drops the
+    set state; bad states and the per-token scorer are refused."""
+    announce("query state: get, set on another engine, freeze, reset")
+    cap, nb = 40, 40
+    k, v, _ = workloads.scoring_tensors(torch, "cuda", L=L, B=cap, Tq=1, seed=83, with_v=True)
+    cp = Capture("bf16", 84)
+    with engine(scorer=1) as a, engine(scorer=1) as b:
+        for eng in (a, b):
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        a.set_turn_spans(query=[(20, 60)], mandatory=[])
+        cp.ubatch(a, 0, 40)
+        cp.ubatch(a, 40, 40)
+        sums, counts = a.get_query()
+        assert counts == [40] * L
+        want = oracle.q_accumulate(cp.rows(range(20, 60)).reshape(L, 40, EQ))
+        assert np.array_equal(sums.view(np.uint32), want.view(np.uint32))
+        sel_a = a.preview_window()
+        scores_a = np.array(a.scores(), dtype=np.float64)
+        with pytest.raises(kv.KvMemError):
+            b.get_query()                                   # nothing captured yet
+        bad = sums.copy()
+        bad[0, 3] = np.inf
+        for s_, c_ in ((bad, counts), (sums, [40] * (L - 1) + [39]), (sums, [0] * L)):
+            with pytest.raises(kv.KvMemError):
+                b.set_query(s_, c_)
+        b.set_query(sums, counts)
+        got_sums, got_counts = b.get_query()
+        assert np.array_equal(got_sums.view(np.uint32), sums.view(np.uint32)) and got_counts == counts
+        sel_b = b.preview_window()
+        assert sel_b.blocks == sel_a.blocks
+        assert np.array_equal(np.array(b.scores(), dtype=np.float64), scores_a)
+        # frozen: a capture keeps no rows, the set state stays
+        b.set_turn_spans(query=[(0, 80)], mandatory=[])
+        cp.ubatch(b, 0, 40)
+        assert np.array_equal(b.get_query()[0].view(np.uint32), sums.view(np.uint32))
+        b.reset_query()                                     # the set state goes; still frozen
+        with pytest.raises(kv.KvMemError):
+            b.get_query()
+        cp.ubatch(b, 0, 40)
+        with pytest.raises(kv.KvMemError):
+            b.query_rows()
+        b.freeze_query(False)
+        cp.ubatch(b, 0, 40)
+        assert b.query_rows() == 40
+    with engine() as t:
+        t.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        with pytest.raises(kv.KvMemError):
+            t.set_query(sums, counts)                       # the per-token scorer reads rows
