@@ -190,6 +190,12 @@ KVMEM_HIP_API int kvmem_store_can_append(const kvmem_store *s, uint32_t end, uin
  * llama-memory-kvmem.cpp:3502-3524). */
 KVMEM_HIP_API int kvmem_store_query_replay_fits(const kvmem_store *s, uint32_t query_begin,
                                                 uint32_t prompt_end);
+/* KvMemStore::prefill_needs_offload (kvmem_store.cpp:340-351): 1 when
+ * incoming_tokens more rows over resident_tokens overflow pool_tokens or
+ * its high watermark (0.95 of it, at least one block), the test can_append
+ * makes for a whole resident history. */
+KVMEM_HIP_API int kvmem_store_prefill_needs_offload(const kvmem_store *s, uint32_t resident_tokens,
+                                                    uint32_t incoming_tokens, uint32_t pool_tokens);
 /* Slots the LIFO free list still holds (llama_kvmem_free_slots,
  * llama-kvmem-hooks.h:85). */
 KVMEM_HIP_API uint32_t kvmem_store_free_slots(const kvmem_store *s);

@@ -259,6 +259,11 @@ int kvmem_store_query_replay_fits(const kvmem_store *s, uint32_t query_begin, ui
     return !s || kvmem_amd::query_replay_fits(s->rt.store(), query_begin, prompt_end) ? 1 : 0;
 }
 
+int kvmem_store_prefill_needs_offload(const kvmem_store *s, uint32_t resident_tokens, uint32_t incoming_tokens,
+                                      uint32_t pool_tokens) {
+    return s && s->rt.store().prefill_needs_offload(resident_tokens, incoming_tokens, pool_tokens) ? 1 : 0;
+}
+
 uint32_t kvmem_store_free_slots(const kvmem_store *s) {
     return s ? s->slots.n_free() : 0u;
 }

@@ -127,6 +127,7 @@ def bind(lib: C.CDLL) -> C.CDLL:
     sig("kvmem_engine_can_append", i32, vp, u32, u32, i32, pstr)
     sig("kvmem_store_query_replay_fits", i32, vp, u32, u32)
     sig("kvmem_store_free_slots", u32, vp)
+    sig("kvmem_store_prefill_needs_offload", i32, vp, u32, u32, u32)
     sig("kvmem_engine_query_replay_fits", i32, vp, u32, u32)
     sig("kvmem_engine_free_slots", u32, vp)
     pf32 = C.POINTER(C.c_float)
@@ -295,6 +296,10 @@ class Store:
 
     def free_slots(self) -> int:
         return self.lib.kvmem_store_free_slots(self.h)
+
+    def prefill_needs_offload(self, resident_tokens: int, incoming_tokens: int, pool_tokens: int) -> bool:
+        return bool(self.lib.kvmem_store_prefill_needs_offload(self.h, resident_tokens, incoming_tokens,
+                                                               pool_tokens))
 
     def blocks_overlapping(self, ranges, force_pos: int = -1) -> list:
         """retrieval_mandatory's mapping of row ranges (+ force_pos) to ids."""

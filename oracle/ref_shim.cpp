@@ -152,6 +152,20 @@ KREF_API int kref_runtime_apply(void *h, const uint32_t *sel, uint32_t n_sel, ui
     }
 }
 
+// KvMemRuntime::commit_resident_selection: 1 if committed, 0 if refused.
+KREF_API int kref_runtime_commit_resident(void *h, const uint32_t *sel, uint32_t n) {
+    auto *r = static_cast<RefRuntime *>(h);
+    return r->rt.commit_resident_selection(std::vector<uint32_t>(sel, sel + n)) ? 1 : 0;
+}
+
+// KvMemStore::prefill_needs_offload of a store with block_tokens per block
+// and the default high watermark.
+KREF_API int kref_prefill_needs_offload(uint32_t block_tokens, uint32_t resident_tokens,
+                                        uint32_t incoming_tokens, uint32_t pool_tokens) {
+    kvmem::KvMemStore st(make_cfg(block_tokens, 1, 0, 0));
+    return st.prefill_needs_offload(resident_tokens, incoming_tokens, pool_tokens) ? 1 : 0;
+}
+
 // Per block: gpu slot (-1 if none), tier, in_working_set, baked_pos.
 KREF_API uint32_t kref_runtime_blocks(void *h, int32_t *gpu_slot, uint8_t *tier, uint8_t *in_ws,
                                       int64_t *baked_pos) {

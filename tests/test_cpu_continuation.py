@@ -13,7 +13,11 @@ alone stands in for it (a block holding a slot is complete).  Pinned by:
   - closed forms for every condition of each check and every reason string
     of can_append, worked out by hand on small stores;
   - the attention epoch: appended rows never move it; cuts and applies that
-    change the working set do.
+    change the working set do;
+  - where oracle/_ref is built, the reference's own KvMemStore::
+    prefill_needs_offload (can_append's pressure test) and KvMemRuntime::
+    commit_resident_selection (what commit_unchanged / commit_resident end
+    in), live over random and edge inputs.
 """
 from __future__ import annotations
 
@@ -237,3 +241,86 @@ def test_free_slots_follow_the_lifo_list():
     assert st.free_slots() == 1
     st.truncate_to(12)                              # blocks 3.. gone, block 5's slot freed
     assert st.free_slots() == 2
+
+
+REF = __import__("conftest").ROOT / "oracle" / "_ref" / "libkvmem_ref.so"
+
+
+def _ref_lib():
+    import ctypes as C
+    ref = C.CDLL(str(REF))
+    pu32 = C.POINTER(C.c_uint32)
+    ref.kref_prefill_needs_offload.argtypes = [C.c_uint32] * 4
+    ref.kref_runtime_new.restype = C.c_void_p
+    ref.kref_runtime_new.argtypes = [C.c_uint32] * 6
+    ref.kref_runtime_free.argtypes = [C.c_void_p]
+    ref.kref_runtime_apply.argtypes = [C.c_void_p, pu32, C.c_uint32, pu32, pu32, pu32, pu32, pu32]
+    ref.kref_runtime_commit_resident.argtypes = [C.c_void_p, pu32, C.c_uint32]
+    ref.kref_runtime_blocks.restype = C.c_uint32
+    ref.kref_runtime_blocks.argtypes = [C.c_void_p, C.POINTER(C.c_int32), C.POINTER(C.c_uint8),
+                                        C.POINTER(C.c_uint8), C.POINTER(C.c_int64)]
+    return ref
+
+
+@pytest.mark.skipif(not REF.exists(), reason="oracle/_ref not built (needs the reference tree)")
+def test_prefill_needs_offload_matches_the_reference_library():
+    """can_append's prefill-pressure test against the reference's own
+    KvMemStore::prefill_needs_offload, on the watermark's edges and at
+    random."""
+    import numpy as np
+    ref = _ref_lib()
+    rng = np.random.default_rng(12)
+    n = 0
+    for bt in (16, 32, 128):
+        st = make_store(bt=bt)
+        cases = [(0, 0, 0), (5, 0, 100), (0, 5, 0), (0, bt, bt), (0, bt + 1, bt), (10, 1, 10)]
+        for pool in (bt, 7 * bt, 384 * bt, 49152, 40000):
+            w = max(int(pool * 0.95), bt)
+            for r in (0, 1, w // 2):
+                for inc in (w - r - 1, w - r, w - r + 1, pool - r, pool - r + 1):
+                    if inc >= 0:
+                        cases.append((r, inc, pool))
+        cases += [tuple(int(x) for x in rng.integers(0, 60000, 3)) for _ in range(500)]
+        for r, inc, pool in cases:
+            assert st.prefill_needs_offload(r, inc, pool) == bool(ref.kref_prefill_needs_offload(bt, r, inc, pool)), \
+                (bt, r, inc, pool)
+            n += 1
+    assert n > 1500
+
+
+@pytest.mark.skipif(not REF.exists(), reason="oracle/_ref not built (needs the reference tree)")
+def test_commit_resident_selection_matches_the_reference_library():
+    """commit_resident_selection after random applies: the same accept or
+    refuse, and the same working-set flags, as the reference's own runtime
+    for the resident set itself, a trimmed one, one with an extra block and
+    an unsorted one."""
+    import ctypes as C
+    import numpy as np
+    ref = _ref_lib()
+    rng = np.random.default_rng(21)
+    bt, nb, budget, n_slots = 16, 40, 12, 16
+    for trial in range(30):
+        st = make_store(bt=bt, budget=budget, n_slots=n_slots)
+        st.register_append(nb * bt)
+        h = ref.kref_runtime_new(bt, budget, 1, 0, n_slots, nb * bt)
+        try:
+            for step in range(4):
+                sel = sorted(rng.choice(nb, int(rng.integers(1, budget + 1)), replace=False).tolist())
+                st.apply(sel)
+                arr = (C.c_uint32 * nb)(*sel)
+                si, so, ctr = (C.c_uint32 * nb)(), (C.c_uint32 * nb)(), (C.c_uint32 * 5)()
+                ni, no = C.c_uint32(), C.c_uint32()
+                ref.kref_runtime_apply(h, arr, len(sel), si, C.byref(ni), so, C.byref(no), ctr)
+                resident = [b for b, s in enumerate(st.blocks()["gpu_slot"]) if s >= 0]
+                extra = sorted(set(resident) | {int(rng.integers(0, nb))})
+                for cand in (resident, resident[:-1], extra, resident[::-1]):
+                    a = (C.c_uint32 * max(1, len(cand)))(*cand)
+                    want = bool(ref.kref_runtime_commit_resident(h, a, len(cand)))
+                    assert st.commit_resident_selection(cand) == want, (trial, step, cand)
+                gs, tr = (C.c_int32 * nb)(), (C.c_uint8 * nb)()
+                ws, bk = (C.c_uint8 * nb)(), (C.c_int64 * nb)()
+                ref.kref_runtime_blocks(h, gs, tr, ws, bk)
+                b = st.blocks()
+                assert b["in_ws"] == list(ws) and b["gpu_slot"] == list(gs), (trial, step)
+        finally:
+            ref.kref_runtime_free(h)
