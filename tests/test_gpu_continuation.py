@@ -14,7 +14,7 @@ can_append and append_resident over the engine's own pool.
 - A changed selection or a changed pool is refused; commit_resident and
   canonical / LIFO views.
 - Rows appended resident in canonical mode continue the slot order and are
-  not staged again by the next apply.
+  not staged again by the next apply, host-planned or device-planned.
 """
 from __future__ import annotations
 
@@ -204,4 +204,32 @@ def test_append_resident_in_canonical_layout(oracle):
         assert st["n_staged"] >= 1
         check_pool(eng, oracle, k, v, [0, nb], kv.TYPE_Q8_0, kv.TYPE_Q8_0,
                    ntok_of=lambda b: 80 if b == nb else T)
+        assert eng.attention_view().valid
+
+
+def test_append_resident_then_device_planned_step(oracle):
+    """Blocks appended resident enter the device plan's resident list like
+    staged ones: a device-planned apply_retrieval after them stages only the
+    blocks it newly selects, moves the rest into window order, and every
+    selected block's rows are the oracle's."""
+    announce("append_resident, then apply_retrieval through the device plan")
+    cap, nb = 24, 18
+    k, v, q = history(cap, seed=59)
+    q2 = (q.float() * -1.0).to(torch.bfloat16)
+    with make_engine(8, 4) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        st = eng.apply_retrieval(q.data_ptr(), q.shape[1])
+        assert st["device_planned"] == 1
+        first = [b for b, s in enumerate(eng.block_slots()) if s >= 0]
+        decode_rows(eng, k, v, nb * T, (nb + 2) * T)        # blocks 18, 19 written in the pool
+        slots = eng.block_slots()
+        assert slots[nb] == len(first) and slots[nb + 1] == len(first) + 1
+        eng.set_request_span(nb * T, 0)                      # the new rows are the query
+        st = eng.apply_retrieval(q2.data_ptr(), q2.shape[1])
+        assert st["device_planned"] == 1
+        sel = [b for b, s in enumerate(eng.block_slots()) if s >= 0]
+        assert nb in sel and nb + 1 in sel
+        assert st["n_staged"] == len(set(sel) - set(first) - {nb, nb + 1})
+        assert [eng.block_slots()[b] for b in sel] == list(range(len(sel)))
+        check_pool(eng, oracle, k, v, sel, kv.TYPE_Q8_0, kv.TYPE_Q8_0)
         assert eng.attention_view().valid
