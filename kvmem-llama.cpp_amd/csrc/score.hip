@@ -675,6 +675,9 @@ extern "C" int kvmem_hip_score_noalloc(kvmem_hip_ctx *ctx, const kvmem_hip_histo
     float *layers = args->layer_scores ? args->layer_scores : reinterpret_cast<float *>(base + layer_off);
     st = score_launch(ctx, args, p, grid, layers, false);
     if (st != KVMEM_HIP_OK) {
+        // a launch that failed after the scorer kernel was queued leaves that
+        // kernel on the array with no owner record: let it drain first
+        (void) hipStreamSynchronize(ctx->stream);
         return st;
     }
     if (!hip_ok(ctx, hipEventRecord(ctx->noalloc_done, ctx->stream), "score_noalloc completion event")) {
