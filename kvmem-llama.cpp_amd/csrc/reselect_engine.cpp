@@ -906,6 +906,11 @@ int kvmem_engine_truncate_to(kvmem_engine *e, uint32_t token_pos) {
         e->packed_valid[id] = 0;
     }
     const uint32_t nb = e->rt.store().block_count();
+    if (e->dirty_tail >= static_cast<int64_t>(nb)) {
+        // the grown tail is gone: a block appended later under its id is a
+        // new one, complete once its rows are written
+        e->dirty_tail = -1;
+    }
     // a block cut short has stale sums
     e->meank_valid = std::min(e->meank_valid, nb > 0 ? nb - 1 : 0u);
     ++e->epoch;

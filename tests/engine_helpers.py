@@ -66,3 +66,24 @@ def block_major_pinned(k, v, n_blocks):
     host_buf = torch.empty((n_blocks, L * 2 * T * E), dtype=torch.float16, pin_memory=True)
     host_buf.copy_(torch.cat([kk, vv], dim=2).reshape(n_blocks, -1).cpu())
     return host_buf
+
+
+def decode_rows(eng, k, v, begin: int, end: int) -> None:
+    """The caller's decode of rows [begin, end): append them resident, then
+    write the pool cells of every block they touch (whole blocks, from the
+    history that already holds the rows), as llama.cpp writes a batch's
+    K/V cells."""
+    eng.append_resident(end - begin)
+    slots = eng.block_slots()
+    ids = list(range(begin // T, (end + T - 1) // T))
+    n_blocks = eng.block_count()
+    last = eng.total_tokens() - (n_blocks - 1) * T
+    c = kv.Context(0)
+    hist = c.make_history(k.data_ptr(), v.data_ptr(), L, n_blocks, T, E, E, 0 if last == T else last,
+                          k.shape[1])
+    pk = [eng.pool_layer(layer)[0] for layer in range(L)]
+    pv = [eng.pool_layer(layer)[1] for layer in range(L)]
+    pool = c.make_pool(L, eng.n_slots(), T, E, E, eng.params.type_k, eng.params.type_v, pk, pv)
+    c.stagein_blocks(hist, pool, ids, [slots[b] for b in ids])
+    c.sync()
+    c.close()

@@ -29,7 +29,7 @@ from conftest import load_pkg  # noqa: E402
 kv = load_pkg()
 from kvmem_amd import host  # noqa: E402
 
-from engine_helpers import E, L, T, check_pool, history, make_engine  # noqa: E402
+from engine_helpers import E, L, T, check_pool, decode_rows, history, make_engine  # noqa: E402
 
 
 def announce(msg: str) -> None:
@@ -48,27 +48,6 @@ def pool_bytes(eng) -> list:
             c.close()
             out.append(buf.cpu())
     return out
-
-
-def decode_rows(eng, k, v, begin: int, end: int) -> None:
-    """The caller's decode of rows [begin, end): append them resident, then
-    write the pool cells of every block they touch (whole blocks, from the
-    history that already holds the rows), as llama.cpp writes a batch's
-    K/V cells."""
-    eng.append_resident(end - begin)
-    slots = eng.block_slots()
-    ids = list(range(begin // T, (end + T - 1) // T))
-    n_blocks = eng.block_count()
-    last = eng.total_tokens() - (n_blocks - 1) * T
-    c = kv.Context(0)
-    hist = c.make_history(k.data_ptr(), v.data_ptr(), L, n_blocks, T, E, E, 0 if last == T else last,
-                          k.shape[1])
-    pk = [eng.pool_layer(layer)[0] for layer in range(L)]
-    pv = [eng.pool_layer(layer)[1] for layer in range(L)]
-    pool = c.make_pool(L, eng.n_slots(), T, E, E, eng.params.type_k, eng.params.type_v, pk, pv)
-    c.stagein_blocks(hist, pool, ids, [slots[b] for b in ids])
-    c.sync()
-    c.close()
 
 
 def test_reference_logits_fixture_flow(oracle):
@@ -233,3 +212,33 @@ def test_append_resident_then_device_planned_step(oracle):
         assert [eng.block_slots()[b] for b in sel] == list(range(len(sel)))
         check_pool(eng, oracle, k, v, sel, kv.TYPE_Q8_0, kv.TYPE_Q8_0)
         assert eng.attention_view().valid
+
+
+def test_truncated_grown_tail_leaves_no_stale_mark(oracle):
+    """A resident partial tail that grew (so the next apply would quantize it
+    again) and is then cut away by a truncation leaves no mark behind: rows
+    decoded afterwards into a new block under the same id make a complete
+    block, the attention view is valid, and the next apply does not stage
+    it again."""
+    announce("grown tail truncated away, then a new block decoded under its id")
+    cap, nb = 20, 10
+    k, v, q = history(cap, seed=67)
+    with make_engine(6, 4) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T + 50)
+        sel = eng.preview(q.data_ptr(), q.shape[1], mandatory=[nb])
+        assert nb in sel.blocks
+        eng.apply(sel)
+        eng.append_tokens(30)                     # the resident tail grows: stale in the pool
+        assert not eng.attention_view().valid
+        eng.truncate_to(nb * T)                   # ... and is cut away with its slot
+        assert eng.block_slots()[nb:] == []
+        decode_rows(eng, k, v, nb * T, nb * T + 40)   # a new block 10, written in the pool
+        view = eng.attention_view()
+        assert view.valid and view.blocks[-1] == nb, view
+        check_pool(eng, oracle, k, v, view.blocks, kv.TYPE_Q8_0, kv.TYPE_Q8_0,
+                   ntok_of=lambda b: 40 if b == nb else T)
+        sel2 = eng.preview(q.data_ptr(), q.shape[1], mandatory=[nb])
+        st = eng.apply(sel2)
+        assert st["n_staged"] == len(set(sel2.blocks) - set(view.blocks)), st
+        check_pool(eng, oracle, k, v, sel2.blocks, kv.TYPE_Q8_0, kv.TYPE_Q8_0,
+                   ntok_of=lambda b: 40 if b == nb else T)

@@ -1,0 +1,264 @@
+"""Seeded random operation sequences on the reselect engine, checked
+against the oracle after every operation.
+
+The reference drives its reselect path from the server loop: retrieval
+steps, rows decoded into the pool, rows appended to the host history,
+restores that truncate to a checkpoint, and host fallbacks after a failed
+device call (src/adapter/llama-memory-kvmem.cpp:2752-2758, 3047-3263;
+tests/mtp-kv-test.cpp:144-214, 300-361).  Here those operations come in a
+seeded random order:
+
+- a retrieval step through the device plan (apply_retrieval), whose
+  resident set must be the preview of the same query and mandatory blocks;
+- preview + apply;
+- a preview made stale by rows appended or cut before its apply;
+- rows appended to the history only (append_tokens);
+- rows decoded resident (append_resident, then the caller writes the pool
+  cells of the blocks they touch, whole blocks from the history);
+- a truncation;
+- an apply whose n-th device operation is refused on the host
+  (kvmem_hip_debug_fail_after: nothing faults);
+- commit_unchanged after a preview with the last apply's query and
+  mandatory blocks, which must succeed exactly when the selection equals
+  the pool's canonical attention view.
+
+A model in the test tracks how many rows of each resident block the pool
+holds.  After every operation: the engine's resident set is the model's;
+slots are distinct and in range; every resident block's pool rows are the
+oracle's quantization of its history rows; after a successful apply the
+resident set is the selection, in window order when the layout is canonical.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from conftest import load_pkg  # noqa: E402
+
+kv = load_pkg()
+from kvmem_amd import workloads  # noqa: E402
+
+from engine_helpers import E, L, T, decode_rows, history, make_engine  # noqa: E402
+
+ALL_KINDS = kv.FAIL_ALLOC | kv.FAIL_COPY | kv.FAIL_LAUNCH
+
+CASES = [
+    # (canonical layout, type_k, type_v, seed)
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 101),
+    (0, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 102),
+    (1, kv.TYPE_Q5_0, kv.TYPE_Q8_0, 103),
+]
+OPS = ["retrieve", "preview_apply", "stale", "append", "decode", "truncate", "fail", "unchanged"]
+WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2], dtype=float)
+N_OPS = 150
+
+
+def announce(msg: str) -> None:
+    print(f"[sequences] {msg}", flush=True)
+
+
+class Model:
+    """What the pool must hold: rows of each resident block, and the token count."""
+
+    def __init__(self, eng, oracle, k, v, types):
+        self.eng, self.oracle, self.types = eng, oracle, types
+        self.bits = (workloads.to_bits(torch, k), workloads.to_bits(torch, v))
+        self.total = eng.total_tokens()
+        self.valid: dict[int, int] = {}
+        self.cache: dict[tuple, np.ndarray] = {}
+
+    def ntok(self, b: int) -> int:
+        return min(T, self.total - b * T)
+
+    def resident(self) -> dict[int, int]:
+        return {b: s for b, s in enumerate(self.eng.block_slots()) if s >= 0}
+
+    def applied(self, sel: list[int]) -> None:
+        self.valid = {b: self.ntok(b) for b in sel}
+
+    def want(self, layer: int, which: int, b: int, n: int) -> np.ndarray:
+        key = (layer, which, b, n)
+        if key not in self.cache:
+            rows = self.bits[which][layer, b].reshape(T, E)[:n]
+            self.cache[key] = self.oracle.quantize_rows_f16(self.types[which], rows)
+        return self.cache[key]
+
+    def check(self, what: str, canonical_sel: list[int] | None = None) -> None:
+        eng = self.eng
+        assert eng.total_tokens() == self.total, what
+        res = self.resident()
+        assert set(res) == set(self.valid), (what, sorted(res), sorted(self.valid))
+        slots = list(res.values())
+        assert len(set(slots)) == len(slots) and all(0 <= s < eng.n_slots() for s in slots), (what, res)
+        if canonical_sel is not None:
+            assert [res[b] for b in canonical_sel] == list(range(len(canonical_sel))), (what, res)
+        c = kv.Context(0)
+        pools = []
+        for layer in range(L):
+            for which in (0, 1):
+                rb = kv.row_size(self.types[which], E)
+                n = eng.n_slots() * T * rb
+                buf = torch.empty(n, dtype=torch.uint8, device="cuda")
+                c.d2d_batched([eng.pool_layer(layer)[which]], [buf.data_ptr()], [n])
+                pools.append((buf, rb))
+        c.sync()
+        c.close()
+        for i, (buf, rb) in enumerate(pools):
+            layer, which = divmod(i, 2)
+            pool = buf.cpu().numpy().reshape(eng.n_slots() * T, rb)
+            for b, s in res.items():
+                n = self.valid[b]
+                got = pool[s * T: s * T + n]
+                assert np.array_equal(got, self.want(layer, which, b, n)), (what, layer, "KV"[which], b, s, n)
+
+
+@pytest.mark.parametrize("case", CASES, ids=["canonical_q8", "lifo_q8_q4", "canonical_q5_q8"])
+def test_random_operation_sequences(oracle, case):
+    canonical, tk, tv, seed = case
+    cap, budget, reserve = 40, 8, 6
+    announce(f"{N_OPS} random operations, canonical={canonical}, types {kv.TYPE_NAMES[tk]}/"
+             f"{kv.TYPE_NAMES[tv]}, seed {seed}")
+    k, v, q = history(cap, seed=seed)
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    perm = torch.randperm(q.shape[2], generator=g).tolist()
+    queries = [q, (q.float() * -1.0).to(torch.bfloat16), q[:, :, perm].contiguous()]
+    rng = np.random.default_rng(seed)
+    counts = dict.fromkeys(OPS, 0)
+    hits = {"unchanged_ok": 0, "failed_apply": 0, "decode_refused": 0, "stale_refused": 0}
+    with make_engine(budget, reserve, tk, tv, canonical_layout=canonical) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, 20 * T + 37)
+        ctx = kv.Context.borrow(eng.ctx_handle())
+        m = Model(eng, oracle, k, v, (tk, tv))
+        m.check("start")
+        last_q, last_mand = 0, []
+
+        def mandatory() -> list[int]:
+            nb = eng.block_count()
+            n = int(rng.integers(0, 3))
+            return sorted({int(x) for x in rng.integers(0, nb, n)})
+
+        def grow(n: int) -> int:
+            return int(min(n, cap * T - m.total))
+
+        for step in range(N_OPS):
+            op = OPS[int(rng.choice(len(OPS), p=WEIGHTS / WEIGHTS.sum()))]
+            qi = int(rng.integers(0, len(queries)))
+            qq = queries[qi]
+            what = f"step {step} {op}"
+            counts[op] += 1
+            if op == "retrieve":
+                mand = mandatory()
+                want = eng.preview(qq.data_ptr(), qq.shape[1], mandatory=mand).blocks
+                st = eng.apply_retrieval(qq.data_ptr(), qq.shape[1], mandatory=mand)
+                got = sorted(m.resident())
+                assert got == want, (what, got, want, st)
+                assert set(mand) <= set(got), what
+                m.applied(want)
+                last_q, last_mand = qi, mand
+                m.check(what, want if canonical else None)
+            elif op == "preview_apply":
+                mand = mandatory()
+                sel = eng.preview(qq.data_ptr(), qq.shape[1], mandatory=mand)
+                before = dict(m.valid)
+                need = sum(1 for b in sel.blocks if before.get(b, -1) < m.ntok(b))
+                st = eng.apply(sel)
+                # a decoded tail that had no slot is staged once more by the engine
+                assert need <= st["n_staged"] <= need + 1, (what, need, st)
+                m.applied(sel.blocks)
+                last_q, last_mand = qi, mand
+                m.check(what, sel.blocks if canonical else None)
+            elif op == "stale":
+                sel = eng.preview(qq.data_ptr(), qq.shape[1])
+                n = grow(int(rng.integers(1, 100)))
+                if n > 0:
+                    eng.append_tokens(n)
+                    m.total += n
+                else:
+                    cut = m.total - int(rng.integers(1, 60))
+                    eng.truncate_to(cut)
+                    m.total = cut
+                    m.valid = {b: min(r, m.ntok(b)) for b, r in m.valid.items() if b * T < cut}
+                with pytest.raises(kv.StaleSelection):
+                    eng.apply(sel)
+                hits["stale_refused"] += 1
+                m.check(what)
+            elif op == "append":
+                n = grow(int(rng.integers(1, 300)))
+                if n:
+                    eng.append_tokens(n)
+                    m.total += n
+                m.check(what)
+            elif op == "decode":
+                n = grow(int(rng.integers(1, 200)))
+                if n == 0:
+                    continue
+                t0 = m.total
+                try:
+                    decode_rows(eng, k, v, t0, t0 + n)
+                except kv.KvMemError as ex:
+                    # no free slot, or another grown tail waits: nothing changed, and the
+                    # caller appends the rows to the history instead
+                    assert ex.code in (kv.ERR_NOMEM, kv.ERR_UNSUPPORTED), (what, str(ex))
+                    assert eng.total_tokens() == t0, what
+                    m.check(what + " refused")
+                    eng.append_tokens(n)
+                    m.total += n
+                    hits["decode_refused"] += 1
+                else:
+                    m.total += n
+                    for b in range(t0 // T, (t0 + n + T - 1) // T):
+                        m.valid[b] = m.ntok(b)
+                m.check(what)
+            elif op == "truncate":
+                if m.total <= 2 * T:
+                    continue
+                cut = int(rng.integers(max(T, m.total - 3 * T), m.total))
+                eng.truncate_to(cut)
+                m.total = cut
+                m.valid = {b: min(r, m.ntok(b)) for b, r in m.valid.items() if b * T < cut}
+                m.check(what)
+            elif op == "fail":
+                sel = eng.preview(qq.data_ptr(), qq.shape[1])
+                before = dict(m.valid)
+                device = bool(rng.integers(0, 2))      # through the device plan, or the host plan
+                ctx.debug_fail_after(ALL_KINDS, int(rng.integers(1, 4)))
+                try:
+                    if device:
+                        eng.apply_retrieval(qq.data_ptr(), qq.shape[1])
+                    else:
+                        eng.apply(sel)
+                    failed = False
+                except kv.KvMemError as ex:
+                    assert "injected failure" in str(ex), (what, str(ex))
+                    failed = True
+                ctx.debug_fail_after(0, 0)
+                if failed:
+                    hits["failed_apply"] += 1
+                    res = m.resident()
+                    assert set(res) <= set(before), (what, sorted(res), sorted(before))
+                    m.valid = {b: before[b] for b in res}
+                    m.check(what + " (failed)")
+                else:
+                    assert sorted(m.resident()) == sel.blocks, what
+                    m.applied(sel.blocks)
+                    last_q, last_mand = qi, []
+                    m.check(what, sel.blocks if canonical else None)
+            elif op == "unchanged":
+                # the check runs against the pool's canonical view, as the reference's
+                # commit_unchanged does (llama-memory-kvmem.cpp:3086-3096)
+                view = eng.attention_view(canonical=bool(canonical))
+                canon = eng.attention_view(canonical=True)
+                qq = queries[last_q]          # the last apply's query and mandatory blocks
+                sel = eng.preview(qq.data_ptr(), qq.shape[1], mandatory=last_mand)
+                ok = eng.commit_unchanged(view, sel)
+                assert ok == (view.valid and canon.valid and sel.blocks == canon.blocks), (what, view, sel.blocks)
+                hits["unchanged_ok"] += int(ok)
+                m.check(what)
+    announce(f"operations {counts}; {hits}")
+    assert hits["stale_refused"] >= 1 and hits["failed_apply"] >= 1, hits
+    if canonical:
+        assert hits["unchanged_ok"] >= 1, hits
