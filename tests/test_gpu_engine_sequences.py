@@ -27,6 +27,8 @@ holds.  After every operation: the engine's resident set is the model's;
 slots are distinct and in range; every resident block's pool rows are the
 oracle's quantization of its history rows; after a successful apply the
 resident set is the selection, in window order when the layout is canonical.
+With a pinned host history and a pinned packed store, every block the engine
+marks as saved holds the oracle's rows in the store.
 """
 from __future__ import annotations
 
@@ -42,15 +44,16 @@ from conftest import load_pkg  # noqa: E402
 kv = load_pkg()
 from kvmem_amd import workloads  # noqa: E402
 
-from engine_helpers import E, L, T, decode_rows, history, make_engine  # noqa: E402
+from engine_helpers import E, L, T, block_major_pinned, decode_rows, history, make_engine  # noqa: E402
 
 ALL_KINDS = kv.FAIL_ALLOC | kv.FAIL_COPY | kv.FAIL_LAUNCH
 
 CASES = [
-    # (canonical layout, type_k, type_v, seed)
-    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 101),
-    (0, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 102),
-    (1, kv.TYPE_Q5_0, kv.TYPE_Q8_0, 103),
+    # (canonical layout, type_k, type_v, seed, pinned host history + packed store)
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 101, False),
+    (0, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 102, False),
+    (1, kv.TYPE_Q5_0, kv.TYPE_Q8_0, 103, False),
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 104, True),
 ]
 OPS = ["retrieve", "preview_apply", "stale", "append", "decode", "truncate", "fail", "unchanged"]
 WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2], dtype=float)
@@ -64,12 +67,13 @@ def announce(msg: str) -> None:
 class Model:
     """What the pool must hold: rows of each resident block, and the token count."""
 
-    def __init__(self, eng, oracle, k, v, types):
-        self.eng, self.oracle, self.types = eng, oracle, types
+    def __init__(self, eng, oracle, k, v, types, store=None):
+        self.eng, self.oracle, self.types, self.store = eng, oracle, types, store
         self.bits = (workloads.to_bits(torch, k), workloads.to_bits(torch, v))
         self.total = eng.total_tokens()
         self.valid: dict[int, int] = {}
         self.cache: dict[tuple, np.ndarray] = {}
+        self.n_packed_checked = 0
 
     def ntok(self, b: int) -> int:
         return min(T, self.total - b * T)
@@ -114,15 +118,38 @@ class Model:
                 n = self.valid[b]
                 got = pool[s * T: s * T + n]
                 assert np.array_equal(got, self.want(layer, which, b, n)), (what, layer, "KV"[which], b, s, n)
+        if self.store is not None:
+            # packed rows the engine restores from: full blocks saved at eviction, each
+            # [layer][T rows of K][T rows of V]
+            rk, rv = (kv.row_size(t, E) for t in self.types)
+            span = L * T * (rk + rv)
+            host = self.store.numpy()
+            for b in range(eng.block_count()):
+                if not eng.packed_valid(b):
+                    continue
+                assert self.ntok(b) == T, (what, b)
+                for layer in range(L):
+                    at = b * span + layer * T * (rk + rv)
+                    kr = host[at: at + T * rk].reshape(T, rk)
+                    vr = host[at + T * rk: at + T * (rk + rv)].reshape(T, rv)
+                    assert np.array_equal(kr, self.want(layer, 0, b, T)), (what, "packed K", b, layer)
+                    assert np.array_equal(vr, self.want(layer, 1, b, T)), (what, "packed V", b, layer)
+                self.n_packed_checked += 1
 
 
-@pytest.mark.parametrize("case", CASES, ids=["canonical_q8", "lifo_q8_q4", "canonical_q5_q8"])
+@pytest.mark.parametrize("case", CASES, ids=["canonical_q8", "lifo_q8_q4", "canonical_q5_q8",
+                                             "pinned_packed_q8_q4"])
 def test_random_operation_sequences(oracle, case):
-    canonical, tk, tv, seed = case
+    canonical, tk, tv, seed, pinned = case
     cap, budget, reserve = 40, 8, 6
     announce(f"{N_OPS} random operations, canonical={canonical}, types {kv.TYPE_NAMES[tk]}/"
-             f"{kv.TYPE_NAMES[tv]}, seed {seed}")
+             f"{kv.TYPE_NAMES[tv]}, seed {seed}, pinned host history and packed store: {pinned}")
     k, v, q = history(cap, seed=seed)
+    hb = store = None
+    if pinned:
+        hb = block_major_pinned(k, v, cap)
+        span = L * T * (kv.row_size(tk, E) + kv.row_size(tv, E))
+        store = torch.zeros(cap * span, dtype=torch.uint8, pin_memory=True)
     g = torch.Generator(device="cpu").manual_seed(seed)
     perm = torch.randperm(q.shape[2], generator=g).tolist()
     queries = [q, (q.float() * -1.0).to(torch.bfloat16), q[:, :, perm].contiguous()]
@@ -131,8 +158,11 @@ def test_random_operation_sequences(oracle, case):
     hits = {"unchanged_ok": 0, "failed_apply": 0, "decode_refused": 0, "stale_refused": 0}
     with make_engine(budget, reserve, tk, tv, canonical_layout=canonical) as eng:
         eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, 20 * T + 37)
+        if pinned:
+            eng.set_host_history(hb.data_ptr(), cap)
+            eng.set_packed_host(store.data_ptr(), cap)
         ctx = kv.Context.borrow(eng.ctx_handle())
-        m = Model(eng, oracle, k, v, (tk, tv))
+        m = Model(eng, oracle, k, v, (tk, tv), store)
         m.check("start")
         last_q, last_mand = 0, []
 
@@ -258,7 +288,10 @@ def test_random_operation_sequences(oracle, case):
                 assert ok == (view.valid and canon.valid and sel.blocks == canon.blocks), (what, view, sel.blocks)
                 hits["unchanged_ok"] += int(ok)
                 m.check(what)
-    announce(f"operations {counts}; {hits}")
+    announce(f"operations {counts}; {hits}; packed blocks checked {m.n_packed_checked}")
     assert hits["stale_refused"] >= 1 and hits["failed_apply"] >= 1, hits
     if canonical:
         assert hits["unchanged_ok"] >= 1, hits
+    if pinned:
+        assert m.n_packed_checked >= 1
+    del hb, store
