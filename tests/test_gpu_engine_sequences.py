@@ -28,7 +28,10 @@ slots are distinct and in range; every resident block's pool rows are the
 oracle's quantization of its history rows; after a successful apply the
 resident set is the selection, in window order when the layout is canonical.
 With a pinned host history and a pinned packed store, every block the engine
-marks as saved holds the oracle's rows in the store.
+marks as saved holds the oracle's rows in the store.  With the row transform
+(NeoX RoPE 256 on K at the original positions, then attn_rot), the pool rows
+are the oracle's transform and quantization; decoded rows are left out there,
+since a transformed pool's decoded cells are the model's to write.
 """
 from __future__ import annotations
 
@@ -44,17 +47,21 @@ from conftest import load_pkg  # noqa: E402
 kv = load_pkg()
 from kvmem_amd import workloads  # noqa: E402
 
-from engine_helpers import E, L, T, block_major_pinned, decode_rows, history, make_engine  # noqa: E402
+from engine_helpers import D, E, L, T, block_major_pinned, decode_rows, history, make_engine  # noqa: E402
+from test_gpu_transform import expected_rows  # noqa: E402
 
 ALL_KINDS = kv.FAIL_ALLOC | kv.FAIL_COPY | kv.FAIL_LAUNCH
 
 CASES = [
-    # (canonical layout, type_k, type_v, seed, pinned host history + packed store)
-    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 101, False),
-    (0, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 102, False),
-    (1, kv.TYPE_Q5_0, kv.TYPE_Q8_0, 103, False),
-    (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 104, True),
+    # (canonical layout, type_k, type_v, seed, pinned host history + packed store,
+    #  row transform: NeoX RoPE 256 on K at the original positions, then attn_rot)
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 101, False, False),
+    (0, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 102, False, False),
+    (1, kv.TYPE_Q5_0, kv.TYPE_Q8_0, 103, False, False),
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 104, True, False),
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 105, False, True),
 ]
+XF = dict(n_rot=256, rope_freq_base=1e6, attn_rot=1)
 OPS = ["retrieve", "preview_apply", "stale", "append", "decode", "truncate", "fail", "unchanged"]
 WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2], dtype=float)
 N_OPS = 150
@@ -67,8 +74,9 @@ def announce(msg: str) -> None:
 class Model:
     """What the pool must hold: rows of each resident block, and the token count."""
 
-    def __init__(self, eng, oracle, k, v, types, store=None):
+    def __init__(self, eng, oracle, k, v, types, store=None, xf=False):
         self.eng, self.oracle, self.types, self.store = eng, oracle, types, store
+        self.theta = oracle.rope_theta(XF["n_rot"], XF["rope_freq_base"]) if xf else None
         self.bits = (workloads.to_bits(torch, k), workloads.to_bits(torch, v))
         self.total = eng.total_tokens()
         self.valid: dict[int, int] = {}
@@ -88,7 +96,13 @@ class Model:
         key = (layer, which, b, n)
         if key not in self.cache:
             rows = self.bits[which][layer, b].reshape(T, E)[:n]
-            self.cache[key] = self.oracle.quantize_rows_f16(self.types[which], rows)
+            if self.theta is None:
+                self.cache[key] = self.oracle.quantize_rows_f16(self.types[which], rows)
+            else:
+                # K: RoPE 256 at positions b*T.. then the width-256 rotation; V: width 64
+                n_rot, width = (XF["n_rot"], 256) if which == 0 else (0, 64)
+                self.cache[key] = expected_rows(self.oracle, self.types[which], rows, D, n_rot,
+                                                self.theta if n_rot else None, b * T, width)
         return self.cache[key]
 
     def check(self, what: str, canonical_sel: list[int] | None = None) -> None:
@@ -138,12 +152,13 @@ class Model:
 
 
 @pytest.mark.parametrize("case", CASES, ids=["canonical_q8", "lifo_q8_q4", "canonical_q5_q8",
-                                             "pinned_packed_q8_q4"])
+                                             "pinned_packed_q8_q4", "rope_hadamard_q8_q4"])
 def test_random_operation_sequences(oracle, case):
-    canonical, tk, tv, seed, pinned = case
+    canonical, tk, tv, seed, pinned, xf = case
     cap, budget, reserve = 40, 8, 6
     announce(f"{N_OPS} random operations, canonical={canonical}, types {kv.TYPE_NAMES[tk]}/"
-             f"{kv.TYPE_NAMES[tv]}, seed {seed}, pinned host history and packed store: {pinned}")
+             f"{kv.TYPE_NAMES[tv]}, seed {seed}, pinned host history and packed store: {pinned}, "
+             f"row transform: {xf}")
     k, v, q = history(cap, seed=seed)
     hb = store = None
     if pinned:
@@ -156,13 +171,13 @@ def test_random_operation_sequences(oracle, case):
     rng = np.random.default_rng(seed)
     counts = dict.fromkeys(OPS, 0)
     hits = {"unchanged_ok": 0, "failed_apply": 0, "decode_refused": 0, "stale_refused": 0}
-    with make_engine(budget, reserve, tk, tv, canonical_layout=canonical) as eng:
+    with make_engine(budget, reserve, tk, tv, canonical_layout=canonical, **(XF if xf else {})) as eng:
         eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, 20 * T + 37)
         if pinned:
             eng.set_host_history(hb.data_ptr(), cap)
             eng.set_packed_host(store.data_ptr(), cap)
         ctx = kv.Context.borrow(eng.ctx_handle())
-        m = Model(eng, oracle, k, v, (tk, tv), store)
+        m = Model(eng, oracle, k, v, (tk, tv), store, xf)
         m.check("start")
         last_q, last_mand = 0, []
 
@@ -176,6 +191,8 @@ def test_random_operation_sequences(oracle, case):
 
         for step in range(N_OPS):
             op = OPS[int(rng.choice(len(OPS), p=WEIGHTS / WEIGHTS.sum()))]
+            if xf and op == "decode":
+                op = "append"   # a transformed pool's decoded cells are the model's to write
             qi = int(rng.integers(0, len(queries)))
             qq = queries[qi]
             what = f"step {step} {op}"
