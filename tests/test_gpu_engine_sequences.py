@@ -31,7 +31,9 @@ With a pinned host history and a pinned packed store, every block the engine
 marks as saved holds the oracle's rows in the store.  With the row transform
 (NeoX RoPE 256 on K at the original positions, then attn_rot), the pool rows
 are the oracle's transform and quantization; decoded rows are left out there,
-since a transformed pool's decoded cells are the model's to write.
+since a transformed pool's decoded cells are the model's to write.  With the
+reference's mean-K scorer, every preview's scores are the oracle's over the
+history as it stands.
 """
 from __future__ import annotations
 
@@ -47,7 +49,7 @@ from conftest import load_pkg  # noqa: E402
 kv = load_pkg()
 from kvmem_amd import workloads  # noqa: E402
 
-from engine_helpers import D, E, L, T, block_major_pinned, decode_rows, history, make_engine  # noqa: E402
+from engine_helpers import D, E, HQ, L, T, block_major_pinned, decode_rows, history, make_engine  # noqa: E402
 from test_gpu_transform import expected_rows  # noqa: E402
 
 ALL_KINDS = kv.FAIL_ALLOC | kv.FAIL_COPY | kv.FAIL_LAUNCH
@@ -61,6 +63,8 @@ CASES = [
     (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 104, True, False),
     (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 105, False, True),
 ]
+# the reference's mean-K cosine scorer over key sums the engine keeps current
+MEANK_CASE = (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 106, False, False)
 XF = dict(n_rot=256, rope_freq_base=1e6, attn_rot=1)
 OPS = ["retrieve", "preview_apply", "stale", "append", "decode", "truncate", "fail", "unchanged"]
 WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2], dtype=float)
@@ -82,6 +86,7 @@ class Model:
         self.valid: dict[int, int] = {}
         self.cache: dict[tuple, np.ndarray] = {}
         self.n_packed_checked = 0
+        self.n_scores_checked = 0
 
     def ntok(self, b: int) -> int:
         return min(T, self.total - b * T)
@@ -104,6 +109,31 @@ class Model:
                 self.cache[key] = expected_rows(self.oracle, self.types[which], rows, D, n_rot,
                                                 self.theta if n_rot else None, b * T, width)
         return self.cache[key]
+
+    def check_meank_scores(self, q, what: str) -> None:
+        """The last preview's scores against the oracle's mean-K chain over the
+        history as it is now: token-order query sums, token-order key sums of
+        every block's rows (the tail's partial ones included), score_retrieval."""
+        got = np.array(self.eng.scores(), dtype=np.float64)
+        nb = self.eng.block_count()
+        assert got.size == nb, (what, got.size, nb)
+        key = ("q", q.data_ptr())
+        if key not in self.cache:
+            self.cache[key] = self.oracle.q_accumulate(q.float().cpu().numpy().reshape(L, q.shape[1], -1))
+        q_sum = self.cache[key]
+        sums = np.zeros((L, nb, E), np.float32)
+        mt = np.zeros((L, nb), np.uint32)
+        for b in range(nb):
+            n = self.ntok(b)
+            for layer in range(L):
+                k2 = ("sum", layer, b, n)
+                if k2 not in self.cache:
+                    self.cache[k2] = self.oracle.meank_sum_f16(self.bits[0][layer, b].reshape(T, E)[:n])
+                sums[layer, b] = self.cache[k2]
+                mt[layer, b] = n
+        want = self.oracle.score_meank(q_sum, [q.shape[1]] * L, sums, mt, HQ, E // D, D)
+        assert np.max(np.abs(got - want)) <= 1e-5, (what, float(np.max(np.abs(got - want))))
+        self.n_scores_checked += 1
 
     def check(self, what: str, canonical_sel: list[int] | None = None) -> None:
         eng = self.eng
@@ -154,11 +184,23 @@ class Model:
 @pytest.mark.parametrize("case", CASES, ids=["canonical_q8", "lifo_q8_q4", "canonical_q5_q8",
                                              "pinned_packed_q8_q4", "rope_hadamard_q8_q4"])
 def test_random_operation_sequences(oracle, case):
+    run_sequence(oracle, case, meank=False)
+
+
+def test_random_operation_sequences_meank_scorer(oracle):
+    """The same operations with the reference's mean-K scorer: after every
+    preview the scores are within 1e-5 of the oracle's over the history as it
+    stands, so the key sums the engine keeps across appended, decoded and
+    truncated rows are current."""
+    run_sequence(oracle, MEANK_CASE, meank=True)
+
+
+def run_sequence(oracle, case, meank: bool) -> None:
     canonical, tk, tv, seed, pinned, xf = case
     cap, budget, reserve = 40, 8, 6
     announce(f"{N_OPS} random operations, canonical={canonical}, types {kv.TYPE_NAMES[tk]}/"
              f"{kv.TYPE_NAMES[tv]}, seed {seed}, pinned host history and packed store: {pinned}, "
-             f"row transform: {xf}")
+             f"row transform: {xf}, mean-K scorer: {meank}")
     k, v, q = history(cap, seed=seed)
     hb = store = None
     if pinned:
@@ -171,7 +213,8 @@ def test_random_operation_sequences(oracle, case):
     rng = np.random.default_rng(seed)
     counts = dict.fromkeys(OPS, 0)
     hits = {"unchanged_ok": 0, "failed_apply": 0, "decode_refused": 0, "stale_refused": 0}
-    with make_engine(budget, reserve, tk, tv, canonical_layout=canonical, **(XF if xf else {})) as eng:
+    with make_engine(budget, reserve, tk, tv, canonical_layout=canonical, scorer=int(meank),
+                     **(XF if xf else {})) as eng:
         eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, 20 * T + 37)
         if pinned:
             eng.set_host_history(hb.data_ptr(), cap)
@@ -200,6 +243,8 @@ def test_random_operation_sequences(oracle, case):
             if op == "retrieve":
                 mand = mandatory()
                 want = eng.preview(qq.data_ptr(), qq.shape[1], mandatory=mand).blocks
+                if meank:
+                    m.check_meank_scores(qq, what)
                 st = eng.apply_retrieval(qq.data_ptr(), qq.shape[1], mandatory=mand)
                 got = sorted(m.resident())
                 assert got == want, (what, got, want, st)
@@ -210,6 +255,8 @@ def test_random_operation_sequences(oracle, case):
             elif op == "preview_apply":
                 mand = mandatory()
                 sel = eng.preview(qq.data_ptr(), qq.shape[1], mandatory=mand)
+                if meank:
+                    m.check_meank_scores(qq, what)
                 before = dict(m.valid)
                 need = sum(1 for b in sel.blocks if before.get(b, -1) < m.ntok(b))
                 st = eng.apply(sel)
@@ -305,10 +352,13 @@ def test_random_operation_sequences(oracle, case):
                 assert ok == (view.valid and canon.valid and sel.blocks == canon.blocks), (what, view, sel.blocks)
                 hits["unchanged_ok"] += int(ok)
                 m.check(what)
-    announce(f"operations {counts}; {hits}; packed blocks checked {m.n_packed_checked}")
+    announce(f"operations {counts}; {hits}; packed blocks checked {m.n_packed_checked}; "
+             f"mean-K score sets checked {m.n_scores_checked}")
     assert hits["stale_refused"] >= 1 and hits["failed_apply"] >= 1, hits
     if canonical:
         assert hits["unchanged_ok"] >= 1, hits
     if pinned:
         assert m.n_packed_checked >= 1
+    if meank:
+        assert m.n_scores_checked >= 10
     del hb, store
