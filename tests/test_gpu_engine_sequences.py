@@ -195,12 +195,19 @@ def test_random_operation_sequences_meank_scorer(oracle):
     run_sequence(oracle, MEANK_CASE, meank=True)
 
 
-def run_sequence(oracle, case, meank: bool) -> None:
+def test_random_operation_sequences_host_only_history(oracle):
+    """The reference's deployment shape: every block only in pinned host
+    memory (no history in HBM), a pinned packed store, the mean-K scorer over
+    key sums the device reads from the pinned blocks."""
+    run_sequence(oracle, (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 107, True, False), meank=True, host_only=True)
+
+
+def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
     canonical, tk, tv, seed, pinned, xf = case
     cap, budget, reserve = 40, 8, 6
     announce(f"{N_OPS} random operations, canonical={canonical}, types {kv.TYPE_NAMES[tk]}/"
              f"{kv.TYPE_NAMES[tv]}, seed {seed}, pinned host history and packed store: {pinned}, "
-             f"row transform: {xf}, mean-K scorer: {meank}")
+             f"row transform: {xf}, mean-K scorer: {meank}, host-only history: {host_only}")
     k, v, q = history(cap, seed=seed)
     hb = store = None
     if pinned:
@@ -215,9 +222,14 @@ def run_sequence(oracle, case, meank: bool) -> None:
     hits = {"unchanged_ok": 0, "failed_apply": 0, "decode_refused": 0, "stale_refused": 0}
     with make_engine(budget, reserve, tk, tv, canonical_layout=canonical, scorer=int(meank),
                      **(XF if xf else {})) as eng:
-        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, 20 * T + 37)
-        if pinned:
+        if host_only:
             eng.set_host_history(hb.data_ptr(), cap)
+            eng.append_tokens(20 * T + 37)
+        else:
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, 20 * T + 37)
+            if pinned:
+                eng.set_host_history(hb.data_ptr(), cap)
+        if pinned:
             eng.set_packed_host(store.data_ptr(), cap)
         ctx = kv.Context.borrow(eng.ctx_handle())
         m = Model(eng, oracle, k, v, (tk, tv), store, xf)
