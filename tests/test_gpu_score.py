@@ -156,3 +156,25 @@ def test_score_full_256k_sampled_and_topk(ctx, oracle):
     assert sel == want_sel
     del k
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("Tq", [80, 200, 512], ids=["2_slices", "4_slices", "8_slices"])
+def test_score_multi_slice_short_chunks(ctx, oracle, Tq):
+    """Queries of several 384-row slices over 4100 blocks, the last one
+    partial: the launch splits the blocks into short chunks (32, 64 and 16
+    blocks for 2, 4 and 8 slices, the last chunk ragged).  Blocks on both
+    sides of chunk boundaries, the last chunk's and the partial last block
+    are checked against the oracle's fp32 scorer."""
+    L, B, Hkv, Hq, D, last_T = 2, 4100, 4, 24, 256, 50
+    announce(f"scorer over {B} blocks, {Tq}-token query ({-(-Tq * Hq // Hkv // 384)} slices)")
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=Tq, seed=90 + Tq)
+    s, ls = run_score(ctx, k, q, kv.TYPE_BF16, Hq, Hkv, D, last_T)
+    assert np.isfinite(s).all()
+    rng = np.random.default_rng(Tq)
+    edges = [0, 1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 4031, 4032, 4095, 4096, 4097, 4098]
+    ids = np.unique(np.concatenate([edges, rng.choice(B - 1, 12, replace=False), [B - 1]]))
+    ksub = workloads.to_bits(torch, k[:, torch.from_numpy(ids.astype(np.int64)).cuda()])
+    want = oracle.score_pertoken_max_f32(q_f32(q), ksub, 0, ids.size, last_block_tokens=last_T)
+    assert_close(ls[:, ids], want, "layer scores")
+    del k
+    torch.cuda.empty_cache()
