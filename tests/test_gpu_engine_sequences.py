@@ -37,6 +37,8 @@ history as it stands.
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -68,7 +70,9 @@ MEANK_CASE = (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 106, False, False)
 XF = dict(n_rot=256, rope_freq_base=1e6, attn_rot=1)
 OPS = ["retrieve", "preview_apply", "stale", "append", "decode", "truncate", "fail", "unchanged"]
 WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2], dtype=float)
-N_OPS = 150
+# KVMEM_SEQ_OPS / KVMEM_SEQ_SEED_OFFSET lengthen a run or draw other seeds
+N_OPS = int(os.environ.get("KVMEM_SEQ_OPS", "150"))
+SEED_OFFSET = int(os.environ.get("KVMEM_SEQ_SEED_OFFSET", "0"))
 
 
 def announce(msg: str) -> None:
@@ -204,6 +208,7 @@ def test_random_operation_sequences_host_only_history(oracle):
 
 def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
     canonical, tk, tv, seed, pinned, xf = case
+    seed += SEED_OFFSET
     cap, budget, reserve = 40, 8, 6
     announce(f"{N_OPS} random operations, canonical={canonical}, types {kv.TYPE_NAMES[tk]}/"
              f"{kv.TYPE_NAMES[tv]}, seed {seed}, pinned host history and packed store: {pinned}, "
