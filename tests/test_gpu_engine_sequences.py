@@ -20,7 +20,13 @@ seeded random order:
   (kvmem_hip_debug_fail_after: nothing faults);
 - commit_unchanged after a preview with the last apply's query and
   mandatory blocks, which must succeed exactly when the selection equals
-  the pool's canonical attention view.
+  the pool's canonical attention view;
+- a request span set or cleared (query rows and force_pos): the blocks
+  retrieval_mandatory derives from it are checked after every operation, as
+  the history grows and shrinks under it, every preview keeps them with the
+  sink and the caller's mandatory blocks whenever they fit the budget, and
+  selection_fits holds exactly when a preview kept every derived block
+  (llama-memory-kvmem.cpp:3026-3045, 3069-3084).
 
 A model in the test tracks how many rows of each resident block the pool
 holds.  After every operation: the engine's resident set is the model's;
@@ -68,8 +74,8 @@ CASES = [
 # the reference's mean-K cosine scorer over key sums the engine keeps current
 MEANK_CASE = (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 106, False, False)
 XF = dict(n_rot=256, rope_freq_base=1e6, attn_rot=1)
-OPS = ["retrieve", "preview_apply", "stale", "append", "decode", "truncate", "fail", "unchanged"]
-WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2], dtype=float)
+OPS = ["retrieve", "preview_apply", "stale", "append", "decode", "truncate", "fail", "unchanged", "span"]
+WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2, 1], dtype=float)
 # KVMEM_SEQ_OPS / KVMEM_SEQ_SEED_OFFSET lengthen a run or draw other seeds
 N_OPS = int(os.environ.get("KVMEM_SEQ_OPS", "150"))
 SEED_OFFSET = int(os.environ.get("KVMEM_SEQ_SEED_OFFSET", "0"))
@@ -224,7 +230,7 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
     queries = [q, (q.float() * -1.0).to(torch.bfloat16), q[:, :, perm].contiguous()]
     rng = np.random.default_rng(seed)
     counts = dict.fromkeys(OPS, 0)
-    hits = {"unchanged_ok": 0, "failed_apply": 0, "decode_refused": 0, "stale_refused": 0}
+    hits = {"unchanged_ok": 0, "failed_apply": 0, "decode_refused": 0, "stale_refused": 0, "spans": 0}
     with make_engine(budget, reserve, tk, tv, canonical_layout=canonical, scorer=int(meank),
                      **(XF if xf else {})) as eng:
         if host_only:
@@ -240,6 +246,24 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
         m = Model(eng, oracle, k, v, (tk, tv), store, xf)
         m.check("start")
         last_q, last_mand = 0, []
+        span = None   # (query_begin, query_end, force_pos) of the request span, or none
+
+        def derived() -> list[int]:
+            """retrieval_mandatory as the history stands: the blocks overlapping
+            the span's rows in block order, then the block holding force_pos."""
+            if span is None:
+                return []
+            qb, qe, fp = span
+            end = qe if qe > 0 else m.total
+            out = [b for b in range(eng.block_count()) if b * T + m.ntok(b) > qb and b * T < end]
+            if 0 <= fp < m.total:
+                out.append(fp // T)
+            return out
+
+        def kept(sel_blocks: list[int], mand: list[int], what: str) -> None:
+            need = {0} | set(mand) | set(derived())
+            if len(need) <= budget:
+                assert need <= set(sel_blocks), (what, sorted(need), sel_blocks)
 
         def mandatory() -> list[int]:
             nb = eng.block_count()
@@ -265,7 +289,7 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 st = eng.apply_retrieval(qq.data_ptr(), qq.shape[1], mandatory=mand)
                 got = sorted(m.resident())
                 assert got == want, (what, got, want, st)
-                assert set(mand) <= set(got), what
+                kept(got, mand, what)
                 m.applied(want)
                 last_q, last_mand = qi, mand
                 m.check(what, want if canonical else None)
@@ -274,6 +298,8 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 sel = eng.preview(qq.data_ptr(), qq.shape[1], mandatory=mand)
                 if meank:
                     m.check_meank_scores(qq, what)
+                kept(sel.blocks, mand, what)
+                assert eng.selection_fits(sel, m.total, 0) == (set(derived()) <= set(sel.blocks)), what
                 before = dict(m.valid)
                 need = sum(1 for b in sel.blocks if before.get(b, -1) < m.ntok(b))
                 st = eng.apply(sel)
@@ -369,6 +395,20 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 assert ok == (view.valid and canon.valid and sel.blocks == canon.blocks), (what, view, sel.blocks)
                 hits["unchanged_ok"] += int(ok)
                 m.check(what)
+            elif op == "span":
+                if rng.integers(0, 3) == 0 or m.total == 0:
+                    eng.set_request_span(-1)
+                    span = None
+                else:
+                    qb = int(rng.integers(0, m.total))
+                    qe = 0 if rng.integers(0, 2) == 0 else int(rng.integers(qb + 1, m.total + 1))
+                    fp = -1 if rng.integers(0, 2) == 0 else int(rng.integers(0, m.total))
+                    eng.set_request_span(qb, qe, fp)
+                    span = (qb, qe, fp)
+                hits["spans"] += int(span is not None)
+                m.check(what)
+            if span is not None:
+                assert eng.retrieval_mandatory() == derived(), (what, span, eng.retrieval_mandatory())
     announce(f"operations {counts}; {hits}; packed blocks checked {m.n_packed_checked}; "
              f"mean-K score sets checked {m.n_scores_checked}")
     assert hits["stale_refused"] >= 1 and hits["failed_apply"] >= 1, hits
