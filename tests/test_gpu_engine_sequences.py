@@ -26,7 +26,13 @@ seeded random order:
   the history grows and shrinks under it, every preview keeps them with the
   sink and the caller's mandatory blocks whenever they fit the budget, and
   selection_fits holds exactly when a preview kept every derived block
-  (llama-memory-kvmem.cpp:3026-3045, 3069-3084).
+  (llama-memory-kvmem.cpp:3026-3045, 3069-3084);
+- query rows captured into the engine's window (bf16 Qcur views at random
+  positions, kept when the span holds them, the newest 48), or the window
+  emptied; then a preview over the window, whose selection and scores must
+  equal a preview over the same rows passed explicitly, bit for bit (the
+  newest 48 rows with a span set, the newest 16 without), and its apply
+  (llama-memory-kvmem.cpp:2157-2172, 2206-2219; tools/llama-kvmem-server.cpp:1032-1038).
 
 A model in the test tracks how many rows of each resident block the pool
 holds.  After every operation: the engine's resident set is the model's;
@@ -74,8 +80,10 @@ CASES = [
 # the reference's mean-K cosine scorer over key sums the engine keeps current
 MEANK_CASE = (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 106, False, False)
 XF = dict(n_rot=256, rope_freq_base=1e6, attn_rot=1)
-OPS = ["retrieve", "preview_apply", "stale", "append", "decode", "truncate", "fail", "unchanged", "span"]
-WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2, 1], dtype=float)
+OPS = ["retrieve", "preview_apply", "stale", "append", "decode", "truncate", "fail", "unchanged", "span",
+       "capture", "wretrieve"]
+WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2, 1, 2, 2], dtype=float)
+QWIN_CAP, QWIN_LAST = 48, 16   # query_max_tokens, query_last
 # KVMEM_SEQ_OPS / KVMEM_SEQ_SEED_OFFSET lengthen a run or draw other seeds
 N_OPS = int(os.environ.get("KVMEM_SEQ_OPS", "150"))
 SEED_OFFSET = int(os.environ.get("KVMEM_SEQ_SEED_OFFSET", "0"))
@@ -120,7 +128,7 @@ class Model:
                                                 self.theta if n_rot else None, b * T, width)
         return self.cache[key]
 
-    def check_meank_scores(self, q, what: str) -> None:
+    def check_meank_scores(self, q, what: str, cache_q: bool = True) -> None:
         """The last preview's scores against the oracle's mean-K chain over the
         history as it is now: token-order query sums, token-order key sums of
         every block's rows (the tail's partial ones included), score_retrieval."""
@@ -128,9 +136,11 @@ class Model:
         nb = self.eng.block_count()
         assert got.size == nb, (what, got.size, nb)
         key = ("q", q.data_ptr())
-        if key not in self.cache:
-            self.cache[key] = self.oracle.q_accumulate(q.float().cpu().numpy().reshape(L, q.shape[1], -1))
-        q_sum = self.cache[key]
+        if not cache_q or key not in self.cache:
+            q_sum = self.oracle.q_accumulate(q.float().cpu().numpy().reshape(L, q.shape[1], -1))
+            if cache_q:   # only for the run's fixed query tensors: a freed pointer is reused
+                self.cache[key] = q_sum
+        q_sum = self.cache[key] if cache_q else q_sum
         sums = np.zeros((L, nb, E), np.float32)
         mt = np.zeros((L, nb), np.uint32)
         for b in range(nb):
@@ -230,9 +240,10 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
     queries = [q, (q.float() * -1.0).to(torch.bfloat16), q[:, :, perm].contiguous()]
     rng = np.random.default_rng(seed)
     counts = dict.fromkeys(OPS, 0)
-    hits = {"unchanged_ok": 0, "failed_apply": 0, "decode_refused": 0, "stale_refused": 0, "spans": 0}
+    hits = {"unchanged_ok": 0, "failed_apply": 0, "decode_refused": 0, "stale_refused": 0, "spans": 0,
+            "captures": 0, "window_previews": 0}
     with make_engine(budget, reserve, tk, tv, canonical_layout=canonical, scorer=int(meank),
-                     **(XF if xf else {})) as eng:
+                     query_max_tokens=QWIN_CAP, query_last=QWIN_LAST, **(XF if xf else {})) as eng:
         if host_only:
             eng.set_host_history(hb.data_ptr(), cap)
             eng.append_tokens(20 * T + 37)
@@ -259,6 +270,15 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
             if 0 <= fp < m.total:
                 out.append(fp // T)
             return out
+
+        window = []   # captured query rows, oldest first: [L][HQ][D] bf16 each
+
+        def contains(pos: int) -> bool:
+            """query_contains: with no span every row is a query row."""
+            if span is None:
+                return True
+            qb, qe, _ = span
+            return qb <= pos and (qe <= 0 or pos < qe)
 
         def kept(sel_blocks: list[int], mand: list[int], what: str) -> None:
             need = {0} | set(mand) | set(derived())
@@ -407,6 +427,45 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                     span = (qb, qe, fp)
                 hits["spans"] += int(span is not None)
                 m.check(what)
+            elif op == "capture":
+                if rng.integers(0, 8) == 0:
+                    eng.reset_query()
+                    window = []
+                else:
+                    n = int(rng.integers(1, 40))
+                    pos0 = int(rng.integers(0, m.total + 1))
+                    positions = list(range(pos0, pos0 + n))
+                    x = (torch.randn((L, n, HQ, D), generator=g) * 2).to(torch.bfloat16)
+                    for layer in range(L):
+                        xd = x[layer].contiguous().cuda()
+                        torch.cuda.synchronize()
+                        eng.capture_q(layer, xd.data_ptr(), kv.TYPE_BF16, 2, D * 2, HQ * D * 2, positions)
+                        ctx.sync()   # the view is freed after this
+                    window += [x[:, i] for i, p in enumerate(positions) if contains(p)]
+                    window = window[-QWIN_CAP:]
+                hits["captures"] += 1
+                m.check(what)
+            elif op == "wretrieve":
+                n = min(len(window), QWIN_CAP if span is not None else QWIN_LAST)
+                if n == 0:   # an empty window is refused
+                    with pytest.raises(kv.KvMemError):
+                        eng.query_rows()
+                    continue
+                assert eng.query_rows() == n, (what, eng.query_rows(), n)
+                sel = eng.preview_window()
+                got = np.array(eng.scores(), dtype=np.float64)
+                qe = torch.stack(window[-n:], dim=1).contiguous().cuda()   # [L][n][HQ][D]
+                torch.cuda.synchronize()
+                sel2 = eng.preview(qe.data_ptr(), n)
+                assert sel.blocks == sel2.blocks, (what, sel.blocks, sel2.blocks)
+                assert np.array_equal(got, np.array(eng.scores(), dtype=np.float64)), what
+                if meank:
+                    m.check_meank_scores(qe, what, cache_q=False)
+                kept(sel.blocks, [], what)
+                eng.apply(sel2)
+                m.applied(sel2.blocks)
+                hits["window_previews"] += 1
+                m.check(what, sel2.blocks if canonical else None)
             if span is not None:
                 assert eng.retrieval_mandatory() == derived(), (what, span, eng.retrieval_mandatory())
     announce(f"operations {counts}; {hits}; packed blocks checked {m.n_packed_checked}; "
