@@ -21,8 +21,10 @@ seeded random order:
 - commit_unchanged after a preview with the last apply's query and
   mandatory blocks, which must succeed exactly when the selection equals
   the pool's canonical attention view;
-- a request span set or cleared (query rows and force_pos): the blocks
-  retrieval_mandatory derives from it are checked after every operation, as
+- a request span (query rows and force_pos) or turn spans (query and
+  mandatory row ranges; a reversed range is refused) set, or the spans
+  cleared: the blocks retrieval_mandatory derives are checked after every
+  operation, as
   the history grows and shrinks under it, every preview keeps them with the
   sink and the caller's mandatory blocks whenever they fit the budget, and
   selection_fits holds exactly when a preview kept every derived block
@@ -257,28 +259,41 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
         m = Model(eng, oracle, k, v, (tk, tv), store, xf)
         m.check("start")
         last_q, last_mand = 0, []
-        span = None   # (query_begin, query_end, force_pos) of the request span, or none
+        # the spans: none, a request span (query rows [qb, qe), qe <= 0 to the end) or turn
+        # spans (query and mandatory row ranges); force_pos stays from the last request span
+        spans = {"kind": None, "qb": -1, "qe": 0, "query": [], "mand": [], "force": -1}
 
         def derived() -> list[int]:
             """retrieval_mandatory as the history stands: the blocks overlapping
-            the span's rows in block order, then the block holding force_pos."""
-            if span is None:
-                return []
-            qb, qe, fp = span
-            end = qe if qe > 0 else m.total
-            out = [b for b in range(eng.block_count()) if b * T + m.ntok(b) > qb and b * T < end]
-            if 0 <= fp < m.total:
-                out.append(fp // T)
+            the mandatory rows in block order, then the block holding force_pos."""
+            if spans["kind"] == "turns":
+                ranges = spans["mand"]
+            elif spans["kind"] == "req":
+                ranges = [(spans["qb"], spans["qe"] if spans["qe"] > 0 else m.total)]
+            else:
+                ranges = []
+            out = [b for b in range(eng.block_count())
+                   if any(b * T + m.ntok(b) > lo and b * T < hi for lo, hi in ranges)]
+            if 0 <= spans["force"] < m.total:
+                out.append(spans["force"] // T)
             return out
 
         window = []   # captured query rows, oldest first: [L][HQ][D] bf16 each
 
         def contains(pos: int) -> bool:
-            """query_contains: with no span every row is a query row."""
-            if span is None:
-                return True
-            qb, qe, _ = span
-            return qb <= pos and (qe <= 0 or pos < qe)
+            """query_contains; with no span every row is a query row."""
+            if spans["kind"] == "turns":
+                return any(lo <= pos < hi for lo, hi in spans["query"])
+            if spans["kind"] == "req":
+                return spans["qb"] <= pos and (spans["qe"] <= 0 or pos < spans["qe"])
+            return True
+
+        def ranges(k: int) -> list[tuple[int, int]]:
+            out = []
+            for _ in range(k):
+                lo = int(rng.integers(0, m.total + 1))
+                out.append((lo, lo + int(rng.integers(0, 3 * T))))
+            return out
 
         def kept(sel_blocks: list[int], mand: list[int], what: str) -> None:
             need = {0} | set(mand) | set(derived())
@@ -416,16 +431,25 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 hits["unchanged_ok"] += int(ok)
                 m.check(what)
             elif op == "span":
-                if rng.integers(0, 3) == 0 or m.total == 0:
+                r = int(rng.integers(0, 4))
+                if r == 0 or m.total == 0:
                     eng.set_request_span(-1)
-                    span = None
+                    spans.update(kind=None, force=-1)
+                elif r == 1:   # turn spans: query and mandatory row ranges
+                    q_r, m_r = ranges(int(rng.integers(1, 3))), ranges(int(rng.integers(0, 3)))
+                    if rng.integers(0, 6) == 0:   # a reversed range is refused, nothing changes
+                        with pytest.raises(kv.KvMemError):
+                            eng.set_turn_spans(query=q_r + [(5, 2)], mandatory=m_r)
+                    else:
+                        eng.set_turn_spans(query=q_r, mandatory=m_r)
+                        spans.update(kind="turns", query=q_r, mand=m_r)
                 else:
                     qb = int(rng.integers(0, m.total))
                     qe = 0 if rng.integers(0, 2) == 0 else int(rng.integers(qb + 1, m.total + 1))
                     fp = -1 if rng.integers(0, 2) == 0 else int(rng.integers(0, m.total))
                     eng.set_request_span(qb, qe, fp)
-                    span = (qb, qe, fp)
-                hits["spans"] += int(span is not None)
+                    spans.update(kind="req", qb=qb, qe=qe, force=fp)
+                hits["spans"] += int(spans["kind"] is not None)
                 m.check(what)
             elif op == "capture":
                 if rng.integers(0, 8) == 0:
@@ -446,7 +470,7 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 hits["captures"] += 1
                 m.check(what)
             elif op == "wretrieve":
-                n = min(len(window), QWIN_CAP if span is not None else QWIN_LAST)
+                n = min(len(window), QWIN_CAP if spans["kind"] is not None else QWIN_LAST)
                 if n == 0:   # an empty window is refused
                     with pytest.raises(kv.KvMemError):
                         eng.query_rows()
@@ -466,8 +490,7 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 m.applied(sel2.blocks)
                 hits["window_previews"] += 1
                 m.check(what, sel2.blocks if canonical else None)
-            if span is not None:
-                assert eng.retrieval_mandatory() == derived(), (what, span, eng.retrieval_mandatory())
+            assert eng.retrieval_mandatory() == derived(), (what, spans, eng.retrieval_mandatory())
     announce(f"operations {counts}; {hits}; packed blocks checked {m.n_packed_checked}; "
              f"mean-K score sets checked {m.n_scores_checked}")
     assert hits["stale_refused"] >= 1 and hits["failed_apply"] >= 1, hits
