@@ -493,11 +493,14 @@ KVMEM_HIP_API uint32_t kvmem_engine_free_slots(const kvmem_engine *e);
  * get: host q_sum [n_layers][n_head*head_dim], q_count [n_layers] receive
  * the state a preview with q = NULL would use -- the rows of the query
  * window summed in token order, or the state set_query set (ERR_INVALID
- * with no captured rows; llama-memory-kvmem.cpp:3104-3119).
- * set: the caller's state replaces the window for previews with q = NULL
- * and freezes the query (capture_q keeps no rows) until reset_query or
- * freeze_query(0) (llama-memory-kvmem.cpp:3121-3137); sums must be finite
- * and the counts equal and nonzero (ERR_INVALID, nothing changed).  The
+ * with neither; llama-memory-kvmem.cpp:3104-3119).
+ * set: the caller's state replaces the rows captured so far for previews
+ * with q = NULL, and freezes the query (capture_q keeps no rows) until
+ * freeze_query(0); rows captured after that add onto the state (sums in
+ * token order, counts), as the reference's harvest adds onto q_sum_ and
+ * q_count_ (llama-memory-kvmem.cpp:2164-2172, 3121-3137).  reset_query
+ * drops the state.  Sums must be finite and the counts equal and nonzero
+ * (ERR_INVALID, nothing changed).  The
  * per-token scorer reads the rows themselves, not their sum:
  * ERR_UNSUPPORTED on an engine with scorer = KVMEM_SCORER_TOKEN_MAX.
  * freeze: while frozen, capture_q keeps no rows (query_contains is false,

@@ -416,8 +416,10 @@ struct kvmem_engine {
     uint32_t qwin_cap = 0;
     std::vector<uint64_t> qwin_count;  // rows captured per layer since the reset
     bool query_frozen = false;         // capture_q keeps no rows (freeze_query, set_query)
-    bool query_imported = false;       // d_qsum holds sums set by set_query
-    std::vector<uint32_t> imp_count;   // their row counts per layer
+    bool query_imported = false;       // a state set by set_query is in use
+    float *d_qimp = nullptr;           // its sums [L][n_head*head_dim]
+    std::vector<uint32_t> imp_count;   // its row counts per layer
+    uint64_t imp_base = 0;             // window rows captured before it was set
     void *packed_base = nullptr;        // pinned packed host store (may be null)
     uint32_t packed_capacity = 0;       // blocks it holds
     std::vector<uint8_t> packed_valid;  // block's packed rows are in the store
@@ -765,6 +767,9 @@ void kvmem_engine_destroy(kvmem_engine *e) {
     }
     if (e->d_qsum) {
         (void) hipFree(e->d_qsum);
+    }
+    if (e->d_qimp) {
+        (void) hipFree(e->d_qimp);
     }
     if (e->d_mt) {
         (void) hipFree(e->d_mt);
@@ -1164,7 +1169,7 @@ int rollback(kvmem_engine *e, ApplyUndo &u, int code) {
 // query_max_tokens captured rows (query_last when no span is set; the
 // server's clamp and fallback, tools/llama-kvmem-server.cpp:1032-1038,
 // 1089-1096).  Every layer must hold the same number of rows.
-int window_rows(kvmem_engine *e, std::vector<uint32_t> &rows) {
+int window_rows(kvmem_engine *e, std::vector<uint32_t> &rows, uint64_t since = 0, bool allow_none = false) {
     rows.clear();
     const uint64_t c = e->qwin_count.empty() ? 0 : e->qwin_count[0];
     for (uint64_t x : e->qwin_count) {
@@ -1172,13 +1177,55 @@ int window_rows(kvmem_engine *e, std::vector<uint32_t> &rows) {
             return e->fail(KVMEM_HIP_ERR_INVALID, "query window: layers hold different numbers of rows");
         }
     }
+    // only rows captured after `since` rows (those since a set_query)
     const uint64_t limit = e->spans_set() ? e->qwin_cap : std::min<uint32_t>(e->qwin_cap, e->p.query_last);
-    const uint64_t n = std::min<uint64_t>(c, limit);
+    const uint64_t n = std::min<uint64_t>(c > since ? c - since : 0, limit);
     if (n == 0) {
-        return e->fail(KVMEM_HIP_ERR_INVALID, "query window: no query rows captured");
+        return allow_none ? KVMEM_HIP_OK : e->fail(KVMEM_HIP_ERR_INVALID, "query window: no query rows captured");
     }
     for (uint64_t i = c - n; i < c; ++i) {
         rows.push_back(static_cast<uint32_t>(i % e->qwin_cap));
+    }
+    return KVMEM_HIP_OK;
+}
+
+// The query state a preview with q = NULL reads, into d_qsum and `counts`:
+// the window's rows summed in token order; after set_query, the set sums
+// with the rows captured since (the query unfrozen) added onto them in
+// token order, and the set counts plus those rows -- as the reference's
+// harvest adds each row onto q_sum_ and q_count_ after set_query
+// (llama-memory-kvmem.cpp:2164-2172, 3121-3137).
+int query_state(kvmem_engine *e, std::vector<uint32_t> &counts) {
+    const uint32_t L = e->p.n_layers;
+    const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
+    const size_t bytes = sizeof(float) * static_cast<size_t>(L) * n_embd_q;
+    if (!e->d_qsum && hipMalloc(&e->d_qsum, bytes) != hipSuccess) {
+        e->d_qsum = nullptr;
+        return e->fail(KVMEM_HIP_ERR_NOMEM, "query sums");
+    }
+    std::vector<uint32_t> rows;
+    int rc = window_rows(e, rows, e->query_imported ? e->imp_base : 0, e->query_imported);
+    if (rc != KVMEM_HIP_OK) {
+        return rc;
+    }
+    if (e->query_imported) {
+        hipStream_t st = static_cast<hipStream_t>(kvmem_hip_get_stream(e->ctx));
+        if (hipMemcpyAsync(e->d_qsum, e->d_qimp, bytes, hipMemcpyDeviceToDevice, st) != hipSuccess) {
+            return e->fail(KVMEM_HIP_ERR_RUNTIME, "query state: copy of the set sums");
+        }
+    }
+    if (!rows.empty()) {
+        rc = kvmem_hip_q_accumulate(e->ctx, e->d_qwin, KVMEM_TYPE_F32, L, e->qwin_cap, n_embd_q, rows.data(),
+                                    static_cast<uint32_t>(rows.size()), e->query_imported ? 0 : 1, e->d_qsum);
+        if (rc != KVMEM_HIP_OK) {
+            return e->fail_ctx(rc, "query state: sums");
+        }
+    }
+    counts.assign(L, static_cast<uint32_t>(rows.size()));
+    if (e->query_imported) {
+        for (uint32_t l = 0; l < L; ++l) {
+            counts[l] += e->imp_count[l];
+        }
     }
     return KVMEM_HIP_OK;
 }
@@ -1227,8 +1274,10 @@ int preview_scores(kvmem_engine *e, const void *q, int32_t q_type, uint32_t n_q_
     }
     const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
     if (imported) {
-        // the set query's sums and counts, as q_sum_ / q_count_ after set_query
-        return meank_scores(e, e->d_qsum, e->imp_count.data());
+        // the set query's sums and counts, with the rows captured since
+        std::vector<uint32_t> counts;
+        const int rc = query_state(e, counts);
+        return rc == KVMEM_HIP_OK ? meank_scores(e, e->d_qsum, counts.data()) : rc;
     }
     if (e->p.scorer == KVMEM_SCORER_MEAN_K) {
         // the reference's scorer over the sum of the query rows
@@ -1849,34 +1898,18 @@ int kvmem_engine_get_query(kvmem_engine *e, float *q_sum, uint32_t *q_count) {
     if (!q_sum || !q_count) {
         return e->fail(KVMEM_HIP_ERR_INVALID, "get_query: null argument");
     }
-    const uint32_t L = e->p.n_layers;
-    const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
-    const size_t bytes = sizeof(float) * static_cast<size_t>(L) * n_embd_q;
-    if (!e->d_qsum && hipMalloc(&e->d_qsum, bytes) != hipSuccess) {
-        e->d_qsum = nullptr;
-        return e->fail(KVMEM_HIP_ERR_NOMEM, "get_query: query sums");
+    std::vector<uint32_t> counts;
+    const int rc = query_state(e, counts);
+    if (rc != KVMEM_HIP_OK) {
+        return rc;
     }
-    if (!e->query_imported) {
-        // the rows a preview would read, summed in token order
-        std::vector<uint32_t> rows;
-        const int rc = window_rows(e, rows);
-        if (rc != KVMEM_HIP_OK) {
-            return rc;
-        }
-        const int arc = kvmem_hip_q_accumulate(e->ctx, e->d_qwin, KVMEM_TYPE_F32, L, e->qwin_cap, n_embd_q,
-                                               rows.data(), static_cast<uint32_t>(rows.size()), 1, e->d_qsum);
-        if (arc != KVMEM_HIP_OK) {
-            return e->fail_ctx(arc, "get_query: sums");
-        }
-        std::fill(q_count, q_count + L, static_cast<uint32_t>(rows.size()));
-    } else {
-        std::copy(e->imp_count.begin(), e->imp_count.end(), q_count);
-    }
+    const size_t bytes = sizeof(float) * static_cast<size_t>(e->p.n_layers) * e->p.n_head * e->p.head_dim;
     hipStream_t st = static_cast<hipStream_t>(kvmem_hip_get_stream(e->ctx));
     if (hipMemcpyAsync(q_sum, e->d_qsum, bytes, hipMemcpyDeviceToHost, st) != hipSuccess ||
         hipStreamSynchronize(st) != hipSuccess) {
         return e->fail(KVMEM_HIP_ERR_RUNTIME, "get_query: copy");
     }
+    std::copy(counts.begin(), counts.end(), q_count);
     return KVMEM_HIP_OK;
 }
 
@@ -1904,16 +1937,19 @@ int kvmem_engine_set_query(kvmem_engine *e, const float *q_sum, const uint32_t *
             return e->fail(KVMEM_HIP_ERR_INVALID, "set_query: row counts must be equal and nonzero");
         }
     }
-    if (!e->d_qsum && hipMalloc(&e->d_qsum, sizeof(float) * n) != hipSuccess) {
-        e->d_qsum = nullptr;
+    if (!e->d_qimp && hipMalloc(&e->d_qimp, sizeof(float) * n) != hipSuccess) {
+        e->d_qimp = nullptr;
         return e->fail(KVMEM_HIP_ERR_NOMEM, "set_query: query sums");
     }
     hipStream_t st = static_cast<hipStream_t>(kvmem_hip_get_stream(e->ctx));
-    if (hipMemcpyAsync(e->d_qsum, q_sum, sizeof(float) * n, hipMemcpyHostToDevice, st) != hipSuccess ||
+    if (hipMemcpyAsync(e->d_qimp, q_sum, sizeof(float) * n, hipMemcpyHostToDevice, st) != hipSuccess ||
         hipStreamSynchronize(st) != hipSuccess) {
         return e->fail(KVMEM_HIP_ERR_RUNTIME, "set_query: copy");
     }
+    // the state replaces the rows captured so far; rows captured once the
+    // query is unfrozen add onto it
     e->imp_count.assign(q_count, q_count + L);
+    e->imp_base = e->qwin_count.empty() ? 0 : e->qwin_count[0];
     e->query_imported = true;
     e->query_frozen = true;
     return KVMEM_HIP_OK;

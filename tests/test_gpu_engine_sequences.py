@@ -34,7 +34,14 @@ seeded random order:
   emptied; then a preview over the window, whose selection and scores must
   equal a preview over the same rows passed explicitly, bit for bit (the
   newest 48 rows with a span set, the newest 16 without), and its apply
-  (llama-memory-kvmem.cpp:2157-2172, 2206-2219; tools/llama-kvmem-server.cpp:1032-1038).
+  (llama-memory-kvmem.cpp:2157-2172, 2206-2219; tools/llama-kvmem-server.cpp:1032-1038);
+- the query state: get_query bit-exact against the oracle's token-order sum
+  of the rows the model holds, set_query of a state read back or of a random
+  finite one (refused as unsupported by the per-token scorer), freeze and
+  unfreeze; a frozen query keeps no captured rows, and rows captured once it
+  is unfrozen add onto a set state, as the reference's harvest adds onto
+  q_sum_ after set_query (llama-memory-kvmem.cpp:2164-2172, 3104-3137); a
+  window preview with a set state scores as the oracle does over it.
 
 A model in the test tracks how many rows of each resident block the pool
 holds.  After every operation: the engine's resident set is the model's;
@@ -83,8 +90,8 @@ CASES = [
 MEANK_CASE = (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 106, False, False)
 XF = dict(n_rot=256, rope_freq_base=1e6, attn_rot=1)
 OPS = ["retrieve", "preview_apply", "stale", "append", "decode", "truncate", "fail", "unchanged", "span",
-       "capture", "wretrieve"]
-WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2, 1, 2, 2], dtype=float)
+       "capture", "wretrieve", "qstate"]
+WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2, 1, 2, 2, 1], dtype=float)
 QWIN_CAP, QWIN_LAST = 48, 16   # query_max_tokens, query_last
 # KVMEM_SEQ_OPS / KVMEM_SEQ_SEED_OFFSET lengthen a run or draw other seeds
 N_OPS = int(os.environ.get("KVMEM_SEQ_OPS", "150"))
@@ -130,19 +137,23 @@ class Model:
                                                 self.theta if n_rot else None, b * T, width)
         return self.cache[key]
 
-    def check_meank_scores(self, q, what: str, cache_q: bool = True) -> None:
+    def check_meank_scores(self, q, what: str, cache_q: bool = True, state=None) -> None:
         """The last preview's scores against the oracle's mean-K chain over the
         history as it is now: token-order query sums, token-order key sums of
         every block's rows (the tail's partial ones included), score_retrieval."""
         got = np.array(self.eng.scores(), dtype=np.float64)
         nb = self.eng.block_count()
         assert got.size == nb, (what, got.size, nb)
-        key = ("q", q.data_ptr())
-        if not cache_q or key not in self.cache:
-            q_sum = self.oracle.q_accumulate(q.float().cpu().numpy().reshape(L, q.shape[1], -1))
-            if cache_q:   # only for the run's fixed query tensors: a freed pointer is reused
-                self.cache[key] = q_sum
-        q_sum = self.cache[key] if cache_q else q_sum
+        if state is not None:   # (sums [L][HQ*D], counts [L]): a query state
+            q_sum, q_count = state
+        else:
+            key = ("q", q.data_ptr())
+            if not cache_q or key not in self.cache:
+                q_sum = self.oracle.q_accumulate(q.float().cpu().numpy().reshape(L, q.shape[1], -1))
+                if cache_q:   # only for the run's fixed query tensors: a freed pointer is reused
+                    self.cache[key] = q_sum
+            q_sum = self.cache[key] if cache_q else q_sum
+            q_count = [q.shape[1]] * L
         sums = np.zeros((L, nb, E), np.float32)
         mt = np.zeros((L, nb), np.uint32)
         for b in range(nb):
@@ -153,7 +164,7 @@ class Model:
                     self.cache[k2] = self.oracle.meank_sum_f16(self.bits[0][layer, b].reshape(T, E)[:n])
                 sums[layer, b] = self.cache[k2]
                 mt[layer, b] = n
-        want = self.oracle.score_meank(q_sum, [q.shape[1]] * L, sums, mt, HQ, E // D, D)
+        want = self.oracle.score_meank(q_sum, q_count, sums, mt, HQ, E // D, D)
         assert np.max(np.abs(got - want)) <= 1e-5, (what, float(np.max(np.abs(got - want))))
         self.n_scores_checked += 1
 
@@ -243,7 +254,7 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
     rng = np.random.default_rng(seed)
     counts = dict.fromkeys(OPS, 0)
     hits = {"unchanged_ok": 0, "failed_apply": 0, "decode_refused": 0, "stale_refused": 0, "spans": 0,
-            "captures": 0, "window_previews": 0}
+            "captures": 0, "window_previews": 0, "states_read": 0, "states_set": 0, "state_previews": 0}
     with make_engine(budget, reserve, tk, tv, canonical_layout=canonical, scorer=int(meank),
                      query_max_tokens=QWIN_CAP, query_last=QWIN_LAST, **(XF if xf else {})) as eng:
         if host_only:
@@ -279,6 +290,28 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
             return out
 
         window = []   # captured query rows, oldest first: [L][HQ][D] bf16 each
+        # the query state: rows captured since the last reset, a state set by set_query
+        # (sums, counts, rows captured before it) and the frozen flag
+        qs = {"captured": 0, "imported": None, "base": 0, "frozen": False}
+
+        def limit() -> int:
+            return QWIN_CAP if spans["kind"] is not None else QWIN_LAST
+
+        def expected_state():
+            """What get_query returns: the newest window rows summed in token order, or a
+            set state with the rows captured since added onto it; None with neither."""
+            if qs["imported"] is None:
+                n = min(len(window), limit())
+                if n == 0:
+                    return None
+                rows = torch.stack(window[-n:], dim=1).float().numpy().reshape(L, n, -1)
+                return oracle.q_accumulate(rows), [n] * L
+            sums, counts = qs["imported"]
+            n = min(qs["captured"] - qs["base"], limit(), len(window))
+            if n == 0:
+                return sums.copy(), list(counts)
+            rows = torch.stack(window[-n:], dim=1).float().numpy().reshape(L, n, -1)
+            return oracle.q_accumulate(rows, q_sum=sums), [c + n for c in counts]
 
         def contains(pos: int) -> bool:
             """query_contains; with no span every row is a query row."""
@@ -453,8 +486,9 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 m.check(what)
             elif op == "capture":
                 if rng.integers(0, 8) == 0:
-                    eng.reset_query()
+                    eng.reset_query()   # a frozen query stays frozen
                     window = []
+                    qs.update(captured=0, imported=None, base=0)
                 else:
                     n = int(rng.integers(1, 40))
                     pos0 = int(rng.integers(0, m.total + 1))
@@ -465,12 +499,23 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                         torch.cuda.synchronize()
                         eng.capture_q(layer, xd.data_ptr(), kv.TYPE_BF16, 2, D * 2, HQ * D * 2, positions)
                         ctx.sync()   # the view is freed after this
-                    window += [x[:, i] for i, p in enumerate(positions) if contains(p)]
-                    window = window[-QWIN_CAP:]
+                    if not qs["frozen"]:   # a frozen query keeps no rows
+                        kept_rows = [x[:, i] for i, p in enumerate(positions) if contains(p)]
+                        window = (window + kept_rows)[-QWIN_CAP:]
+                        qs["captured"] += len(kept_rows)
                 hits["captures"] += 1
                 m.check(what)
+            elif op == "wretrieve" and qs["imported"] is not None and meank:
+                # a set state (with rows captured since): the oracle's scores over it
+                sel = eng.preview_window()
+                m.check_meank_scores(None, what, state=expected_state())
+                kept(sel.blocks, [], what)
+                eng.apply(sel)
+                m.applied(sel.blocks)
+                hits["state_previews"] += 1
+                m.check(what, sel.blocks if canonical else None)
             elif op == "wretrieve":
-                n = min(len(window), QWIN_CAP if spans["kind"] is not None else QWIN_LAST)
+                n = min(len(window), limit())
                 if n == 0:   # an empty window is refused
                     with pytest.raises(kv.KvMemError):
                         eng.query_rows()
@@ -490,6 +535,38 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 m.applied(sel2.blocks)
                 hits["window_previews"] += 1
                 m.check(what, sel2.blocks if canonical else None)
+            elif op == "qstate":
+                r = int(rng.integers(0, 3))
+                want = expected_state()
+                if r == 0:   # get_query
+                    if want is None:
+                        with pytest.raises(kv.KvMemError):
+                            eng.get_query()
+                    else:
+                        got_sums, got_counts = eng.get_query()
+                        assert got_counts == want[1], (what, got_counts, want[1])
+                        assert np.array_equal(got_sums.view(np.uint32), want[0].view(np.uint32)), what
+                        hits["states_read"] += 1
+                elif r == 1:   # set_query: a state read back, or a random finite one
+                    if want is not None and rng.integers(0, 2) == 0:
+                        new_state = (want[0], want[1])
+                    else:
+                        c = int(rng.integers(1, 50))
+                        new_state = ((rng.standard_normal((L, HQ * D)) * c).astype(np.float32), [c] * L)
+                    if not meank:
+                        with pytest.raises(kv.KvMemError) as ex:
+                            eng.set_query(*new_state)
+                        assert ex.value.code == kv.ERR_UNSUPPORTED
+                    else:
+                        eng.set_query(*new_state)
+                        qs.update(imported=(np.array(new_state[0], np.float32), list(new_state[1])),
+                                  base=qs["captured"], frozen=True)
+                        hits["states_set"] += 1
+                else:   # freeze or unfreeze
+                    frozen = bool(rng.integers(0, 2))
+                    eng.freeze_query(frozen)
+                    qs["frozen"] = frozen
+                m.check(what)
             assert eng.retrieval_mandatory() == derived(), (what, spans, eng.retrieval_mandatory())
     announce(f"operations {counts}; {hits}; packed blocks checked {m.n_packed_checked}; "
              f"mean-K score sets checked {m.n_scores_checked}")

@@ -256,3 +256,43 @@ def test_query_state_get_set_freeze(oracle):
         t.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
         with pytest.raises(kv.KvMemError):
             t.set_query(sums, counts)                       # the per-token scorer reads rows
+
+
+def test_set_query_then_unfrozen_rows_add_on(oracle):
+    """After set_query, rows captured once the query is unfrozen add onto the
+    set state, as the reference's harvest adds each row onto q_sum_ and
+    q_count_ after set_query (llama-memory-kvmem.cpp:2164-2172, 3121-3137):
+    the sums are the set ones plus the new rows in token order, the counts
+    the set ones plus the rows; rows captured while frozen, or before the
+    state was set, do not count; a window preview scores from that state."""
+    announce("set state, capture frozen (kept nothing), unfreeze, capture: rows add onto the state")
+    cap, nb = 40, 40
+    k, v, _ = workloads.scoring_tensors(torch, "cuda", L=L, B=cap, Tq=1, seed=85, with_v=True)
+    cp = Capture("bf16", 86)
+    rng = np.random.default_rng(87)
+    with engine(scorer=1) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, nb * T)
+        eng.set_turn_spans(query=[(0, 200)], mandatory=[])
+        cp.ubatch(eng, 0, 12)                           # before the state: replaced by it
+        state = (rng.standard_normal((L, EQ)) * 7).astype(np.float32)
+        eng.set_query(state, [7] * L)
+        cp.ubatch(eng, 12, 5)                           # frozen: kept nothing
+        got, counts = eng.get_query()
+        assert counts == [7] * L and np.array_equal(got.view(np.uint32), state.view(np.uint32))
+        eng.freeze_query(False)
+        cp.ubatch(eng, 17, 6)                           # added onto the state
+        got, counts = eng.get_query()
+        want = oracle.q_accumulate(cp.rows(range(17, 23)).reshape(L, 6, EQ), q_sum=state)
+        assert counts == [13] * L
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        sel = eng.preview_window()
+        scores = np.array(eng.scores(), dtype=np.float64)
+        kb = workloads.to_bits(torch, k)
+        sums = np.stack([[oracle.meank_sum_f16(kb[l, b].reshape(T, E)) for b in range(nb)]
+                         for l in range(L)])
+        want_s = oracle.score_meank(want, [13] * L, sums, np.full((L, nb), T, np.uint32), HQ, HKV, D)
+        assert np.max(np.abs(scores - want_s)) <= 1e-5
+        assert sel.blocks == oracle.pick_topk(scores.astype(np.float32).astype(np.float64), 8, sink=1)
+        eng.reset_query()                               # the state and the rows go
+        with pytest.raises(kv.KvMemError):
+            eng.get_query()
