@@ -10,7 +10,10 @@ seeded random order:
 
 - a retrieval step through the device plan (apply_retrieval), whose
   resident set must be the preview of the same query and mandatory blocks;
-- preview + apply;
+- preview + apply, and apply of a caller's own selection (any order,
+  repeated ids, ids past the history; more blocks than slots is refused
+  with nothing changed, as the reference's set_selection sorts, de-duplicates
+  and drops out-of-range ids, kvmem_store.cpp:758-770);
 - a preview made stale by rows appended or cut before its apply;
 - rows appended to the history only (append_tokens);
 - rows decoded resident (append_resident, then the caller writes the pool
@@ -70,7 +73,7 @@ torch = pytest.importorskip("torch")
 from conftest import load_pkg  # noqa: E402
 
 kv = load_pkg()
-from kvmem_amd import workloads  # noqa: E402
+from kvmem_amd import host, workloads  # noqa: E402
 
 from engine_helpers import D, E, HQ, L, T, block_major_pinned, decode_rows, history, make_engine  # noqa: E402
 from test_gpu_transform import expected_rows  # noqa: E402
@@ -90,8 +93,8 @@ CASES = [
 MEANK_CASE = (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 106, False, False)
 XF = dict(n_rot=256, rope_freq_base=1e6, attn_rot=1)
 OPS = ["retrieve", "preview_apply", "stale", "append", "decode", "truncate", "fail", "unchanged", "span",
-       "capture", "wretrieve", "qstate"]
-WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2, 1, 2, 2, 1], dtype=float)
+       "capture", "wretrieve", "qstate", "apply_ids"]
+WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2, 1, 2, 2, 1, 1], dtype=float)
 QWIN_CAP, QWIN_LAST = 48, 16   # query_max_tokens, query_last
 # KVMEM_SEQ_OPS / KVMEM_SEQ_SEED_OFFSET lengthen a run or draw other seeds
 N_OPS = int(os.environ.get("KVMEM_SEQ_OPS", "150"))
@@ -254,7 +257,8 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
     rng = np.random.default_rng(seed)
     counts = dict.fromkeys(OPS, 0)
     hits = {"unchanged_ok": 0, "failed_apply": 0, "decode_refused": 0, "stale_refused": 0, "spans": 0,
-            "captures": 0, "window_previews": 0, "states_read": 0, "states_set": 0, "state_previews": 0}
+            "captures": 0, "window_previews": 0, "states_read": 0, "states_set": 0, "state_previews": 0,
+            "caller_selections": 0}
     with make_engine(budget, reserve, tk, tv, canonical_layout=canonical, scorer=int(meank),
                      query_max_tokens=QWIN_CAP, query_last=QWIN_LAST, **(XF if xf else {})) as eng:
         if host_only:
@@ -535,6 +539,25 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 m.applied(sel2.blocks)
                 hits["window_previews"] += 1
                 m.check(what, sel2.blocks if canonical else None)
+            elif op == "apply_ids":
+                # a caller's own selection: any order, repeats, ids past the history, at times
+                # more blocks than slots (refused, nothing changes), at times none
+                nb = eng.block_count()
+                ids = [int(x) for x in rng.integers(0, nb + 3, int(rng.integers(0, eng.n_slots() + 4)))]
+                uniq = sorted({i for i in ids if i < nb})
+                before = dict(m.valid)
+                if len(uniq) > eng.n_slots():
+                    with pytest.raises(kv.KvMemError) as ex:
+                        eng.apply(host.Selection(eng.epoch(), m.total, ids))
+                    assert ex.value.code == kv.ERR_INVALID, what
+                    assert m.valid == before
+                    m.check(what + " (refused)")
+                else:
+                    eng.apply(host.Selection(eng.epoch(), m.total, ids))
+                    assert sorted(m.resident()) == uniq, (what, sorted(m.resident()), uniq)
+                    m.applied(uniq)
+                    m.check(what, uniq if canonical else None)
+                hits["caller_selections"] += 1
             elif op == "qstate":
                 r = int(rng.integers(0, 3))
                 want = expected_state()
