@@ -19,6 +19,8 @@ seeded random order:
 - rows decoded resident (append_resident, then the caller writes the pool
   cells of the blocks they touch, whole blocks from the history);
 - a truncation;
+- a swap to other history buffers of the same shape (set_device_history):
+  every block leaves the pool, and the key sums and saved rows go with it;
 - an apply whose n-th device operation is refused on the host
   (kvmem_hip_debug_fail_after: nothing faults);
 - commit_unchanged after a preview with the last apply's query and
@@ -93,8 +95,8 @@ CASES = [
 MEANK_CASE = (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 106, False, False)
 XF = dict(n_rot=256, rope_freq_base=1e6, attn_rot=1)
 OPS = ["retrieve", "preview_apply", "stale", "append", "decode", "truncate", "fail", "unchanged", "span",
-       "capture", "wretrieve", "qstate", "apply_ids"]
-WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2, 1, 2, 2, 1, 1], dtype=float)
+       "capture", "wretrieve", "qstate", "apply_ids", "swap"]
+WEIGHTS = np.array([4, 3, 1, 2, 2, 1, 1, 2, 1, 2, 2, 1, 1, 0.5], dtype=float)
 QWIN_CAP, QWIN_LAST = 48, 16   # query_max_tokens, query_last
 # KVMEM_SEQ_OPS / KVMEM_SEQ_SEED_OFFSET lengthen a run or draw other seeds
 N_OPS = int(os.environ.get("KVMEM_SEQ_OPS", "150"))
@@ -112,6 +114,7 @@ class Model:
         self.eng, self.oracle, self.types, self.store = eng, oracle, types, store
         self.theta = oracle.rope_theta(XF["n_rot"], XF["rope_freq_base"]) if xf else None
         self.bits = (workloads.to_bits(torch, k), workloads.to_bits(torch, v))
+        self.hist = 0   # which history the engine reads (its rows key the cache)
         self.total = eng.total_tokens()
         self.valid: dict[int, int] = {}
         self.cache: dict[tuple, np.ndarray] = {}
@@ -127,8 +130,12 @@ class Model:
     def applied(self, sel: list[int]) -> None:
         self.valid = {b: self.ntok(b) for b in sel}
 
+    def use_history(self, hist: int, k, v) -> None:
+        self.hist = hist
+        self.bits = (workloads.to_bits(torch, k), workloads.to_bits(torch, v))
+
     def want(self, layer: int, which: int, b: int, n: int) -> np.ndarray:
-        key = (layer, which, b, n)
+        key = (self.hist, layer, which, b, n)
         if key not in self.cache:
             rows = self.bits[which][layer, b].reshape(T, E)[:n]
             if self.theta is None:
@@ -162,7 +169,7 @@ class Model:
         for b in range(nb):
             n = self.ntok(b)
             for layer in range(L):
-                k2 = ("sum", layer, b, n)
+                k2 = ("sum", self.hist, layer, b, n)
                 if k2 not in self.cache:
                     self.cache[k2] = self.oracle.meank_sum_f16(self.bits[0][layer, b].reshape(T, E)[:n])
                 sums[layer, b] = self.cache[k2]
@@ -246,6 +253,8 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
              f"{kv.TYPE_NAMES[tv]}, seed {seed}, pinned host history and packed store: {pinned}, "
              f"row transform: {xf}, mean-K scorer: {meank}, host-only history: {host_only}")
     k, v, q = history(cap, seed=seed)
+    k2, v2, _ = history(cap, seed=seed + 500)   # another history of the same shape
+    hists = [(k, v), (k2, v2)]
     hb = store = None
     if pinned:
         hb = block_major_pinned(k, v, cap)
@@ -258,7 +267,7 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
     counts = dict.fromkeys(OPS, 0)
     hits = {"unchanged_ok": 0, "failed_apply": 0, "decode_refused": 0, "stale_refused": 0, "spans": 0,
             "captures": 0, "window_previews": 0, "states_read": 0, "states_set": 0, "state_previews": 0,
-            "caller_selections": 0}
+            "caller_selections": 0, "swaps": 0}
     with make_engine(budget, reserve, tk, tv, canonical_layout=canonical, scorer=int(meank),
                      query_max_tokens=QWIN_CAP, query_last=QWIN_LAST, **(XF if xf else {})) as eng:
         if host_only:
@@ -407,7 +416,7 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                     continue
                 t0 = m.total
                 try:
-                    decode_rows(eng, k, v, t0, t0 + n)
+                    decode_rows(eng, *hists[m.hist], t0, t0 + n)
                 except kv.KvMemError as ex:
                     # no free slot, or another grown tail waits: nothing changed, and the
                     # caller appends the rows to the history instead
@@ -539,6 +548,17 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 m.applied(sel2.blocks)
                 hits["window_previews"] += 1
                 m.check(what, sel2.blocks if canonical else None)
+            elif op == "swap":
+                if pinned or host_only:   # their stage-in reads the pinned copy of the first history
+                    continue
+                # other buffers: a new history, so residency, key sums and saved rows go
+                cur = 1 - m.hist
+                kk, vv = hists[cur]
+                eng.set_device_history(kk.data_ptr(), vv.data_ptr(), cap, m.total)
+                m.use_history(cur, kk, vv)
+                m.valid = {}
+                hits["swaps"] += 1
+                m.check(what)
             elif op == "apply_ids":
                 # a caller's own selection: any order, repeats, ids past the history, at times
                 # more blocks than slots (refused, nothing changes), at times none
