@@ -90,6 +90,7 @@ CASES = [
     (1, kv.TYPE_Q5_0, kv.TYPE_Q8_0, 103, False, False),
     (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 104, True, False),
     (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 105, False, True),
+    (1, kv.TYPE_Q5_0, kv.TYPE_Q8_0, 108, True, True),
 ]
 # the reference's mean-K cosine scorer over key sums the engine keeps current
 MEANK_CASE = (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 106, False, False)
@@ -225,7 +226,8 @@ class Model:
 
 
 @pytest.mark.parametrize("case", CASES, ids=["canonical_q8", "lifo_q8_q4", "canonical_q5_q8",
-                                             "pinned_packed_q8_q4", "rope_hadamard_q8_q4"])
+                                             "pinned_packed_q8_q4", "rope_hadamard_q8_q4",
+                                             "rope_hadamard_pinned_packed_q5_q8"])
 def test_random_operation_sequences(oracle, case):
     run_sequence(oracle, case, meank=False)
 
