@@ -6,6 +6,8 @@
   A member the mirror names that the header lacks fails the compile.
 - Every C++ block of INTEGRATION.md (the calls an adapter would make)
   compiles against the headers, and links against libkvmem_hip.so.
+- The integration driver (tests/integration_driver), which runs those
+  blocks on the GPU against the oracle, builds from them.
 """
 from __future__ import annotations
 
@@ -92,3 +94,15 @@ def test_integration_snippets_compile_and_link(tmp_path):
                         "-Wl,--no-undefined", "-L/opt/rocm/lib", "-lamdhip64"],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not installed")
+def test_integration_driver_builds(tmp_path):
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("integration_driver_build",
+                                                  ROOT / "tests" / "integration_driver" / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    assert len(mod.blocks()) == len(snippets())
+    exe = mod.build(tmp_path / "gen", tmp_path / "bin" / "integration_driver")
+    assert exe.exists()
