@@ -402,7 +402,13 @@ KVMEM_HIP_API int kvmem_hip_score(kvmem_hip_ctx *ctx,
  * finished returns KVMEM_HIP_ERR_BUSY with nothing issued (the caller
  * synchronises, or uses kvmem_hip_score).  The array's last
  * user is tracked on the host: two processes on one GPU each have their
- * own array.  Not timed by kvmem_hip_perf_*. */
+ * own array.  A call on a stream under HIP graph capture issues only two
+ * kernel launches (no allocation, copy, memset or synchronisation), so it
+ * can be captured; the capturing context becomes the array's owner, but
+ * the replays run outside the library's view: the caller orders them with
+ * its own calls and keeps other contexts' calls on this GPU from
+ * overlapping them (such calls are not refused).  Not timed by
+ * kvmem_hip_perf_*. */
 KVMEM_HIP_API int kvmem_hip_score_noalloc(kvmem_hip_ctx *ctx,
                                           const kvmem_hip_history *hist,
                                           const kvmem_hip_score_args *args);

@@ -666,6 +666,15 @@ extern "C" int kvmem_hip_score_noalloc(kvmem_hip_ctx *ctx, const kvmem_hip_histo
                         std::to_string(kNoAllocScratchBytes) + " (use kvmem_hip_score)");
     }
     (void) hipSetDevice(ctx->device);
+    // Under graph capture the launches become graph nodes and the call's
+    // completion cannot be tracked: its replays run when the caller launches
+    // them.  An event recorded in a capture cannot be queried afterwards,
+    // so none is recorded and the capturing context stays the owner.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (!hip_ok(ctx, hipStreamIsCapturing(ctx->stream, &capture), "score_noalloc capture status")) {
+        return KVMEM_HIP_ERR_RUNTIME;
+    }
+    const bool capturing = capture != hipStreamCaptureStatusNone;
     // Take the device's array: free when no call is recorded, when the last
     // one came from this context on this stream (queued behind it), or when
     // the last call's completion event has fired.
@@ -688,9 +697,17 @@ extern "C" int kvmem_hip_score_noalloc(kvmem_hip_ctx *ctx, const kvmem_hip_histo
     st = score_launch(ctx, args, p, grid, layers, false);
     if (st != KVMEM_HIP_OK) {
         // a launch that failed after the scorer kernel was queued leaves that
-        // kernel on the array with no owner record: let it drain first
-        (void) hipStreamSynchronize(ctx->stream);
+        // kernel on the array with no owner record: let it drain first (a
+        // capture holds nothing that runs)
+        if (!capturing) {
+            (void) hipStreamSynchronize(ctx->stream);
+        }
         return st;
+    }
+    if (capturing) {
+        own.ctx = ctx;
+        own.stream = ctx->stream;
+        return KVMEM_HIP_OK;
     }
     if (!hip_ok(ctx, hipEventRecord(ctx->noalloc_done, ctx->stream), "score_noalloc completion event")) {
         own = ScratchOwner{};  // nothing tells when the launched work ends: no owner to wait for

@@ -9,7 +9,8 @@ same inputs, with no allocation by the context in between.  A call that
 needs more scratch than the array holds is refused before any work.  Two
 contexts on one GPU share the array in turn; a call from the second while
 the first one's call is still queued is refused with KVMEM_HIP_ERR_BUSY
-and writes nothing.
+and writes nothing.  A call captured into a HIP graph replays with the
+scorer's results for whatever query its buffer holds at each replay.
 """
 from __future__ import annotations
 
@@ -142,3 +143,56 @@ def test_score_noalloc_two_contexts_share_then_refuse_overlap():
         b.score_noalloc(hb, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, got_b.data_ptr())
         b.sync()
         assert np.array_equal(got_b.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_score_noalloc_under_graph_capture():
+    """One call captured into a HIP graph on the context's stream
+    (torch.cuda.graph in global capture mode, where an allocation or a
+    synchronisation fails the capture), then replayed four times, a new
+    query copied into the captured query buffer and the output cleared
+    before each replay, eager work and synchronisations in between: every
+    replay equals kvmem_hip_score on that query, bit for bit, and the
+    context allocates nothing while capturing or replaying."""
+    L, B, Tq, last_T = 4, 512, 16, 50
+    announce(f"graph capture: L={L} B={B} Tq={Tq} last_T={last_T}")
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=Tq, seed=11)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(12)
+    queries = [torch.randn(q.shape, generator=g, device="cuda").to(q.dtype) for _ in range(4)]
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with kv.Context(0) as ctx:
+        ctx.set_stream(stream.cuda_stream)
+        hist = ctx.make_history(k.data_ptr(), None, L, B, T, E, 0, last_T)
+        out = torch.full((B,), float("nan"), dtype=torch.float32, device="cuda")
+        want = torch.empty(B, dtype=torch.float32, device="cuda")
+        ctx.score(hist, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, want.data_ptr())
+        ctx.score_noalloc(hist, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, out.data_ptr())
+        ctx.sync()
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want.cpu().numpy().view(np.uint32))
+        before = ctx.scratch_info()["allocations"]
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            ctx.score_noalloc(hist, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, out.data_ptr())
+        torch.cuda.synchronize()
+        for i, qi in enumerate(queries):
+            q.copy_(qi)
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            got = out.cpu().numpy()
+            assert ctx.scratch_info()["allocations"] == before
+            ctx.score(hist, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, want.data_ptr())
+            ctx.sync()
+            w = want.cpu().numpy()
+            assert np.isfinite(w).all()
+            assert np.array_equal(got.view(np.uint32), w.view(np.uint32)), f"replay {i}"
+        # eager calls from the capturing context go on as before
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        ctx.score_noalloc(hist, q.data_ptr(), kv.TYPE_BF16, Tq, HQ, HKV, D, out.data_ptr())
+        ctx.sync()
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want.cpu().numpy().view(np.uint32))
+        del graph
+        ctx.set_stream(None)
