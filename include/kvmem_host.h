@@ -279,7 +279,8 @@ KVMEM_HIP_API kvmem_engine_params kvmem_engine_default_params(void);
 
 /* Create the engine: its kvmem_hip_ctx, the slot pool of
  * (budget + reserve) slots per layer for K and V (kv_size = budget +
- * gen_reserve blocks, llama-memory-kvmem.cpp:363-426) and the store. */
+ * gen_reserve blocks, llama-memory-kvmem.cpp:363-426), cleared to zero as
+ * llama.cpp clears its KV cache buffers, and the store. */
 KVMEM_HIP_API int kvmem_engine_create(const kvmem_engine_params *p, kvmem_engine **out);
 KVMEM_HIP_API void kvmem_engine_destroy(kvmem_engine *e);
 KVMEM_HIP_API const char *kvmem_engine_last_error(const kvmem_engine *e);
@@ -336,7 +337,7 @@ KVMEM_HIP_API uint64_t kvmem_engine_epoch(const kvmem_engine *e);
  * The engine's own pool is released.  The caller keeps the tensors alive
  * while the engine uses them; the working set is cleared (every block is
  * staged again by the next apply).  NULL k_layers returns to an engine-owned
- * pool. */
+ * pool, cleared to zero. */
 KVMEM_HIP_API int kvmem_engine_set_pool(kvmem_engine *e, void *const *k_layers,
                                         void *const *v_layers);
 /* Pool slots and per-layer device pool tensors. */

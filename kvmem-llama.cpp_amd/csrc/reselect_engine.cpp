@@ -946,13 +946,20 @@ static bool alloc_own_pool(kvmem_engine *e) {
     e->pool_k.assign(e->p.n_layers, nullptr);
     e->pool_v.assign(e->p.n_layers, nullptr);
     e->own_pool = true;
+    // Cleared, as llama.cpp clears its KV cache buffers: attention reads
+    // every cell of the pool under a mask, and a cell no stage-in or decode
+    // has written (a free slot, the rows past a partial tail) must not hold
+    // NaN bits.
+    hipStream_t s = static_cast<hipStream_t>(kvmem_hip_get_stream(e->ctx));
     for (uint32_t l = 0; l < e->p.n_layers; ++l) {
         if (hipMalloc(&e->pool_k[l], kbytes) != hipSuccess ||
-            hipMalloc(&e->pool_v[l], vbytes) != hipSuccess) {
+            hipMalloc(&e->pool_v[l], vbytes) != hipSuccess ||
+            hipMemsetAsync(e->pool_k[l], 0, kbytes, s) != hipSuccess ||
+            hipMemsetAsync(e->pool_v[l], 0, vbytes, s) != hipSuccess) {
             return false;
         }
     }
-    return true;
+    return kvmem_hip_sync(e->ctx) == KVMEM_HIP_OK;
 }
 
 int kvmem_engine_set_pool(kvmem_engine *e, void *const *k_layers, void *const *v_layers) {

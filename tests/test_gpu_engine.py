@@ -197,3 +197,36 @@ def test_engine_request_and_turn_spans(oracle):
             check_pool(eng, oracle, k, v, sel.blocks, kv.TYPE_Q8_0, kv.TYPE_Q8_0)
         with pytest.raises(kv.KvMemError):
             eng.set_turn_spans(query=[(5, 4)])
+
+
+def test_engine_own_pool_starts_cleared():
+    """The engine's own pool is zero before any stage-in, as llama.cpp
+    clears its KV cache buffers: cells that no stage-in or decode has
+    written (free slots, rows past a partial tail) hold no NaN bits for the
+    attention that reads them under a mask.  The same after set_pool(NULL)
+    replaces a borrowed pool with a new own one."""
+    announce("own pool cleared at creation and after set_pool(NULL)")
+    with make_engine(6, 2, kv.TYPE_Q8_0, kv.TYPE_Q4_0) as eng:
+        ctx = kv.Context(0)
+        try:
+            def all_zero() -> bool:
+                for layer in range(L):
+                    for ptr, ty in zip(eng.pool_layer(layer), (kv.TYPE_Q8_0, kv.TYPE_Q4_0)):
+                        n = eng.n_slots() * T * kv.row_size(ty, E)
+                        buf = torch.full((n,), 0xA5, dtype=torch.uint8, device="cuda")
+                        torch.cuda.synchronize()
+                        ctx.d2d_batched([ptr], [buf.data_ptr()], [n])
+                        ctx.sync()
+                        if bool(buf.any()):
+                            return False
+                return True
+
+            assert all_zero()
+            n = eng.n_slots() * T * kv.row_size(kv.TYPE_Q8_0, E)
+            borrowed = [torch.full((n,), 0x7F, dtype=torch.uint8, device="cuda") for _ in range(2 * L)]
+            torch.cuda.synchronize()
+            eng.set_pool([t.data_ptr() for t in borrowed[:L]], [t.data_ptr() for t in borrowed[L:]])
+            eng.set_pool(None)
+            assert all_zero()
+        finally:
+            ctx.close()
