@@ -233,6 +233,8 @@ def load_library(path: os.PathLike | str | None = None) -> C.CDLL:
     _sig(lib, "kvmem_hip_perf_reset", None, vp)
     _sig(lib, "kvmem_hip_q_window_write", i32, vp, vp, i32, C.c_uint32, C.c_uint32, C.c_size_t, C.c_size_t,
          C.c_size_t, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.c_uint32, vp, C.c_uint32)
+    _sig(lib, "kvmem_hip_q_window_gather", i32, vp, vp, C.c_uint32, C.c_uint32, C.c_uint32,
+         C.POINTER(C.c_uint32), C.c_uint32, i32, vp)
     _sig(lib, "kvmem_hip_transfer_get", i32, vp, C.POINTER(TransferStats))
     if path is None:
         _lib = lib
@@ -522,6 +524,13 @@ class Context:
         assert n == m
         self.check(self.lib.kvmem_hip_q_window_write(self.h, q_ptr, q_type, n_head, head_dim, nb0, nb1, nb2,
                                                      t, r, n, window_ptr, capacity), "q_window_write")
+
+    def q_window_gather(self, window_ptr: int, n_layers: int, capacity: int, n_embd_q: int, rows,
+                        out_type: int, out_ptr: int) -> None:
+        """out[l][i] = window[l][rows[i]] for every layer, converted to out_type."""
+        r, n = _u32_array(rows)
+        self.check(self.lib.kvmem_hip_q_window_gather(self.h, window_ptr, n_layers, capacity, n_embd_q, r, n,
+                                                      out_type, out_ptr), "q_window_gather")
 
     def transfers(self) -> dict:
         """Bytes and calls per direction since the last perf_reset."""

@@ -355,6 +355,10 @@ int kvmem_hip_meank_sums(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
         return fail(ctx, KVMEM_HIP_ERR_INVALID,
                     "meank_sums: n_embd_k must be a multiple of 8 and at most 2048, 16-byte aligned");
     }
+    if (hist->last_block_tokens > hist->block_tokens) {
+        // the kernel sums the last block's rows up to this count
+        return fail(ctx, KVMEM_HIP_ERR_INVALID, "meank_sums: last_block_tokens above block_tokens");
+    }
     for (uint32_t i = 0; i < n; ++i) {
         if (block_ids[i] >= hist->n_blocks) {
             return fail(ctx, KVMEM_HIP_ERR_INVALID, "meank_sums: block id out of range");

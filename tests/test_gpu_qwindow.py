@@ -187,6 +187,60 @@ def test_window_write_checks_rows_against_capacity():
     assert bool((win[1:5] == -7.0).all())
 
 
+def bf16_rne_bits(x: np.ndarray) -> np.ndarray:
+    """f32 -> bf16 bits, round to nearest even (finite inputs)."""
+    u = x.view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def test_window_gather_converts_round_to_nearest_even():
+    """kvmem_hip_q_window_gather: out[l][i] = window[l][rows[i]] for every
+    layer, rows in any order and repeated, copied as f32 or rounded to f16
+    or bf16 to nearest even -- halfway cases, f16 subnormals and f16
+    overflow included (numpy's conversions are the reference); a row at or
+    past the capacity, or an output type other than F32 / F16 / BF16, is
+    refused with nothing written."""
+    announce("q_window_gather: row order, repeats, f32 / f16 / bf16 rounding")
+    cap, n_layers = 9, 2
+    rng = np.random.default_rng(17)
+    win = (rng.standard_normal((n_layers, cap, EQ)) * 3.0).astype(np.float32)
+    special = np.array([1 + 2**-11, 1 + 3 * 2**-11, -(1 + 2**-11), 1.5 * 2**-24, 2**-25, 3 * 2**-26,
+                        65504.0, 65519.0, 65520.0, -70000.0, 1 + 2**-8, 1 + 3 * 2**-8, -(1 + 3 * 2**-8),
+                        3.0e38, 1e-40, 0.0, -0.0], dtype=np.float32)
+    win[:, :, :special.size] = special
+    win[1, 2, -special.size:] = special[::-1]
+    rows = [4, 0, 8, 4, 2]
+    wd = torch.from_numpy(win).to("cuda")
+    want32 = win[:, rows]
+    with np.errstate(over="ignore"):
+        want16 = want32.astype(np.float16).view(np.uint16)
+    wantbf = bf16_rne_bits(want32)
+    with kv.Context(0) as ctx:
+        for name, (tdt, ty) in DTYPES.items():
+            out = torch.full((n_layers, len(rows), EQ), 7, dtype=tdt, device="cuda")
+            torch.cuda.synchronize()
+            ctx.q_window_gather(wd.data_ptr(), n_layers, cap, EQ, rows, ty, out.data_ptr())
+            ctx.sync()
+            if name == "f32":
+                got = out.cpu().numpy().view(np.uint32)
+                assert np.array_equal(got, want32.view(np.uint32)), name
+            else:
+                got = out.cpu().view(torch.int16).numpy().view(np.uint16)
+                want = want16 if name == "f16" else wantbf
+                bad = np.flatnonzero(got.ravel() != want.ravel())
+                assert bad.size == 0, f"{name}: {bad.size} differ, first at {bad[:4]}: " \
+                                      f"{want32.ravel()[bad[:4]]} -> {got.ravel()[bad[:4]]} not {want.ravel()[bad[:4]]}"
+        out = torch.full((n_layers, 2, EQ), -3.0, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        for rows_bad, ty, code in (([0, cap], kv.TYPE_F32, kv.ERR_INVALID),
+                                   ([0, 1], kv.TYPE_Q8_0, kv.ERR_UNSUPPORTED)):
+            with pytest.raises(kv.KvMemError) as ex:
+                ctx.q_window_gather(wd.data_ptr(), n_layers, cap, EQ, rows_bad, ty, out.data_ptr())
+            assert ex.value.code == code, str(ex.value)
+        ctx.sync()
+        assert bool((out == -3.0).all())
+
+
 def test_misaligned_device_history_is_refused():
     """Every reader of the device history (scorer, key sums, stage-in)
     loads 16-byte words: set_device_history refuses a misaligned K or V
