@@ -169,6 +169,18 @@ static void span_close(kvmem_hip_ctx *ctx) {
     ctx->span_set_end = nullptr;
 }
 
+// A stage's timed pair, its end also closing or extending the open
+// scorer-to-stage-in span.
+static void perf_file(kvmem_hip_ctx *ctx, PerfStage s, hipEvent_t start, hipEvent_t end) {
+    ctx->perf_done[s].emplace_back(start, end);
+    if (s == kPerfScore) {
+        span_close(ctx);
+        ctx->span_score_end = end;
+    } else if (s == kPerfSet && ctx->span_score_end) {
+        ctx->span_set_end = end;
+    }
+}
+
 void perf_end(kvmem_hip_ctx *ctx, PerfStage s) {
     hipEvent_t start = ctx->perf_open[s];
     if (!start) {
@@ -177,19 +189,49 @@ void perf_end(kvmem_hip_ctx *ctx, PerfStage s) {
     ctx->perf_open[s] = nullptr;
     hipEvent_t end = perf_event(ctx);
     if (end && hipEventRecord(end, ctx->stream) == hipSuccess) {
-        ctx->perf_done[s].emplace_back(start, end);
-        if (s == kPerfScore) {
-            span_close(ctx);
-            ctx->span_score_end = end;
-        } else if (s == kPerfSet && ctx->span_score_end) {
-            ctx->span_set_end = end;
-        }
+        perf_file(ctx, s, start, end);
         return;
     }
     ctx->perf_free.push_back(start);
     if (end) {
         ctx->perf_free.push_back(end);
     }
+}
+
+bool perf_attach(kvmem_hip_ctx *ctx, PerfStage s) {
+    if (!ctx->perf_on || !(ctx->perf_mask & (1u << s)) || ctx->perf_open[s] || ctx->attach_start) {
+        return false;  // off, not timed, inside this stage, or a pair already waits
+    }
+    hipEvent_t start = perf_event(ctx);
+    hipEvent_t end = start ? perf_event(ctx) : nullptr;
+    if (!end) {
+        if (start) {
+            ctx->perf_free.push_back(start);
+        }
+        return false;
+    }
+    ctx->attach_start = start;
+    ctx->attach_stop = end;
+    ctx->attach_armed = true;
+    return true;
+}
+
+void perf_detach(kvmem_hip_ctx *ctx, PerfStage s, bool ok) {
+    hipEvent_t start = ctx->attach_start;
+    hipEvent_t end = ctx->attach_stop;
+    const bool launched = !ctx->attach_armed;
+    ctx->attach_start = nullptr;
+    ctx->attach_stop = nullptr;
+    ctx->attach_armed = false;
+    if (!start) {
+        return;
+    }
+    if (ok && launched) {
+        perf_file(ctx, s, start, end);
+        return;
+    }
+    ctx->perf_free.push_back(start);
+    ctx->perf_free.push_back(end);
 }
 
 void perf_collect(kvmem_hip_ctx *ctx) {
@@ -473,6 +515,8 @@ void kvmem_hip_destroy(kvmem_hip_ctx *ctx) {
     for (hipEvent_t e : ctx->perf_free) {
         (void) hipEventDestroy(e);
     }
+    if (ctx->attach_start) (void) hipEventDestroy(ctx->attach_start);
+    if (ctx->attach_stop) (void) hipEventDestroy(ctx->attach_stop);
     score_scratch_release(ctx);
     if (ctx->noalloc_done) (void) hipEventDestroy(ctx->noalloc_done);
     if (ctx->own_stream) (void) hipStreamDestroy(ctx->own_stream);

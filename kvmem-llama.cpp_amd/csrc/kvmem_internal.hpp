@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <algorithm>
 #include <cstddef>
@@ -107,6 +108,10 @@ struct kvmem_hip_ctx {
     uint32_t perf_mask = 0xffffffffu;  // stages timed while perf_on (bit = PerfStage)
     std::vector<hipEvent_t> perf_free;                       // reusable events
     hipEvent_t perf_open[kvmem_hip::kPerfStages] = {};       // started, not ended
+    // a stage's event pair handed to the next kernel launch (perf_attach):
+    // the runtime stamps them with that kernel's own start and end
+    hipEvent_t attach_start = nullptr, attach_stop = nullptr;
+    bool attach_armed = false;  // not yet taken by a launch
     std::vector<std::pair<hipEvent_t, hipEvent_t>> perf_done[kvmem_hip::kPerfStages];
     double perf_ms[kvmem_hip::kPerfStages] = {};
     uint64_t perf_n[kvmem_hip::kPerfStages] = {};
@@ -281,6 +286,28 @@ void perf_begin(kvmem_hip_ctx *ctx, PerfStage s);
 void perf_end(kvmem_hip_ctx *ctx, PerfStage s);
 // Forget a started stage without timing it (the call failed).
 void perf_drop(kvmem_hip_ctx *ctx, PerfStage s);
+// A timed stage of exactly one kernel launch: perf_attach hands a start and
+// an end event to the next ctx_launch, which passes them to the runtime with
+// the kernel, so they carry the kernel's own start and end times -- no
+// marker packets around it, which hold the stream idle a few microseconds
+// each.  perf_detach files the pair as the stage's when the launch took it
+// (`ok`), else returns it.  Returns false when the stage is not timed.
+bool perf_attach(kvmem_hip_ctx *ctx, PerfStage s);
+void perf_detach(kvmem_hip_ctx *ctx, PerfStage s, bool ok);
+
+// A kernel launch on the context stream, carrying the events perf_attach
+// left for it, if any.
+template <typename... Params, typename... Args>
+inline void ctx_launch(kvmem_hip_ctx *ctx, void (*kernel)(Params...), dim3 grid, dim3 block, uint32_t shmem,
+                       const Args &...args) {
+    if (ctx->attach_armed) {
+        ctx->attach_armed = false;  // one launch per attachment; perf_detach files the pair
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, ctx->stream, ctx->attach_start, ctx->attach_stop, 0u,
+                              static_cast<Params>(args)...);
+    } else {
+        kernel<<<grid, block, shmem, ctx->stream>>>(args...);
+    }
+}
 
 // A timed stage over a scope: started on construction, ended by ok() once
 // the work is enqueued, dropped on destruction otherwise, so that no
@@ -306,6 +333,32 @@ private:
     kvmem_hip_ctx *ctx_;
     PerfStage s_;
     bool done_ = false;
+};
+
+// A timed stage of one kernel launch over a scope, with the events carried
+// by the launch (perf_attach): filed by ok() once the kernel is enqueued,
+// returned on destruction otherwise.
+class PerfLaunchScope {
+public:
+    PerfLaunchScope(kvmem_hip_ctx *ctx, PerfStage s) : ctx_(ctx), s_(s), on_(perf_attach(ctx, s)) {}
+    ~PerfLaunchScope() {
+        if (on_) {
+            perf_detach(ctx_, s_, false);
+        }
+    }
+    void ok() {
+        if (on_) {
+            perf_detach(ctx_, s_, true);
+            on_ = false;
+        }
+    }
+    PerfLaunchScope(const PerfLaunchScope &) = delete;
+    PerfLaunchScope &operator=(const PerfLaunchScope &) = delete;
+
+private:
+    kvmem_hip_ctx *ctx_;
+    PerfStage s_;
+    bool on_;
 };
 
 // Count `bytes` moved in direction k by `calls` copy operations.

@@ -532,17 +532,18 @@ int score_launch(kvmem_hip_ctx *ctx, const kvmem_hip_score_args *args, const Sco
         return KVMEM_HIP_ERR_RUNTIME;
     }
     if (timed) {
-        perf_begin(ctx, kPerfScore);
+        (void) perf_attach(ctx, kPerfScore);  // the scorer's events ride on its launch
     }
     if (args->head_dim == 256) {
-        score_kernel<256><<<static_cast<uint32_t>(grid), kScoreThreads, 0, ctx->stream>>>(p);
+        ctx_launch(ctx, score_kernel<256>, dim3(static_cast<uint32_t>(grid)), dim3(kScoreThreads), 0, p);
     } else {
-        score_kernel<128><<<static_cast<uint32_t>(grid), kScoreThreads, 0, ctx->stream>>>(p);
+        ctx_launch(ctx, score_kernel<128>, dim3(static_cast<uint32_t>(grid)), dim3(kScoreThreads), 0, p);
     }
+    const bool launched = hip_ok(ctx, hipGetLastError(), "score kernel launch");
     if (timed) {
-        perf_end(ctx, kPerfScore);
+        perf_detach(ctx, kPerfScore, launched);
     }
-    if (!hip_ok(ctx, hipGetLastError(), "score kernel launch")) {
+    if (!launched) {
         return KVMEM_HIP_ERR_RUNTIME;
     }
     // the fold is not bracketed: a timing event costs the stream a few

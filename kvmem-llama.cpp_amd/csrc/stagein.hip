@@ -1430,16 +1430,16 @@ bool launch_quant_x(kvmem_hip_ctx *ctx, int type, uint32_t n_chunks, const Sourc
     }
     switch (type) {
         case KVMEM_TYPE_Q8_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q8_0, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s, args);
+            ctx_launch(ctx, quant_scatter_kernel<KVMEM_TYPE_Q8_0, Source, XF, GROUP>, dim3(n_chunks), dim3(256), static_cast<uint32_t>(tb), s, args);
             break;
         case KVMEM_TYPE_Q4_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q4_0, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s, args);
+            ctx_launch(ctx, quant_scatter_kernel<KVMEM_TYPE_Q4_0, Source, XF, GROUP>, dim3(n_chunks), dim3(256), static_cast<uint32_t>(tb), s, args);
             break;
         case KVMEM_TYPE_Q5_0:
-            quant_scatter_kernel<KVMEM_TYPE_Q5_0, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s, args);
+            ctx_launch(ctx, quant_scatter_kernel<KVMEM_TYPE_Q5_0, Source, XF, GROUP>, dim3(n_chunks), dim3(256), static_cast<uint32_t>(tb), s, args);
             break;
         case KVMEM_TYPE_F16:
-            quant_scatter_kernel<KVMEM_TYPE_F16, Source, XF, GROUP><<<n_chunks, 256, tb, ctx->stream>>>(s, args);
+            ctx_launch(ctx, quant_scatter_kernel<KVMEM_TYPE_F16, Source, XF, GROUP>, dim3(n_chunks), dim3(256), static_cast<uint32_t>(tb), s, args);
             break;
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported type");
@@ -1475,16 +1475,16 @@ bool launch_kv_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, const BlockSource &s
     const size_t tb = XF ? rope_tab_bytes(sk) : 0;  // only K is RoPE'd
     switch (tv) {
         case KVMEM_TYPE_Q8_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q8_0, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args);
+            ctx_launch(ctx, quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q8_0, XF, GROUP>, dim3(grid), dim3(256), static_cast<uint32_t>(tb), sk, sv, n_k, args);
             break;
         case KVMEM_TYPE_Q4_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q4_0, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args);
+            ctx_launch(ctx, quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q4_0, XF, GROUP>, dim3(grid), dim3(256), static_cast<uint32_t>(tb), sk, sv, n_k, args);
             break;
         case KVMEM_TYPE_Q5_0:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q5_0, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args);
+            ctx_launch(ctx, quant_scatter_kv_kernel<TK, KVMEM_TYPE_Q5_0, XF, GROUP>, dim3(grid), dim3(256), static_cast<uint32_t>(tb), sk, sv, n_k, args);
             break;
         case KVMEM_TYPE_F16:
-            quant_scatter_kv_kernel<TK, KVMEM_TYPE_F16, XF, GROUP><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args);
+            ctx_launch(ctx, quant_scatter_kv_kernel<TK, KVMEM_TYPE_F16, XF, GROUP>, dim3(grid), dim3(256), static_cast<uint32_t>(tb), sk, sv, n_k, args);
             break;
         default:
             fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported V type");
@@ -1704,10 +1704,10 @@ template <int TK>
 static bool launch_x64_v(kvmem_hip_ctx *ctx, int tv, uint32_t grid, size_t tb, const BlockSource &sk,
                          const BlockSource &sv, uint32_t n_k, const ArgTables &args) {
     switch (tv) {
-        case KVMEM_TYPE_Q8_0: x64_kv_kernel<TK, KVMEM_TYPE_Q8_0><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args); break;
-        case KVMEM_TYPE_Q4_0: x64_kv_kernel<TK, KVMEM_TYPE_Q4_0><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args); break;
-        case KVMEM_TYPE_Q5_0: x64_kv_kernel<TK, KVMEM_TYPE_Q5_0><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args); break;
-        case KVMEM_TYPE_F16: x64_kv_kernel<TK, KVMEM_TYPE_F16><<<grid, 256, tb, ctx->stream>>>(sk, sv, n_k, args); break;
+        case KVMEM_TYPE_Q8_0: ctx_launch(ctx, x64_kv_kernel<TK, KVMEM_TYPE_Q8_0>, dim3(grid), dim3(256), static_cast<uint32_t>(tb), sk, sv, n_k, args); break;
+        case KVMEM_TYPE_Q4_0: ctx_launch(ctx, x64_kv_kernel<TK, KVMEM_TYPE_Q4_0>, dim3(grid), dim3(256), static_cast<uint32_t>(tb), sk, sv, n_k, args); break;
+        case KVMEM_TYPE_Q5_0: ctx_launch(ctx, x64_kv_kernel<TK, KVMEM_TYPE_Q5_0>, dim3(grid), dim3(256), static_cast<uint32_t>(tb), sk, sv, n_k, args); break;
+        case KVMEM_TYPE_F16: ctx_launch(ctx, x64_kv_kernel<TK, KVMEM_TYPE_F16>, dim3(grid), dim3(256), static_cast<uint32_t>(tb), sk, sv, n_k, args); break;
         default: fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported V type"); return false;
     }
     return true;
@@ -1735,10 +1735,10 @@ static bool launch_x64(kvmem_hip_ctx *ctx, int tk, int tv, uint32_t n_k, uint32_
         }
     } else {
         switch (tk) {
-            case KVMEM_TYPE_Q8_0: x64_kernel<KVMEM_TYPE_Q8_0><<<grid, 256, tb, ctx->stream>>>(sk, args); break;
-            case KVMEM_TYPE_Q4_0: x64_kernel<KVMEM_TYPE_Q4_0><<<grid, 256, tb, ctx->stream>>>(sk, args); break;
-            case KVMEM_TYPE_Q5_0: x64_kernel<KVMEM_TYPE_Q5_0><<<grid, 256, tb, ctx->stream>>>(sk, args); break;
-            case KVMEM_TYPE_F16: x64_kernel<KVMEM_TYPE_F16><<<grid, 256, tb, ctx->stream>>>(sk, args); break;
+            case KVMEM_TYPE_Q8_0: ctx_launch(ctx, x64_kernel<KVMEM_TYPE_Q8_0>, dim3(grid), dim3(256), static_cast<uint32_t>(tb), sk, args); break;
+            case KVMEM_TYPE_Q4_0: ctx_launch(ctx, x64_kernel<KVMEM_TYPE_Q4_0>, dim3(grid), dim3(256), static_cast<uint32_t>(tb), sk, args); break;
+            case KVMEM_TYPE_Q5_0: ctx_launch(ctx, x64_kernel<KVMEM_TYPE_Q5_0>, dim3(grid), dim3(256), static_cast<uint32_t>(tb), sk, args); break;
+            case KVMEM_TYPE_F16: ctx_launch(ctx, x64_kernel<KVMEM_TYPE_F16>, dim3(grid), dim3(256), static_cast<uint32_t>(tb), sk, args); break;
             default: fail(ctx, KVMEM_HIP_ERR_UNSUPPORTED, "stage-in: unsupported K type"); return false;
         }
     }
@@ -2356,7 +2356,7 @@ int kvmem_hip_stagein_blocks(kvmem_hip_ctx *ctx, const kvmem_hip_history *hist,
                                bv * cap, jt, hist->n_layers, T,
                                hist->n_embd_v, 0, xp, false);
     }
-    PerfScope timed(ctx, kPerfSet);
+    PerfLaunchScope timed(ctx, kPerfSet);  // one launch: the events ride on it
     st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp, jt.tables.args);
     if (st == KVMEM_HIP_OK) {
         timed.ok();
@@ -2425,7 +2425,7 @@ int kvmem_hip_stagein_blocks_host(kvmem_hip_ctx *ctx, const kvmem_hip_host_histo
             sv = make_block_source(pool->type_v, view + kbytes, span, layer_bytes, jt, L, T,
                                    hist->n_embd_v, 0, xp, false);
         }
-        PerfScope timed(ctx, kPerfSet);
+        PerfLaunchScope timed(ctx, kPerfSet);  // one launch: the events ride on it
         st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, want_v ? &sv : nullptr, n, xp, jt.tables.args);
         if (st == KVMEM_HIP_OK) {
             timed.ok();
@@ -2885,7 +2885,7 @@ int kvmem_hip_reselect_device_stagein(kvmem_hip_ctx *ctx, const kvmem_hip_histor
     const BlockSource sv = make_block_source(pool->type_v, static_cast<const uint8_t *>(hist->v), bv, bv * cap, jt,
                                              L, T, hist->n_embd_v, 0, xp, false);
     (void) hipSetDevice(ctx->device);
-    PerfScope timed(ctx, kPerfSet);
+    PerfLaunchScope timed(ctx, kPerfSet);  // one launch: the events ride on it
     const int st = launch_block_job(ctx, pool->type_k, sk, pool->type_v, &sv, n_staged, xp, kNoArgTables);
     if (st == KVMEM_HIP_OK) {
         timed.ok();
