@@ -510,7 +510,10 @@ KVMEM_HIP_API int kvmem_engine_get_query(kvmem_engine *e, float *q_sum, uint32_t
 KVMEM_HIP_API int kvmem_engine_set_query(kvmem_engine *e, const float *q_sum, const uint32_t *q_count);
 KVMEM_HIP_API int kvmem_engine_freeze_query(kvmem_engine *e, int frozen);
 
-/* Scores of the last preview (host copy, block count entries). */
+/* Scores of the last preview (host copy, block count entries).  Every
+ * preview scores every block, also when the budget takes them all, as the
+ * reference's preview_retrieval scores before it selects
+ * (llama-memory-kvmem.cpp:3047-3067). */
 KVMEM_HIP_API int kvmem_engine_scores(kvmem_engine *e, float *out, uint32_t n);
 
 #ifdef __cplusplus

@@ -1238,9 +1238,12 @@ int query_state(kvmem_engine *e, std::vector<uint32_t> &counts) {
 }
 
 // The scoring half of a preview: the mandatory ids (the caller's, then the
-// spans'), the store's charge, and, unless every block fits the budget, the
-// scores of every block launched into d_scores (not waited for).  *empty:
-// the store has no block.
+// spans'), the store's charge, and the scores of every block launched into
+// d_scores (not waited for) -- also when every block fits the budget and the
+// selection needs none, as the reference scores on every preview
+// (preview_retrieval, llama-memory-kvmem.cpp:3047-3067), so that the scores
+// a caller reads back are always this preview's.  *empty: the store has no
+// block.
 int preview_scores(kvmem_engine *e, const void *q, int32_t q_type, uint32_t n_q_tokens,
                    const uint32_t *mandatory, uint32_t n_mandatory, kvmem_amd::TopkCharge &charge,
                    bool *empty) {
@@ -1276,9 +1279,6 @@ int preview_scores(kvmem_engine *e, const void *q, int32_t q_type, uint32_t n_q_
     const std::vector<uint32_t> spans = e->retrieval_mandatory();
     mand.insert(mand.end(), spans.begin(), spans.end());
     charge = e->rt.store().charge_topk(mand);
-    if (charge.all_fit) {
-        return KVMEM_HIP_OK;
-    }
     const uint32_t n_embd_q = e->p.n_head * e->p.head_dim;
     if (imported) {
         // the set query's sums and counts, with the rows captured since
@@ -1663,11 +1663,9 @@ int kvmem_engine_preview_meank(kvmem_engine *e, const float *q_sum, const uint32
     const std::vector<uint32_t> spans = e->retrieval_mandatory();
     mand.insert(mand.end(), spans.begin(), spans.end());
     const kvmem_amd::TopkCharge charge = e->rt.store().charge_topk(mand);
-    if (!charge.all_fit) {
-        const int rc = meank_scores(e, q_sum, q_count);
-        if (rc != KVMEM_HIP_OK) {
-            return rc;
-        }
+    const int rc = meank_scores(e, q_sum, q_count);  // also when every block fits, as preview_scores
+    if (rc != KVMEM_HIP_OK) {
+        return rc;
     }
     return select_topk(e, charge, sel, n_sel);
 }

@@ -230,3 +230,32 @@ def test_engine_own_pool_starts_cleared():
             assert all_zero()
         finally:
             ctx.close()
+
+
+@pytest.mark.parametrize("scorer", [0, 1], ids=["per_token_max", "mean_k"])
+def test_engine_scores_when_every_block_fits(oracle, scorer):
+    """A budget that takes every block still scores them: the preview's
+    scores are this preview's (the reference scores before it selects,
+    llama-memory-kvmem.cpp:3047-3067), within 1e-3 of the fp64 oracle for
+    the per-token scorer, and not those of an earlier, larger history."""
+    announce(f"every block fits the budget: scores still computed (scorer {scorer})")
+    cap = 12
+    k, v, q = history(cap, seed=23)
+    with make_engine(8, 2, scorer=scorer) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, 12 * T)
+        sel = eng.preview(q.data_ptr(), q.shape[1])          # 12 blocks, budget 8: scored
+        assert len(sel.blocks) == 8
+        eng.truncate_to(5 * T + 40)                          # 6 blocks: all fit
+        sel = eng.preview(q.data_ptr(), q.shape[1])
+        assert sel.blocks == list(range(6))
+        got = np.array(eng.scores(), dtype=np.float64)
+        assert np.all(got != 0.0)
+        if scorer == 0:
+            want = oracle_scores(oracle, q, k, 6, last_T=40)
+            rel = np.abs(got - want) / np.maximum(np.abs(want), 1e-6)
+            assert rel.max() <= RTOL, f"max rel err {rel.max():.3e}"
+        eng.apply(sel)
+        st = eng.apply_retrieval(q.data_ptr(), q.shape[1])   # all fit: the host path
+        assert st["n_staged"] == 0
+        again = np.array(eng.scores(), dtype=np.float64)
+        assert np.array_equal(again, got)
