@@ -64,6 +64,28 @@ def test_score_small_vs_fp64_oracle(ctx, oracle, D, Tq, q_dtype, last_T):
     assert_close(s, oracle.combine_layers(want_ls, 0), "mean scores")
 
 
+@pytest.mark.parametrize("T,Hq,Hkv,D,Tq,last_T", [
+    (32, 8, 8, 128, 12, 9),      # no grouping: one query head per KV head
+    (64, 6, 2, 256, 10, 1),      # groups of 3
+    (16, 32, 4, 128, 50, 16),    # groups of 8, 400 rows: two slices, full last block
+    (96, 8, 2, 128, 100, 95),    # groups of 4, 400 rows over 128-wide heads: two slices
+    (128, 16, 16, 256, 1, 127),  # one query token
+    (1, 24, 4, 256, 8, 0),       # one-token blocks
+])
+def test_score_other_groupings_and_block_sizes(ctx, oracle, T, Hq, Hkv, D, Tq, last_T):
+    """Head groupings (1, 3, 4, 8 query heads per KV head), block lengths from
+    1 to 128 tokens and queries of several row slices at both head sizes:
+    every layer score and block score within 1e-3 of the fp64 oracle."""
+    announce(f"scorer: T={T} Hq={Hq} Hkv={Hkv} D={D} Tq={Tq} last_T={last_T}")
+    L, B = 3, 13
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=L, B=B, Tq=Tq, seed=5 * T + Hq + Tq, T=T, Hkv=Hkv, Hq=Hq,
+                                        D=D)
+    s, ls = run_score(ctx, k, q, kv.TYPE_BF16, Hq, Hkv, D, last_T)
+    want_ls = oracle.score_pertoken_max(q_f32(q), workloads.to_bits(torch, k), last_T)
+    assert_close(ls, want_ls, "layer scores")
+    assert_close(s, oracle.combine_layers(want_ls, 0), "mean scores")
+
+
 @pytest.mark.parametrize("mode", [kv.LAYER_MEAN, kv.LAYER_MAX, kv.LAYER_SUM])
 def test_score_layer_reduce_modes(ctx, oracle, mode):
     announce(f"layer reduce mode {mode}")
