@@ -77,6 +77,44 @@ def test_meank_scores_vs_oracle(ctx, oracle):
     assert np.max(np.abs(got - want)) <= 1e-5, np.max(np.abs(got - want))
 
 
+@pytest.mark.parametrize("Tb,Hq,Hkv,Dh,last_T", [
+    (32, 8, 8, 128, 5),      # no grouping, 1024-element rows
+    (64, 6, 2, 256, 0),      # groups of 3, 512-element rows
+    (16, 32, 16, 128, 16),   # groups of 2, 2048-element rows (the key sums' widest)
+    (128, 16, 2, 128, 100),  # groups of 8, 256-element rows
+])
+def test_meank_other_groupings(ctx, oracle, Tb, Hq, Hkv, Dh, last_T):
+    """Key sums bit-exact and mean-K scores within 1e-5 of the oracle's chain
+    over head groupings of 1, 2, 3 and 8, row widths from 256 to 2048 and
+    block lengths from 16 to 128 tokens, a partial last block included."""
+    announce(f"mean-K: T={Tb} Hq={Hq} Hkv={Hkv} D={Dh} last_T={last_T}")
+    L, nb, Tq = 3, 9, 5
+    e = Hkv * Dh
+    k, _, q = workloads.scoring_tensors(torch, "cuda", L=L, B=nb, Tq=Tq, seed=Tb + Hq + Dh, T=Tb, Hkv=Hkv, Hq=Hq,
+                                        D=Dh)
+    ks = torch.full((L, nb, e), float("nan"), dtype=torch.float32, device="cuda")
+    mt = torch.zeros((L, nb), dtype=torch.int32, device="cuda")
+    hist = ctx.make_history(k.data_ptr(), None, L, nb, Tb, e, 0, last_T, nb)
+    torch.cuda.synchronize()
+    ctx.meank_sums(hist, list(range(nb)), ks.data_ptr(), mt.data_ptr())
+    ctx.sync()
+    kb = workloads.to_bits(torch, k)
+    got_s, got_mt = ks.cpu().numpy(), mt.cpu().numpy()
+    for layer in range(L):
+        for b in range(nb):
+            nt = last_T if (b == nb - 1 and last_T) else Tb
+            assert got_mt[layer, b] == nt
+            want = oracle.meank_sum_f16(kb[layer, b].reshape(Tb, e)[:nt])
+            assert np.array_equal(got_s[layer, b].view(np.uint32), want.view(np.uint32)), (layer, b)
+    q_sum = torch.from_numpy(oracle.q_accumulate(q.float().cpu().numpy().reshape(L, Tq, -1))).to("cuda")
+    scores = torch.empty(nb, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.score_meank(q_sum.data_ptr(), [Tq] * L, ks.data_ptr(), mt.data_ptr(), L, nb, Hq, Hkv, Dh, scores.data_ptr())
+    ctx.sync()
+    want = oracle.score_meank(q_sum.cpu().numpy(), [Tq] * L, got_s, got_mt.astype(np.uint32), Hq, Hkv, Dh)
+    assert np.max(np.abs(scores.cpu().numpy().astype(np.float64) - want)) <= 1e-5
+
+
 def test_meank_full_history_sampled(ctx, oracle):
     announce("full history 16 layers x 2048 blocks, sampled blocks")
     L, nb = 16, 2048
