@@ -12,7 +12,8 @@
 // out with nontemporal 16-byte stores.  The group scale comes from a two-step
 // quad reduction through DPP, the quantized bytes are packed in registers,
 // written to the wave's LDS region in ggml's byte layout, and copied out
-// with aligned 16-byte global stores.
+// with aligned 16-byte global stores (2-byte stores into a slot that is not
+// a whole number of 16 bytes, which starts 2-byte aligned only).
 //
 // Arithmetic follows ggml's quantize_row_*_ref exactly (restated in the
 // reference's CUDA kernels, llama-kvmem-stagein.cu:180-233):
@@ -840,7 +841,10 @@ __device__ inline void quant_chunk_body(const Source &source, const Chunk &c, ui
     const uint32_t ngw = c.ng > wg0 ? min(static_cast<uint32_t>(kWaveGroups), c.ng - wg0) : 0u;
     const uint32_t nb = ngw * GB;
     uint8_t *dst = c.dst + static_cast<uint64_t>(c.g0 + wg0) * GB;
-    const uint32_t full = nb & ~15u;
+    // A slot whose groups are not a multiple of 8 (block_tokens x groups per
+    // row) starts 2-byte aligned only: its bytes go out 2 at a time (groups
+    // and slots are whole even-sized units, so every such address is even).
+    const uint32_t full = (reinterpret_cast<uintptr_t>(dst) & 15u) == 0 ? (nb & ~15u) : 0u;
     for (uint32_t off = lane * 16u; off < full; off += 1024u) {
         // packed rows are read by attention later, not by this launch
         const u32x4_t w = *reinterpret_cast<const u32x4_t *>(wl + off);
@@ -1377,13 +1381,20 @@ __device__ inline void x64_unit_layers(const BlockSource &s, uint32_t c, uint8_t
         wave_lds_order();
         const uint32_t nb = nvl * 2u * GB;
         uint8_t *out = ch.dst + static_cast<uint64_t>(ch.g0) * GB;
-        const uint32_t full = nb & ~15u;
-        for (uint32_t off = lane * 16u; off < full; off += 1024u) {
-            const u32x4_t w = *reinterpret_cast<const u32x4_t *>(wl + off);
-            __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t *>(out + off));
-        }
-        for (uint32_t off = full + lane * 4u; off < nb; off += 256u) {
-            *reinterpret_cast<uint32_t *>(out + off) = *reinterpret_cast<const uint32_t *>(wl + off);
+        if ((reinterpret_cast<uintptr_t>(out) & 15u) == 0) {
+            const uint32_t full = nb & ~15u;
+            for (uint32_t off = lane * 16u; off < full; off += 1024u) {
+                const u32x4_t w = *reinterpret_cast<const u32x4_t *>(wl + off);
+                __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t *>(out + off));
+            }
+            for (uint32_t off = full + lane * 4u; off < nb; off += 256u) {
+                *reinterpret_cast<uint32_t *>(out + off) = *reinterpret_cast<const uint32_t *>(wl + off);
+            }
+        } else {
+            // a slot of a group count not a multiple of 8 starts 2-byte aligned only
+            for (uint32_t off = lane * 2u; off < nb; off += 128u) {
+                *reinterpret_cast<uint16_t *>(out + off) = *reinterpret_cast<const uint16_t *>(wl + off);
+            }
         }
         wave_lds_order();  // the copy-out reads finish before the next layer's rows land
     }

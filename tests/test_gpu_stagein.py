@@ -104,6 +104,54 @@ def test_stagein_heavy_tailed_multilayer_partial(ctx, oracle, type_):
             assert np.array_equal(got, want), f"layer {l} {name}: {first_diff(got, want)}"
 
 
+@pytest.mark.parametrize("T,E,type_,had", [
+    (7, 96, kv.TYPE_Q8_0, 0),     # 21 groups per slot
+    (100, 160, kv.TYPE_Q5_0, 0),  # 500 groups per slot
+    (1, 32, kv.TYPE_Q4_0, 0),     # one group per slot
+    (13, 96, kv.TYPE_F16, 0),     # F16 slots stay 16-byte aligned
+    (5, 192, kv.TYPE_Q8_0, 64),   # the 64-elements-per-lane transform kernel, 30 groups per slot
+    (3, 64, kv.TYPE_Q4_0, 64),    # 6 groups per slot, one partial lane unit
+])
+def test_stagein_slots_not_16_byte_aligned(ctx, oracle, T, E, type_, had):
+    """Block lengths and row widths whose slots are not a whole number of 16
+    bytes (block_tokens x groups per row not a multiple of 8), so slots start
+    2-byte aligned: every staged block's rows bit-exact at its slot, the
+    partial last block included, and every other pool byte untouched, with
+    and without a Hadamard rotation (64-wide, the 64-elements-per-lane
+    kernel)."""
+    announce(f"unaligned slots: T={T} E={E} type={type_} hadamard={had}")
+    L, B, n_slots = 2, 6, 9
+    last = max(1, T - 3) if T > 1 else 0
+    rng = np.random.default_rng(T * 31 + E)
+    K = workloads.f16_bits((rng.standard_normal((L, B, T, E)) * 2).astype(np.float32))
+    V = workloads.f16_bits(rng.standard_normal((L, B, T, E)).astype(np.float32))
+    ids, slots = [5, 0, 3, 1], [8, 1, 4, 6]   # block 5: the partial last one
+    kd, vd = dev_bits(K), dev_bits(V)
+    rb = kv.row_size(type_, E)
+    pks = [new_pool(n_slots, T, rb) for _ in range(L)]
+    pvs = [new_pool(n_slots, T, rb) for _ in range(L)]
+    xf = ctx.make_transform(64, 0, None, had, had) if had else None
+    hist = ctx.make_history(kd.data_ptr(), vd.data_ptr(), L, B, T, E, E, last)
+    pool = ctx.make_pool(L, n_slots, T, E, E, type_, type_, [p.data_ptr() for p in pks],
+                         [p.data_ptr() for p in pvs], xf)
+    torch.cuda.synchronize()
+    ctx.stagein_blocks(hist, pool, ids, slots)
+    ctx.sync()
+    ntoks = [last if (b == B - 1 and last) else T for b in ids]
+    for layer in range(L):
+        for name, src, p in (("K", K, pks[layer]), ("V", V, pvs[layer])):
+            got = p.cpu().numpy().reshape(n_slots * T, rb)
+            want = np.full((n_slots * T, rb), SENTINEL, dtype=np.uint8)
+            for b, s, nt in zip(ids, slots, ntoks):
+                rows = src[layer, b, :nt]
+                if had:
+                    x = oracle.transform_rows(oracle.f16_to_f32(rows).reshape(nt, E), 64, 0, None, 0, had)
+                    want[s * T: s * T + nt] = oracle.quantize_rows_f32(type_, x)
+                else:
+                    want[s * T: s * T + nt] = oracle.quantize_rows_f16(type_, rows)
+            assert np.array_equal(got, want), f"layer {layer} {name}: {first_diff(got, want)}"
+
+
 def special_rows(E: int = 1024) -> np.ndarray:
     """128 rows of crafted groups (f16 bits), remaining groups random."""
     rng = np.random.default_rng(7)
