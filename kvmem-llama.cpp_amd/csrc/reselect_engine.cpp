@@ -615,6 +615,24 @@ namespace {
 // No block is in the pool any more: every block goes back to the host tier,
 // the working set is empty and every slot is free (the next apply stages
 // its whole selection).
+// Take one block out of the pool, its slot back to the free list: a
+// selection that holds it stages it again.
+void evict_block(kvmem_engine *e, uint32_t id) {
+    if (id >= e->rt.store().block_count()) {
+        return;
+    }
+    const Block &b = e->rt.store().blocks()[id];
+    if (b.tier == Tier::GPU && b.gpu_slot >= 0) {
+        e->slots.free_gpu_slot(b.gpu_slot);
+    }
+    e->rt.store().set_block_tier(id, Tier::CPU);
+    e->rt.store().drop_from_working_set(id);
+    if (e->dirty_tail == static_cast<int64_t>(id)) {
+        e->dirty_tail = -1;
+    }
+    ++e->attn_epoch;
+}
+
 void drop_residency(kvmem_engine *e) {
     for (const Block &b : e->rt.store().blocks()) {
         if (b.tier == Tier::GPU) {
@@ -887,7 +905,15 @@ int kvmem_engine_append_tokens(kvmem_engine *e, uint32_t n_new_tokens) {
         // a partial tail that is in the pool must be staged again
         const Block &tail = e->rt.store().blocks().back();
         if (tail.n_tokens < e->p.block_tokens && tail.tier == Tier::GPU && tail.gpu_slot >= 0) {
-            e->dirty_tail = tail.block_id;
+            const int64_t tail_id = tail.block_id;
+            if (e->dirty_tail >= 0 && e->dirty_tail != tail_id) {
+                // The engine tracks one block whose pool rows are stale.  An
+                // earlier one (a tail that grew, then rows decoded after it)
+                // leaves the pool rather than lose its mark: the next
+                // selection that holds it stages it again.
+                evict_block(e, static_cast<uint32_t>(e->dirty_tail));
+            }
+            e->dirty_tail = tail_id;
         }
     }
     e->rt.register_append(n_new_tokens);

@@ -24,7 +24,7 @@ kv = load_pkg()
 from kvmem_amd import host, workloads  # noqa: E402
 
 from engine_helpers import (E, HKV, HQ, D, L, RTOL, T, block_major_pinned, check_pool,  # noqa: E402,F401
-                            history, make_engine, oracle_scores)
+                            decode_rows, history, make_engine, oracle_scores)
 
 
 def announce(msg: str) -> None:
@@ -259,3 +259,33 @@ def test_engine_scores_when_every_block_fits(oracle, scorer):
         assert st["n_staged"] == 0
         again = np.array(eng.scores(), dtype=np.float64)
         assert np.array_equal(again, got)
+
+
+def test_engine_second_grown_tail_evicts_the_first(oracle):
+    """The engine marks one block whose pool rows are stale.  A resident
+    partial tail grows (block 2: 40 rows in the pool, 128 in the history);
+    rows decoded after it go into a new block (3) that takes a slot; block 3
+    then grows too.  Block 2 leaves the pool rather than lose its mark, and
+    the next apply stages both again: every row bit-exact, none stale."""
+    announce("a second grown tail: the first leaves the pool and is staged again")
+    cap = 8
+    k, v, q = history(cap, seed=29)
+    with make_engine(6, 2) as eng:
+        eng.set_device_history(k.data_ptr(), v.data_ptr(), cap, 2 * T + 40)
+        sel = eng.preview(q.data_ptr(), q.shape[1])
+        assert sel.blocks == [0, 1, 2]
+        eng.apply(sel)
+        eng.append_tokens(T - 40)                       # block 2 full in the history, stale in the pool
+        decode_rows(eng, k, v, 3 * T, 3 * T + 50)       # block 3 takes a slot, its 50 rows written
+        assert eng.block_slots()[3] >= 0
+        before = eng.attention_epoch()
+        eng.append_tokens(30)                           # block 3 grows: block 2 leaves the pool
+        slots = eng.block_slots()
+        assert slots[2] == -1 and slots[3] >= 0, slots
+        assert eng.attention_epoch() > before
+        sel = eng.preview(q.data_ptr(), q.shape[1])
+        assert sel.blocks == [0, 1, 2, 3]
+        st = eng.apply(sel)
+        assert st["n_staged"] == 2                      # blocks 2 and 3, both whole again
+        check_pool(eng, oracle, k, v, sel.blocks, kv.TYPE_Q8_0, kv.TYPE_Q8_0,
+                   ntok_of=lambda b: 80 if b == 3 else T)

@@ -1,7 +1,10 @@
-"""The reselect engine over another geometry, in random operation sequences.
+"""The reselect engine over other geometries, in random operation sequences.
 
-3 layers, 32-token blocks, 8 query heads over 2 KV heads of 128 (GQA 4,
-256-element rows), a 4-token bf16 query; pools of q8_0, q5_0, q4_0 and F16
+Mostly 3 layers, 32-token blocks, 8 query heads over 2 KV heads of 128 (GQA
+4, 256-element rows), a 4-token bf16 query; also 7-token blocks over one KV
+head of 128 and 5-token blocks over three, whose slots are not a whole
+number of 16 bytes (the stage-in's 2-byte stores, the slot moves' gather
+path); pools of q8_0, q5_0, q4_0 and F16
 in both slot layouts, the per-token max scorer and the reference's mean-K
 scorer, the row transform (NeoX RoPE 128 at the original positions, then
 attn_rot: Hadamard 128 on K, 64 on V), and a pinned host history as the only
@@ -42,8 +45,7 @@ from conftest import load_pkg  # noqa: E402
 kv = load_pkg()
 from kvmem_amd import host, workloads  # noqa: E402
 
-L, T, HQ, HKV, D = 3, 32, 8, 2, 128
-E = HKV * D
+GEOM = (3, 32, 8, 2, 128)     # layers, block tokens, query heads, KV heads, head_dim
 CAP, TQ = 40, 4
 RTOL = 1e-3
 N_OPS = int(os.environ.get("KVMEM_GEOM_OPS", "120"))
@@ -52,24 +54,28 @@ OPS = ["preview_apply", "retrieve", "append", "truncate", "decode", "span"]
 WEIGHTS = [0.25, 0.25, 0.12, 0.1, 0.15, 0.13]
 
 CASES = [
-    # (canonical layout, type_k, type_v, budget, reserve, seed, scorer, row transform, host history only)
-    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 6, 3, 201, 0, False, False),
-    (0, kv.TYPE_Q4_0, kv.TYPE_Q5_0, 7, 2, 202, 0, False, False),
-    (1, kv.TYPE_Q5_0, kv.TYPE_Q4_0, 5, 4, 203, 0, False, False),
-    (1, kv.TYPE_Q8_0, kv.TYPE_F16, 6, 3, 204, 0, False, False),
-    (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 6, 3, 205, 1, False, False),
-    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 6, 3, 206, 0, True, False),
-    (1, kv.TYPE_Q5_0, kv.TYPE_Q8_0, 6, 3, 207, 1, False, True),
+    # (canonical layout, type_k, type_v, budget, reserve, seed, scorer, row transform, host history only,
+    #  geometry)
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 6, 3, 201, 0, False, False, GEOM),
+    (0, kv.TYPE_Q4_0, kv.TYPE_Q5_0, 7, 2, 202, 0, False, False, GEOM),
+    (1, kv.TYPE_Q5_0, kv.TYPE_Q4_0, 5, 4, 203, 0, False, False, GEOM),
+    (1, kv.TYPE_Q8_0, kv.TYPE_F16, 6, 3, 204, 0, False, False, GEOM),
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 6, 3, 205, 1, False, False, GEOM),
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 6, 3, 206, 0, True, False, GEOM),
+    (1, kv.TYPE_Q5_0, kv.TYPE_Q8_0, 6, 3, 207, 1, False, True, GEOM),
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q5_0, 6, 3, 208, 0, False, False, (2, 7, 4, 1, 128)),
+    (0, kv.TYPE_Q4_0, kv.TYPE_Q8_0, 7, 2, 209, 0, False, False, (2, 7, 4, 1, 128)),
+    (1, kv.TYPE_Q5_0, kv.TYPE_Q4_0, 6, 3, 210, 1, False, False, (3, 5, 12, 3, 128)),
 ]
 IDS = ["canonical_q8", "lifo_q4_q5", "canonical_q5_q4", "canonical_q8_f16", "meank_q8_q4", "transform_q8",
-       "host_only_meank_q5_q8"]
+       "host_only_meank_q5_q8", "T7_canonical_q8_q5", "T7_lifo_q4_q8", "T5_meank_q5_q4"]
 
 
 def announce(msg: str) -> None:
     print(f"[geometry] {msg}", flush=True)
 
 
-def read_pool(eng, types) -> list:
+def read_pool(eng, types, L: int, T: int, E: int) -> list:
     """[layer][K or V] -> the pool tensor's rows on the host."""
     out = []
     ctx = kv.Context(0)
@@ -92,9 +98,11 @@ def read_pool(eng, types) -> list:
 
 @pytest.mark.parametrize("case", CASES, ids=IDS)
 def test_engine_sequences_other_geometry(oracle, case):
-    canon, tk, tv, budget, reserve, seed, scorer, xf, host_only = case
+    canon, tk, tv, budget, reserve, seed, scorer, xf, host_only, (L, T, HQ, HKV, D) = case
+    E = HKV * D
     announce(f"{N_OPS} operations, canonical={canon}, types {kv.TYPE_NAMES[tk]}/{kv.TYPE_NAMES[tv]}, "
-             f"budget {budget} + {reserve}, scorer {scorer}, transform {xf}, host history only {host_only}")
+             f"budget {budget} + {reserve}, scorer {scorer}, transform {xf}, host history only {host_only}, "
+             f"geometry (L, T, Hq, Hkv, D) = {(L, T, HQ, HKV, D)}")
     rng = np.random.default_rng(seed)
     k, v, _ = workloads.scoring_tensors(torch, "cuda", L=L, B=CAP, Tq=TQ, seed=seed, T=T, Hkv=HKV, Hq=HQ, D=D,
                                         with_v=True)
@@ -135,9 +143,10 @@ def test_engine_sequences_other_geometry(oracle, case):
 
     total = int(rng.integers(8 * T, 20 * T))
     valid: dict[int, int] = {}   # resident block -> rows the pool holds for it
+    stale: list = [None]         # the resident block whose pool rows the engine knows are stale
     span = {"qb": -1, "qe": 0, "force": -1}
     counts = {op: 0 for op in OPS}
-    hits = {"decode_refused": 0, "span_set": 0, "mandatory_checked": 0}
+    hits = {"decode_refused": 0, "span_set": 0, "mandatory_checked": 0, "evicted": 0}
     last_sel: list[int] = []
 
     def ntok(b: int) -> int:
@@ -229,6 +238,7 @@ def test_engine_sequences_other_geometry(oracle, case):
                 hits["mandatory_checked"] += bool(mand)
                 assert chosen == oracle.pick_topk(scores.astype(np.float64), budget, sink=1, mandatory=mand), what
                 valid = {b: ntok(b) for b in chosen}
+                stale[0] = None
                 last_sel = chosen
                 if canon:
                     slots = eng.block_slots()
@@ -237,6 +247,13 @@ def test_engine_sequences_other_geometry(oracle, case):
                 n = min(int(rng.integers(1, 3 * T)), CAP * T - total)
                 if n == 0:
                     continue
+                tail = (total + T - 1) // T - 1
+                if ntok(tail) < T and tail in valid:
+                    # the grown tail is the stale block now; an earlier one leaves the pool
+                    if stale[0] is not None and stale[0] != tail:
+                        valid.pop(stale[0], None)
+                        hits["evicted"] += 1
+                    stale[0] = tail
                 eng.append_tokens(n)
                 total += n
             elif op == "truncate":
@@ -244,11 +261,15 @@ def test_engine_sequences_other_geometry(oracle, case):
                 eng.truncate_to(total)
                 nb = (total + T - 1) // T
                 valid = {b: min(c, ntok(b)) for b, c in valid.items() if b < nb}
+                if stale[0] is not None and stale[0] >= nb:
+                    stale[0] = None
             elif op == "decode":
                 n = min(int(rng.integers(1, 2 * T)), CAP * T - total)
                 if n == 0:
                     continue
                 before = (list(eng.block_slots()), eng.total_tokens())
+                tail = (total + T - 1) // T - 1
+                gets_slot = total % T != 0 and tail not in valid   # a partial tail taking a slot
                 try:
                     decode(eng, total, total + n)
                 except kv.KvMemError as ex:
@@ -260,6 +281,8 @@ def test_engine_sequences_other_geometry(oracle, case):
                     total += n
                     for b in range(begin // T, (total + T - 1) // T):
                         valid[b] = ntok(b)
+                    if gets_slot:
+                        stale[0] = tail
             else:
                 if rng.random() < 0.3:
                     span = {"qb": -1, "qe": 0, "force": -1}
@@ -277,7 +300,7 @@ def test_engine_sequences_other_geometry(oracle, case):
             resident = {b: s for b, s in enumerate(slots) if s >= 0}
             assert set(resident) == set(valid), f"{what}: resident {sorted(resident)} vs {sorted(valid)}"
             assert len(set(resident.values())) == len(resident), f"{what}: shared slots"
-            pool = read_pool(eng, types)
+            pool = read_pool(eng, types, L, T, E)
             for b, s in resident.items():
                 n = valid[b]
                 for layer in range(L):

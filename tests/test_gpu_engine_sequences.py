@@ -118,6 +118,9 @@ class Model:
         self.hist = 0   # which history the engine reads (its rows key the cache)
         self.total = eng.total_tokens()
         self.valid: dict[int, int] = {}
+        # the one resident block whose pool rows the engine knows to be stale
+        # (a partial tail that grew, or a decoded tail that had no slot)
+        self.stale: int | None = None
         self.cache: dict[tuple, np.ndarray] = {}
         self.n_packed_checked = 0
         self.n_scores_checked = 0
@@ -130,6 +133,24 @@ class Model:
 
     def applied(self, sel: list[int]) -> None:
         self.valid = {b: self.ntok(b) for b in sel}
+        self.stale = None
+
+    def tail_grows(self) -> None:
+        """Before append_tokens: a partial tail in the pool becomes the stale
+        block; an earlier stale block leaves the pool (the engine marks one)."""
+        nb = (self.total + T - 1) // T
+        tail = nb - 1
+        if nb and self.ntok(tail) < T and tail in self.valid:
+            if self.stale is not None and self.stale != tail:
+                self.valid.pop(self.stale, None)
+            self.stale = tail
+
+    def cut(self, total: int) -> None:
+        """truncate_to(total): blocks past it gone, the cut one shortened."""
+        self.total = total
+        self.valid = {b: min(r, self.ntok(b)) for b, r in self.valid.items() if b * T < total}
+        if self.stale is not None and self.stale * T >= total:
+            self.stale = None
 
     def use_history(self, hist: int, k, v) -> None:
         self.hist = hist
@@ -395,13 +416,13 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 sel = eng.preview(qq.data_ptr(), qq.shape[1])
                 n = grow(int(rng.integers(1, 100)))
                 if n > 0:
+                    m.tail_grows()
                     eng.append_tokens(n)
                     m.total += n
                 else:
                     cut = m.total - int(rng.integers(1, 60))
                     eng.truncate_to(cut)
-                    m.total = cut
-                    m.valid = {b: min(r, m.ntok(b)) for b, r in m.valid.items() if b * T < cut}
+                    m.cut(cut)
                 with pytest.raises(kv.StaleSelection):
                     eng.apply(sel)
                 hits["stale_refused"] += 1
@@ -409,6 +430,7 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
             elif op == "append":
                 n = grow(int(rng.integers(1, 300)))
                 if n:
+                    m.tail_grows()
                     eng.append_tokens(n)
                     m.total += n
                 m.check(what)
@@ -417,6 +439,8 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 if n == 0:
                     continue
                 t0 = m.total
+                tail = (t0 + T - 1) // T - 1
+                gets_slot = t0 % T != 0 and tail not in m.valid   # a partial tail taking a slot
                 try:
                     decode_rows(eng, *hists[m.hist], t0, t0 + n)
                 except kv.KvMemError as ex:
@@ -425,6 +449,7 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                     assert ex.code in (kv.ERR_NOMEM, kv.ERR_UNSUPPORTED), (what, str(ex))
                     assert eng.total_tokens() == t0, what
                     m.check(what + " refused")
+                    m.tail_grows()
                     eng.append_tokens(n)
                     m.total += n
                     hits["decode_refused"] += 1
@@ -432,14 +457,15 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                     m.total += n
                     for b in range(t0 // T, (t0 + n + T - 1) // T):
                         m.valid[b] = m.ntok(b)
+                    if gets_slot:
+                        m.stale = tail   # its cells were written whole here, yet it is staged again
                 m.check(what)
             elif op == "truncate":
                 if m.total <= 2 * T:
                     continue
                 cut = int(rng.integers(max(T, m.total - 3 * T), m.total))
                 eng.truncate_to(cut)
-                m.total = cut
-                m.valid = {b: min(r, m.ntok(b)) for b, r in m.valid.items() if b * T < cut}
+                m.cut(cut)
                 m.check(what)
             elif op == "fail":
                 sel = eng.preview(qq.data_ptr(), qq.shape[1])
@@ -461,6 +487,8 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                     res = m.resident()
                     assert set(res) <= set(before), (what, sorted(res), sorted(before))
                     m.valid = {b: before[b] for b in res}
+                    if m.stale not in res:   # the mark goes with its block's slot
+                        m.stale = None
                     m.check(what + " (failed)")
                 else:
                     assert sorted(m.resident()) == sel.blocks, what
@@ -559,6 +587,7 @@ def run_sequence(oracle, case, meank: bool, host_only: bool = False) -> None:
                 eng.set_device_history(kk.data_ptr(), vv.data_ptr(), cap, m.total)
                 m.use_history(cur, kk, vv)
                 m.valid = {}
+                m.stale = None
                 hits["swaps"] += 1
                 m.check(what)
             elif op == "apply_ids":
