@@ -1,8 +1,9 @@
 """The reselect engine over other geometries, in random operation sequences.
 
 Mostly 3 layers, 32-token blocks, 8 query heads over 2 KV heads of 128 (GQA
-4, 256-element rows), a 4-token bf16 query; also 7-token blocks over one KV
-head of 128 and 5-token blocks over three, whose slots are not a whole
+4, 256-element rows), a 4-token bf16 query; also one-token blocks, and
+7-token blocks over one KV head of 128 and 5-token blocks over three, whose
+slots are not a whole
 number of 16 bytes (the stage-in's 2-byte stores, the slot moves' gather
 path); pools of q8_0, q5_0, q4_0 and F16
 in both slot layouts, the per-token max scorer and the reference's mean-K
@@ -17,9 +18,11 @@ operation:
   - each preview's scores: within 1e-3 relative of the fp64 per-token
     scorer, or within 1e-5 of the oracle's mean-K chain (token-order query
     and key sums, score_retrieval), over the history as it stands;
-  - its selection: the oracle's top-k over the engine's scores with block 0
-    and the blocks retrieval_mandatory derives (the span's rows and
-    force_pos's block, as the history stands) charged first;
+  - its selection: the oracle's top-k over the engine's scores with the sink
+    blocks (the first one, two or none), the blocks retrieval_mandatory
+    derives (the span's rows and force_pos's block, as the history stands)
+    and the newest `recent` blocks charged first, equal scores going to the
+    lower id or, as the reference's rule, to the higher;
   - the resident blocks are exactly the last selection's plus the decoded
     ones, cut to the history, in distinct slots, slot i = the i-th selected
     block in the canonical layout;
@@ -55,20 +58,26 @@ WEIGHTS = [0.25, 0.25, 0.12, 0.1, 0.15, 0.13]
 
 CASES = [
     # (canonical layout, type_k, type_v, budget, reserve, seed, scorer, row transform, host history only,
-    #  geometry)
-    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 6, 3, 201, 0, False, False, GEOM),
-    (0, kv.TYPE_Q4_0, kv.TYPE_Q5_0, 7, 2, 202, 0, False, False, GEOM),
-    (1, kv.TYPE_Q5_0, kv.TYPE_Q4_0, 5, 4, 203, 0, False, False, GEOM),
-    (1, kv.TYPE_Q8_0, kv.TYPE_F16, 6, 3, 204, 0, False, False, GEOM),
-    (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 6, 3, 205, 1, False, False, GEOM),
-    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 6, 3, 206, 0, True, False, GEOM),
-    (1, kv.TYPE_Q5_0, kv.TYPE_Q8_0, 6, 3, 207, 1, False, True, GEOM),
-    (1, kv.TYPE_Q8_0, kv.TYPE_Q5_0, 6, 3, 208, 0, False, False, (2, 7, 4, 1, 128)),
-    (0, kv.TYPE_Q4_0, kv.TYPE_Q8_0, 7, 2, 209, 0, False, False, (2, 7, 4, 1, 128)),
-    (1, kv.TYPE_Q5_0, kv.TYPE_Q4_0, 6, 3, 210, 1, False, False, (3, 5, 12, 3, 128)),
+    #  geometry, other engine parameters)
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 6, 3, 201, 0, False, False, GEOM, {}),
+    (0, kv.TYPE_Q4_0, kv.TYPE_Q5_0, 7, 2, 202, 0, False, False, GEOM, {}),
+    (1, kv.TYPE_Q5_0, kv.TYPE_Q4_0, 5, 4, 203, 0, False, False, GEOM, {}),
+    (1, kv.TYPE_Q8_0, kv.TYPE_F16, 6, 3, 204, 0, False, False, GEOM, {}),
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q4_0, 6, 3, 205, 1, False, False, GEOM, {}),
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 6, 3, 206, 0, True, False, GEOM, {}),
+    (1, kv.TYPE_Q5_0, kv.TYPE_Q8_0, 6, 3, 207, 1, False, True, GEOM, {}),
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q5_0, 6, 3, 208, 0, False, False, (2, 7, 4, 1, 128), {}),
+    (0, kv.TYPE_Q4_0, kv.TYPE_Q8_0, 7, 2, 209, 0, False, False, (2, 7, 4, 1, 128), {}),
+    (1, kv.TYPE_Q5_0, kv.TYPE_Q4_0, 6, 3, 210, 1, False, False, (3, 5, 12, 3, 128), {}),
+    (1, kv.TYPE_Q8_0, kv.TYPE_Q8_0, 6, 3, 211, 0, False, False, (2, 1, 8, 2, 128), {}),
+    (1, kv.TYPE_Q4_0, kv.TYPE_Q4_0, 8, 3, 212, 0, False, False, GEOM,
+     {"sink_blocks": 2, "recent_blocks": 2, "tie_lower_index": 0}),
+    (0, kv.TYPE_Q8_0, kv.TYPE_Q5_0, 7, 2, 213, 1, False, False, GEOM,
+     {"sink_blocks": 0, "recent_blocks": 1, "tie_lower_index": 0}),
 ]
 IDS = ["canonical_q8", "lifo_q4_q5", "canonical_q5_q4", "canonical_q8_f16", "meank_q8_q4", "transform_q8",
-       "host_only_meank_q5_q8", "T7_canonical_q8_q5", "T7_lifo_q4_q8", "T5_meank_q5_q4"]
+       "host_only_meank_q5_q8", "T7_canonical_q8_q5", "T7_lifo_q4_q8", "T5_meank_q5_q4", "T1_canonical_q8",
+       "sink2_recent2_higher_ties_q4", "lifo_meank_nosink_recent1_q8_q5"]
 
 
 def announce(msg: str) -> None:
@@ -98,11 +107,14 @@ def read_pool(eng, types, L: int, T: int, E: int) -> list:
 
 @pytest.mark.parametrize("case", CASES, ids=IDS)
 def test_engine_sequences_other_geometry(oracle, case):
-    canon, tk, tv, budget, reserve, seed, scorer, xf, host_only, (L, T, HQ, HKV, D) = case
+    canon, tk, tv, budget, reserve, seed, scorer, xf, host_only, (L, T, HQ, HKV, D), extra = case
+    sink = extra.get("sink_blocks", 1)
+    recent = extra.get("recent_blocks", 0)
+    lower_ties = bool(extra.get("tie_lower_index", 1))
     E = HKV * D
     announce(f"{N_OPS} operations, canonical={canon}, types {kv.TYPE_NAMES[tk]}/{kv.TYPE_NAMES[tv]}, "
              f"budget {budget} + {reserve}, scorer {scorer}, transform {xf}, host history only {host_only}, "
-             f"geometry (L, T, Hq, Hkv, D) = {(L, T, HQ, HKV, D)}")
+             f"geometry (L, T, Hq, Hkv, D) = {(L, T, HQ, HKV, D)}, {extra}")
     rng = np.random.default_rng(seed)
     k, v, _ = workloads.scoring_tensors(torch, "cuda", L=L, B=CAP, Tq=TQ, seed=seed, T=T, Hkv=HKV, Hq=HQ, D=D,
                                         with_v=True)
@@ -205,7 +217,7 @@ def test_engine_sequences_other_geometry(oracle, case):
             c.close()
 
     params = dict(n_layers=L, block_tokens=T, n_head=HQ, n_head_kv=HKV, head_dim=D, budget_blocks=budget,
-                  reserve_blocks=reserve, type_k=tk, type_v=tv, canonical_layout=canon, scorer=scorer)
+                  reserve_blocks=reserve, type_k=tk, type_v=tv, canonical_layout=canon, scorer=scorer, **extra)
     if xf:
         params.update(XF)
     with host.Engine(**params) as eng:
@@ -236,7 +248,8 @@ def test_engine_sequences_other_geometry(oracle, case):
                 check_scores(q, scores, nb)
                 mand = derived()
                 hits["mandatory_checked"] += bool(mand)
-                assert chosen == oracle.pick_topk(scores.astype(np.float64), budget, sink=1, mandatory=mand), what
+                assert chosen == oracle.pick_topk(scores.astype(np.float64), budget, sink=sink, recent=recent,
+                                                  mandatory=mand, tie_lower_index=lower_ties), what
                 valid = {b: ntok(b) for b in chosen}
                 stale[0] = None
                 last_sel = chosen
