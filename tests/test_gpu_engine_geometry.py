@@ -51,7 +51,9 @@ from kvmem_amd import host, workloads  # noqa: E402
 GEOM = (3, 32, 8, 2, 128)     # layers, block tokens, query heads, KV heads, head_dim
 CAP, TQ = 40, 4
 RTOL = 1e-3
+# KVMEM_GEOM_OPS / KVMEM_GEOM_SEED_OFFSET lengthen a run or draw other seeds
 N_OPS = int(os.environ.get("KVMEM_GEOM_OPS", "120"))
+SEED_OFFSET = int(os.environ.get("KVMEM_GEOM_SEED_OFFSET", "0"))
 XF = dict(n_rot=128, rope_freq_base=1e6, attn_rot=1)   # attn_rot widths: K 128, V 64
 OPS = ["preview_apply", "retrieve", "append", "truncate", "decode", "span"]
 WEIGHTS = [0.25, 0.25, 0.12, 0.1, 0.15, 0.13]
@@ -115,7 +117,7 @@ def test_engine_sequences_other_geometry(oracle, case):
     announce(f"{N_OPS} operations, canonical={canon}, types {kv.TYPE_NAMES[tk]}/{kv.TYPE_NAMES[tv]}, "
              f"budget {budget} + {reserve}, scorer {scorer}, transform {xf}, host history only {host_only}, "
              f"geometry (L, T, Hq, Hkv, D) = {(L, T, HQ, HKV, D)}, {extra}")
-    rng = np.random.default_rng(seed)
+    rng = np.random.default_rng(seed + SEED_OFFSET)
     k, v, _ = workloads.scoring_tensors(torch, "cuda", L=L, B=CAP, Tq=TQ, seed=seed, T=T, Hkv=HKV, Hq=HQ, D=D,
                                         with_v=True)
     gen = torch.Generator(device="cuda")
