@@ -194,6 +194,29 @@ def test_q_accumulate_bit_exact(ctx, oracle, dtype):
     assert np.array_equal(qs.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+def test_q_accumulate_long_token_list(ctx, oracle):
+    """A token list longer than the kernel arguments hold (768 entries):
+    1000 tokens, repeats included, uploaded; the sums bit-exact in list
+    order, then continued by a second list."""
+    announce("query sums over a 1000-entry token list")
+    L, Tq, E = 2, 1200, 256
+    rng = np.random.default_rng(37)
+    wide = (rng.standard_normal((L, Tq, E)) * 3).astype(np.float32)
+    q = torch.from_numpy(wide).to("cuda")
+    qs = torch.full((L, E), float("nan"), dtype=torch.float32, device="cuda")
+    tokens = rng.integers(0, Tq, 1000).tolist()
+    torch.cuda.synchronize()
+    ctx.q_accumulate(q.data_ptr(), kv.TYPE_F32, L, Tq, E, qs.data_ptr(), tokens=tokens)
+    ctx.sync()
+    want = oracle.q_accumulate(wide, tokens)
+    assert np.array_equal(qs.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    more = rng.integers(0, Tq, 900).tolist()
+    ctx.q_accumulate(q.data_ptr(), kv.TYPE_F32, L, Tq, E, qs.data_ptr(), tokens=more, reset=False)
+    ctx.sync()
+    want = oracle.q_accumulate(wide, more, q_sum=want)
+    assert np.array_equal(qs.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
 def test_engine_scorer_meank_from_query_rows(oracle):
     """scorer = mean-K: preview takes the per-token query itself; the query
     sums, key sums and scores agree with the oracle chain."""

@@ -241,6 +241,29 @@ def test_window_gather_converts_round_to_nearest_even():
         assert bool((out == -3.0).all())
 
 
+def test_window_gather_long_row_list():
+    """A row list longer than the kernel arguments hold (768 entries): 800
+    rows in random order with repeats, uploaded; f32 copies bit-exact and
+    bf16 rounded to nearest even, in every layer."""
+    announce("q_window_gather: 800 rows (uploaded list)")
+    cap, n_layers, e = 1024, 2, 256
+    rng = np.random.default_rng(41)
+    win = (rng.standard_normal((n_layers, cap, e)) * 5).astype(np.float32)
+    rows = rng.integers(0, cap, 800).tolist()
+    wd = torch.from_numpy(win).to("cuda")
+    with kv.Context(0) as ctx:
+        for tdt, ty in ((torch.float32, kv.TYPE_F32), (torch.bfloat16, kv.TYPE_BF16)):
+            out = torch.zeros((n_layers, len(rows), e), dtype=tdt, device="cuda")
+            torch.cuda.synchronize()
+            ctx.q_window_gather(wd.data_ptr(), n_layers, cap, e, rows, ty, out.data_ptr())
+            ctx.sync()
+            if ty == kv.TYPE_F32:
+                assert np.array_equal(out.cpu().numpy().view(np.uint32), win[:, rows].view(np.uint32))
+            else:
+                got = out.cpu().view(torch.int16).numpy().view(np.uint16)
+                assert np.array_equal(got, bf16_rne_bits(np.ascontiguousarray(win[:, rows])))
+
+
 def test_misaligned_device_history_is_refused():
     """Every reader of the device history (scorer, key sums, stage-in)
     loads 16-byte words: set_device_history refuses a misaligned K or V

@@ -149,3 +149,23 @@ def test_engine_selects_over_20000_blocks(oracle):
         assert st["n_staged"] == 512
     del k, v, q
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("n", [5000, 40000], ids=["lds", "streamed"])
+@pytest.mark.parametrize("tie_lower", [True, False])
+def test_topk_many_forced_ids_uploaded(ctx, oracle, n, tie_lower):
+    """More forced ids than travel in the kernel arguments (64): 150 of them,
+    20 repeated, uploaded instead; scores rounded to integers so that many
+    tie.  Both kernels (keys in LDS, and recomputed per pass above 16384
+    blocks), both tie rules: the oracle's selection."""
+    announce(f"{n} blocks, 150 forced ids (uploaded), lower-id ties {tie_lower}")
+    rng = np.random.default_rng(n + int(tie_lower))
+    s = np.round(rng.standard_normal(n) * 8).astype(np.float32)
+    forced = sorted(rng.choice(n, 150, replace=False).tolist())
+    need = 77
+    want = oracle.pick_topk(s.astype(np.float64), len(forced) + need, sink=0, mandatory=forced,
+                            tie_lower_index=tie_lower)
+    d = dev(s)
+    torch.cuda.synchronize()
+    got = ctx.topk(d.data_ptr(), n, need, forced=forced + forced[:20], tie_lower_index=tie_lower)
+    assert got == want
