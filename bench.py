@@ -115,7 +115,7 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
         step()
         restore()
     times, bare, full, staged, moved = [], [], [], [], []
-    score_ms = set_ms = sel_ms = layout_ms = after_ms = 0.0
+    score_ms = set_ms = sel_ms = layout_ms = after_ms = cos_ms = 0.0
     planned = []
     d2d_bytes = 0
     for _ in range(steps):
@@ -161,6 +161,7 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
         ctx.perf_enable(False)
         sel_ms += pf["topk_ms"]
         layout_ms += pf["layout_ms"]
+        cos_ms += pf["meank_cos_ms"]
         d2d_bytes += pf["d2d_bytes"]
         restore()
     assert all(x == staged[0] for x in staged), staged
@@ -169,6 +170,7 @@ def timed_steps(eng, ctx, torch, q, n_q_tokens: int, prev: list, steps: int, war
             "score_ms": score_ms / steps,
             "set_ms": set_ms / steps, "sel_ms": sel_ms / steps, "n_staged": staged[0],
             "layout_ms": layout_ms / steps, "n_moved": max(moved), "d2d_bytes": d2d_bytes // steps,
+            "cos_ms": cos_ms / steps,
             "device_planned": min(planned), "after_score_ms": after_ms / steps, "transfers": xfer}
 
 
@@ -669,10 +671,11 @@ def run_meank_256k(a, torch, kv, workloads, tensors=None) -> dict:
             "value": round(m["ms_step"], 4), "higher_is_better": False, "n_gpus": 1,
             "steps": a.steps, "warmup": a.warmup, "data": "synthetic (seeded N(0,1) keys, bf16 query)",
             "score_roofline": {"bound": "hbm", "kernel": "meank_cos_kernel<256>",
-                               "achieved": round(sums_bytes / (m["score_ms"] * 1e-3) / 1e9, 1),
+                               "achieved": round(sums_bytes / (m["cos_ms"] * 1e-3) / 1e9, 1),
                                "peak": HBM_PEAK_GBS, "unit": "GB/s", "algorithmic_bytes": sums_bytes,
-                               "frac": round(sums_bytes / (m["score_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                               "score_ms": round(m["score_ms"], 4)},
+                               "frac": round(sums_bytes / (m["cos_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                               "kernel_ms": round(m["cos_ms"], 4),
+                               "scoring_span_ms": round(m["score_ms"], 4)},
             "ms_per_step_no_timing_events": round(m["ms_step_no_events"], 4),
             "parts_ms": {"score": round(m["score_ms"], 4), "stagein_kernel": round(m["set_ms"], 4),
                          "topk": round(m["sel_ms"], 4), "layout_kernels": round(m["layout_ms"], 4)},

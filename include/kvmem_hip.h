@@ -585,7 +585,12 @@ KVMEM_HIP_API uint64_t kvmem_hip_debug_fail_left(const kvmem_hip_ctx *ctx);
  * after_score_ms: from the end of a call's scoring to the end of the last
  * stage-in before the next scoring (top-k, the slot plan, moves, stage-in
  * and the idle stream between them); n_after_score such spans.
- * h2d_bytes / d2h_bytes / d2d_bytes: the bytes of kvmem_hip_transfer_get. */
+ * h2d_bytes / d2h_bytes / d2d_bytes: the bytes of kvmem_hip_transfer_get.
+ * meank_cos_ms: the mean-K scorer's cosine kernel alone (events attached to
+ * its launch), the one kernel of that scorer that streams the key sums;
+ * score_ms covers all of its kernels (query, cosine, combine) and the gaps
+ * between them.  The per-token scorer is one kernel, timed in score_ms the
+ * same way. */
 typedef struct kvmem_hip_perf {
     double score_ms;
     double topk_ms;
@@ -606,6 +611,8 @@ typedef struct kvmem_hip_perf {
     uint64_t n_stage_out;
     uint64_t n_plan;
     uint64_t d2h_bytes;
+    double meank_cos_ms;
+    uint64_t n_meank_cos;
 } kvmem_hip_perf;
 
 /* Data this context moved, per direction: [0] host to device, [1] device
@@ -641,6 +648,7 @@ KVMEM_HIP_API int kvmem_hip_perf_enable(kvmem_hip_ctx *ctx, int on);
 #define KVMEM_PERF_STAGE_LAYOUT 16u
 #define KVMEM_PERF_STAGE_STAGE_OUT 32u
 #define KVMEM_PERF_STAGE_PLAN 64u
+#define KVMEM_PERF_STAGE_MEANK_COS 128u
 KVMEM_HIP_API int kvmem_hip_perf_stages(kvmem_hip_ctx *ctx, uint32_t mask);
 KVMEM_HIP_API int kvmem_hip_perf_get(kvmem_hip_ctx *ctx, kvmem_hip_perf *out);
 /* Zero every bucket, count and transfer counter; a stage a failed call

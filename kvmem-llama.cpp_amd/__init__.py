@@ -41,7 +41,7 @@ OK, ERR_INVALID, ERR_RUNTIME, ERR_NOMEM, ERR_STALE, ERR_UNSUPPORTED, ERR_BUSY = 
 
 # stage bits of Context.perf_stages (KVMEM_PERF_STAGE_*)
 PERF_STAGE_SCORE, PERF_STAGE_TOPK, PERF_STAGE_SET, PERF_STAGE_COPY, PERF_STAGE_LAYOUT = 1, 2, 4, 8, 16
-PERF_STAGE_STAGE_OUT, PERF_STAGE_PLAN = 32, 64
+PERF_STAGE_STAGE_OUT, PERF_STAGE_PLAN, PERF_STAGE_MEANK_COS = 32, 64, 128
 PERF_STAGE_ALL = 0xffffffff
 
 # operation kinds of Context.debug_fail_after (kvmem_hip_fail_kind)
@@ -143,7 +143,8 @@ class Perf(C.Structure):
                 ("n_layout", C.c_uint64), ("h2d_bytes", C.c_uint64), ("d2d_bytes", C.c_uint64),
                 ("after_score_ms", C.c_double), ("n_after_score", C.c_uint64),
                 ("stage_out_ms", C.c_double), ("plan_ms", C.c_double), ("n_stage_out", C.c_uint64),
-                ("n_plan", C.c_uint64), ("d2h_bytes", C.c_uint64)]
+                ("n_plan", C.c_uint64), ("d2h_bytes", C.c_uint64), ("meank_cos_ms", C.c_double),
+                ("n_meank_cos", C.c_uint64)]
 
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}

@@ -766,6 +766,8 @@ int kvmem_hip_perf_get(kvmem_hip_ctx *ctx, kvmem_hip_perf *out) {
     out->n_stage_out = ctx->perf_n[kPerfStageOut];
     out->n_plan = ctx->perf_n[kPerfPlan];
     out->d2h_bytes = ctx->xfer_bytes[kXferD2H];
+    out->meank_cos_ms = ctx->perf_ms[kPerfMeankCos];
+    out->n_meank_cos = ctx->perf_n[kPerfMeankCos];
     return KVMEM_HIP_OK;
 }
 

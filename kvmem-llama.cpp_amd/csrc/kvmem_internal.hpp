@@ -38,7 +38,7 @@ struct UploadSlot {
 };
 
 constexpr int kUploadRing = 4;
-constexpr int kPerfStages = 7;  // score, topk, set, copy, layout, stage-out, plan
+constexpr int kPerfStages = 8;  // score, topk, set, copy, layout, stage-out, plan, mean-K cosine
 enum PerfStage {
     kPerfScore = 0,
     kPerfTopk = 1,
@@ -46,7 +46,8 @@ enum PerfStage {
     kPerfCopy = 3,
     kPerfLayout = 4,
     kPerfStageOut = 5,
-    kPerfPlan = 6
+    kPerfPlan = 6,
+    kPerfMeankCos = 7
 };
 // Directions of the transfer counters (llama_kvmem_transfer_stats order).
 enum XferKind { kXferH2D = 0, kXferD2H = 1, kXferD2D = 2 };

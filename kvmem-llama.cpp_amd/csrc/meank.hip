@@ -581,12 +581,17 @@ int kvmem_hip_score_meank(kvmem_hip_ctx *ctx, const kvmem_hip_meank_args *a) {
                                                   qv, nq);
     const uint64_t items = static_cast<uint64_t>(L) * B;  // 16 lanes each
     const uint32_t grid = static_cast<uint32_t>((items * 16 + 255) / 256);
-    if (D == 256) {
-        meank_cos_kernel<256><<<grid, 256, 0, ctx->stream>>>(a->k_sum, a->mean_tokens, qv, nq, invq_dev,
-                                                             L, B, cap, a->n_head_kv, layer_cos);
-    } else {
-        meank_cos_kernel<128><<<grid, 256, 0, ctx->stream>>>(a->k_sum, a->mean_tokens, qv, nq, invq_dev,
-                                                             L, B, cap, a->n_head_kv, layer_cos);
+    {
+        // the cosine kernel, which streams the key sums, also timed alone
+        PerfLaunchScope timed(ctx, kPerfMeankCos);
+        ctx_launch(ctx, D == 256 ? meank_cos_kernel<256> : meank_cos_kernel<128>, dim3(grid), dim3(256), 0,
+                   a->k_sum, a->mean_tokens, qv, nq, invq_dev, L, B, cap, a->n_head_kv, layer_cos);
+        if (hip_ok(ctx, hipGetLastError(), "score_meank launch")) {
+            timed.ok();
+        } else {
+            perf_drop(ctx, kPerfScore);
+            return KVMEM_HIP_ERR_RUNTIME;
+        }
     }
     constexpr uint32_t kCombineBlocks = 256 / kCombineLayers;
     meank_combine_kernel<<<(B + kCombineBlocks - 1) / kCombineBlocks, 256, 0, ctx->stream>>>(layer_cos, a->mean_tokens, invq_dev,

@@ -69,6 +69,14 @@ def test_struct_layouts_match_the_ctypes_mirrors(tmp_path):
             assert got[(name, field)] == getattr(cls, field).offset, (name, field)
 
 
+def test_perf_stage_bits_match_the_header():
+    text = (INCLUDE / "kvmem_hip.h").read_text()
+    bits = dict(re.findall(r"#define KVMEM_PERF_STAGE_(\w+) (\d+)u", text))
+    assert len(bits) >= 8
+    for name, value in bits.items():
+        assert getattr(kv, f"PERF_STAGE_{name}") == int(value), name
+
+
 def snippets() -> list[str]:
     text = (ROOT / "INTEGRATION.md").read_text()
     return re.findall(r"```cpp\n(.*?)```", text, flags=re.S)

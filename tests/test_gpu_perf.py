@@ -164,3 +164,38 @@ def test_engine_plan_bucket_and_skip_count():
             moved = st2["n_moved"] * L * T * 2 * kv.row_size(kv.TYPE_Q8_0, E)
             assert tr["d2d_calls"] >= 1 and tr["d2d_bytes"] >= moved, (tr, st2)
         ctx.perf_enable(False)
+
+
+def test_meank_cosine_kernel_timed_alone():
+    """score_ms covers the mean-K scorer's three kernels; meank_cos_ms the
+    cosine kernel alone, one timed launch per call, inside the score span;
+    the stage mask switches it off."""
+    announce("mean-K scorer: cosine kernel bucket")
+    nl, nb, hq, hkv, d = 4, 512, 8, 4, 256
+    ks = torch.randn((nl, nb, hkv * d), device="cuda")
+    mt = torch.full((nl, nb), 128, dtype=torch.int32, device="cuda")
+    q_sum = torch.randn((nl, hq * d), device="cuda")
+    scores = torch.empty(nb, dtype=torch.float32, device="cuda")
+    with kv.Context(0) as ctx:
+        def score():
+            ctx.score_meank(q_sum.data_ptr(), [4] * nl, ks.data_ptr(), mt.data_ptr(), nl, nb, hq, hkv, d,
+                            scores.data_ptr())
+        torch.cuda.synchronize()
+        score()
+        ctx.sync()
+        ctx.perf_enable(True)
+        ctx.perf_reset()
+        for _ in range(3):
+            score()
+        ctx.sync()
+        pf = ctx.perf()
+        assert pf["n_score"] == 3 and pf["n_meank_cos"] == 3
+        assert 0.0 < pf["meank_cos_ms"] < pf["score_ms"]
+        ctx.perf_stages(kv.PERF_STAGE_ALL & ~kv.PERF_STAGE_MEANK_COS)
+        ctx.perf_reset()
+        score()
+        ctx.sync()
+        pf = ctx.perf()
+        assert pf["n_score"] == 1 and pf["n_meank_cos"] == 0 and pf["meank_cos_ms"] == 0.0
+        ctx.perf_stages(kv.PERF_STAGE_ALL)
+        ctx.perf_enable(False)
