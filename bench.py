@@ -44,6 +44,7 @@ import concurrent.futures as cf
 import importlib.util
 import json
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -774,11 +775,21 @@ def run_copy_calibration(a, torch, kv, workloads) -> dict:
         e1.synchronize()
         t = e0.elapsed_time(e1) / 3
         link[name + "_GBs"] = round((512 << 20) / (t * 1e-3) / 1e9, 1)
+    # plain streaming kernels (kvmem-llama.cpp_amd/calib/hbm_rates.hip, a
+    # child process): the read, write and copy rates this device reaches
+    calib = Path(__file__).resolve().parent / "kvmem-llama.cpp_amd" / "calib" / "hbm_rates"
+    if not calib.exists():
+        raise SystemExit(f"{calib} is missing: build first (__graft_entry__.build())")
+    log("plain streaming kernels: 1 GiB read, write and copy")
+    r = subprocess.run([str(calib)], capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        raise SystemExit(f"hbm_rates failed ({r.returncode}): {r.stderr.strip()}")
+    plain = json.loads(r.stdout.strip().splitlines()[-1])
     return {"metric": "device copy calibration", "bytes_read": n_ops * op, "bytes_written": n_ops * op,
             "kernel_ms": round(ms, 4), "GBs_read_plus_write": round(2 * n_ops * op / (ms * 1e-3) / 1e9, 1),
             "runtime_copy_ms": round(rt_ms, 4),
             "runtime_copy_GBs": round(2 * n_ops * op / (rt_ms * 1e-3) / 1e9, 1), "copy_ok": ok,
-            "pinned_link": link}
+            "pinned_link": link, "plain_kernels": plain}
 
 
 def run_mfma_calibration(a, torch, kv, workloads) -> dict:

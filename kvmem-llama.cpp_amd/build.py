@@ -81,6 +81,22 @@ def build_lib(jobs: int = 8, verbose: bool = False) -> Path:
     return LIB
 
 
+CALIB_SRC = PKG / "calib" / "hbm_rates.hip"
+CALIB_BIN = PKG / "calib" / "hbm_rates"
+
+
+def build_calib() -> Path:
+    """The plain streaming kernels that give this device's reachable HBM
+    read, write and copy rates (bench.py --workload copy_calibration)."""
+    tmp = CALIB_BIN.with_suffix(".tmp")
+    cmd = [HIPCC, *HIP_FLAGS, "-O3", "-std=c++17", "-Wall", str(CALIB_SRC), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"calibration build failed\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, CALIB_BIN)
+    return CALIB_BIN
+
+
 def build_oracle(with_ref: bool = True) -> None:
     make = shutil.which("make") or "make"
     r = subprocess.run([make, "-s", "-C", str(ORACLE), "all"], capture_output=True, text=True)
@@ -101,6 +117,7 @@ def main() -> int:
     a = ap.parse_args()
     build_lib(a.jobs, a.verbose)
     if not a.lib_only:
+        build_calib()
         build_oracle()
     print(f"built {LIB}")
     return 0

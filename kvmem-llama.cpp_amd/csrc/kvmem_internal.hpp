@@ -228,7 +228,9 @@ bool stage_tables(kvmem_hip_ctx *ctx, const void *src, size_t bytes, LaunchTable
 // of the uploaded table (e.g. inside a timing bracket).
 bool launch_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, const char *what);
 bool stage_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, LaunchTables &out, const char *what);
-bool launch_staged_copies(kvmem_hip_ctx *ctx, const LaunchTables &tables, size_t n, const char *what);
+bool launch_staged_copies(kvmem_hip_ctx *ctx, const LaunchTables &tables, size_t n, uint64_t max_bytes,
+                          const char *what);
+uint64_t max_op_bytes(const std::vector<CopyOpDev> &ops);
 // Copies whose count an earlier kernel on the stream writes: min(*count,
 // max_ops) ops of the device table `ops` (a grid sized for max_ops).
 bool launch_dev_copies(kvmem_hip_ctx *ctx, const CopyOpDev *ops, const uint32_t *count, uint32_t max_ops,

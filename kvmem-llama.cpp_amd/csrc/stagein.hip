@@ -2625,7 +2625,7 @@ int kvmem_hip_move_slots(kvmem_hip_ctx *ctx, const kvmem_hip_pool *pool, const u
             return KVMEM_HIP_ERR_RUNTIME;
         }
         PerfScope timed(ctx, kPerfLayout);
-        if (!launch_staged_copies(ctx, save_tables, ops.size(), "move_slots save")) {
+        if (!launch_staged_copies(ctx, save_tables, ops.size(), max_op_bytes(ops), "move_slots save")) {
             return KVMEM_HIP_ERR_RUNTIME;
         }
         if (!ops.empty()) {
