@@ -405,6 +405,47 @@ def test_move_slots_chains_and_cycles(ctx, case, E):
         assert np.array_equal(p.cpu().numpy().reshape(n_slots, T, -1), want)
 
 
+def test_move_slots_pool_beyond_16_bit_slots(ctx):
+    """A pool of 70 000 slots: the chain kernel's segment records switch
+    from 16-bit to 32-bit entries.  A shift chain across slot 65 535 (two
+    segments), a chain between far slots and a 3-cycle through slots above
+    65 535, with partial token counts: the result equals gathering every
+    source first and scattering in order."""
+    announce("move_slots over 70 000 slots (32-bit chain records)")
+    L, n_slots, T, E = 2, 70000, 2, 256
+    rng = np.random.default_rng(71)
+    rb = kv.row_size(kv.TYPE_Q8_0, E)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(71)
+    layers = [torch.randint(0, 256, (n_slots * T * rb,), dtype=torch.uint8, device="cuda", generator=g)
+              for _ in range(2 * L)]
+    pool = ctx.make_pool(L, n_slots, T, E, E, kv.TYPE_Q8_0, kv.TYPE_Q8_0, [p.data_ptr() for p in layers[:L]],
+                         [p.data_ptr() for p in layers[L:]])
+    shift = list(range(65530, 65546))                      # slot i+1 -> slot i
+    src, dst = shift[1:], shift[:-1]
+    far = rng.choice(np.arange(100, 65000), 10, replace=False).tolist() + [69990, 66001, 65999]
+    far = rng.permutation(far).tolist()                    # a chain far[0] <- far[1] <- ...
+    src += far[1:]
+    dst += far[:-1]
+    src += [69999, 7, 66500]                               # a 3-cycle
+    dst += [7, 66500, 69999]
+    assert len(set(src)) == len(src) and len(set(dst)) == len(dst)
+    ntok = [int(x) for x in rng.integers(0, T + 1, len(src))]
+    ntok[:2] = [T, 0]
+    before = [p.cpu().numpy().reshape(n_slots, T, rb).copy() for p in layers]
+    torch.cuda.synchronize()
+    ctx.move_slots(pool, src, dst, ntok)
+    ctx.sync()
+    for b, p in zip(before, layers):
+        want = b.copy()
+        gathered = [b[s_, :nt].copy() for s_, nt in zip(src, ntok)]
+        for d, nt, rows in zip(dst, ntok, gathered):
+            want[d, :nt] = rows
+        assert np.array_equal(p.cpu().numpy().reshape(n_slots, T, rb), want)
+    del layers
+    torch.cuda.empty_cache()
+
+
 def test_scale_shortcuts_exhaustive(ctx):
     """The quantizers' division-free scale arithmetic equals the IEEE
     quotients over every float of its range, on this device."""
