@@ -14,7 +14,7 @@ import pytest
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-from engine_helpers import D, E, HQ, L, T, check_pool, history, kv, make_engine, workloads  # noqa: E402
+from engine_helpers import D, E, HQ, L, T, check_pool, history, host, kv, make_engine, workloads  # noqa: E402
 
 
 def announce(msg: str) -> None:
@@ -460,3 +460,69 @@ def test_device_plan_transform_growing_tail(oracle):
                 want_v = expected_rows(oracle, types[1], vb[layer, b].reshape(T, E)[:nt], D, 0, None, b * T, 64)
                 assert np.array_equal(wd[(layer, 0, b)], want_k), (step, layer, "K")
                 assert np.array_equal(wd[(layer, 1, b)], want_v), (step, layer, "V")
+
+
+@pytest.mark.parametrize("budget,reserve,on_device", [(1100, 20, 0), (1000, 3200, 0), (1024, 3072, 1)],
+                         ids=["selection_1100", "slots_4200", "at_both_limits"])
+def test_device_plan_at_and_past_its_limits(oracle, budget, reserve, on_device):
+    """Past the device plan's limits (1024 selected blocks, 4096 pool
+    slots) apply_retrieval plans on the host even when the device plan is
+    asked for; at exactly both limits it plans on the device.  Over three
+    queries either leaves the same stats, slots and pool bytes as an engine
+    without the device plan, selects the oracle's top-k over its scores,
+    and sampled blocks hold the oracle's q8_0 rows."""
+    announce(f"device plan limits: budget {budget}, reserve {reserve}")
+    lg, tg, hkv, hq, d = 2, 16, 1, 2, 256
+    eg = hkv * d
+    nb = 1300
+    k, v, _ = workloads.scoring_tensors(torch, "cuda", L=lg, B=nb, Tq=1, seed=budget, T=tg, Hkv=hkv, Hq=hq,
+                                        D=d, with_v=True)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(reserve)
+    qs = [torch.randn((lg, 4, hq, d), generator=g, device="cuda").to(torch.bfloat16) for _ in range(3)]
+    kb, vb = workloads.to_bits(torch, k), workloads.to_bits(torch, v)
+    rb = kv.row_size(kv.TYPE_Q8_0, eg)
+    rng = np.random.default_rng(budget + reserve)
+
+    def engine(plan):
+        return host.Engine(n_layers=lg, block_tokens=tg, n_head=hq, n_head_kv=hkv, head_dim=d,
+                           budget_blocks=budget, reserve_blocks=reserve, device_plan=plan)
+
+    def pool_bytes(eng):
+        c = kv.Context.borrow(eng.ctx_handle())
+        out = []
+        for layer in range(lg):
+            for ptr in eng.pool_layer(layer):
+                n = eng.n_slots() * tg * rb
+                buf = torch.empty(n, dtype=torch.uint8, device="cuda")
+                c.d2d_batched([ptr], [buf.data_ptr()], [n])
+                c.sync()
+                out.append(buf.cpu().numpy().reshape(eng.n_slots(), tg, rb))
+        return out
+
+    with engine(1) as dev, engine(0) as ref:
+        assert dev.n_slots() == budget + reserve
+        for eng in (dev, ref):
+            eng.set_device_history(k.data_ptr(), v.data_ptr(), nb, nb * tg)
+        for q in qs:
+            torch.cuda.synchronize()
+            sd = dev.apply_retrieval(q.data_ptr(), q.shape[1])
+            sr = ref.apply_retrieval(q.data_ptr(), q.shape[1])
+            assert sd.pop("device_planned") == on_device and sr.pop("device_planned") == 0
+            assert sd == sr
+            slots = dev.block_slots()
+            assert slots == ref.block_slots()
+            sel = [b for b, s in enumerate(slots) if s >= 0]
+            assert sorted(slots[b] for b in sel) == list(range(len(sel)))  # canonical layout
+            scores = np.array(dev.scores(), dtype=np.float64)
+            assert sel == oracle.pick_topk(scores.astype(np.float32).astype(np.float64), budget, sink=1)
+            pd, pr = pool_bytes(dev), pool_bytes(ref)
+            for a, b in zip(pd, pr):
+                assert np.array_equal(a[[slots[x] for x in sel]], b[[slots[x] for x in sel]])
+            for b in rng.choice(sel, 24, replace=False).tolist():
+                for layer in range(lg):
+                    for which, src in ((0, kb), (1, vb)):
+                        want = oracle.quantize_rows_f16(kv.TYPE_Q8_0, src[layer, b].reshape(tg, eg))
+                        assert np.array_equal(pd[2 * layer + which][slots[b]], want), (layer, which, b)
+    del k, v
+    torch.cuda.empty_cache()
