@@ -194,17 +194,18 @@ def test_q_accumulate_bit_exact(ctx, oracle, dtype):
     assert np.array_equal(qs.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
-def test_q_accumulate_long_token_list(ctx, oracle):
-    """A token list longer than the kernel arguments hold (768 entries):
-    1000 tokens, repeats included, uploaded; the sums bit-exact in list
-    order, then continued by a second list."""
-    announce("query sums over a 1000-entry token list")
+@pytest.mark.parametrize("n_list", [768, 769, 1000])
+def test_q_accumulate_long_token_list(ctx, oracle, n_list):
+    """Token lists at the kernel arguments' capacity (768 entries, the
+    table full) and past it (uploaded), repeats included: the sums
+    bit-exact in list order, then continued by a second list."""
+    announce(f"query sums over a {n_list}-entry token list")
     L, Tq, E = 2, 1200, 256
     rng = np.random.default_rng(37)
     wide = (rng.standard_normal((L, Tq, E)) * 3).astype(np.float32)
     q = torch.from_numpy(wide).to("cuda")
     qs = torch.full((L, E), float("nan"), dtype=torch.float32, device="cuda")
-    tokens = rng.integers(0, Tq, 1000).tolist()
+    tokens = rng.integers(0, Tq, n_list).tolist()
     torch.cuda.synchronize()
     ctx.q_accumulate(q.data_ptr(), kv.TYPE_F32, L, Tq, E, qs.data_ptr(), tokens=tokens)
     ctx.sync()

@@ -241,15 +241,16 @@ def test_window_gather_converts_round_to_nearest_even():
         assert bool((out == -3.0).all())
 
 
-def test_window_gather_long_row_list():
-    """A row list longer than the kernel arguments hold (768 entries): 800
-    rows in random order with repeats, uploaded; f32 copies bit-exact and
-    bf16 rounded to nearest even, in every layer."""
-    announce("q_window_gather: 800 rows (uploaded list)")
+@pytest.mark.parametrize("n_rows", [768, 769, 800])
+def test_window_gather_long_row_list(n_rows):
+    """Row lists at the kernel arguments' capacity (768 entries, the table
+    full) and past it (uploaded), in random order with repeats: f32 copies
+    bit-exact and bf16 rounded to nearest even, in every layer."""
+    announce(f"q_window_gather: {n_rows} rows")
     cap, n_layers, e = 1024, 2, 256
     rng = np.random.default_rng(41)
     win = (rng.standard_normal((n_layers, cap, e)) * 5).astype(np.float32)
-    rows = rng.integers(0, cap, 800).tolist()
+    rows = rng.integers(0, cap, n_rows).tolist()
     wd = torch.from_numpy(win).to("cuda")
     with kv.Context(0) as ctx:
         for tdt, ty in ((torch.float32, kv.TYPE_F32), (torch.bfloat16, kv.TYPE_BF16)):
