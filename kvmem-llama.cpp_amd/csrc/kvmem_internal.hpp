@@ -223,9 +223,11 @@ struct LaunchTables {
 bool stage_tables(kvmem_hip_ctx *ctx, const void *src, size_t bytes, LaunchTables &out, const char *what);
 
 // Upload `ops` and copy them in one launch on the context stream (each op
-// split over 1-8 workgroups so that a launch fills the chip, 16-byte
-// vectors where aligned).  The two halves apart: the upload, then launches
-// of the uploaded table (e.g. inside a timing bracket).
+// split into pieces of about 16 KiB, one per workgroup, and few small ops
+// into more so that a launch fills the chip; 16-byte vectors where
+// aligned).  The two halves apart: the upload, then launches of the
+// uploaded table (e.g. inside a timing bracket), which take the largest
+// op's size to size the pieces.
 bool launch_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, const char *what);
 bool stage_copy_ops(kvmem_hip_ctx *ctx, const std::vector<CopyOpDev> &ops, LaunchTables &out, const char *what);
 bool launch_staged_copies(kvmem_hip_ctx *ctx, const LaunchTables &tables, size_t n, uint64_t max_bytes,
