@@ -59,3 +59,15 @@ def test_headline_line_carries_the_contract_keys():
     # the roofline object's fields
     for k in ('"bound"', '"achieved"', '"peak"', '"unit"', '"frac"', '"traffic"'):
         assert k in src, k
+
+
+def test_calibration_program_is_built_and_checks_its_size():
+    """build() makes kvmem-llama.cpp_amd/calib/hbm_rates, which
+    `bench.py --workload copy_calibration` runs; a size that is not a
+    positive multiple of 16 MiB is refused before any device call."""
+    exe = ROOT / "kvmem-llama.cpp_amd" / "calib" / "hbm_rates"
+    assert exe.exists(), "build first"
+    for arg in ("17", "0", "-16", "131072"):
+        r = subprocess.run([str(exe), arg], capture_output=True, text=True, timeout=60)
+        assert r.returncode == 2, (arg, r.returncode, r.stderr)
+        assert "multiple of 16 MiB" in r.stderr
