@@ -55,6 +55,34 @@ def test_d2d_batched_many_unaligned_ops(ctx):
     assert np.array_equal(got, want), int(np.flatnonzero(got != want)[0])
 
 
+@pytest.mark.parametrize("big", [(5 << 20), (1 << 20) + 7, (64 << 20) + 48])
+def test_d2d_batched_large_and_tiny_ops_together(ctx, big):
+    """Ops are cut into pieces sized from the largest op (about 16 KiB,
+    at most 64 per op): one op of several MiB, aligned or not, beside
+    16-byte, 3-byte and 70 KB ops in the same launch; every byte equal to
+    the source, bytes outside the ops untouched."""
+    print(f"[copies] one {big}-byte op with small ones", flush=True)
+    rng = np.random.default_rng(big & 0xffff)
+    sizes = [big, 16, 3, 70000, 1, 4096, big // 3]
+    src_off, dst_off, pos_s, pos_d = [], [], 0, 5
+    for i, sz in enumerate(sizes):
+        src_off.append(pos_s if i % 2 == 0 else pos_s + 7)
+        pos_s = src_off[-1] + sz + 32
+        dst_off.append((pos_d + 15) // 16 * 16 if i % 3 == 0 else pos_d)
+        pos_d = dst_off[-1] + sz + 32
+    src_h = rng.integers(0, 256, pos_s + 64, dtype=np.uint8)
+    src = torch.from_numpy(src_h).cuda()
+    dst = torch.full((pos_d + 64,), 0x3C, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    ctx.d2d_batched([src.data_ptr() + o for o in src_off], [dst.data_ptr() + o for o in dst_off], sizes)
+    ctx.sync()
+    want = np.full(pos_d + 64, 0x3C, np.uint8)
+    for so, do, sz in zip(src_off, dst_off, sizes):
+        want[do:do + sz] = src_h[so:so + sz]
+    got = dst.cpu().numpy()
+    assert np.array_equal(got, want), int(np.flatnonzero(got != want)[0])
+
+
 def test_d2d_batched_refuses_null_and_empty_ops(ctx):
     print("[copies] null / empty ops refused, n = 0 a no-op", flush=True)
     src = torch.arange(256, dtype=torch.uint8, device="cuda")
